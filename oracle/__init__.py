@@ -1,0 +1,429 @@
+"""CPU ORACLE: test infrastructure only, never product code.
+
+NumPy-level restatement of the tensor.cx CPU reference path for the hip hot
+path. Only tests/, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline
+leg may import this package, and only as the checker. The arithmetic runs in
+``liboracle.so`` (oracle.cpp, bit-identical restatement of the reference loops);
+the shape plans below restate ``cpp/tensorcx/core/shape.cpp``.
+
+Pinning: tests/test_oracle.py checks every function against golden vectors
+written by the reference CPU backend itself (tests/golden/*.npz, made by
+tests/golden/make_golden.py through oracle/_ref), against the reference
+library directly when oracle/_ref is built, and against closed forms.
+"""
+
+from __future__ import annotations
+
+import builtins
+import ctypes
+import os
+import pathlib
+import subprocess
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+_LIB = None
+
+# Reference enum values (cpp/tensorcx/core/operation.h:12-53).
+OPKIND = {
+    "fill": 0, "add": 1, "multiply": 2, "matmul": 3, "sum": 4, "max": 5, "mean": 6,
+    "exp": 7, "gelu": 8, "silu": 9, "softmax": 10, "rmsnorm": 11, "layernorm": 12,
+    "subtract": 13, "divide": 14, "min": 41, "argmax": 42, "linear": 45,
+    "affine_rmsnorm": 46, "affine_layernorm": 47,
+}
+DTYPE = {"float32": 0, "int32": 1, "bool": 2}
+
+
+def default_threads() -> int:
+    return builtins.max(1, builtins.min(16, os.cpu_count() or 1))
+
+
+def build() -> None:
+    """Compiles liboracle.so (and oracle/_ref when /root/reference is present)."""
+    subprocess.run(["make", "-s", "-C", str(HERE), "oracle"], check=True)
+    if pathlib.Path("/root/reference/cpp/tensorcx").is_dir():
+        subprocess.run(["make", "-s", "-j8", "-C", str(HERE), "ref"], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        path = HERE / "liboracle.so"
+        if not path.exists():
+            raise RuntimeError(f"{path} is not built; run `make -C oracle`")
+        _LIB = ctypes.CDLL(str(path))
+    return _LIB
+
+
+def _p(array: np.ndarray):
+    return array.ctypes.data_as(ctypes.c_void_p)
+
+
+def _dims(values) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(values, dtype=np.int64).reshape(-1))
+
+
+# ---------------------------------------------------------------- shape plans
+def contiguous_strides(shape) -> list[int]:
+    """shape.cpp:38-47."""
+    strides, stride = [1] * len(shape), 1
+    for i in range(len(shape) - 1, -1, -1):
+        if shape[i] < 0:
+            raise ValueError("shape dimensions must be non-negative")
+        strides[i] = stride
+        stride *= shape[i]
+    return strides
+
+
+def normalize_axis(axis: int, rank: int) -> int:
+    """cpu_backend.cpp:79-91."""
+    if rank == 0:
+        if axis in (0, -1):
+            return 0
+        raise ValueError("reduction axis is out of range")
+    if axis < 0:
+        axis += rank
+    if axis < 0 or axis >= rank:
+        raise ValueError("reduction axis is out of range")
+    return axis
+
+
+def reduction_dims(shape, axis: int):
+    """cpu_backend.cpp:93-123: (output_shape, outer, reduce, inner)."""
+    axis = normalize_axis(axis, len(shape))
+    if len(shape) == 0:
+        return (), 1, 1, 1
+    outer = int(np.prod(shape[:axis], dtype=np.int64))
+    inner = contiguous_strides(shape)[axis]
+    out_shape = tuple(d for i, d in enumerate(shape) if i != axis)
+    return out_shape, outer, int(shape[axis]), inner
+
+
+def make_matmul_plan(lhs, rhs):
+    """shape.cpp:49-76: numpy matmul broadcasting over leading batch axes."""
+    if len(lhs) == 0 or len(rhs) == 0:
+        raise ValueError("matmul requires rank >= 1 tensors")
+    ls, rs = contiguous_strides(lhs), contiguous_strides(rhs)
+    lv, rv = len(lhs) == 1, len(rhs) == 1
+    m = 1 if lv else lhs[-2]
+    k = lhs[-1]
+    rk = rhs[0] if rv else rhs[-2]
+    n = 1 if rv else rhs[-1]
+    if k != rk:
+        raise ValueError("matmul shape mismatch: contracting dimensions differ")
+    lb = 0 if lv else len(lhs) - 2
+    rb = 0 if rv else len(rhs) - 2
+    rank = builtins.max(lb, rb)
+    batch, lstr, rstr = [1] * rank, [0] * rank, [0] * rank
+    for axis in range(rank):
+        has_l, has_r = axis >= rank - lb, axis >= rank - rb
+        li, ri = axis - (rank - lb), axis - (rank - rb)
+        left = lhs[li] if has_l else 1
+        right = rhs[ri] if has_r else 1
+        if left != right and left != 1 and right != 1:
+            raise ValueError("matmul batch dimensions cannot broadcast")
+        batch[axis] = right if left == 1 else left
+        if has_l and left != 1:
+            lstr[axis] = ls[li]
+        if has_r and right != 1:
+            rstr[axis] = rs[ri]
+    out = list(batch)
+    if not lv:
+        out.append(m)
+    if not rv:
+        out.append(n)
+    return tuple(out), batch, lstr, rstr, m, k, n
+
+
+def matmul_batch_offset(batch: int, shape, strides) -> int:
+    """shape.cpp:78-85."""
+    offset = 0
+    for axis in range(len(shape) - 1, -1, -1):
+        offset += (batch % shape[axis]) * strides[axis]
+        batch //= shape[axis]
+    return offset
+
+
+def make_reduction_plan(shape, axes):
+    """shape.cpp:140-173: (output_shape, index_metadata, reduction_size)."""
+    strides = contiguous_strides(shape)
+    rank = len(shape)
+    selected = [False] * rank
+    for axis in axes:
+        if axis < 0:
+            axis += rank
+        if axis < 0 or axis >= rank:
+            raise ValueError("reduction axis is out of range")
+        if selected[axis]:
+            raise ValueError("reduction axes must not repeat")
+        selected[axis] = True
+    out_shape, meta, reduced = [], [], []
+    for axis in range(rank):
+        if selected[axis]:
+            reduced.append(shape[axis])
+        else:
+            out_shape.append(shape[axis])
+            meta += [shape[axis], strides[axis]]
+    for axis in range(rank):
+        if selected[axis]:
+            meta += [shape[axis], strides[axis]]
+    count = int(np.prod(out_shape, dtype=np.int64))
+    if 0 in reduced:
+        size = 0
+    elif count != 0:
+        size = int(np.prod(reduced, dtype=np.int64))
+    else:
+        size = 1
+    return tuple(out_shape), meta, size
+
+
+def make_broadcast_plan(lhs, rhs):
+    """shape.cpp:202-229: (output_shape, lhs_strides, rhs_strides)."""
+    lc, rc = contiguous_strides(lhs), contiguous_strides(rhs)
+    rank = builtins.max(len(lhs), len(rhs))
+    lp, rp = rank - len(lhs), rank - len(rhs)
+    out, ls, rs = [0] * rank, [0] * rank, [0] * rank
+    for axis in range(rank):
+        left = 1 if axis < lp else lhs[axis - lp]
+        right = 1 if axis < rp else rhs[axis - rp]
+        if left != right and left != 1 and right != 1:
+            raise ValueError("shape mismatch: tensor shapes are not broadcastable")
+        out[axis] = right if left == 1 else left
+        if axis >= lp and left != 1:
+            ls[axis] = lc[axis - lp]
+        if axis >= rp and right != 1:
+            rs[axis] = rc[axis - rp]
+    return tuple(out), ls, rs
+
+
+def checked_epsilon(eps: float) -> np.float32:
+    """cpu_backend.cpp:30-42."""
+    if not np.isfinite(eps) or eps < 0 or eps > float(np.finfo(np.float32).max):
+        raise ValueError("epsilon must be finite and non-negative and representable as float32")
+    rounded = np.float32(eps)
+    if eps > 0 and rounded == 0:
+        raise ValueError("epsilon must be finite and non-negative and representable as float32")
+    return rounded
+
+
+# ------------------------------------------------------------------ operations
+def _f32(x) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    if x.dtype != np.float32:
+        raise ValueError("expected float32 input")
+    return x
+
+
+def matmul(a, b, threads: int | None = None) -> np.ndarray:
+    """cpu_backend.cpp:1251-1276."""
+    a, b = _f32(a), _f32(b)
+    out_shape, batch, lstr, rstr, m, k, n = make_matmul_plan(a.shape, b.shape)
+    out = np.empty(out_shape, dtype=np.float32)
+    batches = int(np.prod(batch, dtype=np.int64)) if batch else 1
+    if out.size == 0:
+        return out
+    lo = _dims([matmul_batch_offset(i, batch, lstr) for i in range(batches)])
+    ro = _dims([matmul_batch_offset(i, batch, rstr) for i in range(batches)])
+    lib().oracle_matmul_f32(_p(a), _p(b), _p(out), ctypes.c_int64(batches), ctypes.c_int64(m),
+                            ctypes.c_int64(n), ctypes.c_int64(k), _p(lo), _p(ro),
+                            ctypes.c_int(threads or default_threads()))
+    return out
+
+
+def _reduce_single(op: int, x: np.ndarray, axis: int, threads) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    out_shape, outer, reduce, inner = reduction_dims(x.shape, axis)
+    if op == 1 and reduce == 0:
+        raise ValueError("max reduction requires a non-empty axis")
+    if op == 2 and x.dtype != np.float32:
+        raise ValueError("mean only supports float32 tensors")
+    out = np.empty(out_shape, dtype=x.dtype)
+    if out.size == 0:
+        return out
+    t = ctypes.c_int(threads or default_threads())
+    if x.dtype == np.float32:
+        lib().oracle_reduce_f32(op, _p(x), _p(out), ctypes.c_int64(outer), ctypes.c_int64(reduce),
+                                ctypes.c_int64(inner), t)
+    elif x.dtype == np.int32:
+        lib().oracle_reduce_i32(op, _p(x), _p(out), ctypes.c_int64(outer), ctypes.c_int64(reduce),
+                                ctypes.c_int64(inner), t)
+    else:
+        raise ValueError("numeric reductions do not support bool tensors")
+    return out
+
+
+def _reduce_axes(op: int, x: np.ndarray, axes, threads) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    if op == 2 and x.dtype != np.float32:
+        raise ValueError("mean only supports float32 tensors")
+    out_shape, meta, size = make_reduction_plan(x.shape, tuple(axes))
+    if op == 1 and size == 0:
+        raise ValueError("max reduction requires non-empty axes")
+    if len(axes) == 0:
+        return x.copy()
+    out = np.empty(out_shape, dtype=x.dtype)
+    if out.size == 0:
+        return out
+    m = _dims(meta)
+    lib().oracle_reduce_axes(op, DTYPE[str(x.dtype)], _p(x), _p(out), _p(m), len(out_shape),
+                             x.ndim, ctypes.c_int64(out.size), ctypes.c_int64(size),
+                             ctypes.c_int(threads or default_threads()))
+    return out
+
+
+def _reduce(op: int, x, axis, threads):
+    """tensor.py:508-529 routing: None -> all axes; one axis -> single-axis path."""
+    x = np.asarray(x)
+    if axis is None:
+        axes = tuple(range(x.ndim))
+        if x.ndim == 0:
+            return _reduce_single(op, x, 0, threads)
+        return _reduce_axes(op, x, axes, threads)
+    if isinstance(axis, (tuple, list)):
+        if len(axis) == 1:
+            return _reduce_single(op, x, axis[0], threads)
+        return _reduce_axes(op, x, tuple(axis), threads)
+    return _reduce_single(op, x, int(axis), threads)
+
+
+def sum(x, axis=None, threads=None):  # noqa: A001
+    return _reduce(0, x, axis, threads)
+
+
+def max(x, axis=None, threads=None):  # noqa: A001
+    return _reduce(1, x, axis, threads)
+
+
+def mean(x, axis=None, threads=None):
+    return _reduce(2, x, axis, threads)
+
+
+def _argext(code: int, x, axis, threads) -> np.ndarray:
+    """math.cpp:39-56 plan + cpu_math.cpp:48-54."""
+    x = np.ascontiguousarray(x)
+    if x.dtype not in (np.float32, np.int32):
+        raise ValueError("math operations require float32 or int32 tensors")
+    if axis is None:
+        axes = tuple(range(x.ndim))
+    elif isinstance(axis, (tuple, list)):
+        axes = tuple(axis)
+    else:
+        axes = () if x.ndim == 0 and axis in (0, -1) else (int(axis),)
+    out_shape, meta, size = make_reduction_plan(x.shape, axes)
+    if size == 0:
+        raise ValueError("min/argmax require a non-empty reduction")
+    out = np.empty(out_shape, dtype=np.int32 if code == 4 else x.dtype)
+    if out.size == 0:
+        return out
+    lib().oracle_argext(code, DTYPE[str(x.dtype)], _p(x), _p(out), _p(_dims(meta)), x.ndim,
+                        ctypes.c_int64(out.size), ctypes.c_int64(size),
+                        ctypes.c_int(threads or default_threads()))
+    return out
+
+
+def min(x, axis=None, threads=None):  # noqa: A001
+    return _argext(3, x, axis, threads)
+
+
+def argmax(x, axis=None, threads=None):
+    return _argext(4, x, axis, threads)
+
+
+def _rowwise(fn: str, x, axis: int, eps, threads) -> np.ndarray:
+    x = _f32(x)
+    _, outer, reduce, inner = reduction_dims(x.shape, axis)
+    args = []
+    if eps is not None:
+        args = [ctypes.c_float(checked_epsilon(eps))]
+    out = np.empty_like(x)
+    if x.size == 0:
+        return out
+    getattr(lib(), fn)(_p(x), _p(out), ctypes.c_int64(outer), ctypes.c_int64(reduce),
+                       ctypes.c_int64(inner), *args, ctypes.c_int(threads or default_threads()))
+    return out
+
+
+def softmax(x, axis=-1, threads=None):
+    """cpu_backend.cpp:125-155."""
+    return _rowwise("oracle_softmax", x, axis, None, threads)
+
+
+def rmsnorm(x, axis=-1, eps=1e-5, threads=None):
+    """cpu_backend.cpp:157-183."""
+    return _rowwise("oracle_rmsnorm", x, axis, eps, threads)
+
+
+def layernorm(x, axis=-1, eps=1e-5, threads=None):
+    """cpu_backend.cpp:185-240."""
+    return _rowwise("oracle_layernorm", x, axis, eps, threads)
+
+
+def _unary(op: int, x, threads) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty_like(x)
+    if x.size:
+        lib().oracle_unary(op, _p(x), _p(out), ctypes.c_int64(x.size),
+                           ctypes.c_int(threads or default_threads()))
+    return out
+
+
+def exp(x, threads=None):
+    return _unary(0, x, threads)
+
+
+def gelu(x, threads=None):
+    return _unary(1, x, threads)
+
+
+def silu(x, threads=None):
+    return _unary(2, x, threads)
+
+
+_BINARY = {"add": 0, "subtract": 1, "multiply": 2, "divide": 3}
+
+
+def binary(name: str, lhs, rhs, threads=None) -> np.ndarray:
+    """cpu_backend.cpp:1014-1097."""
+    lhs, rhs = np.ascontiguousarray(lhs), np.ascontiguousarray(rhs)
+    if lhs.dtype != rhs.dtype:
+        raise ValueError("dtype mismatch for binary operation")
+    if name == "divide" and lhs.dtype != np.float32:
+        raise ValueError("division only supports float32 tensors")
+    shape, ls, rs = make_broadcast_plan(lhs.shape, rhs.shape)
+    out = np.empty(shape, dtype=lhs.dtype)
+    if out.size == 0:
+        return out
+    lib().oracle_binary(_BINARY[name], DTYPE[str(lhs.dtype)], _p(lhs), _p(rhs), _p(out),
+                        _p(_dims(shape)), _p(_dims(ls)), _p(_dims(rs)), len(shape),
+                        ctypes.c_int64(out.size), ctypes.c_int(threads or default_threads()))
+    return out
+
+
+def linear(x, weight, bias=None, threads=None) -> np.ndarray:
+    """inference.cpp:89-102: transpose(W) copy, matmul, then broadcast add."""
+    weight = _f32(weight)
+    out = matmul(x, np.ascontiguousarray(weight.T), threads)
+    if bias is not None:
+        out = binary("add", out, bias, threads)
+    return out
+
+
+def affine_norm(x, axis, eps, weight=None, bias=None, rms=False, threads=None) -> np.ndarray:
+    """inference.cpp:103-122: norm, then multiply by weight, then add bias."""
+    x = _f32(x)
+    out = (rmsnorm if rms else layernorm)(x, axis, eps, threads)
+    view = [1] * x.ndim
+    if x.ndim:
+        view[normalize_axis(axis, x.ndim)] = x.shape[normalize_axis(axis, x.ndim)]
+    if weight is not None:
+        out = binary("multiply", out, np.asarray(weight).reshape(view), threads)
+    if bias is not None:
+        out = binary("add", out, np.asarray(bias).reshape(view), threads)
+    return out
+
+
+def mlp_forward(x, w1, b1, w2, b2, threads=None) -> np.ndarray:
+    """The MLP chain linear -> silu -> linear -> softmax(axis=-1)."""
+    h = silu(linear(x, w1, b1, threads), threads)
+    return softmax(linear(h, w2, b2, threads), -1, threads)
