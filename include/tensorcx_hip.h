@@ -1,0 +1,231 @@
+/*
+ * tensorcx_hip.h: C ABI of the MI355X (gfx950) hip device for tensor.cx.
+ *
+ * The C++ `tensorcx::hip::HipBackend` (tensor.cx_amd/cpp/tensorcx/backends/hip)
+ * implements the reference's backend interface `Backend::execute`
+ * (reference cpp/tensorcx/core/backend.h:67-73) on top of these entry points,
+ * exactly where the reference's CUDA prototype calls the CUDA runtime and its
+ * `launch_*` kernel wrappers. Every entry point takes plain pointers, sizes and
+ * POD descriptors, returns a status code with the values of
+ * `tensorcx::StatusCode` (reference core/status.h:8-13), never throws, and
+ * leaves a message for `tcx_hip_last_error()` on failure. Kernel launchers
+ * enqueue on the given stream and never allocate: scratch space comes in
+ * through a workspace argument sized by the matching *_workspace_bytes query.
+ */
+#ifndef TENSORCX_HIP_H_
+#define TENSORCX_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Values of tensorcx::StatusCode (reference core/status.h:8-13). */
+#define TCX_OK 0
+#define TCX_INVALID_ARGUMENT 1
+#define TCX_UNAVAILABLE 2
+#define TCX_INTERNAL 3
+
+/* Values of tensorcx::DType (reference core/dtype.h:8-12). */
+#define TCX_FLOAT32 0
+#define TCX_INT32 1
+
+typedef void* tcx_stream_t; /* a hipStream_t */
+
+/* ------------------------------------------------------------------ runtime */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* tcx_hip_last_error(void);
+
+/* Initialises the HIP runtime once per process and checks for a device.
+ * Replaces cuda::available() (reference backends/cuda/cuda_backend.h:37;
+ * cuda_backend.cpp:166-169). Returns TCX_UNAVAILABLE without a device and in a
+ * forked child of a process that initialised the runtime
+ * (cf. cuda_context.cpp:16-20). */
+int tcx_hip_init(void);
+int tcx_hip_device_count(int* count);
+
+typedef struct {
+  char name[256];
+  char arch[64];            /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  int compute_units;
+  int clock_khz;
+  int memory_clock_khz;
+  int memory_bus_width;
+  int l2_bytes;
+  int runtime_version;
+  int driver_version;
+  size_t total_bytes;
+  size_t free_bytes;
+} tcx_hip_device_info_t;
+
+/* Replaces cuda::device_name()/device_info() (cuda_backend.h:38-44). */
+int tcx_hip_device_info(int device, tcx_hip_device_info_t* info);
+
+/* This thread's stream (created on first use, default priority). Every
+ * HipBackend::execute runs on it and synchronises it before returning, the
+ * reference's synchronous completion contract (docs/BACKENDS.md:73-80). */
+int tcx_hip_stream(tcx_stream_t* stream);
+int tcx_hip_stream_synchronize(tcx_stream_t stream);
+
+/* ------------------------------------------------------------------- memory */
+
+typedef struct tcx_hip_pool tcx_hip_pool_t;
+
+/* Device allocation for a tensor buffer: from this thread's active pool when
+ * one is entered, else hipMalloc. *owner receives the pool the block came from
+ * (or NULL) and must be passed back to tcx_hip_release. Replaces
+ * CudaBuffer::create (cuda_backend.cpp:58-85). Zero bytes yields NULL. */
+int tcx_hip_allocate(size_t bytes, void** ptr, tcx_hip_pool_t** owner);
+/* Returns a block from tcx_hip_allocate: to its pool's cache when that pool
+ * is still active and has room, else hipFree. Never fails the caller. */
+void tcx_hip_release(void* ptr, size_t bytes, tcx_hip_pool_t* owner);
+
+/* Copies on `stream`, synchronised before return (cuda::from_cpu/to_cpu,
+ * cuda_backend.cpp:215-264). */
+int tcx_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, tcx_stream_t stream);
+int tcx_hip_memcpy_d2h(void* dst, const void* src, size_t bytes, tcx_stream_t stream);
+int tcx_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, tcx_stream_t stream);
+
+/* ---------------------------------------------------------- bounded pool */
+
+/* Injectable allocator seam (reference cuda_memory_pool.h:20-27) so pool
+ * logic is testable without a device. Each returns a TCX_* code;
+ * allocate returns TCX_UNAVAILABLE+100 (TCX_POOL_OOM) for out-of-memory. */
+#define TCX_POOL_OOM 102
+typedef struct {
+  int (*allocate)(void** ptr, size_t bytes);
+  int (*free)(void* ptr);
+  int (*clear_error)(void);
+} tcx_hip_pool_runtime_t;
+
+typedef struct {
+  size_t max_cached_bytes, max_cached_blocks, cached_bytes, cached_blocks;
+  size_t in_use_bytes, peak_in_use_bytes, peak_cached_bytes;
+  uint64_t hits, misses, allocation_calls, free_calls, allocation_failures, oom_retries,
+      uncached_returns, readiness_failures, free_failures, failed_free_bytes;
+  int active;
+} tcx_hip_pool_stats_t;
+
+/* Bounded exact-size block cache with the semantics of the reference's
+ * MemoryPool (cuda_memory_pool.cpp:21-163): thread-scoped, single-use,
+ * not nestable; on allocation OOM with blocks cached it drains the cache and
+ * retries once. `runtime` may be NULL for hipMalloc/hipFree. */
+int tcx_hip_pool_create(size_t max_cached_bytes, size_t max_cached_blocks,
+                        const tcx_hip_pool_runtime_t* runtime, tcx_hip_pool_t** pool);
+int tcx_hip_pool_enter(tcx_hip_pool_t* pool);
+int tcx_hip_pool_exit(tcx_hip_pool_t* pool);
+int tcx_hip_pool_trim(tcx_hip_pool_t* pool);
+int tcx_hip_pool_stats(const tcx_hip_pool_t* pool, tcx_hip_pool_stats_t* stats);
+/* Drops the caller's reference; cached blocks are freed when the last
+ * outstanding buffer from the pool has been released. */
+void tcx_hip_pool_destroy(tcx_hip_pool_t* pool);
+
+/* ------------------------------------------------------------------- events */
+
+/* Device timing (the reference's DeviceTimer, cuda_profiling.h:22-77). */
+int tcx_hip_event_create(void** event);
+int tcx_hip_event_record(void* event, tcx_stream_t stream);
+int tcx_hip_event_synchronize(void* event);
+int tcx_hip_event_elapsed_ms(void* start, void* stop, float* ms);
+int tcx_hip_event_destroy(void* event);
+
+/* ------------------------------------------------------------------ kernels */
+
+#define TCX_HIP_MAX_BATCH_RANK 8
+
+#define TCX_ACT_NONE 0
+#define TCX_ACT_SILU 1
+#define TCX_ACT_GELU 2
+
+typedef struct {
+  int64_t m, n, k;
+  int64_t batch_count;                          /* product of batch_shape (1 if rank 0) */
+  int32_t batch_rank;                           /* <= TCX_HIP_MAX_BATCH_RANK */
+  int32_t rhs_transposed;                       /* 1: rhs is [n, k] row-major */
+  int64_t batch_shape[TCX_HIP_MAX_BATCH_RANK];
+  int64_t lhs_batch_strides[TCX_HIP_MAX_BATCH_RANK]; /* in elements */
+  int64_t rhs_batch_strides[TCX_HIP_MAX_BATCH_RANK];
+  const float* bias;                            /* optional [n], added per column */
+  int32_t activation;                           /* TCX_ACT_*, applied after bias */
+} tcx_hip_gemm_desc_t;
+
+/* out[b] = act(lhs[b] @ rhs[b] (+ bias)), fp32 on v_mfma_f32_16x16x4_f32,
+ * out contiguous [batch..., m, n]. Replaces launch_matmul
+ * (reference backends/cuda/cuda_kernels.h:11-45; kernels/primitives.cu:251-333)
+ * and, with rhs_transposed + bias, the kLinear composite
+ * (core/inference.cpp:89-102) without its transpose copy. */
+int tcx_hip_gemm_f32(const float* lhs, const float* rhs, float* out,
+                     const tcx_hip_gemm_desc_t* desc, tcx_stream_t stream);
+
+#define TCX_REDUCE_SUM 0
+#define TCX_REDUCE_MAX 1
+#define TCX_REDUCE_MEAN 2
+#define TCX_REDUCE_MIN 3
+#define TCX_REDUCE_ARGMAX 4
+
+/* Reduction of x viewed as [outer, reduce, inner] over the middle axis into
+ * out [outer, inner]: the single-axis reduce of cpu_backend.cpp:1154-1249
+ * and min/argmax of cpu_math.cpp:27-76 (argmax writes int32 indices), and any
+ * multi-axis selection whose reduced axes are adjacent. dtype TCX_FLOAT32
+ * (sum, max, mean, min, argmax) or TCX_INT32 (sum wrapping mod 2^32, max,
+ * min, argmax). workspace may be NULL when the query returns 0. */
+size_t tcx_hip_reduce_workspace_bytes(int op, int dtype, int64_t outer, int64_t reduce,
+                                      int64_t inner);
+int tcx_hip_reduce(int op, int dtype, const void* x, void* out, int64_t outer, int64_t reduce,
+                   int64_t inner, void* workspace, size_t workspace_bytes, tcx_stream_t stream);
+
+/* General reduction over any axis selection, with the reference's
+ * make_reduction_plan metadata (core/shape.cpp:140-173): `meta` holds
+ * extent/stride pairs for all `rank` axes, kept axes first then reduced axes,
+ * `outer_rank` of them kept; one output per group in the reference's exact
+ * element order (cpu_backend.cpp:1102-1153; cpu_math.cpp:48-54). */
+int tcx_hip_reduce_axes(int op, int dtype, const void* x, void* out, const int64_t* meta,
+                        int32_t outer_rank, int32_t rank, int64_t groups,
+                        int64_t reduction_size, tcx_stream_t stream);
+
+/* Row softmax / RMSNorm / LayerNorm of x viewed as [outer, reduce, inner] over
+ * the middle axis (cpu_backend.cpp:125-240). gamma/beta are optional [reduce]
+ * affine parameters applied as two separately rounded steps, which is the
+ * kAffine*Norm composite of core/inference.cpp:103-122 fused into one pass. */
+int tcx_hip_softmax_f32(const float* x, float* out, int64_t outer, int64_t reduce,
+                        int64_t inner, tcx_stream_t stream);
+int tcx_hip_rmsnorm_f32(const float* x, const float* gamma, float* out, int64_t outer,
+                        int64_t reduce, int64_t inner, float eps, tcx_stream_t stream);
+int tcx_hip_layernorm_f32(const float* x, const float* gamma, const float* beta, float* out,
+                          int64_t outer, int64_t reduce, int64_t inner, float eps,
+                          tcx_stream_t stream);
+
+/* out[r, c] = act(x[r, c] + bias[c]) (bias optional): fused bias+activation,
+ * the kAdd-broadcast of kLinear followed by kSilu/kGelu (cpu_backend.cpp:
+ * 1004-1006, 1014-1097) in one pass. */
+int tcx_hip_bias_act_f32(const float* x, const float* bias, float* out, int64_t rows,
+                         int64_t cols, int activation, tcx_stream_t stream);
+
+#define TCX_UNARY_EXP 0
+#define TCX_UNARY_GELU 1
+#define TCX_UNARY_SILU 2
+/* Elementwise exp/gelu/silu (cpu_backend.cpp:1000-1010). */
+int tcx_hip_unary_f32(int op, const float* x, float* out, int64_t n, tcx_stream_t stream);
+
+#define TCX_BINARY_ADD 0
+#define TCX_BINARY_SUBTRACT 1
+#define TCX_BINARY_MULTIPLY 2
+#define TCX_BINARY_DIVIDE 3
+#define TCX_HIP_MAX_RANK 8
+/* Broadcast arithmetic over a make_broadcast_plan (core/shape.cpp:202-229):
+ * float32, or int32 wrapping (no divide) as in cpu_backend.cpp:1014-1097. */
+int tcx_hip_binary(int op, int dtype, const void* lhs, const void* rhs, void* out, int32_t rank,
+                   const int64_t* out_shape, const int64_t* lhs_strides,
+                   const int64_t* rhs_strides, tcx_stream_t stream);
+
+/* kFill (cpu_backend.cpp fill): float32 or int32 value into n elements. */
+int tcx_hip_fill(int dtype, void* out, int64_t n, double value, tcx_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TENSORCX_HIP_H_ */

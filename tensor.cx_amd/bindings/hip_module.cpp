@@ -1,0 +1,305 @@
+// Python binding of the hip device: the hip counterpart of the reference's
+// per-device overload block (reference bindings/python_module.cpp:1660-1716)
+// and its shared templates (:800-958). Every op builds a BackendExecution,
+// releases the GIL, calls HipBackend::execute and maps the Status to a Python
+// exception the way throw_status does (python_module.cpp:402-414):
+// kInvalidArgument -> ValueError, anything else -> RuntimeError.
+
+#include <pybind11/numpy.h>
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include <array>
+#include <cstring>
+#include <optional>
+#include <string>
+#include <vector>
+
+#include "tensorcx/backends/hip/hip_backend.h"
+
+namespace py = pybind11;
+using namespace tensorcx;
+
+namespace {
+
+struct HipTensor {
+  Tensor tensor;
+};
+
+[[noreturn]] void throw_status(const Status& status) {
+  if (status.code() == StatusCode::kInvalidArgument) throw py::value_error(status.message());
+  throw std::runtime_error(status.message());
+}
+
+DType parse_dtype(const std::string& name) {
+  if (name == "float32") return DType::kFloat32;
+  if (name == "int32") return DType::kInt32;
+  if (name == "bool") return DType::kBool;
+  throw py::value_error("unsupported dtype: " + name);
+}
+
+Shape to_shape(const std::vector<std::int64_t>& dims) { return Shape(dims.begin(), dims.end()); }
+
+HipTensor run(OpDesc op, std::vector<Tensor> inputs) {
+  std::array<Tensor, 1> outputs{};
+  Status status;
+  {
+    py::gil_scoped_release release;
+    BackendExecution e{BackendOpClass::kPrimitive, std::move(op), inputs, outputs, std::nullopt, std::nullopt, {}};
+    hip::HipBackend backend;
+    status = backend.execute(e);
+  }
+  if (!status.ok()) throw_status(status);
+  return HipTensor{std::move(outputs[0])};
+}
+
+HipTensor unary(OpKind kind, const HipTensor& x) { return run(OpDesc{kind}, {x.tensor}); }
+
+HipTensor axis_op(OpKind kind, const HipTensor& x, std::int64_t axis, double eps = 1e-5) {
+  OpDesc op{kind};
+  op.axis = axis;
+  op.epsilon = eps;
+  return run(op, {x.tensor});
+}
+
+HipTensor axes_op(OpKind kind, const HipTensor& x, const std::vector<std::int64_t>& axes) {
+  OpDesc op{kind};
+  op.reduction_axes = to_shape(axes);
+  return run(op, {x.tensor});
+}
+
+// Built-in fused kernels through BackendOpClass::kKernel (the unchanged ABI's
+// route for backend-provided kernels); the output is preallocated here.
+HipTensor builtin(const std::string& entry, std::vector<const HipTensor*> args, std::uint32_t act, Shape out_shape) {
+  auto created = hip::empty(std::move(out_shape), DType::kFloat32);
+  if (!created) throw_status(created.status());
+  std::array<Tensor, 1> outputs{created.move_value()};
+  std::vector<KernelArgument> kargs;
+  for (const HipTensor* t : args) kargs.push_back(KernelArgument{KernelArgumentKind::kTensor, &t->tensor, 0});
+  kargs.push_back(KernelArgument{KernelArgumentKind::kUInt32, nullptr, act});
+  Status status;
+  {
+    py::gil_scoped_release release;
+    BackendExecution e{BackendOpClass::kKernel, OpDesc{},
+                       {}, outputs, LaunchConfig{1, 1, 1, 1, 1, 1},
+                       CompilationTarget{KernelArtifactKind::kStaticLibrary, hip::kStaticArtifact, entry}, kargs};
+    hip::HipBackend backend;
+    status = backend.execute(e);
+  }
+  if (!status.ok()) throw_status(status);
+  return HipTensor{std::move(outputs[0])};
+}
+
+py::array to_numpy(const HipTensor& t) {
+  std::vector<py::ssize_t> shape(t.tensor.shape.begin(), t.tensor.shape.end());
+  py::array out;
+  if (t.tensor.dtype == DType::kFloat32)
+    out = py::array_t<float>(shape);
+  else if (t.tensor.dtype == DType::kInt32)
+    out = py::array_t<std::int32_t>(shape);
+  else
+    throw py::value_error("unsupported dtype");
+  const std::size_t bytes = static_cast<std::size_t>(out.nbytes());
+  Status status;
+  {
+    void* dst = out.mutable_data();
+    py::gil_scoped_release release;
+    status = hip::to_host(t.tensor, dst, bytes);
+  }
+  if (!status.ok()) throw_status(status);
+  return out;
+}
+
+HipTensor from_numpy(py::array array) {
+  DType dtype;
+  py::array contiguous;
+  if (py::isinstance<py::array_t<float>>(array)) {
+    dtype = DType::kFloat32;
+    contiguous = py::array_t<float, py::array::c_style | py::array::forcecast>(array);
+  } else if (py::isinstance<py::array_t<std::int32_t>>(array)) {
+    dtype = DType::kInt32;
+    contiguous = py::array_t<std::int32_t, py::array::c_style | py::array::forcecast>(array);
+  } else {
+    throw py::value_error("hip tensors are created from float32 or int32 arrays");
+  }
+  Shape shape;
+  for (py::ssize_t i = 0; i < contiguous.ndim(); ++i) shape.push_back(contiguous.shape(i));
+  Expected<Tensor> created = Status();
+  {
+    const void* src = contiguous.data();
+    py::gil_scoped_release release;
+    created = hip::from_host(src, dtype, std::move(shape));
+  }
+  if (!created) throw_status(created.status());
+  return HipTensor{created.move_value()};
+}
+
+struct PoolHandle {
+  tcx_hip_pool_t* pool{nullptr};
+  PoolHandle(std::size_t bytes, std::size_t blocks) {
+    const int rc = tcx_hip_pool_create(bytes, blocks, nullptr, &pool);
+    if (rc != TCX_OK) {
+      if (rc == TCX_INVALID_ARGUMENT) throw py::value_error(tcx_hip_last_error());
+      throw std::runtime_error(tcx_hip_last_error());
+    }
+  }
+  ~PoolHandle() { tcx_hip_pool_destroy(pool); }
+  void check(int rc) {
+    if (rc == TCX_OK) return;
+    if (rc == TCX_INVALID_ARGUMENT) throw py::value_error(tcx_hip_last_error());
+    throw std::runtime_error(tcx_hip_last_error());
+  }
+};
+
+}  // namespace
+
+PYBIND11_MODULE(_core, m) {
+  m.doc() = "tensor.cx hip device (MI355X / gfx950)";
+
+  py::class_<HipTensor>(m, "HipTensor")
+      .def_property_readonly("shape", [](const HipTensor& t) { return py::tuple(py::cast(std::vector<std::int64_t>(t.tensor.shape.begin(), t.tensor.shape.end()))); })
+      .def_property_readonly("strides", [](const HipTensor& t) { return py::tuple(py::cast(std::vector<std::int64_t>(t.tensor.strides.begin(), t.tensor.strides.end()))); })
+      .def_property_readonly("dtype", [](const HipTensor& t) { return std::string(dtype_name(t.tensor.dtype)); })
+      .def_property_readonly("device", [](const HipTensor&) { return std::string("hip"); })
+      .def_property_readonly("nbytes", [](const HipTensor& t) { return numel(t.tensor.shape) * static_cast<std::int64_t>(dtype_size(t.tensor.dtype)); })
+      .def("numpy", &to_numpy);
+
+  m.def("is_available", [] { return hip::available(); });
+  m.def("device_info", [] {
+    auto info = hip::device_info();
+    if (!info) throw_status(info.status());
+    const auto& d = info.value();
+    py::dict out;
+    out["name"] = d.name;
+    out["arch"] = d.arch;
+    out["compute_units"] = d.compute_units;
+    out["clock_khz"] = d.clock_khz;
+    out["memory_clock_khz"] = d.memory_clock_khz;
+    out["memory_bus_width"] = d.memory_bus_width;
+    out["l2_bytes"] = d.l2_bytes;
+    out["runtime_version"] = d.runtime_version;
+    out["driver_version"] = d.driver_version;
+    out["free_bytes"] = d.free_bytes;
+    out["total_bytes"] = d.total_bytes;
+    return out;
+  });
+  m.def("from_numpy", &from_numpy);
+  m.def("empty", [](std::vector<std::int64_t> shape, const std::string& dtype) {
+    auto t = hip::empty(to_shape(shape), parse_dtype(dtype));
+    if (!t) throw_status(t.status());
+    return HipTensor{t.move_value()};
+  });
+  m.def("fill", [](std::vector<std::int64_t> shape, const std::string& dtype, double value) {
+    Shape s = to_shape(shape);
+    OpDesc op{OpKind::kFill};
+    op.scalar_value = value;
+    std::array<Tensor, 1> outputs{Tensor{parse_dtype(dtype), s, contiguous_strides(s), Device{"hip", 0}, nullptr, 0}};
+    Status status;
+    {
+      py::gil_scoped_release release;
+      BackendExecution e{BackendOpClass::kPrimitive, op, {}, outputs, std::nullopt, std::nullopt, {}};
+      hip::HipBackend backend;
+      status = backend.execute(e);
+    }
+    if (!status.ok()) throw_status(status);
+    return HipTensor{std::move(outputs[0])};
+  });
+  m.def("reshape", [](const HipTensor& x, std::vector<std::int64_t> shape) {
+    Shape s = to_shape(shape);
+    if (numel(s) != numel(x.tensor.shape)) throw py::value_error("reshape size mismatch");
+    Tensor t = x.tensor;
+    t.shape = s;
+    t.strides = contiguous_strides(s);
+    return HipTensor{std::move(t)};
+  });
+  m.def("_shares_storage", [](const HipTensor& a, const HipTensor& b) {
+    return a.tensor.buffer && b.tensor.buffer &&
+           a.tensor.buffer->storage_relation(*b.tensor.buffer) != StorageRelation::kDisjoint;
+  });
+
+  m.def("matmul", [](const HipTensor& a, const HipTensor& b) { return run(OpDesc{OpKind::kMatmul}, {a.tensor, b.tensor}); });
+  m.def("linear", [](const HipTensor& x, const HipTensor& w, std::optional<const HipTensor*> b) {
+    std::vector<Tensor> in{x.tensor, w.tensor};
+    if (b && *b) in.push_back((*b)->tensor);
+    return run(OpDesc{OpKind::kLinear}, std::move(in));
+  }, py::arg("x"), py::arg("weight"), py::arg("bias") = py::none());
+  m.def("linear_act", [](const HipTensor& x, const HipTensor& w, const HipTensor& b, std::uint32_t act) {
+    Shape shape = x.tensor.shape;
+    if (shape.empty() || w.tensor.shape.size() != 2) throw py::value_error("linear requires (..., in_features) and (out_features, in_features)");
+    shape.back() = w.tensor.shape[0];
+    return builtin("linear_bias_act", {&x, &w, &b}, act, shape);
+  });
+  m.def("bias_act", [](const HipTensor& x, const HipTensor& b, std::uint32_t act) {
+    return builtin("bias_act", {&x, &b}, act, x.tensor.shape);
+  });
+
+  for (const auto& [name, kind] : std::vector<std::pair<const char*, OpKind>>{
+           {"sum", OpKind::kSum}, {"max", OpKind::kMax}, {"mean", OpKind::kMean}}) {
+    const OpKind k = kind;
+    m.def(name, [k](const HipTensor& x, std::int64_t axis) { return axis_op(k, x, axis); }, py::arg("x"), py::arg("axis") = 0);
+    m.def((std::string("_") + name + "_axes").c_str(),
+          [k](const HipTensor& x, std::vector<std::int64_t> axes) { return axes_op(k, x, axes); });
+  }
+  m.def("_min_axes", [](const HipTensor& x, std::vector<std::int64_t> axes) { return axes_op(OpKind::kMin, x, axes); });
+  m.def("_argmax_axes", [](const HipTensor& x, std::vector<std::int64_t> axes) { return axes_op(OpKind::kArgmax, x, axes); });
+  m.def("softmax", [](const HipTensor& x, std::int64_t axis) { return axis_op(OpKind::kSoftmax, x, axis); }, py::arg("x"), py::arg("axis"));
+  m.def("rmsnorm", [](const HipTensor& x, std::int64_t axis, double eps) { return axis_op(OpKind::kRmsNorm, x, axis, eps); },
+        py::arg("x"), py::arg("axis"), py::arg("eps") = 1e-5);
+  m.def("layernorm", [](const HipTensor& x, std::int64_t axis, double eps) { return axis_op(OpKind::kLayerNorm, x, axis, eps); },
+        py::arg("x"), py::arg("axis"), py::arg("eps") = 1e-5);
+  m.def("_affine_norm", [](const HipTensor& x, std::optional<const HipTensor*> w, std::optional<const HipTensor*> b,
+                           std::int64_t axis, double eps, bool rms) {
+    OpDesc op{rms ? OpKind::kAffineRmsNorm : OpKind::kAffineLayerNorm};
+    op.axis = axis;
+    op.epsilon = eps;
+    std::vector<Tensor> in{x.tensor};
+    if (w && *w) {
+      op.has_weight = true;
+      in.push_back((*w)->tensor);
+    }
+    if (b && *b) {
+      op.has_bias = true;
+      in.push_back((*b)->tensor);
+    }
+    return run(op, std::move(in));
+  });
+  m.def("exp", [](const HipTensor& x) { return unary(OpKind::kExp, x); });
+  m.def("gelu", [](const HipTensor& x) { return unary(OpKind::kGelu, x); });
+  m.def("silu", [](const HipTensor& x) { return unary(OpKind::kSilu, x); });
+  for (const auto& [name, kind] : std::vector<std::pair<const char*, OpKind>>{
+           {"add", OpKind::kAdd}, {"subtract", OpKind::kSubtract}, {"multiply", OpKind::kMultiply},
+           {"divide", OpKind::kDivide}}) {
+    const OpKind k = kind;
+    m.def(name, [k](const HipTensor& a, const HipTensor& b) { return run(OpDesc{k}, {a.tensor, b.tensor}); });
+  }
+
+  py::class_<PoolHandle>(m, "MemoryPool")
+      .def(py::init<std::size_t, std::size_t>(), py::arg("max_cached_bytes"), py::arg("max_cached_blocks") = 64)
+      .def("enter", [](PoolHandle& p) { p.check(tcx_hip_pool_enter(p.pool)); })
+      .def("exit", [](PoolHandle& p) { p.check(tcx_hip_pool_exit(p.pool)); })
+      .def("trim", [](PoolHandle& p) { p.check(tcx_hip_pool_trim(p.pool)); })
+      .def("stats", [](PoolHandle& p) {
+        tcx_hip_pool_stats_t s{};
+        p.check(tcx_hip_pool_stats(p.pool, &s));
+        py::dict d;
+        d["max_cached_bytes"] = s.max_cached_bytes;
+        d["max_cached_blocks"] = s.max_cached_blocks;
+        d["cached_bytes"] = s.cached_bytes;
+        d["cached_blocks"] = s.cached_blocks;
+        d["in_use_bytes"] = s.in_use_bytes;
+        d["peak_in_use_bytes"] = s.peak_in_use_bytes;
+        d["peak_cached_bytes"] = s.peak_cached_bytes;
+        d["hits"] = s.hits;
+        d["misses"] = s.misses;
+        d["allocation_calls"] = s.allocation_calls;
+        d["free_calls"] = s.free_calls;
+        d["allocation_failures"] = s.allocation_failures;
+        d["oom_retries"] = s.oom_retries;
+        d["uncached_returns"] = s.uncached_returns;
+        d["readiness_failures"] = s.readiness_failures;
+        d["free_failures"] = s.free_failures;
+        d["failed_free_bytes"] = s.failed_free_bytes;
+        d["active"] = s.active != 0;
+        return d;
+      });
+}

@@ -1,0 +1,637 @@
+// HipBackend::execute: the hip device's implementation of the reference
+// backend contract (reference backends/cuda/cuda_backend.cpp:290-627 is the
+// slot it fills; semantics follow the CPU reference, cpu_backend.cpp).
+
+#include "tensorcx/backends/hip/hip_backend.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+namespace tensorcx::hip {
+namespace {
+
+// Thrown for a missing or unusable device; mapped to kUnavailable.
+struct Unavailable : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+void ok_or_throw(int code, const char* what) {
+  if (code == TCX_OK) return;
+  const std::string message = std::string(what) + ": " + tcx_hip_last_error();
+  if (code == TCX_INVALID_ARGUMENT) throw std::invalid_argument(message);
+  if (code == TCX_UNAVAILABLE) throw Unavailable(message);
+  throw std::runtime_error(message);
+}
+
+Status status_from_code(int code, const std::string& what) {
+  if (code == TCX_OK) return Status::Ok();
+  const std::string message = what + ": " + tcx_hip_last_error();
+  if (code == TCX_INVALID_ARGUMENT) return Status(StatusCode::kInvalidArgument, message);
+  if (code == TCX_UNAVAILABLE) return Status(StatusCode::kUnavailable, message);
+  return Status(StatusCode::kInternal, message);
+}
+
+tcx_stream_t stream() {
+  tcx_stream_t s = nullptr;
+  ok_or_throw(tcx_hip_stream(&s), "HIP stream");
+  return s;
+}
+
+int tcx_dtype(DType dtype) {
+  if (dtype == DType::kFloat32) return TCX_FLOAT32;
+  if (dtype == DType::kInt32) return TCX_INT32;
+  throw std::invalid_argument("HIP tensors support float32 and int32");
+}
+
+// Validates hip tensor metadata (the from_core_tensor checks of
+// cuda_backend.cpp) and returns its device pointer.
+void* device_ptr(const Tensor& t) {
+  if (t.device.type != "hip") throw std::invalid_argument("HIP operations require HIP tensors");
+  if (t.device.index != 0) throw std::invalid_argument("HIP tensor metadata requires device index 0");
+  if (t.offset != 0) throw std::invalid_argument("HIP tensor metadata with non-zero offset is unsupported");
+  if (t.strides != contiguous_strides(t.shape)) throw std::invalid_argument("HIP tensor metadata must be contiguous");
+  const auto* buffer = dynamic_cast<const HipBuffer*>(t.buffer.get());
+  if (buffer == nullptr) throw std::invalid_argument("HIP tensor metadata requires a HIP buffer");
+  const auto bytes = static_cast<std::size_t>(numel(t.shape)) * dtype_size(t.dtype);
+  if (buffer->nbytes() < bytes) throw std::invalid_argument("HIP tensor buffer is smaller than its shape");
+  return buffer->data();
+}
+
+const float* f32(const Tensor& t) {
+  if (t.dtype != DType::kFloat32) throw std::invalid_argument("operation requires float32 tensors");
+  return static_cast<const float*>(device_ptr(t));
+}
+
+Tensor make_tensor(DType dtype, Shape shape) {
+  auto created = empty(std::move(shape), dtype);
+  if (!created) {
+    const Status& s = created.status();
+    if (s.code() == StatusCode::kUnavailable) throw Unavailable(s.message());
+    if (s.code() == StatusCode::kInvalidArgument) throw std::invalid_argument(s.message());
+    throw std::runtime_error(s.message());
+  }
+  return created.move_value();
+}
+
+void* out_ptr(const Tensor& t) { return static_cast<HipBuffer*>(t.buffer.get())->data(); }
+
+// ------------------------------------------------------------ reductions
+struct RowDims {
+  Shape output_shape;
+  Dim outer, reduce, inner;
+};
+
+Dim normalize_axis(Dim axis, std::size_t rank) {
+  if (rank == 0) {
+    if (axis == 0 || axis == -1) return 0;
+    throw std::invalid_argument("reduction axis is out of range");
+  }
+  const Dim r = static_cast<Dim>(rank);
+  if (axis < 0) axis += r;
+  if (axis < 0 || axis >= r) throw std::invalid_argument("reduction axis is out of range");
+  return axis;
+}
+
+// (outer, reduce, inner) of a single-axis op (cpu_backend.cpp:93-123).
+RowDims row_dims(const Shape& shape, Dim axis) {
+  const Dim a = normalize_axis(axis, shape.size());
+  if (shape.empty()) return {{}, 1, 1, 1};
+  RowDims d{{}, 1, shape[static_cast<std::size_t>(a)], contiguous_strides(shape)[static_cast<std::size_t>(a)]};
+  for (std::size_t i = 0; i < shape.size(); ++i) {
+    if (static_cast<Dim>(i) < a) d.outer *= shape[i];
+    if (static_cast<Dim>(i) != a) d.output_shape.push_back(shape[i]);
+  }
+  return d;
+}
+
+int reduce_code(OpKind kind) {
+  switch (kind) {
+    case OpKind::kSum: return TCX_REDUCE_SUM;
+    case OpKind::kMax: return TCX_REDUCE_MAX;
+    case OpKind::kMean: return TCX_REDUCE_MEAN;
+    case OpKind::kMin: return TCX_REDUCE_MIN;
+    case OpKind::kArgmax: return TCX_REDUCE_ARGMAX;
+    default: throw std::invalid_argument("unsupported reduction");
+  }
+}
+
+void run_rows(int code, const Tensor& x, const Tensor& out, Dim outer, Dim reduce, Dim inner, tcx_stream_t s) {
+  const int dtype = tcx_dtype(x.dtype);
+  const std::size_t ws = tcx_hip_reduce_workspace_bytes(code, dtype, outer, reduce, inner);
+  std::shared_ptr<HipBuffer> workspace;
+  if (ws) {
+    auto created = HipBuffer::create(ws);
+    if (!created) throw std::runtime_error(created.status().message());
+    workspace = created.move_value();
+  }
+  ok_or_throw(tcx_hip_reduce(code, dtype, device_ptr(x), out_ptr(out), outer, reduce, inner,
+                             workspace ? workspace->data() : nullptr, ws, s),
+              "HIP reduction");
+  if (workspace) ok_or_throw(tcx_hip_stream_synchronize(s), "HIP reduction");
+}
+
+// Reduction over an axis selection: adjacent reduced axes become one
+// (outer, reduce, inner) reduction with the same element order; any other
+// selection runs the general metadata kernel.
+void run_selection(int code, const Tensor& x, const Tensor& out, const Shape& axes, const ReductionPlan& plan,
+                   tcx_stream_t s) {
+  const Shape& shape = x.shape;
+  const Dim rank = static_cast<Dim>(shape.size());
+  std::vector<bool> selected(shape.size(), false);
+  for (Dim a : axes) selected[static_cast<std::size_t>(a < 0 ? a + rank : a)] = true;
+  Dim first = -1, last = -1;
+  for (Dim i = 0; i < rank; ++i)
+    if (selected[static_cast<std::size_t>(i)]) {
+      if (first < 0) first = i;
+      last = i;
+    }
+  bool adjacent = first >= 0;
+  for (Dim i = first; adjacent && i <= last; ++i) adjacent = selected[static_cast<std::size_t>(i)];
+  if (adjacent && plan.reduction_size != 0) {
+    Dim outer = 1, reduce = 1, inner = 1;
+    for (Dim i = 0; i < rank; ++i) {
+      const Dim e = shape[static_cast<std::size_t>(i)];
+      if (i < first) outer *= e;
+      else if (i <= last) reduce *= e;
+      else inner *= e;
+    }
+    run_rows(code, x, out, outer, reduce, inner, s);
+    return;
+  }
+  if (rank > TCX_HIP_MAX_RANK) throw std::invalid_argument("HIP reductions support rank <= 8");
+  ok_or_throw(tcx_hip_reduce_axes(code, tcx_dtype(x.dtype), device_ptr(x), out_ptr(out), plan.index_metadata.data(),
+                                  static_cast<int32_t>(plan.output_shape.size()), static_cast<int32_t>(rank),
+                                  numel(plan.output_shape), plan.reduction_size, s),
+              "HIP reduction");
+}
+
+Tensor reduce(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
+  if (x.dtype == DType::kBool) throw std::invalid_argument("numeric reductions do not support bool tensors");
+  (void)device_ptr(x);
+  const int code = reduce_code(op.kind);
+  if (op.reduction_axes) {
+    const auto plan = make_reduction_plan(x.shape, *op.reduction_axes);
+    if (op.kind == OpKind::kMean && x.dtype != DType::kFloat32)
+      throw std::invalid_argument("mean only supports float32 tensors");
+    if (op.kind == OpKind::kMax && plan.reduction_size == 0)
+      throw std::invalid_argument("max reduction requires non-empty axes");
+    if (op.reduction_axes->empty()) {
+      auto copy = clone(x);
+      if (!copy) throw std::runtime_error(copy.status().message());
+      return copy.move_value();
+    }
+    Tensor out = make_tensor(x.dtype, plan.output_shape);
+    if (numel(plan.output_shape) != 0) run_selection(code, x, out, *op.reduction_axes, plan, s);
+    return out;
+  }
+  const RowDims d = row_dims(x.shape, op.axis);
+  if (op.kind == OpKind::kMax && d.reduce == 0) throw std::invalid_argument("max reduction requires a non-empty axis");
+  if (op.kind == OpKind::kMean && x.dtype != DType::kFloat32)
+    throw std::invalid_argument("mean only supports float32 tensors");
+  Tensor out = make_tensor(x.dtype, d.output_shape);
+  if (numel(d.output_shape) != 0) run_rows(code, x, out, d.outer, d.reduce, d.inner, s);
+  return out;
+}
+
+// min / argmax with the reference math plan (core/math.cpp:39-56).
+Tensor argext(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
+  if (x.dtype != DType::kFloat32 && x.dtype != DType::kInt32)
+    throw std::invalid_argument("math operations require float32 or int32 tensors");
+  (void)device_ptr(x);
+  const Shape axes = op.reduction_axes.value_or(x.shape.empty() ? Shape{} : Shape{op.axis});
+  if (x.shape.empty() && !op.reduction_axes && op.axis != 0 && op.axis != -1)
+    throw std::invalid_argument("reduction axis out of range");
+  const auto plan = make_reduction_plan(x.shape, axes);
+  if (plan.reduction_size == 0) throw std::invalid_argument("min/argmax require a non-empty reduction");
+  DType out_dtype = x.dtype;
+  if (op.kind == OpKind::kArgmax) {
+    Dim extent = 1;
+    for (Dim a : axes) {
+      if (a < 0) a += static_cast<Dim>(x.shape.size());
+      const Dim e = x.shape[static_cast<std::size_t>(a)];
+      if (e > std::numeric_limits<std::int32_t>::max() / extent)
+        throw std::invalid_argument("argmax index range exceeds int32");
+      extent *= e;
+    }
+    out_dtype = DType::kInt32;
+  }
+  Tensor out = make_tensor(out_dtype, plan.output_shape);
+  if (numel(plan.output_shape) == 0) return out;
+  const int code = reduce_code(op.kind);
+  if (axes.empty()) {
+    // No reduced axes: every element is its own group of one.
+    ok_or_throw(tcx_hip_reduce(code, tcx_dtype(x.dtype), device_ptr(x), out_ptr(out), numel(x.shape), 1, 1,
+                               nullptr, 0, s),
+                "HIP reduction");
+    return out;
+  }
+  run_selection(code, x, out, axes, plan, s);
+  return out;
+}
+
+// ------------------------------------------------------------ row ops
+float checked_epsilon(double eps) {
+  const float rounded = static_cast<float>(eps);
+  if (!std::isfinite(eps) || eps < 0.0 || eps > static_cast<double>(std::numeric_limits<float>::max()) ||
+      (eps > 0.0 && rounded == 0.0F))
+    throw std::invalid_argument("epsilon must be finite and non-negative and representable as float32");
+  return rounded;
+}
+
+Tensor row_op(const OpDesc& op, const Tensor& x, const Tensor* gamma, const Tensor* beta, tcx_stream_t s) {
+  const RowDims d = row_dims(x.shape, op.axis);
+  const char* name = op.kind == OpKind::kSoftmax ? "softmax" : op.kind == OpKind::kRmsNorm ? "rmsnorm" : "layernorm";
+  float eps = 0.F;
+  if (op.kind != OpKind::kSoftmax) eps = checked_epsilon(op.epsilon);
+  if (x.dtype != DType::kFloat32) throw std::invalid_argument(std::string(name) + " only supports float32 tensors");
+  const float* xp = f32(x);
+  const float* g = gamma ? f32(*gamma) : nullptr;
+  const float* b = beta ? f32(*beta) : nullptr;
+  Tensor out = make_tensor(DType::kFloat32, x.shape);
+  if (numel(x.shape) == 0) return out;
+  auto* o = static_cast<float*>(out_ptr(out));
+  int rc = TCX_OK;
+  if (op.kind == OpKind::kSoftmax)
+    rc = tcx_hip_softmax_f32(xp, o, d.outer, d.reduce, d.inner, s);
+  else if (op.kind == OpKind::kRmsNorm)
+    rc = tcx_hip_rmsnorm_f32(xp, g, o, d.outer, d.reduce, d.inner, eps, s);
+  else
+    rc = tcx_hip_layernorm_f32(xp, g, b, o, d.outer, d.reduce, d.inner, eps, s);
+  ok_or_throw(rc, name);
+  return out;
+}
+
+// kAffineRmsNorm / kAffineLayerNorm with the validation of
+// core/inference.cpp:103-122, computed in one fused pass.
+Tensor affine_norm(const OpDesc& op, std::span<const Tensor> inputs, tcx_stream_t s) {
+  const bool rms = op.kind == OpKind::kAffineRmsNorm;
+  if (inputs.size() != 1U + op.has_weight + op.has_bias || (rms && op.has_bias))
+    throw std::invalid_argument("invalid affine normalization parameters");
+  for (const Tensor& t : inputs) {
+    if (t.dtype != DType::kFloat32) throw std::invalid_argument("inference values require float32 tensors");
+    (void)device_ptr(t);
+  }
+  const Tensor& x = inputs[0];
+  Dim axis = op.axis;
+  if (x.shape.empty()) {
+    if (axis != 0 && axis != -1) throw std::invalid_argument("normalization axis out of range");
+    axis = 0;
+  } else {
+    if (axis < 0) axis += static_cast<Dim>(x.shape.size());
+    if (axis < 0 || axis >= static_cast<Dim>(x.shape.size()))
+      throw std::invalid_argument("normalization axis out of range");
+  }
+  const Shape expected = x.shape.empty() ? Shape{} : Shape{x.shape[static_cast<std::size_t>(axis)]};
+  for (std::size_t i = 1; i < inputs.size(); ++i)
+    if (inputs[i].shape != expected) throw std::invalid_argument("affine parameters must match the normalized axis");
+  const float narrowed = static_cast<float>(op.epsilon);
+  if (!std::isfinite(op.epsilon) || !std::isfinite(narrowed) || op.epsilon < 0 || (op.epsilon > 0 && narrowed == 0))
+    throw std::invalid_argument("epsilon must be finite, non-negative and representable as float32");
+  OpDesc base{rms ? OpKind::kRmsNorm : OpKind::kLayerNorm, op.axis, op.epsilon};
+  const Tensor* gamma = op.has_weight ? &inputs[1] : nullptr;
+  const Tensor* beta = op.has_bias ? &inputs[op.has_weight ? 2 : 1] : nullptr;
+  return row_op(base, x, gamma, beta, s);
+}
+
+// ------------------------------------------------------------ matmul / linear
+Tensor matmul(const Tensor& lhs, const Tensor& rhs, tcx_stream_t s) {
+  if (lhs.dtype != DType::kFloat32 || rhs.dtype != DType::kFloat32)
+    throw std::invalid_argument("matmul only supports float32 tensors");
+  const float* a = f32(lhs);
+  const float* b = f32(rhs);
+  const MatmulPlan plan = make_matmul_plan(lhs.shape, rhs.shape);
+  if (plan.batch_shape.size() > TCX_HIP_MAX_BATCH_RANK)
+    throw std::invalid_argument("HIP matmul supports at most 8 batch dimensions");
+  Tensor out = make_tensor(DType::kFloat32, plan.output_shape);
+  if (numel(plan.output_shape) == 0) return out;
+  tcx_hip_gemm_desc_t d{};
+  d.m = plan.m;
+  d.n = plan.n;
+  d.k = plan.k;
+  // Batches that only walk the lhs contiguously (rhs shared) are one taller
+  // GEMM: rows of consecutive batches are adjacent in both lhs and out.
+  bool rhs_shared = true, lhs_dense = true;
+  Dim expect = plan.m * plan.k;
+  for (std::size_t i = plan.batch_shape.size(); i-- > 0;) {
+    rhs_shared = rhs_shared && plan.rhs_batch_strides[i] == 0;
+    lhs_dense = lhs_dense && (plan.batch_shape[i] == 1 || plan.lhs_batch_strides[i] == expect);
+    expect *= plan.batch_shape[i];
+  }
+  const Dim batches = numel(plan.batch_shape);
+  if (rhs_shared && lhs_dense) {
+    d.m = plan.m * batches;
+    d.batch_count = 1;
+    d.batch_rank = 0;
+  } else {
+    d.batch_count = batches;
+    d.batch_rank = static_cast<int32_t>(plan.batch_shape.size());
+    for (std::size_t i = 0; i < plan.batch_shape.size(); ++i) {
+      d.batch_shape[i] = plan.batch_shape[i];
+      d.lhs_batch_strides[i] = plan.lhs_batch_strides[i];
+      d.rhs_batch_strides[i] = plan.rhs_batch_strides[i];
+    }
+  }
+  ok_or_throw(tcx_hip_gemm_f32(a, b, static_cast<float*>(out_ptr(out)), &d, s), "HIP matmul");
+  return out;
+}
+
+// y = act(x @ weight^T + bias) for x (..., in) and weight (out, in), writing
+// into `out` (contiguous (..., out)). One NT GEMM with the bias and activation
+// in its epilogue: the kLinear composite of core/inference.cpp:89-102 without
+// the transposed weight copy.
+void linear_into(const Tensor& x, const Tensor& w, const Tensor* bias, int act, const Tensor& out, tcx_stream_t s) {
+  tcx_hip_gemm_desc_t d{};
+  d.k = w.shape[1];
+  d.n = w.shape[0];
+  d.m = numel(out.shape) / d.n;  // callers pass a non-empty output, so n > 0
+  d.batch_count = 1;
+  d.rhs_transposed = 1;
+  d.bias = bias ? f32(*bias) : nullptr;
+  d.activation = act;
+  ok_or_throw(tcx_hip_gemm_f32(f32(x), f32(w), static_cast<float*>(out_ptr(out)), &d, s), "HIP linear");
+}
+
+Shape linear_shape(std::span<const Tensor> inputs) {
+  if (inputs.size() < 2 || inputs.size() > 3)
+    throw std::invalid_argument("linear requires input, weight and optional bias");
+  for (const Tensor& t : inputs) {
+    if (t.dtype != DType::kFloat32) throw std::invalid_argument("inference values require float32 tensors");
+    (void)device_ptr(t);
+  }
+  const Tensor& x = inputs[0];
+  const Tensor& w = inputs[1];
+  if (x.shape.empty() || w.shape.size() != 2 || x.shape.back() != w.shape[1])
+    throw std::invalid_argument("linear requires (..., in_features) and (out_features, in_features)");
+  if (inputs.size() == 3 && inputs[2].shape != Shape{w.shape[0]})
+    throw std::invalid_argument("linear bias must have shape (out_features,)");
+  Shape shape = x.shape;
+  shape.back() = w.shape[0];
+  (void)numel(shape);
+  return shape;
+}
+
+Tensor linear(std::span<const Tensor> inputs, tcx_stream_t s) {
+  const Shape shape = linear_shape(inputs);
+  Tensor out = make_tensor(DType::kFloat32, shape);
+  if (numel(shape) == 0) return out;
+  linear_into(inputs[0], inputs[1], inputs.size() == 3 ? &inputs[2] : nullptr, TCX_ACT_NONE, out, s);
+  return out;
+}
+
+// ------------------------------------------------------------ elementwise
+Tensor unary(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
+  const int code = op.kind == OpKind::kExp ? TCX_UNARY_EXP : op.kind == OpKind::kGelu ? TCX_UNARY_GELU : TCX_UNARY_SILU;
+  if (x.dtype != DType::kFloat32) {
+    const char* name = code == TCX_UNARY_EXP ? "exp" : code == TCX_UNARY_GELU ? "gelu" : "silu";
+    throw std::invalid_argument(std::string(name) + " only supports float32 tensors");
+  }
+  const float* xp = f32(x);
+  Tensor out = make_tensor(DType::kFloat32, x.shape);
+  ok_or_throw(tcx_hip_unary_f32(code, xp, static_cast<float*>(out_ptr(out)), numel(x.shape), s), "HIP unary");
+  return out;
+}
+
+Tensor binary(const OpDesc& op, const Tensor& lhs, const Tensor& rhs, tcx_stream_t s) {
+  if (lhs.dtype == DType::kBool || rhs.dtype == DType::kBool)
+    throw std::invalid_argument("arithmetic does not support bool tensors");
+  if (lhs.dtype != rhs.dtype) throw std::invalid_argument("dtype mismatch for binary operation");
+  const int code = op.kind == OpKind::kAdd        ? TCX_BINARY_ADD
+                   : op.kind == OpKind::kSubtract ? TCX_BINARY_SUBTRACT
+                   : op.kind == OpKind::kMultiply ? TCX_BINARY_MULTIPLY
+                                                  : TCX_BINARY_DIVIDE;
+  if (code == TCX_BINARY_DIVIDE && lhs.dtype != DType::kFloat32)
+    throw std::invalid_argument("division only supports float32 tensors");
+  const void* l = device_ptr(lhs);
+  const void* r = device_ptr(rhs);
+  const BroadcastPlan plan = make_broadcast_plan(lhs.shape, rhs.shape);
+  if (plan.output_shape.size() > TCX_HIP_MAX_RANK) throw std::invalid_argument("HIP arithmetic supports rank <= 8");
+  Tensor out = make_tensor(lhs.dtype, plan.output_shape);
+  if (numel(plan.output_shape) == 0) return out;
+  // Row-vector bias on float32 addition: the fused bias kernel, same rounding.
+  const Shape& os = plan.output_shape;
+  if (code == TCX_BINARY_ADD && lhs.dtype == DType::kFloat32 && lhs.shape == os && !os.empty() &&
+      rhs.shape == Shape{os.back()}) {
+    const Dim cols = os.back();
+    ok_or_throw(tcx_hip_bias_act_f32(static_cast<const float*>(l), static_cast<const float*>(r),
+                                     static_cast<float*>(out_ptr(out)), numel(os) / cols, cols, TCX_ACT_NONE, s),
+                "HIP add");
+    return out;
+  }
+  ok_or_throw(tcx_hip_binary(code, tcx_dtype(lhs.dtype), l, r, out_ptr(out), static_cast<int32_t>(os.size()),
+                             os.data(), plan.lhs_strides.data(), plan.rhs_strides.data(), s),
+              "HIP arithmetic");
+  return out;
+}
+
+Tensor fill(const Tensor& descriptor, double value, tcx_stream_t s) {
+  if (descriptor.dtype == DType::kInt32 && !is_int32_representable(value))
+    throw std::invalid_argument("fill value must be an integer in int32 range");
+  Tensor out = make_tensor(descriptor.dtype, descriptor.shape);
+  ok_or_throw(tcx_hip_fill(tcx_dtype(descriptor.dtype), out_ptr(out), numel(descriptor.shape), value, s), "HIP fill");
+  return out;
+}
+
+// ------------------------------------------------------------ kernel class
+Status execute_builtin_kernel(const BackendExecution& e) {
+  if (Status s = validate_kernel_execution_contract(e); !s.ok()) return s;
+  const auto& target = *e.compilation_target;
+  if (target.artifact_kind != KernelArtifactKind::kStaticLibrary || target.artifact != kStaticArtifact)
+    return Status(StatusCode::kInvalidArgument, "HIP kernels must name the tensorcx_hip static library");
+  std::vector<const Tensor*> tensors;
+  std::vector<std::uint32_t> scalars;
+  for (const KernelArgument& a : e.kernel_arguments) {
+    if (a.kind == KernelArgumentKind::kTensor)
+      tensors.push_back(a.tensor);
+    else
+      scalars.push_back(a.uint32_value);
+  }
+  if (e.outputs.size() != 1) return Status(StatusCode::kInvalidArgument, "HIP built-in kernels write one output");
+  const Tensor& out = e.outputs[0];
+  if (out.dtype != DType::kFloat32) return Status(StatusCode::kInvalidArgument, "HIP built-in kernels write float32");
+  (void)device_ptr(out);
+  if (scalars.size() != 1 || scalars[0] > TCX_ACT_GELU)
+    return Status(StatusCode::kInvalidArgument, "HIP built-in kernels take one activation code");
+  const int act = static_cast<int>(scalars[0]);
+  const tcx_stream_t s = stream();
+  if (target.entry_point == "linear_bias_act") {
+    if (tensors.size() != 3) return Status(StatusCode::kInvalidArgument, "linear_bias_act takes x, weight, bias");
+    const Tensor inputs[3] = {*tensors[0], *tensors[1], *tensors[2]};
+    if (linear_shape(inputs) != out.shape)
+      return Status(StatusCode::kInvalidArgument, "linear_bias_act output shape mismatch");
+    if (numel(out.shape) != 0) linear_into(inputs[0], inputs[1], &inputs[2], act, out, s);
+  } else if (target.entry_point == "bias_act") {
+    if (tensors.size() != 2) return Status(StatusCode::kInvalidArgument, "bias_act takes x and bias");
+    const Tensor& x = *tensors[0];
+    const Tensor& b = *tensors[1];
+    if (x.shape.empty() || b.shape != Shape{x.shape.back()} || out.shape != x.shape)
+      return Status(StatusCode::kInvalidArgument, "bias_act requires x (..., n), bias (n,) and a matching output");
+    const Dim cols = x.shape.back();
+    if (numel(x.shape) != 0)
+      ok_or_throw(tcx_hip_bias_act_f32(f32(x), f32(b), static_cast<float*>(out_ptr(out)), numel(x.shape) / cols, cols,
+                                       act, s),
+                  "HIP bias_act");
+  } else {
+    return Status(StatusCode::kInvalidArgument, "unknown HIP built-in kernel entry point");
+  }
+  ok_or_throw(tcx_hip_stream_synchronize(s), "HIP kernel");
+  return Status::Ok();
+}
+
+}  // namespace
+
+// ------------------------------------------------------------ public API
+Expected<std::shared_ptr<HipBuffer>> HipBuffer::create(std::size_t bytes) {
+  std::shared_ptr<HipBuffer> buffer(new HipBuffer());
+  const int rc = tcx_hip_allocate(bytes, &buffer->data_, &buffer->owner_);
+  if (rc != TCX_OK) return status_from_code(rc, "HIP allocation");
+  buffer->bytes_ = bytes;
+  return buffer;
+}
+
+HipBuffer::~HipBuffer() { tcx_hip_release(data_, bytes_, owner_); }
+
+bool available() { return tcx_hip_init() == TCX_OK; }
+
+Expected<DeviceInfo> device_info() {
+  tcx_hip_device_info_t raw{};
+  const int rc = tcx_hip_device_info(0, &raw);
+  if (rc != TCX_OK) return status_from_code(rc, "HIP device info");
+  DeviceInfo info;
+  info.name = raw.name;
+  info.arch = raw.arch;
+  info.compute_units = raw.compute_units;
+  info.clock_khz = raw.clock_khz;
+  info.memory_clock_khz = raw.memory_clock_khz;
+  info.memory_bus_width = raw.memory_bus_width;
+  info.l2_bytes = raw.l2_bytes;
+  info.runtime_version = raw.runtime_version;
+  info.driver_version = raw.driver_version;
+  info.free_bytes = raw.free_bytes;
+  info.total_bytes = raw.total_bytes;
+  return info;
+}
+
+Expected<std::string> device_name() {
+  auto info = device_info();
+  if (!info) return info.status();
+  return info.value().name;
+}
+
+Expected<Tensor> empty(Shape shape, DType dtype) {
+  try {
+    if (dtype != DType::kFloat32 && dtype != DType::kInt32)
+      return Status(StatusCode::kInvalidArgument, "HIP tensors support float32 and int32");
+    const auto bytes = static_cast<std::size_t>(numel(shape)) * dtype_size(dtype);
+    if (const int rc = tcx_hip_init(); rc != TCX_OK) return status_from_code(rc, "HIP device");
+    auto buffer = HipBuffer::create(bytes);
+    if (!buffer) return buffer.status();
+    Shape strides = contiguous_strides(shape);
+    return Tensor{dtype, std::move(shape), std::move(strides), Device{"hip", 0},
+                  std::static_pointer_cast<Buffer>(buffer.move_value()), 0};
+  } catch (const std::invalid_argument& error) {
+    return Status(StatusCode::kInvalidArgument, error.what());
+  }
+}
+
+Expected<Tensor> from_host(const void* host, DType dtype, Shape shape) {
+  auto created = empty(std::move(shape), dtype);
+  if (!created) return created.status();
+  Tensor t = created.move_value();
+  const std::size_t bytes = t.buffer->nbytes();
+  if (bytes) {
+    tcx_stream_t s = nullptr;
+    int rc = tcx_hip_stream(&s);
+    if (rc == TCX_OK) rc = tcx_hip_memcpy_h2d(out_ptr(t), host, bytes, s);
+    if (rc != TCX_OK) return status_from_code(rc, "HIP host to device copy");
+  }
+  return t;
+}
+
+Status to_host(const Tensor& tensor, void* host, std::size_t bytes) {
+  try {
+    const void* src = device_ptr(tensor);
+    const auto need = static_cast<std::size_t>(numel(tensor.shape)) * dtype_size(tensor.dtype);
+    if (bytes != need) return Status(StatusCode::kInvalidArgument, "host buffer size does not match the tensor");
+    if (need == 0) return Status::Ok();
+    tcx_stream_t s = nullptr;
+    int rc = tcx_hip_stream(&s);
+    if (rc == TCX_OK) rc = tcx_hip_memcpy_d2h(host, src, need, s);
+    return status_from_code(rc, "HIP device to host copy");
+  } catch (const std::invalid_argument& error) {
+    return Status(StatusCode::kInvalidArgument, error.what());
+  }
+}
+
+Expected<Tensor> clone(const Tensor& tensor) {
+  try {
+    const void* src = device_ptr(tensor);
+    auto created = empty(tensor.shape, tensor.dtype);
+    if (!created) return created.status();
+    Tensor t = created.move_value();
+    const std::size_t bytes = t.buffer->nbytes();
+    if (bytes) {
+      tcx_stream_t s = nullptr;
+      int rc = tcx_hip_stream(&s);
+      if (rc == TCX_OK) rc = tcx_hip_memcpy_d2d(out_ptr(t), src, bytes, s);
+      if (rc != TCX_OK) return status_from_code(rc, "HIP device copy");
+    }
+    return t;
+  } catch (const std::invalid_argument& error) {
+    return Status(StatusCode::kInvalidArgument, error.what());
+  }
+}
+
+Status HipBackend::execute(const BackendExecution& e) {
+  try {
+    if (e.op_class == BackendOpClass::kKernel) return execute_builtin_kernel(e);
+    if (Status contract = validate_primitive_execution_contract(e, "hip"); !contract.ok()) return contract;
+    if (e.op.kind == OpKind::kFill && e.outputs[0].device.index != 0)
+      return Status(StatusCode::kInvalidArgument, "HIP fill requires device index 0");
+    // Validate every input before touching the device.
+    if (e.op.kind != OpKind::kFill)
+      for (const Tensor& t : e.inputs) (void)device_ptr(t);
+    const tcx_stream_t s = stream();
+    Tensor result;
+    switch (e.op.kind) {
+      case OpKind::kFill: result = fill(e.outputs[0], e.op.scalar_value, s); break;
+      case OpKind::kMatmul: result = matmul(e.inputs[0], e.inputs[1], s); break;
+      case OpKind::kLinear: result = linear(e.inputs, s); break;
+      case OpKind::kSum:
+      case OpKind::kMax:
+      case OpKind::kMean: result = reduce(e.op, e.inputs[0], s); break;
+      case OpKind::kMin:
+      case OpKind::kArgmax: result = argext(e.op, e.inputs[0], s); break;
+      case OpKind::kSoftmax:
+      case OpKind::kRmsNorm:
+      case OpKind::kLayerNorm: result = row_op(e.op, e.inputs[0], nullptr, nullptr, s); break;
+      case OpKind::kAffineRmsNorm:
+      case OpKind::kAffineLayerNorm: result = affine_norm(e.op, e.inputs, s); break;
+      case OpKind::kExp:
+      case OpKind::kGelu:
+      case OpKind::kSilu: result = unary(e.op, e.inputs[0], s); break;
+      case OpKind::kAdd:
+      case OpKind::kSubtract:
+      case OpKind::kMultiply:
+      case OpKind::kDivide: result = binary(e.op, e.inputs[0], e.inputs[1], s); break;
+      default:
+        return Status(StatusCode::kInvalidArgument, "unsupported HIP backend execution operation");
+    }
+    ok_or_throw(tcx_hip_stream_synchronize(s), "HIP execution");
+    e.outputs[0] = std::move(result);  // publish only after the work completed
+    return Status::Ok();
+  } catch (const std::invalid_argument& error) {
+    return Status(StatusCode::kInvalidArgument, error.what());
+  } catch (const Unavailable& error) {
+    return Status(StatusCode::kUnavailable, error.what());
+  } catch (const std::exception& error) {
+    return Status(StatusCode::kInternal, error.what());
+  }
+}
+
+}  // namespace tensorcx::hip

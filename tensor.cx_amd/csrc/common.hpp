@@ -1,0 +1,71 @@
+// Shared helpers for the gfx950 kernels and the C ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "tensorcx_hip.h"
+
+namespace tcx {
+
+// Thread-local failure message behind tcx_hip_last_error().
+void set_error(std::string message);
+int fail(int code, std::string message);
+// Maps a hipError_t to a StatusCode value, recording the message.
+int check(hipError_t error, const char* what);
+// Validates a launch on this thread (runtime ready, not in a forked child).
+int ready();
+
+constexpr int kWave = 64;
+
+using float4_t = float __attribute__((ext_vector_type(4)));
+using int4_t = int __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bool is_nan(float v) { return v != v; }
+
+// Wave-wide butterfly sums: both partners add the same two operands, so every
+// lane ends with identical bits and the order is fixed for a given layout.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
+  return v;
+}
+__device__ __forceinline__ std::uint32_t wave_sum_u32(std::uint32_t v) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1)
+    v += static_cast<std::uint32_t>(__shfl_xor(static_cast<int>(v), offset, kWave));
+  return v;
+}
+
+// (value, index) candidate of an extremum search with the reference's rules
+// (cpu_math.cpp:14-20,48-54; cpu_backend.cpp:1181-1194): a NaN beats every
+// number and the first NaN wins; otherwise the larger (kMax/kArgmax) or smaller
+// (kMin) value wins, +0 and -0 compare equal, and ties keep the lowest index.
+template <bool kLargest>
+__device__ __forceinline__ bool better_f32(float v, std::int64_t i, float best, std::int64_t bi) {
+  const bool vn = is_nan(v), bn = is_nan(best);
+  if (vn != bn) return vn;
+  if (!vn) {
+    if (kLargest ? (v > best) : (v < best)) return true;
+    if (kLargest ? (v < best) : (v > best)) return false;
+  }
+  return i < bi;
+}
+template <bool kLargest>
+__device__ __forceinline__ bool better_i32(int v, std::int64_t i, int best, std::int64_t bi) {
+  if (kLargest ? (v > best) : (v < best)) return true;
+  if (kLargest ? (v < best) : (v > best)) return false;
+  return i < bi;
+}
+
+// Grid helper: enough blocks to cover n items with `per_block` each, capped.
+inline unsigned grid_for(std::int64_t n, std::int64_t per_block, std::int64_t cap = 1 << 20) {
+  std::int64_t g = (n + per_block - 1) / per_block;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return static_cast<unsigned>(g);
+}
+
+}  // namespace tcx

@@ -1,0 +1,209 @@
+// Elementwise kernels: fused bias+activation, exp/gelu/silu, broadcast
+// arithmetic and fill (reference cpu_backend.cpp:1000-1010, 1014-1097 and the
+// fill of cpu_backend.cpp). All are HBM-bound streams with 16-byte accesses
+// where the layout allows; each element is rounded exactly as the reference
+// rounds it (one operation per step, -ffp-contract=off).
+
+#include "common.hpp"
+
+namespace tcx {
+namespace {
+
+__device__ __forceinline__ float act_apply(float v, int act) {
+  if (act == TCX_ACT_SILU) return v / (1.0F + expf(-v));
+  if (act == TCX_ACT_GELU) {
+    const float cubic = 0.044715F * v * v * v;
+    const float inner = 0.7978845608028654F * (v + cubic);
+    return 0.5F * v * (1.0F + tanhf(inner));
+  }
+  return v;
+}
+
+__global__ __launch_bounds__(256) void bias_act_vec_kernel(const float* __restrict__ x,
+                                                           const float* __restrict__ bias,
+                                                           float* __restrict__ out, std::int64_t rows,
+                                                           std::int64_t cols, int act) {
+  const std::int64_t quads = rows * cols / 4;
+  const std::int64_t cq = cols / 4;
+  for (std::int64_t i = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < quads;
+       i += static_cast<std::int64_t>(gridDim.x) * blockDim.x) {
+    float4_t v = reinterpret_cast<const float4_t*>(x)[i];
+    if (bias) {
+      const float4_t b = reinterpret_cast<const float4_t*>(bias)[i % cq];
+      v.x = v.x + b.x; v.y = v.y + b.y; v.z = v.z + b.z; v.w = v.w + b.w;
+    }
+    v.x = act_apply(v.x, act); v.y = act_apply(v.y, act);
+    v.z = act_apply(v.z, act); v.w = act_apply(v.w, act);
+    reinterpret_cast<float4_t*>(out)[i] = v;
+  }
+}
+
+__global__ __launch_bounds__(256) void bias_act_kernel(const float* __restrict__ x, const float* __restrict__ bias,
+                                                       float* __restrict__ out, std::int64_t rows,
+                                                       std::int64_t cols, int act) {
+  const std::int64_t n = rows * cols;
+  for (std::int64_t i = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<std::int64_t>(gridDim.x) * blockDim.x) {
+    float v = x[i];
+    if (bias) v = v + bias[i % cols];
+    out[i] = act_apply(v, act);
+  }
+}
+
+__global__ __launch_bounds__(256) void unary_kernel(const float* __restrict__ x, float* __restrict__ out,
+                                                    std::int64_t n, int op) {
+  for (std::int64_t i = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<std::int64_t>(gridDim.x) * blockDim.x) {
+    const float v = x[i];
+    out[i] = op == TCX_UNARY_EXP ? expf(v) : act_apply(v, op == TCX_UNARY_GELU ? TCX_ACT_GELU : TCX_ACT_SILU);
+  }
+}
+
+struct BroadcastMeta {
+  std::int64_t shape[TCX_HIP_MAX_RANK];
+  std::int64_t lhs[TCX_HIP_MAX_RANK];
+  std::int64_t rhs[TCX_HIP_MAX_RANK];
+  std::int32_t rank;
+};
+
+template <typename T>
+__device__ __forceinline__ T binary_op(T a, T b, int op) {
+  if constexpr (__is_same(T, float)) {
+    switch (op) {
+      case TCX_BINARY_ADD: return a + b;
+      case TCX_BINARY_SUBTRACT: return a - b;
+      case TCX_BINARY_MULTIPLY: return a * b;
+      default: return a / b;
+    }
+  } else {
+    switch (op) {
+      case TCX_BINARY_ADD: return a + b;
+      case TCX_BINARY_SUBTRACT: return a - b;
+      default: return a * b;
+    }
+  }
+}
+
+template <typename T, typename U>
+__global__ __launch_bounds__(256) void binary_kernel(const U* __restrict__ lhs, const U* __restrict__ rhs,
+                                                     U* __restrict__ out, BroadcastMeta m, std::int64_t n,
+                                                     int op) {
+  for (std::int64_t i = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<std::int64_t>(gridDim.x) * blockDim.x) {
+    std::int64_t index = i, l = 0, r = 0;
+    for (int axis = m.rank - 1; axis >= 0; --axis) {
+      const std::int64_t c = index % m.shape[axis];
+      index /= m.shape[axis];
+      l += c * m.lhs[axis];
+      r += c * m.rhs[axis];
+    }
+    // int32 arithmetic runs in uint32 so overflow wraps (cpu_backend.cpp:1070-1093).
+    out[i] = static_cast<U>(binary_op<T>(static_cast<T>(lhs[l]), static_cast<T>(rhs[r]), op));
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void fill_kernel(T* __restrict__ out, std::int64_t n, T value) {
+  for (std::int64_t i = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<std::int64_t>(gridDim.x) * blockDim.x)
+    out[i] = value;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15U) == 0; }
+constexpr std::int64_t kMaxBlocks = 256 * 32;  // 32 blocks per CU for grid-stride loops
+
+}  // namespace
+}  // namespace tcx
+
+extern "C" {
+
+int tcx_hip_bias_act_f32(const float* x, const float* bias, float* out, int64_t rows, int64_t cols, int act,
+                         tcx_stream_t stream) {
+  using namespace tcx;
+  if (rows < 0 || cols < 0) return fail(TCX_INVALID_ARGUMENT, "bias_act extents must be non-negative");
+  if (act < TCX_ACT_NONE || act > TCX_ACT_GELU) return fail(TCX_INVALID_ARGUMENT, "unknown activation");
+  if (rows == 0 || cols == 0) return TCX_OK;
+  if (x == nullptr || out == nullptr) return fail(TCX_INVALID_ARGUMENT, "bias_act buffers are null");
+  const int rc = ready();
+  if (rc != TCX_OK) return rc;
+  const auto s = static_cast<hipStream_t>(stream);
+  if (cols % 4 == 0 && aligned16(x) && aligned16(out) && (bias == nullptr || aligned16(bias))) {
+    hipLaunchKernelGGL(bias_act_vec_kernel, dim3(grid_for(rows * cols / 4, 256, kMaxBlocks)), dim3(256), 0, s,
+                       x, bias, out, rows, cols, act);
+  } else {
+    hipLaunchKernelGGL(bias_act_kernel, dim3(grid_for(rows * cols, 256, kMaxBlocks)), dim3(256), 0, s, x, bias,
+                       out, rows, cols, act);
+  }
+  return check(hipGetLastError(), "bias_act launch");
+}
+
+int tcx_hip_unary_f32(int op, const float* x, float* out, int64_t n, tcx_stream_t stream) {
+  using namespace tcx;
+  if (op < TCX_UNARY_EXP || op > TCX_UNARY_SILU) return fail(TCX_INVALID_ARGUMENT, "unknown unary op");
+  if (n < 0) return fail(TCX_INVALID_ARGUMENT, "unary extent must be non-negative");
+  if (n == 0) return TCX_OK;
+  if (x == nullptr || out == nullptr) return fail(TCX_INVALID_ARGUMENT, "unary buffers are null");
+  const int rc = ready();
+  if (rc != TCX_OK) return rc;
+  hipLaunchKernelGGL(unary_kernel, dim3(grid_for(n, 256, kMaxBlocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, out, n, op);
+  return check(hipGetLastError(), "unary launch");
+}
+
+int tcx_hip_binary(int op, int dtype, const void* lhs, const void* rhs, void* out, int32_t rank,
+                   const int64_t* out_shape, const int64_t* lhs_strides, const int64_t* rhs_strides,
+                   tcx_stream_t stream) {
+  using namespace tcx;
+  if (op < TCX_BINARY_ADD || op > TCX_BINARY_DIVIDE) return fail(TCX_INVALID_ARGUMENT, "unknown binary op");
+  if (dtype != TCX_FLOAT32 && dtype != TCX_INT32)
+    return fail(TCX_INVALID_ARGUMENT, "arithmetic requires float32 or int32 tensors");
+  if (dtype == TCX_INT32 && op == TCX_BINARY_DIVIDE)
+    return fail(TCX_INVALID_ARGUMENT, "division only supports float32 tensors");
+  if (rank < 0 || rank > TCX_HIP_MAX_RANK) return fail(TCX_INVALID_ARGUMENT, "binary rank exceeds the supported maximum");
+  BroadcastMeta m{};
+  m.rank = rank;
+  std::int64_t n = 1;
+  for (int i = 0; i < rank; ++i) {
+    if (out_shape[i] < 0) return fail(TCX_INVALID_ARGUMENT, "binary extents must be non-negative");
+    m.shape[i] = out_shape[i];
+    m.lhs[i] = lhs_strides[i];
+    m.rhs[i] = rhs_strides[i];
+    n *= out_shape[i];
+  }
+  if (n == 0) return TCX_OK;
+  if (lhs == nullptr || rhs == nullptr || out == nullptr) return fail(TCX_INVALID_ARGUMENT, "binary buffers are null");
+  const int rc = ready();
+  if (rc != TCX_OK) return rc;
+  const auto s = static_cast<hipStream_t>(stream);
+  const dim3 grid(grid_for(n, 256, kMaxBlocks));
+  if (dtype == TCX_FLOAT32)
+    hipLaunchKernelGGL((binary_kernel<float, float>), grid, dim3(256), 0, s, static_cast<const float*>(lhs),
+                       static_cast<const float*>(rhs), static_cast<float*>(out), m, n, op);
+  else
+    hipLaunchKernelGGL((binary_kernel<std::uint32_t, std::uint32_t>), grid, dim3(256), 0, s,
+                       static_cast<const std::uint32_t*>(lhs), static_cast<const std::uint32_t*>(rhs),
+                       static_cast<std::uint32_t*>(out), m, n, op);
+  return check(hipGetLastError(), "binary launch");
+}
+
+int tcx_hip_fill(int dtype, void* out, int64_t n, double value, tcx_stream_t stream) {
+  using namespace tcx;
+  if (n < 0) return fail(TCX_INVALID_ARGUMENT, "fill extent must be non-negative");
+  if (n == 0) return TCX_OK;
+  if (out == nullptr) return fail(TCX_INVALID_ARGUMENT, "fill output is null");
+  const int rc = ready();
+  if (rc != TCX_OK) return rc;
+  const auto s = static_cast<hipStream_t>(stream);
+  const dim3 grid(grid_for(n, 256, kMaxBlocks));
+  if (dtype == TCX_FLOAT32)
+    hipLaunchKernelGGL((fill_kernel<float>), grid, dim3(256), 0, s, static_cast<float*>(out), n,
+                       static_cast<float>(value));
+  else if (dtype == TCX_INT32)
+    hipLaunchKernelGGL((fill_kernel<int>), grid, dim3(256), 0, s, static_cast<int*>(out), n,
+                       static_cast<int>(value));
+  else
+    return fail(TCX_INVALID_ARGUMENT, "fill requires float32 or int32");
+  return check(hipGetLastError(), "fill launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,565 @@
+// Reductions: sum / max / mean / min / argmax over float32 and int32.
+//
+// Semantics (reference cpu_backend.cpp:1099-1249, cpu_math.cpp:27-76):
+//   sum    float32: fp32 additions from +0; int32: wraps modulo 2^32
+//   mean   float32 sum / float(count); NaN for an empty reduction
+//   max    value at the first index attaining the maximum; a NaN wins and the
+//          first NaN is returned; +0 and -0 compare equal (first kept)
+//   min    the same with the minimum
+//   argmax int32 index of that element
+// max/min/argmax and int32 sums are order-free under these rules, so the
+// parallel paths are bit-exact. A float32 sum depends on order: rows longer
+// than kSequentialMax use a fixed tree order (per-lane strided partials, then a
+// butterfly), shorter rows and strided (inner > 1) reductions keep the
+// reference's exact left-to-right order, one lane per output.
+//
+// Paths:
+//   row_wave_kernel    inner == 1, long rows: one wave per (row, segment),
+//                      16-byte loads; rows split into segments when there are
+//                      too few rows to fill the GPU (partials in workspace)
+//   finish_kernel      combines per-row segment partials in segment order
+//   lane_kernel        one lane per output, reference element order
+//   axes_kernel        any axis selection through reduction-plan metadata
+
+#include "common.hpp"
+
+namespace tcx {
+namespace {
+
+constexpr std::int64_t kSequentialMax = 64;   // rows up to this length keep exact order
+constexpr std::int64_t kTargetWaves = 8192;   // 32 waves per CU on 256 CUs
+constexpr std::int64_t kMinSegment = 4096;    // elements per segment when splitting rows
+
+// Partial result of one (row, segment): a float or uint32 sum, or a
+// (value bits, index) extremum candidate; index < 0 marks an empty candidate.
+struct Partial {
+  std::uint32_t bits;
+  std::uint32_t pad;
+  std::int64_t index;
+};
+
+template <typename T>
+__device__ __forceinline__ T from_bits(std::uint32_t b) {
+  return __builtin_bit_cast(T, b);
+}
+template <typename T>
+__device__ __forceinline__ std::uint32_t to_bits(T v) {
+  return __builtin_bit_cast(std::uint32_t, v);
+}
+
+template <typename T, bool kLargest>
+__device__ __forceinline__ bool lane_takes(T v, T best) {
+  // Within one lane indices only grow, so ties keep the earlier element.
+  if constexpr (sizeof(T) == 4 && __is_same(T, float)) {
+    return is_nan(v) ? !is_nan(best) : (kLargest ? v > best : v < best);
+  } else {
+    return kLargest ? v > best : v < best;
+  }
+}
+
+template <typename T, bool kLargest>
+__device__ __forceinline__ bool cand_better(T v, std::int64_t i, T best, std::int64_t bi) {
+  if (i < 0) return false;
+  if (bi < 0) return true;
+  if constexpr (__is_same(T, float))
+    return better_f32<kLargest>(v, i, best, bi);
+  else
+    return better_i32<kLargest>(v, i, best, bi);
+}
+
+template <typename T, bool kLargest>
+__device__ __forceinline__ void wave_extremum(T& best, std::int64_t& bi) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) {
+    const T ov = from_bits<T>(static_cast<std::uint32_t>(__shfl_xor(static_cast<int>(to_bits(best)), offset, kWave)));
+    const std::int64_t oi = __shfl_xor(bi, offset, kWave);
+    if (cand_better<T, kLargest>(ov, oi, best, bi)) {
+      best = ov;
+      bi = oi;
+    }
+  }
+}
+
+// ------------------------------------------------------------- row path
+template <typename T>
+using vec4 = T __attribute__((ext_vector_type(4)));
+
+template <int kOp, typename T, bool kVec>
+__global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, void* __restrict__ out,
+                                                       Partial* __restrict__ partials, std::int64_t rows,
+                                                       std::int64_t reduce, std::int64_t segments,
+                                                       std::int64_t seg_len) {
+  const int lane = threadIdx.x & 63;
+  const std::int64_t gw = static_cast<std::int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (gw >= rows * segments) return;
+  const std::int64_t row = gw / segments, seg = gw % segments;
+  const std::int64_t begin = seg * seg_len;
+  const std::int64_t end = min(reduce, begin + seg_len);
+  const T* __restrict__ p = x + row * reduce;
+  constexpr bool kSum = kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN;
+  constexpr bool kLargest = kOp != TCX_REDUCE_MIN;
+
+  if constexpr (kSum) {
+    if constexpr (__is_same(T, float)) {
+      float s0 = 0.F, s1 = 0.F, s2 = 0.F, s3 = 0.F;
+      if constexpr (kVec) {
+        std::int64_t i = begin + lane * 4;
+        for (; i + 3 * 256 < end; i += 4 * 256) {
+          const vec4<float> a = *reinterpret_cast<const vec4<float>*>(p + i);
+          const vec4<float> b = *reinterpret_cast<const vec4<float>*>(p + i + 256);
+          const vec4<float> c = *reinterpret_cast<const vec4<float>*>(p + i + 512);
+          const vec4<float> d = *reinterpret_cast<const vec4<float>*>(p + i + 768);
+          s0 += a.x; s1 += a.y; s2 += a.z; s3 += a.w;
+          s0 += b.x; s1 += b.y; s2 += b.z; s3 += b.w;
+          s0 += c.x; s1 += c.y; s2 += c.z; s3 += c.w;
+          s0 += d.x; s1 += d.y; s2 += d.z; s3 += d.w;
+        }
+        for (; i < end; i += 256) {
+          const vec4<float> a = *reinterpret_cast<const vec4<float>*>(p + i);
+          s0 += a.x; s1 += a.y; s2 += a.z; s3 += a.w;
+        }
+      } else {
+        for (std::int64_t i = begin + lane; i < end; i += 64) s0 += p[i];
+      }
+      float s = wave_sum((s0 + s1) + (s2 + s3));
+      if (lane == 0) {
+        if (segments == 1) {
+          static_cast<float*>(out)[row] = kOp == TCX_REDUCE_MEAN ? s / static_cast<float>(reduce) : s;
+        } else {
+          partials[gw] = Partial{to_bits(s), 0U, 0};
+        }
+      }
+    } else {
+      std::uint32_t s = 0;
+      if constexpr (kVec) {
+        const unsigned* __restrict__ q = reinterpret_cast<const unsigned*>(p);
+        std::int64_t i = begin + lane * 4;
+        for (; i + 3 * 256 < end; i += 4 * 256) {
+          const vec4<unsigned> a = *reinterpret_cast<const vec4<unsigned>*>(q + i);
+          const vec4<unsigned> b = *reinterpret_cast<const vec4<unsigned>*>(q + i + 256);
+          const vec4<unsigned> c = *reinterpret_cast<const vec4<unsigned>*>(q + i + 512);
+          const vec4<unsigned> d = *reinterpret_cast<const vec4<unsigned>*>(q + i + 768);
+          s += (a.x + a.y) + (a.z + a.w);
+          s += (b.x + b.y) + (b.z + b.w);
+          s += (c.x + c.y) + (c.z + c.w);
+          s += (d.x + d.y) + (d.z + d.w);
+        }
+        for (; i < end; i += 256) {
+          const vec4<unsigned> a = *reinterpret_cast<const vec4<unsigned>*>(q + i);
+          s += (a.x + a.y) + (a.z + a.w);
+        }
+      } else {
+        for (std::int64_t i = begin + lane; i < end; i += 64) s += static_cast<std::uint32_t>(p[i]);
+      }
+      s = wave_sum_u32(s);
+      if (lane == 0) {
+        if (segments == 1)
+          static_cast<int*>(out)[row] = static_cast<int>(s);
+        else
+          partials[gw] = Partial{s, 0U, 0};
+      }
+    }
+  } else {
+    T best{};
+    std::int64_t bi = -1;
+    auto visit = [&](T v, std::int64_t i) {
+      if (bi < 0 || lane_takes<T, kLargest>(v, best)) {
+        best = v;
+        bi = i;
+      }
+    };
+    if constexpr (kVec) {
+      std::int64_t i = begin + lane * 4;
+      for (; i + 256 < end; i += 2 * 256) {
+        const vec4<T> a = *reinterpret_cast<const vec4<T>*>(p + i);
+        const vec4<T> b = *reinterpret_cast<const vec4<T>*>(p + i + 256);
+        visit(a.x, i); visit(a.y, i + 1); visit(a.z, i + 2); visit(a.w, i + 3);
+        visit(b.x, i + 256); visit(b.y, i + 257); visit(b.z, i + 258); visit(b.w, i + 259);
+      }
+      for (; i < end; i += 256) {
+        const vec4<T> a = *reinterpret_cast<const vec4<T>*>(p + i);
+        visit(a.x, i); visit(a.y, i + 1); visit(a.z, i + 2); visit(a.w, i + 3);
+      }
+    } else {
+      for (std::int64_t i = begin + lane; i < end; i += 64) visit(p[i], i);
+    }
+    wave_extremum<T, kLargest>(best, bi);
+    if (lane == 0) {
+      if (segments == 1) {
+        if constexpr (kOp == TCX_REDUCE_ARGMAX)
+          static_cast<int*>(out)[row] = static_cast<int>(bi);
+        else
+          static_cast<T*>(out)[row] = best;
+      } else {
+        partials[gw] = Partial{to_bits(best), 0U, bi};
+      }
+    }
+  }
+}
+
+// One wave per row combines that row's segment partials.
+template <int kOp, typename T>
+__global__ __launch_bounds__(256) void finish_kernel(const Partial* __restrict__ partials,
+                                                     void* __restrict__ out, std::int64_t rows,
+                                                     std::int64_t reduce, std::int64_t segments) {
+  const int lane = threadIdx.x & 63;
+  const std::int64_t row = static_cast<std::int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const Partial* p = partials + row * segments;
+  constexpr bool kSum = kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN;
+  constexpr bool kLargest = kOp != TCX_REDUCE_MIN;
+  if constexpr (kSum) {
+    if constexpr (__is_same(T, float)) {
+      float s = 0.F;
+      for (std::int64_t i = lane; i < segments; i += 64) s += from_bits<float>(p[i].bits);
+      s = wave_sum(s);
+      if (lane == 0)
+        static_cast<float*>(out)[row] = kOp == TCX_REDUCE_MEAN ? s / static_cast<float>(reduce) : s;
+    } else {
+      std::uint32_t s = 0;
+      for (std::int64_t i = lane; i < segments; i += 64) s += p[i].bits;
+      s = wave_sum_u32(s);
+      if (lane == 0) static_cast<int*>(out)[row] = static_cast<int>(s);
+    }
+  } else {
+    T best{};
+    std::int64_t bi = -1;
+    for (std::int64_t i = lane; i < segments; i += 64) {
+      const T v = from_bits<T>(p[i].bits);
+      if (cand_better<T, kLargest>(v, p[i].index, best, bi)) {
+        best = v;
+        bi = p[i].index;
+      }
+    }
+    wave_extremum<T, kLargest>(best, bi);
+    if (lane == 0) {
+      if constexpr (kOp == TCX_REDUCE_ARGMAX)
+        static_cast<int*>(out)[row] = static_cast<int>(bi);
+      else
+        static_cast<T*>(out)[row] = best;
+    }
+  }
+}
+
+// ------------------------------------------------------ exact-order paths
+// Sequential per-output loop in the reference's element order.
+template <int kOp, typename T>
+__device__ __forceinline__ void sequential(const T* __restrict__ x, std::int64_t count,
+                                           std::int64_t stride, void* out, std::int64_t id) {
+  if constexpr (kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN) {
+    if constexpr (__is_same(T, float)) {
+      if (kOp == TCX_REDUCE_MEAN && count == 0) {
+        static_cast<float*>(out)[id] = __builtin_nanf("");
+        return;
+      }
+      float s = 0.F;
+      for (std::int64_t r = 0; r < count; ++r) s += x[r * stride];
+      static_cast<float*>(out)[id] = kOp == TCX_REDUCE_MEAN ? s / static_cast<float>(count) : s;
+    } else {
+      std::uint32_t s = 0;
+      for (std::int64_t r = 0; r < count; ++r) s += static_cast<std::uint32_t>(x[r * stride]);
+      static_cast<int*>(out)[id] = static_cast<int>(s);
+    }
+  } else if constexpr (kOp == TCX_REDUCE_MAX) {
+    if constexpr (__is_same(T, float)) {
+      float best = -__builtin_inff();
+      for (std::int64_t r = 0; r < count; ++r) {
+        const float v = x[r * stride];
+        if (is_nan(v)) {
+          best = v;
+          break;
+        }
+        best = (best < v) ? v : best;  // std::max keeps the first of equals
+      }
+      static_cast<float*>(out)[id] = best;
+    } else {
+      int best = static_cast<int>(0x80000000U);
+      for (std::int64_t r = 0; r < count; ++r) {
+        const int v = x[r * stride];
+        best = (best < v) ? v : best;
+      }
+      static_cast<int*>(out)[id] = best;
+    }
+  } else {
+    constexpr bool kLargest = kOp == TCX_REDUCE_ARGMAX;
+    T best = x[0];
+    std::int64_t bi = 0;
+    for (std::int64_t r = 1; r < count; ++r) {
+      const T v = x[r * stride];
+      bool take;
+      if constexpr (__is_same(T, float))
+        take = !is_nan(best) && (is_nan(v) || (kLargest ? best < v : v < best));
+      else
+        take = kLargest ? best < v : v < best;
+      if (take) {
+        best = v;
+        bi = r;
+      }
+    }
+    if constexpr (kOp == TCX_REDUCE_ARGMAX)
+      static_cast<int*>(out)[id] = static_cast<int>(bi);
+    else
+      static_cast<T*>(out)[id] = best;
+  }
+}
+
+template <int kOp, typename T>
+__global__ __launch_bounds__(256) void lane_kernel(const T* __restrict__ x, void* __restrict__ out,
+                                                   std::int64_t outer, std::int64_t reduce,
+                                                   std::int64_t inner) {
+  const std::int64_t id = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (id >= outer * inner) return;
+  const T* base = x + (id / inner) * reduce * inner + id % inner;
+  sequential<kOp, T>(base, reduce, inner, out, id);
+}
+
+struct AxesMeta {
+  std::int64_t extent[TCX_HIP_MAX_RANK];
+  std::int64_t stride[TCX_HIP_MAX_RANK];
+  std::int32_t outer_rank, rank;
+};
+
+__device__ __forceinline__ std::int64_t meta_offset(std::int64_t index, const AxesMeta& m, int begin,
+                                                    int end) {
+  std::int64_t value = 0;
+  for (int axis = end - 1; axis >= begin; --axis) {
+    value += (index % m.extent[axis]) * m.stride[axis];
+    index /= m.extent[axis];
+  }
+  return value;
+}
+
+template <int kOp, typename T>
+__global__ __launch_bounds__(256) void axes_kernel(const T* __restrict__ x, void* __restrict__ out,
+                                                   AxesMeta meta, std::int64_t groups,
+                                                   std::int64_t count) {
+  const std::int64_t g = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (g >= groups) return;
+  const T* base = x + meta_offset(g, meta, 0, meta.outer_rank);
+  constexpr bool kSum = kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN;
+  auto item = [&](std::int64_t r) { return base[meta_offset(r, meta, meta.outer_rank, meta.rank)]; };
+  if constexpr (kSum) {
+    if constexpr (__is_same(T, float)) {
+      float s = 0.F;
+      for (std::int64_t r = 0; r < count; ++r) s += item(r);
+      float v = s;
+      if (kOp == TCX_REDUCE_MEAN) v = count ? s / static_cast<float>(count) : __builtin_nanf("");
+      static_cast<float*>(out)[g] = v;
+    } else {
+      std::uint32_t s = 0;
+      for (std::int64_t r = 0; r < count; ++r) s += static_cast<std::uint32_t>(item(r));
+      static_cast<int*>(out)[g] = static_cast<int>(s);
+    }
+  } else if constexpr (kOp == TCX_REDUCE_MAX) {
+    if constexpr (__is_same(T, float)) {
+      float best = -__builtin_inff();
+      for (std::int64_t r = 0; r < count; ++r) {
+        const float v = item(r);
+        if (is_nan(v)) {
+          best = v;
+          break;
+        }
+        best = (best < v) ? v : best;
+      }
+      static_cast<float*>(out)[g] = best;
+    } else {
+      int best = static_cast<int>(0x80000000U);
+      for (std::int64_t r = 0; r < count; ++r) {
+        const int v = item(r);
+        best = (best < v) ? v : best;
+      }
+      static_cast<int*>(out)[g] = best;
+    }
+  } else {
+    constexpr bool kLargest = kOp == TCX_REDUCE_ARGMAX;
+    T best = item(0);
+    std::int64_t bi = 0;
+    for (std::int64_t r = 1; r < count; ++r) {
+      const T v = item(r);
+      bool take;
+      if constexpr (__is_same(T, float))
+        take = !is_nan(best) && (is_nan(v) || (kLargest ? best < v : v < best));
+      else
+        take = kLargest ? best < v : v < best;
+      if (take) {
+        best = v;
+        bi = r;
+      }
+    }
+    if constexpr (kOp == TCX_REDUCE_ARGMAX)
+      static_cast<int*>(out)[g] = static_cast<int>(bi);
+    else
+      static_cast<T*>(out)[g] = best;
+  }
+}
+
+// ------------------------------------------------------------ planning
+struct RowPlan {
+  bool row_path;
+  std::int64_t segments, seg_len;
+};
+
+RowPlan plan_rows(std::int64_t outer, std::int64_t reduce, std::int64_t inner) {
+  RowPlan p{false, 1, reduce};
+  if (inner != 1 || reduce <= kSequentialMax) return p;
+  p.row_path = true;
+  if (outer < kTargetWaves && reduce > 2 * kMinSegment) {
+    std::int64_t want = (kTargetWaves + outer - 1) / outer;
+    const std::int64_t most = (reduce + kMinSegment - 1) / kMinSegment;
+    if (want > most) want = most;
+    if (want > 1) {
+      // Segment length: a multiple of 1024 elements keeps 16-byte alignment
+      // and whole unrolled strides inside each segment.
+      std::int64_t len = (reduce + want - 1) / want;
+      len = (len + 1023) / 1024 * 1024;
+      p.segments = (reduce + len - 1) / len;
+      p.seg_len = len;
+    }
+  }
+  return p;
+}
+
+bool aligned16(const void* q) { return (reinterpret_cast<std::uintptr_t>(q) & 15U) == 0; }
+
+template <int kOp, typename T>
+int launch_reduce(const T* x, void* out, std::int64_t outer, std::int64_t reduce, std::int64_t inner,
+                  void* workspace, std::size_t workspace_bytes, hipStream_t s) {
+  const RowPlan plan = plan_rows(outer, reduce, inner);
+  if (!plan.row_path) {
+    hipLaunchKernelGGL((lane_kernel<kOp, T>), dim3(grid_for(outer * inner, 256, 0x7fffffff)), dim3(256), 0,
+                       s, x, out, outer, reduce, inner);
+    return check(hipGetLastError(), "reduce lane kernel launch");
+  }
+  Partial* partials = nullptr;
+  if (plan.segments > 1) {
+    const std::size_t need = static_cast<std::size_t>(outer * plan.segments) * sizeof(Partial);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(TCX_INVALID_ARGUMENT, "reduce workspace is smaller than tcx_hip_reduce_workspace_bytes");
+    partials = static_cast<Partial*>(workspace);
+  }
+  const bool vec = reduce % 4 == 0 && aligned16(x);
+  const std::int64_t waves = outer * plan.segments;
+  const dim3 grid(grid_for(waves, 4, 0x7fffffff));
+  if (vec)
+    hipLaunchKernelGGL((row_wave_kernel<kOp, T, true>), grid, dim3(256), 0, s, x, out, partials, outer,
+                       reduce, plan.segments, plan.seg_len);
+  else
+    hipLaunchKernelGGL((row_wave_kernel<kOp, T, false>), grid, dim3(256), 0, s, x, out, partials, outer,
+                       reduce, plan.segments, plan.seg_len);
+  int rc = check(hipGetLastError(), "reduce row kernel launch");
+  if (rc != TCX_OK || plan.segments == 1) return rc;
+  hipLaunchKernelGGL((finish_kernel<kOp, T>), dim3(grid_for(outer, 4, 0x7fffffff)), dim3(256), 0, s,
+                     partials, out, outer, reduce, plan.segments);
+  return check(hipGetLastError(), "reduce finish kernel launch");
+}
+
+template <typename T>
+int dispatch_reduce(int op, const T* x, void* out, std::int64_t outer, std::int64_t reduce,
+                    std::int64_t inner, void* ws, std::size_t wsb, hipStream_t s) {
+  switch (op) {
+    case TCX_REDUCE_SUM: return launch_reduce<TCX_REDUCE_SUM, T>(x, out, outer, reduce, inner, ws, wsb, s);
+    case TCX_REDUCE_MAX: return launch_reduce<TCX_REDUCE_MAX, T>(x, out, outer, reduce, inner, ws, wsb, s);
+    case TCX_REDUCE_MIN: return launch_reduce<TCX_REDUCE_MIN, T>(x, out, outer, reduce, inner, ws, wsb, s);
+    case TCX_REDUCE_ARGMAX: return launch_reduce<TCX_REDUCE_ARGMAX, T>(x, out, outer, reduce, inner, ws, wsb, s);
+    default: break;
+  }
+  if constexpr (__is_same(T, float)) {
+    if (op == TCX_REDUCE_MEAN) return launch_reduce<TCX_REDUCE_MEAN, T>(x, out, outer, reduce, inner, ws, wsb, s);
+  }
+  return fail(TCX_INVALID_ARGUMENT, "unsupported reduction for this dtype");
+}
+
+template <typename T>
+int dispatch_axes(int op, const T* x, void* out, const AxesMeta& m, std::int64_t groups,
+                  std::int64_t count, hipStream_t s) {
+  const dim3 grid(grid_for(groups, 256, 0x7fffffff));
+  switch (op) {
+    case TCX_REDUCE_SUM: hipLaunchKernelGGL((axes_kernel<TCX_REDUCE_SUM, T>), grid, dim3(256), 0, s, x, out, m, groups, count); break;
+    case TCX_REDUCE_MAX: hipLaunchKernelGGL((axes_kernel<TCX_REDUCE_MAX, T>), grid, dim3(256), 0, s, x, out, m, groups, count); break;
+    case TCX_REDUCE_MIN: hipLaunchKernelGGL((axes_kernel<TCX_REDUCE_MIN, T>), grid, dim3(256), 0, s, x, out, m, groups, count); break;
+    case TCX_REDUCE_ARGMAX: hipLaunchKernelGGL((axes_kernel<TCX_REDUCE_ARGMAX, T>), grid, dim3(256), 0, s, x, out, m, groups, count); break;
+    case TCX_REDUCE_MEAN:
+      if constexpr (__is_same(T, float)) {
+        hipLaunchKernelGGL((axes_kernel<TCX_REDUCE_MEAN, T>), grid, dim3(256), 0, s, x, out, m, groups, count);
+        break;
+      }
+      [[fallthrough]];
+    default:
+      return fail(TCX_INVALID_ARGUMENT, "unsupported reduction for this dtype");
+  }
+  return check(hipGetLastError(), "reduce axes kernel launch");
+}
+
+int validate(int op, int dtype, std::int64_t count) {
+  if (dtype != TCX_FLOAT32 && dtype != TCX_INT32)
+    return fail(TCX_INVALID_ARGUMENT, "reductions require float32 or int32 tensors");
+  if (op < TCX_REDUCE_SUM || op > TCX_REDUCE_ARGMAX) return fail(TCX_INVALID_ARGUMENT, "unknown reduction op");
+  if (op == TCX_REDUCE_MEAN && dtype != TCX_FLOAT32)
+    return fail(TCX_INVALID_ARGUMENT, "mean only supports float32 tensors");
+  if ((op == TCX_REDUCE_MAX || op == TCX_REDUCE_MIN || op == TCX_REDUCE_ARGMAX) && count == 0)
+    return fail(TCX_INVALID_ARGUMENT, "max/min/argmax require a non-empty reduction");
+  return TCX_OK;
+}
+
+}  // namespace
+}  // namespace tcx
+
+extern "C" {
+
+size_t tcx_hip_reduce_workspace_bytes(int op, int dtype, int64_t outer, int64_t reduce, int64_t inner) {
+  (void)op;
+  (void)dtype;
+  if (outer <= 0 || reduce <= 0 || inner <= 0) return 0;
+  const tcx::RowPlan plan = tcx::plan_rows(outer, reduce, inner);
+  if (!plan.row_path || plan.segments == 1) return 0;
+  return static_cast<size_t>(outer * plan.segments) * sizeof(tcx::Partial);
+}
+
+int tcx_hip_reduce(int op, int dtype, const void* x, void* out, int64_t outer, int64_t reduce,
+                   int64_t inner, void* workspace, size_t workspace_bytes, tcx_stream_t stream) {
+  using namespace tcx;
+  if (outer < 0 || reduce < 0 || inner < 0) return fail(TCX_INVALID_ARGUMENT, "reduce extents must be non-negative");
+  int rc = validate(op, dtype, reduce);
+  if (rc != TCX_OK) return rc;
+  if (outer == 0 || inner == 0) return TCX_OK;
+  if (x == nullptr && reduce != 0) return fail(TCX_INVALID_ARGUMENT, "reduce input is null");
+  if (out == nullptr) return fail(TCX_INVALID_ARGUMENT, "reduce output is null");
+  rc = ready();
+  if (rc != TCX_OK) return rc;
+  const auto s = static_cast<hipStream_t>(stream);
+  if (dtype == TCX_FLOAT32)
+    return dispatch_reduce<float>(op, static_cast<const float*>(x), out, outer, reduce, inner, workspace,
+                                  workspace_bytes, s);
+  return dispatch_reduce<int>(op, static_cast<const int*>(x), out, outer, reduce, inner, workspace,
+                              workspace_bytes, s);
+}
+
+int tcx_hip_reduce_axes(int op, int dtype, const void* x, void* out, const int64_t* meta,
+                        int32_t outer_rank, int32_t rank, int64_t groups, int64_t reduction_size,
+                        tcx_stream_t stream) {
+  using namespace tcx;
+  if (rank < 0 || rank > TCX_HIP_MAX_RANK || outer_rank < 0 || outer_rank > rank)
+    return fail(TCX_INVALID_ARGUMENT, "reduction rank exceeds the supported maximum");
+  if (groups < 0 || reduction_size < 0) return fail(TCX_INVALID_ARGUMENT, "reduce extents must be non-negative");
+  int rc = validate(op, dtype, reduction_size);
+  if (rc != TCX_OK) return rc;
+  if (groups == 0) return TCX_OK;
+  if (out == nullptr || (x == nullptr && reduction_size != 0))
+    return fail(TCX_INVALID_ARGUMENT, "reduce buffers are null");
+  AxesMeta m{};
+  m.outer_rank = outer_rank;
+  m.rank = rank;
+  for (int i = 0; i < rank; ++i) {
+    m.extent[i] = meta[2 * i];
+    m.stride[i] = meta[2 * i + 1];
+    if (m.extent[i] <= 0) return fail(TCX_INVALID_ARGUMENT, "reduction metadata extents must be positive");
+  }
+  rc = ready();
+  if (rc != TCX_OK) return rc;
+  const auto s = static_cast<hipStream_t>(stream);
+  if (dtype == TCX_FLOAT32)
+    return dispatch_axes<float>(op, static_cast<const float*>(x), out, m, groups, reduction_size, s);
+  return dispatch_axes<int>(op, static_cast<const int*>(x), out, m, groups, reduction_size, s);
+}
+
+}  // extern "C"

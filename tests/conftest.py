@@ -55,6 +55,9 @@ def assert_bits_equal(actual, expected, context=""):
 
 
 def require_gpu():
+    import tensorcx_hip_capi as capi
+    if not capi.LIB_PATH.exists():
+        pytest.fail(f"{capi.LIB_PATH} is not built: run `python tensor.cx_amd/build.py`")
     if not gpu_present():
         if os.environ.get("TENSORCX_REQUIRE_HIP") == "1":
             pytest.fail("TENSORCX_REQUIRE_HIP=1 but no usable HIP device")

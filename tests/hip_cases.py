@@ -1,0 +1,151 @@
+"""Parity metrics and golden-case runners shared by the GPU tests.
+
+Bars (stated once, used everywhere):
+  * bit-exact: max, min, argmax, every int32 result, broadcast arithmetic, and
+    float32 sum/mean on the exact-order paths (reductions of at most
+    SEQUENTIAL_MAX elements along a contiguous run, and strided reductions);
+  * matmul / linear: max|dC| / (sqrt(K) * rms(A) * rms(B)) <= 1e-4;
+  * float32 sum/mean on the tree path: max|d| / sum|x| <= 1e-5 per output;
+  * softmax, LayerNorm, RMSNorm, affine norms, MLP output:
+    allclose(rtol=1e-5, atol=1e-5), the reference's reduction class;
+  * exp / gelu / silu: allclose(rtol=1e-6, atol=1e-6), the elementwise class.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+import oracle
+
+SEQUENTIAL_MAX = 64
+MATMUL_BAR = 1e-4
+SUM_BAR = 1e-5
+
+
+def bits(x):
+    x = np.asarray(x)
+    return x.view(np.uint32) if x.dtype == np.float32 else x
+
+
+def assert_bits(actual, expected, context=""):
+    actual, expected = np.asarray(actual), np.asarray(expected)
+    assert actual.shape == expected.shape, f"{context}: shape {actual.shape} != {expected.shape}"
+    assert actual.dtype == expected.dtype, f"{context}: dtype {actual.dtype} != {expected.dtype}"
+    diff = np.flatnonzero(bits(actual).reshape(-1) != bits(expected).reshape(-1))
+    if diff.size:
+        i = diff[0]
+        raise AssertionError(f"{context}: {diff.size}/{actual.size} differ; first at {i}: "
+                             f"{actual.reshape(-1)[i]!r} vs {expected.reshape(-1)[i]!r}")
+
+
+def matmul_error(actual, expected, a, b) -> float:
+    k = a.shape[-1] if a.ndim else 1
+    if actual.size == 0 or k == 0:
+        return 0.0 if np.array_equal(actual, expected) else np.inf
+    scale = np.sqrt(k) * np.sqrt(np.mean(np.square(a, dtype=np.float64))) * \
+        np.sqrt(np.mean(np.square(b, dtype=np.float64)))
+    return float(np.max(np.abs(actual.astype(np.float64) - expected)) / max(scale, 1e-30))
+
+
+def assert_matmul(actual, expected, a, b, context=""):
+    assert actual.shape == expected.shape, f"{context}: shape {actual.shape} != {expected.shape}"
+    err = matmul_error(actual, expected, a, b)
+    assert err <= MATMUL_BAR, f"{context}: scaled matmul error {err:.3e} > {MATMUL_BAR}"
+    return err
+
+
+def sum_error(actual, expected, x, outer, reduce_, inner) -> float:
+    """max |d| / sum|x| over outputs of an (outer, reduce, inner) reduction."""
+    if actual.size == 0:
+        return 0.0
+    mag = np.abs(x.reshape(outer, reduce_, inner).astype(np.float64)).sum(axis=1).reshape(-1)
+    d = np.abs(actual.reshape(-1).astype(np.float64) - expected.reshape(-1).astype(np.float64))
+    finite = np.isfinite(expected.reshape(-1))
+    assert np.array_equal(np.isnan(actual.reshape(-1)), np.isnan(expected.reshape(-1)))
+    d = np.where(finite, d, 0.0)
+    return float(np.max(d / np.maximum(mag, 1e-30)))
+
+
+def assert_close(actual, expected, rtol, atol, context=""):
+    actual, expected = np.asarray(actual), np.asarray(expected)
+    assert actual.shape == expected.shape, f"{context}: shape {actual.shape} != {expected.shape}"
+    np.testing.assert_allclose(actual, expected, rtol=rtol, atol=atol, equal_nan=True, err_msg=context)
+
+
+def reduction_run(shape, kw):
+    """(outer, reduce, inner, exact) for a golden reduction case."""
+    rank = len(shape)
+    if "axes" in kw:
+        axes = sorted(a % rank for a in kw["axes"]) if rank else []
+    else:
+        axes = [oracle.normalize_axis(kw.get("axis", 0), rank)] if rank else []
+    if not axes:
+        return 1, 1, 1, True
+    adjacent = axes == list(range(axes[0], axes[-1] + 1))
+    if not adjacent:
+        return 1, 1, 1, True
+    outer = int(np.prod(shape[:axes[0]], dtype=np.int64))
+    red = int(np.prod(shape[axes[0]:axes[-1] + 1], dtype=np.int64))
+    inner = int(np.prod(shape[axes[-1] + 1:], dtype=np.int64))
+    return outer, red, inner, inner != 1 or red <= SEQUENTIAL_MAX
+
+
+def run_hip(cx, op, inputs, kw):
+    """Runs one golden case through the tensorcx API on the hip device."""
+    t = [cx.tensor(x, device="hip") for x in inputs]
+    axis = kw.get("axis", 0)
+    if op == "matmul":
+        return cx.matmul(*t)
+    if op in ("sum", "max", "mean"):
+        return getattr(cx, op)(t[0], tuple(kw["axes"]) if "axes" in kw else axis)
+    if op == "min":
+        return cx.min(t[0], tuple(kw["axes"]))
+    if op == "argmax":
+        return cx.Tensor(cx._core._argmax_axes(t[0]._impl, list(kw["axes"])))
+    if op == "softmax":
+        return cx.softmax(t[0], axis)
+    if op in ("rmsnorm", "layernorm"):
+        return getattr(cx, op)(t[0], axis, kw.get("eps", 1e-5))
+    if op in ("exp", "gelu", "silu"):
+        return getattr(cx, op)(t[0])
+    if op == "add":
+        return t[0] + t[1]
+    if op == "subtract":
+        return t[0] - t[1]
+    if op == "multiply":
+        return t[0] * t[1]
+    if op == "divide":
+        return t[0] / t[1]
+    if op == "linear":
+        return cx.linear(*t)
+    if op in ("affine_layernorm", "affine_rmsnorm"):
+        weight = t[1] if kw.get("has_weight") else None
+        bias = t[2] if kw.get("has_bias") else None
+        if op == "affine_rmsnorm":
+            return cx.rmsnorm(t[0], axis, kw.get("eps", 1e-5), weight=weight)
+        return cx.layernorm(t[0], axis, kw.get("eps", 1e-5), weight=weight, bias=bias)
+    raise AssertionError(op)
+
+
+def check_case(name, op, inputs, kw, actual, expected):
+    """Applies the bar for `op` to one result."""
+    if op in ("max", "min", "argmax", "add", "subtract", "multiply", "divide") or \
+            expected.dtype == np.int32:
+        assert_bits(actual, expected, name)
+    elif op in ("sum", "mean"):
+        outer, red, inner, exact = reduction_run(inputs[0].shape, kw)
+        if exact:
+            assert_bits(actual, expected, name)
+        else:
+            err = sum_error(actual, expected, inputs[0], outer, red, inner)
+            assert err <= SUM_BAR, f"{name}: sum error {err:.3e}"
+    elif op in ("matmul", "linear"):
+        if op == "linear":
+            a, b = inputs[0], inputs[1].T
+        else:
+            a, b = inputs[0], inputs[1]
+        assert_matmul(actual, expected, a, b, name)
+    elif op in ("exp", "gelu", "silu"):
+        assert_close(actual, expected, 1e-6, 1e-6, name)
+    else:
+        assert_close(actual, expected, 1e-5, 1e-5, name)

@@ -1,0 +1,270 @@
+"""GPU parity of the hip device against the CPU oracle and reference golden
+vectors, through tensorcx -> HipBackend::execute -> C ABI -> gfx950 kernels.
+
+Bars are those of tests/hip_cases.py. Sizes: golden vectors (small, from the
+reference CPU backend), random edge shapes (oracle), and the BASELINE.json
+configs at full size (oracle, multithreaded but bit-identical).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import require_gpu
+from hip_cases import (assert_bits, assert_close, assert_matmul, check_case, run_hip,
+                       sum_error)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def cx():
+    require_gpu()
+    import tensorcx
+    return tensorcx
+
+
+# ------------------------------------------------------------- golden vectors
+def test_golden_vectors(cx, golden):
+    manifest, arrays = golden
+    failures = []
+    for entry in manifest:
+        inputs = [arrays[k] for k in entry["inputs"]]
+        name, op, kw = entry["name"], entry["op"], entry["kwargs"]
+        if "error" in entry:
+            with pytest.raises(ValueError):
+                run_hip(cx, op, inputs, kw).numpy()
+            continue
+        try:
+            actual = run_hip(cx, op, inputs, kw).numpy()
+            check_case(name, op, inputs, kw, actual, arrays[entry["output"]])
+        except AssertionError as error:
+            failures.append(str(error))
+    assert not failures, f"{len(failures)} golden cases failed:\n" + "\n".join(failures[:20])
+
+
+# ------------------------------------------------------------- matmul
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (2, 3, 4), (15, 17, 31), (17, 16, 15), (32, 33, 16),
+                                   (0, 3, 4), (3, 0, 4), (3, 4, 0), (65, 129, 67), (128, 128, 128),
+                                   (129, 255, 257), (300, 64, 200), (1000, 1000, 1000)])
+def test_matmul_shapes(cx, m, k, n):
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    expected = oracle.matmul(a, b)
+    if k == 0:
+        assert_bits(actual, expected, "k=0")
+    else:
+        assert_matmul(actual, expected, a, b, f"{m}x{k}x{n}")
+
+
+def test_matmul_dyadic_is_exact(cx):
+    # Dyadic inputs make every partial sum exact, so any order matches bitwise.
+    i = np.arange(6 * 130 * 70)
+    a = ((i % 11 - 5) / 8).astype(np.float32).reshape(6, 130, 70)
+    j = np.arange(6 * 70 * 90)
+    b = ((j % 7 - 3) / 8).astype(np.float32).reshape(6, 70, 90)
+    actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    assert_bits(actual, oracle.matmul(a, b), "dyadic batched")
+
+
+@pytest.mark.parametrize("sa,sb", [((2, 1, 5, 7), (3, 7, 4)), ((4, 33, 65), (65, 17)),
+                                   ((65,), (65, 9)), ((9, 65), (65,)), ((3, 1, 40, 36), (1, 5, 36, 44))])
+def test_matmul_broadcast(cx, sa, sb):
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal(sa).astype(np.float32)
+    b = rng.standard_normal(sb).astype(np.float32)
+    actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    assert_matmul(actual, oracle.matmul(a, b), a, b, f"{sa}@{sb}")
+
+
+def test_matmul_errors(cx):
+    a = cx.tensor(np.ones((2, 3), np.float32), device="hip")
+    with pytest.raises(ValueError):
+        cx.matmul(a, a)
+    with pytest.raises(ValueError):
+        cx.matmul(cx.tensor(np.ones((2, 2), np.int32), device="hip"),
+                  cx.tensor(np.ones((2, 2), np.int32), device="hip"))
+
+
+# ------------------------------------------------------------- reductions
+@pytest.mark.parametrize("shape", [(3, 65), (7, 300), (5, 1000), (2, 4097), (64, 8192), (1, 100003),
+                                   (3, 5, 70), (11, 40)])
+def test_reductions_random(cx, shape):
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal(shape).astype(np.float32)
+    h = cx.tensor(x, device="hip")
+    for axis in range(-len(shape), len(shape)):
+        _, outer, red, inner = oracle.reduction_dims(shape, axis)
+        for op in ("max", "min", "argmax"):
+            actual = getattr(cx, op)(h, axis).numpy()
+            assert_bits(actual, getattr(oracle, op)(x, axis), f"{op} {shape} axis {axis}")
+        for op in ("sum", "mean"):
+            actual = getattr(cx, op)(h, axis).numpy()
+            expected = getattr(oracle, op)(x, axis)
+            if inner != 1 or red <= 64:
+                assert_bits(actual, expected, f"{op} {shape} axis {axis}")
+            else:
+                scale = red if op == "mean" else 1
+                assert sum_error(actual * scale, expected * scale, x, outer, red, inner) <= 1e-5
+    full = cx.sum(h).numpy()
+    assert sum_error(full.reshape(1), oracle.sum(x, None).reshape(1), x, 1, x.size, 1) <= 1e-5
+
+
+def test_extrema_ties_nan_and_signed_zero(cx):
+    x = np.zeros((6, 777), np.float32)
+    x[0, 100] = x[0, 500] = 3.0                   # tie -> lowest index
+    x[1, :] = -np.inf                             # all -inf
+    x[2, 300], x[2, 10] = np.nan, -1.0
+    x[2, 600] = np.float32(np.nan) * -1           # a second NaN later
+    x[3, :] = -0.0
+    x[3, 400] = 0.0                               # +0/-0 equal, first kept
+    x[4, 5:] = 7.0
+    x[5, 776] = 9.0
+    h = cx.tensor(x, device="hip")
+    for op in ("max", "min", "argmax"):
+        assert_bits(getattr(cx, op)(h, 1).numpy(), getattr(oracle, op)(x, 1), op)
+        assert_bits(getattr(cx, op)(h, None).numpy(), getattr(oracle, op)(x, None), f"{op} all")
+
+
+def test_int32_reductions_wrap(cx):
+    rng = np.random.default_rng(3)
+    x = rng.integers(-2**31, 2**31 - 1, size=(300, 1031), dtype=np.int64).astype(np.int32)
+    h = cx.tensor(x, device="hip")
+    for axis in (0, 1):
+        for op in ("sum", "max", "min", "argmax"):
+            assert_bits(getattr(cx, op)(h, axis).numpy(), getattr(oracle, op)(x, axis), f"{op} {axis}")
+    assert_bits(cx.sum(h).numpy(), oracle.sum(x, None), "i32 full sum")
+    with pytest.raises(ValueError):
+        cx.mean(h, 1)
+
+
+def test_multi_axis_and_canonical_order(cx):
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((4, 6, 9)).astype(np.float32)
+    h = cx.tensor(x, device="hip")
+    for axes in ((0, 2), (2, 0), (0, 1), (1, 2), (0, 1, 2)):
+        for op in ("sum", "max", "mean", "min"):
+            # Exact order except adjacent runs longer than 64 (tree order, sum bar).
+            check_case(f"{op} {axes}", op, [x], {"axes": list(axes)},
+                       getattr(cx, op)(h, axes).numpy(), getattr(oracle, op)(x, axes))
+    pins = np.array([[1e20, 1], [-1e20, 3]], np.float32)
+    assert cx.sum(cx.tensor(pins, device="hip")).numpy() == 3.0
+    big = np.array([[3e38, 3e38], [-3e38, -3e38]], np.float32)
+    assert np.isposinf(cx.mean(cx.tensor(big, device="hip")).numpy())
+
+
+def test_empty_and_scalar(cx):
+    z = cx.tensor(np.zeros((2, 0, 3), np.float32), device="hip")
+    assert cx.sum(z, 1).numpy().tolist() == [[0, 0, 0], [0, 0, 0]]
+    assert np.all(np.isnan(cx.mean(z, 1).numpy()))
+    with pytest.raises(ValueError):
+        cx.max(z, 1)
+    with pytest.raises(ValueError):
+        cx.argmax(z, 1)
+    s = cx.tensor(np.float32(2.5), device="hip")
+    assert cx.sum(s).numpy() == 2.5 and cx.max(s, 0).numpy() == 2.5
+    assert cx.argmax(s).numpy() == 0
+
+
+# ------------------------------------------------------------- row ops
+@pytest.mark.parametrize("shape,axis", [((16, 4096), 1), ((5, 300), 1), ((7, 8192), 1), ((3, 20000), -1),
+                                        ((3, 7), 0), ((2, 3, 70), 1), ((9, 1), 1), ((4, 1022), 1)])
+def test_row_ops_random(cx, shape, axis):
+    rng = np.random.default_rng(13)
+    x = (rng.standard_normal(shape) * 3).astype(np.float32)
+    h = cx.tensor(x, device="hip")
+    assert_close(cx.softmax(h, axis).numpy(), oracle.softmax(x, axis), 1e-5, 1e-5, "softmax")
+    assert_close(cx.rmsnorm(h, axis).numpy(), oracle.rmsnorm(x, axis), 1e-5, 1e-5, "rmsnorm")
+    assert_close(cx.layernorm(h, axis).numpy(), oracle.layernorm(x, axis), 1e-5, 1e-5, "layernorm")
+    n = shape[axis]
+    g = rng.uniform(0.5, 1.5, size=n).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, size=n).astype(np.float32)
+    gh, bh = cx.tensor(g, device="hip"), cx.tensor(b, device="hip")
+    assert_close(cx.layernorm(h, axis, weight=gh, bias=bh).numpy(),
+                 oracle.affine_norm(x, axis, 1e-5, g, b), 1e-5, 1e-5, "affine layernorm")
+    assert_close(cx.rmsnorm(h, axis, weight=gh).numpy(),
+                 oracle.affine_norm(x, axis, 1e-5, g, None, rms=True), 1e-5, 1e-5, "affine rmsnorm")
+
+
+@pytest.mark.parametrize("eps", [0.0, 1e-45, 1e-5, 1e30])
+def test_constant_rows(cx, eps):
+    x = np.full((4, 512), 2.5, np.float32)
+    x[3] = -7.0
+    h = cx.tensor(x, device="hip")
+    for op in ("rmsnorm", "layernorm"):
+        assert_close(getattr(cx, op)(h, 1, eps).numpy(), getattr(oracle, op)(x, 1, eps), 1e-5, 1e-5, op)
+
+
+def test_row_op_errors(cx):
+    h = cx.tensor(np.ones((2, 8), np.float32), device="hip")
+    for eps in (-1.0, np.nan, np.inf, 1e100, 1e-100):
+        with pytest.raises(ValueError):
+            cx.layernorm(h, 1, eps)
+    with pytest.raises(ValueError):
+        cx.softmax(h, 2)
+    with pytest.raises(ValueError):
+        cx.softmax(cx.tensor(np.ones((2, 8), np.int32), device="hip"), 1)
+
+
+# ------------------------------------------------------------- elementwise / linear
+def test_unary_and_bias_act(cx):
+    x = np.concatenate([np.linspace(-12, 12, 4001, dtype=np.float32),
+                        np.array([0, -0.0, np.inf, -np.inf, np.nan, 100, -100, 1e-38], np.float32)])
+    h = cx.tensor(x, device="hip")
+    for op in ("exp", "gelu", "silu"):
+        assert_close(getattr(cx, op)(h).numpy(), getattr(oracle, op)(x), 1e-6, 1e-6, op)
+    rng = np.random.default_rng(2)
+    y = rng.standard_normal((33, 64)).astype(np.float32)
+    b = rng.standard_normal(64).astype(np.float32)
+    yh, bh = cx.tensor(y, device="hip"), cx.tensor(b, device="hip")
+    assert_bits((yh + bh).numpy(), oracle.binary("add", y, b), "bias add")
+    for act in ("silu", "gelu"):
+        fused = cx.hip.bias_act(yh, bh, act).numpy()
+        assert_close(fused, getattr(oracle, act)(oracle.binary("add", y, b)), 1e-6, 1e-6, act)
+
+
+@pytest.mark.parametrize("shape", [(5, 48), (2, 3, 48), (48,), (257, 130)])
+def test_linear(cx, shape):
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal(shape).astype(np.float32)
+    w = rng.standard_normal((20, shape[-1])).astype(np.float32)
+    b = rng.standard_normal(20).astype(np.float32)
+    xh, wh, bh = (cx.tensor(v, device="hip") for v in (x, w, b))
+    assert_matmul(cx.linear(xh, wh, bh).numpy(), oracle.linear(x, w, b), x, w.T, "linear")
+    assert_matmul(cx.linear(xh, wh).numpy(), oracle.linear(x, w), x, w.T, "linear no bias")
+    fused = cx.hip.linear_act(xh, wh, bh, "silu").numpy()
+    expected = oracle.silu(oracle.linear(x, w, b))
+    assert fused.shape == expected.shape
+    # matmul-class error, propagated through silu (|silu'| <= 1.1)
+    assert np.max(np.abs(fused - expected)) <= 1.1e-4 * np.sqrt(shape[-1]) * np.sqrt(np.mean(x * x)) * \
+        np.sqrt(np.mean(w * w)) + 1e-6
+
+
+def test_concurrent_threads(cx):
+    from concurrent.futures import ThreadPoolExecutor
+    rng = np.random.default_rng(8)
+    a = rng.standard_normal((64, 96)).astype(np.float32)
+    b = rng.standard_normal((96, 80)).astype(np.float32)
+    expected = oracle.softmax(oracle.matmul(a, b), 1)
+
+    def work(_):
+        out = cx.softmax(cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")), 1)
+        return out.numpy()
+
+    with ThreadPoolExecutor(4) as pool:
+        for result in pool.map(work, range(16)):
+            assert_close(result, expected, 1e-5, 1e-5, "threaded chain")
+
+
+def test_memory_pool_reuse(cx):
+    with cx.memory_pool(64 << 20, 8) as pool:
+        x = cx.tensor(np.ones((256, 256), np.float32), device="hip")
+        for _ in range(3):
+            y = cx.softmax(x, 1)
+            del y
+        stats = pool.stats()
+    assert stats["hits"] >= 1 and stats["active"]
