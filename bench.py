@@ -42,21 +42,22 @@ def log(msg: str) -> None:
 
 
 def timed(launch, steps: int, warmup: int):
-    """Runs `launch` warmup+steps times on this thread's stream. Returns
-    (total_ms over the K steps, per-launch event durations in ms)."""
+    """Runs `launch` warmup+steps times on this thread's stream and returns
+    (total_ms, per_launch_ms): two HIP events bracket the K timed launches on
+    the launch stream, with the stream idle on both sides."""
     s = capi.stream()
     for _ in range(warmup):
         launch(s)
     capi.synchronize()
-    events = [capi.Event() for _ in range(steps + 1)]
-    events[0].record(s)
-    for i in range(steps):
+    start, stop = capi.Event(), capi.Event()
+    start.record(s)
+    for _ in range(steps):
         launch(s)
-        events[i + 1].record(s)
-    events[-1].synchronize()
+    stop.record(s)
+    stop.synchronize()
     capi.synchronize()
-    per = [events[i].elapsed_ms(events[i + 1]) for i in range(steps)]
-    return events[0].elapsed_ms(events[-1]), per
+    total = start.elapsed_ms(stop)
+    return total, [total / steps] * steps
 
 
 def rotate(arrays_per_copy):
@@ -252,6 +253,10 @@ def main() -> int:
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     parser.add_argument("--only", default=None, help="run only secondary benches whose name contains this")
     parser.add_argument("--headline-only", action="store_true")
+    parser.add_argument("--no-headline", action="store_true",
+                        help="skip the 4096^3 GEMM (profiling runs of the secondary kernels)")
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="only run 1 GiB device-to-device copies (PMC byte-counter calibration)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every GPU box here has one MI355X; --gpus {args.gpus} is "
@@ -263,6 +268,16 @@ def main() -> int:
     info = capi.device_info()
     log(f"device: {info['name']} {info['arch']} CUs={info['compute_units']} clock={info['clock_khz']} kHz")
 
+    if args.copy_calibration:
+        src, dst = capi.DeviceBuffer(1 << 30), capi.DeviceBuffer(1 << 30)
+        for _ in range(3):
+            capi.check(capi.lib().tcx_hip_memcpy_d2d(dst.ptr, src.ptr, 1 << 30, capi.stream()), "copy")
+        log("copy calibration: 3 x 1 GiB device-to-device copies")
+        return 0
+    if args.no_headline:
+        for r in secondary_benches(args.steps, args.warmup, args.only):
+            print(json.dumps(r), flush=True)
+        return 0
     headline = bench_gemm("c2_4096", args.steps, args.warmup)
     log(f"gemm 4096^3: {headline['achieved']:.1f} TFLOP/s ({headline['frac']:.1%} of fp32 MFMA peak)")
     secondary = [] if args.headline_only else secondary_benches(args.steps, args.warmup, args.only)

@@ -25,6 +25,21 @@ using int4_t = int __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bool is_nan(float v) { return v != v; }
 
+// Streaming loads of data read exactly once. TCX_STREAM_NT selects the
+// non-temporal form (global_load ... nt), which keeps one-pass operands from
+// displacing reusable lines in L2 and the Infinity Cache.
+#ifndef TCX_STREAM_NT
+#define TCX_STREAM_NT 1
+#endif
+template <typename V>
+__device__ __forceinline__ V stream_load(const V* p) {
+#if TCX_STREAM_NT
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
+}
+
 // Wave-wide butterfly sums: both partners add the same two operands, so every
 // lane ends with identical bits and the order is fixed for a given layout.
 __device__ __forceinline__ float wave_sum(float v) {

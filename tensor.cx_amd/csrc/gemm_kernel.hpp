@@ -1,0 +1,325 @@
+// fp32 MFMA GEMM kernel template (v_mfma_f32_16x16x4_f32); included by
+// gemm.hip, which owns the C entry point and the per-shape tile choice.
+#pragma once
+
+#include "common.hpp"
+
+// 1: read the next k-step's LDS fragments before the current MFMAs.
+#ifndef TCX_GEMM_LDS_PIPELINE
+#define TCX_GEMM_LDS_PIPELINE 0
+#endif
+
+namespace tcx {
+namespace gemm {
+
+struct GemmArgs {
+  const float* lhs;
+  const float* rhs;
+  float* out;
+  const float* bias;
+  std::int64_t m, n, k;
+  std::int64_t tiles_m, tiles_n, total_tiles;
+  std::int32_t batch_rank, activation;
+  std::int64_t batch_shape[TCX_HIP_MAX_BATCH_RANK];
+  std::int64_t lhs_bs[TCX_HIP_MAX_BATCH_RANK];
+  std::int64_t rhs_bs[TCX_HIP_MAX_BATCH_RANK];
+};
+
+using floatx4 = float __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float activate(float v, int act) {
+  if (act == TCX_ACT_SILU) return v / (1.0F + expf(-v));
+  if (act == TCX_ACT_GELU) {
+    // Same operation order as cpu_backend.cpp:1000-1003.
+    const float cubic = 0.044715F * v * v * v;
+    const float inner = 0.7978845608028654F * (v + cubic);
+    return 0.5F * v * (1.0F + tanhf(inner));
+  }
+  return v;
+}
+
+template <int N>
+struct Frag;
+template <>
+struct Frag<4> {
+  static __device__ __forceinline__ void load(const float* p, float (&v)[4]) {
+    const float4_t t = *reinterpret_cast<const float4_t*>(p);
+    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+  }
+};
+template <>
+struct Frag<8> {
+  static __device__ __forceinline__ void load(const float* p, float (&v)[8]) {
+    const float4_t t0 = *reinterpret_cast<const float4_t*>(p);
+    const float4_t t1 = *reinterpret_cast<const float4_t*>(p + 4);
+    v[0] = t0.x; v[1] = t0.y; v[2] = t0.z; v[3] = t0.w;
+    v[4] = t1.x; v[5] = t1.y; v[6] = t1.z; v[7] = t1.w;
+  }
+};
+template <>
+struct Frag<2> {
+  static __device__ __forceinline__ void load(const float* p, float (&v)[2]) {
+    const float2 t = *reinterpret_cast<const float2*>(p);
+    v[0] = t.x; v[1] = t.y;
+  }
+};
+
+template <int BM, int BN, int BK, int WM, int WN, int kMinWaves, bool kTransB, bool kVec>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64)
+__attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs a) {
+  constexpr int kWavesN = BN / WN;
+  constexpr int kThreads = (BM / WM) * kWavesN * 64;
+  constexpr int TM = WM / 16, TN = WN / 16;
+  constexpr int LDA = BM + 4, LDB = BN + 4;
+  static_assert(BK % 4 == 0 && (BM * BK) % (4 * kThreads) == 0 && (BN * BK) % (4 * kThreads) == 0);
+  constexpr int kAVec = BM * BK / 4 / kThreads;  // float4 loads per thread for A
+  constexpr int kBVec = BN * BK / 4 / kThreads;
+  constexpr int kAScalar = BM * BK / kThreads;
+  constexpr int kBScalar = BN * BK / kThreads;
+  constexpr int kAReg = kVec ? kAVec * 4 : kAScalar;
+  constexpr int kBReg = kVec ? kBVec * 4 : kBScalar;
+
+  __shared__ float As[2][BK][LDA];
+  __shared__ float Bs[2][BK][LDB];
+
+  // Blocks go round-robin to the 8 XCDs; give each XCD a contiguous run of
+  // tile ids so the blocks sharing an L2 also share A row panels and B column
+  // panels. The remap is a bijection when the grid is a multiple of 8.
+  const std::int64_t grid = a.total_tiles;
+  const std::int64_t bid = blockIdx.x;
+  const std::int64_t tile = (grid % 8 == 0) ? (bid % 8) * (grid / 8) + bid / 8 : bid;
+  const std::int64_t per_batch = a.tiles_m * a.tiles_n;
+  const std::int64_t batch = tile / per_batch;
+  const std::int64_t t = tile % per_batch;
+  constexpr std::int64_t kGroupM = 8;
+  const std::int64_t group_tiles = kGroupM * a.tiles_n;
+  const std::int64_t first_m = (t / group_tiles) * kGroupM;
+  const std::int64_t gm = min(a.tiles_m - first_m, kGroupM);
+  const std::int64_t tm = first_m + (t % group_tiles) % gm;
+  const std::int64_t tn = (t % group_tiles) / gm;
+
+  std::int64_t lhs_off = 0, rhs_off = 0;
+  {
+    std::int64_t b = batch;
+    for (int ax = a.batch_rank - 1; ax >= 0; --ax) {
+      const std::int64_t e = a.batch_shape[ax];
+      const std::int64_t c = b % e;
+      b /= e;
+      lhs_off += c * a.lhs_bs[ax];
+      rhs_off += c * a.rhs_bs[ax];
+    }
+  }
+  const std::int64_t M = a.m, N = a.n, K = a.k;
+  const float* __restrict__ A = a.lhs + lhs_off;
+  const float* __restrict__ B = a.rhs + rhs_off;
+  float* __restrict__ C = a.out + batch * M * N;
+  const std::int64_t m0 = tm * BM, n0 = tn * BN;
+
+  const int tid = threadIdx.x;
+  float ra[kAReg], rb[kBReg];
+
+  // Global -> registers for k-tile starting at k0 (zero outside the matrix).
+  auto load_tile = [&](std::int64_t k0) {
+    if constexpr (kVec) {
+#pragma unroll
+      for (int p = 0; p < kAVec; ++p) {
+        const int idx = tid + p * kThreads;
+        const int row = idx / (BK / 4), kq = idx % (BK / 4);
+        const std::int64_t gm_ = m0 + row, gk = k0 + kq * 4;
+        float4_t v = {0.F, 0.F, 0.F, 0.F};
+        if (gm_ < M && gk < K) v = *reinterpret_cast<const float4_t*>(A + gm_ * K + gk);
+        ra[4 * p + 0] = v.x; ra[4 * p + 1] = v.y; ra[4 * p + 2] = v.z; ra[4 * p + 3] = v.w;
+      }
+#pragma unroll
+      for (int p = 0; p < kBVec; ++p) {
+        const int idx = tid + p * kThreads;
+        float4_t v = {0.F, 0.F, 0.F, 0.F};
+        if constexpr (kTransB) {
+          const int row = idx / (BK / 4), kq = idx % (BK / 4);
+          const std::int64_t gn = n0 + row, gk = k0 + kq * 4;
+          if (gn < N && gk < K) v = *reinterpret_cast<const float4_t*>(B + gn * K + gk);
+        } else {
+          const int krow = idx / (BN / 4), nq = idx % (BN / 4);
+          const std::int64_t gk = k0 + krow, gn = n0 + nq * 4;
+          if (gk < K && gn < N) v = *reinterpret_cast<const float4_t*>(B + gk * N + gn);
+        }
+        rb[4 * p + 0] = v.x; rb[4 * p + 1] = v.y; rb[4 * p + 2] = v.z; rb[4 * p + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int p = 0; p < kAScalar; ++p) {
+        const int idx = tid + p * kThreads;
+        const int row = idx / BK, kk = idx % BK;
+        const std::int64_t gm_ = m0 + row, gk = k0 + kk;
+        ra[p] = (gm_ < M && gk < K) ? A[gm_ * K + gk] : 0.F;
+      }
+#pragma unroll
+      for (int p = 0; p < kBScalar; ++p) {
+        const int idx = tid + p * kThreads;
+        if constexpr (kTransB) {
+          const int row = idx / BK, kk = idx % BK;
+          const std::int64_t gn = n0 + row, gk = k0 + kk;
+          rb[p] = (gn < N && gk < K) ? B[gn * K + gk] : 0.F;
+        } else {
+          const int krow = idx / BN, nn = idx % BN;
+          const std::int64_t gk = k0 + krow, gn = n0 + nn;
+          rb[p] = (gk < K && gn < N) ? B[gk * N + gn] : 0.F;
+        }
+      }
+    }
+  };
+
+  // Registers -> LDS buffer `buf`, A and (transposed) B stored k-major.
+  auto store_tile = [&](int buf) {
+    if constexpr (kVec) {
+#pragma unroll
+      for (int p = 0; p < kAVec; ++p) {
+        const int idx = tid + p * kThreads;
+        const int row = idx / (BK / 4), kq = idx % (BK / 4);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) As[buf][kq * 4 + q][row] = ra[4 * p + q];
+      }
+#pragma unroll
+      for (int p = 0; p < kBVec; ++p) {
+        const int idx = tid + p * kThreads;
+        if constexpr (kTransB) {
+          const int row = idx / (BK / 4), kq = idx % (BK / 4);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) Bs[buf][kq * 4 + q][row] = rb[4 * p + q];
+        } else {
+          const int krow = idx / (BN / 4), nq = idx % (BN / 4);
+          const float4_t v = {rb[4 * p], rb[4 * p + 1], rb[4 * p + 2], rb[4 * p + 3]};
+          *reinterpret_cast<float4_t*>(&Bs[buf][krow][nq * 4]) = v;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int p = 0; p < kAScalar; ++p) {
+        const int idx = tid + p * kThreads;
+        As[buf][idx % BK][idx / BK] = ra[p];
+      }
+#pragma unroll
+      for (int p = 0; p < kBScalar; ++p) {
+        const int idx = tid + p * kThreads;
+        if constexpr (kTransB)
+          Bs[buf][idx % BK][idx / BK] = rb[p];
+        else
+          Bs[buf][idx / BN][idx % BN] = rb[p];
+      }
+    }
+  };
+
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
+  const int r = lane & 15, kl = lane >> 4;
+  floatx4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.F, 0.F, 0.F, 0.F};
+
+  const std::int64_t k_tiles = (K + BK - 1) / BK;
+  if (k_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+  }
+  for (std::int64_t kt = 0; kt < k_tiles; ++kt) {
+    const int buf = static_cast<int>(kt & 1);
+    const bool more = kt + 1 < k_tiles;
+    if (more) load_tile((kt + 1) * BK);
+#if TCX_GEMM_LDS_PIPELINE
+    // Fragments for k-step s+1 are read from LDS while step s's MFMAs run.
+    float av[2][TM], bv[2][TN];
+    Frag<TM>::load(&As[buf][kl][wm * WM + r * TM], av[0]);
+    Frag<TN>::load(&Bs[buf][kl][wn * WN + r * TN], bv[0]);
+#pragma unroll
+    for (int s = 0; s < BK / 4; ++s) {
+      const int cur = s & 1;
+      if (s + 1 < BK / 4) {
+        const int k = (s + 1) * 4 + kl;
+        Frag<TM>::load(&As[buf][k][wm * WM + r * TM], av[cur ^ 1]);
+        Frag<TN>::load(&Bs[buf][k][wn * WN + r * TN], bv[cur ^ 1]);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[cur][i], bv[cur][j], acc[i][j], 0, 0, 0);
+    }
+#else
+#pragma unroll
+    for (int s = 0; s < BK / 4; ++s) {
+      const int k = s * 4 + kl;
+      float av[TM], bv[TN];
+      Frag<TM>::load(&As[buf][k][wm * WM + r * TM], av);
+      Frag<TN>::load(&Bs[buf][k][wn * WN + r * TN], bv);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+#endif
+    if (more) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: bias add then activation, as kAdd then kSilu/kGelu would round.
+  const std::int64_t col0 = n0 + wn * WN + r * TN;
+  float bias[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+    bias[j] = (a.bias != nullptr && col0 + j < N) ? a.bias[col0 + j] : 0.F;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const std::int64_t row = m0 + wm * WM + (kl * 4 + q) * TM + i;
+      if (row >= M) continue;
+      float v[TN];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        float x = acc[i][j][q];
+        if (a.bias != nullptr) x = x + bias[j];
+        v[j] = activate(x, a.activation);
+      }
+      float* dst = C + row * N + col0;
+      if (kVec && TN >= 4 && col0 + TN - 1 < N) {
+#pragma unroll
+        for (int j = 0; j < TN; j += 4)
+          *reinterpret_cast<float4_t*>(dst + j) = float4_t{v[j], v[j + 1], v[j + 2], v[j + 3]};
+      } else {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          if (col0 + j < N) dst[j] = v[j];
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int kMinWaves>
+int launch_config(GemmArgs& args, bool trans_b, bool vec, hipStream_t stream) {
+  args.tiles_m = (args.m + BM - 1) / BM;
+  args.tiles_n = (args.n + BN - 1) / BN;
+  const std::int64_t batches = args.total_tiles;  // caller passes the batch count here
+  args.total_tiles = args.tiles_m * args.tiles_n * batches;
+  if (args.total_tiles > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
+  const dim3 grid(static_cast<unsigned>(args.total_tiles));
+  const dim3 block((BM / WM) * (BN / WN) * 64);
+  if (trans_b) {
+    if (vec)
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, true, true>), grid, block, 0, stream, args);
+    else
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, true, false>), grid, block, 0, stream, args);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, false, true>), grid, block, 0, stream, args);
+    else
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, false, false>), grid, block, 0, stream, args);
+  }
+  return check(hipGetLastError(), "gemm_f32 launch");
+}
+
+}  // namespace gemm
+}  // namespace tcx

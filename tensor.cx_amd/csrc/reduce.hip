@@ -105,17 +105,17 @@ __global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, 
       if constexpr (kVec) {
         std::int64_t i = begin + lane * 4;
         for (; i + 3 * 256 < end; i += 4 * 256) {
-          const vec4<float> a = *reinterpret_cast<const vec4<float>*>(p + i);
-          const vec4<float> b = *reinterpret_cast<const vec4<float>*>(p + i + 256);
-          const vec4<float> c = *reinterpret_cast<const vec4<float>*>(p + i + 512);
-          const vec4<float> d = *reinterpret_cast<const vec4<float>*>(p + i + 768);
+          const vec4<float> a = stream_load(reinterpret_cast<const vec4<float>*>(p + i));
+          const vec4<float> b = stream_load(reinterpret_cast<const vec4<float>*>(p + i + 256));
+          const vec4<float> c = stream_load(reinterpret_cast<const vec4<float>*>(p + i + 512));
+          const vec4<float> d = stream_load(reinterpret_cast<const vec4<float>*>(p + i + 768));
           s0 += a.x; s1 += a.y; s2 += a.z; s3 += a.w;
           s0 += b.x; s1 += b.y; s2 += b.z; s3 += b.w;
           s0 += c.x; s1 += c.y; s2 += c.z; s3 += c.w;
           s0 += d.x; s1 += d.y; s2 += d.z; s3 += d.w;
         }
         for (; i < end; i += 256) {
-          const vec4<float> a = *reinterpret_cast<const vec4<float>*>(p + i);
+          const vec4<float> a = stream_load(reinterpret_cast<const vec4<float>*>(p + i));
           s0 += a.x; s1 += a.y; s2 += a.z; s3 += a.w;
         }
       } else {
@@ -135,17 +135,17 @@ __global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, 
         const unsigned* __restrict__ q = reinterpret_cast<const unsigned*>(p);
         std::int64_t i = begin + lane * 4;
         for (; i + 3 * 256 < end; i += 4 * 256) {
-          const vec4<unsigned> a = *reinterpret_cast<const vec4<unsigned>*>(q + i);
-          const vec4<unsigned> b = *reinterpret_cast<const vec4<unsigned>*>(q + i + 256);
-          const vec4<unsigned> c = *reinterpret_cast<const vec4<unsigned>*>(q + i + 512);
-          const vec4<unsigned> d = *reinterpret_cast<const vec4<unsigned>*>(q + i + 768);
+          const vec4<unsigned> a = stream_load(reinterpret_cast<const vec4<unsigned>*>(q + i));
+          const vec4<unsigned> b = stream_load(reinterpret_cast<const vec4<unsigned>*>(q + i + 256));
+          const vec4<unsigned> c = stream_load(reinterpret_cast<const vec4<unsigned>*>(q + i + 512));
+          const vec4<unsigned> d = stream_load(reinterpret_cast<const vec4<unsigned>*>(q + i + 768));
           s += (a.x + a.y) + (a.z + a.w);
           s += (b.x + b.y) + (b.z + b.w);
           s += (c.x + c.y) + (c.z + c.w);
           s += (d.x + d.y) + (d.z + d.w);
         }
         for (; i < end; i += 256) {
-          const vec4<unsigned> a = *reinterpret_cast<const vec4<unsigned>*>(q + i);
+          const vec4<unsigned> a = stream_load(reinterpret_cast<const vec4<unsigned>*>(q + i));
           s += (a.x + a.y) + (a.z + a.w);
         }
       } else {
@@ -160,29 +160,38 @@ __global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, 
       }
     }
   } else {
+    // Lane-local search in increasing index order; indices are kept relative
+    // to the segment start in 32 bits (segments are capped below 2^31).
     T best{};
-    std::int64_t bi = -1;
-    auto visit = [&](T v, std::int64_t i) {
-      if (bi < 0 || lane_takes<T, kLargest>(v, best)) {
+    int li = -1;
+    auto visit = [&](T v, int j) {
+      if (li < 0 || lane_takes<T, kLargest>(v, best)) {
         best = v;
-        bi = i;
+        li = j;
       }
     };
+    const int len = static_cast<int>(end - begin);
+    const T* __restrict__ q = p + begin;
     if constexpr (kVec) {
-      std::int64_t i = begin + lane * 4;
-      for (; i + 256 < end; i += 2 * 256) {
-        const vec4<T> a = *reinterpret_cast<const vec4<T>*>(p + i);
-        const vec4<T> b = *reinterpret_cast<const vec4<T>*>(p + i + 256);
-        visit(a.x, i); visit(a.y, i + 1); visit(a.z, i + 2); visit(a.w, i + 3);
-        visit(b.x, i + 256); visit(b.y, i + 257); visit(b.z, i + 258); visit(b.w, i + 259);
+      int j = lane * 4;
+      for (; j + 3 * 256 < len; j += 4 * 256) {
+        const vec4<T> a = stream_load(reinterpret_cast<const vec4<T>*>(q + j));
+        const vec4<T> b = stream_load(reinterpret_cast<const vec4<T>*>(q + j + 256));
+        const vec4<T> c = stream_load(reinterpret_cast<const vec4<T>*>(q + j + 512));
+        const vec4<T> d = stream_load(reinterpret_cast<const vec4<T>*>(q + j + 768));
+        visit(a.x, j); visit(a.y, j + 1); visit(a.z, j + 2); visit(a.w, j + 3);
+        visit(b.x, j + 256); visit(b.y, j + 257); visit(b.z, j + 258); visit(b.w, j + 259);
+        visit(c.x, j + 512); visit(c.y, j + 513); visit(c.z, j + 514); visit(c.w, j + 515);
+        visit(d.x, j + 768); visit(d.y, j + 769); visit(d.z, j + 770); visit(d.w, j + 771);
       }
-      for (; i < end; i += 256) {
-        const vec4<T> a = *reinterpret_cast<const vec4<T>*>(p + i);
-        visit(a.x, i); visit(a.y, i + 1); visit(a.z, i + 2); visit(a.w, i + 3);
+      for (; j < len; j += 256) {
+        const vec4<T> a = stream_load(reinterpret_cast<const vec4<T>*>(q + j));
+        visit(a.x, j); visit(a.y, j + 1); visit(a.z, j + 2); visit(a.w, j + 3);
       }
     } else {
-      for (std::int64_t i = begin + lane; i < end; i += 64) visit(p[i], i);
+      for (int j = lane; j < len; j += 64) visit(q[j], j);
     }
+    std::int64_t bi = li < 0 ? -1 : begin + li;
     wave_extremum<T, kLargest>(best, bi);
     if (lane == 0) {
       if (segments == 1) {
@@ -197,13 +206,16 @@ __global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, 
   }
 }
 
-// One wave per row combines that row's segment partials.
+// One 256-thread block per row combines that row's segment partials: thread
+// t folds segments t, t+256, ... in order, then waves and the block combine in
+// a fixed order, so the result is deterministic.
 template <int kOp, typename T>
 __global__ __launch_bounds__(256) void finish_kernel(const Partial* __restrict__ partials,
                                                      void* __restrict__ out, std::int64_t rows,
                                                      std::int64_t reduce, std::int64_t segments) {
-  const int lane = threadIdx.x & 63;
-  const std::int64_t row = static_cast<std::int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  __shared__ Partial waves[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const std::int64_t row = blockIdx.x;
   if (row >= rows) return;
   const Partial* p = partials + row * segments;
   constexpr bool kSum = kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN;
@@ -211,20 +223,28 @@ __global__ __launch_bounds__(256) void finish_kernel(const Partial* __restrict__
   if constexpr (kSum) {
     if constexpr (__is_same(T, float)) {
       float s = 0.F;
-      for (std::int64_t i = lane; i < segments; i += 64) s += from_bits<float>(p[i].bits);
+      for (std::int64_t i = threadIdx.x; i < segments; i += 256) s += from_bits<float>(p[i].bits);
       s = wave_sum(s);
-      if (lane == 0)
-        static_cast<float*>(out)[row] = kOp == TCX_REDUCE_MEAN ? s / static_cast<float>(reduce) : s;
+      if (lane == 0) waves[wave] = Partial{to_bits(s), 0U, 0};
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        const float t = (from_bits<float>(waves[0].bits) + from_bits<float>(waves[1].bits)) +
+                        (from_bits<float>(waves[2].bits) + from_bits<float>(waves[3].bits));
+        static_cast<float*>(out)[row] = kOp == TCX_REDUCE_MEAN ? t / static_cast<float>(reduce) : t;
+      }
     } else {
       std::uint32_t s = 0;
-      for (std::int64_t i = lane; i < segments; i += 64) s += p[i].bits;
+      for (std::int64_t i = threadIdx.x; i < segments; i += 256) s += p[i].bits;
       s = wave_sum_u32(s);
-      if (lane == 0) static_cast<int*>(out)[row] = static_cast<int>(s);
+      if (lane == 0) waves[wave] = Partial{s, 0U, 0};
+      __syncthreads();
+      if (threadIdx.x == 0)
+        static_cast<int*>(out)[row] = static_cast<int>(waves[0].bits + waves[1].bits + waves[2].bits + waves[3].bits);
     }
   } else {
     T best{};
     std::int64_t bi = -1;
-    for (std::int64_t i = lane; i < segments; i += 64) {
+    for (std::int64_t i = threadIdx.x; i < segments; i += 256) {
       const T v = from_bits<T>(p[i].bits);
       if (cand_better<T, kLargest>(v, p[i].index, best, bi)) {
         best = v;
@@ -232,7 +252,16 @@ __global__ __launch_bounds__(256) void finish_kernel(const Partial* __restrict__
       }
     }
     wave_extremum<T, kLargest>(best, bi);
-    if (lane == 0) {
+    if (lane == 0) waves[wave] = Partial{to_bits(best), 0U, bi};
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int w = 1; w < 4; ++w) {
+        const T v = from_bits<T>(waves[w].bits);
+        if (cand_better<T, kLargest>(v, waves[w].index, best, bi)) {
+          best = v;
+          bi = waves[w].index;
+        }
+      }
       if constexpr (kOp == TCX_REDUCE_ARGMAX)
         static_cast<int*>(out)[row] = static_cast<int>(bi);
       else
@@ -416,6 +445,12 @@ RowPlan plan_rows(std::int64_t outer, std::int64_t reduce, std::int64_t inner) {
       p.seg_len = len;
     }
   }
+  // 32-bit in-segment indices: split rows longer than 2^30 elements.
+  constexpr std::int64_t kMaxSegment = std::int64_t{1} << 30;
+  if (p.seg_len > kMaxSegment) {
+    p.segments = (reduce + kMaxSegment - 1) / kMaxSegment;
+    p.seg_len = kMaxSegment;
+  }
   return p;
 }
 
@@ -448,8 +483,8 @@ int launch_reduce(const T* x, void* out, std::int64_t outer, std::int64_t reduce
                        reduce, plan.segments, plan.seg_len);
   int rc = check(hipGetLastError(), "reduce row kernel launch");
   if (rc != TCX_OK || plan.segments == 1) return rc;
-  hipLaunchKernelGGL((finish_kernel<kOp, T>), dim3(grid_for(outer, 4, 0x7fffffff)), dim3(256), 0, s,
-                     partials, out, outer, reduce, plan.segments);
+  hipLaunchKernelGGL((finish_kernel<kOp, T>), dim3(static_cast<unsigned>(outer)), dim3(256), 0, s, partials, out,
+                     outer, reduce, plan.segments);
   return check(hipGetLastError(), "reduce finish kernel launch");
 }
 

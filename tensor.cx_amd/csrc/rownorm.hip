@@ -42,149 +42,191 @@ __device__ __forceinline__ float wave_max_nan(float v) {
   return v;
 }
 
+// e^x for softmax (x <= 0 there): v_exp_f32 of t = x*log2(e) with the
+// rounding error of that product, recovered exactly by an FMA plus the low
+// part of log2(e), applied as a first-order correction. About 2 ulp, against
+// the ~1 ulp of a correctly rounded expf.
+__device__ __forceinline__ float exp_softmax(float x) {
+  constexpr float kLog2e = 1.44269502F;          // float(log2 e)
+  constexpr float kLog2eLo = 1.925963033e-8F;    // log2 e - kLog2e
+  constexpr float kLn2 = 0.693147181F;
+  const float t = x * kLog2e;
+  const float e = __builtin_amdgcn_exp2f(t);
+  const float err = fmaf(x, kLog2e, -t) + x * kLog2eLo;
+  return t >= -125.0F ? fmaf(e, err * kLn2, e) : e;  // underflow, -inf and NaN keep e
+}
+
 __device__ __forceinline__ float finish_scale_ln(float ssd, std::int64_t n, float eps, bool& nan_row) {
   const float denom = ssd / static_cast<float>(n) + eps;
   nan_row = denom == 0.F;
   return 1.0F / sqrtf(denom);
 }
 
-// One wave per row, row cached in registers: kChunks float4 per lane.
-template <RowOp kOp, int kChunks, bool kVec>
-__global__ __launch_bounds__(256) void row_cached_kernel(RowArgs a) {
-  const int lane = threadIdx.x & 63;
-  const std::int64_t row = static_cast<std::int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= a.rows) return;
-  const std::int64_t n = a.n;
-  const float* __restrict__ x = a.x + row * n;
-  float* __restrict__ out = a.out + row * n;
-  float v[kChunks][4];
-  // Element (c, q) sits at column 4*(lane + 64c) + q (vector rows) or at
-  // lane + 64*(4c + q) (scalar rows); `valid` masks the row tail.
-  auto column = [&](int c, int q) -> std::int64_t {
-    return kVec ? 4 * (lane + 64 * static_cast<std::int64_t>(c)) + q
-                : lane + 64 * (4 * static_cast<std::int64_t>(c) + q);
-  };
-#pragma unroll
-  for (int c = 0; c < kChunks; ++c) {
-    if constexpr (kVec) {
-      const std::int64_t i = column(c, 0);
-      float4_t t = {0.F, 0.F, 0.F, 0.F};
-      if (i < n) t = *reinterpret_cast<const float4_t*>(x + i);
-      v[c][0] = t.x; v[c][1] = t.y; v[c][2] = t.z; v[c][3] = t.w;
-    } else {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const std::int64_t i = column(c, q);
-        v[c][q] = i < n ? x[i] : 0.F;
-      }
-    }
-  }
+// One wave per row, row cached in registers (kChunks float4 per lane).
+// Blocks are persistent: each of the grid's blocks walks rows
+// blockIdx*4 + wave, stepping by the grid, so the affine weight and bias are
+// staged into LDS once per block instead of being re-read for every row.
+// Waves per SIMD the register allocation must allow (no scratch spills): the
+// row itself takes 4*kChunks registers.
+template <RowOp kOp, int kChunks>
+constexpr int row_min_waves() {
+  if (kChunks >= 32) return 2;
+  if (kChunks == 16 && kOp != RowOp::kRms) return 3;
+  return 4;
+}
 
-  if constexpr (kOp == RowOp::kSoftmax) {
-    float m = -__builtin_inff();
+template <RowOp kOp, int kChunks, bool kVec, bool kFull>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(row_min_waves<kOp, kChunks>(), 8))) void
+row_cached_kernel(RowArgs a) {
+  extern __shared__ float4_t affine4[];  // gamma [n] then beta [n], when present
+  float* affine = reinterpret_cast<float*>(affine4);
+  const int lane = threadIdx.x & 63;
+  const std::int64_t n = a.n;
+  const bool has_g = a.gamma != nullptr, has_b = a.beta != nullptr;
+  if (has_g || has_b) {
+    for (std::int64_t i = threadIdx.x; i < n; i += 256) {
+      if (has_g) affine[i] = a.gamma[i];
+      if (has_b) affine[n + i] = a.beta[i];
+    }
+    __syncthreads();
+  }
+  // Element (c, q) sits at column 4*(lane + 64c) + q (vector rows) or at
+  // lane + 64*(4c + q) (scalar rows); columns >= n are masked. kFull rows
+  // (n == 256 * kChunks, 16-byte aligned) have no masked elements.
+  auto column = [&](int c, int q) -> int {
+    return kVec ? 4 * (lane + 64 * c) + q : lane + 64 * (4 * c + q);
+  };
+  const int ni = static_cast<int>(n);
+  auto valid = [&](int c, int q) -> bool {
+    if constexpr (kFull) return true;
+    return kVec ? column(c, 0) < ni : column(c, q) < ni;
+  };
+  const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * 4;
+  for (std::int64_t row = static_cast<std::int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); row < a.rows;
+       row += step) {
+    const float* __restrict__ x = a.x + row * n;
+    float* __restrict__ out = a.out + row * n;
+    float v[kChunks][4];
 #pragma unroll
-    for (int c = 0; c < kChunks; ++c)
+    for (int c = 0; c < kChunks; ++c) {
+      if constexpr (kVec) {
+        const int i = column(c, 0);
+        float4_t t = {0.F, 0.F, 0.F, 0.F};
+        if (valid(c, 0)) t = stream_load(reinterpret_cast<const float4_t*>(x + i));
+        v[c][0] = t.x; v[c][1] = t.y; v[c][2] = t.z; v[c][3] = t.w;
+      } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (column(c, q) < n && (is_nan(v[c][q]) || v[c][q] > m)) m = v[c][q];
-    m = wave_max_nan(m);
-    float s = 0.F;
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (column(c, q) < n) {
-          v[c][q] = expf(v[c][q] - m);
-          s += v[c][q];
+        for (int q = 0; q < 4; ++q) {
+          v[c][q] = valid(c, q) ? x[column(c, q)] : 0.F;
         }
       }
-    const float denom = wave_sum(s);
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) v[c][q] = v[c][q] / denom;
-  } else if constexpr (kOp == RowOp::kRms) {
-    float s = 0.F;
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float t = v[c][q] * v[c][q];
-        s += t;  // masked elements are zero
-      }
-    const float ss = wave_sum(s);
-    const float scale = 1.0F / sqrtf(ss / static_cast<float>(n) + a.eps);
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) v[c][q] = v[c][q] * scale;
-  } else {
-    const float first = x[0];
-    float s = 0.F;
-    bool equal = true;
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        s += v[c][q];
-        if (column(c, q) < n) equal = equal && v[c][q] == first;
-      }
-    const float mean = wave_sum(s) / static_cast<float>(n);
-    const bool all_equal = __all(equal);
-    if (all_equal && __builtin_isfinite(first)) {
-      const float fillv = a.eps == 0.F ? __builtin_nanf("") : 0.F;
+    }
+
+    if constexpr (kOp == RowOp::kSoftmax) {
+      float m = -__builtin_inff();
 #pragma unroll
       for (int c = 0; c < kChunks; ++c)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[c][q] = fillv;
+        for (int q = 0; q < 4; ++q)
+          if (valid(c, q) && (is_nan(v[c][q]) || v[c][q] > m)) m = v[c][q];
+      m = wave_max_nan(m);
+      float sum = 0.F;
+#pragma unroll
+      for (int c = 0; c < kChunks; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (valid(c, q)) {
+            v[c][q] = exp_softmax(v[c][q] - m);
+            sum += v[c][q];
+          }
+        }
+      // One correctly rounded reciprocal per row; each output is e * (1/denom),
+      // within 1.5 ulp of the reference's e / denom.
+      const float inv = 1.0F / wave_sum(sum);
+#pragma unroll
+      for (int c = 0; c < kChunks; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[c][q] = v[c][q] * inv;
+    } else if constexpr (kOp == RowOp::kRms) {
+      float sum = 0.F;
+#pragma unroll
+      for (int c = 0; c < kChunks; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float t = v[c][q] * v[c][q];
+          sum += t;  // masked elements are zero
+        }
+      const float ss = wave_sum(sum);
+      const float scale = 1.0F / sqrtf(ss / static_cast<float>(n) + a.eps);
+#pragma unroll
+      for (int c = 0; c < kChunks; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[c][q] = v[c][q] * scale;
     } else {
+      const float first = x[0];
+      float sum = 0.F;
+      bool equal = true;
+#pragma unroll
+      for (int c = 0; c < kChunks; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          sum += v[c][q];
+          if (valid(c, q)) equal = equal && v[c][q] == first;
+        }
+      const float mean = wave_sum(sum) / static_cast<float>(n);
       float d2 = 0.F;
 #pragma unroll
       for (int c = 0; c < kChunks; ++c)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          if (column(c, q) < n) {
+          if (valid(c, q)) {
             const float d = v[c][q] - mean;
             d2 += d * d;
           }
         }
       bool nan_row = false;
       const float scale = finish_scale_ln(wave_sum(d2), n, a.eps, nan_row);
+      // Row-uniform special cases as selects: an all-equal finite row gives 0
+      // (NaN when eps is 0); a zero variance + eps gives NaN.
+      const bool const_row = __all(equal) && __builtin_isfinite(first);
+      const bool special = const_row || nan_row;
+      const float special_value = const_row && a.eps != 0.F ? 0.F : __builtin_nanf("");
 #pragma unroll
       for (int c = 0; c < kChunks; ++c)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          v[c][q] = nan_row ? __builtin_nanf("") : (v[c][q] - mean) * scale;
+        for (int q = 0; q < 4; ++q) v[c][q] = special ? special_value : (v[c][q] - mean) * scale;
     }
-  }
 
-  // Affine steps (multiply then add, each rounded) and the store.
+    // Affine steps (multiply then add, each rounded) and the store.
 #pragma unroll
-  for (int c = 0; c < kChunks; ++c) {
-    if constexpr (kVec) {
-      const std::int64_t i = column(c, 0);
-      if (i >= n) continue;
-      float4_t t = {v[c][0], v[c][1], v[c][2], v[c][3]};
-      if (a.gamma) {
-        const float4_t g = *reinterpret_cast<const float4_t*>(a.gamma + i);
-        t.x = t.x * g.x; t.y = t.y * g.y; t.z = t.z * g.z; t.w = t.w * g.w;
-      }
-      if (a.beta) {
-        const float4_t b = *reinterpret_cast<const float4_t*>(a.beta + i);
-        t.x = t.x + b.x; t.y = t.y + b.y; t.z = t.z + b.z; t.w = t.w + b.w;
-      }
-      __builtin_nontemporal_store(t, reinterpret_cast<float4_t*>(out + i));
-    } else {
+    for (int c = 0; c < kChunks; ++c) {
+      if constexpr (kVec) {
+        const int i = column(c, 0);
+        if (!valid(c, 0)) continue;
+        float4_t t = {v[c][0], v[c][1], v[c][2], v[c][3]};
+        if (has_g) {
+          const float4_t g = affine4[i / 4];
+          t.x = t.x * g.x; t.y = t.y * g.y; t.z = t.z * g.z; t.w = t.w * g.w;
+        }
+        if (has_b) {
+          const float4_t b = affine4[(ni + i) / 4];
+          t.x = t.x + b.x; t.y = t.y + b.y; t.z = t.z + b.z; t.w = t.w + b.w;
+        }
+        __builtin_nontemporal_store(t, reinterpret_cast<float4_t*>(out + i));
+      } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const std::int64_t i = column(c, q);
-        if (i >= n) continue;
-        float t = v[c][q];
-        if (a.gamma) t = t * a.gamma[i];
-        if (a.beta) t = t + a.beta[i];
-        out[i] = t;
+        for (int q = 0; q < 4; ++q) {
+          if (!valid(c, q)) continue;
+          const int i = column(c, q);
+          float t = v[c][q];
+          if (has_g) t = t * affine[i];
+          if (has_b) t = t + affine[ni + i];
+          out[i] = t;
+        }
       }
     }
+    // Keep the next row's loads from being hoisted into this row's live range.
+    asm volatile("" ::: "memory");
   }
 }
 
@@ -349,13 +391,37 @@ __global__ __launch_bounds__(256) void row_lane_kernel(RowArgs a, std::int64_t r
 
 bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15U) == 0; }
 
+// Persistent grid: as many blocks as fit on the device at once (cached per
+// kernel instance and LDS size), never more than there are 4-row groups.
+template <RowOp kOp, int kChunks, bool kVec, bool kFull>
+void launch_cached_as(const RowArgs& a, hipStream_t s) {
+  const std::size_t lds = (a.gamma || a.beta) ? static_cast<std::size_t>(2 * a.n) * sizeof(float) : 0;
+  thread_local int cached_blocks = 0;
+  thread_local std::size_t cached_lds = ~std::size_t{0};
+  if (cached_lds != lds) {
+    int per_cu = 0, cus = 0, device = 0;
+    (void)hipGetDevice(&device);
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, row_cached_kernel<kOp, kChunks, kVec, kFull>, 256, lds) !=
+            hipSuccess ||
+        per_cu < 1)
+      per_cu = 1;
+    cached_blocks = per_cu * (cus > 0 ? cus : 256);
+    cached_lds = lds;
+  }
+  const std::int64_t groups = (a.rows + 3) / 4;
+  const unsigned grid = static_cast<unsigned>(groups < cached_blocks ? groups : cached_blocks);
+  hipLaunchKernelGGL((row_cached_kernel<kOp, kChunks, kVec, kFull>), dim3(grid), dim3(256), lds, s, a);
+}
+
 template <RowOp kOp, int kChunks>
 void launch_cached(const RowArgs& a, bool vec, hipStream_t s) {
-  const dim3 grid(grid_for(a.rows, 4, 0x7fffffff));
-  if (vec)
-    hipLaunchKernelGGL((row_cached_kernel<kOp, kChunks, true>), grid, dim3(256), 0, s, a);
+  if (vec && a.n == 256 * kChunks)
+    launch_cached_as<kOp, kChunks, true, true>(a, s);
+  else if (vec)
+    launch_cached_as<kOp, kChunks, true, false>(a, s);
   else
-    hipLaunchKernelGGL((row_cached_kernel<kOp, kChunks, false>), grid, dim3(256), 0, s, a);
+    launch_cached_as<kOp, kChunks, false, false>(a, s);
 }
 
 template <RowOp kOp>
@@ -374,7 +440,9 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
   const bool vec = reduce % 4 == 0 && aligned16(a.x) && aligned16(a.out) &&
                    (a.gamma == nullptr || aligned16(a.gamma)) && (a.beta == nullptr || aligned16(a.beta));
   const std::int64_t chunks = (reduce + 255) / 256;
-  if (chunks > kMaxChunks) {
+  // Rows wider than the register budget, and unaligned rows wider than 4096
+  // (whose scalar layout would spill), take the block-per-row kernel.
+  if (chunks > kMaxChunks || (!vec && chunks > 16)) {
     if (outer > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "too many rows");
     hipLaunchKernelGGL((row_block_kernel<kOp>), dim3(static_cast<unsigned>(outer)), dim3(256), 0, s, a);
     return check(hipGetLastError(), "row block kernel launch");

@@ -1,0 +1,267 @@
+"""Host-only checks of the C ABI library and the HipBackend boundary.
+
+No kernel runs here: the library must load and export every entry point the
+header declares; the bounded pool's logic is driven through its injectable
+allocator seam (the reference's PoolRuntime idea, cuda_memory_pool.h:20-27);
+device entry points must fail cleanly when no device is visible; and
+hip_backend.cpp must compile against the reference's own core headers, which
+is what makes it a drop-in backend.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+import re
+import subprocess
+
+import pytest
+
+import tensorcx_hip_capi as capi
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "tensorcx_hip.h"
+REFERENCE_CPP = pathlib.Path("/root/reference/cpp")
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(tcx_hip_\w+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert declared_functions() == sorted(capi.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    if not capi.LIB_PATH.exists():
+        pytest.fail("libtensorcx_hip.so is not built: run `python tensor.cx_amd/build.py`")
+    out = subprocess.run(["nm", "-D", "--defined-only", str(capi.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (tcx_hip_\w+)$", out, re.M))
+    missing = [name for name in declared_functions() if name not in exported]
+    assert not missing, f"missing exports: {missing}"
+    lib = capi.lib()
+    for name in declared_functions():
+        assert getattr(lib, name) is not None
+
+
+def test_header_compiles_as_c():
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only", "-x", "c", str(HEADER)],
+                   check=True)
+
+
+class FakeDevice:
+    """Host allocator standing in for hipMalloc/hipFree, with forced OOM."""
+
+    def __init__(self, capacity: int):
+        self.capacity = capacity
+        self.used = 0
+        self.blocks: dict[int, int] = {}
+        self.next = 0x1000
+        self.fail_free = False
+        self.pending = capi.TCX_OK
+        self.allocate = capi.ALLOCATE_FN(self._allocate)
+        self.free = capi.FREE_FN(self._free)
+        self.clear = capi.CLEAR_FN(self._clear)
+
+    def _allocate(self, out, nbytes):
+        if self.used + nbytes > self.capacity:
+            self.pending = capi.TCX_POOL_OOM
+            return capi.TCX_POOL_OOM
+        self.next += 0x100000
+        self.blocks[self.next] = nbytes
+        self.used += nbytes
+        out[0] = self.next
+        return capi.TCX_OK
+
+    def _free(self, ptr):
+        if self.fail_free:
+            return capi.TCX_INTERNAL
+        self.used -= self.blocks.pop(ptr)
+        return capi.TCX_OK
+
+    def _clear(self):
+        code, self.pending = self.pending, capi.TCX_OK
+        return code
+
+    def runtime(self):
+        return capi.PoolRuntime(self.allocate, self.free, self.clear)
+
+
+def make_pool(device: FakeDevice, max_bytes=1 << 20, max_blocks=4):
+    lib = capi.lib()
+    pool = ctypes.c_void_p()
+    rt = device.runtime()
+    capi.check(lib.tcx_hip_pool_create(max_bytes, max_blocks, ctypes.byref(rt), ctypes.byref(pool)))
+    return pool, rt
+
+
+def stats(pool) -> capi.PoolStats:
+    s = capi.PoolStats()
+    capi.check(capi.lib().tcx_hip_pool_stats(pool, ctypes.byref(s)))
+    return s
+
+
+def alloc(nbytes):
+    ptr, owner = ctypes.c_void_p(), ctypes.c_void_p()
+    code = capi.lib().tcx_hip_allocate(nbytes, ctypes.byref(ptr), ctypes.byref(owner))
+    return code, ptr, owner
+
+
+def test_pool_reuses_exact_sizes_and_bounds_the_cache():
+    lib = capi.lib()
+    dev = FakeDevice(1 << 30)
+    pool, rt = make_pool(dev, max_bytes=3000, max_blocks=2)
+    capi.check(lib.tcx_hip_pool_enter(pool))
+    try:
+        code, p1, o1 = alloc(1000)
+        assert code == capi.TCX_OK and o1.value == pool.value
+        lib.tcx_hip_release(p1, 1000, o1)
+        code, p2, o2 = alloc(1000)
+        assert p2.value == p1.value, "exact-size block must be reused"
+        code, p3, o3 = alloc(999)
+        assert p3.value != p1.value, "only exact sizes are reused"
+        s = stats(pool)
+        assert (s.hits, s.misses, s.in_use_bytes) == (1, 2, 1999)
+        # Cache bounds: 2 blocks / 3000 bytes.
+        _, p4, o4 = alloc(2500)
+        for ptr, n, owner in ((p2, 1000, o2), (p3, 999, o3), (p4, 2500, o4)):
+            lib.tcx_hip_release(ptr, n, owner)
+        s = stats(pool)
+        assert s.cached_blocks == 2 and s.cached_bytes == 1999 and s.uncached_returns == 1
+    finally:
+        capi.check(lib.tcx_hip_pool_exit(pool))
+    assert stats(pool).cached_blocks == 0 and dev.used == 0
+    lib.tcx_hip_pool_destroy(pool)
+
+
+def test_pool_drains_cache_and_retries_once_on_oom():
+    lib = capi.lib()
+    dev = FakeDevice(3000)
+    pool, rt = make_pool(dev, max_bytes=1 << 20, max_blocks=8)
+    capi.check(lib.tcx_hip_pool_enter(pool))
+    _, p1, o1 = alloc(2000)
+    lib.tcx_hip_release(p1, 2000, o1)         # cached, still holding 2000 device bytes
+    code, p2, o2 = alloc(2500)                # OOM -> drain -> retry succeeds
+    assert code == capi.TCX_OK
+    s = stats(pool)
+    assert s.oom_retries == 1 and s.cached_blocks == 0 and s.allocation_calls == 3
+    code, p3, _ = alloc(2000)                 # nothing cached to drain: a plain failure
+    assert code == capi.TCX_INTERNAL and "out of memory" in capi.last_error()
+    assert stats(pool).allocation_failures == 1
+    lib.tcx_hip_release(p2, 2500, o2)
+    capi.check(lib.tcx_hip_pool_exit(pool))
+    lib.tcx_hip_pool_destroy(pool)
+    assert dev.used == 0
+
+
+def test_pool_scope_rules():
+    lib = capi.lib()
+    dev = FakeDevice(1 << 20)
+    a, rta = make_pool(dev)
+    b, rtb = make_pool(dev)
+    capi.check(lib.tcx_hip_pool_enter(a))
+    assert lib.tcx_hip_pool_enter(b) == capi.TCX_INVALID_ARGUMENT
+    assert "nested" in capi.last_error()
+    assert lib.tcx_hip_pool_exit(b) == capi.TCX_INVALID_ARGUMENT
+    capi.check(lib.tcx_hip_pool_exit(a))
+    assert lib.tcx_hip_pool_enter(a) == capi.TCX_INVALID_ARGUMENT   # single use
+    assert "single-use" in capi.last_error()
+    bad = ctypes.c_void_p()
+    assert lib.tcx_hip_pool_create(1, 0, None, ctypes.byref(bad)) == capi.TCX_INVALID_ARGUMENT
+    lib.tcx_hip_pool_destroy(a)
+    lib.tcx_hip_pool_destroy(b)
+
+
+def test_pool_outlives_destroy_until_blocks_return():
+    lib = capi.lib()
+    dev = FakeDevice(1 << 20)
+    pool, rt = make_pool(dev)
+    capi.check(lib.tcx_hip_pool_enter(pool))
+    _, p, o = alloc(4096)
+    capi.check(lib.tcx_hip_pool_exit(pool))
+    lib.tcx_hip_pool_destroy(pool)            # a block is still out
+    assert dev.used == 4096
+    lib.tcx_hip_release(p, 4096, o)           # returns to the device, pool goes away
+    assert dev.used == 0
+
+
+def test_pool_free_failures_are_counted():
+    lib = capi.lib()
+    dev = FakeDevice(1 << 20)
+    pool, rt = make_pool(dev)
+    capi.check(lib.tcx_hip_pool_enter(pool))
+    _, p, o = alloc(64)
+    lib.tcx_hip_release(p, 64, o)
+    dev.fail_free = True
+    assert lib.tcx_hip_pool_trim(pool) == capi.TCX_INTERNAL
+    s = stats(pool)
+    assert s.free_failures == 1 and s.failed_free_bytes == 64 and s.cached_blocks == 0
+    dev.fail_free = False
+    capi.check(lib.tcx_hip_pool_exit(pool))
+    lib.tcx_hip_pool_destroy(pool)
+
+
+@pytest.mark.skipif(capi.available(), reason="a HIP device is visible")
+def test_device_calls_fail_cleanly_without_a_device():
+    lib = capi.lib()
+    assert lib.tcx_hip_init() == capi.TCX_UNAVAILABLE
+    s = ctypes.c_void_p()
+    assert lib.tcx_hip_stream(ctypes.byref(s)) == capi.TCX_UNAVAILABLE
+    code, _, _ = alloc(16)
+    assert code == capi.TCX_UNAVAILABLE
+    d = capi.gemm_desc(4, 4, 4)
+    assert lib.tcx_hip_gemm_f32(None, None, None, ctypes.byref(d), None) == capi.TCX_INVALID_ARGUMENT
+    assert lib.tcx_hip_reduce(9, 0, None, None, 1, 1, 1, None, 0, None) == capi.TCX_INVALID_ARGUMENT
+    assert lib.tcx_hip_reduce(2, 1, None, None, 1, 1, 1, None, 0, None) == capi.TCX_INVALID_ARGUMENT
+    assert "float32" in capi.last_error()
+
+
+def test_validation_happens_before_device_use():
+    # Malformed descriptors are rejected with INVALID_ARGUMENT whether or not
+    # a device exists (cf. test_cuda_backend_contract.cpp:416-443).
+    lib = capi.lib()
+    d = capi.gemm_desc(4, 4, 4)
+    d.batch_rank = 9
+    assert lib.tcx_hip_gemm_f32(None, None, None, ctypes.byref(d), None) == capi.TCX_INVALID_ARGUMENT
+    d = capi.gemm_desc(-1, 4, 4)
+    assert lib.tcx_hip_gemm_f32(None, None, None, ctypes.byref(d), None) == capi.TCX_INVALID_ARGUMENT
+    d = capi.gemm_desc(4, 4, 4, activation="none")
+    d.activation = 7
+    assert lib.tcx_hip_gemm_f32(None, None, None, ctypes.byref(d), None) == capi.TCX_INVALID_ARGUMENT
+    assert lib.tcx_hip_reduce(1, 0, None, None, 3, 0, 1, None, 0, None) == capi.TCX_INVALID_ARGUMENT
+    assert "non-empty" in capi.last_error()
+    shape = (ctypes.c_int64 * 9)(*([1] * 9))
+    assert lib.tcx_hip_binary(0, 0, None, None, None, 9, shape, shape, shape, None) == \
+        capi.TCX_INVALID_ARGUMENT
+    assert lib.tcx_hip_binary(3, 1, None, None, None, 1, shape, shape, shape, None) == \
+        capi.TCX_INVALID_ARGUMENT
+    assert lib.tcx_hip_layernorm_f32(None, None, None, None, 1, 4, 1, ctypes.c_float(-1.0), None) == \
+        capi.TCX_INVALID_ARGUMENT
+
+
+@pytest.mark.skipif(not REFERENCE_CPP.is_dir(), reason="reference sources not mounted")
+def test_hip_backend_compiles_against_reference_core_headers():
+    """Drop-in conformance: the backend source builds unchanged against the
+    reference's cpp/tensorcx/core headers (the repository's own restatement of
+    those headers is not on the include path)."""
+    src = ROOT / "tensor.cx_amd" / "cpp" / "tensorcx" / "backends" / "hip" / "hip_backend.cpp"
+    shadow = ROOT / "tensor.cx_amd" / "_build" / "conformance"
+    (shadow / "tensorcx" / "backends" / "hip").mkdir(parents=True, exist_ok=True)
+    header = shadow / "tensorcx" / "backends" / "hip" / "hip_backend.h"
+    header.write_text((src.parent / "hip_backend.h").read_text())
+    subprocess.run(["g++", "-std=c++20", "-fsyntax-only", "-Wall", f"-I{shadow}",
+                    f"-I{REFERENCE_CPP}", f"-I{ROOT / 'include'}", str(src)], check=True)
+
+
+def test_backend_library_has_no_cpu_compute_fallback():
+    """The native module links the HIP library and calls no oracle code."""
+    core = list((ROOT / "tensor.cx_amd" / "python" / "tensorcx").glob("_core*.so"))
+    if not core:
+        pytest.fail("tensorcx/_core is not built")
+    deps = subprocess.run(["ldd", str(core[0])], capture_output=True, text=True,
+                          env={**os.environ, "LD_LIBRARY_PATH": ""}).stdout
+    assert "libtensorcx_hip.so" in deps
+    assert "oracle" not in deps and "tcxref" not in deps
