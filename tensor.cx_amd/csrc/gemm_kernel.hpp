@@ -4,10 +4,6 @@
 
 #include "common.hpp"
 
-// 1: read the next k-step's LDS fragments before the current MFMAs.
-#ifndef TCX_GEMM_LDS_PIPELINE
-#define TCX_GEMM_LDS_PIPELINE 0
-#endif
 
 namespace tcx {
 namespace gemm {
@@ -38,31 +34,40 @@ __device__ __forceinline__ float activate(float v, int act) {
   return v;
 }
 
-template <int N>
-struct Frag;
-template <>
-struct Frag<4> {
-  static __device__ __forceinline__ void load(const float* p, float (&v)[4]) {
-    const float4_t t = *reinterpret_cast<const float4_t*>(p);
-    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
-  }
-};
-template <>
-struct Frag<8> {
-  static __device__ __forceinline__ void load(const float* p, float (&v)[8]) {
-    const float4_t t0 = *reinterpret_cast<const float4_t*>(p);
-    const float4_t t1 = *reinterpret_cast<const float4_t*>(p + 4);
-    v[0] = t0.x; v[1] = t0.y; v[2] = t0.z; v[3] = t0.w;
-    v[4] = t1.x; v[5] = t1.y; v[6] = t1.z; v[7] = t1.w;
-  }
-};
-template <>
-struct Frag<2> {
-  static __device__ __forceinline__ void load(const float* p, float (&v)[2]) {
-    const float2 t = *reinterpret_cast<const float2*>(p);
+// Position inside a wave tile of element e (0 <= e < T) owned by MFMA lane
+// row/column r (0..15) for a T-wide fragment. For T >= 4 the elements come in
+// float4 groups 64 positions apart, so the 16 lanes sharing a k read 256
+// contiguous bytes per group (one conflict-free ds_read_b128 each); for T = 2
+// a lane's pair is adjacent.
+template <int T>
+__device__ __forceinline__ int frag_pos(int r, int e) {
+  if constexpr (T >= 4)
+    return (e >> 2) * 64 + r * 4 + (e & 3);
+  else
+    return r * T + e;
+}
+
+// XOR swizzle of the m (or n) index of tiles stored transposed (k-major from
+// k-contiguous global rows): flips bits 3-4 by k/4, which spreads the scalar
+// transposed stores of the four k-quads over distinct banks and keeps every
+// aligned group of 4 contiguous for the 16-byte fragment reads.
+__device__ __forceinline__ int swz(int k, int m) { return m ^ (((k >> 2) & 3) << 3); }
+
+// Reads the T fragment values of lane row r from LDS row `row` (already
+// offset to the wave tile); `sw` is the row's swizzle (0 when unswizzled).
+template <int T>
+__device__ __forceinline__ void load_frag(const float* row, int r, int sw, float (&v)[T]) {
+  if constexpr (T >= 4) {
+#pragma unroll
+    for (int g = 0; g < T / 4; ++g) {
+      const float4_t t = *reinterpret_cast<const float4_t*>(row + ((g * 64 + r * 4) ^ sw));
+      v[4 * g] = t.x; v[4 * g + 1] = t.y; v[4 * g + 2] = t.z; v[4 * g + 3] = t.w;
+    }
+  } else {
+    const float2 t = *reinterpret_cast<const float2*>(row + ((r * T) ^ sw));
     v[0] = t.x; v[1] = t.y;
   }
-};
+}
 
 template <int BM, int BN, int BK, int WM, int WN, int kMinWaves, bool kTransB, bool kVec>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64)
@@ -177,7 +182,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
         const int idx = tid + p * kThreads;
         const int row = idx / (BK / 4), kq = idx % (BK / 4);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) As[buf][kq * 4 + q][row] = ra[4 * p + q];
+        for (int q = 0; q < 4; ++q) As[buf][kq * 4 + q][swz(kq * 4 + q, row)] = ra[4 * p + q];
       }
 #pragma unroll
       for (int p = 0; p < kBVec; ++p) {
@@ -185,7 +190,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
         if constexpr (kTransB) {
           const int row = idx / (BK / 4), kq = idx % (BK / 4);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) Bs[buf][kq * 4 + q][row] = rb[4 * p + q];
+          for (int q = 0; q < 4; ++q) Bs[buf][kq * 4 + q][swz(kq * 4 + q, row)] = rb[4 * p + q];
         } else {
           const int krow = idx / (BN / 4), nq = idx % (BN / 4);
           const float4_t v = {rb[4 * p], rb[4 * p + 1], rb[4 * p + 2], rb[4 * p + 3]};
@@ -196,13 +201,13 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
 #pragma unroll
       for (int p = 0; p < kAScalar; ++p) {
         const int idx = tid + p * kThreads;
-        As[buf][idx % BK][idx / BK] = ra[p];
+        As[buf][idx % BK][swz(idx % BK, idx / BK)] = ra[p];
       }
 #pragma unroll
       for (int p = 0; p < kBScalar; ++p) {
         const int idx = tid + p * kThreads;
         if constexpr (kTransB)
-          Bs[buf][idx % BK][idx / BK] = rb[p];
+          Bs[buf][idx % BK][swz(idx % BK, idx / BK)] = rb[p];
         else
           Bs[buf][idx / BN][idx % BN] = rb[p];
       }
@@ -228,54 +233,38 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
     const int buf = static_cast<int>(kt & 1);
     const bool more = kt + 1 < k_tiles;
     if (more) load_tile((kt + 1) * BK);
-#if TCX_GEMM_LDS_PIPELINE
-    // Fragments for k-step s+1 are read from LDS while step s's MFMAs run.
-    float av[2][TM], bv[2][TN];
-    Frag<TM>::load(&As[buf][kl][wm * WM + r * TM], av[0]);
-    Frag<TN>::load(&Bs[buf][kl][wn * WN + r * TN], bv[0]);
-#pragma unroll
-    for (int s = 0; s < BK / 4; ++s) {
-      const int cur = s & 1;
-      if (s + 1 < BK / 4) {
-        const int k = (s + 1) * 4 + kl;
-        Frag<TM>::load(&As[buf][k][wm * WM + r * TM], av[cur ^ 1]);
-        Frag<TN>::load(&Bs[buf][k][wn * WN + r * TN], bv[cur ^ 1]);
-      }
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[cur][i], bv[cur][j], acc[i][j], 0, 0, 0);
-    }
-#else
 #pragma unroll
     for (int s = 0; s < BK / 4; ++s) {
       const int k = s * 4 + kl;
+      const int sw = swz(k, 0);
       float av[TM], bv[TN];
-      Frag<TM>::load(&As[buf][k][wm * WM + r * TM], av);
-      Frag<TN>::load(&Bs[buf][k][wn * WN + r * TN], bv);
+      load_frag<TM>(&As[buf][k][wm * WM], r, sw, av);
+      load_frag<TN>(&Bs[buf][k][wn * WN], r, kTransB ? sw : 0, bv);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
     }
-#endif
     if (more) store_tile(buf ^ 1);
     __syncthreads();
   }
 
   // Epilogue: bias add then activation, as kAdd then kSilu/kGelu would round.
-  const std::int64_t col0 = n0 + wn * WN + r * TN;
+  // Register q of block (i, j) holds tile row frag_pos<TM>(4*kl + q, i) and
+  // tile column frag_pos<TN>(r, j).
+  const std::int64_t col_base = n0 + wn * WN;
   float bias[TN];
 #pragma unroll
-  for (int j = 0; j < TN; ++j)
-    bias[j] = (a.bias != nullptr && col0 + j < N) ? a.bias[col0 + j] : 0.F;
+  for (int j = 0; j < TN; ++j) {
+    const std::int64_t col = col_base + frag_pos<TN>(r, j);
+    bias[j] = (a.bias != nullptr && col < N) ? a.bias[col] : 0.F;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const std::int64_t row = m0 + wm * WM + (kl * 4 + q) * TM + i;
+      const std::int64_t row = m0 + wm * WM + frag_pos<TM>(kl * 4 + q, i);
       if (row >= M) continue;
       float v[TN];
 #pragma unroll
@@ -284,15 +273,25 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
         if (a.bias != nullptr) x = x + bias[j];
         v[j] = activate(x, a.activation);
       }
-      float* dst = C + row * N + col0;
-      if (kVec && TN >= 4 && col0 + TN - 1 < N) {
+      float* dst = C + row * N + col_base;
+      if constexpr (TN >= 4) {
 #pragma unroll
-        for (int j = 0; j < TN; j += 4)
-          *reinterpret_cast<float4_t*>(dst + j) = float4_t{v[j], v[j + 1], v[j + 2], v[j + 3]};
+        for (int g = 0; g < TN / 4; ++g) {
+          const std::int64_t col = g * 64 + r * 4;
+          if (kVec && col_base + col + 3 < N) {
+            *reinterpret_cast<float4_t*>(dst + col) = float4_t{v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (col_base + col + e < N) dst[col + e] = v[4 * g + e];
+          }
+        }
       } else {
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          if (col0 + j < N) dst[j] = v[j];
+        for (int j = 0; j < TN; ++j) {
+          const int col = frag_pos<TN>(r, j);
+          if (col_base + col < N) dst[col] = v[j];
+        }
       }
     }
   }
