@@ -79,14 +79,16 @@ extern "C" int tcx_hip_gemm_f32(const float* lhs, const float* rhs, float* out,
   const bool trans_b = d->rhs_transposed != 0;
   args.total_tiles = batches;
   const auto s = static_cast<hipStream_t>(stream);
-  // Tile choice (measured on MI355X over the config shapes): 128x256 blocks of
-  // four 64x128 waves at 2 waves/SIMD when there are >= 512 of them (two per
-  // CU, one full round); 128x128 blocks of eight 32x64 waves when there are
-  // >= 256; 64x64 blocks otherwise (small and edge shapes).
-  const std::int64_t tiles_m128 = (d->m + 127) / 128;
-  if (tiles_m128 * ((d->n + 255) / 256) * batches >= 512)
-    return launch_config<128, 256, 16, 64, 128, 2>(args, trans_b, vec, s);
-  if (tiles_m128 * ((d->n + 127) / 128) * batches >= 256)
+  // Tile choice (swept on MI355X over the config shapes): 256x256 blocks of
+  // eight 64x128 waves, 32-wide k-tiles (133 KB of LDS, 2 waves/SIMD) when
+  // there are >= 256 of them (one full round on 256 CUs); 128x128 blocks of
+  // eight 32x64 waves when there are >= 256 of those; 64x64 blocks otherwise
+  // (small and edge shapes).
+  const std::int64_t tiles_256 = ((d->m + 255) / 256) * ((d->n + 255) / 256) * batches;
+  // (Unaligned shapes take the scalar-load variant, which does not fit the
+  // 256x256 tile's registers; they use the 128x128 tile.)
+  if (vec && tiles_256 >= 256) return launch_config<256, 256, 32, 64, 128, 2, true>(args, trans_b, true, s);
+  if (((d->m + 127) / 128) * ((d->n + 127) / 128) * batches >= 256)
     return launch_config<128, 128, 16, 32, 64, 1>(args, trans_b, vec, s);
   return launch_config<64, 64, 16, 32, 32, 1>(args, trans_b, vec, s);
 }

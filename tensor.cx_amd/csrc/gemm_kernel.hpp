@@ -48,10 +48,16 @@ __device__ __forceinline__ int frag_pos(int r, int e) {
 }
 
 // XOR swizzle of the m (or n) index of tiles stored transposed (k-major from
-// k-contiguous global rows): flips bits 3-4 by k/4, which spreads the scalar
-// transposed stores of the four k-quads over distinct banks and keeps every
-// aligned group of 4 contiguous for the 16-byte fragment reads.
-__device__ __forceinline__ int swz(int k, int m) { return m ^ (((k >> 2) & 3) << 3); }
+// k-contiguous global rows), with rows padded by 8 floats: the k-quad (k/4)
+// flips bits 3-4 of m for 16-wide k-tiles and bits 2-4 for 32-wide ones. With
+// the thread-to-element map of load_tile the scalar transposed stores of a
+// 32-wide k-tile land on distinct banks (SQ_LDS_BANK_CONFLICT reads 0 for
+// them), and an XOR by a multiple of 4 keeps every aligned group of 4
+// contiguous for the 16-byte fragment reads.
+template <int BK>
+__device__ __forceinline__ int swz(int k, int m) {
+  return m ^ (((k >> 2) & 7) << (BK >= 32 ? 2 : 3));
+}
 
 // Reads the T fragment values of lane row r from LDS row `row` (already
 // offset to the wave tile); `sw` is the row's swizzle (0 when unswizzled).
@@ -75,7 +81,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
   constexpr int kWavesN = BN / WN;
   constexpr int kThreads = (BM / WM) * kWavesN * 64;
   constexpr int TM = WM / 16, TN = WN / 16;
-  constexpr int LDA = BM + 4, LDB = BN + 4;
+  constexpr int LDA = BM + 8, LDB = BN + 8;
   static_assert(BK % 4 == 0 && (BM * BK) % (4 * kThreads) == 0 && (BN * BK) % (4 * kThreads) == 0);
   constexpr int kAVec = BM * BK / 4 / kThreads;  // float4 loads per thread for A
   constexpr int kBVec = BN * BK / 4 / kThreads;
@@ -182,7 +188,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
         const int idx = tid + p * kThreads;
         const int row = idx / (BK / 4), kq = idx % (BK / 4);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) As[buf][kq * 4 + q][swz(kq * 4 + q, row)] = ra[4 * p + q];
+        for (int q = 0; q < 4; ++q) As[buf][kq * 4 + q][swz<BK>(kq * 4 + q, row)] = ra[4 * p + q];
       }
 #pragma unroll
       for (int p = 0; p < kBVec; ++p) {
@@ -190,7 +196,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
         if constexpr (kTransB) {
           const int row = idx / (BK / 4), kq = idx % (BK / 4);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) Bs[buf][kq * 4 + q][swz(kq * 4 + q, row)] = rb[4 * p + q];
+          for (int q = 0; q < 4; ++q) Bs[buf][kq * 4 + q][swz<BK>(kq * 4 + q, row)] = rb[4 * p + q];
         } else {
           const int krow = idx / (BN / 4), nq = idx % (BN / 4);
           const float4_t v = {rb[4 * p], rb[4 * p + 1], rb[4 * p + 2], rb[4 * p + 3]};
@@ -201,13 +207,13 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
 #pragma unroll
       for (int p = 0; p < kAScalar; ++p) {
         const int idx = tid + p * kThreads;
-        As[buf][idx % BK][swz(idx % BK, idx / BK)] = ra[p];
+        As[buf][idx % BK][swz<BK>(idx % BK, idx / BK)] = ra[p];
       }
 #pragma unroll
       for (int p = 0; p < kBScalar; ++p) {
         const int idx = tid + p * kThreads;
         if constexpr (kTransB)
-          Bs[buf][idx % BK][swz(idx % BK, idx / BK)] = rb[p];
+          Bs[buf][idx % BK][swz<BK>(idx % BK, idx / BK)] = rb[p];
         else
           Bs[buf][idx / BN][idx % BN] = rb[p];
       }
@@ -236,7 +242,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
 #pragma unroll
     for (int s = 0; s < BK / 4; ++s) {
       const int k = s * 4 + kl;
-      const int sw = swz(k, 0);
+      const int sw = swz<BK>(k, 0);
       float av[TM], bv[TN];
       load_frag<TM>(&As[buf][k][wm * WM], r, sw, av);
       load_frag<TN>(&Bs[buf][k][wn * WN], r, kTransB ? sw : 0, bv);
@@ -297,7 +303,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int kMinWaves>
+template <int BM, int BN, int BK, int WM, int WN, int kMinWaves, bool kVecOnly = false>
 int launch_config(GemmArgs& args, bool trans_b, bool vec, hipStream_t stream) {
   args.tiles_m = (args.m + BM - 1) / BM;
   args.tiles_n = (args.n + BN - 1) / BN;
@@ -306,7 +312,13 @@ int launch_config(GemmArgs& args, bool trans_b, bool vec, hipStream_t stream) {
   if (args.total_tiles > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
   const dim3 grid(static_cast<unsigned>(args.total_tiles));
   const dim3 block((BM / WM) * (BN / WN) * 64);
-  if (trans_b) {
+  if constexpr (kVecOnly) {
+    if (!vec) return fail(TCX_INTERNAL, "gemm tile requires 16-byte aligned operands");
+    if (trans_b)
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, true, true>), grid, block, 0, stream, args);
+    else
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, false, true>), grid, block, 0, stream, args);
+  } else if (trans_b) {
     if (vec)
       hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, true, true>), grid, block, 0, stream, args);
     else

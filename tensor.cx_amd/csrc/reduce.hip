@@ -30,8 +30,9 @@ constexpr std::int64_t kSequentialMax = 64;   // rows up to this length keep exa
 constexpr std::int64_t kTargetWaves = 8192;   // 32 waves per CU on 256 CUs
 constexpr std::int64_t kMinSegment = 4096;    // elements per segment when splitting rows
 
-// Partial result of one (row, segment): a float or uint32 sum, or a
-// (value bits, index) extremum candidate; index < 0 marks an empty candidate.
+// Partial result of one (row, segment) of an extremum search: (value bits,
+// index); index < 0 marks an empty candidate. Sum partials are stored instead
+// as dense 32-bit words (float bits or uint32) at the start of the workspace.
 struct Partial {
   std::uint32_t bits;
   std::uint32_t pad;
@@ -126,7 +127,7 @@ __global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, 
         if (segments == 1) {
           static_cast<float*>(out)[row] = kOp == TCX_REDUCE_MEAN ? s / static_cast<float>(reduce) : s;
         } else {
-          partials[gw] = Partial{to_bits(s), 0U, 0};
+          reinterpret_cast<std::uint32_t*>(partials)[gw] = to_bits(s);  // dense words
         }
       }
     } else {
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, 
         if (segments == 1)
           static_cast<int*>(out)[row] = static_cast<int>(s);
         else
-          partials[gw] = Partial{s, 0U, 0};
+          reinterpret_cast<std::uint32_t*>(partials)[gw] = s;
       }
     }
   } else {
@@ -222,9 +223,20 @@ __global__ __launch_bounds__(256) void finish_kernel(const Partial* __restrict__
   constexpr bool kLargest = kOp != TCX_REDUCE_MIN;
   if constexpr (kSum) {
     if constexpr (__is_same(T, float)) {
-      float s = 0.F;
-      for (std::int64_t i = threadIdx.x; i < segments; i += 256) s += from_bits<float>(p[i].bits);
-      s = wave_sum(s);
+      // Sum partials are dense 32-bit words; 16 independent loads per step.
+      const std::uint32_t* w = reinterpret_cast<const std::uint32_t*>(partials) + row * segments;
+      float acc[16] = {};
+      std::int64_t i = threadIdx.x;
+      for (; i + 15 * 256 < segments; i += 16 * 256) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) acc[u] += from_bits<float>(w[i + u * 256]);
+      }
+      for (; i < segments; i += 256) acc[0] += from_bits<float>(w[i]);
+#pragma unroll
+      for (int u = 8; u > 0; u >>= 1)
+#pragma unroll
+        for (int v = 0; v < u; ++v) acc[v] += acc[v + u];
+      float s = wave_sum(acc[0]);
       if (lane == 0) waves[wave] = Partial{to_bits(s), 0U, 0};
       __syncthreads();
       if (threadIdx.x == 0) {
@@ -233,8 +245,17 @@ __global__ __launch_bounds__(256) void finish_kernel(const Partial* __restrict__
         static_cast<float*>(out)[row] = kOp == TCX_REDUCE_MEAN ? t / static_cast<float>(reduce) : t;
       }
     } else {
+      const std::uint32_t* w = reinterpret_cast<const std::uint32_t*>(partials) + row * segments;
+      std::uint32_t acc[16] = {};
+      std::int64_t i = threadIdx.x;
+      for (; i + 15 * 256 < segments; i += 16 * 256) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) acc[u] += w[i + u * 256];
+      }
+      for (; i < segments; i += 256) acc[0] += w[i];
       std::uint32_t s = 0;
-      for (std::int64_t i = threadIdx.x; i < segments; i += 256) s += p[i].bits;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) s += acc[u];
       s = wave_sum_u32(s);
       if (lane == 0) waves[wave] = Partial{s, 0U, 0};
       __syncthreads();
