@@ -2,12 +2,13 @@
 // the optional affine weight/bias of the kAffine*Norm composites
 // (core/inference.cpp:103-122) fused into the same pass.
 //
-// Contiguous rows (inner == 1) of up to 64*4*kMaxChunks elements: one wave per
-// row holds the whole row in registers (kChunks 16-byte loads per lane), so
-// each element is read from HBM once and written once; the row statistics use
-// wave-wide butterfly reductions. Longer rows use one 256-thread block per
-// row and re-read the row (mostly from L2). Strided rows (inner > 1) use one
-// lane per row in the reference's exact element order.
+// Contiguous rows (inner == 1) stay in registers, so each element is read from
+// HBM once and written once: rows of up to 1024 elements take one wave per row
+// (kChunks 16-byte loads per lane, wave-wide butterfly statistics); rows of up
+// to kMaxSplit elements take one 256-thread block per row (four waves, whose
+// partial statistics meet in LDS). Longer rows use one block per row that
+// re-reads the row (mostly from L2). Strided rows (inner > 1) use one lane per
+// row in the reference's exact element order.
 //
 // Per-element arithmetic follows the reference step by step (exp(x - max),
 // sum, division; (x - mean) * scale; x * scale), each step rounded separately
@@ -19,7 +20,8 @@
 namespace tcx {
 namespace {
 
-constexpr int kMaxChunks = 32;  // rows up to 8192 floats stay in registers
+constexpr int kMaxWaveChunks = 4;  // one wave per row up to 1024 floats
+constexpr int kMaxSplit = 16;      // one block per row up to 256*4*16 floats
 
 enum class RowOp { kSoftmax, kRms, kLayer };
 
@@ -66,17 +68,8 @@ __device__ __forceinline__ float finish_scale_ln(float ssd, std::int64_t n, floa
 // Blocks are persistent: each of the grid's blocks walks rows
 // blockIdx*4 + wave, stepping by the grid, so the affine weight and bias are
 // staged into LDS once per block instead of being re-read for every row.
-// Waves per SIMD the register allocation must allow (no scratch spills): the
-// row itself takes 4*kChunks registers.
-template <RowOp kOp, int kChunks>
-constexpr int row_min_waves() {
-  if (kChunks >= 32) return 2;
-  if (kChunks == 16 && kOp != RowOp::kRms) return 3;
-  return 4;
-}
-
 template <RowOp kOp, int kChunks, bool kVec, bool kFull>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(row_min_waves<kOp, kChunks>(), 8))) void
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 row_cached_kernel(RowArgs a) {
   extern __shared__ float4_t affine4[];  // gamma [n] then beta [n], when present
   float* affine = reinterpret_cast<float*>(affine4);
@@ -223,6 +216,188 @@ row_cached_kernel(RowArgs a) {
           if (has_b) t = t + affine[ni + i];
           out[i] = t;
         }
+      }
+    }
+    // Keep the next row's loads from being hoisted into this row's live range.
+    asm volatile("" ::: "memory");
+  }
+}
+
+// One 256-thread block per row, the row cached in registers: thread t holds
+// kPer float4 at columns 4*(t + 256c) (vector rows) or 4*kPer floats at
+// t + 256*(4c + q) (scalar rows). Each wave reduces its part with butterflies
+// and the four wave partials meet in LDS, combined in wave order. Blocks are
+// persistent (a few per CU walk the rows, stepping by the grid), which keeps
+// the set of rows in flight, and the HBM pages they touch, small. For kPer <= 4
+// the affine weight and bias of a thread's columns stay in registers across
+// rows; wider rows re-read them (L2-resident) for every row.
+template <RowOp kOp, int kPer, bool kVec, bool kFull>
+__global__ __launch_bounds__(256) void row_split_kernel(RowArgs a) {
+  constexpr bool kAffRegs = kPer <= 4;
+  // Statistics exchange, double-buffered by row parity so a wave that runs
+  // ahead never overwrites a slot another wave has yet to read.
+  __shared__ float red[2][2][4];  // [row parity][statistic][wave]
+  __shared__ int same[2][4];      // LayerNorm all-equal flag per wave
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const std::int64_t n = a.n;
+  const int ni = static_cast<int>(n);
+  auto column = [&](int c, int q) -> int { return kVec ? 4 * (t + 256 * c) + q : t + 256 * (4 * c + q); };
+  auto valid = [&](int c, int q) -> bool {
+    if constexpr (kFull) return true;
+    return kVec ? column(c, 0) < ni : column(c, q) < ni;
+  };
+  const bool has_g = a.gamma != nullptr, has_b = a.beta != nullptr;
+  auto load_affine = [&](const float* p, int c, float fallback, float (&dst)[4]) {
+    if constexpr (kVec) {
+      float4_t w = {fallback, fallback, fallback, fallback};
+      if (p != nullptr && valid(c, 0)) w = *reinterpret_cast<const float4_t*>(p + column(c, 0));
+      dst[0] = w.x; dst[1] = w.y; dst[2] = w.z; dst[3] = w.w;
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) dst[q] = (p != nullptr && valid(c, q)) ? p[column(c, q)] : fallback;
+    }
+  };
+  float g[kAffRegs ? kPer : 1][4], b[kAffRegs ? kPer : 1][4];
+  if constexpr (kAffRegs) {
+#pragma unroll
+    for (int c = 0; c < kPer; ++c) {
+      load_affine(a.gamma, c, 1.F, g[c]);
+      load_affine(a.beta, c, 0.F, b[c]);
+    }
+  }
+  auto combine = [&](float v, int par, int stat, bool is_max) -> float {
+    if (lane == 0) red[par][stat][wave] = v;
+    __syncthreads();
+    float r = red[par][stat][0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      const float o = red[par][stat][w];
+      r = is_max ? ((is_nan(o) || o > r) ? o : r) : r + o;
+    }
+    return r;
+  };
+
+  int par = 0;
+  for (std::int64_t row = blockIdx.x; row < a.rows; row += gridDim.x, par ^= 1) {
+    const float* __restrict__ x = a.x + row * n;
+    float* __restrict__ out = a.out + row * n;
+    float v[kPer][4];
+#pragma unroll
+    for (int c = 0; c < kPer; ++c) {
+      if constexpr (kVec) {
+        float4_t q = {0.F, 0.F, 0.F, 0.F};
+        if (valid(c, 0)) q = stream_load(reinterpret_cast<const float4_t*>(x + column(c, 0)));
+        v[c][0] = q.x; v[c][1] = q.y; v[c][2] = q.z; v[c][3] = q.w;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[c][q] = valid(c, q) ? x[column(c, q)] : 0.F;
+      }
+    }
+
+    if constexpr (kOp == RowOp::kSoftmax) {
+      float m = -__builtin_inff();
+#pragma unroll
+      for (int c = 0; c < kPer; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (valid(c, q) && (is_nan(v[c][q]) || v[c][q] > m)) m = v[c][q];
+      m = combine(wave_max_nan(m), par, 0, true);
+      float sum = 0.F;
+#pragma unroll
+      for (int c = 0; c < kPer; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (valid(c, q)) {
+            v[c][q] = exp_softmax(v[c][q] - m);
+            sum += v[c][q];
+          }
+        }
+      // One correctly rounded reciprocal per row; each output is e * (1/denom),
+      // within 1.5 ulp of the reference's e / denom.
+      const float inv = 1.0F / combine(wave_sum(sum), par, 1, false);
+#pragma unroll
+      for (int c = 0; c < kPer; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[c][q] = v[c][q] * inv;
+    } else if constexpr (kOp == RowOp::kRms) {
+      float sum = 0.F;
+#pragma unroll
+      for (int c = 0; c < kPer; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float sq = v[c][q] * v[c][q];
+          sum += sq;  // masked elements are zero
+        }
+      const float ss = combine(wave_sum(sum), par, 0, false);
+      const float scale = 1.0F / sqrtf(ss / static_cast<float>(n) + a.eps);
+#pragma unroll
+      for (int c = 0; c < kPer; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[c][q] = v[c][q] * scale;
+    } else {
+      const float first = x[0];
+      float sum = 0.F;
+      bool equal = true;
+#pragma unroll
+      for (int c = 0; c < kPer; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          sum += v[c][q];  // masked elements are zero
+          if (valid(c, q)) equal = equal && v[c][q] == first;
+        }
+      const bool wave_equal = __all(equal);
+      if (lane == 0) same[par][wave] = wave_equal ? 1 : 0;
+      const float mean = combine(wave_sum(sum), par, 0, false) / static_cast<float>(n);
+      const bool all_equal = same[par][0] && same[par][1] && same[par][2] && same[par][3];
+      float d2 = 0.F;
+#pragma unroll
+      for (int c = 0; c < kPer; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (valid(c, q)) {
+            const float d = v[c][q] - mean;
+            d2 += d * d;
+          }
+        }
+      bool nan_row = false;
+      const float scale = finish_scale_ln(combine(wave_sum(d2), par, 1, false), n, a.eps, nan_row);
+      // Row-uniform special cases as selects: an all-equal finite row gives 0
+      // (NaN when eps is 0); a zero variance + eps gives NaN.
+      const bool const_row = all_equal && __builtin_isfinite(first);
+      const bool special = const_row || nan_row;
+      const float special_value = const_row && a.eps != 0.F ? 0.F : __builtin_nanf("");
+#pragma unroll
+      for (int c = 0; c < kPer; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[c][q] = special ? special_value : (v[c][q] - mean) * scale;
+    }
+
+    // Affine steps (multiply then add, each rounded) and the store.
+#pragma unroll
+    for (int c = 0; c < kPer; ++c) {
+      float gc[4], bc[4];
+      if constexpr (kAffRegs) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) { gc[q] = g[c][q]; bc[q] = b[c][q]; }
+      } else {
+        if (has_g) load_affine(a.gamma, c, 1.F, gc);
+        if (has_b) load_affine(a.beta, c, 0.F, bc);
+      }
+      float r[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        r[q] = v[c][q];
+        if (has_g) r[q] = r[q] * gc[q];
+        if (has_b) r[q] = r[q] + bc[q];
+      }
+      if constexpr (kVec) {
+        if (!valid(c, 0)) continue;
+        const float4_t o = {r[0], r[1], r[2], r[3]};
+        __builtin_nontemporal_store(o, reinterpret_cast<float4_t*>(out + column(c, 0)));
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (valid(c, q)) out[column(c, q)] = r[q];
       }
     }
     // Keep the next row's loads from being hoisted into this row's live range.
@@ -414,6 +589,47 @@ void launch_cached_as(const RowArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((row_cached_kernel<kOp, kChunks, kVec, kFull>), dim3(grid), dim3(256), lds, s, a);
 }
 
+// Persistent split grid: kSplitBlocksPerCu blocks per CU (fewer if the
+// occupancy calculator allows fewer), never more than there are rows. A few
+// blocks per CU keep enough loads in flight while the rows being streamed at
+// any moment stay close together.
+constexpr int kSplitBlocksPerCu = 3;
+
+template <RowOp kOp, int kPer, bool kVec, bool kFull>
+void launch_split_as(const RowArgs& a, hipStream_t s) {
+  thread_local int cached_blocks = 0;
+  if (cached_blocks == 0) {
+    int per_cu = 0, cus = 0, device = 0;
+    (void)hipGetDevice(&device);
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, row_split_kernel<kOp, kPer, kVec, kFull>, 256, 0) !=
+            hipSuccess ||
+        per_cu < 1)
+      per_cu = 1;
+    if (per_cu > kSplitBlocksPerCu) per_cu = kSplitBlocksPerCu;
+    cached_blocks = per_cu * (cus > 0 ? cus : 256);
+  }
+  const unsigned grid = static_cast<unsigned>(a.rows < cached_blocks ? a.rows : cached_blocks);
+  hipLaunchKernelGGL((row_split_kernel<kOp, kPer, kVec, kFull>), dim3(grid), dim3(256), 0, s, a);
+}
+
+// Scalar (unaligned) rows keep one address per element live, so only rows of
+// up to kMaxScalarSplit float4 per thread use the split kernel unaligned.
+constexpr int kMaxScalarSplit = 4;
+
+template <RowOp kOp, int kPer>
+int launch_split(const RowArgs& a, bool vec, hipStream_t s) {
+  if (vec && a.n == 1024 * kPer) {
+    launch_split_as<kOp, kPer, true, true>(a, s);
+  } else if (vec) {
+    launch_split_as<kOp, kPer, true, false>(a, s);
+  } else {
+    if constexpr (kPer > kMaxScalarSplit) return fail(TCX_INTERNAL, "unaligned row too wide for the split kernel");
+    else launch_split_as<kOp, kPer, false, false>(a, s);
+  }
+  return check(hipGetLastError(), "row kernel launch");
+}
+
 template <RowOp kOp, int kChunks>
 void launch_cached(const RowArgs& a, bool vec, hipStream_t s) {
   if (vec && a.n == 256 * kChunks)
@@ -439,20 +655,22 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
   a.n = reduce;
   const bool vec = reduce % 4 == 0 && aligned16(a.x) && aligned16(a.out) &&
                    (a.gamma == nullptr || aligned16(a.gamma)) && (a.beta == nullptr || aligned16(a.beta));
-  const std::int64_t chunks = (reduce + 255) / 256;
-  // Rows wider than the register budget, and unaligned rows wider than 4096
-  // (whose scalar layout would spill), take the block-per-row kernel.
-  if (chunks > kMaxChunks || (!vec && chunks > 16)) {
+  const std::int64_t chunks = (reduce + 255) / 256;  // per lane, one wave per row
+  const std::int64_t per = (reduce + 1023) / 1024;    // per thread, one block per row
+  if (chunks <= 1) launch_cached<kOp, 1>(a, vec, s);
+  else if (chunks <= 2) launch_cached<kOp, 2>(a, vec, s);
+  else if (chunks <= kMaxWaveChunks) launch_cached<kOp, 4>(a, vec, s);
+  else if (per <= 2) return launch_split<kOp, 2>(a, vec, s);
+  else if (per <= 4) return launch_split<kOp, 4>(a, vec, s);
+  else if (vec && per <= 8) return launch_split<kOp, 8>(a, vec, s);
+  else if (vec && per <= kMaxSplit) return launch_split<kOp, 16>(a, vec, s);
+  else {
+    // Rows wider than the register budget (or unaligned rows wider than
+    // kMaxScalarSplit float4 per thread): one block per row, re-read passes.
     if (outer > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "too many rows");
     hipLaunchKernelGGL((row_block_kernel<kOp>), dim3(static_cast<unsigned>(outer)), dim3(256), 0, s, a);
     return check(hipGetLastError(), "row block kernel launch");
   }
-  if (chunks <= 1) launch_cached<kOp, 1>(a, vec, s);
-  else if (chunks <= 2) launch_cached<kOp, 2>(a, vec, s);
-  else if (chunks <= 4) launch_cached<kOp, 4>(a, vec, s);
-  else if (chunks <= 8) launch_cached<kOp, 8>(a, vec, s);
-  else if (chunks <= 16) launch_cached<kOp, 16>(a, vec, s);
-  else launch_cached<kOp, 32>(a, vec, s);
   return check(hipGetLastError(), "row kernel launch");
 }
 

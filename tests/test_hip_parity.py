@@ -171,8 +171,14 @@ def test_empty_and_scalar(cx):
 
 
 # ------------------------------------------------------------- row ops
+# Widths cover each row kernel: one wave per row (<= 1024), one block per row
+# with the row in registers (aligned up to 16384 floats, full and masked;
+# unaligned up to 4096), the re-reading block kernel, and strided rows.
 @pytest.mark.parametrize("shape,axis", [((16, 4096), 1), ((5, 300), 1), ((7, 8192), 1), ((3, 20000), -1),
-                                        ((3, 7), 0), ((2, 3, 70), 1), ((9, 1), 1), ((4, 1022), 1)])
+                                        ((3, 7), 0), ((2, 3, 70), 1), ((9, 1), 1), ((4, 1022), 1),
+                                        ((4, 1024), 1), ((6, 1501), 1), ((4, 2048), 1), ((3, 3001), 1),
+                                        ((5, 4100), 1), ((2, 12288), 1), ((3, 16384), 1), ((2, 16383), 1),
+                                        ((1000, 1028), 1)])
 def test_row_ops_random(cx, shape, axis):
     rng = np.random.default_rng(13)
     x = (rng.standard_normal(shape) * 3).astype(np.float32)
@@ -191,9 +197,11 @@ def test_row_ops_random(cx, shape, axis):
 
 
 @pytest.mark.parametrize("eps", [0.0, 1e-45, 1e-5, 1e30])
-def test_constant_rows(cx, eps):
-    x = np.full((4, 512), 2.5, np.float32)
+@pytest.mark.parametrize("width", [512, 4096, 3001])
+def test_constant_rows(cx, eps, width):
+    x = np.full((5, width), 2.5, np.float32)
     x[3] = -7.0
+    x[4, width - 1] = 2.5000002  # equal except the last element
     h = cx.tensor(x, device="hip")
     for op in ("rmsnorm", "layernorm"):
         assert_close(getattr(cx, op)(h, 1, eps).numpy(), getattr(oracle, op)(x, 1, eps), 1e-5, 1e-5, op)
