@@ -270,9 +270,17 @@ def main() -> int:
 
     if args.copy_calibration:
         src, dst = capi.DeviceBuffer(1 << 30), capi.DeviceBuffer(1 << 30)
-        for _ in range(3):
-            capi.check(capi.lib().tcx_hip_memcpy_d2d(dst.ptr, src.ptr, 1 << 30, capi.stream()), "copy")
-        log("copy calibration: 3 x 1 GiB device-to-device copies")
+        s = capi.stream()
+        ev = [capi.Event() for _ in range(4)]
+        ev[0].record(s)
+        for i in range(3):
+            capi.check(capi.lib().tcx_hip_memcpy_d2d(dst.ptr, src.ptr, 1 << 30, s), "copy")
+            ev[i + 1].record(s)
+        ev[-1].synchronize()
+        ms = [ev[i].elapsed_ms(ev[i + 1]) for i in range(3)]
+        # read + write of 1 GiB each: HIP's own copy kernel as a stream reference
+        log("copy calibration: 3 x 1 GiB device-to-device copies, "
+            + ", ".join(f"{2 * (1 << 30) / m / 1e6:.0f} GB/s" for m in ms) + " (read + write)")
         return 0
     if args.no_headline:
         for r in secondary_benches(args.steps, args.warmup, args.only):
