@@ -31,6 +31,7 @@ extern "C" {
 /* Values of tensorcx::DType (reference core/dtype.h:8-12). */
 #define TCX_FLOAT32 0
 #define TCX_INT32 1
+#define TCX_BOOL 2 /* 1-byte bool (fill and attention masks) */
 
 typedef void* tcx_stream_t; /* a hipStream_t */
 
@@ -221,8 +222,61 @@ int tcx_hip_binary(int op, int dtype, const void* lhs, const void* rhs, void* ou
                    const int64_t* out_shape, const int64_t* lhs_strides,
                    const int64_t* rhs_strides, tcx_stream_t stream);
 
-/* kFill (cpu_backend.cpp fill): float32 or int32 value into n elements. */
+/* kFill (cpu_backend.cpp fill): float32, int32 or bool (value != 0) into n elements. */
 int tcx_hip_fill(int dtype, void* out, int64_t n, double value, tcx_stream_t stream);
+
+/* ---- math extension (replaces the CUDA math launches of reference
+ * backends/cuda/kernels/math.cu; semantics of backends/cpu/cpu_math.cpp) ---- */
+#define TCX_MATH_LOG 0
+#define TCX_MATH_SQRT 1
+#define TCX_MATH_ABS 2
+/* kLog / kSqrt (float32) and kAbs (float32 sign clear; int32 negation in uint32,
+ * so INT32_MIN stays) over n contiguous elements (cpu_math.cpp:40-44). */
+int tcx_hip_math_unary(int op, int dtype, const void* x, void* out, int64_t n, tcx_stream_t stream);
+
+/* kClip over a three-way broadcast plan (math.cpp:32-38): out_shape of `rank`
+ * axes and the broadcast strides of x, lo and hi (cpu_math.cpp:45-50). */
+int tcx_hip_clip(int dtype, const void* x, const void* lo, const void* hi, void* out, int32_t rank,
+                 const int64_t* out_shape, const int64_t* x_strides, const int64_t* lo_strides,
+                 const int64_t* hi_strides, tcx_stream_t stream);
+
+/* kTopK along the middle extent of (outer, reduce, inner) (math.cpp:56-66,
+ * cpu_math.cpp:57-67): values (x's dtype) and int32 indices of shape
+ * (outer, k, inner). NaN first when largest (last otherwise), ties by lower
+ * index; sorted == 0 lists the chosen k in index order. */
+int tcx_hip_topk(int dtype, const void* x, void* values, int32_t* indices, int64_t outer, int64_t reduce,
+                 int64_t inner, int64_t k, int largest, int sorted, tcx_stream_t stream);
+
+/* ---- inference primitives (replace reference backends/cuda/kernels/
+ * inference.cu; semantics of backends/cpu/cpu_inference.cpp) ---- */
+
+/* kEmbedding (cpu_inference.cpp:12-21): out[i, :] = weight[indices[i], :] for
+ * `count` indices into a (vocabulary, width) table, copied bit for bit. Every
+ * index is checked on the device, also when width is 0; an index outside
+ * [0, vocabulary) returns TCX_INVALID_ARGUMENT (out is then unspecified).
+ * `flag` is one caller-provided device int32 of scratch. Synchronizes
+ * `stream` to read the check back. */
+int tcx_hip_embedding_f32(const int32_t* indices, const float* weight, float* out, int64_t count,
+                          int64_t vocabulary, int64_t width, int32_t* flag, tcx_stream_t stream);
+
+#define TCX_MASK_NONE 0
+#define TCX_MASK_BOOL 1     /* 1-byte bool, false masks the score out */
+#define TCX_MASK_ADDITIVE 2 /* float32 added to the scaled score */
+typedef struct {
+  int64_t shape[TCX_HIP_MAX_RANK];         /* attention shape (..., queries, keys) */
+  int64_t score_strides[TCX_HIP_MAX_RANK]; /* broadcast strides of the scores */
+  int64_t mask_strides[TCX_HIP_MAX_RANK];  /* broadcast strides of the mask */
+  int32_t rank;                            /* 2..TCX_HIP_MAX_RANK */
+  int32_t mask_kind;                       /* TCX_MASK_* */
+  int32_t causal;                          /* key > query % queries masked out */
+  float scale;                             /* checked float32 scale */
+} tcx_hip_attention_softmax_desc_t;
+/* kAttentionSoftmax (make_attention_softmax_plan, inference.cpp:59-84;
+ * cpu_inference.cpp:22-47): per row, scores * scale + mask bias with causal /
+ * bool / -inf masking, NaN-first maximum, a row with maximum -inf is zeros,
+ * else exp(s - max) / sum. `out` is contiguous in `shape`. */
+int tcx_hip_attention_softmax_f32(const float* scores, const void* mask, float* out,
+                                  const tcx_hip_attention_softmax_desc_t* desc, tcx_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -29,8 +29,9 @@ _LIB = None
 OPKIND = {
     "fill": 0, "add": 1, "multiply": 2, "matmul": 3, "sum": 4, "max": 5, "mean": 6,
     "exp": 7, "gelu": 8, "silu": 9, "softmax": 10, "rmsnorm": 11, "layernorm": 12,
-    "subtract": 13, "divide": 14, "min": 41, "argmax": 42, "linear": 45,
-    "affine_rmsnorm": 46, "affine_layernorm": 47,
+    "subtract": 13, "divide": 14, "transpose": 21, "log": 38, "sqrt": 39, "abs": 40, "min": 41,
+    "argmax": 42, "clip": 43, "topk": 44, "linear": 45, "affine_rmsnorm": 46,
+    "affine_layernorm": 47, "embedding": 48, "attention": 49, "attention_softmax": 50,
 }
 DTYPE = {"float32": 0, "int32": 1, "bool": 2}
 
@@ -60,8 +61,13 @@ def _p(array: np.ndarray):
     return array.ctypes.data_as(ctypes.c_void_p)
 
 
+def _c(x) -> np.ndarray:
+    """C-contiguous view or copy that keeps rank 0 (np.ascontiguousarray makes it rank 1)."""
+    return np.asarray(x, order="C")
+
+
 def _dims(values) -> np.ndarray:
-    return np.ascontiguousarray(np.asarray(values, dtype=np.int64).reshape(-1))
+    return np.asarray(np.asarray(values, dtype=np.int64).reshape(-1), order="C")
 
 
 # ---------------------------------------------------------------- shape plans
@@ -209,7 +215,7 @@ def checked_epsilon(eps: float) -> np.float32:
 
 # ------------------------------------------------------------------ operations
 def _f32(x) -> np.ndarray:
-    x = np.ascontiguousarray(x)
+    x = _c(x)
     if x.dtype != np.float32:
         raise ValueError("expected float32 input")
     return x
@@ -232,7 +238,7 @@ def matmul(a, b, threads: int | None = None) -> np.ndarray:
 
 
 def _reduce_single(op: int, x: np.ndarray, axis: int, threads) -> np.ndarray:
-    x = np.ascontiguousarray(x)
+    x = _c(x)
     out_shape, outer, reduce, inner = reduction_dims(x.shape, axis)
     if op == 1 and reduce == 0:
         raise ValueError("max reduction requires a non-empty axis")
@@ -254,7 +260,7 @@ def _reduce_single(op: int, x: np.ndarray, axis: int, threads) -> np.ndarray:
 
 
 def _reduce_axes(op: int, x: np.ndarray, axes, threads) -> np.ndarray:
-    x = np.ascontiguousarray(x)
+    x = _c(x)
     if op == 2 and x.dtype != np.float32:
         raise ValueError("mean only supports float32 tensors")
     out_shape, meta, size = make_reduction_plan(x.shape, tuple(axes))
@@ -301,7 +307,7 @@ def mean(x, axis=None, threads=None):
 
 def _argext(code: int, x, axis, threads) -> np.ndarray:
     """math.cpp:39-56 plan + cpu_math.cpp:48-54."""
-    x = np.ascontiguousarray(x)
+    x = _c(x)
     if x.dtype not in (np.float32, np.int32):
         raise ValueError("math operations require float32 or int32 tensors")
     if axis is None:
@@ -385,7 +391,7 @@ _BINARY = {"add": 0, "subtract": 1, "multiply": 2, "divide": 3}
 
 def binary(name: str, lhs, rhs, threads=None) -> np.ndarray:
     """cpu_backend.cpp:1014-1097."""
-    lhs, rhs = np.ascontiguousarray(lhs), np.ascontiguousarray(rhs)
+    lhs, rhs = _c(lhs), _c(rhs)
     if lhs.dtype != rhs.dtype:
         raise ValueError("dtype mismatch for binary operation")
     if name == "divide" and lhs.dtype != np.float32:
@@ -403,7 +409,7 @@ def binary(name: str, lhs, rhs, threads=None) -> np.ndarray:
 def linear(x, weight, bias=None, threads=None) -> np.ndarray:
     """inference.cpp:89-102: transpose(W) copy, matmul, then broadcast add."""
     weight = _f32(weight)
-    out = matmul(x, np.ascontiguousarray(weight.T), threads)
+    out = matmul(x, _c(weight.T), threads)
     if bias is not None:
         out = binary("add", out, bias, threads)
     return out
@@ -427,3 +433,170 @@ def mlp_forward(x, w1, b1, w2, b2, threads=None) -> np.ndarray:
     """The MLP chain linear -> silu -> linear -> softmax(axis=-1)."""
     h = silu(linear(x, w1, b1, threads), threads)
     return softmax(linear(h, w2, b2, threads), -1, threads)
+
+
+# ------------------------------------------------------- ops next to the path
+def _math_input(x) -> np.ndarray:
+    x = _c(x)
+    if x.dtype not in (np.float32, np.int32):
+        raise ValueError("math operations require float32 or int32 tensors")
+    return x
+
+
+def _math_unary(code: int, x, threads) -> np.ndarray:
+    """cpu_math.cpp:40-44 under math.cpp:29-31 (log/sqrt float32 only)."""
+    x = _math_input(x)
+    if code < 2 and x.dtype != np.float32:
+        raise ValueError("log/sqrt only support float32 tensors")
+    out = np.empty_like(x)
+    if x.size:
+        lib().oracle_math_unary(code, DTYPE[str(x.dtype)], _p(x), _p(out), ctypes.c_int64(x.size),
+                                ctypes.c_int(threads or default_threads()))
+    return out
+
+
+def log(x, threads=None):
+    return _math_unary(0, x, threads)
+
+
+def sqrt(x, threads=None):
+    return _math_unary(1, x, threads)
+
+
+def abs(x, threads=None):  # noqa: A001
+    return _math_unary(2, x, threads)
+
+
+def clip(x, lower, upper, threads=None) -> np.ndarray:
+    """cpu_math.cpp:45-50 over the three-way broadcast plan of math.cpp:32-38."""
+    arrays = [_math_input(a) for a in (x, lower, upper)]
+    if builtins.any(a.dtype != arrays[0].dtype for a in arrays):
+        raise ValueError("math input dtypes must match")
+    shape = tuple(arrays[0].shape)
+    for a in arrays:
+        shape = tuple(make_broadcast_plan(shape, a.shape)[0])
+    strides = [d for a in arrays for d in make_broadcast_plan(a.shape, shape)[1]]
+    out = np.empty(shape, dtype=arrays[0].dtype)
+    if out.size:
+        lib().oracle_clip(DTYPE[str(out.dtype)], _p(arrays[0]), _p(arrays[1]), _p(arrays[2]), _p(out),
+                          _p(_dims(shape)), _p(_dims(strides)), len(shape), ctypes.c_int64(out.size),
+                          ctypes.c_int(threads or default_threads()))
+    return out
+
+
+def topk(x, k: int, axis: int = -1, largest: bool = True, sorted: bool = True,  # noqa: A002
+         threads=None):
+    """cpu_math.cpp:57-67 under the plan of math.cpp:56-66: (values, int32 indices)."""
+    x = _math_input(x)
+    if x.ndim == 0:
+        raise ValueError("topk requires rank >= 1")
+    a = axis + x.ndim if axis < 0 else axis
+    if a < 0 or a >= x.ndim:
+        raise ValueError("topk axis out of range")
+    reduce = x.shape[a]
+    if k < 0 or k > reduce:
+        raise ValueError("topk k must be between zero and the axis size")
+    shape = list(x.shape)
+    shape[a] = k
+    values = np.empty(shape, dtype=x.dtype)
+    indices = np.empty(shape, dtype=np.int32)
+    if values.size:
+        outer = int(np.prod(x.shape[:a], dtype=np.int64))
+        inner = int(np.prod(x.shape[a + 1:], dtype=np.int64))
+        lib().oracle_topk(DTYPE[str(x.dtype)], int(largest), int(sorted), _p(x), _p(values), _p(indices),
+                          ctypes.c_int64(outer), ctypes.c_int64(reduce), ctypes.c_int64(inner),
+                          ctypes.c_int64(k), ctypes.c_int(threads or default_threads()))
+    return values, indices
+
+
+def embedding(indices, weight) -> np.ndarray:
+    """cpu_inference.cpp:12-21 under make_embedding_plan (inference.cpp:47-57)."""
+    indices, weight = _c(indices), _c(weight)
+    if indices.dtype != np.int32:
+        raise ValueError("embedding indices must be int32")
+    if weight.dtype != np.float32:
+        raise ValueError("inference values require float32 tensors")
+    if weight.ndim != 2:
+        raise ValueError("embedding weight must have rank 2")
+    if indices.size and (indices.min() < 0 or indices.max() >= weight.shape[0]):
+        raise ValueError("embedding index out of range")
+    out = np.empty(indices.shape + (weight.shape[1],), dtype=np.float32)
+    if out.size:
+        rows = out.reshape(-1, weight.shape[1])
+        for i, index in enumerate(indices.reshape(-1)):  # row copies, bits preserved
+            rows[i] = weight[index]
+    return out
+
+
+def checked_scale(scale: float) -> np.float32:
+    """inference.cpp:15-20."""
+    with np.errstate(over="ignore"):
+        narrowed = np.float32(scale)
+    if not np.isfinite(scale) or not np.isfinite(narrowed) or (scale != 0 and narrowed == 0):
+        raise ValueError("attention scale must be finite and representable as float32")
+    return narrowed
+
+
+def make_attention_softmax_plan(scores_shape, mask, shape, scale):
+    """inference.cpp:59-84: (metadata strides, rows, columns, float scale, mask kind)."""
+    if len(scores_shape) < 2 or len(shape) < 2:
+        raise ValueError("attention scores must have rank >= 2")
+    shape = tuple(shape)
+    if tuple(make_broadcast_plan(scores_shape, shape)[0]) != shape:
+        raise ValueError("attention scores cannot broadcast to target")
+    kind = 0
+    if mask is not None:
+        if mask.dtype not in (np.bool_, np.float32):
+            raise ValueError("attention mask must be bool or float32")
+        if tuple(make_broadcast_plan(mask.shape, shape)[0]) != shape:
+            raise ValueError("attention mask cannot broadcast to scores")
+        kind = 1 if mask.dtype == np.bool_ else 2
+    count = int(np.prod(shape, dtype=np.int64))
+    strides = list(make_broadcast_plan(scores_shape, shape)[1])
+    strides += list(make_broadcast_plan(mask.shape, shape)[1]) if mask is not None else [0] * len(shape)
+    columns = shape[-1]
+    return strides, (count // columns if columns else 0), columns, checked_scale(scale), kind
+
+
+def attention_softmax(scores, mask, shape, scale: float, causal: bool, threads=None) -> np.ndarray:
+    """cpu_inference.cpp:22-47."""
+    scores = _f32(scores)
+    mask = None if mask is None else _c(mask)
+    strides, rows, columns, fscale, kind = make_attention_softmax_plan(scores.shape, mask, shape, scale)
+    out = np.empty(tuple(shape), dtype=np.float32)
+    if rows:
+        m = mask if mask is not None else np.zeros(1, np.float32)
+        lib().oracle_attention_softmax(_p(scores), _p(m), kind, _p(out), _p(_dims(shape)),
+                                       _p(_dims(strides)), len(shape), ctypes.c_int64(rows),
+                                       ctypes.c_int64(columns), ctypes.c_float(fscale), int(causal),
+                                       ctypes.c_int(threads or default_threads()))
+    return out
+
+
+def attention(q, k, v, mask=None, causal: bool = False, scale: float | None = None, threads=None):
+    """inference.cpp:123-161: Q @ transpose(K), attention softmax, then @ V."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    for t in (q, k, v):
+        if t.ndim < 2:
+            raise ValueError("attention tensors require rank >= 2")
+    features, rows, columns = q.shape[-1], q.shape[-2], k.shape[-2]
+    if features <= 0 or features != k.shape[-1] or columns != v.shape[-2]:
+        raise ValueError("attention query/key features and key/value sequence sizes must match")
+    batch: tuple = ()
+    for t in (q, k, v):
+        rank = builtins.max(len(batch), t.ndim - 2)
+        left = (1,) * (rank - len(batch)) + tuple(batch)
+        right = (1,) * (rank - (t.ndim - 2)) + tuple(t.shape[:-2])
+        merged = []
+        for a, b in zip(left, right):
+            if a != b and a != 1 and b != 1:
+                raise ValueError("attention batch dimensions cannot broadcast")
+            merged.append(b if a == 1 else a)
+        batch = tuple(merged)
+    scores_shape = batch + (rows, columns)
+    s = checked_scale(1.0 / np.sqrt(float(features)) if scale is None else scale)
+    mask = None if mask is None else _c(mask)
+    make_attention_softmax_plan(scores_shape, mask, scores_shape, float(s))
+    product = matmul(q, _c(np.swapaxes(k, -1, -2)), threads)
+    probabilities = attention_softmax(product, mask, scores_shape, float(s), causal, threads)
+    return matmul(probabilities, v, threads)

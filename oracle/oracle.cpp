@@ -2,7 +2,8 @@
 //
 // Restatement of the tensor.cx CPU reference arithmetic for the hip hot path
 // (matmul, single- and multi-axis sum/max/mean, min/argmax, softmax, RMSNorm,
-// LayerNorm, elementwise exp/gelu/silu and broadcast binary arithmetic). Only
+// LayerNorm, elementwise exp/gelu/silu and broadcast binary arithmetic) and for
+// the ops next to it (log/sqrt/abs, clip, topk, attention softmax). Only
 // tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, as the
 // checker. Each function keeps the reference loop order and rounding exactly:
 // built with g++ -O2 -ffp-contract=off (no FMA contraction, no reassociation), it
@@ -391,6 +392,137 @@ void oracle_binary(int op, int dtype, const void* lhs, const void* rhs, void* ou
         }
         static_cast<std::int32_t*>(out)[i] = static_cast<std::int32_t>(r);
       }
+    }
+  });
+}
+
+// cpu_math.cpp:40-44: log and sqrt through the float overloads of std::log and
+// std::sqrt; abs clears the sign bit (float32) or negates in uint32 (int32, so
+// INT32_MIN stays INT32_MIN). code: 0 log, 1 sqrt, 2 abs.
+void oracle_math_unary(int code, int dtype, const std::uint32_t* x, std::uint32_t* out, Dim n,
+                       int threads) {
+  const bool fp = dtype == 0;
+  parallel_for(n, threads, [&](Dim begin, Dim end) {
+    for (Dim i = begin; i < end; ++i) {
+      std::uint32_t a = x[i];
+      if (code == 2) {
+        a = fp ? (a & 0x7fffffffu) : ((a & 0x80000000u) ? 0u - a : a);
+      } else {
+        float f;
+        std::memcpy(&f, &a, 4);
+        f = code == 0 ? std::log(f) : std::sqrt(f);
+        std::memcpy(&a, &f, 4);
+      }
+      out[i] = a;
+    }
+  });
+}
+
+// cpu_math.cpp:45-50: clip(x, lo, hi) over a three-way broadcast. A NaN x
+// stays; otherwise a NaN bound, or a bound the value does not exceed (under
+// the +0 == -0 total order), replaces it; lo first, then hi.
+// strides holds rank strides for x, then lo, then hi.
+void oracle_clip(int dtype, const std::uint32_t* x, const std::uint32_t* lo, const std::uint32_t* hi,
+                 std::uint32_t* out, const Dim* shape, const Dim* strides, int rank, Dim count,
+                 int threads) {
+  const bool fp = dtype == 0;
+  parallel_for(count, threads, [&](Dim begin, Dim end) {
+    for (Dim i = begin; i < end; ++i) {
+      Dim flat = i, ox = 0, ol = 0, oh = 0;
+      for (int a = rank; a-- > 0;) {
+        const Dim c = flat % shape[a];
+        flat /= shape[a];
+        ox += c * strides[a];
+        ol += c * strides[rank + a];
+        oh += c * strides[2 * rank + a];
+      }
+      std::uint32_t v = x[ox];
+      const std::uint32_t l = lo[ol], h = hi[oh];
+      if (!word_nan(v, fp)) v = (word_nan(l, fp) || !word_less(l, v, fp)) ? l : v;
+      if (!word_nan(v, fp)) v = (word_nan(h, fp) || !word_less(v, h, fp)) ? h : v;
+      out[i] = v;
+    }
+  });
+}
+
+// cpu_math.cpp:57-67: top-k along an axis (outer, reduce, inner). Order: NaN
+// first when largest (last otherwise), then by value under the +0 == -0 total
+// order, then by lower index. sorted == 0 lists the chosen k by index.
+void oracle_topk(int dtype, int largest, int sorted, const std::uint32_t* x, std::uint32_t* values,
+                 std::int32_t* indices, Dim outer, Dim reduce, Dim inner, Dim k, int threads) {
+  const bool fp = dtype == 0;
+  parallel_for(outer * inner, threads, [&](Dim begin, Dim end) {
+    std::vector<std::int32_t> order(static_cast<std::size_t>(reduce));
+    for (Dim g = begin; g < end; ++g) {
+      const Dim base = (g / inner) * reduce * inner + g % inner;
+      for (Dim j = 0; j < reduce; ++j) order[static_cast<std::size_t>(j)] = static_cast<std::int32_t>(j);
+      const auto before = [&](std::int32_t ia, std::int32_t ib) {
+        const std::uint32_t a = x[base + ia * inner], b = x[base + ib * inner];
+        const bool an = word_nan(a, fp), bn = word_nan(b, fp);
+        if (an != bn) return largest ? an : bn;
+        if (!an && (word_less(a, b, fp) || word_less(b, a, fp)))
+          return largest ? word_less(b, a, fp) : word_less(a, b, fp);
+        return ia < ib;
+      };
+      std::partial_sort(order.begin(), order.begin() + k, order.end(), before);
+      if (!sorted) std::sort(order.begin(), order.begin() + k);
+      for (Dim j = 0; j < k; ++j) {
+        const Dim dest = (g / inner) * k * inner + j * inner + g % inner;
+        values[dest] = x[base + order[static_cast<std::size_t>(j)] * inner];
+        indices[dest] = order[static_cast<std::size_t>(j)];
+      }
+    }
+  });
+}
+
+// cpu_inference.cpp:22-47: attention softmax over the last axis of `shape`.
+// The score of (row, col) is -inf when causal and col > row % rows_per_matrix,
+// or when a bool mask (mask_kind 1) is false; an additive mask (mask_kind 2)
+// of -inf gives -inf; otherwise scores * scale + bias, rounded separately.
+// NaN-first maximum; a row whose maximum is -inf is all zeros; else
+// exp(s - max) / sequential sum. strides: rank strides for scores, then mask.
+void oracle_attention_softmax(const float* scores, const void* mask, int mask_kind, float* out,
+                              const Dim* shape, const Dim* strides, int rank, Dim rows, Dim columns,
+                              float scale, int causal, int threads) {
+  const Dim per_matrix = shape[rank - 2];
+  parallel_for(rows, threads, [&](Dim begin, Dim end) {
+    for (Dim row = begin; row < end; ++row) {
+      const Dim query = row % per_matrix;
+      const auto offset = [&](Dim i, int arg) {
+        Dim result = 0;
+        for (int a = rank; a-- > 0;) {
+          result += i % shape[a] * strides[arg * rank + a];
+          i /= shape[a];
+        }
+        return result;
+      };
+      const auto score = [&](Dim col) -> float {
+        const Dim i = row * columns + col;
+        const float neg_inf = -std::numeric_limits<float>::infinity();
+        if (causal && col > query) return neg_inf;
+        if (mask_kind == 1 && !static_cast<const std::uint8_t*>(mask)[offset(i, 1)]) return neg_inf;
+        const float bias = mask_kind == 2 ? static_cast<const float*>(mask)[offset(i, 1)] : 0.0F;
+        if (bias == neg_inf) return bias;
+        const float product = scores[offset(i, 0)] * scale;
+        return product + bias;
+      };
+      float maximum = -std::numeric_limits<float>::infinity();
+      for (Dim col = 0; col < columns; ++col) {
+        const float v = score(col);
+        if (std::isnan(v)) {
+          maximum = v;
+          break;
+        }
+        maximum = maximum < v ? v : maximum;
+      }
+      float* o = out + row * columns;
+      if (maximum == -std::numeric_limits<float>::infinity()) {
+        for (Dim col = 0; col < columns; ++col) o[col] = 0.0F;
+        continue;
+      }
+      float total = 0.0F;
+      for (Dim col = 0; col < columns; ++col) total += std::exp(score(col) - maximum);
+      for (Dim col = 0; col < columns; ++col) o[col] = std::exp(score(col) - maximum) / total;
     }
   });
 }

@@ -19,7 +19,7 @@ from . import DTYPE, OPKIND
 
 PATH = pathlib.Path(__file__).resolve().parent / "_ref" / "libtcxref.so"
 _LIB = None
-_NP = {0: np.float32, 1: np.int32, 2: np.uint8}
+_NP = {0: np.float32, 1: np.int32, 2: np.bool_}
 
 
 class ReferenceError(Exception):
@@ -41,9 +41,15 @@ def lib() -> ctypes.CDLL:
 
 
 def execute(kind: str, inputs, *, axis: int = 0, eps: float = 1e-5, axes=None,
-            has_weight: bool = False, has_bias: bool = False, n_outputs: int = 1):
+            has_weight: bool = False, has_bias: bool = False, n_outputs: int = 1,
+            causal: bool = False, scale: float | None = None, attention_shape=(),
+            k: int = 0, largest: bool = True, sorted: bool = True):  # noqa: A002
     """Runs one primitive through the reference CpuBackend::execute."""
-    arrays = [np.ascontiguousarray(a) for a in inputs]
+    arrays = [np.asarray(a, order="C") for a in inputs]  # keeps rank 0
+    att = (ctypes.c_int64 * max(1, len(attention_shape)))(*attention_shape)
+    lib().tcxref_set_attributes(int(causal), int(scale is not None), ctypes.c_double(scale or 0.0),
+                                len(attention_shape), att, ctypes.c_int64(k), int(largest), int(sorted),
+                                ctypes.c_double(0.0))
     dtypes = (ctypes.c_int * max(1, len(arrays)))(*[DTYPE[str(a.dtype)] for a in arrays])
     ranks = (ctypes.c_int * max(1, len(arrays)))(*[a.ndim for a in arrays])
     dims = [d for a in arrays for d in a.shape]

@@ -28,6 +28,22 @@ struct Result {
 
 thread_local Result last;
 
+// Attributes beyond the common ones, set by tcxref_set_attributes for the next
+// tcxref_execute call on this thread (core/operation.h OpDesc fields).
+struct Attributes {
+  bool set{false};
+  bool causal{false};
+  bool has_scale{false};
+  double scale{1.0};
+  tensorcx::Shape attention_shape{};
+  std::int64_t k{0};
+  bool largest{true};
+  bool sorted{true};
+  double scalar{0.0};
+};
+
+thread_local Attributes pending;
+
 tensorcx::cpu::CpuTensor make_input(int dtype, int rank, const std::int64_t* shape,
                                     const void* data) {
   tensorcx::Shape s(shape, shape + rank);
@@ -66,6 +82,16 @@ int tcxref_execute(int kind, std::int64_t axis, double epsilon, int has_axes,
     if (has_axes) op.reduction_axes = tensorcx::Shape(axes, axes + n_axes);
     op.has_weight = has_weight != 0;
     op.has_bias = has_bias != 0;
+    if (pending.set) {
+      op.causal = pending.causal;
+      if (pending.has_scale) op.attention_scale = pending.scale;
+      op.attention_shape = pending.attention_shape;
+      op.k = pending.k;
+      op.largest = pending.largest;
+      op.sorted = pending.sorted;
+      op.scalar_value = pending.scalar;
+      pending = Attributes{};
+    }
     std::vector<tensorcx::Tensor> outputs(static_cast<std::size_t>(n_outputs));
     tensorcx::BackendExecution e{tensorcx::BackendOpClass::kPrimitive, op, core_inputs, outputs,
                                  std::nullopt, std::nullopt, {}};
@@ -82,6 +108,23 @@ int tcxref_execute(int kind, std::int64_t axis, double epsilon, int has_axes,
     last.message = error.what();
   }
   return last.status;
+}
+
+// Sets causal / attention_scale / attention_shape / k / largest / sorted /
+// scalar_value for the next tcxref_execute on this thread.
+void tcxref_set_attributes(int causal, int has_scale, double scale, int attention_rank,
+                           const std::int64_t* attention_shape, std::int64_t k, int largest, int sorted,
+                           double scalar) {
+  pending = Attributes{};
+  pending.set = true;
+  pending.causal = causal != 0;
+  pending.has_scale = has_scale != 0;
+  pending.scale = scale;
+  pending.attention_shape = tensorcx::Shape(attention_shape, attention_shape + attention_rank);
+  pending.k = k;
+  pending.largest = largest != 0;
+  pending.sorted = sorted != 0;
+  pending.scalar = scalar;
 }
 
 const char* tcxref_message() { return last.message.c_str(); }

@@ -53,6 +53,19 @@ HipTensor run(OpDesc op, std::vector<Tensor> inputs) {
   return HipTensor{std::move(outputs[0])};
 }
 
+std::pair<HipTensor, HipTensor> run2(OpDesc op, std::vector<Tensor> inputs) {
+  std::array<Tensor, 2> outputs{};
+  Status status;
+  {
+    py::gil_scoped_release release;
+    BackendExecution e{BackendOpClass::kPrimitive, std::move(op), inputs, outputs, std::nullopt, std::nullopt, {}};
+    hip::HipBackend backend;
+    status = backend.execute(e);
+  }
+  if (!status.ok()) throw_status(status);
+  return {HipTensor{std::move(outputs[0])}, HipTensor{std::move(outputs[1])}};
+}
+
 HipTensor unary(OpKind kind, const HipTensor& x) { return run(OpDesc{kind}, {x.tensor}); }
 
 HipTensor axis_op(OpKind kind, const HipTensor& x, std::int64_t axis, double eps = 1e-5) {
@@ -98,7 +111,7 @@ py::array to_numpy(const HipTensor& t) {
   else if (t.tensor.dtype == DType::kInt32)
     out = py::array_t<std::int32_t>(shape);
   else
-    throw py::value_error("unsupported dtype");
+    out = py::array_t<bool>(shape);
   const std::size_t bytes = static_cast<std::size_t>(out.nbytes());
   Status status;
   {
@@ -119,8 +132,11 @@ HipTensor from_numpy(py::array array) {
   } else if (py::isinstance<py::array_t<std::int32_t>>(array)) {
     dtype = DType::kInt32;
     contiguous = py::array_t<std::int32_t, py::array::c_style | py::array::forcecast>(array);
+  } else if (py::isinstance<py::array_t<bool>>(array)) {
+    dtype = DType::kBool;
+    contiguous = py::array_t<bool, py::array::c_style | py::array::forcecast>(array);
   } else {
-    throw py::value_error("hip tensors are created from float32 or int32 arrays");
+    throw py::value_error("hip tensors are created from float32, int32 or bool arrays");
   }
   Shape shape;
   for (py::ssize_t i = 0; i < contiguous.ndim(); ++i) shape.push_back(contiguous.shape(i));
@@ -272,6 +288,44 @@ PYBIND11_MODULE(_core, m) {
     const OpKind k = kind;
     m.def(name, [k](const HipTensor& a, const HipTensor& b) { return run(OpDesc{k}, {a.tensor, b.tensor}); });
   }
+
+  m.def("log", [](const HipTensor& x) { return unary(OpKind::kLog, x); });
+  m.def("sqrt", [](const HipTensor& x) { return unary(OpKind::kSqrt, x); });
+  m.def("abs", [](const HipTensor& x) { return unary(OpKind::kAbs, x); });
+  m.def("_clip", [](const HipTensor& x, const HipTensor& lo, const HipTensor& hi) {
+    return run(OpDesc{OpKind::kClip}, {x.tensor, lo.tensor, hi.tensor});
+  });
+  m.def("_topk", [](const HipTensor& x, std::int64_t k, std::int64_t axis, bool largest, bool sorted) {
+    OpDesc op{OpKind::kTopK};
+    op.k = k;
+    op.axis = axis;
+    op.largest = largest;
+    op.sorted = sorted;
+    return run2(op, {x.tensor});
+  });
+  m.def("embedding", [](const HipTensor& ids, const HipTensor& w) {
+    return run(OpDesc{OpKind::kEmbedding}, {ids.tensor, w.tensor});
+  });
+  m.def("_attention", [](const HipTensor& q, const HipTensor& k, const HipTensor& v,
+                         std::optional<const HipTensor*> mask, bool causal, std::optional<double> scale) {
+    OpDesc op{OpKind::kAttention};
+    op.causal = causal;
+    op.attention_scale = scale;
+    std::vector<Tensor> in{q.tensor, k.tensor, v.tensor};
+    if (mask && *mask) in.push_back((*mask)->tensor);
+    return run(op, std::move(in));
+  }, py::arg("q"), py::arg("k"), py::arg("v"), py::arg("mask") = py::none(), py::arg("causal") = false,
+     py::arg("scale") = py::none());
+  m.def("_attention_softmax", [](const HipTensor& scores, std::optional<const HipTensor*> mask,
+                                 std::vector<std::int64_t> shape, bool causal, std::optional<double> scale) {
+    OpDesc op{OpKind::kAttentionSoftmax};
+    op.attention_shape = to_shape(shape);
+    op.causal = causal;
+    op.attention_scale = scale;
+    std::vector<Tensor> in{scores.tensor};
+    if (mask && *mask) in.push_back((*mask)->tensor);
+    return run(op, std::move(in));
+  }, py::arg("scores"), py::arg("mask"), py::arg("shape"), py::arg("causal") = false, py::arg("scale") = py::none());
 
   py::class_<PoolHandle>(m, "MemoryPool")
       .def(py::init<std::size_t, std::size_t>(), py::arg("max_cached_bytes"), py::arg("max_cached_blocks") = 64)

@@ -305,9 +305,23 @@ Tensor matmul(const Tensor& lhs, const Tensor& rhs, tcx_stream_t s) {
     throw std::invalid_argument("matmul only supports float32 tensors");
   const float* a = f32(lhs);
   const float* b = f32(rhs);
-  const MatmulPlan plan = make_matmul_plan(lhs.shape, rhs.shape);
+  MatmulPlan plan = make_matmul_plan(lhs.shape, rhs.shape);
+  // Size-1 batch axes contribute nothing to any offset: drop them.
+  {
+    MatmulPlan kept = plan;
+    kept.batch_shape.clear();
+    kept.lhs_batch_strides.clear();
+    kept.rhs_batch_strides.clear();
+    for (std::size_t i = 0; i < plan.batch_shape.size(); ++i) {
+      if (plan.batch_shape[i] == 1) continue;
+      kept.batch_shape.push_back(plan.batch_shape[i]);
+      kept.lhs_batch_strides.push_back(plan.lhs_batch_strides[i]);
+      kept.rhs_batch_strides.push_back(plan.rhs_batch_strides[i]);
+    }
+    plan = std::move(kept);
+  }
   if (plan.batch_shape.size() > TCX_HIP_MAX_BATCH_RANK)
-    throw std::invalid_argument("HIP matmul supports at most 8 batch dimensions");
+    throw std::invalid_argument("HIP matmul supports at most 8 batch dimensions of size > 1");
   Tensor out = make_tensor(DType::kFloat32, plan.output_shape);
   if (numel(plan.output_shape) == 0) return out;
   tcx_hip_gemm_desc_t d{};
@@ -432,9 +446,297 @@ Tensor binary(const OpDesc& op, const Tensor& lhs, const Tensor& rhs, tcx_stream
 Tensor fill(const Tensor& descriptor, double value, tcx_stream_t s) {
   if (descriptor.dtype == DType::kInt32 && !is_int32_representable(value))
     throw std::invalid_argument("fill value must be an integer in int32 range");
+  const int dtype = descriptor.dtype == DType::kBool ? TCX_BOOL : tcx_dtype(descriptor.dtype);
   Tensor out = make_tensor(descriptor.dtype, descriptor.shape);
-  ok_or_throw(tcx_hip_fill(tcx_dtype(descriptor.dtype), out_ptr(out), numel(descriptor.shape), value, s), "HIP fill");
+  ok_or_throw(tcx_hip_fill(dtype, out_ptr(out), numel(descriptor.shape), value, s), "HIP fill");
   return out;
+}
+
+// ------------------------------------------------------------ broadcast metadata
+// A broadcast over `shape` with per-operand strides, compressed for the
+// kernels' TCX_HIP_MAX_RANK metadata: size-1 axes are dropped and neighbouring
+// axes that every operand walks contiguously are merged. The last `keep` axes
+// stay as they are (the attention softmax reads its last two).
+struct Strided {
+  Shape shape;
+  std::vector<Shape> strides;
+};
+
+Strided compress(const Shape& shape, const std::vector<Shape>& strides, std::size_t keep = 0) {
+  Strided out;
+  out.strides.resize(strides.size());
+  const std::size_t rank = shape.size();
+  std::size_t merged_ok = 0;  // leading entries of out that may still absorb a neighbour
+  for (std::size_t a = 0; a < rank; ++a) {
+    const bool tail = a + keep >= rank;
+    if (!tail && shape[a] == 1) continue;
+    bool merge = !tail && merged_ok == out.shape.size() && !out.shape.empty();
+    for (std::size_t o = 0; merge && o < strides.size(); ++o)
+      merge = out.strides[o].back() == strides[o][a] * shape[a];
+    if (merge) {
+      out.shape.back() *= shape[a];
+      for (std::size_t o = 0; o < strides.size(); ++o) out.strides[o].back() = strides[o][a];
+      continue;
+    }
+    out.shape.push_back(shape[a]);
+    for (std::size_t o = 0; o < strides.size(); ++o) out.strides[o].push_back(strides[o][a]);
+    if (!tail) merged_ok = out.shape.size();
+  }
+  if (out.shape.size() > TCX_HIP_MAX_RANK) throw std::invalid_argument("HIP broadcast metadata exceeds rank 8");
+  return out;
+}
+
+Shape broadcast_strides(const Shape& from, const Shape& to) { return make_broadcast_plan(from, to).lhs_strides; }
+
+// ------------------------------------------------------------ math extension
+// log / sqrt / abs, clip and topk with the plans of core/math.cpp:13-71.
+void require_math_dtype(const Tensor& t) {
+  if (t.dtype != DType::kFloat32 && t.dtype != DType::kInt32)
+    throw std::invalid_argument("math operations require float32 or int32 tensors");
+}
+
+Tensor math_unary(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
+  require_math_dtype(x);
+  const int code = op.kind == OpKind::kLog ? TCX_MATH_LOG : op.kind == OpKind::kSqrt ? TCX_MATH_SQRT : TCX_MATH_ABS;
+  if (code != TCX_MATH_ABS && x.dtype != DType::kFloat32)
+    throw std::invalid_argument("log/sqrt only support float32 tensors");
+  const void* xp = device_ptr(x);
+  Tensor out = make_tensor(x.dtype, x.shape);
+  ok_or_throw(tcx_hip_math_unary(code, tcx_dtype(x.dtype), xp, out_ptr(out), numel(x.shape), s), "HIP math");
+  return out;
+}
+
+Tensor clip(std::span<const Tensor> inputs, tcx_stream_t s) {
+  if (inputs.size() != 3) throw std::invalid_argument("invalid math operation or input count");
+  for (const Tensor& t : inputs) {
+    require_math_dtype(t);
+    if (t.dtype != inputs[0].dtype) throw std::invalid_argument("math input dtypes must match");
+    (void)device_ptr(t);
+  }
+  Shape shape = inputs[0].shape;
+  for (const Tensor& t : inputs) shape = make_broadcast_plan(shape, t.shape).output_shape;
+  Tensor out = make_tensor(inputs[0].dtype, shape);
+  if (numel(shape) == 0) return out;
+  const Strided m = compress(shape, {broadcast_strides(inputs[0].shape, shape), broadcast_strides(inputs[1].shape, shape),
+                                     broadcast_strides(inputs[2].shape, shape)});
+  ok_or_throw(tcx_hip_clip(tcx_dtype(inputs[0].dtype), device_ptr(inputs[0]), device_ptr(inputs[1]),
+                           device_ptr(inputs[2]), out_ptr(out), static_cast<int32_t>(m.shape.size()), m.shape.data(),
+                           m.strides[0].data(), m.strides[1].data(), m.strides[2].data(), s),
+              "HIP clip");
+  return out;
+}
+
+std::pair<Tensor, Tensor> topk(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
+  require_math_dtype(x);
+  if (x.shape.empty()) throw std::invalid_argument("topk requires rank >= 1");
+  Dim axis = op.axis;
+  if (axis < 0) axis += static_cast<Dim>(x.shape.size());
+  if (axis < 0 || axis >= static_cast<Dim>(x.shape.size())) throw std::invalid_argument("topk axis out of range");
+  const Dim reduce = x.shape[static_cast<std::size_t>(axis)];
+  if (reduce > std::numeric_limits<std::int32_t>::max()) throw std::invalid_argument("topk index range exceeds int32");
+  if (op.k < 0 || op.k > reduce) throw std::invalid_argument("topk k must be between zero and the axis size");
+  Shape shape = x.shape;
+  shape[static_cast<std::size_t>(axis)] = op.k;
+  (void)numel(shape);
+  const void* xp = device_ptr(x);
+  Tensor values = make_tensor(x.dtype, shape);
+  Tensor indices = make_tensor(DType::kInt32, shape);
+  if (numel(shape) == 0) return {std::move(values), std::move(indices)};
+  Dim outer = 1, inner = 1;
+  for (Dim a = 0; a < static_cast<Dim>(x.shape.size()); ++a) {
+    if (a < axis) outer *= x.shape[static_cast<std::size_t>(a)];
+    if (a > axis) inner *= x.shape[static_cast<std::size_t>(a)];
+  }
+  ok_or_throw(tcx_hip_topk(tcx_dtype(x.dtype), xp, out_ptr(values), static_cast<int32_t*>(out_ptr(indices)), outer,
+                           reduce, inner, op.k, op.largest ? 1 : 0, op.sorted ? 1 : 0, s),
+              "HIP topk");
+  return {std::move(values), std::move(indices)};
+}
+
+// ------------------------------------------------------------ inference primitives
+// kEmbedding with make_embedding_plan (core/inference.cpp:47-57).
+Tensor embedding(std::span<const Tensor> inputs, tcx_stream_t s) {
+  if (inputs.size() != 2) throw std::invalid_argument("embedding requires indices and weight");
+  const Tensor& indices = inputs[0];
+  const Tensor& weight = inputs[1];
+  if (indices.dtype != DType::kInt32) throw std::invalid_argument("embedding indices must be int32");
+  if (weight.dtype != DType::kFloat32) throw std::invalid_argument("inference values require float32 tensors");
+  if (weight.shape.size() != 2) throw std::invalid_argument("embedding weight must have rank 2");
+  Shape shape = indices.shape;
+  shape.push_back(weight.shape[1]);
+  (void)numel(shape);
+  const auto* ip = static_cast<const int32_t*>(device_ptr(indices));
+  const float* wp = f32(weight);
+  Tensor out = make_tensor(DType::kFloat32, shape);
+  const Dim count = numel(indices.shape);
+  if (count == 0) return out;
+  Tensor flag = make_tensor(DType::kInt32, Shape{1});
+  ok_or_throw(tcx_hip_embedding_f32(ip, wp, static_cast<float*>(out_ptr(out)), count, weight.shape[0], weight.shape[1],
+                                    static_cast<int32_t*>(out_ptr(flag)), s),
+              "HIP embedding");
+  return out;
+}
+
+float checked_scale(double scale) {
+  const float narrowed = static_cast<float>(scale);
+  if (!std::isfinite(scale) || !std::isfinite(narrowed) || (scale != 0 && narrowed == 0))
+    throw std::invalid_argument("attention scale must be finite and representable as float32");
+  return narrowed;
+}
+
+struct AttentionSoftmaxPlan {
+  Shape shape;
+  int mask_kind;
+  float scale;
+};
+
+// make_attention_softmax_plan (core/inference.cpp:59-84).
+AttentionSoftmaxPlan attention_softmax_plan(const OpDesc& op, std::span<const Tensor> inputs) {
+  if (inputs.empty() || inputs.size() > 2)
+    throw std::invalid_argument("attention softmax requires scores and optional mask");
+  if (inputs[0].dtype != DType::kFloat32) throw std::invalid_argument("inference values require float32 tensors");
+  (void)numel(inputs[0].shape);
+  if (inputs[0].shape.size() < 2 || op.attention_shape.size() < 2)
+    throw std::invalid_argument("attention scores must have rank >= 2");
+  const Shape& shape = op.attention_shape;
+  if (make_broadcast_plan(inputs[0].shape, shape).output_shape != shape)
+    throw std::invalid_argument("attention scores cannot broadcast to target");
+  int mask_kind = TCX_MASK_NONE;
+  if (inputs.size() == 2) {
+    const Tensor& mask = inputs[1];
+    if (mask.dtype != DType::kBool && mask.dtype != DType::kFloat32)
+      throw std::invalid_argument("attention mask must be bool or float32");
+    if (make_broadcast_plan(mask.shape, shape).output_shape != shape)
+      throw std::invalid_argument("attention mask cannot broadcast to scores");
+    mask_kind = mask.dtype == DType::kBool ? TCX_MASK_BOOL : TCX_MASK_ADDITIVE;
+  }
+  (void)numel(shape);
+  return {shape, mask_kind, checked_scale(op.attention_scale.value_or(1.0))};
+}
+
+void attention_softmax_into(const OpDesc& op, const AttentionSoftmaxPlan& plan, const Tensor& scores,
+                            const Tensor* mask, const Tensor& out, tcx_stream_t s) {
+  std::vector<Shape> strides{broadcast_strides(scores.shape, plan.shape)};
+  strides.push_back(mask ? broadcast_strides(mask->shape, plan.shape) : Shape(plan.shape.size(), 0));
+  const Strided m = compress(plan.shape, strides, 2);
+  tcx_hip_attention_softmax_desc_t d{};
+  d.rank = static_cast<int32_t>(m.shape.size());
+  for (std::size_t i = 0; i < m.shape.size(); ++i) {
+    d.shape[i] = m.shape[i];
+    d.score_strides[i] = m.strides[0][i];
+    d.mask_strides[i] = m.strides[1][i];
+  }
+  d.mask_kind = plan.mask_kind;
+  d.causal = op.causal ? 1 : 0;
+  d.scale = plan.scale;
+  ok_or_throw(tcx_hip_attention_softmax_f32(f32(scores), mask ? device_ptr(*mask) : nullptr,
+                                            static_cast<float*>(out_ptr(out)), &d, s),
+              "HIP attention softmax");
+}
+
+Tensor attention_softmax(const OpDesc& op, std::span<const Tensor> inputs, tcx_stream_t s) {
+  const AttentionSoftmaxPlan plan = attention_softmax_plan(op, inputs);
+  for (const Tensor& t : inputs) (void)device_ptr(t);
+  Tensor out = make_tensor(DType::kFloat32, plan.shape);
+  if (numel(plan.shape) == 0) return out;
+  attention_softmax_into(op, plan, inputs[0], inputs.size() == 2 ? &inputs[1] : nullptr, out, s);
+  return out;
+}
+
+// scores[b, i, j] = sum_f q[b, i, f] * k[b, j, f] over broadcast batches: one
+// NT GEMM reading K in place (the reference transposes K first).
+Tensor attention_scores(const Tensor& q, const Tensor& k, tcx_stream_t s) {
+  const Shape qb(q.shape.begin(), q.shape.end() - 2), kb(k.shape.begin(), k.shape.end() - 2);
+  const Dim rows = q.shape[q.shape.size() - 2], columns = k.shape[k.shape.size() - 2], features = q.shape.back();
+  const BroadcastPlan bp = make_broadcast_plan(qb, kb);
+  Shape shape = bp.output_shape;
+  shape.push_back(rows);
+  shape.push_back(columns);
+  Tensor out = make_tensor(DType::kFloat32, shape);
+  if (numel(shape) == 0) return out;
+  Shape ql = bp.lhs_strides, kl = bp.rhs_strides;
+  for (Dim& v : ql) v *= rows * features;
+  for (Dim& v : kl) v *= columns * features;
+  const Strided m = compress(bp.output_shape, {ql, kl});
+  if (m.shape.size() > TCX_HIP_MAX_BATCH_RANK) throw std::invalid_argument("HIP attention supports 8 batch axes");
+  tcx_hip_gemm_desc_t d{};
+  d.m = rows;
+  d.n = columns;
+  d.k = features;
+  d.rhs_transposed = 1;
+  d.batch_rank = static_cast<int32_t>(m.shape.size());
+  d.batch_count = numel(m.shape);
+  for (std::size_t i = 0; i < m.shape.size(); ++i) {
+    d.batch_shape[i] = m.shape[i];
+    d.lhs_batch_strides[i] = m.strides[0][i];
+    d.rhs_batch_strides[i] = m.strides[1][i];
+  }
+  ok_or_throw(tcx_hip_gemm_f32(f32(q), f32(k), static_cast<float*>(out_ptr(out)), &d, s), "HIP attention scores");
+  return out;
+}
+
+// kAttention with the validation of core/inference.cpp:123-161: scores, the
+// attention softmax, then probabilities @ V, each a native launch.
+Tensor attention(const OpDesc& op, std::span<const Tensor> inputs, tcx_stream_t s) {
+  if (op.kind != OpKind::kAttention || inputs.size() < 3 || inputs.size() > 4)
+    throw std::invalid_argument("attention requires query, key, value and optional mask");
+  for (std::size_t i = 0; i < 3; ++i) {
+    if (inputs[i].dtype != DType::kFloat32) throw std::invalid_argument("inference values require float32 tensors");
+    (void)numel(inputs[i].shape);
+    if (inputs[i].shape.size() < 2) throw std::invalid_argument("attention tensors require rank >= 2");
+  }
+  const Tensor& q = inputs[0];
+  const Tensor& k = inputs[1];
+  const Tensor& v = inputs[2];
+  const Dim features = q.shape.back(), rows = q.shape[q.shape.size() - 2], columns = k.shape[k.shape.size() - 2];
+  if (features <= 0 || features != k.shape.back() || columns != v.shape[v.shape.size() - 2])
+    throw std::invalid_argument(
+        "attention query/key features and key/value sequence sizes must match; features must be positive");
+  Shape batch;
+  for (std::size_t i = 0; i < 3; ++i) {
+    const Shape& input = inputs[i].shape;
+    const std::size_t rank = std::max(batch.size(), input.size() - 2);
+    Shape merged(rank, 1);
+    for (std::size_t a = 0; a < rank; ++a) {
+      const Dim left = a < rank - batch.size() ? 1 : batch[a - (rank - batch.size())];
+      const Dim right = a < rank - (input.size() - 2) ? 1 : input[a - (rank - (input.size() - 2))];
+      if (left != right && left != 1 && right != 1) throw std::invalid_argument("attention batch dimensions cannot broadcast");
+      merged[a] = left == 1 ? right : left;
+    }
+    batch = std::move(merged);
+  }
+  Shape scores = batch;
+  scores.push_back(rows);
+  scores.push_back(columns);
+  Shape shape = batch;
+  shape.push_back(rows);
+  shape.push_back(v.shape.back());
+  (void)numel(scores);
+  (void)numel(shape);
+  OpDesc softmax{OpKind::kAttentionSoftmax};
+  softmax.attention_shape = scores;
+  softmax.causal = op.causal;
+  softmax.attention_scale =
+      checked_scale(op.attention_scale.value_or(1.0 / std::sqrt(static_cast<double>(features))));
+  // Validate the mask against the scores before any launch, also for empty outputs.
+  Tensor descriptor = q;
+  descriptor.shape = scores;
+  descriptor.strides = contiguous_strides(scores);
+  std::vector<Tensor> preview{descriptor};
+  if (inputs.size() == 4) preview.push_back(inputs[3]);
+  const AttentionSoftmaxPlan plan = attention_softmax_plan(softmax, preview);
+  for (const Tensor& t : inputs) (void)device_ptr(t);
+  if (numel(shape) == 0) return make_tensor(DType::kFloat32, shape);
+  if (columns == 0) {  // no keys: every output row is an empty sum
+    Tensor zeros;
+    zeros.dtype = DType::kFloat32;
+    zeros.shape = shape;
+    return fill(zeros, 0.0, s);
+  }
+  const Tensor product = attention_scores(q, k, s);
+  Tensor probabilities = make_tensor(DType::kFloat32, scores);
+  attention_softmax_into(softmax, plan, product, inputs.size() == 4 ? &inputs[3] : nullptr, probabilities, s);
+  return matmul(probabilities, v, s);
 }
 
 // ------------------------------------------------------------ kernel class
@@ -525,8 +827,8 @@ Expected<std::string> device_name() {
 
 Expected<Tensor> empty(Shape shape, DType dtype) {
   try {
-    if (dtype != DType::kFloat32 && dtype != DType::kInt32)
-      return Status(StatusCode::kInvalidArgument, "HIP tensors support float32 and int32");
+    if (dtype != DType::kFloat32 && dtype != DType::kInt32 && dtype != DType::kBool)
+      return Status(StatusCode::kInvalidArgument, "HIP tensors support float32, int32 and bool");
     const auto bytes = static_cast<std::size_t>(numel(shape)) * dtype_size(dtype);
     if (const int rc = tcx_hip_init(); rc != TCX_OK) return status_from_code(rc, "HIP device");
     auto buffer = HipBuffer::create(bytes);
@@ -619,6 +921,20 @@ Status HipBackend::execute(const BackendExecution& e) {
       case OpKind::kSubtract:
       case OpKind::kMultiply:
       case OpKind::kDivide: result = binary(e.op, e.inputs[0], e.inputs[1], s); break;
+      case OpKind::kLog:
+      case OpKind::kSqrt:
+      case OpKind::kAbs: result = math_unary(e.op, e.inputs[0], s); break;
+      case OpKind::kClip: result = clip(e.inputs, s); break;
+      case OpKind::kTopK: {
+        auto [values, indices] = topk(e.op, e.inputs[0], s);
+        ok_or_throw(tcx_hip_stream_synchronize(s), "HIP execution");
+        e.outputs[0] = std::move(values);
+        e.outputs[1] = std::move(indices);
+        return Status::Ok();
+      }
+      case OpKind::kEmbedding: result = embedding(e.inputs, s); break;
+      case OpKind::kAttentionSoftmax: result = attention_softmax(e.op, e.inputs, s); break;
+      case OpKind::kAttention: result = attention(e.op, e.inputs, s); break;
       default:
         return Status(StatusCode::kInvalidArgument, "unsupported HIP backend execution operation");
     }

@@ -201,8 +201,11 @@ int tcx_hip_fill(int dtype, void* out, int64_t n, double value, tcx_stream_t str
   else if (dtype == TCX_INT32)
     hipLaunchKernelGGL((fill_kernel<int>), grid, dim3(256), 0, s, static_cast<int*>(out), n,
                        static_cast<int>(value));
+  else if (dtype == TCX_BOOL)
+    hipLaunchKernelGGL((fill_kernel<std::uint8_t>), grid, dim3(256), 0, s, static_cast<std::uint8_t*>(out), n,
+                       static_cast<std::uint8_t>(value != 0.0 ? 1 : 0));
   else
-    return fail(TCX_INVALID_ARGUMENT, "fill requires float32 or int32");
+    return fail(TCX_INVALID_ARGUMENT, "fill requires float32, int32 or bool");
   return check(hipGetLastError(), "fill launch");
 }
 

@@ -37,6 +37,8 @@ EXPORTS = [
     "tcx_hip_gemm_f32", "tcx_hip_reduce_workspace_bytes", "tcx_hip_reduce",
     "tcx_hip_reduce_axes", "tcx_hip_softmax_f32", "tcx_hip_rmsnorm_f32", "tcx_hip_layernorm_f32",
     "tcx_hip_bias_act_f32", "tcx_hip_unary_f32", "tcx_hip_binary", "tcx_hip_fill",
+    "tcx_hip_math_unary", "tcx_hip_clip", "tcx_hip_topk", "tcx_hip_embedding_f32",
+    "tcx_hip_attention_softmax_f32",
 ]
 
 

@@ -139,6 +139,107 @@ def cases():
     add("affine_layernorm_gb", "affine_layernorm", [x, g, be], axis=-1, has_weight=True, has_bias=True)
     add("affine_layernorm_g", "affine_layernorm", [x, g], axis=-1, has_weight=True)
     add("affine_rmsnorm_g", "affine_rmsnorm", [x, g], axis=-1, has_weight=True)
+
+    # ---- log / sqrt / abs (cpu_math.cpp:40-44; cases of test_math_ops.py:26-60)
+    bits = np.array([0, 0x80000000, 1, 2, 0x007fffff, 0x00800000, 0x80000001, 0x807fffff, 0x80800000,
+                     0x3f800000, 0xbf800000, 0x7f7fffff, 0x7f800000, 0xff800000, 0x7fc01234], np.uint32)
+    for op in ("log", "sqrt", "abs"):
+        for shape in [(2, 3, 5), (513,), (0,), ()]:
+            add(f"{op}_{'x'.join(map(str, shape)) or 'scalar'}", op,
+                [rng.uniform(.01, 100, shape).astype(np.float32)])
+        add(f"{op}_ieee", op, [bits.view(np.float32)])
+    add("abs_i32_wrap", "abs", [np.array([-2**31, -2**31 + 1, -16777217, -1, 0, 1, 2**31 - 1], np.int32)])
+    add("log_i32_rejected", "log", [np.array([1, 2], np.int32)])
+
+    # ---- clip (cpu_math.cpp:45-50; test_math_ops.py:94-120)
+    lim = {"float32": (-np.inf, np.inf), "int32": (-2**31, 2**31 - 1)}
+    for dtype in ("float32", "int32"):
+        xi = rng.integers(-10, 10, (2, 3, 4)).astype(dtype)
+        for lo, hi in [(-2, 3), (None, 3), (-2, None), (4, -4), (0, 0)]:
+            lo = lim[dtype][0] if lo is None else lo
+            hi = lim[dtype][1] if hi is None else hi
+            add(f"clip_{dtype}_{lo}_{hi}", "clip", [xi, np.array(lo, dtype), np.array(hi, dtype)])
+        add(f"clip_{dtype}_broadcast", "clip", [np.array([[[-4], [1], [9]]], dtype),
+                                               np.array([[-1, 2, 7, 8]], dtype), np.array([[[3]], [[10]]], dtype)])
+    add("clip_ieee", "clip", [np.array([np.nan, -0., 0., 1e-40, -1e-40, np.inf, -np.inf, 1., 2.], np.float32),
+                              np.array([-1., 0., -0., -2e-40, -2e-40, -1., -1., np.nan, -1.], np.float32),
+                              np.array([1., 0., -0., 2e-40, 2e-40, 1., 1., 2., np.nan], np.float32)])
+    add("clip_random_f32", "clip", [f32(rng, (7, 130)), f32(rng, (130,), .5) - 1, f32(rng, (7, 1), .5) + 1])
+
+    # ---- topk (cpu_math.cpp:57-67; test_math_ops.py:123-180)
+    tx = rng.integers(-3, 4, (3, 5, 6)).astype(np.float32)
+    tx[0, 1, 2] = np.nan
+    tx[2, 3, 1] = np.nan
+    tx[1, 2, 3] = -0.0
+    for dtype in ("float32", "int32"):
+        x = tx if dtype == "float32" else np.nan_to_num(tx).astype(np.int32)
+        for axis in (0, 1, 2, -1):
+            n = x.shape[axis]
+            for k in sorted({0, 1, n // 2, n}):
+                for largest in (True, False):
+                    for srt in (True, False):
+                        add(f"topk_{dtype}_a{axis}_k{k}_{int(largest)}{int(srt)}", "topk", [x], axis=axis, k=k,
+                            largest=largest, sorted=srt, n_outputs=2)
+    add("topk_wide", "topk", [f32(rng, (4, 3000))], axis=1, k=37, n_outputs=2)
+    add("topk_k_too_large", "topk", [f32(rng, (2, 3))], axis=1, k=4, n_outputs=2)
+
+    # ---- embedding (cpu_inference.cpp:12-21; test_inference_ops.py:100-130)
+    for shape in [(), (4,), (2, 3), (2, 0, 3)]:
+        for width in (0, 1, 7):
+            add(f"embedding_{'x'.join(map(str, shape)) or 'scalar'}_w{width}", "embedding",
+                [rng.integers(0, 5, size=shape, dtype=np.int32), f32(rng, (5, width))])
+    ebits = np.array([[0, 0x80000000, 1, 0x7fc01234], [0x7f800000, 0xff800000, 0x80000001, 0x3f800000]],
+                     np.uint32).view(np.float32)
+    add("embedding_bits", "embedding", [np.array([1, 0, 1], np.int32), ebits])
+    add("embedding_index_negative", "embedding", [np.array([-1], np.int32), f32(rng, (2, 3))])
+    add("embedding_index_past_end", "embedding", [np.array([0, 1, 2], np.int32), f32(rng, (2, 3))])
+    add("embedding_big_table", "embedding", [rng.integers(0, 1000, (3, 17), dtype=np.int32), f32(rng, (1000, 96))])
+
+    # ---- attention (inference.cpp:123-161 over cpu_inference.cpp:22-47;
+    #      cases of test_inference_ops.py:133-343)
+    shapes = [((3, 4), (5, 4), (5, 2)), ((2, 3, 4), (2, 5, 4), (2, 5, 6)),
+              ((2, 1, 3, 4), (1, 3, 5, 4), (2, 3, 5, 2)), ((3, 4), (5, 4), (2, 1, 5, 2)),
+              ((0, 4), (5, 4), (5, 2)), ((3, 4), (0, 4), (0, 2)), ((3, 4), (5, 4), (5, 0))]
+    for si, (qs, ks, vs) in enumerate(shapes):
+        q, k, v = f32(rng, qs), f32(rng, ks), f32(rng, vs)
+        ms = (qs[-2], ks[-2])
+        bmask = rng.random(ms) > .4
+        if ms[0]:
+            bmask[0] = False
+        amask = f32(rng, ms)
+        amask[rng.random(ms) < .3] = -np.inf
+        if ms[0]:
+            amask[0] = -np.inf
+        for mname, mask in (("none", None), ("bool", bmask), ("additive", amask), ("false", np.array(False))):
+            for causal in (False, True):
+                ins = [q, k, v] + ([] if mask is None else [mask])
+                add(f"attention_s{si}_{mname}_c{int(causal)}", "attention", ins, causal=causal)
+    q, k, v = f32(rng, (2, 3, 4)), f32(rng, (5, 4)), f32(rng, (5, 3))
+    bm = rng.random((2, 1, 5)) > .3
+    for scale in (0.0, -0.5, 2.0, float(np.float32(.3)), 1e-39, -1e-40):
+        add(f"attention_scale_{scale}", "attention", [q, k, v, bm], scale=scale)
+    for exceptional in (np.nan, np.inf, -np.inf):
+        kk = np.ones((2, 2), np.float32)
+        kk[0] = exceptional
+        for masked in (False, True):
+            add(f"attention_nonfinite_{exceptional}_{masked}", "attention",
+                [np.ones((1, 2), np.float32), kk, f32(rng, (2, 3)), np.array([[not masked, True]])])
+    for bias in (np.nan, np.inf, -np.inf):
+        add(f"attention_bias_{bias}", "attention", [f32(rng, (2, 3)), f32(rng, (4, 3)), f32(rng, (4, 2)),
+                np.array([[bias, 0, -np.inf, 0], [bias, bias, bias, bias]], np.float32)])
+    add("attention_high_rank", "attention", [f32(rng, (1,) * 6 + (3, 4)), f32(rng, (1,) * 6 + (2, 4)),
+                                             f32(rng, (1,) * 6 + (2, 3))])
+    add("attention_long_causal", "attention", [f32(rng, (257, 3)), f32(rng, (513, 3)), f32(rng, (513, 2))],
+        causal=True)
+    add("attention_heads_64", "attention", [f32(rng, (2, 4, 33, 64)), f32(rng, (2, 4, 70, 64)),
+                                            f32(rng, (2, 4, 70, 64))], causal=True)
+    for scale in (float("nan"), float("inf"), 1e300, 1e-300):
+        add(f"attention_bad_scale_{scale}", "attention", [np.zeros((0, 2), np.float32),
+            np.zeros((3, 2), np.float32), np.zeros((3, 1), np.float32)], scale=scale)
+    add("attention_bad_features", "attention", [f32(rng, (2, 3)), f32(rng, (2, 4)), f32(rng, (2, 3))])
+    add("attention_bad_batch", "attention", [f32(rng, (2, 0, 3)), f32(rng, (3, 2, 3)), f32(rng, (3, 2, 3))])
+    add("attention_bad_mask", "attention", [f32(rng, (2, 3)), f32(rng, (2, 3)), f32(rng, (2, 3)),
+                                            np.zeros((2, 3), bool)])
     return c
 
 
@@ -154,8 +255,13 @@ def main() -> None:
             entry["inputs"].append(key)
         try:
             out = ref.execute(op, inputs, **kw)
-            arrays[f"c{index}_out"] = out
-            entry["output"] = f"c{index}_out"
+            if isinstance(out, tuple):
+                for n, o in enumerate(out):
+                    arrays[f"c{index}_out{n}"] = o
+                entry["outputs"] = [f"c{index}_out{n}" for n in range(len(out))]
+            else:
+                arrays[f"c{index}_out"] = out
+                entry["output"] = f"c{index}_out"
         except ref.ReferenceError as error:
             entry["error"] = {"code": error.code, "message": str(error)}
         manifest.append(entry)

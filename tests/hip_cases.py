@@ -8,7 +8,12 @@ Bars (stated once, used everywhere):
   * float32 sum/mean on the tree path: max|d| / sum|x| <= 1e-5 per output;
   * softmax, LayerNorm, RMSNorm, affine norms, MLP output:
     allclose(rtol=1e-5, atol=1e-5), the reference's reduction class;
-  * exp / gelu / silu: allclose(rtol=1e-6, atol=1e-6), the elementwise class.
+  * exp / gelu / silu: allclose(rtol=1e-6, atol=1e-6), the elementwise class;
+  * abs, clip, topk, embedding, sqrt: bit-exact (sqrt is correctly rounded on
+    both sides; NaNs compare as NaN, whatever their payload);
+  * log: allclose(rtol=1e-6, atol=0), the bar of test_math_ops.py:15-21;
+  * attention: allclose(rtol=2e-4, atol=2e-5), the bar of
+    test_inference_ops.py:20-25.
 """
 
 from __future__ import annotations
@@ -124,14 +129,52 @@ def run_hip(cx, op, inputs, kw):
         if op == "affine_rmsnorm":
             return cx.rmsnorm(t[0], axis, kw.get("eps", 1e-5), weight=weight)
         return cx.layernorm(t[0], axis, kw.get("eps", 1e-5), weight=weight, bias=bias)
+    if op in ("log", "sqrt", "abs"):
+        return getattr(cx, op)(t[0])
+    if op == "clip":
+        return cx.clip(*t)
+    if op == "topk":
+        return cx.topk(t[0], kw["k"], axis, kw.get("largest", True), kw.get("sorted", True))
+    if op == "embedding":
+        return cx.embedding(*t)
+    if op == "attention":
+        mask = t[3] if len(t) == 4 else None
+        return cx.attention(*t[:3], mask, is_causal=kw.get("causal", False), scale=kw.get("scale"))
     raise AssertionError(op)
 
 
+def host(result):
+    """numpy value(s) of a run_hip result (a tensor or a tuple of tensors)."""
+    if isinstance(result, tuple):
+        return tuple(r.numpy() for r in result)
+    return result.numpy()
+
+
+def assert_nan_bits(actual, expected, context=""):
+    """Bit-exact except that any NaN matches any NaN."""
+    actual, expected = np.asarray(actual), np.asarray(expected)
+    assert actual.shape == expected.shape and actual.dtype == expected.dtype, context
+    nan_a, nan_e = np.isnan(actual), np.isnan(expected)
+    assert np.array_equal(nan_a, nan_e), f"{context}: NaN positions differ"
+    assert_bits(np.where(nan_a, 0, actual).astype(actual.dtype), np.where(nan_e, 0, expected).astype(expected.dtype),
+                context)
+
+
 def check_case(name, op, inputs, kw, actual, expected):
-    """Applies the bar for `op` to one result."""
-    if op in ("max", "min", "argmax", "add", "subtract", "multiply", "divide") or \
-            expected.dtype == np.int32:
+    """Applies the bar for `op` to one result (or tuple of results)."""
+    if isinstance(expected, tuple):
+        for n, (a, e) in enumerate(zip(actual, expected)):
+            check_case(f"{name} output {n}", op, inputs, kw, a, e)
+        return
+    if op in ("max", "min", "argmax", "add", "subtract", "multiply", "divide", "abs", "clip", "topk",
+              "embedding") or expected.dtype == np.int32:
         assert_bits(actual, expected, name)
+    elif op == "sqrt":
+        assert_nan_bits(actual, expected, name)
+    elif op == "log":
+        assert_close(actual, expected, 1e-6, 0.0, name)
+    elif op == "attention":
+        assert_close(actual, expected, 2e-4, 2e-5, name)
     elif op in ("sum", "mean"):
         outer, red, inner, exact = reduction_run(inputs[0].shape, kw)
         if exact:

@@ -13,7 +13,7 @@ import pytest
 
 import oracle
 from conftest import require_gpu
-from hip_cases import (assert_bits, assert_close, assert_matmul, check_case, run_hip,
+from hip_cases import (assert_bits, assert_close, assert_matmul, check_case, host, run_hip,
                        sum_error)
 
 pytestmark = pytest.mark.gpu
@@ -35,11 +35,13 @@ def test_golden_vectors(cx, golden):
         name, op, kw = entry["name"], entry["op"], entry["kwargs"]
         if "error" in entry:
             with pytest.raises(ValueError):
-                run_hip(cx, op, inputs, kw).numpy()
+                host(run_hip(cx, op, inputs, kw))
             continue
         try:
-            actual = run_hip(cx, op, inputs, kw).numpy()
-            check_case(name, op, inputs, kw, actual, arrays[entry["output"]])
+            actual = host(run_hip(cx, op, inputs, kw))
+            expected = (tuple(arrays[k] for k in entry["outputs"]) if "outputs" in entry
+                        else arrays[entry["output"]])
+            check_case(name, op, inputs, kw, actual, expected)
         except AssertionError as error:
             failures.append(str(error))
     assert not failures, f"{len(failures)} golden cases failed:\n" + "\n".join(failures[:20])

@@ -38,12 +38,29 @@ def run_oracle(op, inputs, kw):
         weight = inputs[1] if kw.get("has_weight") else None
         bias = inputs[2] if kw.get("has_bias") else None
         return oracle.affine_norm(inputs[0], axis, kw.get("eps", 1e-5), weight, bias, rms=rms)
+    if op in ("log", "sqrt", "abs"):
+        return getattr(oracle, op)(inputs[0])
+    if op == "clip":
+        return oracle.clip(*inputs)
+    if op == "topk":
+        return oracle.topk(inputs[0], kw["k"], axis, kw.get("largest", True), kw.get("sorted", True))
+    if op == "embedding":
+        return oracle.embedding(*inputs)
+    if op == "attention":
+        mask = inputs[3] if len(inputs) == 4 else None
+        return oracle.attention(*inputs[:3], mask, kw.get("causal", False), kw.get("scale"))
     raise AssertionError(op)
+
+
+def expected_outputs(entry, arrays):
+    if "outputs" in entry:
+        return tuple(arrays[k] for k in entry["outputs"])
+    return arrays[entry["output"]]
 
 
 def test_golden_vectors_bit_exact(golden):
     manifest, arrays = golden
-    assert len(manifest) > 200
+    assert len(manifest) > 500
     for entry in manifest:
         inputs = [arrays[k] for k in entry["inputs"]]
         if "error" in entry:
@@ -51,7 +68,12 @@ def test_golden_vectors_bit_exact(golden):
                 run_oracle(entry["op"], inputs, entry["kwargs"])
             continue
         actual = run_oracle(entry["op"], inputs, entry["kwargs"])
-        assert_bits_equal(actual, arrays[entry["output"]], entry["name"])
+        expected = expected_outputs(entry, arrays)
+        if isinstance(expected, tuple):
+            for n, (a, e) in enumerate(zip(actual, expected)):
+                assert_bits_equal(a, e, f"{entry['name']} output {n}")
+        else:
+            assert_bits_equal(actual, expected, entry["name"])
 
 
 @pytest.mark.skipif(not ref.available(), reason="oracle/_ref not built (needs /root/reference)")
@@ -172,3 +194,53 @@ def test_plans_match_numpy_broadcasting():
         oracle.make_matmul_plan((2, 3), (4, 5))
     shape, meta, size = oracle.make_reduction_plan((3, 4, 5), (2, 0))
     assert shape == (4,) and size == 15 and meta == [4, 5, 3, 20, 5, 1]
+
+
+def test_math_clip_topk_closed_forms():
+    rng = np.random.default_rng(11)
+    squares = (np.arange(1, 300, dtype=np.float32)) ** 2
+    np.testing.assert_array_equal(oracle.sqrt(squares), np.arange(1, 300, dtype=np.float32))
+    powers = np.float32(2.0) ** np.arange(-20, 20, dtype=np.float32)
+    np.testing.assert_allclose(oracle.log(powers), np.arange(-20, 20) * np.log(2.0), rtol=1e-6, atol=1e-6)
+    x = rng.standard_normal(1000).astype(np.float32)
+    assert_bits_equal(oracle.abs(x), np.abs(x), "abs")
+    assert oracle.abs(np.array([-2**31], np.int32))[0] == -2**31  # uint32 negation wraps
+    lo, hi = np.float32(-0.5), np.float32(0.7)
+    np.testing.assert_array_equal(oracle.clip(x, np.array(lo), np.array(hi)), np.clip(x, lo, hi))
+    # topk equals a stable sort by (-value, index); unsorted lists the same set by index.
+    xi = rng.integers(-5, 6, (4, 50)).astype(np.int32)
+    values, indices = oracle.topk(xi, 9, 1, True, True)
+    order = np.argsort(-xi.astype(np.int64), axis=1, kind="stable")[:, :9]
+    np.testing.assert_array_equal(indices, order)
+    np.testing.assert_array_equal(values, np.take_along_axis(xi, order, 1))
+    _, unsorted = oracle.topk(xi, 9, 1, True, False)
+    np.testing.assert_array_equal(unsorted, np.sort(order, axis=1))
+    low_values, _ = oracle.topk(xi, 9, 1, False, True)
+    np.testing.assert_array_equal(low_values, np.sort(xi, axis=1)[:, :9])
+
+
+def test_embedding_and_attention_closed_forms():
+    rng = np.random.default_rng(12)
+    table = rng.standard_normal((7, 5)).astype(np.float32)
+    ids = rng.integers(0, 7, (3, 4)).astype(np.int32)
+    assert_bits_equal(oracle.embedding(ids, table), table[ids], "embedding")
+    with pytest.raises(ValueError):
+        oracle.embedding(np.array([7], np.int32), table)
+    q, k, v = [rng.standard_normal(s).astype(np.float32) for s in ((2, 6, 8), (2, 9, 8), (2, 9, 3))]
+    mask = rng.random((6, 9)) > 0.3
+    mask[:, 0] = True
+    s = (q.astype(np.float64) @ np.swapaxes(k, -1, -2)) / np.sqrt(8.0)
+    s = np.where(mask & (np.arange(9) <= np.arange(6)[:, None]), s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    expected = (p / p.sum(-1, keepdims=True)) @ v
+    np.testing.assert_allclose(oracle.attention(q, k, v, mask, True), expected, rtol=2e-5, atol=2e-6)
+    # A row with every key masked is all zeros, not NaN (cpu_inference.cpp:36-39).
+    none = np.zeros((6, 9), bool)
+    assert not oracle.attention(q, k, v, none).any()
+    # Causality: keys after the query do not change the output.
+    k2, v2 = k.copy(), v.copy()
+    k2[:, 4:] += 100
+    v2[:, 4:] -= 500
+    a = oracle.attention(q, k, v, None, True)
+    b = oracle.attention(q, k2, v2, None, True)
+    assert_bits_equal(a[:, :4], b[:, :4], "causal prefix")
