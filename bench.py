@@ -7,8 +7,8 @@ C2), inputs resident in HBM, K timed GEMM launches bracketed by stream
 synchronisation, timed with HIP events on the launch stream. The same JSON line
 carries `roofline` for that kernel, `cpu_baseline` (the reference CPU matmul,
 single thread, on a bounded row slab), and `secondary`: the other configs'
-kernels (batched/edge GEMM, reductions, softmax/norms, MLP) each as GB/s or
-TFLOP/s with its roofline fraction.
+kernels (batched/edge GEMM, reductions, softmax/norms, MLP, fused attention)
+each as GB/s or TFLOP/s with its roofline fraction.
 
 Peaks: fp32 MFMA 157.3 TFLOP/s, HBM 8.0 TB/s (MI355X published figures).
 """
@@ -191,6 +191,23 @@ def secondary_benches(steps: int, warmup: int, only: str | None):
                     "frac": flops / (avg * 1e-3) / PEAK_FP32_MFMA,
                     "tokens_per_s": 4096 / (avg * 1e-3)})
         log(f"{out[-1]['name']}: {out[-1]['achieved']:.1f} TFLOP/s ({out[-1]['frac']:.1%})")
+
+    if want("attention"):
+        q, k, v = wl.attention_inputs()
+        bh, seq, d = q.shape
+        dq, dk, dv = (capi.DeviceArray.from_numpy(t) for t in (q, k, v))
+        o = capi.DeviceArray((bh, seq, d))
+        for causal in (False, True):
+            flops = wl.attention_flops(causal)
+            total, per = timed(lambda s, c=causal: capi.flash_attention(
+                dq.ptr, dk.ptr, dv.ptr, o.ptr, bh, seq, seq, d, 1.0 / np.sqrt(d), c, s), steps, warmup)
+            avg = statistics.mean(per)
+            out.append({"name": f"attention_fused_{bh}x{seq}x{d}" + ("_causal" if causal else ""),
+                        "unit": "TFLOP/s", "value": flops / (total / steps * 1e-3) / 1e12,
+                        "kernel_avg_ms": avg, "achieved": flops / (avg * 1e-3) / 1e12,
+                        "peak": PEAK_FP32_MFMA / 1e12, "frac": flops / (avg * 1e-3) / PEAK_FP32_MFMA,
+                        "flop_per_launch": flops})
+            log(f"{out[-1]['name']}: {out[-1]['achieved']:.1f} TFLOP/s ({out[-1]['frac']:.1%})")
     return out
 
 

@@ -278,6 +278,19 @@ typedef struct {
 int tcx_hip_attention_softmax_f32(const float* scores, const void* mask, float* out,
                                   const tcx_hip_attention_softmax_desc_t* desc, tcx_stream_t stream);
 
+/* 1 when tcx_hip_flash_attention_f32 handles these feature sizes
+ * (features == value_features, one of 32, 64, 128), else 0. */
+int tcx_hip_flash_attention_supported(int64_t features, int64_t value_features);
+/* Fused kAttention without a mask (core/inference.cpp:123-161 with
+ * cpu_inference.cpp:22-47): out[b] = softmax(scale * q[b] k[b]^T, causal) v[b]
+ * for `batch` contiguous matrices q [rows, features], k and v [cols, features],
+ * out [rows, features], 16-byte aligned, never materialising the scores.
+ * Causal masks key j > query i. Replaces the three launches of the reference's
+ * attention composite (transpose, matmul, softmax, matmul). */
+int tcx_hip_flash_attention_f32(const float* q, const float* k, const float* v, float* out, int64_t batch,
+                                int64_t rows, int64_t cols, int64_t features, float scale, int causal,
+                                tcx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

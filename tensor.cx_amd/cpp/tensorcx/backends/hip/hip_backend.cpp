@@ -727,6 +727,19 @@ Tensor attention(const OpDesc& op, std::span<const Tensor> inputs, tcx_stream_t 
   const AttentionSoftmaxPlan plan = attention_softmax_plan(softmax, preview);
   for (const Tensor& t : inputs) (void)device_ptr(t);
   if (numel(shape) == 0) return make_tensor(DType::kFloat32, shape);
+  // Unmasked attention over matching batches with 32/64/128 features: the
+  // fused kernel, scores never materialised.
+  const Shape qb(q.shape.begin(), q.shape.end() - 2);
+  if (inputs.size() == 3 && qb == Shape(k.shape.begin(), k.shape.end() - 2) &&
+      qb == Shape(v.shape.begin(), v.shape.end() - 2) &&
+      tcx_hip_flash_attention_supported(features, v.shape.back()) && numel(qb) <= 65535) {
+    Tensor out = make_tensor(DType::kFloat32, shape);
+    ok_or_throw(tcx_hip_flash_attention_f32(f32(q), f32(k), f32(v), static_cast<float*>(out_ptr(out)), numel(qb),
+                                            rows, columns, features, *softmax.attention_scale, op.causal ? 1 : 0,
+                                            s),
+                "HIP attention");
+    return out;
+  }
   if (columns == 0) {  // no keys: every output row is an empty sum
     Tensor zeros;
     zeros.dtype = DType::kFloat32;

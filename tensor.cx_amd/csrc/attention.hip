@@ -1,0 +1,274 @@
+// Fused attention: out = softmax(scale * Q K^T [causal]) V without
+// materialising the scores, on v_mfma_f32_16x16x4_f32.
+//
+// Semantics are those of the reference composite (core/inference.cpp:123-161
+// over backends/cpu/cpu_inference.cpp:22-47) for unmasked and causal
+// attention: a score is dot(q, k) * scale (rounded), a key after the query is
+// -inf under causal, a row with any NaN score is NaN, a row whose maximum is
+// -inf is 0 * V, otherwise exp(s - max) / sum, times V. The sums run in a
+// different order (online softmax over key tiles), inside the reference
+// test's allclose(rtol=2e-4, atol=2e-5).
+//
+// Layout. A block owns 64 queries of one batch matrix (4 waves x 16) and walks
+// the keys in tiles of 64, staged through padded LDS with a register prefetch
+// of the next tile. Each wave computes S^T = K Q^T for its 16 queries, so lane
+// l holds S^T[key 16b + 4(l/16) + v][query l%16] (output layout of the MFMA):
+// those are exactly the A operands (P[query l%16][key]) that the P V MFMAs
+// need, when the k index of step (b, v) is taken as key 16b + 4(l/16) + v. The
+// feature sum of S^T uses the same trick: lane l supplies features
+// 16t + 4(l/16) + e of K and Q at step (t, e), read as one float4 each.
+// Masked keys keep p = 0, so a non-finite V propagates as in the reference's
+// P @ V: tiles the causal mask only partly covers run in full; a tile wholly
+// after the block's last query skips the MFMAs and only marks the feature
+// columns where its V rows hold a non-finite value (0 * inf or 0 * NaN is NaN
+// in every output row of the block). Blocks start with the longest query
+// tiles under causal masking.
+
+#include "common.hpp"
+
+namespace tcx {
+namespace {
+
+constexpr int kQTile = 64;  // queries per block (16 per wave)
+constexpr int kKTile = 64;  // keys per tile
+constexpr int kPad = 4;     // LDS row padding (floats)
+
+using mfma_acc = float __attribute__((ext_vector_type(4)));
+
+struct FlashArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  float* out;
+  std::int64_t rows, cols;
+  float scale;
+  int causal;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void flash_attention_kernel(
+    FlashArgs a) {
+  constexpr int kLd = D + kPad;
+  constexpr int kT = D / 16;                    // float4 groups of features per lane
+  constexpr int kLoads = kKTile * D / 4 / 256;  // float4 per thread per K (or V) tile
+  static_assert(D % 16 == 0 && kLoads >= 1);
+  __shared__ float ks[kKTile * kLd];
+  __shared__ float vs[kKTile * kLd];
+  __shared__ int bad_column[D];  // a wholly masked tile had a non-finite V here
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;  // MFMA row / k-group of this lane
+  const std::int64_t batch = blockIdx.y;
+  // Under causal masking the last query tiles see the most keys: start them first.
+  const std::int64_t qtile = a.causal ? gridDim.x - 1 - blockIdx.x : blockIdx.x;
+  const std::int64_t q0 = qtile * kQTile + wave * 16;
+  const std::int64_t q_last = min(qtile * kQTile + kQTile, a.rows) - 1;  // the block's last query
+  for (int d = tid; d < D; d += 256) bad_column[d] = 0;
+  const float* __restrict__ qb = a.q + batch * a.rows * D;
+  const float* __restrict__ kb = a.k + batch * a.cols * D;
+  const float* __restrict__ vb = a.v + batch * a.cols * D;
+
+  // Q fragment: features 16t + 4g .. +3 of query q0 + r.
+  float4_t qf[kT];
+  {
+    const std::int64_t qrow = q0 + r;
+#pragma unroll
+    for (int t = 0; t < kT; ++t) {
+      qf[t] = float4_t{0.F, 0.F, 0.F, 0.F};
+      if (qrow < a.rows) qf[t] = *reinterpret_cast<const float4_t*>(qb + qrow * D + 16 * t + 4 * g);
+    }
+  }
+
+  mfma_acc o[kT];
+#pragma unroll
+  for (int t = 0; t < kT; ++t) o[t] = mfma_acc{0.F, 0.F, 0.F, 0.F};
+  const float neg_inf = -__builtin_inff();
+  float m = neg_inf, l = 0.F;
+  bool nan_row = false;
+  const std::int64_t query = q0 + r;  // the query whose statistics this lane keeps
+
+  // Tile staging: thread tid moves float4 f = tid + 256 i (row f / (D/4)).
+  float4_t kr[kLoads], vr[kLoads];
+  auto fetch = [&](std::int64_t j0) {
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int f = tid + 256 * i;
+      const std::int64_t row = j0 + f / (D / 4);
+      const int c = (f % (D / 4)) * 4;
+      kr[i] = float4_t{0.F, 0.F, 0.F, 0.F};
+      vr[i] = float4_t{0.F, 0.F, 0.F, 0.F};
+      if (row < a.cols) {
+        kr[i] = *reinterpret_cast<const float4_t*>(kb + row * D + c);
+        vr[i] = *reinterpret_cast<const float4_t*>(vb + row * D + c);
+      }
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int f = tid + 256 * i;
+      const int row = f / (D / 4), c = (f % (D / 4)) * 4;
+      *reinterpret_cast<float4_t*>(&ks[row * kLd + c]) = kr[i];
+      *reinterpret_cast<float4_t*>(&vs[row * kLd + c]) = vr[i];
+    }
+  };
+
+  const std::int64_t tiles = (a.cols + kKTile - 1) / kKTile;
+  // Under causal masking tiles past the block's last query are not run.
+  const std::int64_t run = a.causal ? min(tiles, q_last / kKTile + 1) : tiles;
+  if (run > 0) fetch(0);
+  for (std::int64_t tile = 0; tile < run; ++tile) {
+    const std::int64_t j0 = tile * kKTile;
+    __syncthreads();  // the previous tile's readers are done
+    stage();
+    __syncthreads();
+    if (tile + 1 < run) fetch(j0 + kKTile);
+
+    // S^T for 64 keys (4 blocks of 16) x the wave's 16 queries.
+    mfma_acc s[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      s[b] = mfma_acc{0.F, 0.F, 0.F, 0.F};
+#pragma unroll
+      for (int t = 0; t < kT; ++t) {
+        const float4_t kf = *reinterpret_cast<const float4_t*>(&ks[(16 * b + r) * kLd + 16 * t + 4 * g]);
+        s[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.x, qf[t].x, s[b], 0, 0, 0);
+        s[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.y, qf[t].y, s[b], 0, 0, 0);
+        s[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qf[t].z, s[b], 0, 0, 0);
+        s[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.w, qf[t].w, s[b], 0, 0, 0);
+      }
+    }
+    // Scores, masks and the tile maximum for query `query`.
+    float tmax = neg_inf;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const std::int64_t key = j0 + 16 * b + 4 * g + v;
+        const float product = s[b][v] * a.scale;
+        float sc = product;
+        if (key >= a.cols || (a.causal && key > query)) sc = neg_inf;
+        if (is_nan(sc)) nan_row = true;
+        s[b][v] = sc;
+        tmax = fmaxf(tmax, sc);  // NaN never wins fmaxf; NaN rows are flagged
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+    const float m_new = fmaxf(m, tmax);
+    const bool none = m_new == neg_inf;  // every key so far masked: p = 0
+    const float alpha = none ? 1.F : exp_softmax(m - m_new);
+    float psum = 0.F;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float p = none ? 0.F : exp_softmax(s[b][v] - m_new);
+        s[b][v] = p;
+        psum += p;
+      }
+    psum += __shfl_xor(psum, 16, kWave);
+    psum += __shfl_xor(psum, 32, kWave);
+    l = l * alpha + psum;
+    m = m_new;
+    // Rescale the output rows: lane l holds queries 4g + v of the tile.
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float av = __shfl(alpha, 4 * g + v, kWave);
+#pragma unroll
+      for (int t = 0; t < kT; ++t) o[t][v] *= av;
+    }
+    // O += P V: step (b, v) sums key 16b + 4g + v of lane group g.
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float* vrow = &vs[(16 * b + 4 * g + v) * kLd + r];
+#pragma unroll
+        for (int t = 0; t < kT; ++t)
+          o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(s[b][v], vrow[16 * t], o[t], 0, 0, 0);
+      }
+  }
+
+  // Keys after every query of the block (p = 0): only a non-finite V there
+  // changes the result. Thread tid always covers features 4 (tid % (D/4)) .. +3.
+  if (run < tiles) {
+    const int c = (tid % (D / 4)) * 4;
+    bool bad = false;
+    for (std::int64_t row = run * kKTile + tid / (D / 4); row < a.cols; row += 256 / (D / 4)) {
+      const float4_t w = *reinterpret_cast<const float4_t*>(vb + row * D + c);
+      bad = bad || !__builtin_isfinite(w.x) || !__builtin_isfinite(w.y) || !__builtin_isfinite(w.z) ||
+            !__builtin_isfinite(w.w);
+      if (bad) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (!__builtin_isfinite(w[e])) bad_column[c + e] = 1;  // same value from every writer
+      }
+    }
+  }
+  __syncthreads();  // bad_column is complete
+  // Row statistics of the four lanes sharing a query agree; the NaN flag is
+  // combined over them.
+  int nan_bits = nan_row ? 1 : 0;
+  nan_bits |= __shfl_xor(nan_bits, 16, kWave);
+  nan_bits |= __shfl_xor(nan_bits, 32, kWave);
+  float* __restrict__ ob = a.out + batch * a.rows * D;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int src = 4 * g + v;  // lane holding query 4g + v's statistics
+    const float lv = __shfl(l, src, kWave);
+    const float mv = __shfl(m, src, kWave);
+    const int nv = __shfl(nan_bits, src, kWave);
+    const std::int64_t qrow = q0 + 4 * g + v;
+    if (qrow >= a.rows) continue;
+#pragma unroll
+    for (int t = 0; t < kT; ++t) {
+      float y;
+      if (nv || bad_column[16 * t + r]) y = __builtin_nanf("");
+      else if (mv == neg_inf) y = o[t][v] * 0.F;  // 0 * V (NaN if V is not finite)
+      else y = o[t][v] / lv;
+      ob[qrow * D + 16 * t + r] = y;
+    }
+  }
+}
+
+template <int D>
+int launch_flash(const FlashArgs& a, std::int64_t batch, hipStream_t s) {
+  const std::int64_t qtiles = (a.rows + kQTile - 1) / kQTile;
+  if (qtiles > 0x7fffffff || batch > 65535) return fail(TCX_INVALID_ARGUMENT, "attention grid is too large");
+  hipLaunchKernelGGL((flash_attention_kernel<D>), dim3(static_cast<unsigned>(qtiles), static_cast<unsigned>(batch)),
+                     dim3(256), 0, s, a);
+  return check(hipGetLastError(), "flash attention launch");
+}
+
+}  // namespace
+}  // namespace tcx
+
+extern "C" {
+
+int tcx_hip_flash_attention_supported(int64_t features, int64_t value_features) {
+  return features == value_features && (features == 32 || features == 64 || features == 128) ? 1 : 0;
+}
+
+int tcx_hip_flash_attention_f32(const float* q, const float* k, const float* v, float* out, int64_t batch,
+                                int64_t rows, int64_t cols, int64_t features, float scale, int causal,
+                                tcx_stream_t stream) {
+  using namespace tcx;
+  if (batch < 0 || rows < 0 || cols < 0) return fail(TCX_INVALID_ARGUMENT, "attention extents must be non-negative");
+  if (!tcx_hip_flash_attention_supported(features, features))
+    return fail(TCX_INVALID_ARGUMENT, "fused attention supports 32, 64 or 128 features");
+  if (batch == 0 || rows == 0) return TCX_OK;
+  if (q == nullptr || out == nullptr || (cols > 0 && (k == nullptr || v == nullptr)))
+    return fail(TCX_INVALID_ARGUMENT, "attention buffers are null");
+  for (const void* p : {static_cast<const void*>(q), static_cast<const void*>(k), static_cast<const void*>(v),
+                        static_cast<const void*>(out)})
+    if (p != nullptr && (reinterpret_cast<std::uintptr_t>(p) & 15U) != 0)
+      return fail(TCX_INVALID_ARGUMENT, "fused attention buffers must be 16-byte aligned");
+  if (int rc = ready(); rc != TCX_OK) return rc;
+  const FlashArgs a{q, k, v, out, rows, cols, scale, causal != 0};
+  const auto s = static_cast<hipStream_t>(stream);
+  if (features == 32) return launch_flash<32>(a, batch, s);
+  if (features == 64) return launch_flash<64>(a, batch, s);
+  return launch_flash<128>(a, batch, s);
+}
+
+}  // extern "C"

@@ -40,6 +40,20 @@ __device__ __forceinline__ V stream_load(const V* p) {
 #endif
 }
 
+// e^x for softmax arguments (x <= 0): v_exp_f32 of t = x*log2(e) with the
+// rounding error of that product, recovered exactly by an FMA plus the low
+// part of log2(e), applied as a first-order correction. About 2 ulp, against
+// the ~1 ulp of a correctly rounded expf.
+__device__ __forceinline__ float exp_softmax(float x) {
+  constexpr float kLog2e = 1.44269502F;        // float(log2 e)
+  constexpr float kLog2eLo = 1.925963033e-8F;  // log2 e - kLog2e
+  constexpr float kLn2 = 0.693147181F;
+  const float t = x * kLog2e;
+  const float e = __builtin_amdgcn_exp2f(t);
+  const float err = fmaf(x, kLog2e, -t) + x * kLog2eLo;
+  return t >= -125.0F ? fmaf(e, err * kLn2, e) : e;  // underflow, -inf and NaN keep e
+}
+
 // Wave-wide butterfly sums: both partners add the same two operands, so every
 // lane ends with identical bits and the order is fixed for a given layout.
 __device__ __forceinline__ float wave_sum(float v) {

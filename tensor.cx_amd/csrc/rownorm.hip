@@ -44,20 +44,6 @@ __device__ __forceinline__ float wave_max_nan(float v) {
   return v;
 }
 
-// e^x for softmax (x <= 0 there): v_exp_f32 of t = x*log2(e) with the
-// rounding error of that product, recovered exactly by an FMA plus the low
-// part of log2(e), applied as a first-order correction. About 2 ulp, against
-// the ~1 ulp of a correctly rounded expf.
-__device__ __forceinline__ float exp_softmax(float x) {
-  constexpr float kLog2e = 1.44269502F;          // float(log2 e)
-  constexpr float kLog2eLo = 1.925963033e-8F;    // log2 e - kLog2e
-  constexpr float kLn2 = 0.693147181F;
-  const float t = x * kLog2e;
-  const float e = __builtin_amdgcn_exp2f(t);
-  const float err = fmaf(x, kLog2e, -t) + x * kLog2eLo;
-  return t >= -125.0F ? fmaf(e, err * kLn2, e) : e;  // underflow, -inf and NaN keep e
-}
-
 __device__ __forceinline__ float finish_scale_ln(float ssd, std::int64_t n, float eps, bool& nan_row) {
   const float denom = ssd / static_cast<float>(n) + eps;
   nan_row = denom == 0.F;

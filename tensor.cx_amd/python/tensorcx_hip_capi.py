@@ -38,7 +38,7 @@ EXPORTS = [
     "tcx_hip_reduce_axes", "tcx_hip_softmax_f32", "tcx_hip_rmsnorm_f32", "tcx_hip_layernorm_f32",
     "tcx_hip_bias_act_f32", "tcx_hip_unary_f32", "tcx_hip_binary", "tcx_hip_fill",
     "tcx_hip_math_unary", "tcx_hip_clip", "tcx_hip_topk", "tcx_hip_embedding_f32",
-    "tcx_hip_attention_softmax_f32",
+    "tcx_hip_attention_softmax_f32", "tcx_hip_flash_attention_supported", "tcx_hip_flash_attention_f32",
 ]
 
 
@@ -129,6 +129,9 @@ def lib() -> ctypes.CDLL:
         L.tcx_hip_binary.argtypes = [ctypes.c_int, ctypes.c_int, vp, vp, vp, ctypes.c_int32, vp, vp,
                                      vp, vp]
         L.tcx_hip_fill.argtypes = [ctypes.c_int, vp, i64, ctypes.c_double, vp]
+        L.tcx_hip_flash_attention_supported.argtypes = [i64, i64]
+        L.tcx_hip_flash_attention_f32.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, ctypes.c_float,
+                                                  ctypes.c_int, vp]
         _LIB = L
     return _LIB
 
@@ -291,3 +294,10 @@ def layernorm(x: int, gamma: int | None, beta: int | None, out: int, outer, redu
 
 def bias_act(x: int, bias: int | None, out: int, rows: int, cols: int, activation="none", s=None) -> None:
     check(lib().tcx_hip_bias_act_f32(x, bias, out, rows, cols, ACT[activation], s or stream()), "bias_act")
+
+
+def flash_attention(q, k, v, out, batch: int, rows: int, cols: int, features: int, scale: float,
+                    causal: bool, stream_=None):
+    """Fused attention on device pointers (tcx_hip_flash_attention_f32)."""
+    check(lib().tcx_hip_flash_attention_f32(q, k, v, out, batch, rows, cols, features, scale, int(causal),
+                                            stream_ or stream()), "flash_attention")

@@ -62,3 +62,21 @@ def mlp_inputs():
     w2 = np.random.default_rng(9).uniform(-math.sqrt(6 / 4096), math.sqrt(6 / 4096),
                                           (1024, 4096)).astype(np.float32)
     return x, w1, np.zeros(4096, np.float32), w2, np.zeros(1024, np.float32)
+
+
+ATTENTION = {"batch_heads": 16, "seq": 2048, "features": 128}
+
+
+def attention_inputs():
+    """Attention bench: q, k, v [16, 2048, 128] ~ N(0,1), seeds 10/11/12 (16 batch-heads of
+    2048 tokens, head dimension 128)."""
+    shape = (ATTENTION["batch_heads"], ATTENTION["seq"], ATTENTION["features"])
+    return tuple(np.random.default_rng(seed).standard_normal(shape).astype(np.float32) for seed in (10, 11, 12))
+
+
+def attention_flops(causal: bool = False) -> int:
+    """Q K^T and P V: 2 * 2 * batch_heads * features * (query, key) pairs, counting only the
+    seq * (seq + 1) / 2 pairs a causal mask keeps."""
+    a = ATTENTION
+    pairs = a["seq"] * (a["seq"] + 1) // 2 if causal else a["seq"] ** 2
+    return 4 * a["batch_heads"] * pairs * a["features"]

@@ -335,3 +335,31 @@ def test_inference_pipeline(cx):
     a = oracle.attention(p, p, p, None, True)
     expected = oracle.linear(oracle.affine_norm(a, -1, 1e-5, gain, shift), weight)
     assert_close(output.numpy(), expected, 2e-4, 2e-5, "pipeline")
+
+
+# ------------------------------------------------------------- fused attention
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (64, 64), (65, 130), (200, 37), (5, 0), (3, 257)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_fused_attention(cx, d, rows, cols, causal):
+    # Unmasked attention over matching batches takes the fused kernel.
+    q, k, v = f32((2, 3, rows, d), 1), f32((2, 3, cols, d), 2), f32((2, 3, cols, d), 3)
+    attention_check(cx, q, k, v, None, causal)
+    attention_check(cx, q, k, v, None, causal, scale=0.05)
+
+
+def test_fused_attention_special_values(cx):
+    q, k, v = f32((1, 70, 64), 4), f32((1, 90, 64), 5), f32((1, 90, 64), 6)
+    q[0, 3, 7] = np.nan            # a NaN query: its row is NaN
+    k[0, 11] = np.inf              # an infinite key: +inf / NaN scores
+    k[0, 12] = -np.inf
+    v[0, 80, 5] = np.nan           # a NaN value behind the causal mask of early queries
+    with np.errstate(all="ignore"):
+        for causal in (False, True):
+            attention_check(cx, q, k, v, None, causal)
+    # All scores -inf for one query: 0 * V.
+    q2, k2, v2 = np.ones((1, 2, 32), np.float32), np.ones((1, 3, 32), np.float32), f32((1, 3, 32), 7)
+    q2[0, 1] = -np.inf
+    k2[0, :, :] = 1.0
+    with np.errstate(all="ignore"):
+        attention_check(cx, q2, k2, v2)
