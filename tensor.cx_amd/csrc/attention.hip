@@ -16,7 +16,9 @@
 // those are exactly the A operands (P[query l%16][key]) that the P V MFMAs
 // need, when the k index of step (b, v) is taken as key 16b + 4(l/16) + v. The
 // feature sum of S^T uses the same trick: lane l supplies features
-// 16t + 4(l/16) + e of K and Q at step (t, e), read as one float4 each.
+// 16t + 4(l/16) + e of K and Q at step (t, e), read as one float4 each. The
+// output tile t holds features kT*j + t in its column j (kT = D/16 tiles), so
+// a lane reads its V operands, and writes its outputs, as kT contiguous floats.
 // Masked keys keep p = 0, so a non-finite V propagates as in the reference's
 // P @ V: tiles the causal mask only partly covers run in full; a tile wholly
 // after the block's last query skips the MFMAs and only marks the feature
@@ -45,6 +47,40 @@ struct FlashArgs {
   int causal;
 };
 
+using float2_t = float __attribute__((ext_vector_type(2)));
+
+// N contiguous floats (N = 2, 4 or 8) with 8- or 16-byte accesses.
+template <int N>
+__device__ __forceinline__ void load_row(const float* p, float (&v)[N]) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int t = 0; t < N; t += 4) {
+      const float4_t w = *reinterpret_cast<const float4_t*>(p + t);
+      v[t] = w.x;
+      v[t + 1] = w.y;
+      v[t + 2] = w.z;
+      v[t + 3] = w.w;
+    }
+  } else {
+    static_assert(N == 2);
+    const float2_t w = *reinterpret_cast<const float2_t*>(p);
+    v[0] = w.x;
+    v[1] = w.y;
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void store_row(float* p, const float (&v)[N]) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int t = 0; t < N; t += 4)
+      *reinterpret_cast<float4_t*>(p + t) = float4_t{v[t], v[t + 1], v[t + 2], v[t + 3]};
+  } else {
+    static_assert(N == 2);
+    *reinterpret_cast<float2_t*>(p) = float2_t{v[0], v[1]};
+  }
+}
+
 template <int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void flash_attention_kernel(
     FlashArgs a) {
@@ -58,9 +94,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, g = lane >> 4;  // MFMA row / k-group of this lane
-  const std::int64_t batch = blockIdx.y;
-  // Under causal masking the last query tiles see the most keys: start them first.
-  const std::int64_t qtile = a.causal ? gridDim.x - 1 - blockIdx.x : blockIdx.x;
+  // Under causal masking the last query tiles see the most keys. Work items
+  // are ranked by their key-tile count; the first half of the grid takes them
+  // heaviest first and the second half lightest first, so the two blocks that
+  // share a CU (launch ids L and L + grid/2) carry about the same total work.
+  std::int64_t batch = blockIdx.y, qtile = blockIdx.x;
+  if (a.causal) {
+    const std::int64_t n = static_cast<std::int64_t>(gridDim.x) * gridDim.y;
+    const std::int64_t id = static_cast<std::int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
+    const std::int64_t half = (n + 1) / 2;
+    const std::int64_t rank = id < half ? id : n - 1 - (id - half);
+    qtile = gridDim.x - 1 - rank / gridDim.y;
+    batch = rank % gridDim.y;
+  }
   const std::int64_t q0 = qtile * kQTile + wave * 16;
   const std::int64_t q_last = min(qtile * kQTile + kQTile, a.rows) - 1;  // the block's last query
   for (int d = tid; d < D; d += 256) bad_column[d] = 0;
@@ -124,30 +170,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     __syncthreads();
     if (tile + 1 < run) fetch(j0 + kKTile);
 
-    // S^T for 64 keys (4 blocks of 16) x the wave's 16 queries.
+    // S^T for 64 keys (4 blocks of 16) x the wave's 16 queries. The four
+    // block accumulators take turns, so consecutive MFMAs are independent.
     mfma_acc s[4];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      s[b] = mfma_acc{0.F, 0.F, 0.F, 0.F};
+    for (int b = 0; b < 4; ++b) s[b] = mfma_acc{0.F, 0.F, 0.F, 0.F};
 #pragma unroll
-      for (int t = 0; t < kT; ++t) {
-        const float4_t kf = *reinterpret_cast<const float4_t*>(&ks[(16 * b + r) * kLd + 16 * t + 4 * g]);
-        s[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.x, qf[t].x, s[b], 0, 0, 0);
-        s[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.y, qf[t].y, s[b], 0, 0, 0);
-        s[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qf[t].z, s[b], 0, 0, 0);
-        s[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.w, qf[t].w, s[b], 0, 0, 0);
-      }
+    for (int t = 0; t < kT; ++t) {
+      float4_t kf[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        kf[b] = *reinterpret_cast<const float4_t*>(&ks[(16 * b + r) * kLd + 16 * t + 4 * g]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) s[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[b][e], qf[t][e], s[b], 0, 0, 0);
     }
-    // Scores, masks and the tile maximum for query `query`.
+    // Scores, masks and the tile maximum for query `query`: key j0 + kk is
+    // kept when kk < limit (inside the sequence, and not after the query).
+    std::int64_t lim = a.cols - j0;
+    if (a.causal) lim = min(lim, query - j0 + 1);
+    const int limit = static_cast<int>(max<std::int64_t>(min<std::int64_t>(lim, kKTile), 0));
     float tmax = neg_inf;
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const std::int64_t key = j0 + 16 * b + 4 * g + v;
         const float product = s[b][v] * a.scale;
         float sc = product;
-        if (key >= a.cols || (a.causal && key > query)) sc = neg_inf;
+        if (16 * b + 4 * g + v >= limit) sc = neg_inf;
         if (is_nan(sc)) nan_row = true;
         s[b][v] = sc;
         tmax = fmaxf(tmax, sc);  // NaN never wins fmaxf; NaN rows are flagged
@@ -177,15 +228,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 #pragma unroll
       for (int t = 0; t < kT; ++t) o[t][v] *= av;
     }
-    // O += P V: step (b, v) sums key 16b + 4g + v of lane group g.
+    // O += P V: step (b, v) sums key 16b + 4g + v of lane group g; tile t
+    // takes feature kT*r + t, so the lane's V operands are contiguous.
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float* vrow = &vs[(16 * b + 4 * g + v) * kLd + r];
+        const float* vrow = &vs[(16 * b + 4 * g + v) * kLd + kT * r];
+        float vv[kT];
+        load_row<kT>(vrow, vv);
 #pragma unroll
-        for (int t = 0; t < kT; ++t)
-          o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(s[b][v], vrow[16 * t], o[t], 0, 0, 0);
+        for (int t = 0; t < kT; ++t) o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(s[b][v], vv[t], o[t], 0, 0, 0);
       }
   }
 
@@ -220,14 +273,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     const int nv = __shfl(nan_bits, src, kWave);
     const std::int64_t qrow = q0 + 4 * g + v;
     if (qrow >= a.rows) continue;
+    float y[kT];
 #pragma unroll
     for (int t = 0; t < kT; ++t) {
-      float y;
-      if (nv || bad_column[16 * t + r]) y = __builtin_nanf("");
-      else if (mv == neg_inf) y = o[t][v] * 0.F;  // 0 * V (NaN if V is not finite)
-      else y = o[t][v] / lv;
-      ob[qrow * D + 16 * t + r] = y;
+      if (nv || bad_column[kT * r + t]) y[t] = __builtin_nanf("");
+      else if (mv == neg_inf) y[t] = o[t][v] * 0.F;  // 0 * V (NaN if V is not finite)
+      else y[t] = o[t][v] / lv;
     }
+    store_row<kT>(ob + qrow * D + kT * r, y);
   }
 }
 
