@@ -9,7 +9,7 @@
 // different order (online softmax over key tiles), inside the reference
 // test's allclose(rtol=2e-4, atol=2e-5).
 //
-// Layout. A block owns 64 queries of one batch matrix (4 waves x 16) and walks
+// Layout. A block owns 16 queries per wave of one batch matrix and walks
 // the keys in tiles of 64, staged through padded LDS with a register prefetch
 // of the next tile. Each wave computes S^T = K Q^T for its 16 queries, so lane
 // l holds S^T[key 16b + 4(l/16) + v][query l%16] (output layout of the MFMA):
@@ -31,8 +31,13 @@
 namespace tcx {
 namespace {
 
-constexpr int kQTile = 64;  // queries per block (16 per wave)
 constexpr int kKTile = 64;  // keys per tile
+// Waves per block (16 queries each), measured on MI355X at 16 x 2048 x 128:
+// 8 waves share each K/V tile over 128 queries (97 TFLOP/s unmasked against 93
+// with 4); causal runs use 4, so twice as many blocks let the balanced block
+// order pair long and short query tiles on each CU (78 against 53 TFLOP/s).
+constexpr int kWavesFull = 8;
+constexpr int kWavesCausal = 4;
 constexpr int kPad = 4;     // LDS row padding (floats)
 
 using mfma_acc = float __attribute__((ext_vector_type(4)));
@@ -81,12 +86,14 @@ __device__ __forceinline__ void store_row(float* p, const float (&v)[N]) {
   }
 }
 
-template <int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void flash_attention_kernel(
+template <int D, int kWaves>
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 8))) void flash_attention_kernel(
     FlashArgs a) {
+  constexpr int kThreads = 64 * kWaves;
+  constexpr int kQTile = 16 * kWaves;  // queries per block (16 per wave)
   constexpr int kLd = D + kPad;
   constexpr int kT = D / 16;                    // float4 groups of features per lane
-  constexpr int kLoads = kKTile * D / 4 / 256;  // float4 per thread per K (or V) tile
+  constexpr int kLoads = kKTile * D / 4 / kThreads;  // float4 per thread per K (or V) tile
   static_assert(D % 16 == 0 && kLoads >= 1);
   __shared__ float ks[kKTile * kLd];
   __shared__ float vs[kKTile * kLd];
@@ -109,7 +116,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   }
   const std::int64_t q0 = qtile * kQTile + wave * 16;
   const std::int64_t q_last = min(qtile * kQTile + kQTile, a.rows) - 1;  // the block's last query
-  for (int d = tid; d < D; d += 256) bad_column[d] = 0;
+  for (int d = tid; d < D; d += kThreads) bad_column[d] = 0;
   const float* __restrict__ qb = a.q + batch * a.rows * D;
   const float* __restrict__ kb = a.k + batch * a.cols * D;
   const float* __restrict__ vb = a.v + batch * a.cols * D;
@@ -133,12 +140,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   bool nan_row = false;
   const std::int64_t query = q0 + r;  // the query whose statistics this lane keeps
 
-  // Tile staging: thread tid moves float4 f = tid + 256 i (row f / (D/4)).
+  // Tile staging: thread tid moves float4 f = tid + kThreads i (row f / (D/4)).
   float4_t kr[kLoads], vr[kLoads];
   auto fetch = [&](std::int64_t j0) {
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
-      const int f = tid + 256 * i;
+      const int f = tid + kThreads * i;
       const std::int64_t row = j0 + f / (D / 4);
       const int c = (f % (D / 4)) * 4;
       kr[i] = float4_t{0.F, 0.F, 0.F, 0.F};
@@ -152,7 +159,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   auto stage = [&]() {
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
-      const int f = tid + 256 * i;
+      const int f = tid + kThreads * i;
       const int row = f / (D / 4), c = (f % (D / 4)) * 4;
       *reinterpret_cast<float4_t*>(&ks[row * kLd + c]) = kr[i];
       *reinterpret_cast<float4_t*>(&vs[row * kLd + c]) = vr[i];
@@ -243,11 +250,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   }
 
   // Keys after every query of the block (p = 0): only a non-finite V there
-  // changes the result. Thread tid always covers features 4 (tid % (D/4)) .. +3.
+  // changes the result. Thread tid always covers features 4 (tid % (D/4)) .. +3
+  // (kThreads is a multiple of D/4).
   if (run < tiles) {
     const int c = (tid % (D / 4)) * 4;
     bool bad = false;
-    for (std::int64_t row = run * kKTile + tid / (D / 4); row < a.cols; row += 256 / (D / 4)) {
+    for (std::int64_t row = run * kKTile + tid / (D / 4); row < a.cols; row += kThreads / (D / 4)) {
       const float4_t w = *reinterpret_cast<const float4_t*>(vb + row * D + c);
       bad = bad || !__builtin_isfinite(w.x) || !__builtin_isfinite(w.y) || !__builtin_isfinite(w.z) ||
             !__builtin_isfinite(w.w);
@@ -284,12 +292,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   }
 }
 
-template <int D>
+template <int D, int kWaves>
 int launch_flash(const FlashArgs& a, std::int64_t batch, hipStream_t s) {
+  constexpr int kQTile = 16 * kWaves;
   const std::int64_t qtiles = (a.rows + kQTile - 1) / kQTile;
   if (qtiles > 0x7fffffff || batch > 65535) return fail(TCX_INVALID_ARGUMENT, "attention grid is too large");
-  hipLaunchKernelGGL((flash_attention_kernel<D>), dim3(static_cast<unsigned>(qtiles), static_cast<unsigned>(batch)),
-                     dim3(256), 0, s, a);
+  hipLaunchKernelGGL((flash_attention_kernel<D, kWaves>),
+                     dim3(static_cast<unsigned>(qtiles), static_cast<unsigned>(batch)), dim3(64 * kWaves), 0, s, a);
   return check(hipGetLastError(), "flash attention launch");
 }
 
@@ -319,9 +328,14 @@ int tcx_hip_flash_attention_f32(const float* q, const float* k, const float* v, 
   if (int rc = ready(); rc != TCX_OK) return rc;
   const FlashArgs a{q, k, v, out, rows, cols, scale, causal != 0};
   const auto s = static_cast<hipStream_t>(stream);
-  if (features == 32) return launch_flash<32>(a, batch, s);
-  if (features == 64) return launch_flash<64>(a, batch, s);
-  return launch_flash<128>(a, batch, s);
+  if (a.causal) {
+    if (features == 32) return launch_flash<32, kWavesCausal>(a, batch, s);
+    if (features == 64) return launch_flash<64, kWavesCausal>(a, batch, s);
+    return launch_flash<128, kWavesCausal>(a, batch, s);
+  }
+  if (features == 32) return launch_flash<32, kWavesFull>(a, batch, s);
+  if (features == 64) return launch_flash<64, kWavesFull>(a, batch, s);
+  return launch_flash<128, kWavesFull>(a, batch, s);
 }
 
 }  // extern "C"
