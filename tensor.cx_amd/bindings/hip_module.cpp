@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "tensorcx/backends/hip/hip_backend.h"
+#include "tensorcx/core/profiling.h"
 
 namespace py = pybind11;
 using namespace tensorcx;
@@ -326,6 +327,57 @@ PYBIND11_MODULE(_core, m) {
     if (mask && *mask) in.push_back((*mask)->tensor);
     return run(op, std::move(in));
   }, py::arg("scores"), py::arg("mask"), py::arg("shape"), py::arg("causal") = false, py::arg("scale") = py::none());
+
+  // Runtime profiling sessions (the reference's _profile_begin/_profile_end).
+  m.def("_profile_begin", [](std::int64_t max_events, bool device_timing) {
+    if (max_events < 1 || max_events > 100000) throw py::value_error("max_events must be an integer in [1, 100000]");
+    try {
+      return begin_profile(static_cast<std::size_t>(max_events), device_timing);
+    } catch (const std::invalid_argument& error) {
+      throw py::value_error(error.what());
+    }
+  });
+  m.def("_profile_end", [](std::uint64_t token) {
+    const ProfileResult r = end_profile(token);
+    auto op_name = [](const std::optional<OpKind>& op) -> py::object {
+      return op ? py::object(py::str(profile_operation_name(*op))) : py::object(py::none());
+    };
+    py::list events;
+    for (const ProfileEvent& e : r.events) {
+      py::dict d;
+      d["id"] = e.id;
+      d["parent_id"] = e.parent_id;
+      d["start_ns"] = e.start_ns;
+      d["duration_ns"] = e.duration_ns;
+      d["self_ns"] = e.self_ns;
+      d["category"] = profile_category_name(e.category);
+      d["name"] = e.name;
+      d["backend"] = e.backend;
+      d["bytes"] = e.bytes ? py::object(py::int_(*e.bytes)) : py::object(py::none());
+      d["operation"] = op_name(e.operation);
+      events.append(d);
+    }
+    py::list device_events;
+    for (const auto& e : r.device_events) {
+      py::dict d;
+      d["id"] = e.id;
+      d["host_event_id"] = e.host_event_id;
+      d["name"] = e.name;
+      d["backend"] = e.backend;
+      d["operation"] = op_name(e.operation);
+      d["elapsed_ms"] = e.elapsed_ms ? py::object(py::float_(*e.elapsed_ms)) : py::object(py::none());
+      d["error"] = e.error ? py::object(py::str(e.error)) : py::object(py::none());
+      device_events.append(d);
+    }
+    py::dict out;
+    out["elapsed_ns"] = r.elapsed_ns;
+    out["dropped_events"] = r.dropped_events;
+    out["events"] = events;
+    out["device_timing"] = r.device_timing;
+    out["dropped_device_events"] = r.dropped_device_events;
+    out["device_events"] = device_events;
+    return out;
+  });
 
   py::class_<PoolHandle>(m, "MemoryPool")
       .def(py::init<std::size_t, std::size_t>(), py::arg("max_cached_bytes"), py::arg("max_cached_blocks") = 64)

@@ -4,6 +4,8 @@
 
 #include "tensorcx/backends/hip/hip_backend.h"
 
+#include "tensorcx/core/profiling.h"
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -41,6 +43,11 @@ tcx_stream_t stream() {
   tcx_stream_t s = nullptr;
   ok_or_throw(tcx_hip_stream(&s), "HIP stream");
   return s;
+}
+
+void synchronize(tcx_stream_t s) {
+  ProfileScope span(ProfileCategory::kSynchronize, "stream_synchronize", "hip");
+  ok_or_throw(tcx_hip_stream_synchronize(s), "HIP execution");
 }
 
 int tcx_dtype(DType dtype) {
@@ -794,7 +801,7 @@ Status execute_builtin_kernel(const BackendExecution& e) {
   } else {
     return Status(StatusCode::kInvalidArgument, "unknown HIP built-in kernel entry point");
   }
-  ok_or_throw(tcx_hip_stream_synchronize(s), "HIP kernel");
+  synchronize(s);
   return Status::Ok();
 }
 
@@ -802,6 +809,7 @@ Status execute_builtin_kernel(const BackendExecution& e) {
 
 // ------------------------------------------------------------ public API
 Expected<std::shared_ptr<HipBuffer>> HipBuffer::create(std::size_t bytes) {
+  ProfileScope span(ProfileCategory::kAllocation, "hip_allocate", "hip", bytes);
   std::shared_ptr<HipBuffer> buffer(new HipBuffer());
   const int rc = tcx_hip_allocate(bytes, &buffer->data_, &buffer->owner_);
   if (rc != TCX_OK) return status_from_code(rc, "HIP allocation");
@@ -809,7 +817,10 @@ Expected<std::shared_ptr<HipBuffer>> HipBuffer::create(std::size_t bytes) {
   return buffer;
 }
 
-HipBuffer::~HipBuffer() { tcx_hip_release(data_, bytes_, owner_); }
+HipBuffer::~HipBuffer() {
+  ProfileScope span(ProfileCategory::kDeallocation, "hip_release", "hip", bytes_);
+  tcx_hip_release(data_, bytes_, owner_);
+}
 
 bool available() { return tcx_hip_init() == TCX_OK; }
 
@@ -860,6 +871,7 @@ Expected<Tensor> from_host(const void* host, DType dtype, Shape shape) {
   Tensor t = created.move_value();
   const std::size_t bytes = t.buffer->nbytes();
   if (bytes) {
+    ProfileScope span(ProfileCategory::kCopy, "host_to_device", "hip", bytes);
     tcx_stream_t s = nullptr;
     int rc = tcx_hip_stream(&s);
     if (rc == TCX_OK) rc = tcx_hip_memcpy_h2d(out_ptr(t), host, bytes, s);
@@ -874,6 +886,7 @@ Status to_host(const Tensor& tensor, void* host, std::size_t bytes) {
     const auto need = static_cast<std::size_t>(numel(tensor.shape)) * dtype_size(tensor.dtype);
     if (bytes != need) return Status(StatusCode::kInvalidArgument, "host buffer size does not match the tensor");
     if (need == 0) return Status::Ok();
+    ProfileScope span(ProfileCategory::kCopy, "device_to_host", "hip", need);
     tcx_stream_t s = nullptr;
     int rc = tcx_hip_stream(&s);
     if (rc == TCX_OK) rc = tcx_hip_memcpy_d2h(host, src, need, s);
@@ -902,7 +915,51 @@ Expected<Tensor> clone(const Tensor& tensor) {
   }
 }
 
+namespace {
+
+// One device interval per executed operation: HIP events recorded on the
+// execution stream before the first and after the last launch, read after the
+// synchronising wait that ends every execute (the reference's DeviceTimer
+// pattern, backends/cuda/cuda_profiling.h:22-77).
+class DeviceInterval {
+ public:
+  DeviceInterval(const char* name, tcx_stream_t stream) noexcept : token_(reserve_device_profile(name, "hip")) {
+    if (!token_) return;
+    if (tcx_hip_event_create(&start_) != TCX_OK || tcx_hip_event_create(&stop_) != TCX_OK ||
+        tcx_hip_event_record(start_, stream) != TCX_OK)
+      error_ = "event_failed";
+  }
+  void stop(tcx_stream_t stream) noexcept {
+    if (token_ && !error_ && tcx_hip_event_record(stop_, stream) != TCX_OK) error_ = "event_failed";
+    stopped_ = true;
+  }
+  ~DeviceInterval() {
+    if (token_) {
+      float ms = 0.F;
+      const char* error = error_ ? error_ : !stopped_ ? "launch_failed" : nullptr;
+      if (!error && (tcx_hip_event_synchronize(stop_) != TCX_OK || tcx_hip_event_elapsed_ms(start_, stop_, &ms) != TCX_OK))
+        error = "event_failed";
+      finish_device_profile(token_, error ? std::nullopt : std::optional<float>(ms), error);
+    }
+    if (start_) tcx_hip_event_destroy(start_);
+    if (stop_) tcx_hip_event_destroy(stop_);
+  }
+  DeviceInterval(const DeviceInterval&) = delete;
+  DeviceInterval& operator=(const DeviceInterval&) = delete;
+
+ private:
+  DeviceProfileToken token_;
+  void* start_{};
+  void* stop_{};
+  const char* error_{};
+  bool stopped_{};
+};
+
+}  // namespace
+
 Status HipBackend::execute(const BackendExecution& e) {
+  ProfileScope dispatch(ProfileCategory::kDispatch, "execute", "hip", std::nullopt,
+                        e.op_class == BackendOpClass::kPrimitive ? std::optional<OpKind>(e.op.kind) : std::nullopt);
   try {
     if (e.op_class == BackendOpClass::kKernel) return execute_builtin_kernel(e);
     if (Status contract = validate_primitive_execution_contract(e, "hip"); !contract.ok()) return contract;
@@ -912,6 +969,7 @@ Status HipBackend::execute(const BackendExecution& e) {
     if (e.op.kind != OpKind::kFill)
       for (const Tensor& t : e.inputs) (void)device_ptr(t);
     const tcx_stream_t s = stream();
+    DeviceInterval interval("hip_kernels", s);
     Tensor result;
     switch (e.op.kind) {
       case OpKind::kFill: result = fill(e.outputs[0], e.op.scalar_value, s); break;
@@ -940,7 +998,8 @@ Status HipBackend::execute(const BackendExecution& e) {
       case OpKind::kClip: result = clip(e.inputs, s); break;
       case OpKind::kTopK: {
         auto [values, indices] = topk(e.op, e.inputs[0], s);
-        ok_or_throw(tcx_hip_stream_synchronize(s), "HIP execution");
+        interval.stop(s);
+        synchronize(s);
         e.outputs[0] = std::move(values);
         e.outputs[1] = std::move(indices);
         return Status::Ok();
@@ -951,7 +1010,8 @@ Status HipBackend::execute(const BackendExecution& e) {
       default:
         return Status(StatusCode::kInvalidArgument, "unsupported HIP backend execution operation");
     }
-    ok_or_throw(tcx_hip_stream_synchronize(s), "HIP execution");
+    interval.stop(s);
+    synchronize(s);
     e.outputs[0] = std::move(result);  // publish only after the work completed
     return Status::Ok();
   } catch (const std::invalid_argument& error) {

@@ -271,7 +271,7 @@ def test_concurrent_threads(cx):
 
 
 def test_memory_pool_reuse(cx):
-    with cx.memory_pool(64 << 20, 8) as pool:
+    with cx.memory_pool("hip", max_cached_bytes=64 << 20, max_cached_blocks=8) as pool:
         x = cx.tensor(np.ones((256, 256), np.float32), device="hip")
         for _ in range(3):
             y = cx.softmax(x, 1)
