@@ -225,6 +225,82 @@ int tcx_hip_binary(int op, int dtype, const void* lhs, const void* rhs, void* ou
 /* kFill (cpu_backend.cpp fill): float32, int32 or bool (value != 0) into n elements. */
 int tcx_hip_fill(int dtype, void* out, int64_t n, double value, tcx_stream_t stream);
 
+/* ---- data movement and conversion (replaces the CUDA executor paths of
+ * reference backends/cuda/kernels/elementwise.cu; semantics of
+ * backends/cpu/cpu_backend.cpp:801-930) ---- */
+
+/* kTranspose / kSlice (make_transpose_plan, make_slice_plan, shape.cpp:87-200):
+ * out (contiguous over out_shape) [i] = in[offset + sum_a idx_a(i) * in_strides[a]],
+ * bit for bit, for 1- or 4-byte elements. */
+int tcx_hip_gather_strided(int elem_bytes, const void* in, void* out, int32_t rank, const int64_t* out_shape,
+                           const int64_t* in_strides, int64_t offset, tcx_stream_t stream);
+/* One kConcat input (cpu_backend.cpp:317-339): a contiguous [outer, block]
+ * input copied into out at out[o * out_block + dst_offset + j]. */
+int tcx_hip_copy_blocks(int elem_bytes, const void* in, void* out, int64_t outer, int64_t block, int64_t out_block,
+                        int64_t dst_offset, tcx_stream_t stream);
+/* kCast (cpu_backend.cpp:834-876) between TCX_FLOAT32 / TCX_INT32 / TCX_BOOL:
+ * to/from bool tests value != 0; float32 -> int32 truncates toward zero after
+ * every value was checked finite and inside [-2^31, 2^31) (else
+ * TCX_INVALID_ARGUMENT; `flag` is one device int32 of scratch and the stream
+ * is synchronised for that check); int32 -> float32 rounds to nearest. */
+int tcx_hip_cast(int from_dtype, int to_dtype, const void* in, void* out, int64_t n, int32_t* flag,
+                 tcx_stream_t stream);
+
+#define TCX_SCALAR_NEGATE 0
+#define TCX_SCALAR_ADD 1
+#define TCX_SCALAR_SUBTRACT 2
+#define TCX_SCALAR_MULTIPLY 3
+#define TCX_SCALAR_DIVIDE 4
+/* kNegate and k{Add,Subtract,Multiply,Divide}Scalar (cpu_backend.cpp:878-930):
+ * float32 with the scalar rounded to float32 once, int32 wrapping in uint32
+ * (no division; the scalar must be an int32 integer); scalar_left puts the
+ * scalar on the left. */
+int tcx_hip_scalar_op(int op, int dtype, const void* in, void* out, int64_t n, double scalar, int scalar_left,
+                      tcx_stream_t stream);
+
+/* ---- predicates (replace reference backends/cuda/kernels/predicate.cu;
+ * semantics of backends/cpu/cpu_predicate.cpp) ---- */
+#define TCX_PRED_EQUAL 0
+#define TCX_PRED_NOT_EQUAL 1
+#define TCX_PRED_LESS 2
+#define TCX_PRED_LESS_EQUAL 3
+#define TCX_PRED_GREATER 4
+#define TCX_PRED_GREATER_EQUAL 5
+#define TCX_PRED_LOGICAL_AND 6
+#define TCX_PRED_LOGICAL_OR 7
+#define TCX_PRED_LOGICAL_XOR 8
+#define TCX_PRED_LOGICAL_NOT 9
+#define TCX_PRED_WHERE 10
+#define TCX_PRED_FLAG_INT32 1 /* 4-byte comparisons are int32 (else float32) */
+typedef struct {
+  int64_t shape[TCX_HIP_MAX_RANK];      /* broadcast output shape */
+  int64_t strides[3][TCX_HIP_MAX_RANK]; /* broadcast strides of inputs a, b, c */
+  int32_t rank;
+  int32_t flags;                        /* TCX_PRED_FLAG_* */
+} tcx_hip_broadcast3_t;
+/* make_predicate_plan (core/predicate.cpp:23-44), cpu_predicate.cpp:22-50:
+ * comparisons of a and b (elem_bytes 4: float32 or int32 per flags; 1: bool)
+ * and logical ops of bool a (, b) into bool out; where(a: bool, b, c) copies
+ * the chosen elem_bytes-wide element bit for bit. */
+int tcx_hip_predicate(int op, int elem_bytes, const void* a, const void* b, const void* c, void* out,
+                      const tcx_hip_broadcast3_t* plan, tcx_stream_t stream);
+/* kAny (all == 0) / kAll over make_reduction_plan metadata (core/shape.cpp:
+ * 140-173; cpu_predicate.cpp:52-70): (extent, stride) pairs of `rank` axes,
+ * kept axes first; false / true for an empty selection. */
+int tcx_hip_bool_reduce(int all, const uint8_t* x, uint8_t* out, const int64_t* meta, int32_t rank, int64_t groups,
+                        int64_t reduce, tcx_stream_t stream);
+/* kMaskedSelect (cpu_predicate.cpp:72-96) in two launches around one host
+ * step: tcx_hip_mask_count writes the true entries of each of the
+ * tcx_hip_mask_chunks(n) chunks of the n-entry bool mask; the caller turns
+ * them into exclusive offsets and the total, then tcx_hip_masked_select writes
+ * the selected entry indices (`index`, total int64 of scratch) and copies the
+ * `block`-element rows of `in` they select to `out`, in index order. */
+int64_t tcx_hip_mask_chunks(int64_t n);
+int tcx_hip_mask_count(const uint8_t* mask, int64_t n, int64_t* chunk_counts, tcx_stream_t stream);
+int tcx_hip_masked_select(int elem_bytes, const void* in, const uint8_t* mask, int64_t n, int64_t block,
+                          const int64_t* chunk_offsets, int64_t total, int64_t* index, void* out,
+                          tcx_stream_t stream);
+
 /* ---- math extension (replaces the CUDA math launches of reference
  * backends/cuda/kernels/math.cu; semantics of backends/cpu/cpu_math.cpp) ---- */
 #define TCX_MATH_LOG 0

@@ -600,3 +600,187 @@ def attention(q, k, v, mask=None, causal: bool = False, scale: float | None = No
     product = matmul(q, _c(np.swapaxes(k, -1, -2)), threads)
     probabilities = attention_softmax(product, mask, scores_shape, float(s), causal, threads)
     return matmul(probabilities, v, threads)
+
+
+# ------------------------------------------------- layout, casts and predicates
+OPKIND.update({"negative": 15, "add_scalar": 16, "subtract_scalar": 17, "multiply_scalar": 18,
+               "divide_scalar": 19, "astype": 20, "slice": 22, "concat": 23, "equal": 24, "not_equal": 25,
+               "less": 26, "less_equal": 27, "greater": 28, "greater_equal": 29, "logical_and": 30,
+               "logical_or": 31, "logical_xor": 32, "logical_not": 33, "where": 34, "any": 35, "all": 36,
+               "masked_select": 37})
+_NP_OF = {"float32": np.float32, "int32": np.int32, "bool": np.bool_}
+
+
+def scalar_op(name: str, x, scalar: float = 0.0, scalar_left: bool = False) -> np.ndarray:
+    """cpu_backend.cpp:878-930: negate and scalar arithmetic; float32 rounds the
+    scalar once, int32 wraps in uint32 (no division, integer scalars only)."""
+    x = _c(x)
+    if x.dtype == np.bool_:
+        raise ValueError("numeric operations do not support bool")
+    if x.dtype == np.int32 and name != "negative":
+        if name == "divide_scalar":
+            raise ValueError("division only supports float32 tensors")
+        if not (float(scalar).is_integer() and -2**31 <= scalar <= 2**31 - 1):
+            raise ValueError("arithmetic scalar must be an integer in int32 range")
+    if x.dtype == np.float32:
+        with np.errstate(all="ignore"):
+            s = np.float32(scalar)
+            lhs, rhs = (s, x) if scalar_left else (x, s)
+            out = {"negative": lambda: -x, "add_scalar": lambda: lhs + rhs,
+                   "subtract_scalar": lambda: lhs - rhs, "multiply_scalar": lambda: lhs * rhs,
+                   "divide_scalar": lambda: lhs / rhs}[name]()
+        return np.asarray(out, dtype=np.float32)
+    v = x.astype(np.uint32)
+    s = np.uint32(int(scalar) & 0xFFFFFFFF) if name != "negative" else np.uint32(0)
+    lhs, rhs = (s, v) if scalar_left else (v, s)
+    with np.errstate(all="ignore"):
+        out = {"negative": lambda: np.uint32(0) - v, "add_scalar": lambda: lhs + rhs,
+               "subtract_scalar": lambda: lhs - rhs, "multiply_scalar": lambda: lhs * rhs}[name]()
+    return np.asarray(out, dtype=np.uint32).view(np.int32)
+
+
+def astype(x, dtype: str) -> np.ndarray:
+    """cpu_backend.cpp:834-876: bool conversions test != 0; float32 -> int32
+    truncates after every value was checked finite and in [-2^31, 2^31)."""
+    x = _c(x)
+    if dtype not in _NP_OF:
+        raise ValueError("unsupported cast target dtype")
+    if dtype == "bool" or x.dtype == np.bool_:
+        return (x != 0).astype(_NP_OF[dtype])
+    if x.dtype == _NP_OF[dtype]:
+        return x.copy()
+    if dtype == "int32":
+        if x.size and (not np.isfinite(x).all() or x.min() < -2147483648.0 or x.max() >= 2147483648.0):
+            raise ValueError("float32 value is out of range for int32 cast")
+        return x.astype(np.int32)
+    return x.astype(np.float32)
+
+
+def make_transpose_plan(shape, axes):
+    """shape.cpp:175-200: a full permutation, negative axes allowed."""
+    rank = len(shape)
+    if len(axes) != rank:
+        raise ValueError("transpose axes must be a full permutation")
+    seen = set()
+    out = []
+    for a in axes:
+        a = a + rank if a < 0 else a
+        if a < 0 or a >= rank:
+            raise ValueError("transpose axis is out of range")
+        if a in seen:
+            raise ValueError("transpose axes must not repeat")
+        seen.add(a)
+        out.append(a)
+    return tuple(out)
+
+
+def transpose(x, axes) -> np.ndarray:
+    x = _c(x)
+    return np.ascontiguousarray(np.transpose(x, make_transpose_plan(x.shape, tuple(axes)))).reshape(
+        tuple(x.shape[a] for a in make_transpose_plan(x.shape, tuple(axes))))
+
+
+def slice_(x, starts, steps, lengths) -> np.ndarray:
+    """make_slice_plan (shape.cpp:87-114): every visited index in bounds."""
+    x = _c(x)
+    if not (len(starts) == len(steps) == len(lengths) == x.ndim):
+        raise ValueError("slice metadata must match input rank")
+    index = []
+    for extent, start, step, length in zip(x.shape, starts, steps, lengths):
+        if step == 0:
+            raise ValueError("slice step cannot be zero")
+        if length < 0:
+            raise ValueError("shape dimensions must be non-negative")
+        if length == 0:
+            index.append(np.zeros(0, np.int64))
+            continue
+        if start < 0 or start >= extent:
+            raise ValueError("slice start is out of bounds")
+        last = start + step * (length - 1)
+        if last < 0 or last >= extent:
+            raise ValueError("slice endpoint is out of bounds")
+        index.append(start + step * np.arange(length, dtype=np.int64))
+    if not index:
+        return x.copy()
+    return np.ascontiguousarray(x[np.ix_(*index)])
+
+
+def concat(arrays, axis: int) -> np.ndarray:
+    """make_concat_plan (shape.cpp:116-138)."""
+    arrays = [_c(a) for a in arrays]
+    if not arrays:
+        raise ValueError("concat requires at least one tensor")
+    if builtins.any(a.dtype != arrays[0].dtype for a in arrays):
+        raise ValueError("concat dtypes must match")
+    rank = arrays[0].ndim
+    a = axis + rank if axis < 0 else axis
+    if a < 0 or a >= rank:
+        raise ValueError("concat axis is out of range")
+    for arr in arrays:
+        if arr.ndim != rank:
+            raise ValueError("concat ranks must match")
+        if builtins.any(arr.shape[i] != arrays[0].shape[i] for i in range(rank) if i != a):
+            raise ValueError("concat non-axis dimensions must match")
+    return np.ascontiguousarray(np.concatenate(arrays, axis=a))
+
+
+_COMPARE = {"equal": np.equal, "not_equal": np.not_equal, "less": np.less, "less_equal": np.less_equal,
+            "greater": np.greater, "greater_equal": np.greater_equal}
+_LOGICAL = {"logical_and": np.logical_and, "logical_or": np.logical_or, "logical_xor": np.logical_xor}
+
+
+def predicate(name: str, *inputs) -> np.ndarray:
+    """make_predicate_plan (predicate.cpp:23-44), cpu_predicate.cpp:22-50."""
+    inputs = [_c(a) for a in inputs]
+    arity = 3 if name == "where" else 1 if name == "logical_not" else 2
+    if len(inputs) != arity:
+        raise ValueError("invalid predicate operation or input count")
+    if name == "where":
+        if inputs[0].dtype != np.bool_:
+            raise ValueError("where condition must be bool")
+        if inputs[1].dtype != inputs[2].dtype:
+            raise ValueError("where branch dtypes must match")
+    else:
+        for a in inputs:
+            if a.dtype != inputs[0].dtype:
+                raise ValueError("comparison dtypes must match")
+            if name.startswith("logical") and a.dtype != np.bool_:
+                raise ValueError("logical operations require bool tensors")
+    shape: tuple = ()
+    for a in inputs:
+        shape = tuple(make_broadcast_plan(shape, a.shape)[0])
+    b = [np.broadcast_to(a, shape) for a in inputs]
+    if name == "where":
+        return np.ascontiguousarray(np.where(b[0], b[1], b[2]))
+    if name == "logical_not":
+        return np.ascontiguousarray(np.logical_not(b[0]))
+    if name in _LOGICAL:
+        return np.ascontiguousarray(_LOGICAL[name](b[0], b[1]))
+    with np.errstate(invalid="ignore"):
+        return np.ascontiguousarray(_COMPARE[name](b[0], b[1]))
+
+
+def bool_reduce(name: str, x, axes) -> np.ndarray:
+    """make_boolean_reduction_plan (predicate.cpp:46-55), cpu_predicate.cpp:52-70."""
+    x = _c(x)
+    if x.dtype != np.bool_:
+        raise ValueError("any/all require bool tensors")
+    out_shape, _, _ = make_reduction_plan(x.shape, tuple(axes))
+    rank = x.ndim
+    norm = tuple(a + rank if a < 0 else a for a in axes)
+    fn = np.all if name == "all" else np.any
+    return np.ascontiguousarray(fn(x, axis=norm)).reshape(out_shape)
+
+
+def masked_select(x, mask) -> np.ndarray:
+    """make_masked_select_plan (predicate.cpp:57-72), cpu_predicate.cpp:72-96."""
+    x, mask = _c(x), _c(mask)
+    if mask.dtype != np.bool_:
+        raise ValueError("mask must be bool")
+    if mask.ndim > x.ndim:
+        raise ValueError("mask rank exceeds input rank")
+    if tuple(x.shape[:mask.ndim]) != tuple(mask.shape):
+        raise ValueError("mask must match leading input dimensions")
+    tail = x.shape[mask.ndim:]
+    flat = x.reshape((int(np.prod(mask.shape, dtype=np.int64)),) + tail)
+    return np.ascontiguousarray(flat[mask.reshape(-1)])

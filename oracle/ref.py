@@ -43,13 +43,20 @@ def lib() -> ctypes.CDLL:
 def execute(kind: str, inputs, *, axis: int = 0, eps: float = 1e-5, axes=None,
             has_weight: bool = False, has_bias: bool = False, n_outputs: int = 1,
             causal: bool = False, scale: float | None = None, attention_shape=(),
-            k: int = 0, largest: bool = True, sorted: bool = True):  # noqa: A002
+            k: int = 0, largest: bool = True, sorted: bool = True,  # noqa: A002
+            scalar: float = 0.0, scalar_left: bool = False, target_dtype: str | None = None,
+            perm=None, starts=None, steps=None, lengths=None):
     """Runs one primitive through the reference CpuBackend::execute."""
     arrays = [np.asarray(a, order="C") for a in inputs]  # keeps rank 0
     att = (ctypes.c_int64 * max(1, len(attention_shape)))(*attention_shape)
     lib().tcxref_set_attributes(int(causal), int(scale is not None), ctypes.c_double(scale or 0.0),
                                 len(attention_shape), att, ctypes.c_int64(k), int(largest), int(sorted),
-                                ctypes.c_double(0.0))
+                                ctypes.c_double(scalar))
+    if perm is not None or starts is not None or target_dtype is not None or scalar_left:
+        def arr(v):
+            return (ctypes.c_int64 * max(1, len(v or ())))(*(v or ()))
+        lib().tcxref_set_layout(len(perm or ()), arr(perm), len(starts or ()), arr(starts), arr(steps),
+                                arr(lengths), DTYPE[target_dtype or "float32"], int(scalar_left))
     dtypes = (ctypes.c_int * max(1, len(arrays)))(*[DTYPE[str(a.dtype)] for a in arrays])
     ranks = (ctypes.c_int * max(1, len(arrays)))(*[a.ndim for a in arrays])
     dims = [d for a in arrays for d in a.shape]

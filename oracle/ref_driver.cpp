@@ -40,6 +40,10 @@ struct Attributes {
   bool largest{true};
   bool sorted{true};
   double scalar{0.0};
+  bool layout{false};
+  tensorcx::Shape axes{}, starts{}, steps{}, lengths{};
+  int target_dtype{0};
+  bool scalar_left{false};
 };
 
 thread_local Attributes pending;
@@ -90,6 +94,14 @@ int tcxref_execute(int kind, std::int64_t axis, double epsilon, int has_axes,
       op.largest = pending.largest;
       op.sorted = pending.sorted;
       op.scalar_value = pending.scalar;
+      if (pending.layout) {
+        op.axes = pending.axes;
+        op.slice_starts = pending.starts;
+        op.slice_steps = pending.steps;
+        op.slice_shape = pending.lengths;
+        op.target_dtype = static_cast<tensorcx::DType>(pending.target_dtype);
+        op.scalar_left = pending.scalar_left;
+      }
       pending = Attributes{};
     }
     std::vector<tensorcx::Tensor> outputs(static_cast<std::size_t>(n_outputs));
@@ -125,6 +137,22 @@ void tcxref_set_attributes(int causal, int has_scale, double scale, int attentio
   pending.largest = largest != 0;
   pending.sorted = sorted != 0;
   pending.scalar = scalar;
+}
+
+// Adds transpose axes, slice starts/steps/lengths (each `rank` long, the
+// ones not used may be NULL), the cast target dtype and the scalar operand
+// side to the attributes of the next tcxref_execute (call after
+// tcxref_set_attributes).
+void tcxref_set_layout(int axes_rank, const std::int64_t* axes, int slice_rank, const std::int64_t* starts,
+                       const std::int64_t* steps, const std::int64_t* lengths, int target_dtype, int scalar_left) {
+  pending.set = true;
+  pending.layout = true;
+  pending.axes = axes ? tensorcx::Shape(axes, axes + axes_rank) : tensorcx::Shape{};
+  pending.starts = starts ? tensorcx::Shape(starts, starts + slice_rank) : tensorcx::Shape{};
+  pending.steps = steps ? tensorcx::Shape(steps, steps + slice_rank) : tensorcx::Shape{};
+  pending.lengths = lengths ? tensorcx::Shape(lengths, lengths + slice_rank) : tensorcx::Shape{};
+  pending.target_dtype = target_dtype;
+  pending.scalar_left = scalar_left != 0;
 }
 
 const char* tcxref_message() { return last.message.c_str(); }

@@ -328,6 +328,62 @@ PYBIND11_MODULE(_core, m) {
     return run(op, std::move(in));
   }, py::arg("scores"), py::arg("mask"), py::arg("shape"), py::arg("causal") = false, py::arg("scale") = py::none());
 
+  // Scalar arithmetic, casts and layout (the reference's _core names).
+  m.def("negative", [](const HipTensor& x) { return unary(OpKind::kNegate, x); });
+  for (const auto& [name, kind] : std::vector<std::pair<const char*, OpKind>>{
+           {"add_scalar", OpKind::kAddScalar}, {"subtract_scalar", OpKind::kSubtractScalar},
+           {"multiply_scalar", OpKind::kMultiplyScalar}, {"divide_scalar", OpKind::kDivideScalar}}) {
+    const OpKind k = kind;
+    m.def(name, [k](const HipTensor& x, double value, bool scalar_left) {
+      OpDesc op{k};
+      op.scalar_value = value;
+      op.scalar_left = scalar_left;
+      return run(op, {x.tensor});
+    }, py::arg("x"), py::arg("value"), py::arg("scalar_left") = false);
+  }
+  m.def("astype", [](const HipTensor& x, const std::string& dtype) {
+    OpDesc op{OpKind::kCast};
+    op.target_dtype = parse_dtype(dtype);
+    return run(op, {x.tensor});
+  });
+  m.def("transpose", [](const HipTensor& x, std::vector<std::int64_t> axes) {
+    OpDesc op{OpKind::kTranspose};
+    op.axes = to_shape(axes);
+    return run(op, {x.tensor});
+  });
+  m.def("_slice", [](const HipTensor& x, std::vector<std::int64_t> starts, std::vector<std::int64_t> steps,
+                     std::vector<std::int64_t> lengths) {
+    OpDesc op{OpKind::kSlice};
+    op.slice_starts = to_shape(starts);
+    op.slice_steps = to_shape(steps);
+    op.slice_shape = to_shape(lengths);
+    return run(op, {x.tensor});
+  });
+  m.def("_concat", [](const HipTensor& first, const std::vector<const HipTensor*>& rest, std::int64_t axis) {
+    OpDesc op{OpKind::kConcat};
+    op.axis = axis;
+    std::vector<Tensor> in{first.tensor};
+    for (const HipTensor* t : rest) in.push_back(t->tensor);
+    return run(op, std::move(in));
+  });
+  for (const auto& [name, kind] : std::vector<std::pair<const char*, OpKind>>{
+           {"equal", OpKind::kEqual}, {"not_equal", OpKind::kNotEqual}, {"less", OpKind::kLess},
+           {"less_equal", OpKind::kLessEqual}, {"greater", OpKind::kGreater},
+           {"greater_equal", OpKind::kGreaterEqual}, {"logical_and", OpKind::kLogicalAnd},
+           {"logical_or", OpKind::kLogicalOr}, {"logical_xor", OpKind::kLogicalXor}}) {
+    const OpKind k = kind;
+    m.def(name, [k](const HipTensor& a, const HipTensor& b) { return run(OpDesc{k}, {a.tensor, b.tensor}); });
+  }
+  m.def("logical_not", [](const HipTensor& x) { return unary(OpKind::kLogicalNot, x); });
+  m.def("where", [](const HipTensor& c, const HipTensor& a, const HipTensor& b) {
+    return run(OpDesc{OpKind::kWhere}, {c.tensor, a.tensor, b.tensor});
+  });
+  m.def("_any_axes", [](const HipTensor& x, std::vector<std::int64_t> axes) { return axes_op(OpKind::kAny, x, axes); });
+  m.def("_all_axes", [](const HipTensor& x, std::vector<std::int64_t> axes) { return axes_op(OpKind::kAll, x, axes); });
+  m.def("masked_select", [](const HipTensor& x, const HipTensor& mask) {
+    return run(OpDesc{OpKind::kMaskedSelect}, {x.tensor, mask.tensor});
+  });
+
   // Runtime profiling sessions (the reference's _profile_begin/_profile_end).
   m.def("_profile_begin", [](std::int64_t max_events, bool device_timing) {
     if (max_events < 1 || max_events > 100000) throw py::value_error("max_events must be an integer in [1, 100000]");

@@ -4,6 +4,7 @@
 
 #include "tensorcx/backends/hip/hip_backend.h"
 
+#include "tensorcx/core/predicate.h"
 #include "tensorcx/core/profiling.h"
 
 #include <algorithm>
@@ -759,6 +760,193 @@ Tensor attention(const OpDesc& op, std::span<const Tensor> inputs, tcx_stream_t 
   return matmul(probabilities, v, s);
 }
 
+// ------------------------------------------------------------ layout, casts, scalars
+// kNegate / k*Scalar / kCast / kTranspose / kSlice / kConcat with the checks of
+// cpu_backend.cpp:801-930 and the plans of core/shape.cpp.
+int element_bytes(DType dtype) { return static_cast<int>(dtype_size(dtype)); }
+
+// Scratch device memory that outlives no call (flags, counts, offsets).
+std::shared_ptr<HipBuffer> scratch(std::size_t bytes) {
+  auto created = HipBuffer::create(bytes);
+  if (!created) {
+    const Status& st = created.status();
+    if (st.code() == StatusCode::kUnavailable) throw Unavailable(st.message());
+    throw std::runtime_error(st.message());
+  }
+  return created.move_value();
+}
+
+Tensor scalar_op(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
+  if (x.dtype == DType::kBool) throw std::invalid_argument("numeric operations do not support bool");
+  const int code = op.kind == OpKind::kNegate           ? TCX_SCALAR_NEGATE
+                   : op.kind == OpKind::kAddScalar      ? TCX_SCALAR_ADD
+                   : op.kind == OpKind::kSubtractScalar ? TCX_SCALAR_SUBTRACT
+                   : op.kind == OpKind::kMultiplyScalar ? TCX_SCALAR_MULTIPLY
+                                                        : TCX_SCALAR_DIVIDE;
+  if (x.dtype == DType::kInt32 && code != TCX_SCALAR_NEGATE) {
+    if (code == TCX_SCALAR_DIVIDE) throw std::invalid_argument("division only supports float32 tensors");
+    if (!is_int32_representable(op.scalar_value))
+      throw std::invalid_argument("arithmetic scalar must be an integer in int32 range");
+  }
+  const void* xp = device_ptr(x);
+  Tensor out = make_tensor(x.dtype, x.shape);
+  ok_or_throw(tcx_hip_scalar_op(code, tcx_dtype(x.dtype), xp, out_ptr(out), numel(x.shape), op.scalar_value,
+                                op.scalar_left ? 1 : 0, s),
+              "HIP scalar arithmetic");
+  return out;
+}
+
+int any_dtype(DType d) { return d == DType::kBool ? TCX_BOOL : tcx_dtype(d); }
+
+Tensor cast(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
+  const DType to = op.target_dtype;
+  if (to != DType::kFloat32 && to != DType::kInt32 && to != DType::kBool)
+    throw std::invalid_argument("unsupported cast target dtype");
+  const void* xp = device_ptr(x);
+  Tensor out = make_tensor(to, x.shape);
+  const Dim n = numel(x.shape);
+  if (n == 0) return out;
+  std::shared_ptr<HipBuffer> flag;
+  if (x.dtype == DType::kFloat32 && to == DType::kInt32) flag = scratch(sizeof(std::int32_t));
+  ok_or_throw(tcx_hip_cast(any_dtype(x.dtype), any_dtype(to), xp, out_ptr(out), n,
+                           flag ? static_cast<std::int32_t*>(flag->data()) : nullptr, s),
+              "HIP cast");
+  return out;
+}
+
+// A strided gather of x through `plan`, with size-1 axes dropped and
+// contiguous runs merged to fit the kernel's metadata.
+Tensor gather(const Tensor& x, const TransposePlan& plan, tcx_stream_t s) {
+  const void* xp = device_ptr(x);
+  Tensor out = make_tensor(x.dtype, plan.output_shape);
+  if (numel(plan.output_shape) == 0) return out;
+  const Strided m = compress(plan.output_shape, {plan.input_strides});
+  ok_or_throw(tcx_hip_gather_strided(element_bytes(x.dtype), xp, out_ptr(out), static_cast<int32_t>(m.shape.size()),
+                                     m.shape.data(), m.strides[0].data(), plan.offset, s),
+              "HIP gather");
+  return out;
+}
+
+Tensor concat(const OpDesc& op, std::span<const Tensor> inputs, tcx_stream_t s) {
+  std::vector<Shape> shapes;
+  for (const Tensor& t : inputs) {
+    if (t.dtype != inputs[0].dtype) throw std::invalid_argument("concat dtypes must match");
+    (void)device_ptr(t);
+    shapes.push_back(t.shape);
+  }
+  const ConcatPlan plan = make_concat_plan(shapes, op.axis);
+  Tensor out = make_tensor(inputs[0].dtype, plan.output_shape);
+  if (numel(plan.output_shape) == 0) return out;
+  const Dim out_block = plan.output_shape[plan.axis] * plan.inner;
+  Dim outer = 1;
+  for (std::size_t a = 0; a < plan.axis; ++a) outer *= plan.output_shape[a];
+  Dim offset = 0;
+  for (const Tensor& t : inputs) {
+    const Dim block = t.shape[plan.axis] * plan.inner;
+    ok_or_throw(tcx_hip_copy_blocks(element_bytes(t.dtype), device_ptr(t), out_ptr(out), outer, block, out_block,
+                                    offset, s),
+                "HIP concat");
+    offset += block;
+  }
+  return out;
+}
+
+// ------------------------------------------------------------ predicates
+int predicate_code(OpKind kind) {
+  switch (kind) {
+    case OpKind::kEqual: return TCX_PRED_EQUAL;
+    case OpKind::kNotEqual: return TCX_PRED_NOT_EQUAL;
+    case OpKind::kLess: return TCX_PRED_LESS;
+    case OpKind::kLessEqual: return TCX_PRED_LESS_EQUAL;
+    case OpKind::kGreater: return TCX_PRED_GREATER;
+    case OpKind::kGreaterEqual: return TCX_PRED_GREATER_EQUAL;
+    case OpKind::kLogicalAnd: return TCX_PRED_LOGICAL_AND;
+    case OpKind::kLogicalOr: return TCX_PRED_LOGICAL_OR;
+    case OpKind::kLogicalXor: return TCX_PRED_LOGICAL_XOR;
+    case OpKind::kLogicalNot: return TCX_PRED_LOGICAL_NOT;
+    default: return TCX_PRED_WHERE;
+  }
+}
+
+Tensor predicate(const OpDesc& op, std::span<const Tensor> inputs, tcx_stream_t s) {
+  const PredicatePlan plan = make_predicate_plan(op, inputs);
+  std::vector<const void*> ptrs;
+  for (const Tensor& t : inputs) ptrs.push_back(device_ptr(t));
+  Tensor out = make_tensor(plan.output_dtype, plan.output_shape);
+  if (numel(plan.output_shape) == 0) return out;
+  std::vector<Shape> strides = plan.input_strides;
+  while (strides.size() < 3) strides.push_back(Shape(plan.output_shape.size(), 0));
+  const Strided m = compress(plan.output_shape, strides);
+  tcx_hip_broadcast3_t d{};
+  d.rank = static_cast<int32_t>(m.shape.size());
+  for (std::size_t a = 0; a < m.shape.size(); ++a) {
+    d.shape[a] = m.shape[a];
+    for (int k = 0; k < 3; ++k) d.strides[k][a] = m.strides[static_cast<std::size_t>(k)][a];
+  }
+  const bool where = op.kind == OpKind::kWhere;
+  const DType compared = where ? inputs[1].dtype : inputs[0].dtype;
+  if (compared == DType::kInt32) d.flags = TCX_PRED_FLAG_INT32;
+  ok_or_throw(tcx_hip_predicate(predicate_code(op.kind), element_bytes(compared), ptrs[0],
+                                ptrs.size() > 1 ? ptrs[1] : nullptr, ptrs.size() > 2 ? ptrs[2] : nullptr, out_ptr(out),
+                                &d, s),
+              "HIP predicate");
+  return out;
+}
+
+Tensor bool_reduce(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
+  if (x.dtype != DType::kBool) throw std::invalid_argument("any/all require bool tensors");
+  const ReductionPlan plan = make_boolean_reduction_plan(op, x.shape);
+  const void* xp = device_ptr(x);
+  Tensor out = make_tensor(DType::kBool, plan.output_shape);
+  const Dim groups = numel(plan.output_shape);
+  if (groups == 0) return out;
+  if (x.shape.size() > TCX_HIP_MAX_RANK) throw std::invalid_argument("HIP boolean reductions support rank <= 8");
+  ok_or_throw(tcx_hip_bool_reduce(op.kind == OpKind::kAll ? 1 : 0, static_cast<const uint8_t*>(xp),
+                                  static_cast<uint8_t*>(out_ptr(out)), plan.index_metadata.data(),
+                                  static_cast<int32_t>(x.shape.size()), groups, plan.reduction_size, s),
+              "HIP boolean reduction");
+  return out;
+}
+
+// masked_select: counts per chunk, host offsets, then index compaction and a
+// row gather (cpu_predicate.cpp:72-96).
+Tensor masked_select(const Tensor& x, const Tensor& mask, tcx_stream_t s) {
+  const MaskedSelectPlan plan = make_masked_select_plan(x, mask);
+  const void* xp = device_ptr(x);
+  const auto* mp = static_cast<const uint8_t*>(device_ptr(mask));
+  const Dim n = numel(mask.shape);
+  Dim total = 0;
+  std::vector<std::int64_t> offsets;
+  std::shared_ptr<HipBuffer> counts_dev;
+  if (n > 0) {
+    const Dim chunks = tcx_hip_mask_chunks(n);
+    counts_dev = scratch(static_cast<std::size_t>(chunks) * sizeof(std::int64_t));
+    auto* counts = static_cast<std::int64_t*>(counts_dev->data());
+    ok_or_throw(tcx_hip_mask_count(mp, n, counts, s), "HIP mask count");
+    offsets.resize(static_cast<std::size_t>(chunks));
+    ok_or_throw(tcx_hip_memcpy_d2h(offsets.data(), counts, offsets.size() * sizeof(std::int64_t), s),
+                "HIP mask count copy");
+    for (std::int64_t& c : offsets) {  // counts -> exclusive offsets
+      const std::int64_t here = c;
+      c = total;
+      total += here;
+    }
+  }
+  Shape shape{total};
+  shape.insert(shape.end(), plan.tail_shape.begin(), plan.tail_shape.end());
+  Tensor out = make_tensor(x.dtype, shape);
+  if (total == 0) return out;
+  ok_or_throw(tcx_hip_memcpy_h2d(counts_dev->data(), offsets.data(), offsets.size() * sizeof(std::int64_t), s),
+              "HIP mask offset copy");
+  auto index = scratch(static_cast<std::size_t>(total) * sizeof(std::int64_t));
+  ok_or_throw(tcx_hip_masked_select(element_bytes(x.dtype), xp, mp, n, plan.block_size,
+                                    static_cast<const std::int64_t*>(counts_dev->data()), total,
+                                    static_cast<std::int64_t*>(index->data()), out_ptr(out), s),
+              "HIP masked select");
+  synchronize(s);  // the scratch buffers are released on return
+  return out;
+}
+
 // ------------------------------------------------------------ kernel class
 Status execute_builtin_kernel(const BackendExecution& e) {
   if (Status s = validate_kernel_execution_contract(e); !s.ok()) return s;
@@ -1007,6 +1195,32 @@ Status HipBackend::execute(const BackendExecution& e) {
       case OpKind::kEmbedding: result = embedding(e.inputs, s); break;
       case OpKind::kAttentionSoftmax: result = attention_softmax(e.op, e.inputs, s); break;
       case OpKind::kAttention: result = attention(e.op, e.inputs, s); break;
+      case OpKind::kNegate:
+      case OpKind::kAddScalar:
+      case OpKind::kSubtractScalar:
+      case OpKind::kMultiplyScalar:
+      case OpKind::kDivideScalar: result = scalar_op(e.op, e.inputs[0], s); break;
+      case OpKind::kCast: result = cast(e.op, e.inputs[0], s); break;
+      case OpKind::kTranspose: result = gather(e.inputs[0], make_transpose_plan(e.inputs[0].shape, e.op.axes), s); break;
+      case OpKind::kSlice:
+        result = gather(e.inputs[0],
+                        make_slice_plan(e.inputs[0].shape, e.op.slice_starts, e.op.slice_steps, e.op.slice_shape), s);
+        break;
+      case OpKind::kConcat: result = concat(e.op, e.inputs, s); break;
+      case OpKind::kEqual:
+      case OpKind::kNotEqual:
+      case OpKind::kLess:
+      case OpKind::kLessEqual:
+      case OpKind::kGreater:
+      case OpKind::kGreaterEqual:
+      case OpKind::kLogicalAnd:
+      case OpKind::kLogicalOr:
+      case OpKind::kLogicalXor:
+      case OpKind::kLogicalNot:
+      case OpKind::kWhere: result = predicate(e.op, e.inputs, s); break;
+      case OpKind::kAny:
+      case OpKind::kAll: result = bool_reduce(e.op, e.inputs[0], s); break;
+      case OpKind::kMaskedSelect: result = masked_select(e.inputs[0], e.inputs[1], s); break;
       default:
         return Status(StatusCode::kInvalidArgument, "unsupported HIP backend execution operation");
     }

@@ -135,4 +135,68 @@ ReductionPlan make_reduction_plan(const Shape& input, const Shape& axes) {
   return plan;
 }
 
+TransposePlan make_transpose_plan(const Shape& input, const Shape& axes) {
+  (void)numel(input);
+  const Shape strides = contiguous_strides(input);
+  if (axes.size() != input.size()) throw std::invalid_argument("transpose axes must be a full permutation");
+  const Dim rank = static_cast<Dim>(input.size());
+  std::vector<bool> used(input.size(), false);
+  TransposePlan plan{Shape(input.size()), Shape(input.size()), 0};
+  for (std::size_t i = 0; i < axes.size(); ++i) {
+    const Dim axis = axes[i] < 0 ? axes[i] + rank : axes[i];
+    if (axis < 0 || axis >= rank) throw std::invalid_argument("transpose axis is out of range");
+    if (used[static_cast<std::size_t>(axis)]) throw std::invalid_argument("transpose axes must not repeat");
+    used[static_cast<std::size_t>(axis)] = true;
+    plan.output_shape[i] = input[static_cast<std::size_t>(axis)];
+    plan.input_strides[i] = strides[static_cast<std::size_t>(axis)];
+  }
+  (void)numel(plan.output_shape);
+  return plan;
+}
+
+TransposePlan make_slice_plan(const Shape& input, const Shape& starts, const Shape& steps, const Shape& lengths) {
+  (void)numel(input);
+  const Shape strides = contiguous_strides(input);
+  if (starts.size() != input.size() || steps.size() != input.size() || lengths.size() != input.size())
+    throw std::invalid_argument("slice metadata must match input rank");
+  const Dim total = numel(lengths);
+  TransposePlan plan{lengths, Shape(input.size(), 0), 0};
+  for (std::size_t a = 0; a < input.size(); ++a) {
+    const Dim start = starts[a], step = steps[a], length = lengths[a];
+    if (step == 0) throw std::invalid_argument("slice step cannot be zero");
+    if (length == 0) continue;
+    if (start < 0 || start >= input[a]) throw std::invalid_argument("slice start is out of bounds");
+    if (length > 1) {
+      // The last index start + step * (length - 1) must stay in [0, extent);
+      // compared by division so the product cannot overflow.
+      const bool past_end = step > 0 && step > (input[a] - 1 - start) / (length - 1);
+      const bool before_start = step < 0 && step < -(start / (length - 1));
+      if (past_end || before_start) throw std::invalid_argument("slice endpoint is out of bounds");
+      if (total != 0) plan.input_strides[a] = step * strides[a];
+    }
+    if (total != 0) plan.offset += start * strides[a];
+  }
+  return plan;
+}
+
+ConcatPlan make_concat_plan(const std::vector<Shape>& inputs, Dim axis) {
+  if (inputs.empty()) throw std::invalid_argument("concat requires at least one tensor");
+  const Dim rank = static_cast<Dim>(inputs[0].size());
+  if (axis < 0) axis += rank;
+  if (axis < 0 || axis >= rank) throw std::invalid_argument("concat axis is out of range");
+  const auto ax = static_cast<std::size_t>(axis);
+  Shape output = inputs[0];
+  output[ax] = 0;
+  for (const Shape& shape : inputs) {
+    (void)numel(shape);
+    if (shape.size() != output.size()) throw std::invalid_argument("concat ranks must match");
+    for (std::size_t i = 0; i < shape.size(); ++i)
+      if (i != ax && shape[i] != output[i]) throw std::invalid_argument("concat non-axis dimensions must match");
+    if (shape[ax] > std::numeric_limits<Dim>::max() - output[ax]) throw std::invalid_argument("concat dimension overflow");
+    output[ax] += shape[ax];
+  }
+  (void)numel(output);
+  return {output, ax, contiguous_strides(output)[ax]};
+}
+
 }  // namespace tensorcx

@@ -1,7 +1,7 @@
 // Shapes and the shape plans the hip backend needs. Names and plan fields
 // follow the reference's core/shape.h:8-70 (numel, contiguous_strides,
-// BroadcastPlan, MatmulPlan, ReductionPlan) so plans mean the same thing on
-// both sides of the backend boundary.
+// BroadcastPlan, MatmulPlan, ReductionPlan, TransposePlan, ConcatPlan) so
+// plans mean the same thing on both sides of the backend boundary.
 #pragma once
 
 #include <cstdint>
@@ -43,5 +43,24 @@ struct ReductionPlan {
   Dim reduction_size{1};
 };
 ReductionPlan make_reduction_plan(const Shape& input, const Shape& axes);
+
+// A strided view of a contiguous input: output element i reads
+// offset + sum over axes of index * input_strides.
+struct TransposePlan {
+  Shape output_shape;
+  Shape input_strides;
+  Dim offset{0};
+};
+// A full permutation of the axes (negative axes allowed, no repeats).
+TransposePlan make_transpose_plan(const Shape& input, const Shape& axes);
+// Per-axis start / step / length, every visited index in bounds.
+TransposePlan make_slice_plan(const Shape& input, const Shape& starts, const Shape& steps, const Shape& lengths);
+
+struct ConcatPlan {
+  Shape output_shape;
+  std::size_t axis;
+  Dim inner;  // contiguous stride of the concatenation axis in the output
+};
+ConcatPlan make_concat_plan(const std::vector<Shape>& inputs, Dim axis);
 
 }  // namespace tensorcx

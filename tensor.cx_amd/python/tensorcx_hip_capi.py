@@ -39,6 +39,8 @@ EXPORTS = [
     "tcx_hip_bias_act_f32", "tcx_hip_unary_f32", "tcx_hip_binary", "tcx_hip_fill",
     "tcx_hip_math_unary", "tcx_hip_clip", "tcx_hip_topk", "tcx_hip_embedding_f32",
     "tcx_hip_attention_softmax_f32", "tcx_hip_flash_attention_supported", "tcx_hip_flash_attention_f32",
+    "tcx_hip_gather_strided", "tcx_hip_copy_blocks", "tcx_hip_cast", "tcx_hip_scalar_op", "tcx_hip_predicate",
+    "tcx_hip_bool_reduce", "tcx_hip_mask_chunks", "tcx_hip_mask_count", "tcx_hip_masked_select",
 ]
 
 

@@ -240,6 +240,97 @@ def cases():
     add("attention_bad_batch", "attention", [f32(rng, (2, 0, 3)), f32(rng, (3, 2, 3)), f32(rng, (3, 2, 3))])
     add("attention_bad_mask", "attention", [f32(rng, (2, 3)), f32(rng, (2, 3)), f32(rng, (2, 3)),
                                             np.zeros((2, 3), bool)])
+
+    # ---- scalar arithmetic and negate (cpu_backend.cpp:878-930)
+    xs = f32(rng, (4, 33), 3.0)
+    xs[0, :4] = [np.nan, np.inf, -0.0, 1e-40]
+    xi = rng.integers(-2**31, 2**31 - 1, (5, 7), dtype=np.int64).astype(np.int32)
+    xi[0, :3] = [-2**31, 2**31 - 1, 0]
+    add("negative_f32", "negative", [xs])
+    add("negative_i32_wrap", "negative", [xi])
+    for name in ("add_scalar", "subtract_scalar", "multiply_scalar", "divide_scalar"):
+        for left in (False, True):
+            add(f"{name}_f32_{int(left)}", name, [xs], scalar=0.1, scalar_left=left)
+        add(f"{name}_f32_inf", name, [xs], scalar=float("inf"))
+        if name != "divide_scalar":
+            add(f"{name}_i32_{int(left)}", name, [xi], scalar=-123457, scalar_left=True)
+            add(f"{name}_i32_wrap", name, [xi], scalar=2**31 - 1)
+    add("divide_scalar_i32_rejected", "divide_scalar", [xi], scalar=2.0)
+    add("add_scalar_i32_fraction_rejected", "add_scalar", [xi], scalar=0.5)
+    add("negative_bool_rejected", "negative", [np.array([True, False])])
+
+    # ---- casts (cpu_backend.cpp:834-876)
+    cf = np.array([0.0, -0.0, 1.9, -1.9, 2147483520.0, -2147483648.0, 1e-40, 3.5e6], np.float32)
+    ci = np.array([0, 1, -1, 2**31 - 1, -2**31, 16777217, 7], np.int32)
+    cb = np.array([True, False, True])
+    for src, arr in (("f32", cf), ("i32", ci), ("bool", cb)):
+        for dst in ("float32", "int32", "bool"):
+            add(f"astype_{src}_{dst}", "astype", [arr], target_dtype=dst)
+    for bad in (np.nan, np.inf, -np.inf, 2147483648.0, -2147483904.0):
+        add(f"astype_f32_i32_bad_{bad}", "astype", [np.array([1.0, bad], np.float32)], target_dtype="int32")
+    add("astype_empty", "astype", [np.zeros((0, 3), np.float32)], target_dtype="int32")
+
+    # ---- transpose / slice / concat (shape.cpp:87-200; cpu_backend.cpp:808-833, 317-339)
+    xt = f32(rng, (2, 3, 4, 5))
+    for perm in ((0, 1, 2, 3), (3, 2, 1, 0), (1, 3, 0, 2), (-1, 0, -3, 2)):
+        add(f"transpose_{'_'.join(map(str, perm))}", "transpose", [xt], perm=list(perm))
+    add("transpose_bool", "transpose", [rng.random((3, 5)) > .5], perm=[1, 0])
+    add("transpose_i32", "transpose", [xi], perm=[1, 0])
+    add("transpose_scalar", "transpose", [np.float32(3.5)], perm=[])
+    add("transpose_repeat_rejected", "transpose", [xt], perm=[0, 0, 1, 2])
+    for si, (starts, steps, lengths) in enumerate((([0, 0, 0, 0], [1, 1, 1, 1], [2, 3, 4, 5]),
+                                                  ([1, 2, 3, 4], [-1, -1, -1, -1], [2, 3, 4, 5]),
+                                                  ([0, 1, 0, 4], [1, 1, 2, -2], [2, 2, 2, 3]),
+                                                  ([1, 0, 2, 0], [1, 1, 1, 1], [1, 0, 1, 5]))):
+        add(f"slice_{si}", "slice", [xt], starts=starts, steps=steps, lengths=lengths)
+    add("slice_oob_rejected", "slice", [xt], starts=[0, 0, 0, 3], steps=[1, 1, 1, 1], lengths=[2, 3, 4, 3])
+    a1, a2, a3 = f32(rng, (2, 3, 4)), f32(rng, (2, 1, 4)), f32(rng, (2, 0, 4))
+    add("concat_axis1", "concat", [a1, a2, a3], axis=1)
+    add("concat_axis0", "concat", [a1, f32(rng, (3, 3, 4))], axis=0)
+    add("concat_axis_neg", "concat", [a1, f32(rng, (2, 3, 2))], axis=-1)
+    add("concat_bool", "concat", [rng.random((2, 3)) > .5, rng.random((2, 2)) > .5], axis=1)
+    add("concat_mismatch_rejected", "concat", [a1, f32(rng, (2, 3, 5))], axis=1)
+
+    # ---- predicates (cpu_predicate.cpp:22-50)
+    pa = np.array([[0.0, -0.0, np.nan, 1.0, -np.inf, 2.5]], np.float32)
+    pb = np.array([[0.0], [np.nan], [2.5]], np.float32)
+    pia = rng.integers(-3, 4, (4, 1, 6)).astype(np.int32)
+    pib = rng.integers(-3, 4, (5, 6)).astype(np.int32)
+    pba, pbb = rng.random((3, 1)) > .5, rng.random((1, 4)) > .5
+    for name in ("equal", "not_equal", "less", "less_equal", "greater", "greater_equal"):
+        add(f"{name}_f32", name, [pa, pb])
+        add(f"{name}_i32", name, [pia, pib])
+        add(f"{name}_bool", name, [pba, pbb])
+    for name in ("logical_and", "logical_or", "logical_xor"):
+        add(f"{name}", name, [pba, pbb])
+    add("logical_not", "logical_not", [pba])
+    add("logical_and_f32_rejected", "logical_and", [pa, pa])
+    add("equal_mixed_rejected", "equal", [pa, pia])
+    cond = rng.random((3, 1, 6)) > .5
+    add("where_f32", "where", [cond, pa, pb[:, :1]])
+    add("where_i32", "where", [cond, pib[:1], np.int32(-9) * np.ones((), np.int32)])
+    add("where_bool", "where", [cond, pba[:, :1], ~pba[:, :1]])
+    add("where_cond_rejected", "where", [pa, pa, pa])
+
+    # ---- any / all (cpu_predicate.cpp:52-70)
+    xb = rng.random((3, 4, 5)) > .7
+    for name in ("any", "all"):
+        for axes in ([0], [1], [2], [0, 2], [], [0, 1, 2], [-1]):
+            add(f"{name}_axes_{'_'.join(map(str, axes)) or 'none'}", name, [xb], axes=axes)
+        add(f"{name}_empty", name, [np.zeros((2, 0), bool)], axes=[1])
+        add(f"{name}_f32_rejected", name, [pa], axes=[1])
+
+    # ---- masked_select (cpu_predicate.cpp:72-96)
+    mx = f32(rng, (4, 5, 3))
+    add("masked_select_leading", "masked_select", [mx, rng.random((4,)) > .5])
+    add("masked_select_two", "masked_select", [mx, rng.random((4, 5)) > .5])
+    add("masked_select_full", "masked_select", [mx, rng.random((4, 5, 3)) > .5])
+    add("masked_select_none", "masked_select", [mx, np.zeros((4, 5), bool)])
+    add("masked_select_i32", "masked_select", [pib, pib > 0])
+    add("masked_select_bool", "masked_select", [xb, xb[:, :, 0]])
+    add("masked_select_shape_rejected", "masked_select", [mx, np.ones((5,), bool)])
+    big = f32(rng, (3000, 2))
+    add("masked_select_chunks", "masked_select", [big, rng.random((3000,)) > .4])
     return c
 
 

@@ -11,6 +11,8 @@ Bars (stated once, used everywhere):
   * exp / gelu / silu: allclose(rtol=1e-6, atol=1e-6), the elementwise class;
   * abs, clip, topk, embedding, sqrt: bit-exact (sqrt is correctly rounded on
     both sides; NaNs compare as NaN, whatever their payload);
+  * scalar arithmetic, casts, transpose / slice / concat, comparisons, logical
+    ops, where, any / all, masked_select: bit-exact;
   * log: allclose(rtol=1e-6, atol=0), the bar of test_math_ops.py:15-21;
   * attention: allclose(rtol=2e-4, atol=2e-5), the bar of
     test_inference_ops.py:20-25.
@@ -140,6 +142,26 @@ def run_hip(cx, op, inputs, kw):
     if op == "attention":
         mask = t[3] if len(t) == 4 else None
         return cx.attention(*t[:3], mask, is_causal=kw.get("causal", False), scale=kw.get("scale"))
+    if op == "negative":
+        return -t[0]
+    if op in ("add_scalar", "subtract_scalar", "multiply_scalar", "divide_scalar"):
+        core = getattr(cx._core, op)
+        return cx.Tensor(core(t[0]._impl, kw.get("scalar", 0.0), scalar_left=kw.get("scalar_left", False)))
+    if op == "astype":
+        return cx.astype(t[0], kw["target_dtype"])
+    if op == "transpose":
+        return cx.Tensor(cx._core.transpose(t[0]._impl, list(kw["perm"])))
+    if op == "slice":
+        return cx.Tensor(cx._core._slice(t[0]._impl, kw["starts"], kw["steps"], kw["lengths"]))
+    if op == "concat":
+        return cx.Tensor(cx._core._concat(t[0]._impl, [x._impl for x in t[1:]], axis))
+    if op in ("any", "all"):
+        return cx.Tensor(getattr(cx._core, f"_{op}_axes")(t[0]._impl, list(kw["axes"])))
+    if op == "masked_select":
+        return cx.masked_select(*t)
+    if op in ("equal", "not_equal", "less", "less_equal", "greater", "greater_equal", "logical_and",
+              "logical_or", "logical_xor", "logical_not", "where"):
+        return cx.Tensor(getattr(cx._core, op)(*[x._impl for x in t]))
     raise AssertionError(op)
 
 
@@ -167,9 +189,13 @@ def check_case(name, op, inputs, kw, actual, expected):
             check_case(f"{name} output {n}", op, inputs, kw, a, e)
         return
     if op in ("max", "min", "argmax", "add", "subtract", "multiply", "divide", "abs", "clip", "topk",
-              "embedding") or expected.dtype == np.int32:
+              "embedding", "negative", "astype", "transpose", "slice", "concat", "equal", "not_equal", "less", "less_equal", "greater",
+              "greater_equal", "logical_and", "logical_or", "logical_xor", "logical_not", "where", "any",
+              "all", "masked_select") or expected.dtype in (np.int32, np.bool_):
         assert_bits(actual, expected, name)
-    elif op == "sqrt":
+    elif op in ("sqrt", "add_scalar", "subtract_scalar", "multiply_scalar", "divide_scalar"):
+        # IEEE 754 leaves the payload of an arithmetic NaN open: NaN positions
+        # must agree, every other bit must match.
         assert_nan_bits(actual, expected, name)
     elif op == "log":
         assert_close(actual, expected, 1e-6, 0.0, name)

@@ -49,6 +49,23 @@ def run_oracle(op, inputs, kw):
     if op == "attention":
         mask = inputs[3] if len(inputs) == 4 else None
         return oracle.attention(*inputs[:3], mask, kw.get("causal", False), kw.get("scale"))
+    if op in ("negative", "add_scalar", "subtract_scalar", "multiply_scalar", "divide_scalar"):
+        return oracle.scalar_op(op, inputs[0], kw.get("scalar", 0.0), kw.get("scalar_left", False))
+    if op == "astype":
+        return oracle.astype(inputs[0], kw["target_dtype"])
+    if op == "transpose":
+        return oracle.transpose(inputs[0], kw["perm"])
+    if op == "slice":
+        return oracle.slice_(inputs[0], kw["starts"], kw["steps"], kw["lengths"])
+    if op == "concat":
+        return oracle.concat(inputs, axis)
+    if op in ("any", "all"):
+        return oracle.bool_reduce(op, inputs[0], kw["axes"])
+    if op == "masked_select":
+        return oracle.masked_select(*inputs)
+    if op in ("equal", "not_equal", "less", "less_equal", "greater", "greater_equal", "logical_and",
+              "logical_or", "logical_xor", "logical_not", "where"):
+        return oracle.predicate(op, *inputs)
     raise AssertionError(op)
 
 
@@ -60,7 +77,7 @@ def expected_outputs(entry, arrays):
 
 def test_golden_vectors_bit_exact(golden):
     manifest, arrays = golden
-    assert len(manifest) > 500
+    assert len(manifest) > 600
     for entry in manifest:
         inputs = [arrays[k] for k in entry["inputs"]]
         if "error" in entry:
