@@ -83,6 +83,20 @@ int tcx_hip_allocate(size_t bytes, void** ptr, tcx_hip_pool_t** owner);
 /* Returns a block from tcx_hip_allocate: to its pool's cache when that pool
  * is still active and has room, else hipFree. Never fails the caller. */
 void tcx_hip_release(void* ptr, size_t bytes, tcx_hip_pool_t* owner);
+/* tcx_hip_release that never caches the block: storage that was exposed to
+ * another framework (DLPack export, copies included) may still be read by
+ * work on streams this library cannot see, so it goes straight back to
+ * hipFree, which waits for the device (the reference's exported-buffer rule,
+ * bindings/dlpack.cpp:204-206 and cuda_buffer.h:35). */
+void tcx_hip_release_uncached(void* ptr, size_t bytes, tcx_hip_pool_t* owner);
+
+/* Checks memory handed over by another framework before a tensor borrows it
+ * (replaces the checks of CudaBuffer::borrow, cuda_backend.cpp:106-144):
+ * [ptr, ptr + bytes) must be device memory of device 0 inside one allocation.
+ * Then it waits for all work on the device, so the producer's writes on any
+ * of its streams are complete before the borrowed storage is read. bytes == 0
+ * only waits. */
+int tcx_hip_borrow_check(const void* ptr, size_t bytes);
 
 /* Copies on `stream`, synchronised before return (cuda::from_cpu/to_cpu,
  * cuda_backend.cpp:215-264). */

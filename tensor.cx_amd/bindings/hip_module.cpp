@@ -15,22 +15,17 @@
 #include <string>
 #include <vector>
 
+#include "hip_binding.h"
 #include "tensorcx/backends/hip/hip_backend.h"
 #include "tensorcx/core/profiling.h"
 
 namespace py = pybind11;
 using namespace tensorcx;
 
+using tcx_bind::HipTensor;
+using tcx_bind::throw_status;
+
 namespace {
-
-struct HipTensor {
-  Tensor tensor;
-};
-
-[[noreturn]] void throw_status(const Status& status) {
-  if (status.code() == StatusCode::kInvalidArgument) throw py::value_error(status.message());
-  throw std::runtime_error(status.message());
-}
 
 DType parse_dtype(const std::string& name) {
   if (name == "float32") return DType::kFloat32;
@@ -229,10 +224,16 @@ PYBIND11_MODULE(_core, m) {
     t.strides = contiguous_strides(s);
     return HipTensor{std::move(t)};
   });
+  // True for the same storage range, False for disjoint storage; a partial
+  // overlap is an error (python_module.cpp:914-919).
   m.def("_shares_storage", [](const HipTensor& a, const HipTensor& b) {
-    return a.tensor.buffer && b.tensor.buffer &&
-           a.tensor.buffer->storage_relation(*b.tensor.buffer) != StorageRelation::kDisjoint;
+    if (!a.tensor.buffer || !b.tensor.buffer) return false;
+    const StorageRelation relation = a.tensor.buffer->storage_relation(*b.tensor.buffer);
+    if (relation == StorageRelation::kPartialOverlap)
+      throw py::value_error("kernel arguments have unsupported partial storage overlap");
+    return relation == StorageRelation::kSameRange;
   });
+  tcx_bind::bind_dlpack(m);
 
   m.def("matmul", [](const HipTensor& a, const HipTensor& b) { return run(OpDesc{OpKind::kMatmul}, {a.tensor, b.tensor}); });
   m.def("linear", [](const HipTensor& x, const HipTensor& w, std::optional<const HipTensor*> b) {

@@ -63,7 +63,7 @@ def build_backend() -> pathlib.Path:
     import pybind11
 
     cpp = PKG / "cpp"
-    sources = sorted((cpp / "tensorcx").rglob("*.cpp")) + [PKG / "bindings" / "hip_module.cpp"]
+    sources = sorted((cpp / "tensorcx").rglob("*.cpp")) + sorted((PKG / "bindings").glob("*.cpp"))
     include = [f"-I{cpp}", f"-I{ROOT / 'include'}", f"-I{pybind11.get_include()}",
                f"-I{sysconfig.get_paths()['include']}"]
     suffix = sysconfig.get_config_var("EXT_SUFFIX") or ".so"

@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdint>
 #include <cstring>
 #include <limits>
 #include <stdexcept>
@@ -86,6 +87,10 @@ Tensor make_tensor(DType dtype, Shape shape) {
   }
   return created.move_value();
 }
+
+// Fused kernels load 16 bytes at a time; borrowed storage may sit at any
+// element-aligned address, and then takes the unfused route.
+bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15U) == 0; }
 
 void* out_ptr(const Tensor& t) { return static_cast<HipBuffer*>(t.buffer.get())->data(); }
 
@@ -740,7 +745,8 @@ Tensor attention(const OpDesc& op, std::span<const Tensor> inputs, tcx_stream_t 
   const Shape qb(q.shape.begin(), q.shape.end() - 2);
   if (inputs.size() == 3 && qb == Shape(k.shape.begin(), k.shape.end() - 2) &&
       qb == Shape(v.shape.begin(), v.shape.end() - 2) &&
-      tcx_hip_flash_attention_supported(features, v.shape.back()) && numel(qb) <= 65535) {
+      tcx_hip_flash_attention_supported(features, v.shape.back()) && numel(qb) <= 65535 &&
+      aligned16(device_ptr(q)) && aligned16(device_ptr(k)) && aligned16(device_ptr(v))) {
     Tensor out = make_tensor(DType::kFloat32, shape);
     ok_or_throw(tcx_hip_flash_attention_f32(f32(q), f32(k), f32(v), static_cast<float*>(out_ptr(out)), numel(qb),
                                             rows, columns, features, *softmax.attention_scale, op.causal ? 1 : 0,
@@ -1005,9 +1011,28 @@ Expected<std::shared_ptr<HipBuffer>> HipBuffer::create(std::size_t bytes) {
   return buffer;
 }
 
+Expected<std::shared_ptr<HipBuffer>> HipBuffer::borrow(void* data, std::size_t bytes, std::shared_ptr<void> owner) {
+  if (!owner || (bytes != 0 && data == nullptr))
+    return Status(StatusCode::kInvalidArgument, "borrowed HIP storage requires an owner and data");
+  const int rc = tcx_hip_borrow_check(data, bytes);
+  if (rc != TCX_OK) return status_from_code(rc, "HIP borrow");
+  std::shared_ptr<HipBuffer> buffer(new HipBuffer());
+  buffer->data_ = bytes ? data : nullptr;
+  buffer->bytes_ = bytes;
+  buffer->external_ = std::move(owner);
+  return buffer;
+}
+
+StorageIdentity HipBuffer::storage_identity() const {
+  static const char device0 = 0;
+  return {&device0, reinterpret_cast<std::uintptr_t>(data_), bytes_};
+}
+
 HipBuffer::~HipBuffer() {
+  if (external_) return;  // the external owner's deleter runs when external_ goes
   ProfileScope span(ProfileCategory::kDeallocation, "hip_release", "hip", bytes_);
-  tcx_hip_release(data_, bytes_, owner_);
+  if (exported_.load(std::memory_order_relaxed)) tcx_hip_release_uncached(data_, bytes_, owner_);
+  else tcx_hip_release(data_, bytes_, owner_);
 }
 
 bool available() { return tcx_hip_init() == TCX_OK; }
@@ -1098,6 +1123,33 @@ Expected<Tensor> clone(const Tensor& tensor) {
       if (rc != TCX_OK) return status_from_code(rc, "HIP device copy");
     }
     return t;
+  } catch (const std::invalid_argument& error) {
+    return Status(StatusCode::kInvalidArgument, error.what());
+  }
+}
+
+Expected<Tensor> borrow(void* data, DType dtype, Shape shape, std::shared_ptr<void> owner) {
+  try {
+    if (dtype != DType::kFloat32 && dtype != DType::kInt32 && dtype != DType::kBool)
+      return Status(StatusCode::kInvalidArgument, "HIP tensors support float32, int32 and bool");
+    const auto bytes = static_cast<std::size_t>(numel(shape)) * dtype_size(dtype);
+    if (bytes && reinterpret_cast<std::uintptr_t>(data) % dtype_size(dtype))
+      return Status(StatusCode::kInvalidArgument, "borrowed HIP pointer is misaligned");
+    auto buffer = HipBuffer::borrow(data, bytes, std::move(owner));
+    if (!buffer) return buffer.status();
+    Shape strides = contiguous_strides(shape);
+    return Tensor{dtype, std::move(shape), std::move(strides), Device{"hip", 0},
+                  std::static_pointer_cast<Buffer>(buffer.move_value()), 0};
+  } catch (const std::invalid_argument& error) {
+    return Status(StatusCode::kInvalidArgument, error.what());
+  }
+}
+
+Expected<void*> export_storage(const Tensor& tensor) {
+  try {
+    void* data = device_ptr(tensor);
+    static_cast<HipBuffer*>(tensor.buffer.get())->mark_exported();
+    return data;
   } catch (const std::invalid_argument& error) {
     return Status(StatusCode::kInvalidArgument, error.what());
   }

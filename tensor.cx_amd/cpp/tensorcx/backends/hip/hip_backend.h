@@ -8,6 +8,7 @@
 // the boundary. All device work goes through the C ABI in tensorcx_hip.h.
 #pragma once
 
+#include <atomic>
 #include <cstddef>
 #include <memory>
 #include <string>
@@ -18,22 +19,36 @@
 
 namespace tensorcx::hip {
 
-// Device memory owned by a hip tensor; returned to its pool (or freed) when
-// the last tensor referring to it goes away.
+// Device memory of a hip tensor. Owned memory returns to its pool (or is
+// freed) when the last tensor referring to it goes away; borrowed memory
+// (another framework's, through DLPack) releases its external owner instead.
+// Mirrors CudaBuffer (reference backends/cuda/cuda_buffer.h:22-42).
 class HipBuffer final : public Buffer {
  public:
   static Expected<std::shared_ptr<HipBuffer>> create(std::size_t bytes);
+  // Wraps `bytes` of device-0 memory at `data`, kept alive by `owner`, after
+  // tcx_hip_borrow_check (CudaBuffer::borrow, cuda_backend.cpp:106-144).
+  static Expected<std::shared_ptr<HipBuffer>> borrow(void* data, std::size_t bytes, std::shared_ptr<void> owner);
   ~HipBuffer() override;
   HipBuffer(const HipBuffer&) = delete;
   HipBuffer& operator=(const HipBuffer&) = delete;
   std::size_t nbytes() const override { return bytes_; }
+  // Device memory is one address space: identity is the address range, so
+  // independently wrapped views of the same memory relate as the reference's
+  // CudaBuffer::storage_relation does (cuda_backend.cpp:87-98).
+  StorageIdentity storage_identity() const override;
   void* data() const { return data_; }
+  bool borrowed() const { return external_ != nullptr; }
+  // Storage seen by another framework never returns to a pool cache.
+  void mark_exported() { exported_.store(true, std::memory_order_relaxed); }
 
  private:
   HipBuffer() = default;
   void* data_{nullptr};
   std::size_t bytes_{0};
   tcx_hip_pool_t* owner_{nullptr};
+  std::shared_ptr<void> external_;
+  std::atomic<bool> exported_{false};
 };
 
 class HipBackend final : public Backend {
@@ -60,6 +75,12 @@ Expected<Tensor> from_host(const void* host, DType dtype, Shape shape);
 Status to_host(const Tensor& tensor, void* host, std::size_t bytes);
 // A new device tensor with the same contents (independent storage).
 Expected<Tensor> clone(const Tensor& tensor);
+// A contiguous hip tensor over another framework's device-0 memory, kept
+// alive by `owner` (the CUDA import of bindings/dlpack.cpp:142-153).
+Expected<Tensor> borrow(void* data, DType dtype, Shape shape, std::shared_ptr<void> owner);
+// The device address of a contiguous hip tensor handed to another framework;
+// its storage is marked exported (bindings/dlpack.cpp:193-207).
+Expected<void*> export_storage(const Tensor& tensor);
 
 // Built-in kernels reachable through BackendOpClass::kKernel with
 // KernelArtifactKind::kStaticLibrary and artifact kStaticArtifact:

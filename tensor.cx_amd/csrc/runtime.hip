@@ -153,11 +153,11 @@ int pool_allocate(tcx_hip_pool* pool, size_t bytes, void** ptr) {
   return TCX_OK;
 }
 
-void pool_release(tcx_hip_pool* pool, void* ptr, size_t bytes) {
+void pool_release(tcx_hip_pool* pool, void* ptr, size_t bytes, bool allow_cache) {
   {
     std::lock_guard lock(pool->mutex);
     pool->stats.in_use_bytes -= bytes;
-    bool cache = pool->stats.active && pool->cached.size() < pool->stats.max_cached_blocks &&
+    bool cache = allow_cache && pool->stats.active && pool->cached.size() < pool->stats.max_cached_blocks &&
                  bytes <= pool->stats.max_cached_bytes - pool->stats.cached_bytes;
     if (cache && pool->default_runtime && tcx::thread_stream != nullptr &&
         hipStreamQuery(tcx::thread_stream) != hipSuccess) {
@@ -275,10 +275,45 @@ int tcx_hip_allocate(size_t bytes, void** ptr, tcx_hip_pool_t** owner) {
 void tcx_hip_release(void* ptr, size_t bytes, tcx_hip_pool_t* owner) {
   if (ptr == nullptr) return;
   if (owner != nullptr) {
-    pool_release(owner, ptr, bytes);
+    pool_release(owner, ptr, bytes, true);
     return;
   }
   (void)hipFree(ptr);
+}
+
+void tcx_hip_release_uncached(void* ptr, size_t bytes, tcx_hip_pool_t* owner) {
+  if (ptr == nullptr) return;
+  if (owner != nullptr) {
+    pool_release(owner, ptr, bytes, false);
+    return;
+  }
+  (void)hipFree(ptr);
+}
+
+int tcx_hip_borrow_check(const void* ptr, size_t bytes) {
+  const int status = tcx::ready();
+  if (status != TCX_OK) return status;
+  if (bytes != 0) {
+    if (ptr == nullptr) return tcx::fail(TCX_INVALID_ARGUMENT, "borrowed HIP storage requires data");
+    hipPointerAttribute_t attributes{};
+    if (hipPointerGetAttributes(&attributes, ptr) != hipSuccess) {
+      (void)hipGetLastError();  // an unknown pointer is an argument error, not a sticky one
+      return tcx::fail(TCX_INVALID_ARGUMENT, "invalid borrowed HIP pointer");
+    }
+    if (attributes.type != hipMemoryTypeDevice || attributes.device != 0)
+      return tcx::fail(TCX_INVALID_ARGUMENT, "borrowed HIP pointer must be device memory of device 0");
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, const_cast<void*>(ptr)) != hipSuccess) {
+      (void)hipGetLastError();
+      return tcx::fail(TCX_INVALID_ARGUMENT, "borrowed HIP pointer has no allocation range");
+    }
+    const auto begin = reinterpret_cast<std::uintptr_t>(base), at = reinterpret_cast<std::uintptr_t>(ptr);
+    if (at < begin || at - begin > size || bytes > size - (at - begin))
+      return tcx::fail(TCX_INVALID_ARGUMENT, "borrowed HIP range exceeds its allocation");
+  }
+  // The producer may have queued its writes on any of its streams.
+  return tcx::check(hipDeviceSynchronize(), "borrowed HIP readiness");
 }
 
 static int copy(void* dst, const void* src, size_t bytes, hipMemcpyKind kind, tcx_stream_t stream,

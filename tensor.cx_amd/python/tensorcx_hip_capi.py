@@ -30,7 +30,7 @@ MAX_BATCH_RANK = 8
 EXPORTS = [
     "tcx_hip_last_error", "tcx_hip_init", "tcx_hip_device_count", "tcx_hip_device_info",
     "tcx_hip_stream", "tcx_hip_stream_synchronize", "tcx_hip_allocate", "tcx_hip_release",
-    "tcx_hip_memcpy_h2d", "tcx_hip_memcpy_d2h", "tcx_hip_memcpy_d2d", "tcx_hip_pool_create",
+    "tcx_hip_release_uncached", "tcx_hip_borrow_check", "tcx_hip_memcpy_h2d", "tcx_hip_memcpy_d2h", "tcx_hip_memcpy_d2d", "tcx_hip_pool_create",
     "tcx_hip_pool_enter", "tcx_hip_pool_exit", "tcx_hip_pool_trim", "tcx_hip_pool_stats",
     "tcx_hip_pool_destroy", "tcx_hip_event_create", "tcx_hip_event_record",
     "tcx_hip_event_synchronize", "tcx_hip_event_elapsed_ms", "tcx_hip_event_destroy",
