@@ -75,23 +75,36 @@ __device__ __forceinline__ void load_frag(const float* row, int r, int sw, float
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int kMinWaves, bool kTransB, bool kVec>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64)
+// KS > 1 splits K inside the block: KS groups of waves each cover the whole
+// block tile, group g taking rows [g*BK, (g+1)*BK) of every staged k-tile of
+// KS*BK, and the groups' partial tiles are added through LDS in group order at
+// the end (deterministic). It multiplies the waves per CU for shapes with few
+// output tiles without any extra HBM traffic.
+template <int BM, int BN, int BK, int WM, int WN, int kMinWaves, bool kTransB, bool kVec, int KS = 1>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64 * KS)
 __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs a) {
   constexpr int kWavesN = BN / WN;
-  constexpr int kThreads = (BM / WM) * kWavesN * 64;
+  constexpr int kGroupWaves = (BM / WM) * kWavesN;  // waves covering the block tile once
+  constexpr int kThreads = kGroupWaves * 64 * KS;
+  constexpr int BKT = BK * KS;  // k extent staged per iteration
   constexpr int TM = WM / 16, TN = WN / 16;
   constexpr int LDA = BM + 8, LDB = BN + 8;
-  static_assert(BK % 4 == 0 && (BM * BK) % (4 * kThreads) == 0 && (BN * BK) % (4 * kThreads) == 0);
-  constexpr int kAVec = BM * BK / 4 / kThreads;  // float4 loads per thread for A
-  constexpr int kBVec = BN * BK / 4 / kThreads;
-  constexpr int kAScalar = BM * BK / kThreads;
-  constexpr int kBScalar = BN * BK / kThreads;
+  static_assert(BK % 4 == 0 && (BM * BKT) % (4 * kThreads) == 0 && (BN * BKT) % (4 * kThreads) == 0);
+  constexpr int kAVec = BM * BKT / 4 / kThreads;  // float4 loads per thread for A
+  constexpr int kBVec = BN * BKT / 4 / kThreads;
+  constexpr int kAScalar = BM * BKT / kThreads;
+  constexpr int kBScalar = BN * BKT / kThreads;
   constexpr int kAReg = kVec ? kAVec * 4 : kAScalar;
   constexpr int kBReg = kVec ? kBVec * 4 : kBScalar;
+  constexpr int kElems = TM * TN * 4;  // accumulator floats per lane
+  constexpr int kStage = 2 * BKT * (LDA + LDB);
+  constexpr int kReduce = (KS - 1) * kGroupWaves * kElems * 64;
 
-  __shared__ float As[2][BK][LDA];
-  __shared__ float Bs[2][BK][LDB];
+  // Two staging buffers for A and B; after the k loop the same memory holds
+  // the split-K partial tiles.
+  __shared__ float smem[kStage > kReduce ? kStage : kReduce];
+  auto As = reinterpret_cast<float (*)[BKT][LDA]>(smem);
+  auto Bs = reinterpret_cast<float (*)[BKT][LDB]>(smem + 2 * BKT * LDA);
 
   // Blocks go round-robin to the 8 XCDs; give each XCD a contiguous run of
   // tile ids so the blocks sharing an L2 also share A row panels and B column
@@ -135,7 +148,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
 #pragma unroll
       for (int p = 0; p < kAVec; ++p) {
         const int idx = tid + p * kThreads;
-        const int row = idx / (BK / 4), kq = idx % (BK / 4);
+        const int row = idx / (BKT / 4), kq = idx % (BKT / 4);
         const std::int64_t gm_ = m0 + row, gk = k0 + kq * 4;
         float4_t v = {0.F, 0.F, 0.F, 0.F};
         if (gm_ < M && gk < K) v = *reinterpret_cast<const float4_t*>(A + gm_ * K + gk);
@@ -146,7 +159,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
         const int idx = tid + p * kThreads;
         float4_t v = {0.F, 0.F, 0.F, 0.F};
         if constexpr (kTransB) {
-          const int row = idx / (BK / 4), kq = idx % (BK / 4);
+          const int row = idx / (BKT / 4), kq = idx % (BKT / 4);
           const std::int64_t gn = n0 + row, gk = k0 + kq * 4;
           if (gn < N && gk < K) v = *reinterpret_cast<const float4_t*>(B + gn * K + gk);
         } else {
@@ -160,7 +173,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
 #pragma unroll
       for (int p = 0; p < kAScalar; ++p) {
         const int idx = tid + p * kThreads;
-        const int row = idx / BK, kk = idx % BK;
+        const int row = idx / BKT, kk = idx % BKT;
         const std::int64_t gm_ = m0 + row, gk = k0 + kk;
         ra[p] = (gm_ < M && gk < K) ? A[gm_ * K + gk] : 0.F;
       }
@@ -168,7 +181,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
       for (int p = 0; p < kBScalar; ++p) {
         const int idx = tid + p * kThreads;
         if constexpr (kTransB) {
-          const int row = idx / BK, kk = idx % BK;
+          const int row = idx / BKT, kk = idx % BKT;
           const std::int64_t gn = n0 + row, gk = k0 + kk;
           rb[p] = (gn < N && gk < K) ? B[gn * K + gk] : 0.F;
         } else {
@@ -186,17 +199,17 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
 #pragma unroll
       for (int p = 0; p < kAVec; ++p) {
         const int idx = tid + p * kThreads;
-        const int row = idx / (BK / 4), kq = idx % (BK / 4);
+        const int row = idx / (BKT / 4), kq = idx % (BKT / 4);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) As[buf][kq * 4 + q][swz<BK>(kq * 4 + q, row)] = ra[4 * p + q];
+        for (int q = 0; q < 4; ++q) As[buf][kq * 4 + q][swz<BKT>(kq * 4 + q, row)] = ra[4 * p + q];
       }
 #pragma unroll
       for (int p = 0; p < kBVec; ++p) {
         const int idx = tid + p * kThreads;
         if constexpr (kTransB) {
-          const int row = idx / (BK / 4), kq = idx % (BK / 4);
+          const int row = idx / (BKT / 4), kq = idx % (BKT / 4);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) Bs[buf][kq * 4 + q][swz<BK>(kq * 4 + q, row)] = rb[4 * p + q];
+          for (int q = 0; q < 4; ++q) Bs[buf][kq * 4 + q][swz<BKT>(kq * 4 + q, row)] = rb[4 * p + q];
         } else {
           const int krow = idx / (BN / 4), nq = idx % (BN / 4);
           const float4_t v = {rb[4 * p], rb[4 * p + 1], rb[4 * p + 2], rb[4 * p + 3]};
@@ -207,13 +220,13 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
 #pragma unroll
       for (int p = 0; p < kAScalar; ++p) {
         const int idx = tid + p * kThreads;
-        As[buf][idx % BK][swz<BK>(idx % BK, idx / BK)] = ra[p];
+        As[buf][idx % BKT][swz<BKT>(idx % BKT, idx / BKT)] = ra[p];
       }
 #pragma unroll
       for (int p = 0; p < kBScalar; ++p) {
         const int idx = tid + p * kThreads;
         if constexpr (kTransB)
-          Bs[buf][idx % BK][swz<BK>(idx % BK, idx / BK)] = rb[p];
+          Bs[buf][idx % BKT][swz<BKT>(idx % BKT, idx / BKT)] = rb[p];
         else
           Bs[buf][idx / BN][idx % BN] = rb[p];
       }
@@ -221,7 +234,8 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
   };
 
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / kWavesN, wn = wave % kWavesN;
+  const int group = wave / kGroupWaves, gwave = wave % kGroupWaves;
+  const int wm = gwave / kWavesN, wn = gwave % kWavesN;
   const int r = lane & 15, kl = lane >> 4;
   floatx4 acc[TM][TN];
 #pragma unroll
@@ -229,20 +243,22 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.F, 0.F, 0.F, 0.F};
 
-  const std::int64_t k_tiles = (K + BK - 1) / BK;
+  // Tile kt+1 sits in registers while tile kt's MFMAs run; its LDS stores
+  // and the global loads of tile kt+2 both go before the barrier, so after
+  // the barrier a wave only waits for its first fragment reads.
+  const std::int64_t k_tiles = (K + BKT - 1) / BKT;
   if (k_tiles > 0) {
     load_tile(0);
     store_tile(0);
+    if (k_tiles > 1) load_tile(BKT);
     __syncthreads();
   }
   for (std::int64_t kt = 0; kt < k_tiles; ++kt) {
     const int buf = static_cast<int>(kt & 1);
-    const bool more = kt + 1 < k_tiles;
-    if (more) load_tile((kt + 1) * BK);
 #pragma unroll
     for (int s = 0; s < BK / 4; ++s) {
-      const int k = s * 4 + kl;
-      const int sw = swz<BK>(k, 0);
+      const int k = group * BK + s * 4 + kl;
+      const int sw = swz<BKT>(k, 0);
       float av[TM], bv[TN];
       load_frag<TM>(&As[buf][k][wm * WM], r, sw, av);
       load_frag<TN>(&Bs[buf][k][wn * WN], r, kTransB ? sw : 0, bv);
@@ -252,8 +268,36 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
         for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
     }
-    if (more) store_tile(buf ^ 1);
+    if (kt + 1 < k_tiles) store_tile(buf ^ 1);
+    if (kt + 2 < k_tiles) load_tile((kt + 2) * BKT);
     __syncthreads();
+  }
+  if constexpr (KS > 1) {
+    // Groups 1..KS-1 hand their partial tiles to group 0 through LDS (free
+    // after the loop's last barrier, or unused when K == 0); group 0 adds
+    // them in group order and alone runs the epilogue.
+    float* red = smem;
+    auto slot = [&](int g, int i, int j, int q) {
+      return (((g - 1) * kGroupWaves + gwave) * kElems + (i * TN + j) * 4 + q) * 64 + lane;
+    };
+    if (group > 0) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) red[slot(group, i, j, q)] = acc[i][j][q];
+    }
+    __syncthreads();
+    if (group > 0) return;
+#pragma unroll
+    for (int g = 1; g < KS; ++g)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) acc[i][j][q] += red[slot(g, i, j, q)];
   }
 
   // Epilogue: bias add then activation, as kAdd then kSilu/kGelu would round.
@@ -303,7 +347,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
   }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int kMinWaves, bool kVecOnly = false>
+template <int BM, int BN, int BK, int WM, int WN, int kMinWaves, bool kVecOnly = false, int KS = 1>
 int launch_config(GemmArgs& args, bool trans_b, bool vec, hipStream_t stream) {
   args.tiles_m = (args.m + BM - 1) / BM;
   args.tiles_n = (args.n + BN - 1) / BN;
@@ -311,23 +355,23 @@ int launch_config(GemmArgs& args, bool trans_b, bool vec, hipStream_t stream) {
   args.total_tiles = args.tiles_m * args.tiles_n * batches;
   if (args.total_tiles > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
   const dim3 grid(static_cast<unsigned>(args.total_tiles));
-  const dim3 block((BM / WM) * (BN / WN) * 64);
+  const dim3 block((BM / WM) * (BN / WN) * 64 * KS);
   if constexpr (kVecOnly) {
     if (!vec) return fail(TCX_INTERNAL, "gemm tile requires 16-byte aligned operands");
     if (trans_b)
-      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, true, true>), grid, block, 0, stream, args);
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, true, true, KS>), grid, block, 0, stream, args);
     else
-      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, false, true>), grid, block, 0, stream, args);
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, false, true, KS>), grid, block, 0, stream, args);
   } else if (trans_b) {
     if (vec)
-      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, true, true>), grid, block, 0, stream, args);
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, true, true, KS>), grid, block, 0, stream, args);
     else
-      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, true, false>), grid, block, 0, stream, args);
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, true, false, KS>), grid, block, 0, stream, args);
   } else {
     if (vec)
-      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, false, true>), grid, block, 0, stream, args);
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, false, true, KS>), grid, block, 0, stream, args);
     else
-      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, false, false>), grid, block, 0, stream, args);
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WM, WN, kMinWaves, false, false, KS>), grid, block, 0, stream, args);
   }
   return check(hipGetLastError(), "gemm_f32 launch");
 }
