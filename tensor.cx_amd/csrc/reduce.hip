@@ -173,7 +173,84 @@ __global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, 
     };
     const int len = static_cast<int>(end - begin);
     const T* __restrict__ q = p + begin;
-    if constexpr (kVec) {
+    bool exact = true;  // run the exact scan below
+    int fast_index = -1;  // fast path result (segment-relative index, value)
+    T fast_value{};
+    if constexpr (kVec && __is_same(T, float)) {
+      // Fast float path: four independent (value, index) chains per lane, one
+      // per float4 component, each seeing its elements in increasing index
+      // order. A strict compare keeps the earlier index on ties and treats +0
+      // and -0 as equal, which is the reference's rule for NaN-free data.
+      // NaNs are only flagged here: a wave that saw one re-scans its segment
+      // with the exact loop.
+      // Chain c of this lane holds element lane*4 + c + cr[c]; the offsets r
+      // stepped through are wave-uniform, so they live in scalar registers.
+      // Chains start at -inf (+inf for min) with no element: one that never
+      // takes an element saw only that infinity (or a NaN, which the re-scan
+      // handles), so its candidate is its first element.
+      constexpr float kStart = kLargest ? -__builtin_inff() : __builtin_inff();
+      float cb[4] = {kStart, kStart, kStart, kStart};
+      int cr[4] = {-1, -1, -1, -1};
+      bool nan_seen = false;
+      const int lane4 = lane * 4;
+      auto step = [&](int c, float v, int r) {
+        const bool take = kLargest ? v > cb[c] : v < cb[c];
+        cb[c] = take ? v : cb[c];
+        cr[c] = take ? r : cr[c];
+        nan_seen |= v != v;
+      };
+      int r = 0;
+      // Every lane's four groups are in range while r + 1024 <= len.
+      for (; r + 1024 <= len; r += 1024) {
+        const vec4<float> a = stream_load(reinterpret_cast<const vec4<float>*>(q + lane4 + r));
+        const vec4<float> b = stream_load(reinterpret_cast<const vec4<float>*>(q + lane4 + r + 256));
+        const vec4<float> c = stream_load(reinterpret_cast<const vec4<float>*>(q + lane4 + r + 512));
+        const vec4<float> d = stream_load(reinterpret_cast<const vec4<float>*>(q + lane4 + r + 768));
+        step(0, a.x, r); step(1, a.y, r); step(2, a.z, r); step(3, a.w, r);
+        step(0, b.x, r + 256); step(1, b.y, r + 256); step(2, b.z, r + 256); step(3, b.w, r + 256);
+        step(0, c.x, r + 512); step(1, c.y, r + 512); step(2, c.z, r + 512); step(3, c.w, r + 512);
+        step(0, d.x, r + 768); step(1, d.y, r + 768); step(2, d.z, r + 768); step(3, d.w, r + 768);
+      }
+      for (; r < len; r += 256) {
+        if (lane4 + r < len) {
+          const vec4<float> a = stream_load(reinterpret_cast<const vec4<float>*>(q + lane4 + r));
+          step(0, a.x, r); step(1, a.y, r); step(2, a.z, r); step(3, a.w, r);
+        }
+      }
+      exact = __any(nan_seen);
+      if (!exact) {
+        // NaN-free wave: one order-preserving 64-bit key per candidate, the
+        // value (+0 and -0 merged) above the complemented index, so a plain
+        // maximum picks the extreme value and, among equal ones, the lowest
+        // index. Key 0 means no candidate (real keys are >= 2^32).
+        auto key_of = [](float v, int idx) -> std::uint64_t {
+          std::uint32_t u = to_bits(v);
+          if (u == 0x80000000U) u = 0;
+          u = (u & 0x80000000U) ? ~u : (u | 0x80000000U);
+          if constexpr (!kLargest) u = ~u;
+          return (static_cast<std::uint64_t>(u) << 32) | (0xFFFFFFFFU - static_cast<std::uint32_t>(idx));
+        };
+        std::uint64_t key = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const std::uint64_t k = lane4 < len ? key_of(cb[c], lane4 + c + (cr[c] < 0 ? 0 : cr[c])) : 0;
+          key = k > key ? k : key;
+        }
+#pragma unroll
+        for (int offset = 32; offset > 0; offset >>= 1) {
+          const std::uint64_t o = __shfl_xor(key, offset, kWave);
+          key = o > key ? o : key;
+        }
+        // The winning element sits in chain (win & 3) of lane (win & 255) / 4;
+        // its own bits give the value (and the sign of a zero).
+        fast_index = key ? static_cast<int>(0xFFFFFFFFU - static_cast<std::uint32_t>(key)) : -1;
+        const int c = fast_index & 3;
+        const float mine = c == 0 ? cb[0] : c == 1 ? cb[1] : c == 2 ? cb[2] : cb[3];
+        fast_value = __shfl(mine, (fast_index & 255) >> 2, kWave);
+      }
+    }
+    if (!exact) {
+    } else if constexpr (kVec) {
       int j = lane * 4;
       for (; j + 3 * 256 < len; j += 4 * 256) {
         const vec4<T> a = stream_load(reinterpret_cast<const vec4<T>*>(q + j));
@@ -192,8 +269,14 @@ __global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, 
     } else {
       for (int j = lane; j < len; j += 64) visit(q[j], j);
     }
-    std::int64_t bi = li < 0 ? -1 : begin + li;
-    wave_extremum<T, kLargest>(best, bi);
+    std::int64_t bi;
+    if (!exact) {
+      best = fast_value;
+      bi = fast_index < 0 ? -1 : begin + fast_index;
+    } else {
+      bi = li < 0 ? -1 : begin + li;
+      wave_extremum<T, kLargest>(best, bi);
+    }
     if (lane == 0) {
       if (segments == 1) {
         if constexpr (kOp == TCX_REDUCE_ARGMAX)

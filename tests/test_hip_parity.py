@@ -132,6 +132,42 @@ def test_extrema_ties_nan_and_signed_zero(cx):
         assert_bits(getattr(cx, op)(h, None).numpy(), getattr(oracle, op)(x, None), f"{op} all")
 
 
+@pytest.mark.parametrize("width", [1024, 1028, 4096, 32768])
+def test_extrema_special_values_vector_rows(cx, width):
+    """16-byte rows: ties across float4 components, lanes and loop steps, signed
+    zeros, infinities and NaNs (which send the wave to the exact re-scan)."""
+    rows = 12
+    x = np.zeros((rows, width), np.float32)
+    x[0, 5] = x[0, 6] = 3.0                       # tie inside one lane's float4
+    x[1, 7] = x[1, 3] = 3.0                       # tie across lanes
+    x[2, 8 + 256] = x[2, 8] = 3.0                 # tie across loop steps
+    x[3, :] = -0.0
+    x[3, width // 2] = 0.0                        # +0/-0 equal: first (-0) kept
+    x[4, :] = -np.inf
+    x[5, :] = np.inf
+    x[6, 300], x[6, 10] = np.nan, -1.0
+    x[6, width - 1] = np.float32(np.nan) * -1     # a second NaN later
+    x[7, width - 1] = 9.0                         # extreme at the last element
+    x[7, width - 4] = -9.0
+    x[8, width - 2] = np.nan                      # NaN in the tail group only
+    x[9] = np.random.default_rng(12).integers(-3, 4, width)  # many ties
+    x[10, ::97] = 5.0
+    x[10, ::89] = -5.0
+    x[11] = np.random.default_rng(13).standard_normal(width)
+    h = cx.tensor(x, device="hip")
+    for op in ("max", "min", "argmax"):
+        assert_bits(getattr(cx, op)(h, 1).numpy(), getattr(oracle, op)(x, 1), f"{op} width {width}")
+    # One long row split into segments, with a NaN in a late segment.
+    y = np.random.default_rng(14).integers(-2, 3, 1 << 20).astype(np.float32)
+    hy = cx.tensor(y, device="hip")
+    for op in ("max", "min", "argmax"):
+        assert_bits(getattr(cx, op)(hy, None).numpy(), getattr(oracle, op)(y, None), f"{op} long row")
+    y[777777] = np.nan
+    hy = cx.tensor(y, device="hip")
+    for op in ("max", "min", "argmax"):
+        assert_bits(getattr(cx, op)(hy, None).numpy(), getattr(oracle, op)(y, None), f"{op} long row NaN")
+
+
 def test_int32_reductions_wrap(cx):
     rng = np.random.default_rng(3)
     x = rng.integers(-2**31, 2**31 - 1, size=(300, 1031), dtype=np.int64).astype(np.int32)
