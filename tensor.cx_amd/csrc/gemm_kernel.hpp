@@ -347,6 +347,215 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
   }
 }
 
+// Full-tile GEMM with global -> LDS direct loads (buffer_load ... lds), for
+// B given as [k, n] when every tile is full, rows are 16-byte aligned and the
+// grid is at least one round. Each tile's loads are issued into the other
+// LDS stage right after a barrier and land while the current stage's MFMAs
+// run: no staging registers, no LDS store instructions, no wait before the
+// barrier beyond the loads themselves.
+//
+// LDS layout: A m-major ([m][k], the eight 16-byte chunks of a 32-wide row
+// XOR-swizzled by (m / 2) % 8, so both the DMA writes and the fragment reads
+// are conflict-free), B k-major with rows padded by 8 floats. One wave
+// instruction fills 8 rows of A (64 lanes x 16 B, contiguous) or one row of
+// B. A lane reads 4 consecutive k of one A row in one ds_read_b128, so inside
+// each 16-k group MFMA step s of lane group kl uses k = 4 * kl + s for A and B
+// alike (a permutation of the k order, covered by the parity bound).
+//
+// The two stages are separate LDS arrays and the k loop handles them in
+// pairs. The loads are issued as assembly: the compiler adds no waits for
+// them, and the loop waits (vmcnt 0) right before each barrier.
+template <int BM, int BN, int BK, int WM, int WN, int kMinWaves>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64)
+__attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(GemmArgs a) {
+  constexpr int kWavesN = BN / WN, kWaves = (BM / WM) * kWavesN;
+  constexpr int TM = WM / 16, TN = WN / 16;
+  constexpr int LDB = BN + 8;
+  constexpr int kChunks = BK / 4;
+  static_assert(kChunks == 8 && BN == 256 && TN % 4 == 0, "one wave instruction = 8 rows of A or one row of B");
+  constexpr int kARows = 64 / kChunks;          // A rows per wave instruction
+  constexpr int kAInst = BM / kARows / kWaves;  // A instructions per wave and tile
+  constexpr int kBInst = BK / kWaves;           // B instructions per wave and tile
+  static_assert(kAInst * kARows * kWaves == BM && kBInst * kWaves == BK);
+  __shared__ float A0[BM][BK], A1[BM][BK];
+  __shared__ float B0[BK][LDB], B1[BK][LDB];
+
+  // Same XCD-aware tile order as gemm_f32_kernel.
+  const std::int64_t grid = a.total_tiles;
+  const std::int64_t bid = blockIdx.x;
+  const std::int64_t tile = (grid % 8 == 0) ? (bid % 8) * (grid / 8) + bid / 8 : bid;
+  const std::int64_t per_batch = a.tiles_m * a.tiles_n;
+  const std::int64_t batch = tile / per_batch;
+  const std::int64_t t = tile % per_batch;
+  constexpr std::int64_t kGroupM = 8;
+  const std::int64_t group_tiles = kGroupM * a.tiles_n;
+  const std::int64_t first_m = (t / group_tiles) * kGroupM;
+  const std::int64_t gm = min(a.tiles_m - first_m, kGroupM);
+  const std::int64_t tm = first_m + (t % group_tiles) % gm;
+  const std::int64_t tn = (t % group_tiles) / gm;
+  std::int64_t lhs_off = 0, rhs_off = 0;
+  {
+    std::int64_t b = batch;
+    for (int ax = a.batch_rank - 1; ax >= 0; --ax) {
+      const std::int64_t e = a.batch_shape[ax];
+      const std::int64_t c = b % e;
+      b /= e;
+      lhs_off += c * a.lhs_bs[ax];
+      rhs_off += c * a.rhs_bs[ax];
+    }
+  }
+  const std::int64_t M = a.m, N = a.n, K = a.k;
+  const float* __restrict__ A = a.lhs + lhs_off;
+  const float* __restrict__ B = a.rhs + rhs_off;
+  float* __restrict__ C = a.out + batch * M * N;
+  const std::int64_t m0 = tm * BM, n0 = tn * BN;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  auto achunk = [](int row, int kc) { return kc ^ ((row >> 1) & 7); };
+
+  // Buffer resources based at the block's A row panel and B column panel; a
+  // 32-bit byte offset per lane and a scalar offset per instruction and tile
+  // (the launcher checks that both panels span less than 2^31 bytes).
+  using int4v = int __attribute__((ext_vector_type(4)));
+  auto rsrc_of = [](const float* base) {
+    const auto addr = reinterpret_cast<std::uint64_t>(base);
+    return int4v{static_cast<int>(addr), static_cast<int>(addr >> 32), 0x7fffffff, 0x00020000};
+  };
+  const int4v a_rsrc = rsrc_of(A + m0 * K);
+  const int4v b_rsrc = rsrc_of(B + n0);
+  // Lane of instruction p writes A row (p * kWaves + wave) * 8 + lane / 8; the
+  // chunk swizzle of that row does not depend on p.
+  const int a_row = wave * kARows + lane / kChunks;
+  const int a_voff = (a_row * static_cast<int>(K) + 4 * achunk(a_row, lane % kChunks)) * 4;
+  const int b_voff = (wave * static_cast<int>(N) + 4 * lane) * 4;
+  auto lds_of = [](const void* p) {
+    return static_cast<unsigned>(reinterpret_cast<std::uintptr_t>((__attribute__((address_space(3))) const void*)p));
+  };
+  // 16 bytes per lane from rsrc + voff + soff into LDS at lds_byte + 16 * lane.
+  // M0 is reserved by the compiler (clang warns about naming it) and only
+  // these loads use it here; listing it records that the asm writes it.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  auto dma16 = [](const int4v& rsrc, unsigned lds_byte, int voff, int soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :: "s"(lds_byte), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
+  };
+#pragma clang diagnostic pop
+  auto issue = [&](float (&As)[BM][BK], float (&Bs)[BK][LDB], int k0) {
+    __builtin_amdgcn_sched_barrier(0);
+    const unsigned a_lds = lds_of(&As[0][0]) + static_cast<unsigned>(wave * kARows * BK * 4);
+    const unsigned b_lds = lds_of(&Bs[0][0]) + static_cast<unsigned>(wave * LDB * 4);
+#pragma unroll
+    for (int p = 0; p < kAInst; ++p)
+      dma16(a_rsrc, a_lds + p * kWaves * kARows * BK * 4, a_voff,
+            __builtin_amdgcn_readfirstlane((p * kWaves * kARows * static_cast<int>(K) + k0) * 4));
+#pragma unroll
+    for (int p = 0; p < kBInst; ++p)
+      dma16(b_rsrc, b_lds + p * kWaves * LDB * 4, b_voff,
+            __builtin_amdgcn_readfirstlane((p * kWaves + k0) * static_cast<int>(N) * 4));
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
+  const int r = lane & 15, kl = lane >> 4;
+  floatx4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.F, 0.F, 0.F, 0.F};
+
+  // Block i of the wave covers tile rows 16 i + (0..15); B columns keep the
+  // frag_pos map (16-byte fragment reads and output stores).
+  auto compute = [&](const float (&As)[BM][BK], const float (&Bs)[BK][LDB]) {
+#pragma unroll
+    for (int g = 0; g < BK / 16; ++g) {
+      __builtin_amdgcn_sched_barrier(0);
+      float4_t a4[TM];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = wm * WM + 16 * i + r;
+        a4[i] = *reinterpret_cast<const float4_t*>(&As[row][achunk(row, g * 4 + kl) * 4]);
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        float bv[TN];
+        load_frag<TN>(&Bs[g * 16 + 4 * kl + s][wn * WN], r, 0, bv);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[i][s], bv[j], acc[i][j], 0, 0, 0);
+      }
+    }
+  };
+
+  const int k_tiles = static_cast<int>(K / BK);
+  issue(A0, B0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  // Pairs of k-tiles: stage 0 is read while stage 1 loads, then the reverse.
+  int kt = 0;
+  for (; kt + 2 <= k_tiles; kt += 2) {
+    issue(A1, B1, (kt + 1) * BK);
+    compute(A0, B0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (kt + 2 < k_tiles) issue(A0, B0, (kt + 2) * BK);
+    compute(A1, B1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  if (kt < k_tiles) compute(A0, B0);  // odd count: the last tile sits in stage 0
+
+  // Epilogue as in gemm_f32_kernel (full tiles: no bounds checks).
+  const std::int64_t col_base = n0 + wn * WN;
+  float bias[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) bias[j] = a.bias != nullptr ? a.bias[col_base + frag_pos<TN>(r, j)] : 0.F;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const std::int64_t row = m0 + wm * WM + 16 * i + kl * 4 + q;
+      float v[TN];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        float x = acc[i][j][q];
+        if (a.bias != nullptr) x = x + bias[j];
+        v[j] = activate(x, a.activation);
+      }
+      float* dst = C + row * N + col_base;
+#pragma unroll
+      for (int g = 0; g < TN / 4; ++g)
+        *reinterpret_cast<float4_t*>(dst + g * 64 + r * 4) = float4_t{v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
+    }
+  }
+}
+
+// True when gemm_f32_direct_kernel<BM, BN, BK, ...> can take the problem:
+// full tiles, k > 0, and byte offsets inside one A row panel (BM x K) and one
+// B column panel (K x N) below 2^31.
+template <int BM, int BN, int BK>
+bool direct_fits(std::int64_t m, std::int64_t n, std::int64_t k) {
+  return m % BM == 0 && n % BN == 0 && k % BK == 0 && k > 0 &&
+         static_cast<double>(BM) * k * 4 < 2147483647.0 && static_cast<double>(k) * n * 4 < 2147483647.0;
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int kMinWaves>
+int launch_direct(GemmArgs& args, hipStream_t stream) {
+  if (!direct_fits<BM, BN, BK>(args.m, args.n, args.k))
+    return fail(TCX_INTERNAL, "direct gemm needs full tiles and 31-bit panel offsets");
+  args.tiles_m = args.m / BM;
+  args.tiles_n = args.n / BN;
+  args.total_tiles = args.tiles_m * args.tiles_n * args.total_tiles;  // caller passes the batch count
+  if (args.total_tiles > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
+  hipLaunchKernelGGL((gemm_f32_direct_kernel<BM, BN, BK, WM, WN, kMinWaves>),
+                     dim3(static_cast<unsigned>(args.total_tiles)), dim3((BM / WM) * (BN / WN) * 64), 0, stream,
+                     args);
+  return check(hipGetLastError(), "gemm_f32 direct launch");
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int kMinWaves, bool kVecOnly = false, int KS = 1>
 int launch_config(GemmArgs& args, bool trans_b, bool vec, hipStream_t stream) {
   args.tiles_m = (args.m + BM - 1) / BM;

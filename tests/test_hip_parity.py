@@ -73,6 +73,30 @@ def test_matmul_dyadic_is_exact(cx):
     assert_bits(actual, oracle.matmul(a, b), "dyadic batched")
 
 
+@pytest.mark.parametrize("sa,sb", [((4096, 32), (32, 4096)), ((4096, 96), (96, 4096)),
+                                   ((8, 1024, 512), (512, 2048)), ((2, 1, 2048, 256), (1, 4, 256, 2048))])
+def test_matmul_full_tiles(cx, sa, sb):
+    """Shapes of >= 256 full 256x256 tiles take the direct-to-LDS kernel: one
+    k-tile, an odd tile count, a broadcast batch on either side. Checked
+    against float64 products under the matmul bar."""
+    rng = np.random.default_rng(17)
+    a = rng.standard_normal(sa).astype(np.float32)
+    b = rng.standard_normal(sb).astype(np.float32)
+    actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    assert_matmul(actual, np.matmul(a.astype(np.float64), b.astype(np.float64)), a, b, f"{sa}@{sb}")
+
+
+def test_matmul_dyadic_full_tiles_exact(cx):
+    # Exact in any order: pins the k permutation, swizzles and tile placement
+    # of the direct-to-LDS kernel bit for bit.
+    i = np.arange(4096 * 160)
+    a = ((i % 13 - 6) / 8).astype(np.float32).reshape(4096, 160)
+    j = np.arange(160 * 4096)
+    b = ((j % 9 - 4) / 16).astype(np.float32).reshape(160, 4096)
+    actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    assert_bits(actual, (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32), "dyadic full tiles")
+
+
 @pytest.mark.parametrize("sa,sb", [((2, 1, 5, 7), (3, 7, 4)), ((4, 33, 65), (65, 17)),
                                    ((65,), (65, 9)), ((9, 65), (65,)), ((3, 1, 40, 36), (1, 5, 36, 44))])
 def test_matmul_broadcast(cx, sa, sb):
