@@ -92,10 +92,11 @@ extern "C" int tcx_hip_gemm_f32(const float* lhs, const float* rhs, float* out,
   const std::int64_t tiles_256 = ((d->m + 255) / 256) * ((d->n + 255) / 256) * batches;
   // (Unaligned shapes take the scalar-load variant, which does not fit the
   // 256x256 tile's registers; they use the 128x128 tile.)
-  // Full 256x256 tiles with B as [k, n]: the direct-to-LDS variant (4096^3:
-  // 1.03 ms -> 0.96 ms, batched 32x1024^3: 0.55-0.59 ms -> 0.51 ms).
-  if (vec && !trans_b && tiles_256 >= 256 && gemm::direct_fits<256, 256, 32>(d->m, d->n, d->k))
-    return gemm::launch_direct<256, 256, 32, 64, 128, 2>(args, s);
+  // Full 256x256 tiles: the direct-to-LDS variant (4096^3: 1.03 ms ->
+  // 0.96 ms, batched 32x1024^3: 0.55-0.59 ms -> 0.51 ms, transposed B at
+  // 4096x4096x1024: 305 us -> 290 us).
+  if (vec && tiles_256 >= 256 && gemm::direct_fits<256, 256, 32>(d->m, d->n, d->k))
+    return gemm::launch_direct<256, 256, 32, 64, 128, 2>(args, trans_b, s);
   if (vec && tiles_256 >= 256) return launch_config<256, 256, 32, 64, 128, 2, true>(args, trans_b, true, s);
   if (((d->m + 127) / 128) * ((d->n + 127) / 128) * batches >= 256)
     return launch_config<128, 128, 16, 32, 64, 2, false, 2>(args, trans_b, vec, s);

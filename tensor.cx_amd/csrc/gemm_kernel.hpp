@@ -2,6 +2,8 @@
 // gemm.hip, which owns the C entry point and the per-shape tile choice.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 
@@ -365,7 +367,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
 // The two stages are separate LDS arrays and the k loop handles them in
 // pairs. The loads are issued as assembly: the compiler adds no waits for
 // them, and the loop waits (vmcnt 0) right before each barrier.
-template <int BM, int BN, int BK, int WM, int WN, int kMinWaves>
+template <int BM, int BN, int BK, int WM, int WN, int kMinWaves, bool kTransB>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64)
 __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(GemmArgs a) {
   constexpr int kWavesN = BN / WN, kWaves = (BM / WM) * kWavesN;
@@ -375,10 +377,13 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
   static_assert(kChunks == 8 && BN == 256 && TN % 4 == 0, "one wave instruction = 8 rows of A or one row of B");
   constexpr int kARows = 64 / kChunks;          // A rows per wave instruction
   constexpr int kAInst = BM / kARows / kWaves;  // A instructions per wave and tile
-  constexpr int kBInst = BK / kWaves;           // B instructions per wave and tile
-  static_assert(kAInst * kARows * kWaves == BM && kBInst * kWaves == BK);
+  // B instructions per wave and tile: one k-row each ([k, n] B), or 8
+  // n-rows each for a transposed B stored like A.
+  constexpr int kBInst = kTransB ? BN / kARows / kWaves : BK / kWaves;
+  static_assert(kAInst * kARows * kWaves == BM && (kTransB ? kBInst * kARows * kWaves == BN : kBInst * kWaves == BK));
+  using BTile = std::conditional_t<kTransB, float[BN][BK], float[BK][LDB]>;
   __shared__ float A0[BM][BK], A1[BM][BK];
-  __shared__ float B0[BK][LDB], B1[BK][LDB];
+  __shared__ BTile B0, B1;
 
   // Same XCD-aware tile order as gemm_f32_kernel.
   const std::int64_t grid = a.total_tiles;
@@ -423,12 +428,14 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
     return int4v{static_cast<int>(addr), static_cast<int>(addr >> 32), 0x7fffffff, 0x00020000};
   };
   const int4v a_rsrc = rsrc_of(A + m0 * K);
-  const int4v b_rsrc = rsrc_of(B + n0);
+  const int4v b_rsrc = rsrc_of(kTransB ? B + n0 * K : B + n0);
   // Lane of instruction p writes A row (p * kWaves + wave) * 8 + lane / 8; the
   // chunk swizzle of that row does not depend on p.
   const int a_row = wave * kARows + lane / kChunks;
   const int a_voff = (a_row * static_cast<int>(K) + 4 * achunk(a_row, lane % kChunks)) * 4;
-  const int b_voff = (wave * static_cast<int>(N) + 4 * lane) * 4;
+  const int b_row = a_row;  // transposed B: same lane map as A over n rows
+  const int b_voff = kTransB ? (b_row * static_cast<int>(K) + 4 * achunk(b_row, lane % kChunks)) * 4
+                             : (wave * static_cast<int>(N) + 4 * lane) * 4;
   auto lds_of = [](const void* p) {
     return static_cast<unsigned>(reinterpret_cast<std::uintptr_t>((__attribute__((address_space(3))) const void*)p));
   };
@@ -442,18 +449,26 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
                  :: "s"(lds_byte), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
   };
 #pragma clang diagnostic pop
-  auto issue = [&](float (&As)[BM][BK], float (&Bs)[BK][LDB], int k0) {
+  auto issue = [&](float (&As)[BM][BK], BTile& Bs, int k0) {
     __builtin_amdgcn_sched_barrier(0);
     const unsigned a_lds = lds_of(&As[0][0]) + static_cast<unsigned>(wave * kARows * BK * 4);
-    const unsigned b_lds = lds_of(&Bs[0][0]) + static_cast<unsigned>(wave * LDB * 4);
 #pragma unroll
     for (int p = 0; p < kAInst; ++p)
       dma16(a_rsrc, a_lds + p * kWaves * kARows * BK * 4, a_voff,
             __builtin_amdgcn_readfirstlane((p * kWaves * kARows * static_cast<int>(K) + k0) * 4));
+    if constexpr (kTransB) {
+      const unsigned b_lds = lds_of(&Bs[0][0]) + static_cast<unsigned>(wave * kARows * BK * 4);
 #pragma unroll
-    for (int p = 0; p < kBInst; ++p)
-      dma16(b_rsrc, b_lds + p * kWaves * LDB * 4, b_voff,
-            __builtin_amdgcn_readfirstlane((p * kWaves + k0) * static_cast<int>(N) * 4));
+      for (int p = 0; p < kBInst; ++p)
+        dma16(b_rsrc, b_lds + p * kWaves * kARows * BK * 4, b_voff,
+              __builtin_amdgcn_readfirstlane((p * kWaves * kARows * static_cast<int>(K) + k0) * 4));
+    } else {
+      const unsigned b_lds = lds_of(&Bs[0][0]) + static_cast<unsigned>(wave * LDB * 4);
+#pragma unroll
+      for (int p = 0; p < kBInst; ++p)
+        dma16(b_rsrc, b_lds + p * kWaves * LDB * 4, b_voff,
+              __builtin_amdgcn_readfirstlane((p * kWaves + k0) * static_cast<int>(N) * 4));
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -465,9 +480,10 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.F, 0.F, 0.F, 0.F};
 
-  // Block i of the wave covers tile rows 16 i + (0..15); B columns keep the
-  // frag_pos map (16-byte fragment reads and output stores).
-  auto compute = [&](const float (&As)[BM][BK], const float (&Bs)[BK][LDB]) {
+  // Block i of the wave covers tile rows 16 i + (0..15). B columns keep the
+  // frag_pos map for a [k, n] B (16-byte fragment reads and output stores);
+  // a transposed B is read like A, block j covering columns 16 j + (0..15).
+  auto compute = [&](const float (&As)[BM][BK], const BTile& Bs) {
 #pragma unroll
     for (int g = 0; g < BK / 16; ++g) {
       __builtin_amdgcn_sched_barrier(0);
@@ -477,15 +493,31 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
         const int row = wm * WM + 16 * i + r;
         a4[i] = *reinterpret_cast<const float4_t*>(&As[row][achunk(row, g * 4 + kl) * 4]);
       }
+      if constexpr (kTransB) {
+        float4_t b4[TN];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        float bv[TN];
-        load_frag<TN>(&Bs[g * 16 + 4 * kl + s][wn * WN], r, 0, bv);
+        for (int j = 0; j < TN; ++j) {
+          const int col = wn * WN + 16 * j + r;
+          b4[j] = *reinterpret_cast<const float4_t*>(&Bs[col][achunk(col, g * 4 + kl) * 4]);
+        }
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int s = 0; s < 4; ++s)
 #pragma unroll
-          for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[i][s], bv[j], acc[i][j], 0, 0, 0);
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[i][s], b4[j][s], acc[i][j], 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          float bv[TN];
+          load_frag<TN>(&Bs[g * 16 + 4 * kl + s][wn * WN], r, 0, bv);
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[i][s], bv[j], acc[i][j], 0, 0, 0);
+        }
       }
     }
   };
@@ -510,9 +542,10 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
 
   // Epilogue as in gemm_f32_kernel (full tiles: no bounds checks).
   const std::int64_t col_base = n0 + wn * WN;
+  auto col_of = [&](int j) { return kTransB ? 16 * j + r : frag_pos<TN>(r, j); };
   float bias[TN];
 #pragma unroll
-  for (int j = 0; j < TN; ++j) bias[j] = a.bias != nullptr ? a.bias[col_base + frag_pos<TN>(r, j)] : 0.F;
+  for (int j = 0; j < TN; ++j) bias[j] = a.bias != nullptr ? a.bias[col_base + col_of(j)] : 0.F;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -526,16 +559,21 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
         v[j] = activate(x, a.activation);
       }
       float* dst = C + row * N + col_base;
+      if constexpr (kTransB) {
 #pragma unroll
-      for (int g = 0; g < TN / 4; ++g)
-        *reinterpret_cast<float4_t*>(dst + g * 64 + r * 4) = float4_t{v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
+        for (int j = 0; j < TN; ++j) dst[16 * j + r] = v[j];
+      } else {
+#pragma unroll
+        for (int g = 0; g < TN / 4; ++g)
+          *reinterpret_cast<float4_t*>(dst + g * 64 + r * 4) = float4_t{v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
+      }
     }
   }
 }
 
 // True when gemm_f32_direct_kernel<BM, BN, BK, ...> can take the problem:
 // full tiles, k > 0, and byte offsets inside one A row panel (BM x K) and one
-// B column panel (K x N) below 2^31.
+// B column panel (K x N, or BN x K transposed) below 2^31.
 template <int BM, int BN, int BK>
 bool direct_fits(std::int64_t m, std::int64_t n, std::int64_t k) {
   return m % BM == 0 && n % BN == 0 && k % BK == 0 && k > 0 &&
@@ -543,16 +581,18 @@ bool direct_fits(std::int64_t m, std::int64_t n, std::int64_t k) {
 }
 
 template <int BM, int BN, int BK, int WM, int WN, int kMinWaves>
-int launch_direct(GemmArgs& args, hipStream_t stream) {
+int launch_direct(GemmArgs& args, bool trans_b, hipStream_t stream) {
   if (!direct_fits<BM, BN, BK>(args.m, args.n, args.k))
     return fail(TCX_INTERNAL, "direct gemm needs full tiles and 31-bit panel offsets");
   args.tiles_m = args.m / BM;
   args.tiles_n = args.n / BN;
   args.total_tiles = args.tiles_m * args.tiles_n * args.total_tiles;  // caller passes the batch count
   if (args.total_tiles > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
-  hipLaunchKernelGGL((gemm_f32_direct_kernel<BM, BN, BK, WM, WN, kMinWaves>),
-                     dim3(static_cast<unsigned>(args.total_tiles)), dim3((BM / WM) * (BN / WN) * 64), 0, stream,
-                     args);
+  const dim3 grid(static_cast<unsigned>(args.total_tiles)), block((BM / WM) * (BN / WN) * 64);
+  if (trans_b)
+    hipLaunchKernelGGL((gemm_f32_direct_kernel<BM, BN, BK, WM, WN, kMinWaves, true>), grid, block, 0, stream, args);
+  else
+    hipLaunchKernelGGL((gemm_f32_direct_kernel<BM, BN, BK, WM, WN, kMinWaves, false>), grid, block, 0, stream, args);
   return check(hipGetLastError(), "gemm_f32 direct launch");
 }
 

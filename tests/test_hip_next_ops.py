@@ -337,6 +337,14 @@ def test_inference_pipeline(cx):
     assert_close(output.numpy(), expected, 2e-4, 2e-5, "pipeline")
 
 
+def test_attention_masked_full_tiles(cx):
+    # 8 x 2048 x 2048 scores over K = 64: 512 full 256x256 tiles, so the
+    # score product (B transposed) takes the direct-to-LDS GEMM kernel.
+    q, k, v = f32((8, 2048, 64), 21), f32((8, 2048, 64), 22), f32((8, 2048, 64), 23)
+    mask = np.random.default_rng(24).random((2048, 2048)) > .2
+    attention_check(cx, q, k, v, mask)
+
+
 # ------------------------------------------------------------- fused attention
 @pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("rows,cols", [(1, 1), (64, 64), (65, 130), (200, 37), (5, 0), (3, 257)])

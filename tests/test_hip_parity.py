@@ -314,6 +314,24 @@ def test_linear(cx, shape):
         np.sqrt(np.mean(w * w)) + 1e-6
 
 
+def test_linear_full_tiles(cx):
+    # 4096 x 4096 outputs: the transposed-B direct-to-LDS kernel, with the bias
+    # and SiLU epilogue; checked against float64.
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((4096, 256)).astype(np.float32)
+    w = rng.standard_normal((4096, 256)).astype(np.float32)
+    b = rng.standard_normal(4096).astype(np.float32)
+    xh, wh, bh = (cx.tensor(v, device="hip") for v in (x, w, b))
+    exact = x.astype(np.float64) @ w.astype(np.float64).T
+    assert_matmul(cx.linear(xh, wh).numpy(), exact, x, w.T, "linear full tiles")
+    assert_matmul(cx.linear(xh, wh, bh).numpy(), exact + b, x, w.T, "linear full tiles + bias")
+    fused = cx.hip.linear_act(xh, wh, bh, "silu").numpy()
+    z = exact + b
+    expected = z / (1.0 + np.exp(-z))
+    bound = 1.1e-4 * np.sqrt(256) * np.sqrt(np.mean(x * x)) * np.sqrt(np.mean(w * w)) + 1e-6
+    assert np.max(np.abs(fused - expected)) <= bound
+
+
 def test_concurrent_threads(cx):
     from concurrent.futures import ThreadPoolExecutor
     rng = np.random.default_rng(8)
