@@ -263,21 +263,37 @@ __global__ __launch_bounds__(256) void row_split_kernel(RowArgs a) {
     return r;
   };
 
-  int par = 0;
-  for (std::int64_t row = blockIdx.x; row < a.rows; row += gridDim.x, par ^= 1) {
+  // Rows of up to 4 float4 per thread prefetch the block's next row into a
+  // second register set while the current row reduces and stores (global
+  // loads stay in flight across the barriers). Wider rows load in place.
+  constexpr bool kPrefetch = kPer <= 4;
+  auto load_row = [&](std::int64_t row, float (&dst)[kPer][4], float& first) {
     const float* __restrict__ x = a.x + row * n;
-    float* __restrict__ out = a.out + row * n;
-    float v[kPer][4];
 #pragma unroll
     for (int c = 0; c < kPer; ++c) {
       if constexpr (kVec) {
         float4_t q = {0.F, 0.F, 0.F, 0.F};
         if (valid(c, 0)) q = stream_load(reinterpret_cast<const float4_t*>(x + column(c, 0)));
-        v[c][0] = q.x; v[c][1] = q.y; v[c][2] = q.z; v[c][3] = q.w;
+        dst[c][0] = q.x; dst[c][1] = q.y; dst[c][2] = q.z; dst[c][3] = q.w;
       } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[c][q] = valid(c, q) ? x[column(c, q)] : 0.F;
+        for (int q = 0; q < 4; ++q) dst[c][q] = valid(c, q) ? x[column(c, q)] : 0.F;
       }
+    }
+    if constexpr (kOp == RowOp::kLayer) first = x[0];
+  };
+  float v[kPer][4], nv[kPrefetch ? kPer : 1][4];
+  float first = 0.F, next_first = 0.F;
+  if (kPrefetch && blockIdx.x < a.rows) load_row(blockIdx.x, v, first);
+
+  int par = 0;
+  for (std::int64_t row = blockIdx.x; row < a.rows; row += gridDim.x, par ^= 1) {
+    float* __restrict__ out = a.out + row * n;
+    if constexpr (kPrefetch) {
+      const std::int64_t next = row + gridDim.x;
+      if (next < a.rows) load_row(next, nv, next_first);
+    } else {
+      load_row(row, v, first);
     }
 
     if constexpr (kOp == RowOp::kSoftmax) {
@@ -321,7 +337,6 @@ __global__ __launch_bounds__(256) void row_split_kernel(RowArgs a) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[c][q] = v[c][q] * scale;
     } else {
-      const float first = x[0];
       float sum = 0.F;
       bool equal = true;
 #pragma unroll
@@ -386,7 +401,14 @@ __global__ __launch_bounds__(256) void row_split_kernel(RowArgs a) {
           if (valid(c, q)) out[column(c, q)] = r[q];
       }
     }
-    // Keep the next row's loads from being hoisted into this row's live range.
+    if constexpr (kPrefetch) {
+#pragma unroll
+      for (int c = 0; c < kPer; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[c][q] = nv[c][q];
+      first = next_first;
+    }
+    // Keep later rows' loads from being hoisted into this row's live range.
     asm volatile("" ::: "memory");
   }
 }
