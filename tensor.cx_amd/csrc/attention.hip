@@ -50,6 +50,7 @@ struct FlashArgs {
   std::int64_t rows, cols;
   float scale;
   int causal;
+  int xcd_blocks;  // direct kernel: group the blocks of a batch matrix on one XCD
 };
 
 using float2_t = float __attribute__((ext_vector_type(2)));
@@ -292,6 +293,385 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
   }
 }
 
+// The same computation with K/V tiles loaded straight into LDS
+// (buffer_load ... lds), pipelined so that matrix cores stay busy through the
+// softmax: while the scores of key tile j go through the softmax (VALU), the
+// same wave's MFMAs already compute the scores of tile j + 1. K therefore runs
+// one tile ahead of V: iteration j reads K tile j + 1 and V tile j, and loads
+// K tile j + 2 and V tile j + 1 into the other halves of two-stage buffers,
+// with one barrier per tile. Rows are unpadded and their 16-byte chunks
+// XOR-swizzled by row (period 16), which keeps the K reads (16 rows, one
+// chunk each) and the V reads (16 chunks of one row) conflict-free. Keys past
+// the sequence read as zero (buffer range check), like the staged kernel's
+// zero fill.
+template <int D>
+__device__ __forceinline__ int kv_chunk(int row, int c) {
+  if constexpr (D / 4 >= 16) return c ^ (row & 15);
+  else return c ^ ((row >> 1) & 7);
+}
+
+// Output tile t of lane r holds feature direct_feature(r, t): four
+// consecutive features per 16-byte chunk, chunk r of each 64-feature half
+// (features kT r + t for D = 32).
+template <int kT>
+__device__ __forceinline__ int direct_feature(int r, int t) {
+  if constexpr (kT >= 4) return 64 * (t / 4) + 4 * r + (t % 4);
+  else return kT * r + t;
+}
+
+template <int D, int kWaves, bool kCausal>
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 8))) void flash_attention_direct_kernel(
+    FlashArgs a) {
+  constexpr int kQTile = 16 * kWaves;
+  constexpr int kT = D / 16;
+  constexpr int kChunks = D / 4;                         // 16-byte chunks per K/V row
+  constexpr int kRowsPerInst = 64 / kChunks;             // rows one wave instruction fills
+  constexpr int kInst = kKTile / kRowsPerInst / kWaves;  // instructions per wave per K (or V) tile
+  static_assert(D % 16 == 0 && kInst >= 1 && kInst * kRowsPerInst * kWaves == kKTile);
+  __shared__ float ks[2][kKTile * D];
+  __shared__ float vs[2][kKTile * D];
+  __shared__ int bad_column[D];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  std::int64_t batch = blockIdx.y, qtile = blockIdx.x;
+  if (a.xcd_blocks) {
+    // Launch id L runs on XCD L % 8: give XCD x the consecutive (batch-major)
+    // work items x * n/8 .. (x + 1) * n/8 - 1, so that the query tiles of one
+    // batch matrix share its K and V in that XCD's L2 (n % 8 == 0).
+    const std::int64_t n = static_cast<std::int64_t>(gridDim.x) * gridDim.y;
+    const std::int64_t id = static_cast<std::int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
+    const std::int64_t item = (id % 8) * (n / 8) + id / 8;
+    batch = item / gridDim.x;
+    qtile = item % gridDim.x;
+  }
+  if constexpr (kCausal) {
+    const std::int64_t n = static_cast<std::int64_t>(gridDim.x) * gridDim.y;
+    const std::int64_t id = static_cast<std::int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
+    const std::int64_t half = (n + 1) / 2;
+    const std::int64_t rank = id < half ? id : n - 1 - (id - half);
+    qtile = gridDim.x - 1 - rank / gridDim.y;
+    batch = rank % gridDim.y;
+  }
+  const std::int64_t q0 = qtile * kQTile + wave * 16;
+  const std::int64_t q_last = min(qtile * kQTile + kQTile, a.rows) - 1;
+  for (int d = tid; d < D; d += 64 * kWaves) bad_column[d] = 0;
+  const float* __restrict__ qb = a.q + batch * a.rows * D;
+  const float* __restrict__ kb = a.k + batch * a.cols * D;
+  const float* __restrict__ vb = a.v + batch * a.cols * D;
+
+  float4_t qf[kT];
+  {
+    const std::int64_t qrow = q0 + r;
+#pragma unroll
+    for (int t = 0; t < kT; ++t) {
+      // Unconditional loads (a row past the end reads row 0, then zero):
+      // loads under a divergent branch would make the compiler wait for
+      // every outstanding load inside the key loop.
+      const std::int64_t qc = qrow < a.rows ? qrow : 0;
+      qf[t] = *reinterpret_cast<const float4_t*>(qb + qc * D + 16 * t + 4 * g);
+      if (qrow >= a.rows) qf[t] = float4_t{0.F, 0.F, 0.F, 0.F};
+    }
+  }
+  mfma_acc o[kT];
+#pragma unroll
+  for (int t = 0; t < kT; ++t) o[t] = mfma_acc{0.F, 0.F, 0.F, 0.F};
+  const float neg_inf = -__builtin_inff();
+  float m = neg_inf, l = 0.F;
+  const std::int64_t query = q0 + r;
+
+  // Buffer resources over this batch's K and V (num_records = its bytes, so
+  // keys past the sequence read as zero). Instruction p of a wave fills rows
+  // (p * kWaves + wave) * kRowsPerInst .. + kRowsPerInst - 1 of the tile;
+  // lane i writes chunk slot i % kChunks of row i / kChunks, which holds
+  // global chunk kv_chunk(row, slot). The launcher checks that the byte
+  // offsets fit in 31 bits.
+  using int4v = int __attribute__((ext_vector_type(4)));
+  const int kv_bytes = static_cast<int>(a.cols * D * 4);
+  auto rsrc_of = [&](const float* base) {
+    const auto addr = reinterpret_cast<std::uint64_t>(base);
+    return int4v{static_cast<int>(addr), static_cast<int>(addr >> 32), kv_bytes, 0x00020000};
+  };
+  const int4v k_rsrc = rsrc_of(kb), v_rsrc = rsrc_of(vb);
+  int voff[kInst];
+#pragma unroll
+  for (int p = 0; p < kInst; ++p) {
+    const int row = (p * kWaves + wave) * kRowsPerInst + lane / kChunks;
+    voff[p] = (row * D + 4 * kv_chunk<D>(row, lane % kChunks)) * 4;
+  }
+  auto lds_of = [](const void* ptr) {
+    return static_cast<unsigned>(reinterpret_cast<std::uintptr_t>((__attribute__((address_space(3))) const void*)ptr));
+  };
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  auto dma16 = [](const int4v& rsrc, unsigned lds_byte, int off, int soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :: "s"(lds_byte), "v"(off), "s"(rsrc), "s"(soff) : "memory", "m0");
+  };
+#pragma clang diagnostic pop
+  auto issue = [&](const int4v& rsrc, float* stage, std::int64_t tile) {
+    const int soff = __builtin_amdgcn_readfirstlane(static_cast<int>(tile * kKTile * D * 4));
+#pragma unroll
+    for (int p = 0; p < kInst; ++p) {
+      const unsigned row_byte = static_cast<unsigned>((p * kWaves + wave) * kRowsPerInst * D * 4);
+      dma16(rsrc, lds_of(stage) + row_byte, voff[p], soff);
+    }
+  };
+
+  // Lane exchanges: xor 16 inside each half-wave (swizzle, bit-mask mode:
+  // and 0x1f, xor 0x10), xor 32 and the broadcast of query 4g + v's factor
+  // to lane group g through precomputed permute addresses.
+  auto xor16 = [](float x) { return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401f)); };
+  const int xor32_addr = (lane ^ 32) << 2;
+  auto xor32 = [&](float x) { return __int_as_float(__builtin_amdgcn_ds_bpermute(xor32_addr, __float_as_int(x))); };
+  int row_addr[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) row_addr[v] = (4 * g + v) << 2;
+
+  // Fragment reads. K: the four 16-key blocks of feature group t (lane (r, g)
+  // reads chunk 4t + g of key 16b + r). V: key row 16b + 4g + v, features
+  // direct_feature(r, t): chunks r, 16 + r, ... (half of chunk r / 2 for
+  // D = 32), so the 16 lanes of a row read 16 different chunks.
+  auto read_k = [&](const float* __restrict__ kt_, int t, float4_t (&kf)[4]) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int row = 16 * b + r;
+      kf[b] = *reinterpret_cast<const float4_t*>(&kt_[row * D + 4 * kv_chunk<D>(row, 4 * t + g)]);
+    }
+  };
+  auto read_v = [&](const float* __restrict__ vt_, int step, float (&vv)[kT]) {
+    const int row = 16 * (step / 4) + 4 * g + step % 4;
+    if constexpr (kT >= 4) {
+#pragma unroll
+      for (int h = 0; h < kT / 4; ++h) {
+        const float4_t w = *reinterpret_cast<const float4_t*>(&vt_[row * D + 4 * kv_chunk<D>(row, 16 * h + r)]);
+        vv[4 * h] = w.x; vv[4 * h + 1] = w.y; vv[4 * h + 2] = w.z; vv[4 * h + 3] = w.w;
+      }
+    } else {
+      const float2_t w =
+          *reinterpret_cast<const float2_t*>(&vt_[row * D + 4 * kv_chunk<D>(row, r / 2) + 2 * (r % 2)]);
+      vv[0] = w.x; vv[1] = w.y;
+    }
+  };
+
+  // The online softmax of one tile as kSteps small steps, so that they can be
+  // spread between the MFMAs of the next tile's scores:
+  //   0-3       scale (and mask) of key block b, running tile maximum
+  //   4         row maximum over the four lane groups, new running maximum,
+  //             rescale factor alpha
+  //   5         alpha of query 4g + v to lane group g
+  //   6..5+kT   rescale output tile t
+  //   6+kT..9+kT  p = exp(s - max) of key block b, partial row sum
+  //   10+kT     row sum over the lane groups, l and m updated
+  // Every key so far masked (m_new = -inf): the finite stand-in m_sub keeps
+  // p = exp(-inf) = 0 without a per-score select, and alpha = 0 leaves the
+  // zero rows zero (or NaN). A NaN score is skipped by fmaxf but gives p = NaN,
+  // so l and the whole row turn NaN; so does a +inf score (inf - inf). The
+  // exponential is exp2((s - max) log2 e): rounding the product costs at most
+  // |t| 2^-24 ln 2 relative on a term exp(-t) (1e-6 for the terms above
+  // 2^-24 of the largest), far inside the reference's rtol 2e-4.
+  constexpr int kSteps = 11 + kT;
+  float tmax = neg_inf, m_new = neg_inf, m_sub = 0.F, alpha = 1.F, psum = 0.F;
+  float av[4];
+  int limit = kKTile;
+  auto begin_tile = [&](std::int64_t tile) {
+    const std::int64_t j0 = tile * kKTile;
+    std::int64_t lim = a.cols - j0;
+    if constexpr (kCausal) lim = min(lim, query - j0 + 1);
+    limit = static_cast<int>(max<std::int64_t>(min<std::int64_t>(lim, kKTile), 0));
+    tmax = neg_inf;
+    psum = 0.F;
+  };
+  constexpr float kLog2e = 1.44269502F;  // float(log2 e)
+  auto exp_p = [](float x) { return __builtin_amdgcn_exp2f(x * kLog2e); };
+  // kMask: the tile may hold keys past the sequence or after the query.
+  auto step = [&]<int I, bool kMask>(mfma_acc (&s)[4]) {
+    if constexpr (I < 4) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float sc = s[I][v] * a.scale;
+        if constexpr (kMask) {
+          if (16 * I + 4 * g + v >= limit) sc = neg_inf;
+        }
+        s[I][v] = sc;
+        tmax = fmaxf(tmax, sc);
+      }
+    } else if constexpr (I == 4) {
+      tmax = fmaxf(tmax, xor16(tmax));
+      tmax = fmaxf(tmax, xor32(tmax));
+      m_new = fmaxf(m, tmax);
+      m_sub = m_new == neg_inf ? 0.F : m_new;
+      alpha = exp_p(m - m_sub);
+    } else if constexpr (I == 5) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        av[v] = __int_as_float(__builtin_amdgcn_ds_bpermute(row_addr[v], __float_as_int(alpha)));
+    } else if constexpr (I < 6 + kT) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o[I - 6][v] *= av[v];
+    } else if constexpr (I < 10 + kT) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float p = exp_p(s[I - 6 - kT][v] - m_sub);
+        s[I - 6 - kT][v] = p;
+        psum += p;
+      }
+    } else {
+      psum += xor16(psum);
+      psum += xor32(psum);
+      l = l * alpha + psum;
+      m = m_new;
+    }
+  };
+  auto all_steps = [&]<int... I>(mfma_acc (&s)[4], std::integer_sequence<int, I...>) {
+    (step.template operator()<I, true>(s), ...);
+  };
+
+  // O += P V in 16 steps (key 16b + 4g + v of lane group g at step 4b + v),
+  // each reading the next step's V operands before its own MFMAs.
+  auto accumulate = [&]<int... I>(const float* __restrict__ vt_, const mfma_acc (&p)[4], float (&vv)[2][kT],
+                                  std::integer_sequence<int, I...>) {
+    auto one = [&]<int J>() {
+      if constexpr (J + 1 < 16) read_v(vt_, J + 1, vv[(J + 1) & 1]);
+#pragma unroll
+      for (int t = 0; t < kT; ++t) o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[J / 4][J % 4], vv[J & 1][t], o[t], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    (one.template operator()<I>(), ...);
+  };
+
+  // The next tile's scores in 4 kT quads of four MFMAs (feature group
+  // t = Q / 4, k step e = Q % 4), with softmax step I of the current tile in
+  // quad I * 4 kT / kSteps and the K reads of group t + 1 in the first quad of
+  // group t; the last quad also reads the first P V step's V operands.
+  auto scores_with_softmax = [&]<int... Q>(const float* __restrict__ kt_, const float* __restrict__ vt_,
+                                           mfma_acc (&s_next)[4], mfma_acc (&s)[4], float4_t (&kf)[2][4],
+                                           float (&vv)[2][kT], std::integer_sequence<int, Q...>) {
+    auto quad = [&]<int J>() {
+      constexpr int t = J / 4, e = J % 4;
+      if constexpr (e == 0 && t + 1 < kT) read_k(kt_, t + 1, kf[(t + 1) & 1]);
+      if constexpr (J == 4 * kT - 1) read_v(vt_, 0, vv[0]);
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        s_next[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[t & 1][b][e], qf[t][e], s_next[b], 0, 0, 0);
+      [&]<int... I>(std::integer_sequence<int, I...>) {
+        ([&] {
+          if constexpr (I * 4 * kT / kSteps == J) step.template operator()<I, kCausal>(s);
+        }(), ...);
+      }(std::make_integer_sequence<int, kSteps>{});
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    (quad.template operator()<Q>(), ...);
+  };
+  // Scores of one tile without interleaving (first tile).
+  auto scores = [&](const float* __restrict__ kt_, mfma_acc (&s)[4]) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) s[b] = mfma_acc{0.F, 0.F, 0.F, 0.F};
+#pragma unroll
+    for (int t = 0; t < kT; ++t) {
+      float4_t kf[4];
+      read_k(kt_, t, kf);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) s[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[b][e], qf[t][e], s[b], 0, 0, 0);
+    }
+  };
+
+  const std::int64_t tiles = (a.cols + kKTile - 1) / kKTile;
+  // Under causal masking tiles past the block's last query are not run. The
+  // loop below takes every tile but the last, which are full unless masked
+  // causally.
+  const std::int64_t run = kCausal ? min(tiles, q_last / kKTile + 1) : tiles;
+  mfma_acc s_cur[4], s_next[4];
+  float4_t kf[2][4];
+  float vv[2][kT];
+  if (run > 0) {
+    issue(k_rsrc, ks[0], 0);
+    issue(v_rsrc, vs[0], 0);
+    if (run > 1) issue(k_rsrc, ks[1], 1);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // K 0, V 0 and K 1 have landed
+    scores(ks[0], s_cur);
+    __syncthreads();  // every wave is done with K stage 0
+  } else {
+    __syncthreads();  // bad_column is cleared
+  }
+  // Iteration `tile`: K tile + 1 sits in stage (tile + 1) & 1, V tile in
+  // stage tile & 1; K tile + 2 and V tile + 1 load into the other stages,
+  // whose last readers finished before the previous barrier.
+  std::int64_t tile = 0;
+  for (; tile + 1 < run; ++tile) {
+    const int st = static_cast<int>(tile & 1);
+    issue(v_rsrc, vs[st ^ 1], tile + 1);
+    if (tile + 2 < run) issue(k_rsrc, ks[st], tile + 2);
+    begin_tile(tile);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) s_next[b] = mfma_acc{0.F, 0.F, 0.F, 0.F};
+    read_k(ks[st ^ 1], 0, kf[0]);
+    scores_with_softmax(ks[st ^ 1], vs[st], s_next, s_cur, kf, vv, std::make_integer_sequence<int, 4 * kT>{});
+    accumulate(vs[st], s_cur, vv, std::make_integer_sequence<int, 16>{});
+#pragma unroll
+    for (int b = 0; b < 4; ++b) s_cur[b] = s_next[b];
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads have landed
+    __syncthreads();                // and every wave is done with this iteration's stages
+  }
+  if (tile < run) {
+    begin_tile(tile);
+    all_steps(s_cur, std::make_integer_sequence<int, kSteps>{});
+    read_v(vs[tile & 1], 0, vv[0]);
+    accumulate(vs[tile & 1], s_cur, vv, std::make_integer_sequence<int, 16>{});
+  }
+
+  if (run < tiles) {
+    const int c = (tid % (D / 4)) * 4;
+    bool bad = false;
+    for (std::int64_t row = run * kKTile + tid / (D / 4); row < a.cols; row += (64 * kWaves) / (D / 4)) {
+      const float4_t w = *reinterpret_cast<const float4_t*>(vb + row * D + c);
+      bad = bad || !__builtin_isfinite(w.x) || !__builtin_isfinite(w.y) || !__builtin_isfinite(w.z) ||
+            !__builtin_isfinite(w.w);
+      if (bad) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (!__builtin_isfinite(w[e])) bad_column[c + e] = 1;
+      }
+    }
+  }
+  __syncthreads();
+  float* __restrict__ ob = a.out + batch * a.rows * D;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int src = 4 * g + v;
+    const float lv = __shfl(l, src, kWave);
+    const float mv = __shfl(m, src, kWave);
+    const std::int64_t qrow = q0 + 4 * g + v;
+    if (qrow >= a.rows) continue;
+    float y[kT];
+#pragma unroll
+    for (int t = 0; t < kT; ++t) {
+      if (bad_column[direct_feature<kT>(r, t)]) y[t] = __builtin_nanf("");
+      else if (mv == neg_inf) y[t] = o[t][v] * 0.F;
+      else y[t] = o[t][v] / lv;
+    }
+    float* const orow = ob + qrow * D;
+    if constexpr (kT >= 4) {
+#pragma unroll
+      for (int h = 0; h < kT / 4; ++h)
+        *reinterpret_cast<float4_t*>(orow + direct_feature<kT>(r, 4 * h)) =
+            float4_t{y[4 * h], y[4 * h + 1], y[4 * h + 2], y[4 * h + 3]};
+    } else {
+      store_row<kT>(orow + kT * r, y);
+    }
+  }
+}
+
+// The direct kernel's byte offsets (row * D * 4 inside one batch matrix of K
+// or V, plus one tile) must fit in 31 bits.
+inline bool flash_direct_fits(std::int64_t cols, std::int64_t features) {
+  return static_cast<double>(cols + kKTile) * features * 4 < 2147483647.0;
+}
+
 template <int D, int kWaves>
 int launch_flash(const FlashArgs& a, std::int64_t batch, hipStream_t s) {
   constexpr int kQTile = 16 * kWaves;
@@ -299,6 +679,18 @@ int launch_flash(const FlashArgs& a, std::int64_t batch, hipStream_t s) {
   if (qtiles > 0x7fffffff || batch > 65535) return fail(TCX_INVALID_ARGUMENT, "attention grid is too large");
   hipLaunchKernelGGL((flash_attention_kernel<D, kWaves>),
                      dim3(static_cast<unsigned>(qtiles), static_cast<unsigned>(batch)), dim3(64 * kWaves), 0, s, a);
+  return check(hipGetLastError(), "flash attention launch");
+}
+
+template <int D>
+int launch_flash_direct(FlashArgs a, std::int64_t batch, hipStream_t s) {
+  constexpr int kQTile = 16 * kWavesFull;
+  const std::int64_t qtiles = (a.rows + kQTile - 1) / kQTile;
+  if (qtiles > 0x7fffffff || batch > 65535) return fail(TCX_INVALID_ARGUMENT, "attention grid is too large");
+  a.xcd_blocks = (qtiles * batch) % 8 == 0 ? 1 : 0;
+  hipLaunchKernelGGL((flash_attention_direct_kernel<D, kWavesFull, false>),
+                     dim3(static_cast<unsigned>(qtiles), static_cast<unsigned>(batch)), dim3(64 * kWavesFull), 0, s,
+                     a);
   return check(hipGetLastError(), "flash attention launch");
 }
 
@@ -326,12 +718,17 @@ int tcx_hip_flash_attention_f32(const float* q, const float* k, const float* v, 
     if (p != nullptr && (reinterpret_cast<std::uintptr_t>(p) & 15U) != 0)
       return fail(TCX_INVALID_ARGUMENT, "fused attention buffers must be 16-byte aligned");
   if (int rc = ready(); rc != TCX_OK) return rc;
-  const FlashArgs a{q, k, v, out, rows, cols, scale, causal != 0};
+  const FlashArgs a{q, k, v, out, rows, cols, scale, causal != 0, 0};
   const auto s = static_cast<hipStream_t>(stream);
   if (a.causal) {
     if (features == 32) return launch_flash<32, kWavesCausal>(a, batch, s);
     if (features == 64) return launch_flash<64, kWavesCausal>(a, batch, s);
     return launch_flash<128, kWavesCausal>(a, batch, s);
+  }
+  if (cols > 0 && flash_direct_fits(cols, features)) {
+    if (features == 32) return launch_flash_direct<32>(a, batch, s);
+    if (features == 64) return launch_flash_direct<64>(a, batch, s);
+    return launch_flash_direct<128>(a, batch, s);
   }
   if (features == 32) return launch_flash<32, kWavesFull>(a, batch, s);
   if (features == 64) return launch_flash<64, kWavesFull>(a, batch, s);

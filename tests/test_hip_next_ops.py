@@ -347,13 +347,22 @@ def test_attention_masked_full_tiles(cx):
 
 # ------------------------------------------------------------- fused attention
 @pytest.mark.parametrize("d", [32, 64, 128])
-@pytest.mark.parametrize("rows,cols", [(1, 1), (64, 64), (65, 130), (200, 37), (5, 0), (3, 257)])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (64, 64), (65, 130), (200, 37), (5, 0), (3, 257), (300, 1000)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_fused_attention(cx, d, rows, cols, causal):
     # Unmasked attention over matching batches takes the fused kernel.
     q, k, v = f32((2, 3, rows, d), 1), f32((2, 3, cols, d), 2), f32((2, 3, cols, d), 3)
     attention_check(cx, q, k, v, None, causal)
     attention_check(cx, q, k, v, None, causal, scale=0.05)
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_fused_attention_xcd_block_order(cx, d, causal):
+    # 8 batch matrices x 3 query tiles: the unmasked kernel regroups its blocks
+    # by batch matrix (launch count a multiple of 8).
+    q, k, v = f32((2, 4, 300, d), 21), f32((2, 4, 700, d), 22), f32((2, 4, 700, d), 23)
+    attention_check(cx, q, k, v, None, causal)
 
 
 def test_fused_attention_special_values(cx):
