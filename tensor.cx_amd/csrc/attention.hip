@@ -9,22 +9,25 @@
 // different order (online softmax over key tiles), inside the reference
 // test's allclose(rtol=2e-4, atol=2e-5).
 //
-// Layout. A block owns 16 queries per wave of one batch matrix and walks
-// the keys in tiles of 64, staged through padded LDS with a register prefetch
-// of the next tile. Each wave computes S^T = K Q^T for its 16 queries, so lane
-// l holds S^T[key 16b + 4(l/16) + v][query l%16] (output layout of the MFMA):
+// Layout. A block owns 16 queries per wave of one batch matrix and walks the
+// keys in tiles of 64: flash_attention_kernel (causal) stages them through
+// padded LDS with a register prefetch of the next tile;
+// flash_attention_direct_kernel (unmasked) loads them straight into LDS and
+// overlaps each tile's softmax with the next tile's score MFMAs (details at
+// that kernel). Each wave computes S^T = K Q^T for its 16 queries, so lane l
+// holds S^T[key 16b + 4(l/16) + v][query l%16] (output layout of the MFMA):
 // those are exactly the A operands (P[query l%16][key]) that the P V MFMAs
 // need, when the k index of step (b, v) is taken as key 16b + 4(l/16) + v. The
 // feature sum of S^T uses the same trick: lane l supplies features
-// 16t + 4(l/16) + e of K and Q at step (t, e), read as one float4 each. The
-// output tile t holds features kT*j + t in its column j (kT = D/16 tiles), so
-// a lane reads its V operands, and writes its outputs, as kT contiguous floats.
-// Masked keys keep p = 0, so a non-finite V propagates as in the reference's
-// P @ V: tiles the causal mask only partly covers run in full; a tile wholly
-// after the block's last query skips the MFMAs and only marks the feature
-// columns where its V rows hold a non-finite value (0 * inf or 0 * NaN is NaN
-// in every output row of the block). Blocks start with the longest query
-// tiles under causal masking.
+// 16t + 4(l/16) + e of K and Q at step (t, e), read as one float4 each. In the
+// staged kernel output tile t holds features kT*j + t in its column j
+// (kT = D/16 tiles), so a lane reads its V operands, and writes its outputs,
+// as kT contiguous floats. Masked keys keep p = 0, so a non-finite V
+// propagates as in the reference's P @ V: tiles the causal mask only partly
+// covers run in full; a tile wholly after the block's last query skips the
+// MFMAs and only marks the feature columns where its V rows hold a non-finite
+// value (0 * inf or 0 * NaN is NaN in every output row of the block). Blocks
+// start with the longest query tiles under causal masking.
 
 #include "common.hpp"
 
@@ -87,6 +90,14 @@ __device__ __forceinline__ void store_row(float* p, const float (&v)[N]) {
   }
 }
 
+// exp(x) for x <= 0 (or NaN) as exp2(x log2 e): rounding the product costs at
+// most |t| 2^-24 ln 2 relative on a term exp(-t), 1e-6 for the terms above
+// 2^-24 of the largest, far inside the reference's rtol 2e-4.
+__device__ __forceinline__ float exp_attention(float x) {
+  constexpr float kLog2e = 1.44269502F;  // float(log2 e)
+  return __builtin_amdgcn_exp2f(x * kLog2e);
+}
+
 template <int D, int kWaves>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 8))) void flash_attention_kernel(
     FlashArgs a) {
@@ -138,7 +149,6 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
   for (int t = 0; t < kT; ++t) o[t] = mfma_acc{0.F, 0.F, 0.F, 0.F};
   const float neg_inf = -__builtin_inff();
   float m = neg_inf, l = 0.F;
-  bool nan_row = false;
   const std::int64_t query = q0 + r;  // the query whose statistics this lane keeps
 
   // Tile staging: thread tid moves float4 f = tid + kThreads i (row f / (D/4)).
@@ -204,24 +214,26 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
     for (int b = 0; b < 4; ++b)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float product = s[b][v] * a.scale;
-        float sc = product;
+        float sc = s[b][v] * a.scale;
         if (16 * b + 4 * g + v >= limit) sc = neg_inf;
-        if (is_nan(sc)) nan_row = true;
         s[b][v] = sc;
-        tmax = fmaxf(tmax, sc);  // NaN never wins fmaxf; NaN rows are flagged
+        tmax = fmaxf(tmax, sc);  // NaN never wins fmaxf; it reaches p below
       }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
     const float m_new = fmaxf(m, tmax);
-    const bool none = m_new == neg_inf;  // every key so far masked: p = 0
-    const float alpha = none ? 1.F : exp_softmax(m - m_new);
+    // Every key so far masked (m_new = -inf): the finite stand-in keeps
+    // p = exp(-inf) = 0 without a per-score select, and alpha = 0 leaves the
+    // zero rows zero (or NaN). A NaN or +inf score gives p = NaN, so l and the
+    // row turn NaN as in the reference.
+    const float m_sub = m_new == neg_inf ? 0.F : m_new;
+    const float alpha = exp_attention(m - m_sub);
     float psum = 0.F;
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float p = none ? 0.F : exp_softmax(s[b][v] - m_new);
+        const float p = exp_attention(s[b][v] - m_sub);
         s[b][v] = p;
         psum += p;
       }
@@ -268,24 +280,18 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
     }
   }
   __syncthreads();  // bad_column is complete
-  // Row statistics of the four lanes sharing a query agree; the NaN flag is
-  // combined over them.
-  int nan_bits = nan_row ? 1 : 0;
-  nan_bits |= __shfl_xor(nan_bits, 16, kWave);
-  nan_bits |= __shfl_xor(nan_bits, 32, kWave);
   float* __restrict__ ob = a.out + batch * a.rows * D;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int src = 4 * g + v;  // lane holding query 4g + v's statistics
     const float lv = __shfl(l, src, kWave);
     const float mv = __shfl(m, src, kWave);
-    const int nv = __shfl(nan_bits, src, kWave);
     const std::int64_t qrow = q0 + 4 * g + v;
     if (qrow >= a.rows) continue;
     float y[kT];
 #pragma unroll
     for (int t = 0; t < kT; ++t) {
-      if (nv || bad_column[kT * r + t]) y[t] = __builtin_nanf("");
+      if (bad_column[kT * r + t]) y[t] = __builtin_nanf("");
       else if (mv == neg_inf) y[t] = o[t][v] * 0.F;  // 0 * V (NaN if V is not finite)
       else y[t] = o[t][v] / lv;
     }
@@ -467,10 +473,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
   // Every key so far masked (m_new = -inf): the finite stand-in m_sub keeps
   // p = exp(-inf) = 0 without a per-score select, and alpha = 0 leaves the
   // zero rows zero (or NaN). A NaN score is skipped by fmaxf but gives p = NaN,
-  // so l and the whole row turn NaN; so does a +inf score (inf - inf). The
-  // exponential is exp2((s - max) log2 e): rounding the product costs at most
-  // |t| 2^-24 ln 2 relative on a term exp(-t) (1e-6 for the terms above
-  // 2^-24 of the largest), far inside the reference's rtol 2e-4.
+  // so l and the whole row turn NaN; so does a +inf score (inf - inf).
   constexpr int kSteps = 11 + kT;
   float tmax = neg_inf, m_new = neg_inf, m_sub = 0.F, alpha = 1.F, psum = 0.F;
   float av[4];
@@ -483,8 +486,6 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
     tmax = neg_inf;
     psum = 0.F;
   };
-  constexpr float kLog2e = 1.44269502F;  // float(log2 e)
-  auto exp_p = [](float x) { return __builtin_amdgcn_exp2f(x * kLog2e); };
   // kMask: the tile may hold keys past the sequence or after the query.
   auto step = [&]<int I, bool kMask>(mfma_acc (&s)[4]) {
     if constexpr (I < 4) {
@@ -502,7 +503,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
       tmax = fmaxf(tmax, xor32(tmax));
       m_new = fmaxf(m, tmax);
       m_sub = m_new == neg_inf ? 0.F : m_new;
-      alpha = exp_p(m - m_sub);
+      alpha = exp_attention(m - m_sub);
     } else if constexpr (I == 5) {
 #pragma unroll
       for (int v = 0; v < 4; ++v)
@@ -513,7 +514,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
     } else if constexpr (I < 10 + kT) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float p = exp_p(s[I - 6 - kT][v] - m_sub);
+        const float p = exp_attention(s[I - 6 - kT][v] - m_sub);
         s[I - 6 - kT][v] = p;
         psum += p;
       }
