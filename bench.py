@@ -41,13 +41,35 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def timed(launch, steps: int, warmup: int):
-    """Runs `launch` warmup+steps times on this thread's stream and returns
-    (total_ms, per_launch_ms): two HIP events bracket the K timed launches on
-    the launch stream, with the stream idle on both sides."""
+# Secondary benches warm up for at least this much GPU time: the GPU clock
+# ramps up over the first milliseconds of sustained load, and each secondary
+# starts after host-side input generation has let it idle. A 4096x4096x1024
+# GEMM measured 283 us after 3 warm-up launches and 256 us after 300; the
+# 4096^3 headline (1 ms per launch) measured the same either way.
+SECONDARY_WARM_MS = 20.0
+
+
+def timed(launch, steps: int, warmup: int, warm_ms: float = 0.0):
+    """Runs `launch` warmup times, then (untimed) until warm_ms of GPU time has
+    passed, then K = steps timed times on this thread's stream, and returns
+    (total_ms, per_launch_ms, warm-up launches): two HIP events bracket the K
+    timed launches on the launch stream, with the stream idle on both sides."""
     s = capi.stream()
+    launches = 0
     for _ in range(warmup):
         launch(s)
+        launches += 1
+    if warm_ms > 0:
+        begin, now = capi.Event(), capi.Event()
+        begin.record(s)
+        while launches < 20000:
+            for _ in range(8):
+                launch(s)
+            launches += 8
+            now.record(s)
+            now.synchronize()
+            if begin.elapsed_ms(now) >= warm_ms:
+                break
     capi.synchronize()
     start, stop = capi.Event(), capi.Event()
     start.record(s)
@@ -57,7 +79,7 @@ def timed(launch, steps: int, warmup: int):
     stop.synchronize()
     capi.synchronize()
     total = start.elapsed_ms(stop)
-    return total, [total / steps] * steps
+    return total, [total / steps] * steps, launches
 
 
 def rotate(arrays_per_copy):
@@ -71,7 +93,7 @@ def rotate(arrays_per_copy):
     return nxt
 
 
-def bench_gemm(name: str, steps: int, warmup: int, transposed=False):
+def bench_gemm(name: str, steps: int, warmup: int, transposed=False, warm_ms: float = 0.0):
     a, b = wl.gemm_inputs(name)
     da, db = capi.DeviceArray.from_numpy(a), capi.DeviceArray.from_numpy(b)
     if a.ndim == 3:
@@ -84,23 +106,23 @@ def bench_gemm(name: str, steps: int, warmup: int, transposed=False):
         m, k, n = a.shape[0], a.shape[1], b.shape[1]
         desc = capi.gemm_desc(m, n, k)
         out = capi.DeviceArray((m, n))
-    total, per = timed(lambda s: capi.gemm(da.ptr, db.ptr, out.ptr, desc, s), steps, warmup)
+    total, per, warm = timed(lambda s: capi.gemm(da.ptr, db.ptr, out.ptr, desc, s), steps, warmup, warm_ms)
     flops = wl.gemm_flops(name)
     avg = statistics.mean(per)
     return {"name": f"gemm_{name}", "unit": "TFLOP/s", "value": flops / (total / steps * 1e-3) / 1e12,
             "kernel_avg_ms": avg, "kernel_median_ms": statistics.median(per),
             "achieved": flops / (avg * 1e-3) / 1e12, "peak": PEAK_FP32_MFMA / 1e12,
             "frac": flops / (avg * 1e-3) / PEAK_FP32_MFMA, "flop_per_launch": flops,
-            "ms_per_step": total / steps}
+            "ms_per_step": total / steps, "warmup_launches": warm}
 
 
 def bench_hbm(name: str, launch_for, nbytes: int, steps: int, warmup: int):
-    total, per = timed(launch_for, steps, warmup)
+    total, per, warm = timed(launch_for, steps, warmup, SECONDARY_WARM_MS)
     avg = statistics.mean(per)
     return {"name": name, "unit": "GB/s", "value": nbytes / (total / steps * 1e-3) / 1e9,
             "kernel_avg_ms": avg, "kernel_median_ms": statistics.median(per),
             "achieved": nbytes / (avg * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
-            "frac": nbytes / (avg * 1e-3) / PEAK_HBM, "bytes_per_launch": nbytes}
+            "frac": nbytes / (avg * 1e-3) / PEAK_HBM, "bytes_per_launch": nbytes, "warmup_launches": warm}
 
 
 def secondary_benches(steps: int, warmup: int, only: str | None):
@@ -111,7 +133,7 @@ def secondary_benches(steps: int, warmup: int, only: str | None):
 
     for name in ("c2_batched", "c2_edge", "c1_512"):
         if want(name):
-            out.append(bench_gemm(name, steps, warmup))
+            out.append(bench_gemm(name, steps, warmup, warm_ms=SECONDARY_WARM_MS))
             log(f"{out[-1]['name']}: {out[-1]['achieved']:.1f} TFLOP/s ({out[-1]['frac']:.1%})")
 
     if want("reduce") or want("sum") or want("max") or want("argmax"):
@@ -182,14 +204,14 @@ def secondary_benches(steps: int, warmup: int, only: str | None):
             capi.gemm(h.ptr, dw2.ptr, logits.ptr, d2, s)
             capi.softmax(logits.ptr, prob.ptr, 4096, 1024, 1, s)
 
-        total, per = timed(mlp, steps, warmup)
+        total, per, warm = timed(mlp, steps, warmup, SECONDARY_WARM_MS)
         flops = 2 * 2 * 4096 * 4096 * 1024
         avg = statistics.mean(per)
         out.append({"name": "mlp_forward_4096x1024x4096", "unit": "TFLOP/s",
                     "value": flops / (total / steps * 1e-3) / 1e12, "step_avg_ms": avg,
                     "achieved": flops / (avg * 1e-3) / 1e12, "peak": PEAK_FP32_MFMA / 1e12,
                     "frac": flops / (avg * 1e-3) / PEAK_FP32_MFMA,
-                    "tokens_per_s": 4096 / (avg * 1e-3)})
+                    "tokens_per_s": 4096 / (avg * 1e-3), "warmup_launches": warm})
         log(f"{out[-1]['name']}: {out[-1]['achieved']:.1f} TFLOP/s ({out[-1]['frac']:.1%})")
 
     if want("attention"):
@@ -199,14 +221,15 @@ def secondary_benches(steps: int, warmup: int, only: str | None):
         o = capi.DeviceArray((bh, seq, d))
         for causal in (False, True):
             flops = wl.attention_flops(causal)
-            total, per = timed(lambda s, c=causal: capi.flash_attention(
-                dq.ptr, dk.ptr, dv.ptr, o.ptr, bh, seq, seq, d, 1.0 / np.sqrt(d), c, s), steps, warmup)
+            total, per, warm = timed(lambda s, c=causal: capi.flash_attention(
+                dq.ptr, dk.ptr, dv.ptr, o.ptr, bh, seq, seq, d, 1.0 / np.sqrt(d), c, s), steps, warmup,
+                SECONDARY_WARM_MS)
             avg = statistics.mean(per)
             out.append({"name": f"attention_fused_{bh}x{seq}x{d}" + ("_causal" if causal else ""),
                         "unit": "TFLOP/s", "value": flops / (total / steps * 1e-3) / 1e12,
                         "kernel_avg_ms": avg, "achieved": flops / (avg * 1e-3) / 1e12,
                         "peak": PEAK_FP32_MFMA / 1e12, "frac": flops / (avg * 1e-3) / PEAK_FP32_MFMA,
-                        "flop_per_launch": flops})
+                        "flop_per_launch": flops, "warmup_launches": warm})
             log(f"{out[-1]['name']}: {out[-1]['achieved']:.1f} TFLOP/s ({out[-1]['frac']:.1%})")
     return out
 
@@ -265,7 +288,9 @@ def main() -> int:
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=30)
-    parser.add_argument("--warmup", type=int, default=5)
+    # 20 untimed steps (about 20 ms for the 1 ms headline) let the GPU clock
+    # settle before the timed steps.
+    parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     parser.add_argument("--only", default=None, help="run only secondary benches whose name contains this")
