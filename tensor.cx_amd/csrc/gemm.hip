@@ -86,9 +86,10 @@ extern "C" int tcx_hip_gemm_f32(const float* lhs, const float* rhs, float* out,
   // leave the CUs short of waves, so the smaller tiles split K inside the
   // block: 128x128 blocks of two groups of eight 32x64 waves (4 waves/SIMD)
   // when there are >= 256 of those, else 64x64 blocks of four groups of four
-  // 32x32 waves (small and edge shapes). The measured gains were 7% on the
-  // MLP's 4096x1024x4096 GEMM and 21% on 1000^3 over the same tiles without
-  // the split.
+  // 32x32 waves when there are >= 256 of those (1000^3), else 32x32 blocks of
+  // eight one-wave groups with 32-wide k-tiles (small shapes; 512^3: 17.9 ->
+  // 11.8 us). The measured gains were 7% on the MLP's 4096x1024x4096 GEMM and
+  // 21% on 1000^3 over the same tiles without the split.
   const std::int64_t tiles_256 = ((d->m + 255) / 256) * ((d->n + 255) / 256) * batches;
   // (Unaligned shapes take the scalar-load variant, which does not fit the
   // 256x256 tile's registers; they use the 128x128 tile.)
@@ -100,5 +101,7 @@ extern "C" int tcx_hip_gemm_f32(const float* lhs, const float* rhs, float* out,
   if (vec && tiles_256 >= 256) return launch_config<256, 256, 32, 64, 128, 2, true>(args, trans_b, true, s);
   if (((d->m + 127) / 128) * ((d->n + 127) / 128) * batches >= 256)
     return launch_config<128, 128, 16, 32, 64, 2, false, 2>(args, trans_b, vec, s);
+  if (((d->m + 63) / 64) * ((d->n + 63) / 64) * batches < 256)
+    return launch_config<32, 32, 32, 32, 32, 2, false, 8>(args, trans_b, vec, s);
   return launch_config<64, 64, 16, 32, 32, 4, false, 4>(args, trans_b, vec, s);
 }

@@ -50,7 +50,8 @@ def test_golden_vectors(cx, golden):
 # ------------------------------------------------------------- matmul
 @pytest.mark.parametrize("m,k,n", [(1, 1, 1), (2, 3, 4), (15, 17, 31), (17, 16, 15), (32, 33, 16),
                                    (0, 3, 4), (3, 0, 4), (3, 4, 0), (65, 129, 67), (128, 128, 128),
-                                   (129, 255, 257), (300, 64, 200), (1000, 1000, 1000)])
+                                   (129, 255, 257), (300, 64, 200), (700, 300, 500), (512, 512, 512),
+                                   (1000, 1000, 1000)])
 def test_matmul_shapes(cx, m, k, n):
     rng = np.random.default_rng(7)
     a = rng.standard_normal((m, k)).astype(np.float32)
