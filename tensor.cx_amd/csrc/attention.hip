@@ -322,9 +322,10 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
   // and the K reads of group t + 1 in the first quad of group t; the last quad
   // also reads the first P V step's V operands.
   constexpr int kQuads = kT * kB;
-  auto scores_with_softmax = [&]<int... Q>(const float* __restrict__ kt_, const float* __restrict__ vt_,
-                                           mfma_acc (&s_next)[kB], mfma_acc (&s)[kB], float4_t (&kf)[2][kB],
-                                           float (&vv)[2][kT], std::integer_sequence<int, Q...>) {
+  auto scores_with_softmax = [&]<bool kMask, int... Q>(const float* __restrict__ kt_, const float* __restrict__ vt_,
+                                                       mfma_acc (&s_next)[kB], mfma_acc (&s)[kB],
+                                                       float4_t (&kf)[2][kB], float (&vv)[2][kT],
+                                                       std::bool_constant<kMask>, std::integer_sequence<int, Q...>) {
     auto quad = [&]<int J>() {
       constexpr int t = J / kB, e0 = (J % kB) * (4 / kB);
       if constexpr (J % kB == 0 && t + 1 < kT) read_k(kt_, t + 1, kf[(t + 1) & 1]);
@@ -336,7 +337,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
           s_next[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[t & 1][b][e], qf[t][e], s_next[b], 0, 0, 0);
       [&]<int... I>(std::integer_sequence<int, I...>) {
         ([&] {
-          if constexpr (I * kQuads / kSteps == J) step.template operator()<I, kCausal>(s);
+          if constexpr (I * kQuads / kSteps == J) step.template operator()<I, kMask>(s);
         }(), ...);
       }(std::make_integer_sequence<int, kSteps>{});
       __builtin_amdgcn_sched_barrier(0);
@@ -389,7 +390,16 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
 #pragma unroll
     for (int b = 0; b < kB; ++b) s_next[b] = mfma_acc{0.F, 0.F, 0.F, 0.F};
     read_k(ks[st ^ 1], 0, kf[0]);
-    scores_with_softmax(ks[st ^ 1], vs[st], s_next, s_cur, kf, vv, std::make_integer_sequence<int, kQuads>{});
+    // Under causal masking only tiles reaching past the block's first query
+    // need the mask: a wave-uniform branch between two schedules at D = 128
+    // (+2 %). At D = 64 the second schedule raised the register count from
+    // 127 to 157, which costs a block per CU (-18 %), so D < 128 masks all.
+    if (kCausal && (D < 128 || (tile + 1) * kKeys - 1 > qtile * kQTile))
+      scores_with_softmax(ks[st ^ 1], vs[st], s_next, s_cur, kf, vv, std::true_type{},
+                          std::make_integer_sequence<int, kQuads>{});
+    else
+      scores_with_softmax(ks[st ^ 1], vs[st], s_next, s_cur, kf, vv, std::false_type{},
+                          std::make_integer_sequence<int, kQuads>{});
     accumulate(vs[st], s_cur, vv, std::make_integer_sequence<int, 4 * kB>{});
 #pragma unroll
     for (int b = 0; b < kB; ++b) s_cur[b] = s_next[b];
