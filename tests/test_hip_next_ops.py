@@ -365,6 +365,23 @@ def test_fused_attention_xcd_block_order(cx, d, causal):
     attention_check(cx, q, k, v, None, causal)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_fused_attention_bench_size(cx, causal):
+    # The bench workload (16 x 2048 x 128): checked against float64 truth
+    # (the sequential-dot oracle would take minutes at this size), with the
+    # attention bar of the reference test.
+    import tensorcx_workloads as wl
+    q, k, v = wl.attention_inputs()
+    got = cx.attention(*(hip(cx, t) for t in (q, k, v)), None, is_causal=causal).numpy()
+    q64, k64, v64 = (t.astype(np.float64) for t in (q, k, v))
+    s = (q64 @ np.swapaxes(k64, -1, -2)) / np.sqrt(q.shape[-1])
+    if causal:
+        s = np.where(np.tril(np.ones(s.shape[-2:], dtype=bool)), s, -np.inf)
+    p = np.exp(s - s.max(axis=-1, keepdims=True))
+    expected = (p / p.sum(axis=-1, keepdims=True)) @ v64
+    assert_close(got, expected, 2e-4, 2e-5, "attention bench size")
+
+
 def test_fused_attention_special_values(cx):
     q, k, v = f32((1, 70, 64), 4), f32((1, 90, 64), 5), f32((1, 90, 64), 6)
     q[0, 3, 7] = np.nan            # a NaN query: its row is NaN
