@@ -745,7 +745,7 @@ Tensor attention(const OpDesc& op, std::span<const Tensor> inputs, tcx_stream_t 
   const Shape qb(q.shape.begin(), q.shape.end() - 2);
   if (inputs.size() == 3 && qb == Shape(k.shape.begin(), k.shape.end() - 2) &&
       qb == Shape(v.shape.begin(), v.shape.end() - 2) &&
-      tcx_hip_flash_attention_supported(features, v.shape.back()) && numel(qb) <= 65535 &&
+      tcx_hip_flash_attention_supported(features, v.shape.back()) &&
       aligned16(device_ptr(q)) && aligned16(device_ptr(k)) && aligned16(device_ptr(v))) {
     Tensor out = make_tensor(DType::kFloat32, shape);
     ok_or_throw(tcx_hip_flash_attention_f32(f32(q), f32(k), f32(v), static_cast<float*>(out_ptr(out)), numel(qb),

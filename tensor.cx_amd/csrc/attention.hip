@@ -39,6 +39,7 @@ struct FlashArgs {
   const float* v;
   float* out;
   std::int64_t rows, cols;
+  std::int64_t qtiles, batch;  // work items: qtiles query tiles of each batch matrix
   float scale;
   int causal;
   int xcd_blocks;  // group the blocks of one batch matrix on one XCD
@@ -111,24 +112,29 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
-  std::int64_t batch = blockIdx.y, qtile = blockIdx.x;
+  // One block per work item on a 1-D grid of n = qtiles x batch blocks; the
+  // launch id maps to an item (batch-major by default).
+  const std::int64_t n = a.qtiles * a.batch;
+  const std::int64_t id = blockIdx.x;
+  std::int64_t batch = id / a.qtiles, qtile = id % a.qtiles;
   if (a.xcd_blocks) {
     // Launch id L runs on XCD L % 8: give XCD x the consecutive (batch-major)
     // work items x * n/8 .. (x + 1) * n/8 - 1, so that the query tiles of one
     // batch matrix share its K and V in that XCD's L2 (n % 8 == 0).
-    const std::int64_t n = static_cast<std::int64_t>(gridDim.x) * gridDim.y;
-    const std::int64_t id = static_cast<std::int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
     const std::int64_t item = (id % 8) * (n / 8) + id / 8;
-    batch = item / gridDim.x;
-    qtile = item % gridDim.x;
+    batch = item / a.qtiles;
+    qtile = item % a.qtiles;
   }
   if constexpr (kCausal) {
-    const std::int64_t n = static_cast<std::int64_t>(gridDim.x) * gridDim.y;
-    const std::int64_t id = static_cast<std::int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;
+    // Under causal masking the last query tiles see the most keys. Work items
+    // are ranked by their key-tile count; the first half of the grid takes
+    // them heaviest first and the second half lightest first, so the two
+    // blocks that share a CU (launch ids L and L + n/2) carry about the same
+    // total work.
     const std::int64_t half = (n + 1) / 2;
     const std::int64_t rank = id < half ? id : n - 1 - (id - half);
-    qtile = gridDim.x - 1 - rank / gridDim.y;
-    batch = rank % gridDim.y;
+    qtile = a.qtiles - 1 - rank / a.batch;
+    batch = rank % a.batch;
   }
   const std::int64_t q0 = qtile * kQTile + wave * 16;
   const std::int64_t q_last = min(qtile * kQTile + kQTile, a.rows) - 1;
@@ -458,12 +464,14 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
 template <int D, int kWaves, int kKeys, bool kCausal>
 int launch_flash(FlashArgs a, std::int64_t batch, hipStream_t s) {
   constexpr int kQTile = 16 * kWaves;
-  const std::int64_t qtiles = (a.rows + kQTile - 1) / kQTile;
-  if (qtiles > 0x7fffffff || batch > 65535) return fail(TCX_INVALID_ARGUMENT, "attention grid is too large");
+  a.qtiles = (a.rows + kQTile - 1) / kQTile;
+  a.batch = batch;
+  if (a.qtiles > 0x7fffffff / batch) return fail(TCX_INVALID_ARGUMENT, "attention grid is too large");
+  const std::int64_t blocks = a.qtiles * batch;
   // Causal blocks keep their heavy/light order instead.
-  a.xcd_blocks = !kCausal && (qtiles * batch) % 8 == 0 ? 1 : 0;
-  hipLaunchKernelGGL((flash_attention_kernel<D, kWaves, kKeys, kCausal>),
-                     dim3(static_cast<unsigned>(qtiles), static_cast<unsigned>(batch)), dim3(64 * kWaves), 0, s, a);
+  a.xcd_blocks = !kCausal && blocks % 8 == 0 ? 1 : 0;
+  hipLaunchKernelGGL((flash_attention_kernel<D, kWaves, kKeys, kCausal>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(64 * kWaves), 0, s, a);
   return check(hipGetLastError(), "flash attention launch");
 }
 
@@ -491,7 +499,7 @@ int tcx_hip_flash_attention_f32(const float* q, const float* k, const float* v, 
     if (p != nullptr && (reinterpret_cast<std::uintptr_t>(p) & 15U) != 0)
       return fail(TCX_INVALID_ARGUMENT, "fused attention buffers must be 16-byte aligned");
   if (int rc = ready(); rc != TCX_OK) return rc;
-  const FlashArgs a{q, k, v, out, rows, cols, scale, causal != 0, 0};
+  const FlashArgs a{q, k, v, out, rows, cols, 0, 0, scale, causal != 0, 0};
   const auto s = static_cast<hipStream_t>(stream);
   // Tile shapes measured on MI355X at 2048 x 2048. Unmasked: 8 waves and
   // 64-key tiles for D = 128 and 64 (one block per CU at D = 128: 110 against

@@ -382,6 +382,14 @@ def test_fused_attention_bench_size(cx, causal):
     assert_close(got, expected, 2e-4, 2e-5, "attention bench size")
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_fused_attention_many_batch_matrices(cx, causal):
+    # More batch matrices than a grid dimension of 65535 blocks holds: the
+    # fused kernel runs on a 1-D grid of (batch, query tile) items.
+    q, k, v = f32((66000, 3, 32), 24), f32((66000, 5, 32), 25), f32((66000, 5, 32), 26)
+    attention_check(cx, q, k, v, None, causal)
+
+
 def test_fused_attention_special_values(cx):
     q, k, v = f32((1, 70, 64), 4), f32((1, 90, 64), 5), f32((1, 90, 64), 6)
     q[0, 3, 7] = np.nan            # a NaN query: its row is NaN
