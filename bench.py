@@ -106,7 +106,8 @@ def bench_gemm(name: str, steps: int, warmup: int, transposed=False, warm_ms: fl
         m, k, n = a.shape[0], a.shape[1], b.shape[1]
         desc = capi.gemm_desc(m, n, k)
         out = capi.DeviceArray((m, n))
-    total, per, warm = timed(lambda s: capi.gemm(da.ptr, db.ptr, out.ptr, desc, s), steps, warmup, warm_ms)
+    ws = capi.gemm_workspace(desc)  # None unless the shape runs with K split
+    total, per, warm = timed(lambda s: capi.gemm(da.ptr, db.ptr, out.ptr, desc, s, ws), steps, warmup, warm_ms)
     flops = wl.gemm_flops(name)
     avg = statistics.mean(per)
     return {"name": f"gemm_{name}", "unit": "TFLOP/s", "value": flops / (total / steps * 1e-3) / 1e12,
@@ -199,9 +200,11 @@ def secondary_benches(steps: int, warmup: int, only: str | None):
         d1 = capi.gemm_desc(4096, 4096, 1024, rhs_transposed=True, bias=db1.ptr, activation="silu")
         d2 = capi.gemm_desc(4096, 1024, 4096, rhs_transposed=True, bias=db2.ptr)
 
+        ws1, ws2 = capi.gemm_workspace(d1), capi.gemm_workspace(d2)  # the second linear splits K
+
         def mlp(s):
-            capi.gemm(dx.ptr, dw1.ptr, h.ptr, d1, s)
-            capi.gemm(h.ptr, dw2.ptr, logits.ptr, d2, s)
+            capi.gemm(dx.ptr, dw1.ptr, h.ptr, d1, s, ws1)
+            capi.gemm(h.ptr, dw2.ptr, logits.ptr, d2, s, ws2)
             capi.softmax(logits.ptr, prob.ptr, 4096, 1024, 1, s)
 
         total, per, warm = timed(mlp, steps, warmup, SECONDARY_WARM_MS)

@@ -175,6 +175,19 @@ typedef struct {
 int tcx_hip_gemm_f32(const float* lhs, const float* rhs, float* out,
                      const tcx_hip_gemm_desc_t* desc, tcx_stream_t stream);
 
+/* Workspace bytes that tcx_hip_gemm_f32_ws can use for desc: > 0 when the
+ * shape has few output tiles and a long K, which then runs with K split over
+ * several blocks whose partial sums land in the workspace; 0 otherwise. */
+size_t tcx_hip_gemm_workspace_bytes(const tcx_hip_gemm_desc_t* desc);
+/* tcx_hip_gemm_f32 with that workspace (16-byte aligned). With NULL or fewer
+ * bytes than the query it runs unsplit. Same results to the matmul bar (the
+ * split partial sums are added in split order, then bias and activation);
+ * the workspace must stay allocated until the stream has run the call. Same
+ * reference interfaces as tcx_hip_gemm_f32. */
+int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* out,
+                        const tcx_hip_gemm_desc_t* desc, void* workspace,
+                        size_t workspace_bytes, tcx_stream_t stream);
+
 #define TCX_REDUCE_SUM 0
 #define TCX_REDUCE_MAX 1
 #define TCX_REDUCE_MEAN 2

@@ -134,6 +134,23 @@ int reduce_code(OpKind kind) {
   }
 }
 
+// One GEMM through tcx_hip_gemm_f32_ws: shapes that run faster with K split
+// over several blocks get their workspace from the thread's pool (without it,
+// when that allocation fails, the GEMM runs unsplit), held until the stream
+// has run the call.
+void run_gemm(const float* lhs, const float* rhs, float* out, const tcx_hip_gemm_desc_t& d, tcx_stream_t s,
+              const char* what) {
+  const std::size_t ws = tcx_hip_gemm_workspace_bytes(&d);
+  std::shared_ptr<HipBuffer> workspace;
+  if (ws) {
+    auto created = HipBuffer::create(ws);
+    if (created) workspace = created.move_value();
+  }
+  ok_or_throw(tcx_hip_gemm_f32_ws(lhs, rhs, out, &d, workspace ? workspace->data() : nullptr, workspace ? ws : 0, s),
+              what);
+  if (workspace) ok_or_throw(tcx_hip_stream_synchronize(s), what);
+}
+
 void run_rows(int code, const Tensor& x, const Tensor& out, Dim outer, Dim reduce, Dim inner, tcx_stream_t s) {
   const int dtype = tcx_dtype(x.dtype);
   const std::size_t ws = tcx_hip_reduce_workspace_bytes(code, dtype, outer, reduce, inner);
@@ -364,7 +381,7 @@ Tensor matmul(const Tensor& lhs, const Tensor& rhs, tcx_stream_t s) {
       d.rhs_batch_strides[i] = plan.rhs_batch_strides[i];
     }
   }
-  ok_or_throw(tcx_hip_gemm_f32(a, b, static_cast<float*>(out_ptr(out)), &d, s), "HIP matmul");
+  run_gemm(a, b, static_cast<float*>(out_ptr(out)), d, s, "HIP matmul");
   return out;
 }
 
@@ -381,7 +398,7 @@ void linear_into(const Tensor& x, const Tensor& w, const Tensor* bias, int act, 
   d.rhs_transposed = 1;
   d.bias = bias ? f32(*bias) : nullptr;
   d.activation = act;
-  ok_or_throw(tcx_hip_gemm_f32(f32(x), f32(w), static_cast<float*>(out_ptr(out)), &d, s), "HIP linear");
+  run_gemm(f32(x), f32(w), static_cast<float*>(out_ptr(out)), d, s, "HIP linear");
 }
 
 Shape linear_shape(std::span<const Tensor> inputs) {
@@ -684,7 +701,7 @@ Tensor attention_scores(const Tensor& q, const Tensor& k, tcx_stream_t s) {
     d.lhs_batch_strides[i] = m.strides[0][i];
     d.rhs_batch_strides[i] = m.strides[1][i];
   }
-  ok_or_throw(tcx_hip_gemm_f32(f32(q), f32(k), static_cast<float*>(out_ptr(out)), &d, s), "HIP attention scores");
+  run_gemm(f32(q), f32(k), static_cast<float*>(out_ptr(out)), d, s, "HIP attention scores");
   return out;
 }
 

@@ -33,11 +33,49 @@ using gemm::launch_config;
 
 bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15U) == 0; }
 
+// K split of the direct 256x256 kernel for shapes with fewer than 256 full
+// output tiles and a long K: the smallest power of two that gives >= 256
+// blocks (at most 16), when every split keeps >= 512 of K in whole k-tiles.
+// Measured against the tile the shape would take otherwise: 4096x1024x4096
+// with a transposed B (the MLP's second linear) 295 -> 270 us at 4 splits,
+// 2048x2048x4096 279 -> 270 us, 1024x1024x8192 546 -> 261 us at 8. 1 = none.
+std::int64_t gemm_splits(const tcx_hip_gemm_desc_t* d, std::int64_t batches) {
+  if (!gemm::direct_fits<256, 256, 32>(d->m, d->n, d->k) || d->n % 4 != 0) return 1;
+  const std::int64_t tiles = (d->m / 256) * (d->n / 256) * batches;
+  std::int64_t splits = 1;
+  while (tiles * splits < 256 && splits < 16) splits *= 2;
+  if (splits == 1 || d->k % (32 * splits) != 0 || d->k / splits < 512) return 1;
+  return splits;
+}
+
+std::int64_t batch_product(const tcx_hip_gemm_desc_t* d) {
+  std::int64_t batches = 1;
+  for (int i = 0; i < d->batch_rank; ++i) batches *= d->batch_shape[i];
+  return batches;
+}
+
 }  // namespace
 }  // namespace tcx
 
+extern "C" size_t tcx_hip_gemm_workspace_bytes(const tcx_hip_gemm_desc_t* d) {
+  using namespace tcx;
+  if (d == nullptr || d->m <= 0 || d->n <= 0 || d->k <= 0 || d->batch_rank < 0 ||
+      d->batch_rank > TCX_HIP_MAX_BATCH_RANK)
+    return 0;
+  const std::int64_t batches = batch_product(d);
+  if (batches <= 0) return 0;
+  const std::int64_t splits = gemm_splits(d, batches);
+  if (splits == 1) return 0;
+  return static_cast<size_t>(splits * batches * d->m * d->n) * sizeof(float);
+}
+
 extern "C" int tcx_hip_gemm_f32(const float* lhs, const float* rhs, float* out,
                                 const tcx_hip_gemm_desc_t* d, tcx_stream_t stream) {
+  return tcx_hip_gemm_f32_ws(lhs, rhs, out, d, nullptr, 0, stream);
+}
+
+extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* out, const tcx_hip_gemm_desc_t* d,
+                                   void* workspace, size_t workspace_bytes, tcx_stream_t stream) {
   using namespace tcx;
   if (d == nullptr) return fail(TCX_INVALID_ARGUMENT, "gemm descriptor is null");
   if (d->m < 0 || d->n < 0 || d->k < 0 || d->batch_count < 0)
@@ -98,6 +136,17 @@ extern "C" int tcx_hip_gemm_f32(const float* lhs, const float* rhs, float* out,
   // 4096x4096x1024: 305 us -> 290 us).
   if (vec && tiles_256 >= 256 && gemm::direct_fits<256, 256, 32>(d->m, d->n, d->k))
     return gemm::launch_direct<256, 256, 32, 64, 128, 2>(args, trans_b, s);
+  // Fewer full 256x256 tiles and a long K: split K over several blocks when
+  // the caller brought the workspace (tcx_hip_gemm_workspace_bytes).
+  if (vec && workspace != nullptr && aligned16(workspace)) {
+    const std::int64_t splits = gemm_splits(d, batches);
+    const size_t need = static_cast<size_t>(splits * batches * d->m * d->n) * sizeof(float);
+    if (splits > 1 && workspace_bytes >= need) {
+      args.splits = static_cast<std::int32_t>(splits);
+      args.partial = static_cast<float*>(workspace);
+      return gemm::launch_direct<256, 256, 32, 64, 128, 2>(args, trans_b, s);
+    }
+  }
   if (vec && tiles_256 >= 256) return launch_config<256, 256, 32, 64, 128, 2, true>(args, trans_b, true, s);
   if (((d->m + 127) / 128) * ((d->n + 127) / 128) * batches >= 256)
     return launch_config<128, 128, 16, 32, 64, 2, false, 2>(args, trans_b, vec, s);

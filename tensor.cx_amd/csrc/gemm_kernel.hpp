@@ -21,6 +21,11 @@ struct GemmArgs {
   std::int64_t batch_shape[TCX_HIP_MAX_BATCH_RANK];
   std::int64_t lhs_bs[TCX_HIP_MAX_BATCH_RANK];
   std::int64_t rhs_bs[TCX_HIP_MAX_BATCH_RANK];
+  // Direct kernel with a K split: `splits` blocks per output tile each sum
+  // K / splits of k and write their partial tile to partial[split] (laid out
+  // like out); split_reduce_kernel then adds them. splits <= 1: no split.
+  std::int32_t splits;
+  float* partial;
 };
 
 using floatx4 = float __attribute__((ext_vector_type(4)));
@@ -385,10 +390,15 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
   __shared__ float A0[BM][BK], A1[BM][BK];
   __shared__ BTile B0, B1;
 
-  // Same XCD-aware tile order as gemm_f32_kernel.
+  // Same XCD-aware tile order as gemm_f32_kernel, over (split, batch, tile)
+  // work items (split-major, so the blocks of one XCD share panels).
   const std::int64_t grid = a.total_tiles;
   const std::int64_t bid = blockIdx.x;
-  const std::int64_t tile = (grid % 8 == 0) ? (bid % 8) * (grid / 8) + bid / 8 : bid;
+  const std::int64_t item = (grid % 8 == 0) ? (bid % 8) * (grid / 8) + bid / 8 : bid;
+  const std::int64_t splits = a.splits > 1 ? a.splits : 1;
+  const std::int64_t per_split = grid / splits;
+  const std::int64_t split = item / per_split;
+  const std::int64_t tile = item % per_split;
   const std::int64_t per_batch = a.tiles_m * a.tiles_n;
   const std::int64_t batch = tile / per_batch;
   const std::int64_t t = tile % per_batch;
@@ -412,8 +422,13 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
   const std::int64_t M = a.m, N = a.n, K = a.k;
   const float* __restrict__ A = a.lhs + lhs_off;
   const float* __restrict__ B = a.rhs + rhs_off;
-  float* __restrict__ C = a.out + batch * M * N;
+  const bool partial = splits > 1;
+  float* __restrict__ C = partial ? a.partial + (split * (per_split / per_batch) + batch) * M * N
+                                  : a.out + batch * M * N;
   const std::int64_t m0 = tm * BM, n0 = tn * BN;
+  // This block's k range: [k_base, k_base + K / splits).
+  const int k_len = static_cast<int>(K / splits);
+  const int k_base = static_cast<int>(split) * k_len;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -449,7 +464,8 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
                  :: "s"(lds_byte), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
   };
 #pragma clang diagnostic pop
-  auto issue = [&](float (&As)[BM][BK], BTile& Bs, int k0) {
+  auto issue = [&](float (&As)[BM][BK], BTile& Bs, int k_rel) {
+    const int k0 = k_base + k_rel;
     __builtin_amdgcn_sched_barrier(0);
     const unsigned a_lds = lds_of(&As[0][0]) + static_cast<unsigned>(wave * kARows * BK * 4);
 #pragma unroll
@@ -522,7 +538,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
     }
   };
 
-  const int k_tiles = static_cast<int>(K / BK);
+  const int k_tiles = k_len / BK;
   issue(A0, B0, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -540,12 +556,14 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
   }
   if (kt < k_tiles) compute(A0, B0);  // odd count: the last tile sits in stage 0
 
-  // Epilogue as in gemm_f32_kernel (full tiles: no bounds checks).
+  // Epilogue as in gemm_f32_kernel (full tiles: no bounds checks); a split
+  // block stores its raw partial sums.
   const std::int64_t col_base = n0 + wn * WN;
   auto col_of = [&](int j) { return kTransB ? 16 * j + r : frag_pos<TN>(r, j); };
+  const bool epilogue = !partial;
   float bias[TN];
 #pragma unroll
-  for (int j = 0; j < TN; ++j) bias[j] = a.bias != nullptr ? a.bias[col_base + col_of(j)] : 0.F;
+  for (int j = 0; j < TN; ++j) bias[j] = epilogue && a.bias != nullptr ? a.bias[col_base + col_of(j)] : 0.F;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -555,8 +573,11 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         float x = acc[i][j][q];
-        if (a.bias != nullptr) x = x + bias[j];
-        v[j] = activate(x, a.activation);
+        if (epilogue) {
+          if (a.bias != nullptr) x = x + bias[j];
+          x = activate(x, a.activation);
+        }
+        v[j] = x;
       }
       float* dst = C + row * N + col_base;
       if constexpr (kTransB) {
@@ -571,6 +592,27 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
   }
 }
 
+// out = act(partial[0] + ... + partial[splits - 1] (+ bias)) for the K-split
+// direct GEMM, the partial sums added in split order and the bias after them
+// (the unsplit epilogue's order: full sum, bias, activation). count4 float4s
+// of out; n % 4 == 0.
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ partial, float* __restrict__ out,
+                                                           const float* __restrict__ bias, std::int64_t count4,
+                                                           std::int64_t n, int splits, int act) {
+  const auto* p4 = reinterpret_cast<const float4_t*>(partial);
+  auto* o4 = reinterpret_cast<float4_t*>(out);
+  for (std::int64_t i = static_cast<std::int64_t>(blockIdx.x) * 256 + threadIdx.x; i < count4;
+       i += static_cast<std::int64_t>(gridDim.x) * 256) {
+    float4_t v = stream_load(p4 + i);
+    for (int sp = 1; sp < splits; ++sp) v += stream_load(p4 + sp * count4 + i);
+    if (bias != nullptr) {
+      const float* b = bias + (4 * i) % n;  // any alignment
+      v += float4_t{b[0], b[1], b[2], b[3]};
+    }
+    o4[i] = float4_t{activate(v.x, act), activate(v.y, act), activate(v.z, act), activate(v.w, act)};
+  }
+}
+
 // True when gemm_f32_direct_kernel<BM, BN, BK, ...> can take the problem:
 // full tiles, k > 0, and byte offsets inside one A row panel (BM x K) and one
 // B column panel (K x N, or BN x K transposed) below 2^31.
@@ -580,20 +622,32 @@ bool direct_fits(std::int64_t m, std::int64_t n, std::int64_t k) {
          static_cast<double>(BM) * k * 4 < 2147483647.0 && static_cast<double>(k) * n * 4 < 2147483647.0;
 }
 
+// Launches the direct kernel; with splits > 1 (K % (BK * splits) == 0 and a
+// workspace of splits x batches x m x n floats in args.partial) it runs
+// splits blocks per tile over K / splits each, then split_reduce_kernel.
 template <int BM, int BN, int BK, int WM, int WN, int kMinWaves>
 int launch_direct(GemmArgs& args, bool trans_b, hipStream_t stream) {
   if (!direct_fits<BM, BN, BK>(args.m, args.n, args.k))
     return fail(TCX_INTERNAL, "direct gemm needs full tiles and 31-bit panel offsets");
+  const std::int64_t splits = args.splits > 1 ? args.splits : 1;
+  if (splits > 1 && (args.k % (BK * splits) != 0 || args.partial == nullptr))
+    return fail(TCX_INTERNAL, "split gemm needs K a multiple of the split k-tiles and a workspace");
+  const std::int64_t batches = args.total_tiles;  // caller passes the batch count
   args.tiles_m = args.m / BM;
   args.tiles_n = args.n / BN;
-  args.total_tiles = args.tiles_m * args.tiles_n * args.total_tiles;  // caller passes the batch count
+  args.total_tiles = args.tiles_m * args.tiles_n * batches * splits;
   if (args.total_tiles > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
   const dim3 grid(static_cast<unsigned>(args.total_tiles)), block((BM / WM) * (BN / WN) * 64);
   if (trans_b)
     hipLaunchKernelGGL((gemm_f32_direct_kernel<BM, BN, BK, WM, WN, kMinWaves, true>), grid, block, 0, stream, args);
   else
     hipLaunchKernelGGL((gemm_f32_direct_kernel<BM, BN, BK, WM, WN, kMinWaves, false>), grid, block, 0, stream, args);
-  return check(hipGetLastError(), "gemm_f32 direct launch");
+  int rc = check(hipGetLastError(), "gemm_f32 direct launch");
+  if (rc != TCX_OK || splits == 1) return rc;
+  const std::int64_t count4 = batches * args.m * args.n / 4;
+  hipLaunchKernelGGL(split_reduce_kernel, dim3(grid_for(count4, 256, 256 * 16)), dim3(256), 0, stream, args.partial,
+                     args.out, args.bias, count4, args.n, static_cast<int>(splits), args.activation);
+  return check(hipGetLastError(), "gemm_f32 split reduce launch");
 }
 
 template <int BM, int BN, int BK, int WM, int WN, int kMinWaves, bool kVecOnly = false, int KS = 1>

@@ -34,7 +34,8 @@ EXPORTS = [
     "tcx_hip_pool_enter", "tcx_hip_pool_exit", "tcx_hip_pool_trim", "tcx_hip_pool_stats",
     "tcx_hip_pool_destroy", "tcx_hip_event_create", "tcx_hip_event_record",
     "tcx_hip_event_synchronize", "tcx_hip_event_elapsed_ms", "tcx_hip_event_destroy",
-    "tcx_hip_gemm_f32", "tcx_hip_reduce_workspace_bytes", "tcx_hip_reduce",
+    "tcx_hip_gemm_f32", "tcx_hip_gemm_workspace_bytes", "tcx_hip_gemm_f32_ws",
+    "tcx_hip_reduce_workspace_bytes", "tcx_hip_reduce",
     "tcx_hip_reduce_axes", "tcx_hip_softmax_f32", "tcx_hip_rmsnorm_f32", "tcx_hip_layernorm_f32",
     "tcx_hip_bias_act_f32", "tcx_hip_unary_f32", "tcx_hip_binary", "tcx_hip_fill",
     "tcx_hip_math_unary", "tcx_hip_clip", "tcx_hip_topk", "tcx_hip_embedding_f32",
@@ -118,6 +119,9 @@ def lib() -> ctypes.CDLL:
         L.tcx_hip_event_elapsed_ms.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_float)]
         L.tcx_hip_event_destroy.argtypes = [vp]
         L.tcx_hip_gemm_f32.argtypes = [vp, vp, vp, ctypes.POINTER(GemmDesc), vp]
+        L.tcx_hip_gemm_workspace_bytes.argtypes = [ctypes.POINTER(GemmDesc)]
+        L.tcx_hip_gemm_workspace_bytes.restype = sz
+        L.tcx_hip_gemm_f32_ws.argtypes = [vp, vp, vp, ctypes.POINTER(GemmDesc), vp, sz, vp]
         L.tcx_hip_reduce_workspace_bytes.argtypes = [ctypes.c_int, ctypes.c_int, i64, i64, i64]
         L.tcx_hip_reduce_workspace_bytes.restype = sz
         L.tcx_hip_reduce.argtypes = [ctypes.c_int, ctypes.c_int, vp, vp, i64, i64, i64, vp, sz, vp]
@@ -263,8 +267,20 @@ def gemm_desc(m, n, k, *, batch_shape=(), lhs_batch_strides=(), rhs_batch_stride
     return d
 
 
-def gemm(lhs: int, rhs: int, out: int, desc: GemmDesc, s: int | None = None) -> None:
-    check(lib().tcx_hip_gemm_f32(lhs, rhs, out, ctypes.byref(desc), s or stream()), "gemm")
+def gemm(lhs: int, rhs: int, out: int, desc: GemmDesc, s: int | None = None,
+         workspace: DeviceBuffer | None = None) -> None:
+    """tcx_hip_gemm_f32, or tcx_hip_gemm_f32_ws with a workspace (gemm_workspace)."""
+    if workspace is None:
+        check(lib().tcx_hip_gemm_f32(lhs, rhs, out, ctypes.byref(desc), s or stream()), "gemm")
+    else:
+        check(lib().tcx_hip_gemm_f32_ws(lhs, rhs, out, ctypes.byref(desc), workspace.address, workspace.nbytes,
+                                        s or stream()), "gemm")
+
+
+def gemm_workspace(desc: GemmDesc) -> DeviceBuffer | None:
+    """The workspace tcx_hip_gemm_f32_ws can use for desc (None when it needs none)."""
+    nbytes = lib().tcx_hip_gemm_workspace_bytes(ctypes.byref(desc))
+    return DeviceBuffer(nbytes) if nbytes else None
 
 
 def reduce(op: str, dtype: int, x: int, out: int, outer: int, reduce_: int, inner: int,

@@ -47,6 +47,24 @@ def test_library_exports_every_declared_symbol():
         assert getattr(lib, name) is not None
 
 
+@pytest.mark.parametrize("m,n,k,batch,trans,expect", [
+    (4096, 1024, 4096, (), True, 4 * 4096 * 1024 * 4),   # the MLP's second linear: 4 splits
+    (1024, 1024, 8192, (), False, 16 * 1024 * 1024 * 4),  # 16 tiles: 16 splits of 512
+    (512, 512, 8192, (4,), False, 16 * 4 * 512 * 512 * 4),  # batched: 16 tiles
+    (4096, 4096, 4096, (), False, 0),                     # 256 tiles already
+    (1000, 1000, 1000, (), False, 0),                     # partial tiles
+    (1024, 1024, 1024, (), False, 0),                     # splits would keep < 512 of K
+    (512, 512, 512, (), False, 0),
+])
+def test_gemm_workspace_query(m, n, k, batch, trans, expect):
+    if not capi.LIB_PATH.exists():
+        pytest.fail("libtensorcx_hip.so is not built: run `python tensor.cx_amd/build.py`")
+    strides = tuple(m * k for _ in batch), tuple(k * n for _ in batch)
+    d = capi.gemm_desc(m, n, k, batch_shape=batch, lhs_batch_strides=strides[0], rhs_batch_strides=strides[1],
+                       rhs_transposed=trans)
+    assert capi.lib().tcx_hip_gemm_workspace_bytes(ctypes.byref(d)) == expect
+
+
 def test_header_compiles_as_c():
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only", "-x", "c", str(HEADER)],
                    check=True)

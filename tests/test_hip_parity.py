@@ -64,6 +64,44 @@ def test_matmul_shapes(cx, m, k, n):
         assert_matmul(actual, expected, a, b, f"{m}x{k}x{n}")
 
 
+@pytest.mark.parametrize("sa,sb", [((1024, 8192), (8192, 1024)), ((2048, 4096), (4096, 2048)),
+                                   ((4, 512, 8192), (4, 8192, 512))])
+def test_matmul_split_k(cx, sa, sb):
+    # Few output tiles and a long K: K split over blocks through the pool
+    # workspace, checked against float64 truth at the matmul bar.
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal(sa).astype(np.float32)
+    b = rng.standard_normal(sb).astype(np.float32)
+    actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    assert_matmul(actual, a.astype(np.float64) @ b.astype(np.float64), a, b, f"split {sa}x{sb}")
+
+
+def test_gemm_split_k_matches_unsplit(cx):
+    # The C ABI with and without the workspace, linear form with bias + SiLU:
+    # both within the bar of float64 truth, and of each other.
+    import tensorcx_hip_capi as capi
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((2048, 4096)).astype(np.float32)
+    w = rng.standard_normal((1024, 4096)).astype(np.float32)
+    bias = rng.standard_normal(1024).astype(np.float32)
+    dx, dw, db = (capi.DeviceArray.from_numpy(t) for t in (x, w, bias))
+    d = capi.gemm_desc(2048, 1024, 4096, rhs_transposed=True, bias=db.ptr, activation="silu")
+    ws = capi.gemm_workspace(d)
+    assert ws is not None and ws.nbytes == 8 * 2048 * 1024 * 4
+    outs = []
+    for workspace in (None, ws):
+        out = capi.DeviceArray((2048, 1024))
+        capi.gemm(dx.ptr, dw.ptr, out.ptr, d, None, workspace)
+        capi.synchronize()
+        outs.append(out.numpy())
+    pre = x.astype(np.float64) @ w.astype(np.float64).T + bias
+    truth = pre / (1 + np.exp(-pre))
+    scale = 1e-4 * np.sqrt(4096) * np.sqrt(np.mean(x.astype(np.float64) ** 2) * np.mean(w.astype(np.float64) ** 2))
+    for out in outs:
+        assert np.max(np.abs(out - truth)) <= scale
+    assert np.max(np.abs(outs[0] - outs[1])) <= scale
+
+
 def test_matmul_dyadic_is_exact(cx):
     # Dyadic inputs make every partial sum exact, so any order matches bitwise.
     i = np.arange(6 * 130 * 70)
