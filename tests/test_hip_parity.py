@@ -76,6 +76,27 @@ def test_matmul_split_k(cx, sa, sb):
     assert_matmul(actual, a.astype(np.float64) @ b.astype(np.float64), a, b, f"split {sa}x{sb}")
 
 
+def test_matmul_split_k_special_values(cx):
+    # Non-finite values in different K splits: +inf alone, +inf and -inf in two
+    # splits of one row, NaN. The partials add as the unsplit sum would:
+    # NaN / inf positions and signs as float64 truth, the rest at the bar.
+    rng = np.random.default_rng(13)
+    a = rng.standard_normal((1024, 8192)).astype(np.float32)
+    b = rng.standard_normal((8192, 1024)).astype(np.float32)
+    a[0, 10] = np.inf
+    a[1, 100], a[1, 5000] = np.inf, -np.inf
+    a[2, 7000] = np.nan
+    actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    with np.errstate(invalid="ignore"):
+        truth = a.astype(np.float64) @ b.astype(np.float64)
+    head = slice(0, 3)
+    assert np.array_equal(np.isnan(actual[head]), np.isnan(truth[head]))
+    assert np.array_equal(np.isinf(actual[head]), np.isinf(truth[head]))
+    inf = np.isinf(truth[head])
+    assert np.array_equal(np.sign(actual[head][inf]), np.sign(truth[head][inf]))
+    assert_matmul(actual[3:], truth[3:], a[3:], b, "split special values, finite rows")
+
+
 def test_gemm_split_k_matches_unsplit(cx):
     # The C ABI with and without the workspace, linear form with bias + SiLU:
     # both within the bar of float64 truth, and of each other.
