@@ -304,8 +304,8 @@ def main() -> int:
                         help="only run 1 GiB device-to-device copies (PMC byte-counter calibration)")
     args = parser.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: every GPU box here has one MI355X; --gpus {args.gpus} is "
-              "not supported (the multi-GPU sharding plan is described in DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU: this build runs every kernel on one MI355X and has no "
+              f"multi-GPU path, so --gpus {args.gpus} is not supported", file=sys.stderr)
         return 2
     if not capi.available():
         print(f"no usable HIP device: {capi.last_error()}", file=sys.stderr)
