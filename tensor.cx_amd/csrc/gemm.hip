@@ -123,11 +123,11 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
   // there are >= 256 of them (one full round on 256 CUs). Fewer output tiles
   // leave the CUs short of waves, so the smaller tiles split K inside the
   // block: 128x128 blocks of two groups of eight 32x64 waves (4 waves/SIMD)
-  // when there are >= 256 of those, else 64x64 blocks of four groups of four
-  // 32x32 waves when there are >= 256 of those (1000^3), else 32x32 blocks of
-  // eight one-wave groups with 32-wide k-tiles (small shapes; 512^3: 17.9 ->
-  // 11.8 us). The measured gains were 7% on the MLP's 4096x1024x4096 GEMM and
-  // 21% on 1000^3 over the same tiles without the split.
+  // when there are enough of those (below), else 64x64 blocks of four groups
+  // of four 32x32 waves when there are >= 128 of those (1000^3), else 32x32
+  // blocks of eight one-wave groups with 32-wide k-tiles (small shapes; 512^3:
+  // 17.9 -> 11.8 us). The measured gains were 7% on the MLP's 4096x1024x4096
+  // GEMM and 21% on 1000^3 over the same tiles without the split.
   const std::int64_t tiles_256 = ((d->m + 255) / 256) * ((d->n + 255) / 256) * batches;
   // (Unaligned shapes take the scalar-load variant, which does not fit the
   // 256x256 tile's registers; they use the 128x128 tile.)
@@ -148,9 +148,19 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
     }
   }
   if (vec && tiles_256 >= 256) return launch_config<256, 256, 32, 64, 128, 2, true>(args, trans_b, true, s);
-  if (((d->m + 127) / 128) * ((d->n + 127) / 128) * batches >= 256)
+  // 128x128 tiles when there are >= 256 of them and the last round of 256
+  // blocks is >= 90 % full (3000x3000x1000: 576 tiles fill 75 % and ran 221 us
+  // against 203 us with 64x64 tiles).
+  const std::int64_t tiles_128 = ((d->m + 127) / 128) * ((d->n + 127) / 128) * batches;
+  if (tiles_128 >= 256 && tiles_128 * 10 >= (tiles_128 + 255) / 256 * 256 * 9)
     return launch_config<128, 128, 16, 32, 64, 2, false, 2>(args, trans_b, vec, s);
-  if (((d->m + 63) / 64) * ((d->n + 63) / 64) * batches < 256)
-    return launch_config<32, 32, 32, 32, 32, 2, false, 8>(args, trans_b, vec, s);
+  const std::int64_t tiles_64 = ((d->m + 63) / 64) * ((d->n + 63) / 64) * batches;
+  if (tiles_64 < 128) return launch_config<32, 32, 32, 32, 32, 2, false, 8>(args, trans_b, vec, s);
+  // Up to three rounds of 64x64 tiles: the direct-to-LDS 64x64 kernel, edge
+  // tiles included (1000^3: 30.0 -> 28.5 us, transposed 31.2 -> 28.1 us,
+  // 768^3 23.4 -> 22.6 us). With more rounds the register-staged kernel
+  // measured as fast or faster (3000x3000x1000: 203 against 212 us).
+  if (vec && tiles_64 <= 768 && gemm::direct64_fits(d->m, d->n, d->k))
+    return gemm::launch_direct64(args, trans_b, s);
   return launch_config<64, 64, 16, 32, 32, 4, false, 4>(args, trans_b, vec, s);
 }

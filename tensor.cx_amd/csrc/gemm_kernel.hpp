@@ -650,6 +650,246 @@ int launch_direct(GemmArgs& args, bool trans_b, hipStream_t stream) {
   return check(hipGetLastError(), "gemm_f32 split reduce launch");
 }
 
+// Direct-to-LDS GEMM for 64x64 output tiles of any shape (edge tiles
+// included): 16 waves in four K groups of four 32x32 waves, each group taking
+// 16 of every 64 staged k (its partial tile is added in group order at the
+// end, as in gemm_f32_kernel with KS = 4). Tiles go from HBM to LDS with
+// buffer_load ... lds through four stages (three tiles in flight), two
+// 16-byte instructions per wave and stage.
+//   Edges: each operand panel is read through a buffer resource whose
+//   num_records ends at the matrix, so rows past M (and past N for a
+//   transposed B, or k rows past K for a [k, n] B) read as zero. Lanes whose
+//   k is past K in an A row (or a transposed B row) get an out-of-range offset
+//   and read zero too, so that a value past K, which may be infinite, never
+//   meets the zero of the other operand. Columns past N of a [k, n] B read
+//   the next row's data, which only reaches output columns that are not
+//   stored.
+//   LDS layouts (conflict-free reads): A (and a transposed B) [64 rows][64 k]
+//   with the 16-byte chunk c of row r at c ^ (r & 15); a [k, n] B
+//   [64 k][64 n] with chunk c of k row kr at c ^ (8 ((kr >> 2) & 1)), which
+//   puts the two k rows one 32-lane read pass takes in opposite halves of
+//   the banks.
+//   Output column of MFMA column r in block j: 32 wn + 2r + j for a [k, n] B
+//   (a lane's two columns are adjacent, one 8-byte read per k), 32 wn + 16j +
+//   r for a transposed B.
+template <bool kTransB>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8))) void gemm_f32_direct64_kernel(
+    GemmArgs a) {
+  constexpr int BM = 64, BN = 64, KS = 4, BKT = 64, kStages = 4;
+  constexpr int kGroupWaves = 4;
+  constexpr std::int64_t kGroupM = 8;
+  __shared__ float As[kStages][BM][BKT];
+  __shared__ float Bs[kStages][64][64];  // [n][k] transposed, [k][n] otherwise
+
+  const std::int64_t grid = a.total_tiles;
+  const std::int64_t bid = blockIdx.x;
+  const std::int64_t tile = (grid % 8 == 0) ? (bid % 8) * (grid / 8) + bid / 8 : bid;
+  const std::int64_t per_batch = a.tiles_m * a.tiles_n;
+  const std::int64_t batch = tile / per_batch;
+  const std::int64_t t = tile % per_batch;
+  const std::int64_t group_tiles = kGroupM * a.tiles_n;
+  const std::int64_t first_m = (t / group_tiles) * kGroupM;
+  const std::int64_t gm = min(a.tiles_m - first_m, kGroupM);
+  const std::int64_t tm = first_m + (t % group_tiles) % gm;
+  const std::int64_t tn = (t % group_tiles) / gm;
+  std::int64_t lhs_off = 0, rhs_off = 0;
+  {
+    std::int64_t b = batch;
+    for (int ax = a.batch_rank - 1; ax >= 0; --ax) {
+      const std::int64_t e = a.batch_shape[ax];
+      const std::int64_t c = b % e;
+      b /= e;
+      lhs_off += c * a.lhs_bs[ax];
+      rhs_off += c * a.rhs_bs[ax];
+    }
+  }
+  const std::int64_t M = a.m, N = a.n, K = a.k;
+  const float* __restrict__ A = a.lhs + lhs_off;
+  const float* __restrict__ B = a.rhs + rhs_off;
+  float* __restrict__ C = a.out + batch * M * N;
+  const std::int64_t m0 = tm * BM, n0 = tn * BN;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int group = wave / kGroupWaves, gwave = wave % kGroupWaves;
+  const int wm = gwave / 2, wn = gwave % 2;
+  const int r = lane & 15, kl = lane >> 4;
+
+  using int4v = int __attribute__((ext_vector_type(4)));
+  auto rsrc_of = [](const float* base, std::int64_t bytes) {
+    const auto addr = reinterpret_cast<std::uint64_t>(base);
+    return int4v{static_cast<int>(addr), static_cast<int>(addr >> 32), static_cast<int>(bytes), 0x00020000};
+  };
+  // Panels: A rows m0.. (M - m0 rows), B columns n0.. (a [k, n] B: through
+  // its last element) or rows n0.. (transposed: N - n0 rows). The launcher
+  // checks that every panel spans less than 2^31 bytes.
+  const int4v a_rsrc = rsrc_of(A + m0 * K, (M - m0) * K * 4);
+  const int4v b_rsrc = kTransB ? rsrc_of(B + n0 * K, (N - n0) * K * 4) : rsrc_of(B + n0, (K * N - n0) * 4);
+  // Instruction of wave w: rows 4w .. 4w + 3 of the stage's A tile and of its
+  // B tile; lane i fills chunk slot i % 16 of row 4w + i / 16.
+  const int row = 4 * wave + lane / 16, slot = lane % 16;
+  const int a_chunk = slot ^ (row & 15);
+  const int a_voff = (row * static_cast<int>(K) + 4 * a_chunk) * 4;
+  const int b_chunk = kTransB ? a_chunk : slot ^ (8 * ((row >> 2) & 1));
+  const int b_voff = kTransB ? a_voff : (row * static_cast<int>(N) + 4 * b_chunk) * 4;
+  auto lds_of = [](const void* p) {
+    return static_cast<unsigned>(reinterpret_cast<std::uintptr_t>((__attribute__((address_space(3))) const void*)p));
+  };
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  auto dma16 = [](const int4v& rsrc, unsigned lds_byte, int voff, int soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :: "s"(lds_byte), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
+  };
+#pragma clang diagnostic pop
+  // An offset past every panel (voff + soff stays below 2^32): a zero read.
+  constexpr int kOut = 0x7fffffff;
+  auto issue = [&](int stage, int k0) {
+    const unsigned row_byte = static_cast<unsigned>(4 * wave * 64 * 4);
+    const bool a_in = k0 + 4 * a_chunk < K;
+    dma16(a_rsrc, lds_of(&As[stage][0][0]) + row_byte, a_in ? a_voff : kOut, __builtin_amdgcn_readfirstlane(k0 * 4));
+    if constexpr (kTransB) {
+      dma16(b_rsrc, lds_of(&Bs[stage][0][0]) + row_byte, a_in ? b_voff : kOut,
+            __builtin_amdgcn_readfirstlane(k0 * 4));
+    } else {
+      dma16(b_rsrc, lds_of(&Bs[stage][0][0]) + row_byte, b_voff,
+            __builtin_amdgcn_readfirstlane(k0 * static_cast<int>(N) * 4));
+    }
+  };
+
+  floatx4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.F, 0.F, 0.F, 0.F};
+  auto compute = [&](int stage) {
+    const int kc = group * 4 + kl;  // this lane's k chunk of the group's 16 k
+    float4_t a4[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int ar = wm * 32 + 16 * i + r;
+      a4[i] = *reinterpret_cast<const float4_t*>(&As[stage][ar][4 * (kc ^ (ar & 15))]);
+    }
+    if constexpr (kTransB) {
+      float4_t b4[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int bc = wn * 32 + 16 * j + r;
+        b4[j] = *reinterpret_cast<const float4_t*>(&Bs[stage][bc][4 * (kc ^ (bc & 15))]);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[i][q], b4[j][q], acc[i][j], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int kr = group * 16 + 4 * kl + q;
+        const int c = wn * 8 + r / 2;  // chunk of columns 32 wn + 2r, + 1
+        using float2v = float __attribute__((ext_vector_type(2)));
+        const float2v bv =
+            *reinterpret_cast<const float2v*>(&Bs[stage][kr][4 * (c ^ (8 * ((kr >> 2) & 1))) + 2 * (r & 1)]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[i][q], bv.x, acc[i][0], 0, 0, 0);
+          acc[i][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[i][q], bv.y, acc[i][1], 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  // Pipeline: tiles kt + 1 and kt + 2 are in flight while tile kt is read;
+  // tile kt + 3 goes into the stage tile kt - 1 used, free since the last
+  // barrier. Each wave has two loads per tile outstanding.
+  const int k_tiles = static_cast<int>((K + BKT - 1) / BKT);
+  for (int p = 0; p < 3 && p < k_tiles; ++p) issue(p, p * BKT);
+  if (k_tiles > 2) __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4): tile 0 has landed
+  else __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int kt = 0; kt < k_tiles; ++kt) {
+    if (kt + 3 < k_tiles) issue((kt + 3) % kStages, (kt + 3) * BKT);
+    compute(kt % kStages);
+    if (kt + 3 < k_tiles) __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4): tile kt + 1 has landed
+    else __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // Groups 1..3 pass their partial tiles through LDS (the stages are free
+  // after the last barrier); group 0 adds them in group order.
+  float* red = &As[0][0][0];  // (KS - 1) x 4 waves x 64 lanes x 16 floats = 48 KB
+  if (group > 0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          red[((((group - 1) * kGroupWaves + gwave) * 16 + (i * 2 + j) * 4 + q) * 64) + lane] = acc[i][j][q];
+  }
+  __syncthreads();
+  if (group > 0) return;
+#pragma unroll
+  for (int g = 1; g < KS; ++g)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          acc[i][j][q] += red[((((g - 1) * kGroupWaves + gwave) * 16 + (i * 2 + j) * 4 + q) * 64) + lane];
+
+  auto col_of = [&](int j) { return kTransB ? 16 * j + r : 2 * r + j; };
+  float bias[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const std::int64_t col = n0 + wn * 32 + col_of(j);
+    bias[j] = a.bias != nullptr && col < N ? a.bias[col] : 0.F;
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const std::int64_t orow = m0 + wm * 32 + 16 * i + 4 * kl + q;
+      if (orow >= M) continue;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const std::int64_t col = n0 + wn * 32 + col_of(j);
+        if (col >= N) continue;
+        float x = acc[i][j][q];
+        if (a.bias != nullptr) x = x + bias[j];
+        C[orow * N + col] = activate(x, a.activation);
+      }
+    }
+}
+
+// True when gemm_f32_direct64_kernel can take the problem: 16-byte rows
+// (k and n multiples of 4, 16-byte aligned operands, checked by the caller)
+// and every byte offset into a panel, a tile's 64 rows included, below 2^31.
+inline bool direct64_fits(std::int64_t m, std::int64_t n, std::int64_t k) {
+  constexpr double kLimit = 2147483647.0;
+  const double rows_m = static_cast<double>(m < 64 ? 64 : m), rows_n = static_cast<double>(n < 64 ? 64 : n);
+  return m > 0 && n > 0 && k > 0 && k % 4 == 0 && n % 4 == 0 && rows_m * k * 4 < kLimit &&
+         rows_n * k * 4 < kLimit && (static_cast<double>(k) + 64) * n * 4 < kLimit;
+}
+
+inline int launch_direct64(GemmArgs& args, bool trans_b, hipStream_t stream) {
+  if (!direct64_fits(args.m, args.n, args.k))
+    return fail(TCX_INTERNAL, "direct 64x64 gemm needs 16-byte rows and 31-bit panel offsets");
+  args.tiles_m = (args.m + 63) / 64;
+  args.tiles_n = (args.n + 63) / 64;
+  args.total_tiles = args.tiles_m * args.tiles_n * args.total_tiles;  // caller passes the batch count
+  if (args.total_tiles > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
+  const dim3 grid(static_cast<unsigned>(args.total_tiles)), block(1024);
+  if (trans_b)
+    hipLaunchKernelGGL(gemm_f32_direct64_kernel<true>, grid, block, 0, stream, args);
+  else
+    hipLaunchKernelGGL(gemm_f32_direct64_kernel<false>, grid, block, 0, stream, args);
+  return check(hipGetLastError(), "gemm_f32 direct 64x64 launch");
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int kMinWaves, bool kVecOnly = false, int KS = 1>
 int launch_config(GemmArgs& args, bool trans_b, bool vec, hipStream_t stream) {
   args.tiles_m = (args.m + BM - 1) / BM;

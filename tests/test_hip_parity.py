@@ -51,7 +51,7 @@ def test_golden_vectors(cx, golden):
 @pytest.mark.parametrize("m,k,n", [(1, 1, 1), (2, 3, 4), (15, 17, 31), (17, 16, 15), (32, 33, 16),
                                    (0, 3, 4), (3, 0, 4), (3, 4, 0), (65, 129, 67), (128, 128, 128),
                                    (129, 255, 257), (300, 64, 200), (700, 300, 500), (512, 512, 512),
-                                   (1000, 1000, 1000)])
+                                   (768, 768, 768), (1000, 1000, 1000), (1000, 1004, 996)])
 def test_matmul_shapes(cx, m, k, n):
     rng = np.random.default_rng(7)
     a = rng.standard_normal((m, k)).astype(np.float32)
@@ -62,6 +62,42 @@ def test_matmul_shapes(cx, m, k, n):
         assert_bits(actual, expected, "k=0")
     else:
         assert_matmul(actual, expected, a, b, f"{m}x{k}x{n}")
+
+
+def test_matmul_direct64_k_tail_isolation(cx):
+    # 64x64 direct-to-LDS tiles with a K tail (1000 = 15 x 64 + 40): an
+    # infinity at the start of the next row, which the tail of a row's last
+    # k-tile would read, must not reach that row (it is zeroed, not 0 * inf).
+    rng = np.random.default_rng(14)
+    a = rng.standard_normal((1000, 1000)).astype(np.float32)
+    b = rng.standard_normal((1000, 1000)).astype(np.float32)
+    a[5, 0] = np.inf        # row 4's tail reads a[5, 0..23] past its K
+    a[9, 999] = -np.inf     # row 9 itself: -inf times its B row
+    actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    with np.errstate(invalid="ignore"):
+        truth = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.all(np.isfinite(actual[4])) and np.all(np.isfinite(actual[10]))
+    bad = [5, 9]
+    assert np.array_equal(np.isinf(actual[bad]), np.isinf(truth[bad]))
+    assert np.array_equal(np.isnan(actual[bad]), np.isnan(truth[bad]))
+    keep = np.setdiff1d(np.arange(1000), bad)
+    assert_matmul(actual[keep], truth[keep], a[keep], b, "direct64 finite rows")
+    # Transposed B (a linear's weight): the weight row after a column's row.
+    w = rng.standard_normal((1000, 1000)).astype(np.float32)
+    w[7, 0] = np.inf
+    lin = cx.linear(cx.tensor(a[keep[:512]], device="hip"), cx.tensor(w, device="hip")).numpy()
+    with np.errstate(invalid="ignore"):
+        lt = a[keep[:512]].astype(np.float64) @ w.astype(np.float64).T
+    assert np.all(np.isfinite(lin[:, 6])) and np.array_equal(np.isinf(lin[:, 7]), np.isinf(lt[:, 7]))
+
+
+@pytest.mark.parametrize("sa,sb", [((4, 500, 700), (4, 700, 600)), ((3, 1000, 1000), (1000, 1000))])
+def test_matmul_direct64_batched(cx, sa, sb):
+    rng = np.random.default_rng(15)
+    a = rng.standard_normal(sa).astype(np.float32)
+    b = rng.standard_normal(sb).astype(np.float32)
+    actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    assert_matmul(actual, a.astype(np.float64) @ b.astype(np.float64), a, b, f"direct64 {sa}x{sb}")
 
 
 @pytest.mark.parametrize("sa,sb", [((1024, 8192), (8192, 1024)), ((2048, 4096), (4096, 2048)),
