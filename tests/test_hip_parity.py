@@ -91,8 +91,13 @@ def test_matmul_direct64_k_tail_isolation(cx):
     assert np.all(np.isfinite(lin[:, 6])) and np.array_equal(np.isinf(lin[:, 7]), np.isinf(lt[:, 7]))
 
 
-@pytest.mark.parametrize("sa,sb", [((4, 500, 700), (4, 700, 600)), ((3, 1000, 1000), (1000, 1000))])
+@pytest.mark.parametrize("sa,sb", [((4, 500, 700), (4, 700, 600)), ((3, 1000, 1000), (1000, 1000)),
+                                   ((8192, 1000), (1000, 4)), ((4, 1000), (1000, 8192)),
+                                   ((999, 1001), (1001, 1003))])
 def test_matmul_direct64_batched(cx, sa, sb):
+    # Batched and skinny 64x64-tile shapes (a 4-wide n or m: all but 4 rows or
+    # columns of each tile past the edge), and an unaligned k (1001) that
+    # takes the register-staged 64x64 tile instead.
     rng = np.random.default_rng(15)
     a = rng.standard_normal(sa).astype(np.float32)
     b = rng.standard_normal(sb).astype(np.float32)
