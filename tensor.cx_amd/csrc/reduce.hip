@@ -290,14 +290,19 @@ __global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, 
   }
 }
 
-// One 256-thread block per row combines that row's segment partials: thread
-// t folds segments t, t+256, ... in order, then waves and the block combine in
-// a fixed order, so the result is deterministic.
-template <int kOp, typename T>
-__global__ __launch_bounds__(256) void finish_kernel(const Partial* __restrict__ partials,
-                                                     void* __restrict__ out, std::int64_t rows,
-                                                     std::int64_t reduce, std::int64_t segments) {
-  __shared__ Partial waves[4];
+// One block of kThreads threads per row combines that row's segment
+// partials: thread t folds segments t, t + kThreads, ... in order (kUnroll
+// independent loads per step), then the waves and the block combine in a fixed
+// order, so the result is deterministic. 1024 threads fetch the 8192 partials
+// of a full-tensor sum in one round of loads (the partials come from the L2 of
+// every XCD), 256 suit many rows with few segments each.
+template <int kOp, typename T, int kThreads>
+__global__ __launch_bounds__(kThreads) void finish_kernel(const Partial* __restrict__ partials,
+                                                          void* __restrict__ out, std::int64_t rows,
+                                                          std::int64_t reduce, std::int64_t segments) {
+  constexpr int kWaves = kThreads / 64;
+  constexpr int kUnroll = 8192 / kThreads < 16 ? 8192 / kThreads : 16;
+  __shared__ Partial waves[kWaves];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const std::int64_t row = blockIdx.x;
   if (row >= rows) return;
@@ -306,49 +311,59 @@ __global__ __launch_bounds__(256) void finish_kernel(const Partial* __restrict__
   constexpr bool kLargest = kOp != TCX_REDUCE_MIN;
   if constexpr (kSum) {
     if constexpr (__is_same(T, float)) {
-      // Sum partials are dense 32-bit words; 16 independent loads per step.
+      // Sum partials are dense 32-bit words.
       const std::uint32_t* w = reinterpret_cast<const std::uint32_t*>(partials) + row * segments;
-      float acc[16] = {};
+      float acc[kUnroll] = {};
       std::int64_t i = threadIdx.x;
-      for (; i + 15 * 256 < segments; i += 16 * 256) {
+      for (; i + (kUnroll - 1) * kThreads < segments; i += kUnroll * kThreads) {
 #pragma unroll
-        for (int u = 0; u < 16; ++u) acc[u] += from_bits<float>(w[i + u * 256]);
+        for (int u = 0; u < kUnroll; ++u) acc[u] += from_bits<float>(w[i + u * kThreads]);
       }
-      for (; i < segments; i += 256) acc[0] += from_bits<float>(w[i]);
+      for (; i < segments; i += kThreads) acc[0] += from_bits<float>(w[i]);
 #pragma unroll
-      for (int u = 8; u > 0; u >>= 1)
+      for (int u = kUnroll / 2; u > 0; u >>= 1)
 #pragma unroll
         for (int v = 0; v < u; ++v) acc[v] += acc[v + u];
       float s = wave_sum(acc[0]);
       if (lane == 0) waves[wave] = Partial{to_bits(s), 0U, 0};
       __syncthreads();
       if (threadIdx.x == 0) {
-        const float t = (from_bits<float>(waves[0].bits) + from_bits<float>(waves[1].bits)) +
-                        (from_bits<float>(waves[2].bits) + from_bits<float>(waves[3].bits));
-        static_cast<float*>(out)[row] = kOp == TCX_REDUCE_MEAN ? t / static_cast<float>(reduce) : t;
+        // Pairwise over the waves: (w0 + w1) + (w2 + w3) for four, and so on.
+        float t[kWaves];
+#pragma unroll
+        for (int k = 0; k < kWaves; ++k) t[k] = from_bits<float>(waves[k].bits);
+#pragma unroll
+        for (int u = kWaves / 2; u > 0; u >>= 1)
+#pragma unroll
+          for (int v = 0; v < u; ++v) t[v] = t[2 * v] + t[2 * v + 1];
+        static_cast<float*>(out)[row] = kOp == TCX_REDUCE_MEAN ? t[0] / static_cast<float>(reduce) : t[0];
       }
     } else {
       const std::uint32_t* w = reinterpret_cast<const std::uint32_t*>(partials) + row * segments;
-      std::uint32_t acc[16] = {};
+      std::uint32_t acc[kUnroll] = {};
       std::int64_t i = threadIdx.x;
-      for (; i + 15 * 256 < segments; i += 16 * 256) {
+      for (; i + (kUnroll - 1) * kThreads < segments; i += kUnroll * kThreads) {
 #pragma unroll
-        for (int u = 0; u < 16; ++u) acc[u] += w[i + u * 256];
+        for (int u = 0; u < kUnroll; ++u) acc[u] += w[i + u * kThreads];
       }
-      for (; i < segments; i += 256) acc[0] += w[i];
+      for (; i < segments; i += kThreads) acc[0] += w[i];
       std::uint32_t s = 0;
 #pragma unroll
-      for (int u = 0; u < 16; ++u) s += acc[u];
+      for (int u = 0; u < kUnroll; ++u) s += acc[u];
       s = wave_sum_u32(s);
       if (lane == 0) waves[wave] = Partial{s, 0U, 0};
       __syncthreads();
-      if (threadIdx.x == 0)
-        static_cast<int*>(out)[row] = static_cast<int>(waves[0].bits + waves[1].bits + waves[2].bits + waves[3].bits);
+      if (threadIdx.x == 0) {
+        std::uint32_t t = 0;
+#pragma unroll
+        for (int k = 0; k < kWaves; ++k) t += waves[k].bits;
+        static_cast<int*>(out)[row] = static_cast<int>(t);
+      }
     }
   } else {
     T best{};
     std::int64_t bi = -1;
-    for (std::int64_t i = threadIdx.x; i < segments; i += 256) {
+    for (std::int64_t i = threadIdx.x; i < segments; i += kThreads) {
       const T v = from_bits<T>(p[i].bits);
       if (cand_better<T, kLargest>(v, p[i].index, best, bi)) {
         best = v;
@@ -359,7 +374,7 @@ __global__ __launch_bounds__(256) void finish_kernel(const Partial* __restrict__
     if (lane == 0) waves[wave] = Partial{to_bits(best), 0U, bi};
     __syncthreads();
     if (threadIdx.x == 0) {
-      for (int w = 1; w < 4; ++w) {
+      for (int w = 1; w < kWaves; ++w) {
         const T v = from_bits<T>(waves[w].bits);
         if (cand_better<T, kLargest>(v, waves[w].index, best, bi)) {
           best = v;
@@ -587,8 +602,12 @@ int launch_reduce(const T* x, void* out, std::int64_t outer, std::int64_t reduce
                        reduce, plan.segments, plan.seg_len);
   int rc = check(hipGetLastError(), "reduce row kernel launch");
   if (rc != TCX_OK || plan.segments == 1) return rc;
-  hipLaunchKernelGGL((finish_kernel<kOp, T>), dim3(static_cast<unsigned>(outer)), dim3(256), 0, s, partials, out,
-                     outer, reduce, plan.segments);
+  if (plan.segments >= 2048)
+    hipLaunchKernelGGL((finish_kernel<kOp, T, 1024>), dim3(static_cast<unsigned>(outer)), dim3(1024), 0, s, partials,
+                       out, outer, reduce, plan.segments);
+  else
+    hipLaunchKernelGGL((finish_kernel<kOp, T, 256>), dim3(static_cast<unsigned>(outer)), dim3(256), 0, s, partials,
+                       out, outer, reduce, plan.segments);
   return check(hipGetLastError(), "reduce finish kernel launch");
 }
 
