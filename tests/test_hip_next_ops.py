@@ -390,6 +390,21 @@ def test_fused_attention_many_batch_matrices(cx, causal):
     attention_check(cx, q, k, v, None, causal)
 
 
+@pytest.mark.parametrize("d", [32, 64, 128])
+def test_fused_attention_causal_value_scan(cx, d):
+    # Non-finite values in V rows behind the causal mask of whole query tiles:
+    # the tail scan (rows past a block's last run tile) must flag exactly their
+    # columns, across its 8-deep unrolled passes and its remainder loop.
+    q, k, v = f32((2, 700, d), 31), f32((2, 700, d), 32), f32((2, 700, d), 33)
+    v[0, 650, 3] = np.nan
+    v[0, 699, d - 1] = np.inf
+    v[0, 130, 0] = -np.inf
+    v[1, 64, d // 2] = np.inf     # the first row the first query tile's scan reads
+    v[1, 520, 1] = np.nan
+    with np.errstate(all="ignore"):
+        attention_check(cx, q, k, v, None, True)
+
+
 def test_fused_attention_special_values(cx):
     q, k, v = f32((1, 70, 64), 4), f32((1, 90, 64), 5), f32((1, 90, 64), 6)
     q[0, 3, 7] = np.nan            # a NaN query: its row is NaN
