@@ -390,60 +390,78 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
   __shared__ float A0[BM][BK], A1[BM][BK];
   __shared__ BTile B0, B1;
 
-  // Same XCD-aware tile order as gemm_f32_kernel, over (split, batch, tile)
-  // work items (split-major, so the blocks of one XCD share panels).
-  const std::int64_t grid = a.total_tiles;
-  const std::int64_t bid = blockIdx.x;
-  const std::int64_t item = (grid % 8 == 0) ? (bid % 8) * (grid / 8) + bid / 8 : bid;
-  const std::int64_t splits = a.splits > 1 ? a.splits : 1;
-  const std::int64_t per_split = grid / splits;
-  const std::int64_t split = item / per_split;
-  const std::int64_t tile = item % per_split;
-  const std::int64_t per_batch = a.tiles_m * a.tiles_n;
-  const std::int64_t batch = tile / per_batch;
-  const std::int64_t t = tile % per_batch;
-  constexpr std::int64_t kGroupM = 8;
-  const std::int64_t group_tiles = kGroupM * a.tiles_n;
-  const std::int64_t first_m = (t / group_tiles) * kGroupM;
-  const std::int64_t gm = min(a.tiles_m - first_m, kGroupM);
-  const std::int64_t tm = first_m + (t % group_tiles) % gm;
-  const std::int64_t tn = (t % group_tiles) / gm;
-  std::int64_t lhs_off = 0, rhs_off = 0;
-  {
-    std::int64_t b = batch;
-    for (int ax = a.batch_rank - 1; ax >= 0; --ax) {
-      const std::int64_t e = a.batch_shape[ax];
-      const std::int64_t c = b % e;
-      b /= e;
-      lhs_off += c * a.lhs_bs[ax];
-      rhs_off += c * a.rhs_bs[ax];
-    }
+  // Work items are (split, batch, tile), split-major, in the XCD-aware tile
+  // order of gemm_f32_kernel. A grid of fewer blocks than items is persistent:
+  // block b runs XCD b % 8's items (b / 8) + j (gridDim / 8), so each round
+  // of an XCD's blocks covers consecutive items that share panels in its L2.
+  // Item counts fit 31 bits (the launcher checks). The transposed-B variant
+  // runs one item per block: its loop state would not fit the registers left
+  // beside the 252 it uses (the persistent build reloaded spills in the k loop).
+  constexpr bool kPersist = !kTransB;
+  const int items = static_cast<int>(a.total_tiles);
+  const int blocks = static_cast<int>(gridDim.x), bid = static_cast<int>(blockIdx.x);
+  int item = bid, item_step = blocks, item_end = items;
+  if (items % 8 == 0 && blocks % 8 == 0) {
+    const int xcd = bid % 8, xcd_items = items / 8;
+    item = xcd * xcd_items + bid / 8;
+    item_step = blocks / 8;
+    item_end = (xcd + 1) * xcd_items;
   }
+  const int splits = a.splits > 1 ? a.splits : 1;
+  const int per_split = items / splits;
+  const int per_batch = static_cast<int>(a.tiles_m * a.tiles_n);
+  const int tiles_m = static_cast<int>(a.tiles_m), tiles_n = static_cast<int>(a.tiles_n);
   const std::int64_t M = a.m, N = a.n, K = a.k;
-  const float* __restrict__ A = a.lhs + lhs_off;
-  const float* __restrict__ B = a.rhs + rhs_off;
   const bool partial = splits > 1;
-  float* __restrict__ C = partial ? a.partial + (split * (per_split / per_batch) + batch) * M * N
-                                  : a.out + batch * M * N;
-  const std::int64_t m0 = tm * BM, n0 = tn * BN;
-  // This block's k range: [k_base, k_base + K / splits).
+  // Each item's k range: [k_base, k_base + K / splits).
   const int k_len = static_cast<int>(K / splits);
-  const int k_base = static_cast<int>(split) * k_len;
 
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  auto achunk = [](int row, int kc) { return kc ^ ((row >> 1) & 7); };
-
-  // Buffer resources based at the block's A row panel and B column panel; a
-  // 32-bit byte offset per lane and a scalar offset per instruction and tile
-  // (the launcher checks that both panels span less than 2^31 bytes).
   using int4v = int __attribute__((ext_vector_type(4)));
   auto rsrc_of = [](const float* base) {
     const auto addr = reinterpret_cast<std::uint64_t>(base);
     return int4v{static_cast<int>(addr), static_cast<int>(addr >> 32), 0x7fffffff, 0x00020000};
   };
-  const int4v a_rsrc = rsrc_of(A + m0 * K);
-  const int4v b_rsrc = rsrc_of(kTransB ? B + n0 * K : B + n0);
+  // Per-item state: buffer resources based at the item's A row panel and B
+  // column panel (32-bit byte offsets per lane and a scalar offset per
+  // instruction and tile; the launcher checks that both panels span less than
+  // 2^31 bytes), its k base and the origin of its output tile.
+  int4v a_rsrc{}, b_rsrc{};
+  int k_base = 0, tile_n0 = 0;
+  float* out_tile = nullptr;
+  auto setup = [&](int it) {
+    const int split = it / per_split;
+    const int tile = it - split * per_split;
+    const int batch = tile / per_batch;
+    const int t = tile - batch * per_batch;
+    constexpr int kGroupM = 8;
+    const int group_tiles = kGroupM * tiles_n;
+    const int first_m = (t / group_tiles) * kGroupM;
+    const int gm = min(tiles_m - first_m, kGroupM);
+    const int tm = first_m + (t % group_tiles) % gm;
+    const int tn = (t % group_tiles) / gm;
+    std::int64_t lhs_off = 0, rhs_off = 0;
+    int b = batch;
+    for (int ax = a.batch_rank - 1; ax >= 0; --ax) {
+      const int e = static_cast<int>(a.batch_shape[ax]);
+      const int c = b % e;
+      b /= e;
+      lhs_off += c * a.lhs_bs[ax];
+      rhs_off += c * a.rhs_bs[ax];
+    }
+    const std::int64_t m0 = static_cast<std::int64_t>(tm) * BM, n0 = static_cast<std::int64_t>(tn) * BN;
+    float* const c_mat = partial ? a.partial + (static_cast<std::int64_t>(split) * (per_split / per_batch) + batch) * M * N
+                                 : a.out + static_cast<std::int64_t>(batch) * M * N;
+    out_tile = c_mat + m0 * N + n0;
+    tile_n0 = tn * BN;
+    k_base = split * k_len;
+    a_rsrc = rsrc_of(a.lhs + lhs_off + m0 * K);
+    b_rsrc = rsrc_of(kTransB ? a.rhs + rhs_off + n0 * K : a.rhs + rhs_off + n0);
+  };
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  auto achunk = [](int row, int kc) { return kc ^ ((row >> 1) & 7); };
+
   // Lane of instruction p writes A row (p * kWaves + wave) * 8 + lane / 8; the
   // chunk swizzle of that row does not depend on p.
   const int a_row = wave * kARows + lane / kChunks;
@@ -491,10 +509,6 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
   const int wm = wave / kWavesN, wn = wave % kWavesN;
   const int r = lane & 15, kl = lane >> 4;
   floatx4 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.F, 0.F, 0.F, 0.F};
 
   // Block i of the wave covers tile rows 16 i + (0..15). B columns keep the
   // frag_pos map for a [k, n] B (16-byte fragment reads and output stores);
@@ -539,56 +553,86 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
   };
 
   const int k_tiles = k_len / BK;
+  setup(item);  // gridDim <= items: every block has a first item
   issue(A0, B0, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  // Pairs of k-tiles: stage 0 is read while stage 1 loads, then the reverse.
-  int kt = 0;
-  for (; kt + 2 <= k_tiles; kt += 2) {
-    issue(A1, B1, (kt + 1) * BK);
-    compute(A0, B0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (kt + 2 < k_tiles) issue(A0, B0, (kt + 2) * BK);
-    compute(A1, B1);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-  }
-  if (kt < k_tiles) compute(A0, B0);  // odd count: the last tile sits in stage 0
+  const std::int64_t col_off = wn * WN;
+  auto col_of = [&](int jj) { return kTransB ? 16 * jj + r : frag_pos<TN>(r, jj); };
+  for (;;) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int jj = 0; jj < TN; ++jj) acc[i][jj] = floatx4{0.F, 0.F, 0.F, 0.F};
+    // Pairs of k-tiles: stage 0 is read while stage 1 loads, then the reverse.
+    int kt = 0;
+    for (; kt + 2 <= k_tiles; kt += 2) {
+      issue(A1, B1, (kt + 1) * BK);
+      compute(A0, B0);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (kt + 2 < k_tiles) issue(A0, B0, (kt + 2) * BK);
+      compute(A1, B1);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+    if (kt < k_tiles) compute(A0, B0);  // odd count: the last tile sits in stage 0
 
-  // Epilogue as in gemm_f32_kernel (full tiles: no bounds checks); a split
-  // block stores its raw partial sums.
-  const std::int64_t col_base = n0 + wn * WN;
-  auto col_of = [&](int j) { return kTransB ? 16 * j + r : frag_pos<TN>(r, j); };
-  const bool epilogue = !partial;
-  float bias[TN];
+    // Epilogue as in gemm_f32_kernel (full tiles: no bounds checks); a split
+    // item stores its raw partial sums. The next item's first k-tile is
+    // issued before the stores, and only those loads are waited for: the
+    // vector memory counter completes in issue order, so vmcnt(stores) leaves
+    // this item's stores draining under the next item's MFMAs.
+    float* const out_c = out_tile + static_cast<std::int64_t>(wm * WM + kl * 4) * N + col_off;
+    const bool epilogue = !partial;
+    const bool with_bias = epilogue && a.bias != nullptr;
+    float bias[TN];
 #pragma unroll
-  for (int j = 0; j < TN; ++j) bias[j] = epilogue && a.bias != nullptr ? a.bias[col_base + col_of(j)] : 0.F;
+    for (int jj = 0; jj < TN; ++jj) bias[jj] = with_bias ? a.bias[tile_n0 + col_off + col_of(jj)] : 0.F;
+    item += item_step;
+    const bool next = kPersist && item < item_end;
+    if (next) {
+      // The bias loads complete here, before the tile loads go out, so that
+      // waiting for them does not wait for those loads.
+      if (with_bias) __builtin_amdgcn_s_waitcnt(0);
+      if (k_tiles % 2 != 0) __syncthreads();  // every wave is done reading stage 0
+      setup(item);
+      issue(A0, B0, 0);
+    }
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
+    for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const std::int64_t row = m0 + wm * WM + 16 * i + kl * 4 + q;
-      float v[TN];
+      for (int q = 0; q < 4; ++q) {
+        const int row = 16 * i + q;  // + wm WM + 4 kl, in out_c
+        float v[TN];
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        float x = acc[i][j][q];
-        if (epilogue) {
-          if (a.bias != nullptr) x = x + bias[j];
-          x = activate(x, a.activation);
+        for (int jj = 0; jj < TN; ++jj) {
+          float x = acc[i][jj][q];
+          if (epilogue) {
+            if (with_bias) x = x + bias[jj];
+            x = activate(x, a.activation);
+          }
+          v[jj] = x;
         }
-        v[j] = x;
-      }
-      float* dst = C + row * N + col_base;
-      if constexpr (kTransB) {
+        float* dst = out_c + row * N;
+        if constexpr (kTransB) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) dst[16 * j + r] = v[j];
-      } else {
+          for (int jj = 0; jj < TN; ++jj) dst[16 * jj + r] = v[jj];
+        } else {
 #pragma unroll
-        for (int g = 0; g < TN / 4; ++g)
-          *reinterpret_cast<float4_t*>(dst + g * 64 + r * 4) = float4_t{v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
+          for (int g = 0; g < TN / 4; ++g)
+            *reinterpret_cast<float4_t*>(dst + g * 64 + r * 4) =
+                float4_t{v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
+        }
       }
     }
+    if (!next) break;
+    // Stores per wave: TM * 4 rows of TN / 4 16-byte stores (TN 4-byte stores
+    // for a transposed B); the count field holds at most 63.
+    constexpr int kStores = kTransB ? TM * 4 * TN : TM * 4 * (TN / 4);
+    constexpr int kVm = kStores < 63 ? kStores : 63;
+    __builtin_amdgcn_s_waitcnt((kVm & 15) | (7 << 4) | (15 << 8) | ((kVm >> 4) << 14));
+    __syncthreads();
   }
 }
 
@@ -637,7 +681,23 @@ int launch_direct(GemmArgs& args, bool trans_b, hipStream_t stream) {
   args.tiles_n = args.n / BN;
   args.total_tiles = args.tiles_m * args.tiles_n * batches * splits;
   if (args.total_tiles > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
-  const dim3 grid(static_cast<unsigned>(args.total_tiles)), block((BM / WM) * (BN / WN) * 64);
+  // [k, n] B with more items than blocks that fit at once: a persistent grid
+  // of that many blocks (batched 32 x 1024^3: 512 items on 256 CUs, two per
+  // block).
+  const int threads = (BM / WM) * (BN / WN) * 64;
+  thread_local int fit = 0;
+  if (fit == 0) {
+    int per_cu = 0, cus = 0, device = 0;
+    (void)hipGetDevice(&device);
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, gemm_f32_direct_kernel<BM, BN, BK, WM, WN, kMinWaves, false>, threads, 0) != hipSuccess ||
+        per_cu < 1)
+      per_cu = 1;
+    fit = per_cu * (cus > 0 ? cus : 256);
+  }
+  const std::int64_t blocks = !trans_b && args.total_tiles > fit ? fit : args.total_tiles;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(threads);
   if (trans_b)
     hipLaunchKernelGGL((gemm_f32_direct_kernel<BM, BN, BK, WM, WN, kMinWaves, true>), grid, block, 0, stream, args);
   else

@@ -187,6 +187,55 @@ def test_matmul_full_tiles(cx, sa, sb):
     assert_matmul(actual, np.matmul(a.astype(np.float64), b.astype(np.float64)), a, b, f"{sa}@{sb}")
 
 
+@pytest.mark.parametrize("sa,sb", [((32, 1024, 1024), (32, 1024, 1024)), ((65, 512, 96), (65, 96, 512)),
+                                   ((72, 512, 96), (96, 512)), ((600, 256, 64), (600, 64, 256)),
+                                   ((34, 512, 1024), (34, 1024, 512))])
+def test_matmul_persistent_tiles(cx, sa, sb):
+    """More full 256x256 items than blocks that fit at once: the direct kernel
+    runs a persistent grid, each block taking several items and issuing the
+    next item's loads before its stores. The bench's batched config (two items
+    per block), an item count that is not a multiple of 8 (plain order) with
+    an odd k-tile count, the XCD order with an odd k-tile count and a
+    broadcast B, up to three items per block, and K split over two items per
+    output tile (136 tiles, 272 items). Checked against float64 products."""
+    rng = np.random.default_rng(19)
+    a = rng.standard_normal(sa).astype(np.float32)
+    b = rng.standard_normal(sb).astype(np.float32)
+    actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    assert_matmul(actual, np.matmul(a.astype(np.float64), b.astype(np.float64)), a, b, f"{sa}@{sb}")
+
+
+def test_matmul_persistent_tiles_dyadic_exact(cx):
+    # Exact in any order: pins the item -> tile map of the persistent grid bit
+    # for bit (260 items, plain order, three k-tiles).
+    i = np.arange(65 * 512 * 96)
+    a = ((i % 13 - 6) / 8).astype(np.float32).reshape(65, 512, 96)
+    j = np.arange(65 * 96 * 512)
+    b = ((j % 9 - 4) / 16).astype(np.float32).reshape(65, 96, 512)
+    actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    assert_bits(actual, np.matmul(a.astype(np.float64), b.astype(np.float64)).astype(np.float32),
+                "dyadic persistent")
+
+
+def test_gemm_persistent_bias_activation(cx):
+    # The C ABI with a [k, n] B, bias and SiLU over 512 full tiles: the
+    # persistent kernel's bias path (bias loads before the next item's tile
+    # loads), against float64 truth at the matmul bar.
+    import tensorcx_hip_capi as capi
+    rng = np.random.default_rng(20)
+    x = rng.standard_normal((8192, 64)).astype(np.float32)
+    w = rng.standard_normal((64, 4096)).astype(np.float32)
+    bias = rng.standard_normal(4096).astype(np.float32)
+    dx, dw, db = (capi.DeviceArray.from_numpy(t) for t in (x, w, bias))
+    out = capi.DeviceArray((8192, 4096))
+    capi.gemm(dx.ptr, dw.ptr, out.ptr, capi.gemm_desc(8192, 4096, 64, bias=db.ptr, activation="silu"))
+    capi.synchronize()
+    pre = x.astype(np.float64) @ w.astype(np.float64) + bias
+    truth = pre / (1 + np.exp(-pre))
+    scale = 1e-4 * np.sqrt(64) * np.sqrt(np.mean(x.astype(np.float64) ** 2) * np.mean(w.astype(np.float64) ** 2))
+    assert np.max(np.abs(out.numpy() - truth)) <= scale
+
+
 def test_matmul_dyadic_full_tiles_exact(cx):
     # Exact in any order: pins the k permutation, swizzles and tile placement
     # of the direct-to-LDS kernel bit for bit.
