@@ -2,8 +2,8 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only NAME]
 
-Headline (the JSON `value`): fp32 matmul TFLOP/s at 4096^3 (BASELINE config
-C2), inputs resident in HBM, K timed GEMM launches bracketed by stream
+Headline (the JSON `value`): fp32 matmul TFLOP/s at 4096^3 (config C2, the
+second entry of BASELINE.json's configs), inputs resident in HBM, K timed GEMM launches bracketed by stream
 synchronisation, timed with HIP events on the launch stream. The same JSON line
 carries `roofline` for that kernel, `cpu_baseline` (the reference CPU matmul,
 single thread, on a bounded row slab), and `secondary`: the other configs'

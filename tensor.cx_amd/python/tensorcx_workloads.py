@@ -1,4 +1,5 @@
-"""The synthetic workloads of the hip hot path (the five BASELINE configs).
+"""The synthetic workloads of the hip hot path: the five entries of
+BASELINE.json's configs, C1-C5 in order.
 
 Inputs follow the reference idiom (python/tensorcx/tensor.py:496): NumPy
 default_rng(seed) (PCG64), float64 draws cast to float32, operands drawn from
