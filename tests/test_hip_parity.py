@@ -408,6 +408,45 @@ def test_row_ops_random(cx, shape, axis):
                  oracle.affine_norm(x, axis, 1e-5, g, None, rms=True), 1e-5, 1e-5, "affine rmsnorm")
 
 
+@pytest.mark.parametrize("width", [200, 500, 1024, 2048, 3001, 4096, 8192, 16384, 20003, 70000])
+def test_row_ops_special_values_wide_rows(cx, width):
+    # Non-finite values in rows of every width class (one-wave cached rows,
+    # split rows at 2, 4, 8 and 16 float4 per thread, unaligned scalar rows,
+    # block-per-row re-read rows): a NaN, +inf last, -inf first, a row of
+    # -inf, +inf with -inf, and a row whose squares overflow to inf.
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal((7, width)).astype(np.float32)
+    x[0, width // 2] = np.nan
+    x[1, width - 1] = np.inf
+    x[2, 0] = -np.inf
+    x[3] = -np.inf
+    x[4, 1], x[4, width - 2] = np.inf, -np.inf
+    x[5] *= np.float32(1e20)
+    g = rng.uniform(0.5, 1.5, size=width).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, size=width).astype(np.float32)
+    h, gh, bh = (cx.tensor(t, device="hip") for t in (x, g, b))
+    with np.errstate(all="ignore"):
+        assert_close(cx.softmax(h, 1).numpy(), oracle.softmax(x, 1), 1e-5, 1e-5, "softmax")
+        assert_close(cx.rmsnorm(h, 1).numpy(), oracle.rmsnorm(x, 1), 1e-5, 1e-5, "rmsnorm")
+        assert_close(cx.layernorm(h, 1).numpy(), oracle.layernorm(x, 1), 1e-5, 1e-5, "layernorm")
+        assert_close(cx.layernorm(h, 1, weight=gh, bias=bh).numpy(), oracle.affine_norm(x, 1, 1e-5, g, b),
+                     1e-5, 1e-5, "affine layernorm")
+        assert_close(cx.rmsnorm(h, 1, weight=gh).numpy(), oracle.affine_norm(x, 1, 1e-5, g, None, rms=True),
+                     1e-5, 1e-5, "affine rmsnorm")
+        # The same rows through the reductions: extrema bit-exact; sums carry
+        # NaN / inf as in any order (no finite overflow), the rest at the bar.
+        for op in ("max", "min", "argmax"):
+            assert_bits(getattr(cx, op)(h, 1).numpy(), getattr(oracle, op)(x, 1), f"{op} special {width}")
+        for op in ("sum", "mean"):
+            actual, expected = getattr(cx, op)(h, 1).numpy(), getattr(oracle, op)(x, 1)
+            assert np.array_equal(np.isinf(actual), np.isinf(expected)), op
+            assert np.array_equal(np.sign(actual[np.isinf(expected)]), np.sign(expected[np.isinf(expected)])), op
+            assert np.array_equal(np.isnan(actual), np.isnan(expected)), op
+            fin = np.isfinite(expected)
+            scale = width if op == "mean" else 1
+            assert sum_error(actual[fin] * scale, expected[fin] * scale, x[fin], int(fin.sum()), width, 1) <= 1e-5, op
+
+
 @pytest.mark.parametrize("eps", [0.0, 1e-45, 1e-5, 1e30])
 @pytest.mark.parametrize("width", [512, 4096, 3001])
 def test_constant_rows(cx, eps, width):
