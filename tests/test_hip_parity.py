@@ -486,6 +486,28 @@ def test_unary_and_bias_act(cx):
         assert_close(fused, getattr(oracle, act)(oracle.binary("add", y, b)), 1e-6, 1e-6, act)
 
 
+@pytest.mark.parametrize("rows,cols", [(3, 5), (7, 1001), (2048, 2052), (4096, 4096)])
+def test_bias_act_special_values(cx, rows, cols):
+    # The fused bias + activation kernel (float4 path for 4-aligned rows,
+    # scalar path otherwise, grid-stride loops at the largest size) with
+    # non-finite and overflowing inputs in both operands, against the
+    # reference's add-then-activation.
+    rng = np.random.default_rng(29)
+    y = rng.standard_normal((rows, cols)).astype(np.float32) * 4
+    b = rng.standard_normal(cols).astype(np.float32)
+    specials = np.array([np.nan, np.inf, -np.inf, 100., -100., 1e30, -1e30, 0., -0., 1e-38], np.float32)
+    flat = y.reshape(-1)
+    idx = rng.choice(flat.size, size=min(flat.size, 4 * specials.size), replace=False)
+    flat[idx] = np.resize(specials, idx.size)
+    b[rng.choice(cols, size=min(cols, 3), replace=False)] = np.array([np.inf, -np.inf, np.nan], np.float32)[:min(cols, 3)]
+    yh, bh = cx.tensor(y, device="hip"), cx.tensor(b, device="hip")
+    with np.errstate(all="ignore"):
+        pre = oracle.binary("add", y, b)
+        for act in ("silu", "gelu"):
+            fused = cx.hip.bias_act(yh, bh, act).numpy()
+            assert_close(fused, getattr(oracle, act)(pre), 1e-6, 1e-6, f"{act} {rows}x{cols}")
+
+
 @pytest.mark.parametrize("shape", [(5, 48), (2, 3, 48), (48,), (257, 130)])
 def test_linear(cx, shape):
     rng = np.random.default_rng(4)
