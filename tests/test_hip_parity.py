@@ -205,6 +205,33 @@ def test_matmul_persistent_tiles(cx, sa, sb):
     assert_matmul(actual, np.matmul(a.astype(np.float64), b.astype(np.float64)), a, b, f"{sa}@{sb}")
 
 
+@pytest.mark.parametrize("n,linear", [(2048, False), (4096, False), (2048, True)])
+def test_matmul_full_tiles_special_values(cx, n, linear):
+    # Non-finite values through the 256x256 direct kernel: one item per block
+    # (2048 columns), the persistent grid (4096 columns, two items per block)
+    # and the transposed-B linear. A +inf, a -inf and a NaN in rows of A and a
+    # +inf in a column of B: NaN / inf positions and signs as float64 truth,
+    # the finite rest at the matmul bar.
+    rng = np.random.default_rng(31)
+    a = rng.standard_normal((8192, 64)).astype(np.float32)
+    b = rng.standard_normal((64, n)).astype(np.float32)
+    a[5, 3], a[300, 10], a[4000, 63] = np.inf, -np.inf, np.nan
+    b[7, n - 1] = np.inf
+    ah = cx.tensor(a, device="hip")
+    if linear:
+        actual = cx.linear(ah, cx.tensor(np.ascontiguousarray(b.T), device="hip")).numpy()
+    else:
+        actual = cx.matmul(ah, cx.tensor(b, device="hip")).numpy()
+    with np.errstate(invalid="ignore", over="ignore"):
+        truth = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.array_equal(np.isnan(actual), np.isnan(truth))
+    assert np.array_equal(np.isinf(actual), np.isinf(truth))
+    inf = np.isinf(truth)
+    assert np.array_equal(np.sign(actual[inf]), np.sign(truth[inf]))
+    rows = np.setdiff1d(np.arange(8192), [5, 300, 4000])
+    assert_matmul(actual[rows][:, :n - 1], truth[rows][:, :n - 1], a[rows], b[:, :n - 1], "special full tiles")
+
+
 def test_matmul_persistent_tiles_dyadic_exact(cx):
     # Exact in any order: pins the item -> tile map of the persistent grid bit
     # for bit (260 items, plain order, three k-tiles).
