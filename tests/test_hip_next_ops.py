@@ -405,8 +405,9 @@ def test_fused_attention_causal_value_scan(cx, d):
         attention_check(cx, q, k, v, None, True)
 
 
-def test_fused_attention_special_values(cx):
-    q, k, v = f32((1, 70, 64), 4), f32((1, 90, 64), 5), f32((1, 90, 64), 6)
+@pytest.mark.parametrize("d", [32, 64, 128])
+def test_fused_attention_special_values(cx, d):
+    q, k, v = f32((1, 70, d), 4), f32((1, 90, d), 5), f32((1, 90, d), 6)
     q[0, 3, 7] = np.nan            # a NaN query: its row is NaN
     k[0, 11] = np.inf              # an infinite key: +inf / NaN scores
     k[0, 12] = -np.inf
@@ -415,7 +416,7 @@ def test_fused_attention_special_values(cx):
         for causal in (False, True):
             attention_check(cx, q, k, v, None, causal)
     # All scores -inf for one query: 0 * V.
-    q2, k2, v2 = np.ones((1, 2, 32), np.float32), np.ones((1, 3, 32), np.float32), f32((1, 3, 32), 7)
+    q2, k2, v2 = np.ones((1, 2, d), np.float32), np.ones((1, 3, d), np.float32), f32((1, 3, d), 7)
     q2[0, 1] = -np.inf
     k2[0, :, :] = 1.0
     with np.errstate(all="ignore"):
