@@ -33,14 +33,28 @@ using gemm::launch_config;
 
 bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15U) == 0; }
 
+// Transposed B (linear's W [n, k]) with fewer than one round of full
+// 256x256 tiles but >= 256 full 128x128 ones: the direct kernel on 128x128
+// tiles of eight 64x32 waves over the whole K (64 KB of LDS), no split and no
+// reduction pass. Measured against the K split it replaces: 4096x1024x4096
+// (the MLP's second linear) 265.0 -> 249.6 us, 4096x2048x2048 270.2 -> 245.6,
+// 2048x2048x2048 154.1 -> 136.0.
+bool direct128_trans(const tcx_hip_gemm_desc_t* d, std::int64_t batches) {
+  if (d->rhs_transposed == 0 || !gemm::direct_fits<128, 128, 32>(d->m, d->n, d->k)) return false;
+  const std::int64_t tiles_256 = ((d->m + 255) / 256) * ((d->n + 255) / 256) * batches;
+  return tiles_256 < 256 && (d->m / 128) * (d->n / 128) * batches >= 256;
+}
+
 // K split of the direct 256x256 kernel for shapes with fewer than 256 full
 // output tiles and a long K: the smallest power of two that gives >= 256
 // blocks (at most 16), when every split keeps >= 512 of K in whole k-tiles.
 // Measured against the tile the shape would take otherwise: 4096x1024x4096
-// with a transposed B (the MLP's second linear) 295 -> 270 us at 4 splits,
-// 2048x2048x4096 279 -> 270 us, 1024x1024x8192 546 -> 261 us at 8. 1 = none.
+// with a transposed B 295 -> 270 us at 4 splits (that shape now takes the
+// 128x128 tiles above), 2048x2048x4096 279 -> 270 us, 1024x1024x8192
+// 546 -> 261 us at 8. 1 = none.
 std::int64_t gemm_splits(const tcx_hip_gemm_desc_t* d, std::int64_t batches) {
   if (!gemm::direct_fits<256, 256, 32>(d->m, d->n, d->k) || d->n % 4 != 0) return 1;
+  if (direct128_trans(d, batches)) return 1;
   const std::int64_t tiles = (d->m / 256) * (d->n / 256) * batches;
   std::int64_t splits = 1;
   while (tiles * splits < 256 && splits < 16) splits *= 2;
@@ -136,6 +150,7 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
   // 4096x4096x1024: 305 us -> 290 us).
   if (vec && tiles_256 >= 256 && gemm::direct_fits<256, 256, 32>(d->m, d->n, d->k))
     return gemm::launch_direct<256, 256, 32, 64, 128, 2>(args, trans_b, s);
+  if (vec && direct128_trans(d, batches)) return gemm::launch_direct<128, 128, 32, 64, 32, 2>(args, true, s);
   // Fewer full 256x256 tiles and a long K: split K over several blocks when
   // the caller brought the workspace (tcx_hip_gemm_workspace_bytes).
   if (vec && workspace != nullptr && aligned16(workspace)) {

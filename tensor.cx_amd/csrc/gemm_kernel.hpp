@@ -379,7 +379,10 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
   constexpr int TM = WM / 16, TN = WN / 16;
   constexpr int LDB = BN + 8;
   constexpr int kChunks = BK / 4;
-  static_assert(kChunks == 8 && BN == 256 && TN % 4 == 0, "one wave instruction = 8 rows of A or one row of B");
+  // A [k, n] B takes one 256-float row per wave instruction and 16-byte
+  // output stores; a transposed B is loaded like A (8 rows per instruction).
+  static_assert(kChunks == 8 && (kTransB || (BN == 256 && TN % 4 == 0)),
+                "one wave instruction = 8 rows of A or one row of B");
   constexpr int kARows = 64 / kChunks;          // A rows per wave instruction
   constexpr int kAInst = BM / kARows / kWaves;  // A instructions per wave and tile
   // B instructions per wave and tile: one k-row each ([k, n] B), or 8
@@ -681,27 +684,36 @@ int launch_direct(GemmArgs& args, bool trans_b, hipStream_t stream) {
   args.tiles_n = args.n / BN;
   args.total_tiles = args.tiles_m * args.tiles_n * batches * splits;
   if (args.total_tiles > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
-  // [k, n] B with more items than blocks that fit at once: a persistent grid
-  // of that many blocks (batched 32 x 1024^3: 512 items on 256 CUs, two per
-  // block).
   const int threads = (BM / WM) * (BN / WN) * 64;
-  thread_local int fit = 0;
-  if (fit == 0) {
-    int per_cu = 0, cus = 0, device = 0;
-    (void)hipGetDevice(&device);
-    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, gemm_f32_direct_kernel<BM, BN, BK, WM, WN, kMinWaves, false>, threads, 0) != hipSuccess ||
-        per_cu < 1)
-      per_cu = 1;
-    fit = per_cu * (cus > 0 ? cus : 256);
+  std::int64_t blocks = args.total_tiles;
+  if constexpr (BN == 256) {
+    // [k, n] B with more items than blocks that fit at once: a persistent
+    // grid of that many blocks (batched 32 x 1024^3: 512 items on 256 CUs,
+    // two per block).
+    thread_local int fit = 0;
+    if (fit == 0) {
+      int per_cu = 0, cus = 0, device = 0;
+      (void)hipGetDevice(&device);
+      (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+              &per_cu, gemm_f32_direct_kernel<BM, BN, BK, WM, WN, kMinWaves, false>, threads, 0) != hipSuccess ||
+          per_cu < 1)
+        per_cu = 1;
+      fit = per_cu * (cus > 0 ? cus : 256);
+    }
+    if (!trans_b && blocks > fit) blocks = fit;
   }
-  const std::int64_t blocks = !trans_b && args.total_tiles > fit ? fit : args.total_tiles;
   const dim3 grid(static_cast<unsigned>(blocks)), block(threads);
-  if (trans_b)
+  if constexpr (BN == 256) {
+    if (trans_b)
+      hipLaunchKernelGGL((gemm_f32_direct_kernel<BM, BN, BK, WM, WN, kMinWaves, true>), grid, block, 0, stream, args);
+    else
+      hipLaunchKernelGGL((gemm_f32_direct_kernel<BM, BN, BK, WM, WN, kMinWaves, false>), grid, block, 0, stream, args);
+  } else {
+    // Narrower tiles exist for a transposed B only.
+    if (!trans_b) return fail(TCX_INTERNAL, "direct gemm with a [k, n] B needs 256-wide tiles");
     hipLaunchKernelGGL((gemm_f32_direct_kernel<BM, BN, BK, WM, WN, kMinWaves, true>), grid, block, 0, stream, args);
-  else
-    hipLaunchKernelGGL((gemm_f32_direct_kernel<BM, BN, BK, WM, WN, kMinWaves, false>), grid, block, 0, stream, args);
+  }
   int rc = check(hipGetLastError(), "gemm_f32 direct launch");
   if (rc != TCX_OK || splits == 1) return rc;
   const std::int64_t count4 = batches * args.m * args.n / 4;

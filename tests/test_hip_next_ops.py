@@ -345,6 +345,15 @@ def test_attention_masked_full_tiles(cx):
     attention_check(cx, q, k, v, mask)
 
 
+def test_attention_masked_direct128_scores(cx):
+    # 8 x 1024 x 1024 scores over K = 64: 512 full 128x128 tiles but only 128
+    # of 256x256, so the batched score product (B transposed) takes the
+    # direct 128x128 kernel.
+    q, k, v = f32((8, 1024, 64), 25), f32((8, 1024, 64), 26), f32((8, 1024, 64), 27)
+    mask = np.random.default_rng(28).random((1024, 1024)) > .2
+    attention_check(cx, q, k, v, mask)
+
+
 # ------------------------------------------------------------- fused attention
 @pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("rows,cols", [(1, 1), (64, 64), (65, 130), (200, 37), (5, 0), (3, 257), (300, 1000)])

@@ -552,6 +552,46 @@ def test_linear(cx, shape):
         np.sqrt(np.mean(w * w)) + 1e-6
 
 
+@pytest.mark.parametrize("xs,ws", [((4096, 4096), (1024, 4096)), ((4, 1024, 256), (1024, 256)),
+                                   ((2048, 2048), (2048, 2048))])
+def test_linear_direct128(cx, xs, ws):
+    # Linear layers with fewer than one round of 256x256 tiles but >= 256
+    # full 128x128 ones (the MLP's second linear, a batched input, a square
+    # 2048 layer) take the direct 128x128 kernel over the whole K, with bias.
+    rng = np.random.default_rng(33)
+    x = rng.standard_normal(xs).astype(np.float32)
+    w = rng.standard_normal(ws).astype(np.float32)
+    b = rng.standard_normal(ws[0]).astype(np.float32)
+    got = cx.linear(cx.tensor(x, device="hip"), cx.tensor(w, device="hip"), cx.tensor(b, device="hip")).numpy()
+    truth = x.astype(np.float64) @ w.astype(np.float64).T + b
+    x2 = x.reshape(-1, xs[-1])
+    assert_matmul(got.reshape(-1, ws[0]) - b, truth.reshape(-1, ws[0]) - b, x2, w.T, f"linear {xs}x{ws}")
+
+
+def test_linear_direct128_dyadic_exact_and_special(cx):
+    # 16 x 16 tiles of 128x128 over K = 96 (three k-tiles): exact in any
+    # order with dyadic inputs (pins the tile map and the fragment layout bit
+    # for bit), then non-finite values in x rows and a W row.
+    i = np.arange(2048 * 96)
+    x = ((i % 13 - 6) / 8).astype(np.float32).reshape(2048, 96)
+    j = np.arange(2048 * 96)
+    w = ((j % 11 - 5) / 16).astype(np.float32).reshape(2048, 96)
+    b = ((np.arange(2048) % 7 - 3) / 4).astype(np.float32)
+    xh, wh, bh = (cx.tensor(t, device="hip") for t in (x, w, b))
+    exact = (x.astype(np.float64) @ w.astype(np.float64).T + b).astype(np.float32)
+    assert_bits(cx.linear(xh, wh, bh).numpy(), exact, "dyadic direct128")
+    x[5, 3], x[700, 10], x[1500, 95] = np.inf, -np.inf, np.nan
+    w[2047, 40] = np.inf
+    got = cx.linear(cx.tensor(x, device="hip"), cx.tensor(w, device="hip"), bh).numpy()
+    with np.errstate(invalid="ignore", over="ignore"):
+        truth = x.astype(np.float64) @ w.astype(np.float64).T + b
+    assert np.array_equal(np.isnan(got), np.isnan(truth))
+    assert np.array_equal(np.isinf(got), np.isinf(truth))
+    assert np.array_equal(np.sign(got[np.isinf(truth)]), np.sign(truth[np.isinf(truth)]))
+    fin = np.isfinite(truth)
+    assert np.array_equal(got[fin], truth[fin].astype(np.float32))
+
+
 def test_linear_full_tiles(cx):
     # 4096 x 4096 outputs: the transposed-B direct-to-LDS kernel, with the bias
     # and SiLU epilogue; checked against float64.
