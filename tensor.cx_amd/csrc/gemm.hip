@@ -33,16 +33,16 @@ using gemm::launch_config;
 
 bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15U) == 0; }
 
-// Transposed B (linear's W [n, k]) with fewer than one round of full
-// 256x256 tiles but >= 256 full 128x128 ones: the direct kernel on 128x128
-// tiles of eight 64x32 waves over the whole K (64 KB of LDS), no split and no
-// reduction pass. Measured against the K split it replaces: 4096x1024x4096
-// (the MLP's second linear) 265.0 -> 249.6 us, 4096x2048x2048 270.2 -> 245.6,
-// 2048x2048x2048 154.1 -> 136.0.
-bool direct128_trans(const tcx_hip_gemm_desc_t* d, std::int64_t batches) {
-  if (d->rhs_transposed == 0 || !gemm::direct_fits<128, 128, 32>(d->m, d->n, d->k)) return false;
-  const std::int64_t tiles_256 = ((d->m + 255) / 256) * ((d->n + 255) / 256) * batches;
-  return tiles_256 < 256 && (d->m / 128) * (d->n / 128) * batches >= 256;
+// Shapes of >= 256 full 128x128 tiles: the direct kernel on 128x128 tiles of
+// eight waves (64x32 for a transposed B, 32x64 for a [k, n] B; 64-68 KB of
+// LDS and 79-84 registers, so two blocks share a CU), persistent past the
+// blocks that fit. Against the 256x256 direct tiles (one block per CU):
+// 4096^3 940.0 -> 931.3 us, batched 32x1024^3 495.9 -> 482.8,
+// 4096x4096x1024 250.6 -> 243.3 (transposed 258.8 -> 253.5), 8192x8192x1024
+// 979.5 -> 959.7; against the K split: 4096x1024x4096 260.2 -> 243.7
+// (transposed 265.0 -> 249.6), 2048^3 145.6 -> 125.8.
+bool direct128_fits(const tcx_hip_gemm_desc_t* d, std::int64_t batches) {
+  return gemm::direct_fits<128, 128, 32>(d->m, d->n, d->k) && (d->m / 128) * (d->n / 128) * batches >= 256;
 }
 
 // K split of the direct 256x256 kernel for shapes with fewer than 256 full
@@ -54,7 +54,7 @@ bool direct128_trans(const tcx_hip_gemm_desc_t* d, std::int64_t batches) {
 // 546 -> 261 us at 8. 1 = none.
 std::int64_t gemm_splits(const tcx_hip_gemm_desc_t* d, std::int64_t batches) {
   if (!gemm::direct_fits<256, 256, 32>(d->m, d->n, d->k) || d->n % 4 != 0) return 1;
-  if (direct128_trans(d, batches)) return 1;
+  if (direct128_fits(d, batches)) return 1;
   const std::int64_t tiles = (d->m / 256) * (d->n / 256) * batches;
   std::int64_t splits = 1;
   while (tiles * splits < 256 && splits < 16) splits *= 2;
@@ -132,27 +132,30 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
   const bool trans_b = d->rhs_transposed != 0;
   args.total_tiles = batches;
   const auto s = static_cast<hipStream_t>(stream);
-  // Tile choice (swept on MI355X over the config shapes): 256x256 blocks of
-  // eight 64x128 waves, 32-wide k-tiles (133 KB of LDS, 2 waves/SIMD) when
-  // there are >= 256 of them (one full round on 256 CUs). Fewer output tiles
-  // leave the CUs short of waves, so the smaller tiles split K inside the
-  // block: 128x128 blocks of two groups of eight 32x64 waves (4 waves/SIMD)
-  // when there are enough of those (below), else 64x64 blocks of four groups
-  // of four 32x32 waves when there are >= 128 of those (1000^3), else 32x32
-  // blocks of eight one-wave groups with 32-wide k-tiles (small shapes; 512^3:
-  // 17.9 -> 11.8 us). The measured gains were 7% on the MLP's 4096x1024x4096
-  // GEMM and 21% on 1000^3 over the same tiles without the split.
+  // Tile choice (swept on MI355X over the config shapes): full 128x128 tiles
+  // on the direct-to-LDS kernel when there are >= 256 of them; else, with a
+  // workspace and a long K, the direct 256x256 kernel split over K. Partial
+  // tiles take the register-staged kernels: 256x256 blocks of eight 64x128
+  // waves (133 KB of LDS, 2 waves/SIMD) for >= 256 tiles, then, as fewer
+  // output tiles leave the CUs short of waves, smaller tiles that split K
+  // inside the block: 128x128 blocks of two groups of eight 32x64 waves
+  // (4 waves/SIMD) when there are enough of those (below), else 64x64 blocks
+  // of four groups of four 32x32 waves when there are >= 128 of those
+  // (1000^3), else 32x32 blocks of eight one-wave groups with 32-wide k-tiles
+  // (small shapes; 512^3: 17.9 -> 11.8 us). The in-block split gained 7 % on
+  // 4096x1024x4096 and 21 % on 1000^3 over the same tiles without it.
   const std::int64_t tiles_256 = ((d->m + 255) / 256) * ((d->n + 255) / 256) * batches;
   // (Unaligned shapes take the scalar-load variant, which does not fit the
   // 256x256 tile's registers; they use the 128x128 tile.)
-  // Full 256x256 tiles: the direct-to-LDS variant (4096^3: 1.03 ms ->
-  // 0.96 ms, batched 32x1024^3: 0.55-0.59 ms -> 0.51 ms, transposed B at
-  // 4096x4096x1024: 305 us -> 290 us).
-  if (vec && tiles_256 >= 256 && gemm::direct_fits<256, 256, 32>(d->m, d->n, d->k))
-    return gemm::launch_direct<256, 256, 32, 64, 128, 2>(args, trans_b, s);
-  if (vec && direct128_trans(d, batches)) return gemm::launch_direct<128, 128, 32, 64, 32, 2>(args, true, s);
-  // Fewer full 256x256 tiles and a long K: split K over several blocks when
-  // the caller brought the workspace (tcx_hip_gemm_workspace_bytes).
+  // Full 128x128 tiles, >= 256 of them: the direct-to-LDS kernel (see
+  // direct128_fits).
+  if (vec && direct128_fits(d, batches)) {
+    if (trans_b) return gemm::launch_direct<128, 128, 32, 64, 32, 2>(args, true, s);
+    return gemm::launch_direct<128, 128, 32, 32, 64, 2>(args, false, s);
+  }
+  // Fewer full tiles and a long K: split K over several blocks of the direct
+  // 256x256 kernel when the caller brought the workspace
+  // (tcx_hip_gemm_workspace_bytes).
   if (vec && workspace != nullptr && aligned16(workspace)) {
     const std::int64_t splits = gemm_splits(d, batches);
     const size_t need = static_cast<size_t>(splits * batches * d->m * d->n) * sizeof(float);

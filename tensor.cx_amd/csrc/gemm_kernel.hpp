@@ -379,9 +379,10 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
   constexpr int TM = WM / 16, TN = WN / 16;
   constexpr int LDB = BN + 8;
   constexpr int kChunks = BK / 4;
-  // A [k, n] B takes one 256-float row per wave instruction and 16-byte
-  // output stores; a transposed B is loaded like A (8 rows per instruction).
-  static_assert(kChunks == 8 && (kTransB || (BN == 256 && TN % 4 == 0)),
+  // A [k, n] B takes one k row per wave instruction (all 64 lanes for 256
+  // floats, the first 32 for 128) and 16-byte output stores; a transposed B
+  // is loaded like A (8 rows per instruction).
+  static_assert(kChunks == 8 && (kTransB || ((BN == 256 || BN == 128) && TN % 4 == 0)),
                 "one wave instruction = 8 rows of A or one row of B");
   constexpr int kARows = 64 / kChunks;          // A rows per wave instruction
   constexpr int kAInst = BM / kARows / kWaves;  // A instructions per wave and tile
@@ -502,9 +503,12 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
     } else {
       const unsigned b_lds = lds_of(&Bs[0][0]) + static_cast<unsigned>(wave * LDB * 4);
 #pragma unroll
-      for (int p = 0; p < kBInst; ++p)
-        dma16(b_rsrc, b_lds + p * kWaves * LDB * 4, b_voff,
-              __builtin_amdgcn_readfirstlane((p * kWaves + k0) * static_cast<int>(N) * 4));
+      for (int p = 0; p < kBInst; ++p) {
+        const int soff = __builtin_amdgcn_readfirstlane((p * kWaves + k0) * static_cast<int>(N) * 4);
+        // Lanes past the row stay off: the DMA writes LDS at M0 + 16 * lane,
+        // which for them would be the next (padded) row.
+        if (BN == 256 || lane < BN / 4) dma16(b_rsrc, b_lds + p * kWaves * LDB * 4, b_voff, soff);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -686,7 +690,9 @@ int launch_direct(GemmArgs& args, bool trans_b, hipStream_t stream) {
   if (args.total_tiles > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
   const int threads = (BM / WM) * (BN / WN) * 64;
   std::int64_t blocks = args.total_tiles;
-  if constexpr (BN == 256) {
+  // A [k, n] B needs 256- or 128-wide tiles of 4-column fragments.
+  constexpr bool kKnB = (BN == 256 || BN == 128) && (WN / 16) % 4 == 0;
+  if constexpr (kKnB) {
     // [k, n] B with more items than blocks that fit at once: a persistent
     // grid of that many blocks (batched 32 x 1024^3: 512 items on 256 CUs,
     // two per block).
@@ -704,14 +710,13 @@ int launch_direct(GemmArgs& args, bool trans_b, hipStream_t stream) {
     if (!trans_b && blocks > fit) blocks = fit;
   }
   const dim3 grid(static_cast<unsigned>(blocks)), block(threads);
-  if constexpr (BN == 256) {
+  if constexpr (kKnB) {
     if (trans_b)
       hipLaunchKernelGGL((gemm_f32_direct_kernel<BM, BN, BK, WM, WN, kMinWaves, true>), grid, block, 0, stream, args);
     else
       hipLaunchKernelGGL((gemm_f32_direct_kernel<BM, BN, BK, WM, WN, kMinWaves, false>), grid, block, 0, stream, args);
   } else {
-    // Narrower tiles exist for a transposed B only.
-    if (!trans_b) return fail(TCX_INTERNAL, "direct gemm with a [k, n] B needs 256-wide tiles");
+    if (!trans_b) return fail(TCX_INTERNAL, "this direct gemm tile takes a transposed B only");
     hipLaunchKernelGGL((gemm_f32_direct_kernel<BM, BN, BK, WM, WN, kMinWaves, true>), grid, block, 0, stream, args);
   }
   int rc = check(hipGetLastError(), "gemm_f32 direct launch");

@@ -48,9 +48,9 @@ def test_library_exports_every_declared_symbol():
 
 
 @pytest.mark.parametrize("m,n,k,batch,trans,expect", [
-    (4096, 1024, 4096, (), True, 0),                      # the MLP's second linear: 128x128 tiles
-    (4096, 1024, 4096, (), False, 4 * 4096 * 1024 * 4),  # the same with a [k, n] B: 4 splits
-    (2048, 1024, 4096, (), True, 8 * 2048 * 1024 * 4),   # 128 tiles of 128x128: 8 splits
+    (4096, 1024, 4096, (), True, 0),                      # the MLP's second linear: 256 128x128 tiles
+    (4096, 1024, 4096, (), False, 0),                     # the same with a [k, n] B
+    (2048, 1024, 4096, (), True, 8 * 2048 * 1024 * 4),   # 128 tiles of 128x128: 8 splits of 256x256
     (1024, 1024, 8192, (), False, 16 * 1024 * 1024 * 4),  # 16 tiles: 16 splits of 512
     (512, 512, 8192, (4,), False, 16 * 4 * 512 * 512 * 4),  # batched: 16 tiles
     (4096, 4096, 4096, (), False, 0),                     # 256 tiles already

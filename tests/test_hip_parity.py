@@ -177,8 +177,8 @@ def test_matmul_dyadic_is_exact(cx):
 @pytest.mark.parametrize("sa,sb", [((4096, 32), (32, 4096)), ((4096, 96), (96, 4096)),
                                    ((8, 1024, 512), (512, 2048)), ((2, 1, 2048, 256), (1, 4, 256, 2048))])
 def test_matmul_full_tiles(cx, sa, sb):
-    """Shapes of >= 256 full 256x256 tiles take the direct-to-LDS kernel: one
-    k-tile, an odd tile count, a broadcast batch on either side. Checked
+    """Shapes of >= 256 full 128x128 tiles take the direct-to-LDS kernel: one
+    k-tile, an odd k-tile count, a broadcast batch on either side. Checked
     against float64 products under the matmul bar."""
     rng = np.random.default_rng(17)
     a = rng.standard_normal(sa).astype(np.float32)
@@ -187,17 +187,18 @@ def test_matmul_full_tiles(cx, sa, sb):
     assert_matmul(actual, np.matmul(a.astype(np.float64), b.astype(np.float64)), a, b, f"{sa}@{sb}")
 
 
-@pytest.mark.parametrize("sa,sb", [((32, 1024, 1024), (32, 1024, 1024)), ((65, 512, 96), (65, 96, 512)),
-                                   ((72, 512, 96), (96, 512)), ((600, 256, 64), (600, 64, 256)),
-                                   ((34, 512, 1024), (34, 1024, 512))])
+@pytest.mark.parametrize("sa,sb", [((32, 1024, 1024), (32, 1024, 1024)), ((65, 384, 96), (65, 96, 384)),
+                                   ((72, 512, 96), (96, 512)), ((600, 256, 128), (600, 128, 256)),
+                                   ((34, 256, 4096), (34, 4096, 256))])
 def test_matmul_persistent_tiles(cx, sa, sb):
-    """More full 256x256 items than blocks that fit at once: the direct kernel
-    runs a persistent grid, each block taking several items and issuing the
-    next item's loads before its stores. The bench's batched config (two items
-    per block), an item count that is not a multiple of 8 (plain order) with
-    an odd k-tile count, the XCD order with an odd k-tile count and a
-    broadcast B, up to three items per block, and K split over two items per
-    output tile (136 tiles, 272 items). Checked against float64 products."""
+    """More full items than blocks that fit at once: the direct kernel runs a
+    persistent grid, each block taking several items and issuing the next
+    item's loads before its stores. On 128x128 tiles (512 blocks): the
+    bench's batched config (2048 items, four per block), an item count that is
+    not a multiple of 8 (585, plain order) with an odd k-tile count, the XCD
+    order with an odd k-tile count and a broadcast B (1152 items), up to five
+    items per block (2400); on 256x256 tiles split over K (one block per CU):
+    34 tiles x 8 splits = 272 items. Checked against float64 products."""
     rng = np.random.default_rng(19)
     a = rng.standard_normal(sa).astype(np.float32)
     b = rng.standard_normal(sb).astype(np.float32)
@@ -205,11 +206,11 @@ def test_matmul_persistent_tiles(cx, sa, sb):
     assert_matmul(actual, np.matmul(a.astype(np.float64), b.astype(np.float64)), a, b, f"{sa}@{sb}")
 
 
-@pytest.mark.parametrize("n,linear", [(2048, False), (4096, False), (2048, True)])
+@pytest.mark.parametrize("n,linear", [(1024, False), (4096, False), (2048, True)])
 def test_matmul_full_tiles_special_values(cx, n, linear):
-    # Non-finite values through the 256x256 direct kernel: one item per block
-    # (2048 columns), the persistent grid (4096 columns, two items per block)
-    # and the transposed-B linear. A +inf, a -inf and a NaN in rows of A and a
+    # Non-finite values through the direct 128x128 kernel: one item per block
+    # (1024 columns, 512 items), the persistent grid (4096 columns, four items
+    # per block) and the transposed-B linear. A +inf, a -inf and a NaN in rows of A and a
     # +inf in a column of B: NaN / inf positions and signs as float64 truth,
     # the finite rest at the matmul bar.
     rng = np.random.default_rng(31)
@@ -234,18 +235,18 @@ def test_matmul_full_tiles_special_values(cx, n, linear):
 
 def test_matmul_persistent_tiles_dyadic_exact(cx):
     # Exact in any order: pins the item -> tile map of the persistent grid bit
-    # for bit (260 items, plain order, three k-tiles).
-    i = np.arange(65 * 512 * 96)
-    a = ((i % 13 - 6) / 8).astype(np.float32).reshape(65, 512, 96)
-    j = np.arange(65 * 96 * 512)
-    b = ((j % 9 - 4) / 16).astype(np.float32).reshape(65, 96, 512)
+    # for bit (585 items of 128x128, plain order, three k-tiles).
+    i = np.arange(65 * 384 * 96)
+    a = ((i % 13 - 6) / 8).astype(np.float32).reshape(65, 384, 96)
+    j = np.arange(65 * 96 * 384)
+    b = ((j % 9 - 4) / 16).astype(np.float32).reshape(65, 96, 384)
     actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
     assert_bits(actual, np.matmul(a.astype(np.float64), b.astype(np.float64)).astype(np.float32),
                 "dyadic persistent")
 
 
 def test_gemm_persistent_bias_activation(cx):
-    # The C ABI with a [k, n] B, bias and SiLU over 512 full tiles: the
+    # The C ABI with a [k, n] B, bias and SiLU over 2048 full tiles: the
     # persistent kernel's bias path (bias loads before the next item's tile
     # loads), against float64 truth at the matmul bar.
     import tensorcx_hip_capi as capi
@@ -557,7 +558,8 @@ def test_linear(cx, shape):
 def test_linear_direct128(cx, xs, ws):
     # Linear layers with fewer than one round of 256x256 tiles but >= 256
     # full 128x128 ones (the MLP's second linear, a batched input, a square
-    # 2048 layer) take the direct 128x128 kernel over the whole K, with bias.
+    # 2048 layer) take the direct 128x128 kernel over the whole K rather than
+    # a K split, with bias.
     rng = np.random.default_rng(33)
     x = rng.standard_normal(xs).astype(np.float32)
     w = rng.standard_normal(ws).astype(np.float32)
