@@ -45,19 +45,17 @@ bool direct128_fits(const tcx_hip_gemm_desc_t* d, std::int64_t batches) {
   return gemm::direct_fits<128, 128, 32>(d->m, d->n, d->k) && (d->m / 128) * (d->n / 128) * batches >= 256;
 }
 
-// K split of the direct 256x256 kernel for shapes with fewer than 256 full
-// output tiles and a long K: the smallest power of two that gives >= 256
-// blocks (at most 16), when every split keeps >= 512 of K in whole k-tiles.
-// Measured against the tile the shape would take otherwise: 4096x1024x4096
-// with a transposed B 295 -> 270 us at 4 splits (that shape now takes the
-// 128x128 tiles above), 2048x2048x4096 279 -> 270 us, 1024x1024x8192
-// 546 -> 261 us at 8. 1 = none.
+// K split of the direct 128x128 kernel for shapes with fewer than 256 full
+// 128x128 tiles and a long K: the smallest power of two that gives >= 512
+// items (two blocks per CU; at most 16 splits), when every split keeps >= 512
+// of K in whole k-tiles. 1 = none. (First built on 256x256 tiles with a
+// 256-block target: 1024x1024x8192 546 -> 261 us at 8 splits.)
 std::int64_t gemm_splits(const tcx_hip_gemm_desc_t* d, std::int64_t batches) {
-  if (!gemm::direct_fits<256, 256, 32>(d->m, d->n, d->k) || d->n % 4 != 0) return 1;
+  if (!gemm::direct_fits<128, 128, 32>(d->m, d->n, d->k) || d->n % 4 != 0) return 1;
   if (direct128_fits(d, batches)) return 1;
-  const std::int64_t tiles = (d->m / 256) * (d->n / 256) * batches;
+  const std::int64_t tiles = (d->m / 128) * (d->n / 128) * batches;
   std::int64_t splits = 1;
-  while (tiles * splits < 256 && splits < 16) splits *= 2;
+  while (tiles * splits < 512 && splits < 16) splits *= 2;
   if (splits == 1 || d->k % (32 * splits) != 0 || d->k / splits < 512) return 1;
   return splits;
 }
@@ -154,7 +152,7 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
     return gemm::launch_direct<128, 128, 32, 32, 64, 2>(args, false, s);
   }
   // Fewer full tiles and a long K: split K over several blocks of the direct
-  // 256x256 kernel when the caller brought the workspace
+  // 128x128 kernel when the caller brought the workspace
   // (tcx_hip_gemm_workspace_bytes).
   if (vec && workspace != nullptr && aligned16(workspace)) {
     const std::int64_t splits = gemm_splits(d, batches);
@@ -162,7 +160,8 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
     if (splits > 1 && workspace_bytes >= need) {
       args.splits = static_cast<std::int32_t>(splits);
       args.partial = static_cast<float*>(workspace);
-      return gemm::launch_direct<256, 256, 32, 64, 128, 2>(args, trans_b, s);
+      if (trans_b) return gemm::launch_direct<128, 128, 32, 64, 32, 2>(args, true, s);
+      return gemm::launch_direct<128, 128, 32, 32, 64, 2>(args, false, s);
     }
   }
   if (vec && tiles_256 >= 256) return launch_config<256, 256, 32, 64, 128, 2, true>(args, trans_b, true, s);

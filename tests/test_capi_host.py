@@ -50,12 +50,13 @@ def test_library_exports_every_declared_symbol():
 @pytest.mark.parametrize("m,n,k,batch,trans,expect", [
     (4096, 1024, 4096, (), True, 0),                      # the MLP's second linear: 256 128x128 tiles
     (4096, 1024, 4096, (), False, 0),                     # the same with a [k, n] B
-    (2048, 1024, 4096, (), True, 8 * 2048 * 1024 * 4),   # 128 tiles of 128x128: 8 splits of 256x256
-    (1024, 1024, 8192, (), False, 16 * 1024 * 1024 * 4),  # 16 tiles: 16 splits of 512
-    (512, 512, 8192, (4,), False, 16 * 4 * 512 * 512 * 4),  # batched: 16 tiles
+    (2048, 1024, 4096, (), True, 4 * 2048 * 1024 * 4),   # 128 tiles of 128x128: 4 splits
+    (1024, 1024, 8192, (), False, 8 * 1024 * 1024 * 4),   # 64 tiles: 8 splits of 1024
+    (512, 512, 8192, (4,), False, 8 * 4 * 512 * 512 * 4),  # batched: 64 tiles
     (4096, 4096, 4096, (), False, 0),                     # 256 tiles already
     (1000, 1000, 1000, (), False, 0),                     # partial tiles
     (1024, 1024, 1024, (), False, 0),                     # splits would keep < 512 of K
+    (512, 512, 16384, (), False, 16 * 512 * 512 * 4),     # 16 tiles: the 16-split cap
     (512, 512, 512, (), False, 0),
 ])
 def test_gemm_workspace_query(m, n, k, batch, trans, expect):

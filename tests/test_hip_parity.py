@@ -149,7 +149,7 @@ def test_gemm_split_k_matches_unsplit(cx):
     dx, dw, db = (capi.DeviceArray.from_numpy(t) for t in (x, w, bias))
     d = capi.gemm_desc(2048, 1024, 4096, rhs_transposed=True, bias=db.ptr, activation="silu")
     ws = capi.gemm_workspace(d)
-    assert ws is not None and ws.nbytes == 8 * 2048 * 1024 * 4
+    assert ws is not None and ws.nbytes == 4 * 2048 * 1024 * 4
     outs = []
     for workspace in (None, ws):
         out = capi.DeviceArray((2048, 1024))
@@ -197,8 +197,8 @@ def test_matmul_persistent_tiles(cx, sa, sb):
     bench's batched config (2048 items, four per block), an item count that is
     not a multiple of 8 (585, plain order) with an odd k-tile count, the XCD
     order with an odd k-tile count and a broadcast B (1152 items), up to five
-    items per block (2400); on 256x256 tiles split over K (one block per CU):
-    34 tiles x 8 splits = 272 items. Checked against float64 products."""
+    items per block (2400), and K split over 4 items per tile (136 tiles, 544
+    items). Checked against float64 products."""
     rng = np.random.default_rng(19)
     a = rng.standard_normal(sa).astype(np.float32)
     b = rng.standard_normal(sb).astype(np.float32)
