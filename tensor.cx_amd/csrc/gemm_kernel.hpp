@@ -355,17 +355,19 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
 }
 
 // Full-tile GEMM with global -> LDS direct loads (buffer_load ... lds), for
-// B given as [k, n] when every tile is full, rows are 16-byte aligned and the
-// grid is at least one round. Each tile's loads are issued into the other
-// LDS stage right after a barrier and land while the current stage's MFMAs
-// run: no staging registers, no LDS store instructions, no wait before the
-// barrier beyond the loads themselves.
+// B given as [k, n] or transposed, when every tile is full and rows are
+// 16-byte aligned (128x128 tiles for every such shape of >= 256 tiles and for
+// the K split; the template also builds 256x256 tiles). Each tile's loads are
+// issued into the other LDS stage right after a barrier and land while the
+// current stage's MFMAs run: no staging registers, no LDS store
+// instructions, no wait before the barrier beyond the loads themselves.
 //
 // LDS layout: A m-major ([m][k], the eight 16-byte chunks of a 32-wide row
 // XOR-swizzled by (m / 2) % 8, so both the DMA writes and the fragment reads
-// are conflict-free), B k-major with rows padded by 8 floats. One wave
-// instruction fills 8 rows of A (64 lanes x 16 B, contiguous) or one row of
-// B. A lane reads 4 consecutive k of one A row in one ds_read_b128, so inside
+// are conflict-free), a [k, n] B k-major with rows padded by 8 floats, a
+// transposed B like A. One wave instruction fills 8 rows of A (64 lanes x
+// 16 B, contiguous) or one k row of a [k, n] B (64 lanes for 256 columns,
+// the first 32 for 128). A lane reads 4 consecutive k of one A row in one ds_read_b128, so inside
 // each 16-k group MFMA step s of lane group kl uses k = 4 * kl + s for A and B
 // alike (a permutation of the k order, covered by the parity bound).
 //
