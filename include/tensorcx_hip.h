@@ -205,11 +205,19 @@ size_t tcx_hip_reduce_workspace_bytes(int op, int dtype, int64_t outer, int64_t 
 int tcx_hip_reduce(int op, int dtype, const void* x, void* out, int64_t outer, int64_t reduce,
                    int64_t inner, void* workspace, size_t workspace_bytes, tcx_stream_t stream);
 
+/* Metadata capacity of tcx_hip_reduce_axes and tcx_hip_binary. Callers fold
+ * the shape first (size-1 axes dropped, neighbouring axes that every operand
+ * walks alike merged), which leaves every axis with extent >= 2, so a folded
+ * rank above 40 would need more than 2^40 elements: any tensor that fits in
+ * device memory folds within it. */
+#define TCX_HIP_MAX_FOLDED_RANK 40
+
 /* General reduction over any axis selection, with the reference's
  * make_reduction_plan metadata (core/shape.cpp:140-173): `meta` holds
- * extent/stride pairs for all `rank` axes, kept axes first then reduced axes,
- * `outer_rank` of them kept; one output per group in the reference's exact
- * element order (cpu_backend.cpp:1102-1153; cpu_math.cpp:48-54). */
+ * extent/stride pairs for all `rank` (<= TCX_HIP_MAX_FOLDED_RANK) axes, kept
+ * axes first then reduced axes, `outer_rank` of them kept; one output per
+ * group in the reference's exact element order (cpu_backend.cpp:1102-1153;
+ * cpu_math.cpp:48-54). */
 int tcx_hip_reduce_axes(int op, int dtype, const void* x, void* out, const int64_t* meta,
                         int32_t outer_rank, int32_t rank, int64_t groups,
                         int64_t reduction_size, tcx_stream_t stream);
@@ -243,8 +251,9 @@ int tcx_hip_unary_f32(int op, const float* x, float* out, int64_t n, tcx_stream_
 #define TCX_BINARY_MULTIPLY 2
 #define TCX_BINARY_DIVIDE 3
 #define TCX_HIP_MAX_RANK 8
-/* Broadcast arithmetic over a make_broadcast_plan (core/shape.cpp:202-229):
- * float32, or int32 wrapping (no divide) as in cpu_backend.cpp:1014-1097. */
+/* Broadcast arithmetic over a make_broadcast_plan (core/shape.cpp:202-229) of
+ * `rank` <= TCX_HIP_MAX_FOLDED_RANK axes: float32, or int32 wrapping (no
+ * divide) as in cpu_backend.cpp:1014-1097. */
 int tcx_hip_binary(int op, int dtype, const void* lhs, const void* rhs, void* out, int32_t rank,
                    const int64_t* out_shape, const int64_t* lhs_strides,
                    const int64_t* rhs_strides, tcx_stream_t stream);

@@ -72,7 +72,7 @@ def execute(kind: str, inputs, *, axis: int = 0, eps: float = 1e-5, axes=None,
     results = []
     for index in range(n_outputs):
         dtype, rank = ctypes.c_int(), ctypes.c_int()
-        shape = (ctypes.c_int64 * 16)()
+        shape = (ctypes.c_int64 * 512)()
         if lib().tcxref_result_info(index, ctypes.byref(dtype), ctypes.byref(rank), shape) != 0:
             raise ReferenceError(3, "missing reference output")
         out = np.empty(tuple(shape[i] for i in range(rank.value)), dtype=_NP[dtype.value])

@@ -157,13 +157,13 @@ void tcxref_set_layout(int axes_rank, const std::int64_t* axes, int slice_rank, 
 
 const char* tcxref_message() { return last.message.c_str(); }
 
-// Output `index` (0 = first output): dtype, rank and up to 16 dims.
+// Output `index` (0 = first output): dtype, rank and up to 512 dims.
 int tcxref_result_info(int index, int* dtype, int* rank, std::int64_t* shape) {
   const tensorcx::Tensor* t = index == 0 ? &last.tensor
                               : static_cast<std::size_t>(index) <= last.extra.size()
                                   ? &last.extra[static_cast<std::size_t>(index - 1)]
                                   : nullptr;
-  if (!t || !t->buffer || t->shape.size() > 16) return -1;
+  if (!t || !t->buffer || t->shape.size() > 512) return -1;
   *dtype = static_cast<int>(t->dtype);
   *rank = static_cast<int>(t->shape.size());
   for (std::size_t i = 0; i < t->shape.size(); ++i) shape[i] = t->shape[i];

@@ -94,6 +94,45 @@ bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15
 
 void* out_ptr(const Tensor& t) { return static_cast<HipBuffer*>(t.buffer.get())->data(); }
 
+// ------------------------------------------------------------ broadcast metadata
+// A broadcast over `shape` with per-operand strides, compressed for the
+// kernels' metadata (at most `max_rank` axes): size-1 axes are dropped and
+// neighbouring axes that every operand walks contiguously are merged. The
+// last `keep` axes stay as they are (the attention softmax reads its last
+// two).
+struct Strided {
+  Shape shape;
+  std::vector<Shape> strides;
+};
+
+Strided compress(const Shape& shape, const std::vector<Shape>& strides, std::size_t keep = 0,
+                 std::size_t max_rank = TCX_HIP_MAX_RANK) {
+  Strided out;
+  out.strides.resize(strides.size());
+  const std::size_t rank = shape.size();
+  std::size_t merged_ok = 0;  // leading entries of out that may still absorb a neighbour
+  for (std::size_t a = 0; a < rank; ++a) {
+    const bool tail = a + keep >= rank;
+    if (!tail && shape[a] == 1) continue;
+    bool merge = !tail && merged_ok == out.shape.size() && !out.shape.empty();
+    for (std::size_t o = 0; merge && o < strides.size(); ++o)
+      merge = out.strides[o].back() == strides[o][a] * shape[a];
+    if (merge) {
+      out.shape.back() *= shape[a];
+      for (std::size_t o = 0; o < strides.size(); ++o) out.strides[o].back() = strides[o][a];
+      continue;
+    }
+    out.shape.push_back(shape[a]);
+    for (std::size_t o = 0; o < strides.size(); ++o) out.strides[o].push_back(strides[o][a]);
+    if (!tail) merged_ok = out.shape.size();
+  }
+  if (out.shape.size() > max_rank)
+    throw std::invalid_argument("HIP broadcast metadata exceeds rank " + std::to_string(max_rank));
+  return out;
+}
+
+Shape broadcast_strides(const Shape& from, const Shape& to) { return make_broadcast_plan(from, to).lhs_strides; }
+
 // ------------------------------------------------------------ reductions
 struct RowDims {
   Shape output_shape;
@@ -166,38 +205,80 @@ void run_rows(int code, const Tensor& x, const Tensor& out, Dim outer, Dim reduc
   if (workspace) ok_or_throw(tcx_hip_stream_synchronize(s), "HIP reduction");
 }
 
-// Reduction over an axis selection: adjacent reduced axes become one
-// (outer, reduce, inner) reduction with the same element order; any other
-// selection runs the general metadata kernel.
+// An axis selection over a contiguous shape, folded: size-1 axes are dropped
+// (they move no offset) and neighbouring axes that are both reduced or both
+// kept are merged (row-major order over two adjacent axes is row-major order
+// over their product). The reference's element order, kept axes row-major
+// and reduced axes row-major in axis order (make_reduction_plan,
+// shape.cpp:140-173; cpu_backend.cpp:1102-1153), is the same before and after,
+// and so is every argmax index.
+struct FoldedAxes {
+  Shape extent;
+  std::vector<bool> reduced;
+};
+
+FoldedAxes fold_axes(const Shape& shape, const std::vector<bool>& selected) {
+  FoldedAxes f;
+  for (std::size_t i = 0; i < shape.size(); ++i) {
+    if (shape[i] == 1) continue;
+    if (!f.extent.empty() && f.reduced.back() == selected[i]) {
+      f.extent.back() *= shape[i];  // bounded by numel(shape)
+    } else {
+      f.extent.push_back(shape[i]);
+      f.reduced.push_back(selected[i]);
+    }
+  }
+  return f;
+}
+
+// Reduction over an axis selection into a non-empty output. After folding, a
+// selection that is one run of axes is an (outer, reduce, inner) reduction
+// with the same element order; any other runs the general metadata kernel
+// over the folded axes, kept first.
 void run_selection(int code, const Tensor& x, const Tensor& out, const Shape& axes, const ReductionPlan& plan,
                    tcx_stream_t s) {
-  const Shape& shape = x.shape;
-  const Dim rank = static_cast<Dim>(shape.size());
-  std::vector<bool> selected(shape.size(), false);
+  const Dim groups = numel(plan.output_shape);
+  if (plan.reduction_size == 0) {  // an empty selected axis: sum 0, mean NaN
+    run_rows(code, x, out, groups, 0, 1, s);
+    return;
+  }
+  const Dim rank = static_cast<Dim>(x.shape.size());
+  std::vector<bool> selected(x.shape.size(), false);
   for (Dim a : axes) selected[static_cast<std::size_t>(a < 0 ? a + rank : a)] = true;
-  Dim first = -1, last = -1;
-  for (Dim i = 0; i < rank; ++i)
-    if (selected[static_cast<std::size_t>(i)]) {
-      if (first < 0) first = i;
-      last = i;
-    }
-  bool adjacent = first >= 0;
-  for (Dim i = first; adjacent && i <= last; ++i) adjacent = selected[static_cast<std::size_t>(i)];
-  if (adjacent && plan.reduction_size != 0) {
+  const FoldedAxes f = fold_axes(x.shape, selected);
+  const auto runs = std::count(f.reduced.begin(), f.reduced.end(), true);
+  if (runs <= 1) {
     Dim outer = 1, reduce = 1, inner = 1;
-    for (Dim i = 0; i < rank; ++i) {
-      const Dim e = shape[static_cast<std::size_t>(i)];
-      if (i < first) outer *= e;
-      else if (i <= last) reduce *= e;
-      else inner *= e;
+    bool seen = false;
+    for (std::size_t i = 0; i < f.extent.size(); ++i) {
+      if (f.reduced[i]) {
+        reduce = f.extent[i];
+        seen = true;
+      } else if (seen) {
+        inner *= f.extent[i];
+      } else {
+        outer *= f.extent[i];
+      }
     }
     run_rows(code, x, out, outer, reduce, inner, s);
     return;
   }
-  if (rank > TCX_HIP_MAX_RANK) throw std::invalid_argument("HIP reductions support rank <= 8");
-  ok_or_throw(tcx_hip_reduce_axes(code, tcx_dtype(x.dtype), device_ptr(x), out_ptr(out), plan.index_metadata.data(),
-                                  static_cast<int32_t>(plan.output_shape.size()), static_cast<int32_t>(rank),
-                                  numel(plan.output_shape), plan.reduction_size, s),
+  // Every folded axis has extent >= 2, so a folded rank above the kernel's
+  // metadata capacity would need more than 2^40 elements.
+  if (f.extent.size() > TCX_HIP_MAX_FOLDED_RANK)
+    throw std::invalid_argument("HIP reduction metadata exceeds the folded rank limit");
+  const Shape strides = contiguous_strides(f.extent);
+  std::vector<std::int64_t> meta;
+  int32_t kept = 0;
+  for (int pass = 0; pass < 2; ++pass)
+    for (std::size_t i = 0; i < f.extent.size(); ++i)
+      if (f.reduced[i] == (pass == 1)) {
+        meta.push_back(f.extent[i]);
+        meta.push_back(strides[i]);
+        kept += pass == 0;
+      }
+  ok_or_throw(tcx_hip_reduce_axes(code, tcx_dtype(x.dtype), device_ptr(x), out_ptr(out), meta.data(), kept,
+                                  static_cast<int32_t>(f.extent.size()), groups, plan.reduction_size, s),
               "HIP reduction");
 }
 
@@ -335,53 +416,50 @@ Tensor matmul(const Tensor& lhs, const Tensor& rhs, tcx_stream_t s) {
     throw std::invalid_argument("matmul only supports float32 tensors");
   const float* a = f32(lhs);
   const float* b = f32(rhs);
-  MatmulPlan plan = make_matmul_plan(lhs.shape, rhs.shape);
-  // Size-1 batch axes contribute nothing to any offset: drop them.
-  {
-    MatmulPlan kept = plan;
-    kept.batch_shape.clear();
-    kept.lhs_batch_strides.clear();
-    kept.rhs_batch_strides.clear();
-    for (std::size_t i = 0; i < plan.batch_shape.size(); ++i) {
-      if (plan.batch_shape[i] == 1) continue;
-      kept.batch_shape.push_back(plan.batch_shape[i]);
-      kept.lhs_batch_strides.push_back(plan.lhs_batch_strides[i]);
-      kept.rhs_batch_strides.push_back(plan.rhs_batch_strides[i]);
-    }
-    plan = std::move(kept);
-  }
-  if (plan.batch_shape.size() > TCX_HIP_MAX_BATCH_RANK)
-    throw std::invalid_argument("HIP matmul supports at most 8 batch dimensions of size > 1");
+  const MatmulPlan plan = make_matmul_plan(lhs.shape, rhs.shape);
   Tensor out = make_tensor(DType::kFloat32, plan.output_shape);
   if (numel(plan.output_shape) == 0) return out;
+  // Batch axes folded: size-1 axes move no offset, and neighbouring axes that
+  // both operands walk contiguously (or both broadcast) are one axis. The
+  // batch index order, and so the output layout, is unchanged.
+  const Strided batch =
+      compress(plan.batch_shape, {plan.lhs_batch_strides, plan.rhs_batch_strides}, 0, TCX_HIP_MAX_FOLDED_RANK);
+  auto* c = static_cast<float*>(out_ptr(out));
   tcx_hip_gemm_desc_t d{};
   d.m = plan.m;
   d.n = plan.n;
   d.k = plan.k;
-  // Batches that only walk the lhs contiguously (rhs shared) are one taller
-  // GEMM: rows of consecutive batches are adjacent in both lhs and out.
-  bool rhs_shared = true, lhs_dense = true;
-  Dim expect = plan.m * plan.k;
-  for (std::size_t i = plan.batch_shape.size(); i-- > 0;) {
-    rhs_shared = rhs_shared && plan.rhs_batch_strides[i] == 0;
-    lhs_dense = lhs_dense && (plan.batch_shape[i] == 1 || plan.lhs_batch_strides[i] == expect);
-    expect *= plan.batch_shape[i];
+  d.batch_count = 1;
+  if (batch.shape.size() == 1 && batch.strides[1][0] == 0 && batch.strides[0][0] == plan.m * plan.k) {
+    // Batches that only walk the lhs contiguously (rhs shared) are one taller
+    // GEMM: rows of consecutive batches are adjacent in both lhs and out.
+    d.m = plan.m * batch.shape[0];
+    run_gemm(a, b, c, d, s, "HIP matmul");
+    return out;
   }
-  const Dim batches = numel(plan.batch_shape);
-  if (rhs_shared && lhs_dense) {
-    d.m = plan.m * batches;
-    d.batch_count = 1;
-    d.batch_rank = 0;
-  } else {
-    d.batch_count = batches;
-    d.batch_rank = static_cast<int32_t>(plan.batch_shape.size());
-    for (std::size_t i = 0; i < plan.batch_shape.size(); ++i) {
-      d.batch_shape[i] = plan.batch_shape[i];
-      d.lhs_batch_strides[i] = plan.lhs_batch_strides[i];
-      d.rhs_batch_strides[i] = plan.rhs_batch_strides[i];
+  // The last TCX_HIP_MAX_BATCH_RANK folded axes go to the kernel; any axes in
+  // front of them (alternating broadcast patterns only) are walked here, one
+  // launch per index.
+  const std::size_t rank = batch.shape.size();
+  const std::size_t lead = rank > TCX_HIP_MAX_BATCH_RANK ? rank - TCX_HIP_MAX_BATCH_RANK : 0;
+  d.batch_rank = static_cast<int32_t>(rank - lead);
+  for (std::size_t i = lead; i < rank; ++i) {
+    d.batch_shape[i - lead] = batch.shape[i];
+    d.lhs_batch_strides[i - lead] = batch.strides[0][i];
+    d.rhs_batch_strides[i - lead] = batch.strides[1][i];
+    d.batch_count *= batch.shape[i];
+  }
+  const Dim launches = numel(Shape(batch.shape.begin(), batch.shape.begin() + static_cast<std::ptrdiff_t>(lead)));
+  for (Dim index = 0; index < launches; ++index) {
+    Dim rest = index, lhs_off = 0, rhs_off = 0;
+    for (std::size_t i = lead; i-- > 0;) {
+      const Dim coord = rest % batch.shape[i];
+      rest /= batch.shape[i];
+      lhs_off += coord * batch.strides[0][i];
+      rhs_off += coord * batch.strides[1][i];
     }
+    run_gemm(a + lhs_off, b + rhs_off, c + index * d.batch_count * plan.m * plan.n, d, s, "HIP matmul");
   }
-  run_gemm(a, b, static_cast<float*>(out_ptr(out)), d, s, "HIP matmul");
   return out;
 }
 
@@ -428,6 +506,7 @@ Tensor linear(std::span<const Tensor> inputs, tcx_stream_t s) {
   return out;
 }
 
+
 // ------------------------------------------------------------ elementwise
 Tensor unary(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
   const int code = op.kind == OpKind::kExp ? TCX_UNARY_EXP : op.kind == OpKind::kGelu ? TCX_UNARY_GELU : TCX_UNARY_SILU;
@@ -454,7 +533,6 @@ Tensor binary(const OpDesc& op, const Tensor& lhs, const Tensor& rhs, tcx_stream
   const void* l = device_ptr(lhs);
   const void* r = device_ptr(rhs);
   const BroadcastPlan plan = make_broadcast_plan(lhs.shape, rhs.shape);
-  if (plan.output_shape.size() > TCX_HIP_MAX_RANK) throw std::invalid_argument("HIP arithmetic supports rank <= 8");
   Tensor out = make_tensor(lhs.dtype, plan.output_shape);
   if (numel(plan.output_shape) == 0) return out;
   // Row-vector bias on float32 addition: the fused bias kernel, same rounding.
@@ -467,8 +545,11 @@ Tensor binary(const OpDesc& op, const Tensor& lhs, const Tensor& rhs, tcx_stream
                 "HIP add");
     return out;
   }
-  ok_or_throw(tcx_hip_binary(code, tcx_dtype(lhs.dtype), l, r, out_ptr(out), static_cast<int32_t>(os.size()),
-                             os.data(), plan.lhs_strides.data(), plan.rhs_strides.data(), s),
+  // Size-1 axes dropped and axes both operands walk contiguously merged: any
+  // rank folds to at most one axis per change of broadcast pattern.
+  const Strided m = compress(os, {plan.lhs_strides, plan.rhs_strides}, 0, TCX_HIP_MAX_FOLDED_RANK);
+  ok_or_throw(tcx_hip_binary(code, tcx_dtype(lhs.dtype), l, r, out_ptr(out), static_cast<int32_t>(m.shape.size()),
+                             m.shape.data(), m.strides[0].data(), m.strides[1].data(), s),
               "HIP arithmetic");
   return out;
 }
@@ -482,41 +563,6 @@ Tensor fill(const Tensor& descriptor, double value, tcx_stream_t s) {
   return out;
 }
 
-// ------------------------------------------------------------ broadcast metadata
-// A broadcast over `shape` with per-operand strides, compressed for the
-// kernels' TCX_HIP_MAX_RANK metadata: size-1 axes are dropped and neighbouring
-// axes that every operand walks contiguously are merged. The last `keep` axes
-// stay as they are (the attention softmax reads its last two).
-struct Strided {
-  Shape shape;
-  std::vector<Shape> strides;
-};
-
-Strided compress(const Shape& shape, const std::vector<Shape>& strides, std::size_t keep = 0) {
-  Strided out;
-  out.strides.resize(strides.size());
-  const std::size_t rank = shape.size();
-  std::size_t merged_ok = 0;  // leading entries of out that may still absorb a neighbour
-  for (std::size_t a = 0; a < rank; ++a) {
-    const bool tail = a + keep >= rank;
-    if (!tail && shape[a] == 1) continue;
-    bool merge = !tail && merged_ok == out.shape.size() && !out.shape.empty();
-    for (std::size_t o = 0; merge && o < strides.size(); ++o)
-      merge = out.strides[o].back() == strides[o][a] * shape[a];
-    if (merge) {
-      out.shape.back() *= shape[a];
-      for (std::size_t o = 0; o < strides.size(); ++o) out.strides[o].back() = strides[o][a];
-      continue;
-    }
-    out.shape.push_back(shape[a]);
-    for (std::size_t o = 0; o < strides.size(); ++o) out.strides[o].push_back(strides[o][a]);
-    if (!tail) merged_ok = out.shape.size();
-  }
-  if (out.shape.size() > TCX_HIP_MAX_RANK) throw std::invalid_argument("HIP broadcast metadata exceeds rank 8");
-  return out;
-}
-
-Shape broadcast_strides(const Shape& from, const Shape& to) { return make_broadcast_plan(from, to).lhs_strides; }
 
 // ------------------------------------------------------------ math extension
 // log / sqrt / abs, clip and topk with the plans of core/math.cpp:13-71.

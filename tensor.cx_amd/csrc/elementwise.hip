@@ -60,9 +60,9 @@ __global__ __launch_bounds__(256) void unary_kernel(const float* __restrict__ x,
 }
 
 struct BroadcastMeta {
-  std::int64_t shape[TCX_HIP_MAX_RANK];
-  std::int64_t lhs[TCX_HIP_MAX_RANK];
-  std::int64_t rhs[TCX_HIP_MAX_RANK];
+  std::int64_t shape[TCX_HIP_MAX_FOLDED_RANK];
+  std::int64_t lhs[TCX_HIP_MAX_FOLDED_RANK];
+  std::int64_t rhs[TCX_HIP_MAX_FOLDED_RANK];
   std::int32_t rank;
 };
 
@@ -159,7 +159,8 @@ int tcx_hip_binary(int op, int dtype, const void* lhs, const void* rhs, void* ou
     return fail(TCX_INVALID_ARGUMENT, "arithmetic requires float32 or int32 tensors");
   if (dtype == TCX_INT32 && op == TCX_BINARY_DIVIDE)
     return fail(TCX_INVALID_ARGUMENT, "division only supports float32 tensors");
-  if (rank < 0 || rank > TCX_HIP_MAX_RANK) return fail(TCX_INVALID_ARGUMENT, "binary rank exceeds the supported maximum");
+  if (rank < 0 || rank > TCX_HIP_MAX_FOLDED_RANK)
+    return fail(TCX_INVALID_ARGUMENT, "binary rank exceeds the supported maximum");
   BroadcastMeta m{};
   m.rank = rank;
   std::int64_t n = 1;

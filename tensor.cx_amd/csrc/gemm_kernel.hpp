@@ -737,12 +737,12 @@ int launch_direct(GemmArgs& args, bool trans_b, hipStream_t stream) {
 // 16-byte instructions per wave and stage.
 //   Edges: each operand panel is read through a buffer resource whose
 //   num_records ends at the matrix, so rows past M (and past N for a
-//   transposed B, or k rows past K for a [k, n] B) read as zero. Lanes whose
-//   k is past K in an A row (or a transposed B row) get an out-of-range offset
-//   and read zero too, so that a value past K, which may be infinite, never
-//   meets the zero of the other operand. Columns past N of a [k, n] B read
-//   the next row's data, which only reaches output columns that are not
-//   stored.
+//   transposed B) read as zero through the VGPR offset alone. Lanes whose k
+//   is past K in an A row (or a transposed B row), and lanes of a [k, n] B
+//   whose k row is past K or whose column chunk is past N, get an
+//   out-of-range VGPR offset and read zero too: a value past K, which may be
+//   infinite (the next batch's B rows, say), never meets the zero of the
+//   other operand, and no load leaves the operand's own rows.
 //   LDS layouts (conflict-free reads): A (and a transposed B) [64 rows][64 k]
 //   with the 16-byte chunk c of row r at c ^ (r & 15); a [k, n] B
 //   [64 k][64 n] with chunk c of k row kr at c ^ (8 ((kr >> 2) & 1)), which
@@ -831,7 +831,11 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8))) vo
       dma16(b_rsrc, lds_of(&Bs[stage][0][0]) + row_byte, a_in ? b_voff : kOut,
             __builtin_amdgcn_readfirstlane(k0 * 4));
     } else {
-      dma16(b_rsrc, lds_of(&Bs[stage][0][0]) + row_byte, b_voff,
+      // k rows past K and column chunks past N take the out-of-range offset
+      // on the VGPR side alone, so the zero fill does not depend on whether
+      // the range check counts the SGPR offset.
+      const bool b_in = k0 + row < K && n0 + 4 * b_chunk < N;
+      dma16(b_rsrc, lds_of(&Bs[stage][0][0]) + row_byte, b_in ? b_voff : kOut,
             __builtin_amdgcn_readfirstlane(k0 * static_cast<int>(N) * 4));
     }
   };

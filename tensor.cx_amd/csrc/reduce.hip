@@ -462,8 +462,8 @@ __global__ __launch_bounds__(256) void lane_kernel(const T* __restrict__ x, void
 }
 
 struct AxesMeta {
-  std::int64_t extent[TCX_HIP_MAX_RANK];
-  std::int64_t stride[TCX_HIP_MAX_RANK];
+  std::int64_t extent[TCX_HIP_MAX_FOLDED_RANK];
+  std::int64_t stride[TCX_HIP_MAX_FOLDED_RANK];
   std::int32_t outer_rank, rank;
 };
 
@@ -696,7 +696,7 @@ int tcx_hip_reduce_axes(int op, int dtype, const void* x, void* out, const int64
                         int32_t outer_rank, int32_t rank, int64_t groups, int64_t reduction_size,
                         tcx_stream_t stream) {
   using namespace tcx;
-  if (rank < 0 || rank > TCX_HIP_MAX_RANK || outer_rank < 0 || outer_rank > rank)
+  if (rank < 0 || rank > TCX_HIP_MAX_FOLDED_RANK || outer_rank < 0 || outer_rank > rank)
     return fail(TCX_INVALID_ARGUMENT, "reduction rank exceeds the supported maximum");
   if (groups < 0 || reduction_size < 0) return fail(TCX_INVALID_ARGUMENT, "reduce extents must be non-negative");
   int rc = validate(op, dtype, reduction_size);

@@ -331,7 +331,146 @@ def cases():
     add("masked_select_shape_rejected", "masked_select", [mx, np.ones((5,), bool)])
     big = f32(rng, (3000, 2))
     add("masked_select_chunks", "masked_select", [big, rng.random((3000,)) > .4])
+    suite_tables(add)
+    folded_shapes(add)
     return c
+
+
+def python_route(shape, axis):
+    """The backend request the reference's Python layer makes for
+    x.sum/max/mean(axis) (python/tensorcx/tensor.py:508-529): one axis (or a
+    scalar's 0/-1) goes to the single-axis op, anything else to the axes op."""
+    rank = len(shape)
+    if axis is None:
+        axes, scalar = tuple(range(rank)), rank == 0
+    else:
+        single = isinstance(axis, int)
+        axes = (axis,) if single else tuple(axis)
+        scalar = rank == 0 and single and axis in (0, -1)
+        if scalar:
+            axes = ()
+    if scalar or len(axes) == 1:
+        return {"axis": axes[0] if axes else 0}
+    return {"axes": list(axes)}
+
+
+def label(shape, axis):
+    dims = "x".join(map(str, shape)) or "scalar"
+    if axis is None:
+        return f"{dims}_all"
+    if isinstance(axis, int):
+        return f"{dims}_a{axis}"
+    return f"{dims}_axes{'_'.join(map(str, axis)) or 'none'}"
+
+
+def suite_tables(add):
+    """Case tables of the reference's device-generic suites, with their own
+    inputs: tests/python/test_multi_axis_reductions.py:19-27 (values
+    np.resize([-5, -1, 0, 2, 7]) in float32 and int32),
+    test_int32_primitives.py:24,95-98 (the int32 EDGES), test_batched_matmul.py:
+    14-28 (U(-1, 1) from seed 741 per case) and test_inference_ops.py:15-16,
+    55-101 (normal draws from seeds 31, 4/5 and 9/6)."""
+    multi_axis = [
+        ((2, 3, 4), None), ((2, 3, 4), ()), ((2, 3, 4), (0, 2)),
+        ((2, 3, 4), (2, 0)), ((2, 3, 4), (-1, 0)), ((2, 3, 4), (0, 1, 2)),
+        ((2, 3, 4), (0, 1)), ((2, 3, 4), (1, 2)), ((2, 3, 4), (1,)),
+        ((2, 3, 4), -1), ((1, 1, 1), (0, 2)), ((257, 2, 3), (1, 2)),
+        ((2, 3, 257), (0, 2)), ((0, 2, 3), (1, 2)), ((2, 0, 3), (0, 2)),
+        ((2, 0, 3), (1, 2)), ((2, 0, 3), None), ((2, 0, 3), ()),
+        ((0, 2, 0), (0, 2)), ((0,), None), ((), None), ((), ()), ((), 0), ((), -1),
+    ]
+    for shape, axis in multi_axis:
+        for dtype in (np.float32, np.int32):
+            values = np.resize(np.array([-5, -1, 0, 2, 7], dtype=dtype), shape)
+            for op in ("sum", "max", "mean"):
+                add(f"suite_multi_axis_{op}_{np.dtype(dtype).name}_{label(shape, axis)}", op, [values],
+                    **python_route(shape, axis))
+    edges = np.array([-2**31, 2**31 - 1, -16777217, 16777217, -1, 0, 1, 65537], dtype=np.int32)
+    int32_tables = [((2, 3, 257), 0), ((2, 3, 257), 1), ((3, 257), -1),
+                    ((2, 3, 257), (0, 2)), ((2, 3, 257), (2, 0)), ((3, 257), None),
+                    ((2, 3), ()), ((2, 0, 3), 1), ((0, 2, 3), (1, 2)),
+                    ((0, 2, 3), (0, 2)), ((2, 0, 3), None), ((), 0), ((), -1), ((), None)]
+    for shape, axis in int32_tables:
+        for op in ("sum", "max"):
+            add(f"suite_int32_{op}_{label(shape, axis)}", op, [np.resize(edges, shape)], **python_route(shape, axis))
+    batched = [
+        ((3,), (3,)), ((2, 3), (3,)), ((3,), (3, 4)),
+        ((2, 3, 4), (2, 4, 5)), ((2, 3, 4), (4, 5)),
+        ((3, 4), (2, 4, 5)), ((4,), (2, 4, 5)), ((2, 3, 4), (4,)),
+        ((2, 1, 3, 4), (1, 5, 4, 6)), ((1, 2, 3, 4), (3, 1, 4, 5)),
+        ((2, 1, 1, 3, 4), (1, 5, 1, 4, 2)),
+        ((2, 17, 19), (1, 19, 33)), ((2, 33, 17), (2, 17, 1)),
+        ((0,), (0,)), ((2, 0), (0,)), ((0,), (0, 3)),
+        ((2, 3, 0), (1, 0, 4)), ((0, 3, 4), (1, 4, 2)),
+        ((1, 3, 4), (0, 4, 2)), ((2, 0, 4), (2, 4, 3)),
+        ((2, 3, 4), (2, 4, 0)), ((0, 2, 3, 0), (1, 2, 0, 4)),
+        ((2, 1, 0, 3), (1, 5, 3, 4)), ((3,), (0, 3, 4)),
+        ((0, 2, 3), (3,)), ((2, 1, 3, 4), (5, 4, 2)),
+    ]
+    for shapes in batched:
+        rng = np.random.default_rng(741)
+        a, b = (rng.uniform(-1, 1, s).astype(np.float32) for s in shapes)
+        add(f"suite_batched_matmul_{label(shapes[0], None)}_{label(shapes[1], None)}", "matmul", [a, b])
+
+    def normal(shape, seed=31):
+        return np.random.default_rng(seed).normal(size=shape).astype(np.float32)
+
+    for shape, out in [((3,), 4), ((2, 3), 5), ((2, 1, 4, 3), 2), ((0, 3), 2), ((2, 0), 3), ((2, 3), 0),
+                       ((0,), 2)]:
+        a, w, b = normal(shape), normal((out, shape[-1]), 4), normal((out,), 9)
+        add(f"suite_linear_{label(shape, None)}_out{out}", "linear", [a, w])
+        add(f"suite_linear_bias_{label(shape, None)}_out{out}", "linear", [a, w, b])
+    for shape, axis in [((2, 3, 4), -1), ((2, 3, 4), 1), ((2, 3, 4), 0), ((3,), -1), ((), 0), ((), -1),
+                        ((0, 3), 1), ((2, 0, 3), 1)]:
+        a = normal(shape)
+        pshape = (shape[axis],) if shape else ()
+        w, b = normal(pshape, 5), normal(pshape, 6)
+        add(f"suite_affine_rmsnorm_w_{label(shape, axis)}", "affine_rmsnorm", [a, w], axis=axis, has_weight=True)
+        add(f"suite_affine_layernorm_w_{label(shape, axis)}", "affine_layernorm", [a, w], axis=axis,
+            has_weight=True)
+        add(f"suite_affine_layernorm_wb_{label(shape, axis)}", "affine_layernorm", [a, w, b], axis=axis,
+            has_weight=True, has_bias=True)
+        add(f"suite_affine_layernorm_b_{label(shape, axis)}", "affine_layernorm", [a, b], axis=axis,
+            has_bias=True)
+
+
+def folded_shapes(add):
+    """High-rank requests that the hip device folds before launching (size-1
+    axes dropped, neighbouring axes of one kind merged): the selection of
+    tests/python/test_multi_axis_reductions.py:143-149 at rank 64, selections that fold
+    into one long row or into more axes than 8, a rank-12 broadcast, and a
+    batched matmul whose batch axes alternate between the operands."""
+    rng = np.random.default_rng(20261202)
+    # NumPy arrays stop at 64 axes; the rank-300 case itself runs in the GPU
+    # tests through reshape.
+    high = np.arange(6, dtype=np.float32).reshape((2,) + (1,) * 62 + (3,))
+    for op in ("sum", "max", "mean"):
+        add(f"fold_rank64_{op}", op, [high], axes=[63, 0])
+    add("fold_rank64_sum_i32", "sum", [high.astype(np.int32)], axes=[63, 0])
+    add("fold_rank64_min", "min", [high], axes=[63, 0])
+    add("fold_rank64_argmax", "argmax", [high], axes=[0, 63])
+    long_row = f32(rng, (70, 1, 1, 90))
+    for op in ("sum", "mean", "max"):
+        add(f"fold_long_row_{op}", op, [long_row], axes=[0, 3])
+    add("fold_long_row_argmax", "argmax", [long_row], axes=[0, 3])
+    alternating = f32(rng, (2, 3, 1, 2, 3, 2, 1, 3, 2, 3, 2))
+    for op in ("sum", "max", "mean"):
+        add(f"fold_alternating_{op}", op, [alternating], axes=[0, 3, 5, 8, 10])
+    add("fold_alternating_min", "min", [alternating], axes=[1, 4, 7, 9])
+    add("fold_alternating_argmax", "argmax", [alternating], axes=[1, 4, 7, 9])
+    add("fold_alternating_sum_i32", "sum",
+        [rng.integers(-2**31, 2**31 - 1, (2, 3, 1, 2, 3, 2, 1, 3, 2, 3, 2), dtype=np.int64).astype(np.int32)],
+        axes=[0, 3, 5, 8, 10])
+    lhs_shape = (2, 1, 3, 1, 2, 1, 2, 1, 3, 1, 2, 2)
+    rhs_shape = (1, 2, 1, 3, 1, 2, 1, 2, 1, 3, 2, 1)
+    for op in ("add", "subtract", "multiply", "divide"):
+        add(f"fold_rank12_{op}", op, [f32(rng, lhs_shape), f32(rng, rhs_shape)])
+    add("fold_rank12_add_i32", "add",
+        [rng.integers(-2**31, 2**31 - 1, lhs_shape, dtype=np.int64).astype(np.int32),
+         rng.integers(-2**31, 2**31 - 1, rhs_shape, dtype=np.int64).astype(np.int32)])
+    add("fold_batch10_matmul", "matmul", [f32(rng, (2, 1, 2, 1, 2, 1, 2, 1, 2, 1, 3, 4)),
+                                          f32(rng, (1, 2, 1, 2, 1, 2, 1, 2, 1, 2, 4, 5))])
+    add("fold_batch_size1_matmul", "matmul", [f32(rng, (1, 3, 1, 1, 2, 1, 5, 6)), f32(rng, (3, 1, 1, 2, 1, 6, 4))])
 
 
 def main() -> None:

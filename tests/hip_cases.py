@@ -80,20 +80,33 @@ def assert_close(actual, expected, rtol, atol, context=""):
 
 
 def reduction_run(shape, kw):
-    """(outer, reduce, inner, exact) for a golden reduction case."""
+    """(outer, reduce, inner, exact) for a golden reduction case, folded as the
+    hip backend folds a selection: size-1 axes dropped, neighbouring axes of
+    one kind merged. One run of reduced axes is an (outer, reduce, inner)
+    reduction, exact in order when inner > 1 or reduce <= SEQUENTIAL_MAX;
+    any other selection runs the exact-order metadata kernel."""
     rank = len(shape)
     if "axes" in kw:
-        axes = sorted(a % rank for a in kw["axes"]) if rank else []
+        axes = {a % rank for a in kw["axes"]} if rank else set()
     else:
-        axes = [oracle.normalize_axis(kw.get("axis", 0), rank)] if rank else []
-    if not axes:
+        axes = {oracle.normalize_axis(kw.get("axis", 0), rank)} if rank else set()
+    folded = []  # [extent, reduced]
+    for i, extent in enumerate(shape):
+        if extent == 1:
+            continue
+        if folded and folded[-1][1] == (i in axes):
+            folded[-1][0] *= extent
+        else:
+            folded.append([extent, i in axes])
+    runs = [i for i, (_, reduced) in enumerate(folded) if reduced]
+    if len(runs) > 1:
         return 1, 1, 1, True
-    adjacent = axes == list(range(axes[0], axes[-1] + 1))
-    if not adjacent:
+    if not runs:
         return 1, 1, 1, True
-    outer = int(np.prod(shape[:axes[0]], dtype=np.int64))
-    red = int(np.prod(shape[axes[0]:axes[-1] + 1], dtype=np.int64))
-    inner = int(np.prod(shape[axes[-1] + 1:], dtype=np.int64))
+    r = runs[0]
+    outer = int(np.prod([e for e, _ in folded[:r]], dtype=np.int64))
+    inner = int(np.prod([e for e, _ in folded[r + 1:]], dtype=np.int64))
+    red = folded[r][0]
     return outer, red, inner, inner != 1 or red <= SEQUENTIAL_MAX
 
 
@@ -127,7 +140,7 @@ def run_hip(cx, op, inputs, kw):
         return cx.linear(*t)
     if op in ("affine_layernorm", "affine_rmsnorm"):
         weight = t[1] if kw.get("has_weight") else None
-        bias = t[2] if kw.get("has_bias") else None
+        bias = t[-1] if kw.get("has_bias") else None
         if op == "affine_rmsnorm":
             return cx.rmsnorm(t[0], axis, kw.get("eps", 1e-5), weight=weight)
         return cx.layernorm(t[0], axis, kw.get("eps", 1e-5), weight=weight, bias=bias)

@@ -91,6 +91,25 @@ def test_matmul_direct64_k_tail_isolation(cx):
     assert np.all(np.isfinite(lin[:, 6])) and np.array_equal(np.isinf(lin[:, 7]), np.isinf(lt[:, 7]))
 
 
+def test_matmul_direct64_kn_b_k_tail_isolation(cx):
+    # A [k, n] B with K = 700 = 10 x 64 + 60: batch 0's last k-tile spans
+    # k rows 640..703, and rows 700..703 of that span are batch 1's B rows
+    # 0..3. Infinities there must read as zero for batch 0 (not 0 * inf), and
+    # still reach batch 1's outputs as the reference's sums give them.
+    rng = np.random.default_rng(16)
+    a = rng.standard_normal((2, 500, 700)).astype(np.float32)
+    b = rng.standard_normal((2, 700, 600)).astype(np.float32)
+    b[1, 0:4, :] = np.inf
+    b[1, 2, 5] = -np.inf
+    actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    assert np.all(np.isfinite(actual[0]))
+    assert_matmul(actual[0], a[0].astype(np.float64) @ b[0].astype(np.float64), a[0], b[0], "batch 0")
+    with np.errstate(invalid="ignore"):
+        truth = a[1].astype(np.float64) @ b[1].astype(np.float64)
+    assert np.array_equal(np.isnan(actual[1]), np.isnan(truth))
+    assert np.array_equal(np.isinf(actual[1]), np.isinf(truth))
+
+
 @pytest.mark.parametrize("sa,sb", [((4, 500, 700), (4, 700, 600)), ((3, 1000, 1000), (1000, 1000)),
                                    ((8192, 1000), (1000, 4)), ((4, 1000), (1000, 8192)),
                                    ((999, 1001), (1001, 1003))])
@@ -395,6 +414,79 @@ def test_multi_axis_and_canonical_order(cx):
     assert cx.sum(cx.tensor(pins, device="hip")).numpy() == 3.0
     big = np.array([[3e38, 3e38], [-3e38, -3e38]], np.float32)
     assert np.isposinf(cx.mean(cx.tensor(big, device="hip")).numpy())
+
+
+@pytest.mark.parametrize("name", ["sum", "max", "mean"])
+def test_high_rank_and_empty_metadata(cx, name):
+    # tests/python/test_multi_axis_reductions.py:143-163 of the reference on
+    # hip: a rank-300 selection folds to one 6-element row; a zero-size
+    # tensor whose reduced iteration space would overflow int64 has no outputs
+    # to compute; a selection whose output shape overflows is rejected.
+    x = cx.tensor(np.arange(6, dtype=np.float32), device="hip").reshape((2,) + (1,) * 298 + (3,))
+    y = getattr(x, name)((299, 0), keepdims=True)
+    assert y.shape == (1,) * 300 and y.device == "hip"
+    assert y.reshape(()).numpy() == {"sum": 15.0, "max": 5.0, "mean": 2.5}[name]
+    assert getattr(x, name)((299, 0)).shape == (1,) * 298
+    empty = cx.empty((0, 1, 2**62, 4, 0), device="hip")
+    assert getattr(empty, name)((1, 2, 3)).shape == (0, 0)
+    if name == "max":
+        with pytest.raises(ValueError):
+            getattr(empty, name)(None)
+    else:
+        value = getattr(empty, name)(None).numpy()
+        assert (value == 0) if name == "sum" else np.isnan(value)
+    with pytest.raises(ValueError, match="overflow"):
+        getattr(empty, name)((0, 4))
+    # int32 through the same fold (mean rejects int32, as on the CPU path).
+    xi = cx.tensor(np.arange(6, dtype=np.int32), device="hip").reshape((2,) + (1,) * 298 + (3,))
+    if name == "mean":
+        with pytest.raises(ValueError, match="float32"):
+            xi.mean((299, 0))
+    else:
+        assert getattr(xi, name)((299, 0)).reshape(()).numpy() == {"sum": 15, "max": 5}[name]
+
+
+def test_folded_selections_at_scale(cx):
+    # Selections that fold into one long row (size-1 axes between the reduced
+    # ones) take the tree path; alternating selections over more than eight
+    # folded axes take the metadata kernel at its 40-axis capacity.
+    rng = np.random.default_rng(17)
+    x = rng.standard_normal((300, 1, 1, 700)).astype(np.float32)
+    h = cx.tensor(x, device="hip")
+    for op in ("sum", "mean", "max", "min"):
+        check_case(f"{op} long row", op, [x], {"axes": [0, 3]}, getattr(cx, op)(h, (0, 3)).numpy(),
+                   getattr(oracle, op)(x, (0, 3)))
+    shape = (3, 2, 4, 1, 3, 2, 5, 1, 2, 3, 2, 2)
+    y = rng.standard_normal(shape).astype(np.float32)
+    hy = cx.tensor(y, device="hip")
+    for axes in ((0, 2, 5, 8, 10), (1, 4, 6, 9, 11)):
+        for op in ("sum", "mean", "max", "min"):
+            assert_bits(getattr(cx, op)(hy, axes).numpy(), getattr(oracle, op)(y, axes), f"{op} {axes}")
+    yi = rng.integers(-2**31, 2**31 - 1, shape, dtype=np.int64).astype(np.int32)
+    hi = cx.tensor(yi, device="hip")
+    assert_bits(cx.sum(hi, (0, 2, 5, 8, 10)).numpy(), oracle.sum(yi, (0, 2, 5, 8, 10)), "i32 sum")
+    assert_bits(cx.max(hi, (1, 4, 6, 9, 11)).numpy(), oracle.max(yi, (1, 4, 6, 9, 11)), "i32 max")
+
+
+def test_folded_broadcast_and_batches(cx):
+    # Rank-12 broadcasts whose patterns alternate fold to 12 axes (past the
+    # old 8-axis metadata), bit-exact against the oracle; a batched matmul
+    # with 10 alternating batch axes walks its two leading axes on the host.
+    rng = np.random.default_rng(18)
+    ls, rs = (2, 1, 3, 1, 2, 1, 2, 1, 3, 1, 2, 2), (1, 2, 1, 3, 1, 2, 1, 2, 1, 3, 2, 1)
+    a, b = rng.standard_normal(ls).astype(np.float32), rng.standard_normal(rs).astype(np.float32)
+    ha, hb = cx.tensor(a, device="hip"), cx.tensor(b, device="hip")
+    for op, fn in (("add", lambda p, q: p + q), ("subtract", lambda p, q: p - q),
+                   ("multiply", lambda p, q: p * q), ("divide", lambda p, q: p / q)):
+        assert_bits(fn(ha, hb).numpy(), oracle.binary(op, a, b), f"rank-12 {op}")
+    ai = rng.integers(-2**31, 2**31 - 1, ls, dtype=np.int64).astype(np.int32)
+    bi = rng.integers(-2**31, 2**31 - 1, rs, dtype=np.int64).astype(np.int32)
+    assert_bits((cx.tensor(ai, device="hip") * cx.tensor(bi, device="hip")).numpy(),
+                oracle.binary("multiply", ai, bi), "rank-12 int32 multiply")
+    p = rng.standard_normal((2, 1, 2, 1, 2, 1, 2, 1, 2, 1, 33, 40)).astype(np.float32)
+    q = rng.standard_normal((1, 2, 1, 2, 1, 2, 1, 2, 1, 2, 40, 17)).astype(np.float32)
+    actual = cx.matmul(cx.tensor(p, device="hip"), cx.tensor(q, device="hip")).numpy()
+    assert_matmul(actual, oracle.matmul(p, q), p, q, "batch rank 10")
 
 
 def test_empty_and_scalar(cx):

@@ -36,7 +36,7 @@ def run_oracle(op, inputs, kw):
     if op in ("affine_layernorm", "affine_rmsnorm"):
         rms = op == "affine_rmsnorm"
         weight = inputs[1] if kw.get("has_weight") else None
-        bias = inputs[2] if kw.get("has_bias") else None
+        bias = inputs[-1] if kw.get("has_bias") else None
         return oracle.affine_norm(inputs[0], axis, kw.get("eps", 1e-5), weight, bias, rms=rms)
     if op in ("log", "sqrt", "abs"):
         return getattr(oracle, op)(inputs[0])
