@@ -18,8 +18,14 @@
 //                      16-byte loads; rows split into segments when there are
 //                      too few rows to fill the GPU (partials in workspace)
 //   finish_kernel      combines per-row segment partials in segment order
+//   row_fused_kernel   the segmented row path in one launch (no workspace):
+//                      the last block of a row to arrive combines the row's
+//                      block partials, kept in the file's static scratch
 //   lane_kernel        one lane per output, reference element order
 //   axes_kernel        any axis selection through reduction-plan metadata
+
+#include <mutex>
+#include <string>
 
 #include "common.hpp"
 
@@ -85,18 +91,12 @@ __device__ __forceinline__ void wave_extremum(T& best, std::int64_t& bi) {
 template <typename T>
 using vec4 = T __attribute__((ext_vector_type(4)));
 
+// One wave's reduction of elements [begin, end) of row p (an empty range
+// gives 0, or an extremum candidate with index -1). Sums return their bits
+// (float or uint32) in .bits; extrema return (value bits, row index).
 template <int kOp, typename T, bool kVec>
-__global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, void* __restrict__ out,
-                                                       Partial* __restrict__ partials, std::int64_t rows,
-                                                       std::int64_t reduce, std::int64_t segments,
-                                                       std::int64_t seg_len) {
-  const int lane = threadIdx.x & 63;
-  const std::int64_t gw = static_cast<std::int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (gw >= rows * segments) return;
-  const std::int64_t row = gw / segments, seg = gw % segments;
-  const std::int64_t begin = seg * seg_len;
-  const std::int64_t end = min(reduce, begin + seg_len);
-  const T* __restrict__ p = x + row * reduce;
+__device__ __forceinline__ Partial wave_reduce(const T* __restrict__ p, std::int64_t begin, std::int64_t end,
+                                               int lane) {
   constexpr bool kSum = kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN;
   constexpr bool kLargest = kOp != TCX_REDUCE_MIN;
 
@@ -122,14 +122,7 @@ __global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, 
       } else {
         for (std::int64_t i = begin + lane; i < end; i += 64) s0 += p[i];
       }
-      float s = wave_sum((s0 + s1) + (s2 + s3));
-      if (lane == 0) {
-        if (segments == 1) {
-          static_cast<float*>(out)[row] = kOp == TCX_REDUCE_MEAN ? s / static_cast<float>(reduce) : s;
-        } else {
-          reinterpret_cast<std::uint32_t*>(partials)[gw] = to_bits(s);  // dense words
-        }
-      }
+      return Partial{to_bits(wave_sum((s0 + s1) + (s2 + s3))), 0U, 0};
     } else {
       std::uint32_t s = 0;
       if constexpr (kVec) {
@@ -152,13 +145,7 @@ __global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, 
       } else {
         for (std::int64_t i = begin + lane; i < end; i += 64) s += static_cast<std::uint32_t>(p[i]);
       }
-      s = wave_sum_u32(s);
-      if (lane == 0) {
-        if (segments == 1)
-          static_cast<int*>(out)[row] = static_cast<int>(s);
-        else
-          reinterpret_cast<std::uint32_t*>(partials)[gw] = s;
-      }
+      return Partial{wave_sum_u32(s), 0U, 0};
     }
   } else {
     // Lane-local search in increasing index order; indices are kept relative
@@ -277,17 +264,48 @@ __global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, 
       bi = li < 0 ? -1 : begin + li;
       wave_extremum<T, kLargest>(best, bi);
     }
-    if (lane == 0) {
-      if (segments == 1) {
-        if constexpr (kOp == TCX_REDUCE_ARGMAX)
-          static_cast<int*>(out)[row] = static_cast<int>(bi);
-        else
-          static_cast<T*>(out)[row] = best;
-      } else {
-        partials[gw] = Partial{to_bits(best), 0U, bi};
-      }
-    }
+    return Partial{to_bits(best), 0U, bi};
   }
+}
+
+// Writes the final value of `row` from its combined result.
+template <int kOp, typename T>
+__device__ __forceinline__ void store_row(void* out, std::int64_t row, const Partial& r, std::int64_t reduce) {
+  if constexpr (kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN) {
+    if constexpr (__is_same(T, float)) {
+      const float s = from_bits<float>(r.bits);
+      static_cast<float*>(out)[row] = kOp == TCX_REDUCE_MEAN ? s / static_cast<float>(reduce) : s;
+    } else {
+      static_cast<int*>(out)[row] = static_cast<int>(r.bits);
+    }
+  } else if constexpr (kOp == TCX_REDUCE_ARGMAX) {
+    static_cast<int*>(out)[row] = static_cast<int>(r.index);
+  } else {
+    static_cast<T*>(out)[row] = from_bits<T>(r.bits);
+  }
+}
+
+// One wave per (row, segment). With one segment per row the wave writes the
+// row's result; otherwise it writes its partial to the workspace (sums as
+// dense 32-bit words, extrema as records) for finish_kernel.
+template <int kOp, typename T, bool kVec>
+__global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, void* __restrict__ out,
+                                                       Partial* __restrict__ partials, std::int64_t rows,
+                                                       std::int64_t reduce, std::int64_t segments,
+                                                       std::int64_t seg_len) {
+  const int lane = threadIdx.x & 63;
+  const std::int64_t gw = static_cast<std::int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (gw >= rows * segments) return;
+  const std::int64_t row = gw / segments, seg = gw % segments;
+  const std::int64_t begin = seg * seg_len;
+  const Partial r = wave_reduce<kOp, T, kVec>(x + row * reduce, begin, min(reduce, begin + seg_len), lane);
+  if (lane != 0) return;
+  if (segments == 1)
+    store_row<kOp, T>(out, row, r, reduce);
+  else if constexpr (kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN)
+    reinterpret_cast<std::uint32_t*>(partials)[gw] = r.bits;
+  else
+    partials[gw] = r;
 }
 
 // One block of kThreads threads per row combines that row's segment
@@ -296,16 +314,14 @@ __global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, 
 // order, so the result is deterministic. 1024 threads fetch the 8192 partials
 // of a full-tensor sum in one round of loads (the partials come from the L2 of
 // every XCD), 256 suit many rows with few segments each.
+// Every thread of the block calls it (it synchronises the block).
 template <int kOp, typename T, int kThreads>
-__global__ __launch_bounds__(kThreads) void finish_kernel(const Partial* __restrict__ partials,
-                                                          void* __restrict__ out, std::int64_t rows,
-                                                          std::int64_t reduce, std::int64_t segments) {
+__device__ __forceinline__ void combine_row(const Partial* __restrict__ partials, void* __restrict__ out,
+                                            std::int64_t row, std::int64_t reduce, std::int64_t segments) {
   constexpr int kWaves = kThreads / 64;
   constexpr int kUnroll = 8192 / kThreads < 16 ? 8192 / kThreads : 16;
   __shared__ Partial waves[kWaves];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const std::int64_t row = blockIdx.x;
-  if (row >= rows) return;
   const Partial* p = partials + row * segments;
   constexpr bool kSum = kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN;
   constexpr bool kLargest = kOp != TCX_REDUCE_MIN;
@@ -387,6 +403,69 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const Partial* __restr
         static_cast<T*>(out)[row] = best;
     }
   }
+}
+
+template <int kOp, typename T, int kThreads>
+__global__ __launch_bounds__(kThreads) void finish_kernel(const Partial* __restrict__ partials,
+                                                          void* __restrict__ out, std::int64_t rows,
+                                                          std::int64_t reduce, std::int64_t segments) {
+  if (static_cast<std::int64_t>(blockIdx.x) >= rows) return;
+  combine_row<kOp, T, kThreads>(partials, out, blockIdx.x, reduce, segments);
+}
+
+// Single-launch segmented reduction (the no-allocation path). Block b takes
+// row b / groups and its four waves take segments 4 (b % groups) .. + 3, so a
+// row has 4 * groups segments (the last ones may be empty). Thread 0 combines
+// its waves' partials in wave order into one block partial, publishes it and
+// counts the block in counters[row]; the row's last block to arrive combines
+// the row's block partials in group order (combine_row, whichever block that
+// is), writes the result and returns the counter to zero for the next call.
+// No block waits for another, so every block runs to completion.
+template <int kOp, typename T, bool kVec>
+__global__ __launch_bounds__(256) void row_fused_kernel(const T* __restrict__ x, void* __restrict__ out,
+                                                        Partial* __restrict__ block_partials,
+                                                        std::uint32_t* __restrict__ counters, std::int64_t reduce,
+                                                        std::int64_t groups, std::int64_t seg_len) {
+  constexpr bool kSum = kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN;
+  constexpr bool kLargest = kOp != TCX_REDUCE_MIN;
+  __shared__ Partial part[4];
+  __shared__ int last;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const std::int64_t row = blockIdx.x / groups, group = blockIdx.x % groups;
+  const std::int64_t begin = (4 * group + wave) * seg_len;
+  const Partial r = wave_reduce<kOp, T, kVec>(x + row * reduce, min(reduce, begin), min(reduce, begin + seg_len),
+                                              lane);
+  if (lane == 0) part[wave] = r;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    if constexpr (kSum) {
+      std::uint32_t bits;
+      if constexpr (__is_same(T, float))
+        bits = to_bits((from_bits<float>(part[0].bits) + from_bits<float>(part[1].bits)) +
+                       (from_bits<float>(part[2].bits) + from_bits<float>(part[3].bits)));
+      else
+        bits = (part[0].bits + part[1].bits) + (part[2].bits + part[3].bits);
+      reinterpret_cast<std::uint32_t*>(block_partials)[blockIdx.x] = bits;
+    } else {
+      T best = from_bits<T>(part[0].bits);
+      std::int64_t bi = part[0].index;
+      for (int w = 1; w < 4; ++w) {
+        const T v = from_bits<T>(part[w].bits);
+        if (cand_better<T, kLargest>(v, part[w].index, best, bi)) {
+          best = v;
+          bi = part[w].index;
+        }
+      }
+      block_partials[blockIdx.x] = Partial{to_bits(best), 0U, bi};
+    }
+    __threadfence();  // the partial is visible device-wide before the count
+    last = atomicAdd(&counters[row], 1U) == static_cast<std::uint32_t>(groups - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();  // every other block's partial is visible to this block
+  combine_row<kOp, T, 256>(block_partials, out, row, reduce, groups);
+  if (threadIdx.x == 0) atomicExch(&counters[row], 0U);
 }
 
 // ------------------------------------------------------ exact-order paths
@@ -611,18 +690,98 @@ int launch_reduce(const T* x, void* out, std::int64_t outer, std::int64_t reduce
   return check(hipGetLastError(), "reduce finish kernel launch");
 }
 
+// The no-allocation scratch: block partials and per-row arrival counters of
+// row_fused_kernel. It fits every plan whose two-launch workspace
+// (tcx_hip_reduce_workspace_bytes) is at most
+// TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE: outer * segments <= 16384 partials
+// with segments >= 2, so outer <= 8192 rows and outer * groups <= 16384.
+constexpr std::int64_t kScratchPartials = TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE / sizeof(Partial);
+constexpr std::int64_t kScratchRows = kScratchPartials / 2;
+constexpr std::size_t kScratchBytes =
+    kScratchPartials * sizeof(Partial) + kScratchRows * sizeof(std::uint32_t);
+
+}  // namespace
+}  // namespace tcx
+
+// One copy per device, zero at load. The counters return to zero at the end
+// of every complete call, so each call starts from zeroed counters.
+static __device__ __align__(256) unsigned char scratch[tcx::kScratchBytes];
+
+namespace tcx {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+void* scratch_device[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once per
+// device (with that device current) on the first no-allocation call there.
+// Host code passes this address, never the symbol itself, to kernels.
+int scratch_address(void** address) {
+  int device = 0;
+  int rc = check(hipGetDevice(&device), "hipGetDevice");
+  if (rc != TCX_OK) return rc;
+  if (device < 0 || device >= kMaxDevices) return fail(TCX_UNAVAILABLE, "device index outside the scratch table");
+  std::lock_guard lock(scratch_mutex);
+  if (scratch_device[device] == nullptr) {
+    void* found = nullptr;
+    rc = check(hipGetSymbolAddress(&found, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (rc != TCX_OK) return rc;
+    scratch_device[device] = found;
+  }
+  *address = scratch_device[device];
+  return TCX_OK;
+}
+
+// tcx_hip_reduce without a workspace: plans with one segment per row run the
+// same kernels; segmented plans run row_fused_kernel over the scratch.
+template <int kOp, typename T>
+int launch_reduce_noalloc(const T* x, void* out, std::int64_t outer, std::int64_t reduce, std::int64_t inner,
+                          hipStream_t s) {
+  const RowPlan plan = plan_rows(outer, reduce, inner);
+  if (!plan.row_path || plan.segments == 1) return launch_reduce<kOp, T>(x, out, outer, reduce, inner, nullptr, 0, s);
+  const std::int64_t groups = (plan.segments + 3) / 4;
+  const std::int64_t need = outer * plan.segments * static_cast<std::int64_t>(sizeof(Partial));
+  if (need > TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE || outer > kScratchRows || outer * groups > kScratchPartials)
+    return fail(TCX_INVALID_ARGUMENT, "reduction plan needs " + std::to_string(need) +
+                                          " bytes of partials; the no-allocation scratch holds " +
+                                          std::to_string(TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE));
+  void* base = nullptr;
+  const int rc = scratch_address(&base);
+  if (rc != TCX_OK) return rc;
+  auto* partials = static_cast<Partial*>(base);
+  auto* counters = reinterpret_cast<std::uint32_t*>(partials + kScratchPartials);
+  const dim3 grid(static_cast<unsigned>(outer * groups));
+  if (reduce % 4 == 0 && aligned16(x))
+    hipLaunchKernelGGL((row_fused_kernel<kOp, T, true>), grid, dim3(256), 0, s, x, out, partials, counters, reduce,
+                       groups, plan.seg_len);
+  else
+    hipLaunchKernelGGL((row_fused_kernel<kOp, T, false>), grid, dim3(256), 0, s, x, out, partials, counters, reduce,
+                       groups, plan.seg_len);
+  return check(hipGetLastError(), "reduce fused row kernel launch");
+}
+
+template <int kOp, typename T>
+int launch_any(const T* x, void* out, std::int64_t outer, std::int64_t reduce, std::int64_t inner, void* ws,
+               std::size_t wsb, bool noalloc, hipStream_t s) {
+  if (noalloc) return launch_reduce_noalloc<kOp, T>(x, out, outer, reduce, inner, s);
+  return launch_reduce<kOp, T>(x, out, outer, reduce, inner, ws, wsb, s);
+}
+
 template <typename T>
 int dispatch_reduce(int op, const T* x, void* out, std::int64_t outer, std::int64_t reduce,
-                    std::int64_t inner, void* ws, std::size_t wsb, hipStream_t s) {
+                    std::int64_t inner, void* ws, std::size_t wsb, bool noalloc, hipStream_t s) {
   switch (op) {
-    case TCX_REDUCE_SUM: return launch_reduce<TCX_REDUCE_SUM, T>(x, out, outer, reduce, inner, ws, wsb, s);
-    case TCX_REDUCE_MAX: return launch_reduce<TCX_REDUCE_MAX, T>(x, out, outer, reduce, inner, ws, wsb, s);
-    case TCX_REDUCE_MIN: return launch_reduce<TCX_REDUCE_MIN, T>(x, out, outer, reduce, inner, ws, wsb, s);
-    case TCX_REDUCE_ARGMAX: return launch_reduce<TCX_REDUCE_ARGMAX, T>(x, out, outer, reduce, inner, ws, wsb, s);
+    case TCX_REDUCE_SUM: return launch_any<TCX_REDUCE_SUM, T>(x, out, outer, reduce, inner, ws, wsb, noalloc, s);
+    case TCX_REDUCE_MAX: return launch_any<TCX_REDUCE_MAX, T>(x, out, outer, reduce, inner, ws, wsb, noalloc, s);
+    case TCX_REDUCE_MIN: return launch_any<TCX_REDUCE_MIN, T>(x, out, outer, reduce, inner, ws, wsb, noalloc, s);
+    case TCX_REDUCE_ARGMAX:
+      return launch_any<TCX_REDUCE_ARGMAX, T>(x, out, outer, reduce, inner, ws, wsb, noalloc, s);
     default: break;
   }
   if constexpr (__is_same(T, float)) {
-    if (op == TCX_REDUCE_MEAN) return launch_reduce<TCX_REDUCE_MEAN, T>(x, out, outer, reduce, inner, ws, wsb, s);
+    if (op == TCX_REDUCE_MEAN)
+      return launch_any<TCX_REDUCE_MEAN, T>(x, out, outer, reduce, inner, ws, wsb, noalloc, s);
   }
   return fail(TCX_INVALID_ARGUMENT, "unsupported reduction for this dtype");
 }
@@ -673,8 +832,9 @@ size_t tcx_hip_reduce_workspace_bytes(int op, int dtype, int64_t outer, int64_t 
   return static_cast<size_t>(outer * plan.segments) * sizeof(tcx::Partial);
 }
 
-int tcx_hip_reduce(int op, int dtype, const void* x, void* out, int64_t outer, int64_t reduce,
-                   int64_t inner, void* workspace, size_t workspace_bytes, tcx_stream_t stream) {
+namespace {
+int reduce_entry(int op, int dtype, const void* x, void* out, int64_t outer, int64_t reduce, int64_t inner,
+                 void* workspace, size_t workspace_bytes, bool noalloc, tcx_stream_t stream) {
   using namespace tcx;
   if (outer < 0 || reduce < 0 || inner < 0) return fail(TCX_INVALID_ARGUMENT, "reduce extents must be non-negative");
   int rc = validate(op, dtype, reduce);
@@ -687,9 +847,20 @@ int tcx_hip_reduce(int op, int dtype, const void* x, void* out, int64_t outer, i
   const auto s = static_cast<hipStream_t>(stream);
   if (dtype == TCX_FLOAT32)
     return dispatch_reduce<float>(op, static_cast<const float*>(x), out, outer, reduce, inner, workspace,
-                                  workspace_bytes, s);
+                                  workspace_bytes, noalloc, s);
   return dispatch_reduce<int>(op, static_cast<const int*>(x), out, outer, reduce, inner, workspace,
-                              workspace_bytes, s);
+                              workspace_bytes, noalloc, s);
+}
+}  // namespace
+
+int tcx_hip_reduce(int op, int dtype, const void* x, void* out, int64_t outer, int64_t reduce,
+                   int64_t inner, void* workspace, size_t workspace_bytes, tcx_stream_t stream) {
+  return reduce_entry(op, dtype, x, out, outer, reduce, inner, workspace, workspace_bytes, false, stream);
+}
+
+int tcx_hip_reduce_noalloc(int op, int dtype, const void* x, void* out, int64_t outer, int64_t reduce,
+                           int64_t inner, tcx_stream_t stream) {
+  return reduce_entry(op, dtype, x, out, outer, reduce, inner, nullptr, 0, true, stream);
 }
 
 int tcx_hip_reduce_axes(int op, int dtype, const void* x, void* out, const int64_t* meta,

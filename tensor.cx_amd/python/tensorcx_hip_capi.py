@@ -20,6 +20,7 @@ LIB_PATH = PKG / "lib" / "libtensorcx_hip.so"
 TCX_OK, TCX_INVALID_ARGUMENT, TCX_UNAVAILABLE, TCX_INTERNAL = 0, 1, 2, 3
 TCX_FLOAT32, TCX_INT32 = 0, 1
 TCX_POOL_OOM = 102
+REDUCE_NOALLOC_MAX_WORKSPACE = 262144
 ACT = {"none": 0, "silu": 1, "gelu": 2}
 REDUCE = {"sum": 0, "max": 1, "mean": 2, "min": 3, "argmax": 4}
 UNARY = {"exp": 0, "gelu": 1, "silu": 2}
@@ -35,7 +36,7 @@ EXPORTS = [
     "tcx_hip_pool_destroy", "tcx_hip_event_create", "tcx_hip_event_record",
     "tcx_hip_event_synchronize", "tcx_hip_event_elapsed_ms", "tcx_hip_event_destroy",
     "tcx_hip_gemm_f32", "tcx_hip_gemm_workspace_bytes", "tcx_hip_gemm_f32_ws",
-    "tcx_hip_reduce_workspace_bytes", "tcx_hip_reduce",
+    "tcx_hip_reduce_workspace_bytes", "tcx_hip_reduce", "tcx_hip_reduce_noalloc",
     "tcx_hip_reduce_axes", "tcx_hip_softmax_f32", "tcx_hip_rmsnorm_f32", "tcx_hip_layernorm_f32",
     "tcx_hip_bias_act_f32", "tcx_hip_unary_f32", "tcx_hip_binary", "tcx_hip_fill",
     "tcx_hip_math_unary", "tcx_hip_clip", "tcx_hip_topk", "tcx_hip_embedding_f32",
@@ -125,6 +126,7 @@ def lib() -> ctypes.CDLL:
         L.tcx_hip_reduce_workspace_bytes.argtypes = [ctypes.c_int, ctypes.c_int, i64, i64, i64]
         L.tcx_hip_reduce_workspace_bytes.restype = sz
         L.tcx_hip_reduce.argtypes = [ctypes.c_int, ctypes.c_int, vp, vp, i64, i64, i64, vp, sz, vp]
+        L.tcx_hip_reduce_noalloc.argtypes = [ctypes.c_int, ctypes.c_int, vp, vp, i64, i64, i64, vp]
         L.tcx_hip_reduce_axes.argtypes = [ctypes.c_int, ctypes.c_int, vp, vp, vp, ctypes.c_int32,
                                           ctypes.c_int32, i64, i64, vp]
         L.tcx_hip_softmax_f32.argtypes = [vp, vp, i64, i64, i64, vp]
@@ -289,6 +291,13 @@ def reduce(op: str, dtype: int, x: int, out: int, outer: int, reduce_: int, inne
     ws_bytes = workspace.nbytes if workspace is not None else 0
     check(lib().tcx_hip_reduce(REDUCE[op], dtype, x, out, outer, reduce_, inner, ws_ptr, ws_bytes,
                                s or stream()), f"reduce {op}")
+
+
+def reduce_noalloc(op: str, dtype: int, x: int, out: int, outer: int, reduce_: int, inner: int,
+                   s: int | None = None) -> None:
+    """tcx_hip_reduce_noalloc: no workspace, the library's static scratch."""
+    check(lib().tcx_hip_reduce_noalloc(REDUCE[op], dtype, x, out, outer, reduce_, inner, s or stream()),
+          f"reduce_noalloc {op}")
 
 
 def reduce_workspace(op: str, dtype: int, outer: int, reduce_: int, inner: int) -> DeviceBuffer | None:

@@ -68,6 +68,28 @@ def test_gemm_workspace_query(m, n, k, batch, trans, expect):
     assert capi.lib().tcx_hip_gemm_workspace_bytes(ctypes.byref(d)) == expect
 
 
+def test_reduce_workspace_fits_the_noalloc_scratch():
+    # tcx_hip_reduce_noalloc accepts every plan whose workspace query is at
+    # most TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE; the query stays under it for
+    # every float32 tensor that fits in 288 GB of HBM (at most 2^36
+    # elements): segments are sized to about 8192 waves, so rows x segments
+    # stays below 16384 partials of 16 bytes, and rows longer than 2^30
+    # elements add at most 64 segments. A sweep of row counts and row lengths
+    # around the segmenting thresholds shows it.
+    if not capi.LIB_PATH.exists():
+        pytest.fail("libtensorcx_hip.so is not built: run `python tensor.cx_amd/build.py`")
+    query = capi.lib().tcx_hip_reduce_workspace_bytes
+    largest = 0
+    for rows in (1, 2, 3, 5, 63, 64, 1000, 4095, 4097, 8000, 8191, 8192, 16384):
+        for cols in (65, 8192, 8193, 16384, 100_000, 2**20 + 3, 2**26, 2**31 + 5, 2**33):
+            if rows * cols > 2**36:
+                continue
+            for op in ("sum", "max", "argmax"):
+                largest = max(largest, query(capi.REDUCE[op], capi.TCX_FLOAT32, rows, cols, 1))
+    assert 0 < largest <= capi.REDUCE_NOALLOC_MAX_WORKSPACE
+    assert query(0, capi.TCX_FLOAT32, 1, 8192 * 8192, 1) == 8192 * 16  # the full-tensor sum
+
+
 def test_header_compiles_as_c():
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only", "-x", "c", str(HEADER)],
                    check=True)
