@@ -12,6 +12,7 @@
 #include <cstdint>
 #include <cstring>
 #include <limits>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <utility>
@@ -190,9 +191,22 @@ void run_gemm(const float* lhs, const float* rhs, float* out, const tcx_hip_gemm
   if (workspace) ok_or_throw(tcx_hip_stream_synchronize(s), what);
 }
 
+// Serialises this process's calls of tcx_hip_reduce_noalloc, whose scratch is
+// one per device: each holds it from launch until its stream has finished.
+std::mutex reduce_scratch_mutex;
+
 void run_rows(int code, const Tensor& x, const Tensor& out, Dim outer, Dim reduce, Dim inner, tcx_stream_t s) {
   const int dtype = tcx_dtype(x.dtype);
   const std::size_t ws = tcx_hip_reduce_workspace_bytes(code, dtype, outer, reduce, inner);
+  if (ws != 0 && ws <= TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE) {
+    // Segmented rows (a full-tensor sum, few long rows): one launch over the
+    // library's static scratch instead of a workspace and a second launch.
+    std::lock_guard lock(reduce_scratch_mutex);
+    ok_or_throw(tcx_hip_reduce_noalloc(code, dtype, device_ptr(x), out_ptr(out), outer, reduce, inner, s),
+                "HIP reduction");
+    ok_or_throw(tcx_hip_stream_synchronize(s), "HIP reduction");
+    return;
+  }
   std::shared_ptr<HipBuffer> workspace;
   if (ws) {
     auto created = HipBuffer::create(ws);
