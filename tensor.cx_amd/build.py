@@ -84,6 +84,26 @@ def build_backend() -> pathlib.Path:
     return target
 
 
+def build_contract() -> pathlib.Path:
+    """The backend ABI contract program (tests/cpp/hip_backend_contract.cpp),
+    linked against the backend objects of build_backend and the HIP library,
+    into tests/cpp/_bin/ (built here, run by the tests on CPU and GPU)."""
+    cpp = PKG / "cpp"
+    test_dir = ROOT / "tests" / "cpp"
+    out_dir = test_dir / "_bin"
+    out_dir.mkdir(exist_ok=True)
+    objects = sorted(OBJ.glob("cxx_cpp_*.o"))
+    if not objects:
+        raise SystemExit("build_contract needs build_backend first")
+    target = out_dir / "hip_backend_contract"
+    tmp = out_dir / "hip_backend_contract.tmp"
+    run(["g++", *CXX_FLAGS, f"-I{cpp}", f"-I{ROOT / 'include'}", "-o", str(tmp),
+         str(test_dir / "hip_backend_contract.cpp"), *map(str, objects), f"-L{LIB}", "-ltensorcx_hip",
+         "-Wl,-rpath,$ORIGIN/../../../tensor.cx_amd/lib", "-pthread"])
+    tmp.replace(target)
+    return target
+
+
 def main() -> None:
     parser = argparse.ArgumentParser()
     parser.add_argument("--hip-only", action="store_true")
@@ -91,6 +111,7 @@ def main() -> None:
     print(build_hip())
     if not args.hip_only:
         print(build_backend())
+        print(build_contract())
 
 
 if __name__ == "__main__":

@@ -48,6 +48,30 @@ tcx_stream_t stream() {
   return s;
 }
 
+// The thread's stream, fetched at its first use: an execution validates its
+// whole request (metadata, axes, shapes, dtypes) before it touches the
+// device, so a malformed request is kInvalidArgument even where no device is
+// present.
+class Stream {
+ public:
+  operator tcx_stream_t() {  // NOLINT(google-explicit-constructor): used where a launcher takes one
+    if (stream_ == nullptr) stream_ = stream();
+    return stream_;
+  }
+  bool used() const { return stream_ != nullptr; }
+
+ private:
+  tcx_stream_t stream_{nullptr};
+};
+
+// Bytes of a contiguous tensor, rejecting sizes past size_t.
+std::size_t byte_size(const Shape& shape, DType dtype) {
+  const auto count = static_cast<std::size_t>(numel(shape));
+  if (count > std::numeric_limits<std::size_t>::max() / dtype_size(dtype))
+    throw std::invalid_argument("tensor byte size overflow");
+  return count * dtype_size(dtype);
+}
+
 void synchronize(tcx_stream_t s) {
   ProfileScope span(ProfileCategory::kSynchronize, "stream_synchronize", "hip");
   ok_or_throw(tcx_hip_stream_synchronize(s), "HIP execution");
@@ -68,7 +92,7 @@ void* device_ptr(const Tensor& t) {
   if (t.strides != contiguous_strides(t.shape)) throw std::invalid_argument("HIP tensor metadata must be contiguous");
   const auto* buffer = dynamic_cast<const HipBuffer*>(t.buffer.get());
   if (buffer == nullptr) throw std::invalid_argument("HIP tensor metadata requires a HIP buffer");
-  const auto bytes = static_cast<std::size_t>(numel(t.shape)) * dtype_size(t.dtype);
+  const auto bytes = byte_size(t.shape, t.dtype);
   if (buffer->nbytes() < bytes) throw std::invalid_argument("HIP tensor buffer is smaller than its shape");
   return buffer->data();
 }
@@ -178,7 +202,7 @@ int reduce_code(OpKind kind) {
 // over several blocks get their workspace from the thread's pool (without it,
 // when that allocation fails, the GEMM runs unsplit), held until the stream
 // has run the call.
-void run_gemm(const float* lhs, const float* rhs, float* out, const tcx_hip_gemm_desc_t& d, tcx_stream_t s,
+void run_gemm(const float* lhs, const float* rhs, float* out, const tcx_hip_gemm_desc_t& d, Stream& s,
               const char* what) {
   const std::size_t ws = tcx_hip_gemm_workspace_bytes(&d);
   std::shared_ptr<HipBuffer> workspace;
@@ -195,7 +219,7 @@ void run_gemm(const float* lhs, const float* rhs, float* out, const tcx_hip_gemm
 // one per device: each holds it from launch until its stream has finished.
 std::mutex reduce_scratch_mutex;
 
-void run_rows(int code, const Tensor& x, const Tensor& out, Dim outer, Dim reduce, Dim inner, tcx_stream_t s) {
+void run_rows(int code, const Tensor& x, const Tensor& out, Dim outer, Dim reduce, Dim inner, Stream& s) {
   const int dtype = tcx_dtype(x.dtype);
   const std::size_t ws = tcx_hip_reduce_workspace_bytes(code, dtype, outer, reduce, inner);
   if (ws != 0 && ws <= TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE) {
@@ -250,7 +274,7 @@ FoldedAxes fold_axes(const Shape& shape, const std::vector<bool>& selected) {
 // with the same element order; any other runs the general metadata kernel
 // over the folded axes, kept first.
 void run_selection(int code, const Tensor& x, const Tensor& out, const Shape& axes, const ReductionPlan& plan,
-                   tcx_stream_t s) {
+                   Stream& s) {
   const Dim groups = numel(plan.output_shape);
   if (plan.reduction_size == 0) {  // an empty selected axis: sum 0, mean NaN
     run_rows(code, x, out, groups, 0, 1, s);
@@ -296,7 +320,7 @@ void run_selection(int code, const Tensor& x, const Tensor& out, const Shape& ax
               "HIP reduction");
 }
 
-Tensor reduce(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
+Tensor reduce(const OpDesc& op, const Tensor& x, Stream& s) {
   if (x.dtype == DType::kBool) throw std::invalid_argument("numeric reductions do not support bool tensors");
   (void)device_ptr(x);
   const int code = reduce_code(op.kind);
@@ -325,7 +349,7 @@ Tensor reduce(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
 }
 
 // min / argmax with the reference math plan (core/math.cpp:39-56).
-Tensor argext(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
+Tensor argext(const OpDesc& op, const Tensor& x, Stream& s) {
   if (x.dtype != DType::kFloat32 && x.dtype != DType::kInt32)
     throw std::invalid_argument("math operations require float32 or int32 tensors");
   (void)device_ptr(x);
@@ -369,7 +393,7 @@ float checked_epsilon(double eps) {
   return rounded;
 }
 
-Tensor row_op(const OpDesc& op, const Tensor& x, const Tensor* gamma, const Tensor* beta, tcx_stream_t s) {
+Tensor row_op(const OpDesc& op, const Tensor& x, const Tensor* gamma, const Tensor* beta, Stream& s) {
   const RowDims d = row_dims(x.shape, op.axis);
   const char* name = op.kind == OpKind::kSoftmax ? "softmax" : op.kind == OpKind::kRmsNorm ? "rmsnorm" : "layernorm";
   float eps = 0.F;
@@ -394,7 +418,7 @@ Tensor row_op(const OpDesc& op, const Tensor& x, const Tensor* gamma, const Tens
 
 // kAffineRmsNorm / kAffineLayerNorm with the validation of
 // core/inference.cpp:103-122, computed in one fused pass.
-Tensor affine_norm(const OpDesc& op, std::span<const Tensor> inputs, tcx_stream_t s) {
+Tensor affine_norm(const OpDesc& op, std::span<const Tensor> inputs, Stream& s) {
   const bool rms = op.kind == OpKind::kAffineRmsNorm;
   if (inputs.size() != 1U + op.has_weight + op.has_bias || (rms && op.has_bias))
     throw std::invalid_argument("invalid affine normalization parameters");
@@ -425,7 +449,7 @@ Tensor affine_norm(const OpDesc& op, std::span<const Tensor> inputs, tcx_stream_
 }
 
 // ------------------------------------------------------------ matmul / linear
-Tensor matmul(const Tensor& lhs, const Tensor& rhs, tcx_stream_t s) {
+Tensor matmul(const Tensor& lhs, const Tensor& rhs, Stream& s) {
   if (lhs.dtype != DType::kFloat32 || rhs.dtype != DType::kFloat32)
     throw std::invalid_argument("matmul only supports float32 tensors");
   const float* a = f32(lhs);
@@ -481,7 +505,7 @@ Tensor matmul(const Tensor& lhs, const Tensor& rhs, tcx_stream_t s) {
 // into `out` (contiguous (..., out)). One NT GEMM with the bias and activation
 // in its epilogue: the kLinear composite of core/inference.cpp:89-102 without
 // the transposed weight copy.
-void linear_into(const Tensor& x, const Tensor& w, const Tensor* bias, int act, const Tensor& out, tcx_stream_t s) {
+void linear_into(const Tensor& x, const Tensor& w, const Tensor* bias, int act, const Tensor& out, Stream& s) {
   tcx_hip_gemm_desc_t d{};
   d.k = w.shape[1];
   d.n = w.shape[0];
@@ -512,7 +536,7 @@ Shape linear_shape(std::span<const Tensor> inputs) {
   return shape;
 }
 
-Tensor linear(std::span<const Tensor> inputs, tcx_stream_t s) {
+Tensor linear(std::span<const Tensor> inputs, Stream& s) {
   const Shape shape = linear_shape(inputs);
   Tensor out = make_tensor(DType::kFloat32, shape);
   if (numel(shape) == 0) return out;
@@ -522,7 +546,7 @@ Tensor linear(std::span<const Tensor> inputs, tcx_stream_t s) {
 
 
 // ------------------------------------------------------------ elementwise
-Tensor unary(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
+Tensor unary(const OpDesc& op, const Tensor& x, Stream& s) {
   const int code = op.kind == OpKind::kExp ? TCX_UNARY_EXP : op.kind == OpKind::kGelu ? TCX_UNARY_GELU : TCX_UNARY_SILU;
   if (x.dtype != DType::kFloat32) {
     const char* name = code == TCX_UNARY_EXP ? "exp" : code == TCX_UNARY_GELU ? "gelu" : "silu";
@@ -534,7 +558,7 @@ Tensor unary(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
   return out;
 }
 
-Tensor binary(const OpDesc& op, const Tensor& lhs, const Tensor& rhs, tcx_stream_t s) {
+Tensor binary(const OpDesc& op, const Tensor& lhs, const Tensor& rhs, Stream& s) {
   if (lhs.dtype == DType::kBool || rhs.dtype == DType::kBool)
     throw std::invalid_argument("arithmetic does not support bool tensors");
   if (lhs.dtype != rhs.dtype) throw std::invalid_argument("dtype mismatch for binary operation");
@@ -568,7 +592,7 @@ Tensor binary(const OpDesc& op, const Tensor& lhs, const Tensor& rhs, tcx_stream
   return out;
 }
 
-Tensor fill(const Tensor& descriptor, double value, tcx_stream_t s) {
+Tensor fill(const Tensor& descriptor, double value, Stream& s) {
   if (descriptor.dtype == DType::kInt32 && !is_int32_representable(value))
     throw std::invalid_argument("fill value must be an integer in int32 range");
   const int dtype = descriptor.dtype == DType::kBool ? TCX_BOOL : tcx_dtype(descriptor.dtype);
@@ -585,7 +609,7 @@ void require_math_dtype(const Tensor& t) {
     throw std::invalid_argument("math operations require float32 or int32 tensors");
 }
 
-Tensor math_unary(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
+Tensor math_unary(const OpDesc& op, const Tensor& x, Stream& s) {
   require_math_dtype(x);
   const int code = op.kind == OpKind::kLog ? TCX_MATH_LOG : op.kind == OpKind::kSqrt ? TCX_MATH_SQRT : TCX_MATH_ABS;
   if (code != TCX_MATH_ABS && x.dtype != DType::kFloat32)
@@ -596,7 +620,7 @@ Tensor math_unary(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
   return out;
 }
 
-Tensor clip(std::span<const Tensor> inputs, tcx_stream_t s) {
+Tensor clip(std::span<const Tensor> inputs, Stream& s) {
   if (inputs.size() != 3) throw std::invalid_argument("invalid math operation or input count");
   for (const Tensor& t : inputs) {
     require_math_dtype(t);
@@ -616,7 +640,7 @@ Tensor clip(std::span<const Tensor> inputs, tcx_stream_t s) {
   return out;
 }
 
-std::pair<Tensor, Tensor> topk(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
+std::pair<Tensor, Tensor> topk(const OpDesc& op, const Tensor& x, Stream& s) {
   require_math_dtype(x);
   if (x.shape.empty()) throw std::invalid_argument("topk requires rank >= 1");
   Dim axis = op.axis;
@@ -645,7 +669,7 @@ std::pair<Tensor, Tensor> topk(const OpDesc& op, const Tensor& x, tcx_stream_t s
 
 // ------------------------------------------------------------ inference primitives
 // kEmbedding with make_embedding_plan (core/inference.cpp:47-57).
-Tensor embedding(std::span<const Tensor> inputs, tcx_stream_t s) {
+Tensor embedding(std::span<const Tensor> inputs, Stream& s) {
   if (inputs.size() != 2) throw std::invalid_argument("embedding requires indices and weight");
   const Tensor& indices = inputs[0];
   const Tensor& weight = inputs[1];
@@ -705,7 +729,7 @@ AttentionSoftmaxPlan attention_softmax_plan(const OpDesc& op, std::span<const Te
 }
 
 void attention_softmax_into(const OpDesc& op, const AttentionSoftmaxPlan& plan, const Tensor& scores,
-                            const Tensor* mask, const Tensor& out, tcx_stream_t s) {
+                            const Tensor* mask, const Tensor& out, Stream& s) {
   std::vector<Shape> strides{broadcast_strides(scores.shape, plan.shape)};
   strides.push_back(mask ? broadcast_strides(mask->shape, plan.shape) : Shape(plan.shape.size(), 0));
   const Strided m = compress(plan.shape, strides, 2);
@@ -724,7 +748,7 @@ void attention_softmax_into(const OpDesc& op, const AttentionSoftmaxPlan& plan, 
               "HIP attention softmax");
 }
 
-Tensor attention_softmax(const OpDesc& op, std::span<const Tensor> inputs, tcx_stream_t s) {
+Tensor attention_softmax(const OpDesc& op, std::span<const Tensor> inputs, Stream& s) {
   const AttentionSoftmaxPlan plan = attention_softmax_plan(op, inputs);
   for (const Tensor& t : inputs) (void)device_ptr(t);
   Tensor out = make_tensor(DType::kFloat32, plan.shape);
@@ -735,7 +759,7 @@ Tensor attention_softmax(const OpDesc& op, std::span<const Tensor> inputs, tcx_s
 
 // scores[b, i, j] = sum_f q[b, i, f] * k[b, j, f] over broadcast batches: one
 // NT GEMM reading K in place (the reference transposes K first).
-Tensor attention_scores(const Tensor& q, const Tensor& k, tcx_stream_t s) {
+Tensor attention_scores(const Tensor& q, const Tensor& k, Stream& s) {
   const Shape qb(q.shape.begin(), q.shape.end() - 2), kb(k.shape.begin(), k.shape.end() - 2);
   const Dim rows = q.shape[q.shape.size() - 2], columns = k.shape[k.shape.size() - 2], features = q.shape.back();
   const BroadcastPlan bp = make_broadcast_plan(qb, kb);
@@ -767,7 +791,7 @@ Tensor attention_scores(const Tensor& q, const Tensor& k, tcx_stream_t s) {
 
 // kAttention with the validation of core/inference.cpp:123-161: scores, the
 // attention softmax, then probabilities @ V, each a native launch.
-Tensor attention(const OpDesc& op, std::span<const Tensor> inputs, tcx_stream_t s) {
+Tensor attention(const OpDesc& op, std::span<const Tensor> inputs, Stream& s) {
   if (op.kind != OpKind::kAttention || inputs.size() < 3 || inputs.size() > 4)
     throw std::invalid_argument("attention requires query, key, value and optional mask");
   for (std::size_t i = 0; i < 3; ++i) {
@@ -859,7 +883,7 @@ std::shared_ptr<HipBuffer> scratch(std::size_t bytes) {
   return created.move_value();
 }
 
-Tensor scalar_op(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
+Tensor scalar_op(const OpDesc& op, const Tensor& x, Stream& s) {
   if (x.dtype == DType::kBool) throw std::invalid_argument("numeric operations do not support bool");
   const int code = op.kind == OpKind::kNegate           ? TCX_SCALAR_NEGATE
                    : op.kind == OpKind::kAddScalar      ? TCX_SCALAR_ADD
@@ -881,7 +905,7 @@ Tensor scalar_op(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
 
 int any_dtype(DType d) { return d == DType::kBool ? TCX_BOOL : tcx_dtype(d); }
 
-Tensor cast(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
+Tensor cast(const OpDesc& op, const Tensor& x, Stream& s) {
   const DType to = op.target_dtype;
   if (to != DType::kFloat32 && to != DType::kInt32 && to != DType::kBool)
     throw std::invalid_argument("unsupported cast target dtype");
@@ -899,7 +923,7 @@ Tensor cast(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
 
 // A strided gather of x through `plan`, with size-1 axes dropped and
 // contiguous runs merged to fit the kernel's metadata.
-Tensor gather(const Tensor& x, const TransposePlan& plan, tcx_stream_t s) {
+Tensor gather(const Tensor& x, const TransposePlan& plan, Stream& s) {
   const void* xp = device_ptr(x);
   Tensor out = make_tensor(x.dtype, plan.output_shape);
   if (numel(plan.output_shape) == 0) return out;
@@ -910,7 +934,7 @@ Tensor gather(const Tensor& x, const TransposePlan& plan, tcx_stream_t s) {
   return out;
 }
 
-Tensor concat(const OpDesc& op, std::span<const Tensor> inputs, tcx_stream_t s) {
+Tensor concat(const OpDesc& op, std::span<const Tensor> inputs, Stream& s) {
   std::vector<Shape> shapes;
   for (const Tensor& t : inputs) {
     if (t.dtype != inputs[0].dtype) throw std::invalid_argument("concat dtypes must match");
@@ -951,7 +975,7 @@ int predicate_code(OpKind kind) {
   }
 }
 
-Tensor predicate(const OpDesc& op, std::span<const Tensor> inputs, tcx_stream_t s) {
+Tensor predicate(const OpDesc& op, std::span<const Tensor> inputs, Stream& s) {
   const PredicatePlan plan = make_predicate_plan(op, inputs);
   std::vector<const void*> ptrs;
   for (const Tensor& t : inputs) ptrs.push_back(device_ptr(t));
@@ -976,7 +1000,7 @@ Tensor predicate(const OpDesc& op, std::span<const Tensor> inputs, tcx_stream_t 
   return out;
 }
 
-Tensor bool_reduce(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
+Tensor bool_reduce(const OpDesc& op, const Tensor& x, Stream& s) {
   if (x.dtype != DType::kBool) throw std::invalid_argument("any/all require bool tensors");
   const ReductionPlan plan = make_boolean_reduction_plan(op, x.shape);
   const void* xp = device_ptr(x);
@@ -993,7 +1017,7 @@ Tensor bool_reduce(const OpDesc& op, const Tensor& x, tcx_stream_t s) {
 
 // masked_select: counts per chunk, host offsets, then index compaction and a
 // row gather (cpu_predicate.cpp:72-96).
-Tensor masked_select(const Tensor& x, const Tensor& mask, tcx_stream_t s) {
+Tensor masked_select(const Tensor& x, const Tensor& mask, Stream& s) {
   const MaskedSelectPlan plan = make_masked_select_plan(x, mask);
   const void* xp = device_ptr(x);
   const auto* mp = static_cast<const uint8_t*>(device_ptr(mask));
@@ -1036,6 +1060,8 @@ Status execute_builtin_kernel(const BackendExecution& e) {
   const auto& target = *e.compilation_target;
   if (target.artifact_kind != KernelArtifactKind::kStaticLibrary || target.artifact != kStaticArtifact)
     return Status(StatusCode::kInvalidArgument, "HIP kernels must name the tensorcx_hip static library");
+  if (target.entry_point != "linear_bias_act" && target.entry_point != "bias_act")
+    return Status(StatusCode::kInvalidArgument, "unknown HIP built-in kernel entry point");
   std::vector<const Tensor*> tensors;
   std::vector<std::uint32_t> scalars;
   for (const KernelArgument& a : e.kernel_arguments) {
@@ -1051,7 +1077,7 @@ Status execute_builtin_kernel(const BackendExecution& e) {
   if (scalars.size() != 1 || scalars[0] > TCX_ACT_GELU)
     return Status(StatusCode::kInvalidArgument, "HIP built-in kernels take one activation code");
   const int act = static_cast<int>(scalars[0]);
-  const tcx_stream_t s = stream();
+  Stream s;
   if (target.entry_point == "linear_bias_act") {
     if (tensors.size() != 3) return Status(StatusCode::kInvalidArgument, "linear_bias_act takes x, weight, bias");
     const Tensor inputs[3] = {*tensors[0], *tensors[1], *tensors[2]};
@@ -1069,10 +1095,8 @@ Status execute_builtin_kernel(const BackendExecution& e) {
       ok_or_throw(tcx_hip_bias_act_f32(f32(x), f32(b), static_cast<float*>(out_ptr(out)), numel(x.shape) / cols, cols,
                                        act, s),
                   "HIP bias_act");
-  } else {
-    return Status(StatusCode::kInvalidArgument, "unknown HIP built-in kernel entry point");
   }
-  synchronize(s);
+  if (s.used()) synchronize(s);
   return Status::Ok();
 }
 
@@ -1143,7 +1167,7 @@ Expected<Tensor> empty(Shape shape, DType dtype) {
   try {
     if (dtype != DType::kFloat32 && dtype != DType::kInt32 && dtype != DType::kBool)
       return Status(StatusCode::kInvalidArgument, "HIP tensors support float32, int32 and bool");
-    const auto bytes = static_cast<std::size_t>(numel(shape)) * dtype_size(dtype);
+    const auto bytes = byte_size(shape, dtype);
     if (const int rc = tcx_hip_init(); rc != TCX_OK) return status_from_code(rc, "HIP device");
     auto buffer = HipBuffer::create(bytes);
     if (!buffer) return buffer.status();
@@ -1209,7 +1233,7 @@ Expected<Tensor> borrow(void* data, DType dtype, Shape shape, std::shared_ptr<vo
   try {
     if (dtype != DType::kFloat32 && dtype != DType::kInt32 && dtype != DType::kBool)
       return Status(StatusCode::kInvalidArgument, "HIP tensors support float32, int32 and bool");
-    const auto bytes = static_cast<std::size_t>(numel(shape)) * dtype_size(dtype);
+    const auto bytes = byte_size(shape, dtype);
     if (bytes && reinterpret_cast<std::uintptr_t>(data) % dtype_size(dtype))
       return Status(StatusCode::kInvalidArgument, "borrowed HIP pointer is misaligned");
     auto buffer = HipBuffer::borrow(data, bytes, std::move(owner));
@@ -1240,14 +1264,27 @@ namespace {
 // pattern, backends/cuda/cuda_profiling.h:22-77).
 class DeviceInterval {
  public:
-  DeviceInterval(const char* name, tcx_stream_t stream) noexcept : token_(reserve_device_profile(name, "hip")) {
+  DeviceInterval(const char* name, Stream& stream) noexcept : token_(reserve_device_profile(name, "hip")) {
     if (!token_) return;
+    tcx_stream_t s = nullptr;
+    try {
+      s = stream;
+    } catch (const std::exception&) {
+      error_ = "event_failed";
+      return;
+    }
     if (tcx_hip_event_create(&start_) != TCX_OK || tcx_hip_event_create(&stop_) != TCX_OK ||
-        tcx_hip_event_record(start_, stream) != TCX_OK)
+        tcx_hip_event_record(start_, s) != TCX_OK)
       error_ = "event_failed";
   }
-  void stop(tcx_stream_t stream) noexcept {
-    if (token_ && !error_ && tcx_hip_event_record(stop_, stream) != TCX_OK) error_ = "event_failed";
+  void stop(Stream& stream) noexcept {
+    if (token_ && !error_) {
+      try {
+        if (tcx_hip_event_record(stop_, stream) != TCX_OK) error_ = "event_failed";
+      } catch (const std::exception&) {
+        error_ = "event_failed";
+      }
+    }
     stopped_ = true;
   }
   ~DeviceInterval() {
@@ -1285,7 +1322,7 @@ Status HipBackend::execute(const BackendExecution& e) {
     // Validate every input before touching the device.
     if (e.op.kind != OpKind::kFill)
       for (const Tensor& t : e.inputs) (void)device_ptr(t);
-    const tcx_stream_t s = stream();
+    Stream s;
     DeviceInterval interval("hip_kernels", s);
     Tensor result;
     switch (e.op.kind) {
@@ -1316,7 +1353,7 @@ Status HipBackend::execute(const BackendExecution& e) {
       case OpKind::kTopK: {
         auto [values, indices] = topk(e.op, e.inputs[0], s);
         interval.stop(s);
-        synchronize(s);
+        if (s.used()) synchronize(s);
         e.outputs[0] = std::move(values);
         e.outputs[1] = std::move(indices);
         return Status::Ok();
@@ -1354,7 +1391,7 @@ Status HipBackend::execute(const BackendExecution& e) {
         return Status(StatusCode::kInvalidArgument, "unsupported HIP backend execution operation");
     }
     interval.stop(s);
-    synchronize(s);
+    if (s.used()) synchronize(s);  // nothing to wait for when nothing was launched
     e.outputs[0] = std::move(result);  // publish only after the work completed
     return Status::Ok();
   } catch (const std::invalid_argument& error) {

@@ -90,6 +90,26 @@ def test_reduce_workspace_fits_the_noalloc_scratch():
     assert query(0, capi.TCX_FLOAT32, 1, 8192 * 8192, 1) == 8192 * 16  # the full-tensor sum
 
 
+CONTRACT = ROOT / "tests" / "cpp" / "_bin" / "hip_backend_contract"
+
+
+def test_backend_contract_rejects_malformed_requests_without_a_device():
+    # tests/cpp/hip_backend_contract.cpp part 1: every malformed request is
+    # kInvalidArgument before any allocation (a host-backed pool counts
+    # none), with its output slots untouched; a well-formed one is stopped
+    # only by the missing device. Exit 77 = passed without a device.
+    if not CONTRACT.exists():
+        pytest.fail(f"{CONTRACT} is not built: run `python tensor.cx_amd/build.py`")
+    from conftest import gpu_present
+    if gpu_present():
+        pytest.skip("a device is present: tests/test_hip_contract.py runs the whole contract")
+    env = {k: v for k, v in os.environ.items() if k != "TENSORCX_REQUIRE_HIP"}
+    result = subprocess.run([str(CONTRACT)], capture_output=True, text=True, timeout=120, env=env)
+    assert result.returncode == 77, result.stdout + result.stderr
+    assert "malformed requests rejected before allocation" in result.stdout
+    assert "metadata validation passed" in result.stdout
+
+
 def test_header_compiles_as_c():
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only", "-x", "c", str(HEADER)],
                    check=True)
