@@ -214,18 +214,16 @@ int tcx_hip_reduce(int op, int dtype, const void* x, void* out, int64_t outer, i
 
 /* tcx_hip_reduce without a workspace, for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc); it has no counterpart in the reference. Calls whose
- * tcx_hip_reduce_workspace_bytes would be 0 run exactly as tcx_hip_reduce;
- * segmented plans (few long rows, e.g. a full-tensor sum) run in one launch
- * over a static per-device scratch of 288 KiB, held until the process ends,
- * and are accepted when tcx_hip_reduce_workspace_bytes is at most
- * TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE (else TCX_INVALID_ARGUMENT), which
- * holds for every float32 or int32 input that fits in 288 GB. Results:
- * bit-identical to tcx_hip_reduce for max/min/argmax and int32 sums; float32
- * sums of segmented rows combine in another fixed order (deterministic, same
- * error bar). All calls on one GPU share the scratch: calls that overlap in
- * time on one GPU (other streams, other threads) race and must be serialised
- * by the caller. It never allocates. */
+ * hipMalloc); it has no counterpart in the reference. It runs the kernels of
+ * tcx_hip_reduce with the segment partials of segmented plans (few long rows,
+ * e.g. a full-tensor sum) in a static per-device scratch of 256 KiB, held
+ * until the process ends, so its results are bit-identical to
+ * tcx_hip_reduce's. Plans are accepted when tcx_hip_reduce_workspace_bytes is
+ * at most TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE (else TCX_INVALID_ARGUMENT),
+ * which holds for every float32 or int32 input that fits in 288 GB. All calls
+ * on one GPU share the scratch: calls that overlap in time on one GPU (other
+ * streams, other threads) race and must be serialised by the caller. It
+ * never allocates. */
 #define TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE 262144
 int tcx_hip_reduce_noalloc(int op, int dtype, const void* x, void* out, int64_t outer, int64_t reduce,
                            int64_t inner, tcx_stream_t stream);

@@ -223,8 +223,8 @@ void run_rows(int code, const Tensor& x, const Tensor& out, Dim outer, Dim reduc
   const int dtype = tcx_dtype(x.dtype);
   const std::size_t ws = tcx_hip_reduce_workspace_bytes(code, dtype, outer, reduce, inner);
   if (ws != 0 && ws <= TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE) {
-    // Segmented rows (a full-tensor sum, few long rows): one launch over the
-    // library's static scratch instead of a workspace and a second launch.
+    // Segmented rows (a full-tensor sum, few long rows): the partials go to
+    // the library's static scratch, so no workspace is allocated per call.
     std::lock_guard lock(reduce_scratch_mutex);
     ok_or_throw(tcx_hip_reduce_noalloc(code, dtype, device_ptr(x), out_ptr(out), outer, reduce, inner, s),
                 "HIP reduction");

@@ -18,9 +18,6 @@
 //                      16-byte loads; rows split into segments when there are
 //                      too few rows to fill the GPU (partials in workspace)
 //   finish_kernel      combines per-row segment partials in segment order
-//   row_fused_kernel   the segmented row path in one launch (no workspace):
-//                      the last block of a row to arrive combines the row's
-//                      block partials, kept in the file's static scratch
 //   lane_kernel        one lane per output, reference element order
 //   axes_kernel        any axis selection through reduction-plan metadata
 
@@ -413,61 +410,6 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(const Partial* __restr
   combine_row<kOp, T, kThreads>(partials, out, blockIdx.x, reduce, segments);
 }
 
-// Single-launch segmented reduction (the no-allocation path). Block b takes
-// row b / groups and its four waves take segments 4 (b % groups) .. + 3, so a
-// row has 4 * groups segments (the last ones may be empty). Thread 0 combines
-// its waves' partials in wave order into one block partial, publishes it and
-// counts the block in counters[row]; the row's last block to arrive combines
-// the row's block partials in group order (combine_row, whichever block that
-// is), writes the result and returns the counter to zero for the next call.
-// No block waits for another, so every block runs to completion.
-template <int kOp, typename T, bool kVec>
-__global__ __launch_bounds__(256) void row_fused_kernel(const T* __restrict__ x, void* __restrict__ out,
-                                                        Partial* __restrict__ block_partials,
-                                                        std::uint32_t* __restrict__ counters, std::int64_t reduce,
-                                                        std::int64_t groups, std::int64_t seg_len) {
-  constexpr bool kSum = kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN;
-  constexpr bool kLargest = kOp != TCX_REDUCE_MIN;
-  __shared__ Partial part[4];
-  __shared__ int last;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const std::int64_t row = blockIdx.x / groups, group = blockIdx.x % groups;
-  const std::int64_t begin = (4 * group + wave) * seg_len;
-  const Partial r = wave_reduce<kOp, T, kVec>(x + row * reduce, min(reduce, begin), min(reduce, begin + seg_len),
-                                              lane);
-  if (lane == 0) part[wave] = r;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    if constexpr (kSum) {
-      std::uint32_t bits;
-      if constexpr (__is_same(T, float))
-        bits = to_bits((from_bits<float>(part[0].bits) + from_bits<float>(part[1].bits)) +
-                       (from_bits<float>(part[2].bits) + from_bits<float>(part[3].bits)));
-      else
-        bits = (part[0].bits + part[1].bits) + (part[2].bits + part[3].bits);
-      reinterpret_cast<std::uint32_t*>(block_partials)[blockIdx.x] = bits;
-    } else {
-      T best = from_bits<T>(part[0].bits);
-      std::int64_t bi = part[0].index;
-      for (int w = 1; w < 4; ++w) {
-        const T v = from_bits<T>(part[w].bits);
-        if (cand_better<T, kLargest>(v, part[w].index, best, bi)) {
-          best = v;
-          bi = part[w].index;
-        }
-      }
-      block_partials[blockIdx.x] = Partial{to_bits(best), 0U, bi};
-    }
-    __threadfence();  // the partial is visible device-wide before the count
-    last = atomicAdd(&counters[row], 1U) == static_cast<std::uint32_t>(groups - 1);
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();  // every other block's partial is visible to this block
-  combine_row<kOp, T, 256>(block_partials, out, row, reduce, groups);
-  if (threadIdx.x == 0) atomicExch(&counters[row], 0U);
-}
-
 // ------------------------------------------------------ exact-order paths
 // Sequential per-output loop in the reference's element order.
 template <int kOp, typename T>
@@ -690,21 +632,16 @@ int launch_reduce(const T* x, void* out, std::int64_t outer, std::int64_t reduce
   return check(hipGetLastError(), "reduce finish kernel launch");
 }
 
-// The no-allocation scratch: block partials and per-row arrival counters of
-// row_fused_kernel. It fits every plan whose two-launch workspace
-// (tcx_hip_reduce_workspace_bytes) is at most
-// TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE: outer * segments <= 16384 partials
-// with segments >= 2, so outer <= 8192 rows and outer * groups <= 16384.
-constexpr std::int64_t kScratchPartials = TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE / sizeof(Partial);
-constexpr std::int64_t kScratchRows = kScratchPartials / 2;
-constexpr std::size_t kScratchBytes =
-    kScratchPartials * sizeof(Partial) + kScratchRows * sizeof(std::uint32_t);
+// The no-allocation scratch: the segment partials of the two-launch row path
+// (row_wave_kernel writes them, finish_kernel combines them), for every plan
+// whose workspace query is at most TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE.
+constexpr std::size_t kScratchBytes = TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE;
 
 }  // namespace
 }  // namespace tcx
 
-// One copy per device, zero at load. The counters return to zero at the end
-// of every complete call, so each call starts from zeroed counters.
+// One copy per device, held until the process ends. Each call writes the
+// partials it reads, so nothing needs clearing between calls.
 static __device__ __align__(256) unsigned char scratch[tcx::kScratchBytes];
 
 namespace tcx {
@@ -733,32 +670,22 @@ int scratch_address(void** address) {
   return TCX_OK;
 }
 
-// tcx_hip_reduce without a workspace: plans with one segment per row run the
-// same kernels; segmented plans run row_fused_kernel over the scratch.
+// tcx_hip_reduce with the static scratch as its workspace: the same kernels,
+// the same partials and combine order, so the same bits.
 template <int kOp, typename T>
 int launch_reduce_noalloc(const T* x, void* out, std::int64_t outer, std::int64_t reduce, std::int64_t inner,
                           hipStream_t s) {
   const RowPlan plan = plan_rows(outer, reduce, inner);
   if (!plan.row_path || plan.segments == 1) return launch_reduce<kOp, T>(x, out, outer, reduce, inner, nullptr, 0, s);
-  const std::int64_t groups = (plan.segments + 3) / 4;
   const std::int64_t need = outer * plan.segments * static_cast<std::int64_t>(sizeof(Partial));
-  if (need > TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE || outer > kScratchRows || outer * groups > kScratchPartials)
+  if (need > TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE)
     return fail(TCX_INVALID_ARGUMENT, "reduction plan needs " + std::to_string(need) +
                                           " bytes of partials; the no-allocation scratch holds " +
                                           std::to_string(TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE));
   void* base = nullptr;
   const int rc = scratch_address(&base);
   if (rc != TCX_OK) return rc;
-  auto* partials = static_cast<Partial*>(base);
-  auto* counters = reinterpret_cast<std::uint32_t*>(partials + kScratchPartials);
-  const dim3 grid(static_cast<unsigned>(outer * groups));
-  if (reduce % 4 == 0 && aligned16(x))
-    hipLaunchKernelGGL((row_fused_kernel<kOp, T, true>), grid, dim3(256), 0, s, x, out, partials, counters, reduce,
-                       groups, plan.seg_len);
-  else
-    hipLaunchKernelGGL((row_fused_kernel<kOp, T, false>), grid, dim3(256), 0, s, x, out, partials, counters, reduce,
-                       groups, plan.seg_len);
-  return check(hipGetLastError(), "reduce fused row kernel launch");
+  return launch_reduce<kOp, T>(x, out, outer, reduce, inner, base, kScratchBytes, s);
 }
 
 template <int kOp, typename T>
