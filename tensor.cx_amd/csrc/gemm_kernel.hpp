@@ -733,8 +733,8 @@ int launch_direct(GemmArgs& args, bool trans_b, hipStream_t stream) {
 // included): 16 waves in four K groups of four 32x32 waves, each group taking
 // 16 of every 64 staged k (its partial tile is added in group order at the
 // end, as in gemm_f32_kernel with KS = 4). Tiles go from HBM to LDS with
-// buffer_load ... lds through four stages (three tiles in flight), two
-// 16-byte instructions per wave and stage.
+// buffer_load ... lds through four stages, two k-tiles between barriers,
+// two 16-byte instructions per wave and stage.
 //   Edges: each operand panel is read through a buffer resource whose
 //   num_records ends at the matrix, so rows past M (and past N for a
 //   transposed B) read as zero through the VGPR offset alone. Lanes whose k
@@ -845,28 +845,24 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8))) vo
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.F, 0.F, 0.F, 0.F};
-  auto compute = [&](int stage) {
+  // A wave's operands of one k-tile: a[i][q] and b[j][q] feed the MFMA of
+  // block (i, j) at k step q.
+  struct Frag {
+    float4_t a[2], b[2];
+  };
+  auto load = [&](int stage, Frag& f) {
     const int kc = group * 4 + kl;  // this lane's k chunk of the group's 16 k
-    float4_t a4[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int ar = wm * 32 + 16 * i + r;
-      a4[i] = *reinterpret_cast<const float4_t*>(&As[stage][ar][4 * (kc ^ (ar & 15))]);
+      f.a[i] = *reinterpret_cast<const float4_t*>(&As[stage][ar][4 * (kc ^ (ar & 15))]);
     }
     if constexpr (kTransB) {
-      float4_t b4[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int bc = wn * 32 + 16 * j + r;
-        b4[j] = *reinterpret_cast<const float4_t*>(&Bs[stage][bc][4 * (kc ^ (bc & 15))]);
+        f.b[j] = *reinterpret_cast<const float4_t*>(&Bs[stage][bc][4 * (kc ^ (bc & 15))]);
       }
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[i][q], b4[j][q], acc[i][j], 0, 0, 0);
     } else {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -875,55 +871,70 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8))) vo
         using float2v = float __attribute__((ext_vector_type(2)));
         const float2v bv =
             *reinterpret_cast<const float2v*>(&Bs[stage][kr][4 * (c ^ (8 * ((kr >> 2) & 1))) + 2 * (r & 1)]);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[i][q], bv.x, acc[i][0], 0, 0, 0);
-          acc[i][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[i][q], bv.y, acc[i][1], 0, 0, 0);
-        }
+        f.b[0][q] = bv.x;
+        f.b[1][q] = bv.y;
       }
     }
   };
+  auto mma = [&](const Frag& f) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[i][q], f.b[j][q], acc[i][j], 0, 0, 0);
+  };
+  auto compute = [&](int stage) {
+    Frag f;
+    load(stage, f);
+    mma(f);
+  };
 
-  // Pipeline: tiles kt + 1 and kt + 2 are in flight while tile kt is read;
-  // tile kt + 3 goes into the stage tile kt - 1 used, free since the last
-  // barrier. Each wave has two loads per tile outstanding.
+  // Two k-tiles per barrier over four stages: tiles kt and kt + 1 are read
+  // between two barriers while tiles kt + 2 and kt + 3 land in the stages of
+  // kt - 2 and kt - 1, free since the last barrier. Each wave runs 32 MFMAs
+  // between barriers and a load has two tiles' MFMAs to land (one tile per
+  // barrier, three tiles ahead, measured 26.0 against 24.0 us at 1000^3).
+  // Each wave has two loads per tile in flight.
   const int k_tiles = static_cast<int>((K + BKT - 1) / BKT);
-  for (int p = 0; p < 3 && p < k_tiles; ++p) issue(p, p * BKT);
-  if (k_tiles > 2) __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4): tile 0 has landed
+  for (int p = 0; p < kStages && p < k_tiles; ++p) issue(p, p * BKT);
+  // Tiles 0 and 1 have landed: vmcnt(4) with four tiles in flight, vmcnt(2)
+  // with three.
+  if (k_tiles > 3) __builtin_amdgcn_s_waitcnt(0x0F74);
+  else if (k_tiles == 3) __builtin_amdgcn_s_waitcnt(0x0F72);
   else __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  for (int kt = 0; kt < k_tiles; ++kt) {
-    if (kt + 3 < k_tiles) issue((kt + 3) % kStages, (kt + 3) * BKT);
+  for (int kt = 0; kt < k_tiles; kt += 2) {
+    if (kt >= 2 && kt + 2 < k_tiles) issue((kt + 2) % kStages, (kt + 2) * BKT);
+    if (kt >= 2 && kt + 3 < k_tiles) issue((kt + 3) % kStages, (kt + 3) * BKT);
     compute(kt % kStages);
-    if (kt + 3 < k_tiles) __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4): tile kt + 1 has landed
-    else __builtin_amdgcn_s_waitcnt(0);
+    if (kt + 1 < k_tiles) compute((kt + 1) % kStages);
+    __builtin_amdgcn_s_waitcnt(0);  // tiles kt + 2 and kt + 3 have landed
     __syncthreads();
   }
 
-  // Groups 1..3 pass their partial tiles through LDS (the stages are free
-  // after the last barrier); group 0 adds them in group order.
-  float* red = &As[0][0][0];  // (KS - 1) x 4 waves x 64 lanes x 16 floats = 48 KB
-  if (group > 0) {
+  // Every group passes its partial tile through LDS (the stages are free
+  // after the last barrier); group g then adds the four partials of rows
+  // 16 g .. 16 g + 15 of its tile in group order (the sum order of an
+  // unsplit k loop over the groups' ranges, the same bits whichever group
+  // adds) and stores them, so the adds and stores are spread over all
+  // sixteen waves.
+  float* red = &As[0][0][0];  // KS x 4 waves x 64 lanes x 16 floats = 64 KB
+  auto red_at = [&](int g, int w, int i, int j, int q, int ln) {
+    return red + ((((g * kGroupWaves + w) * 16 + (i * 2 + j) * 4 + q) * 64) + ln);
+  };
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          red[((((group - 1) * kGroupWaves + gwave) * 16 + (i * 2 + j) * 4 + q) * 64) + lane] = acc[i][j][q];
-  }
+      for (int q = 0; q < 4; ++q) *red_at(group, gwave, i, j, q, lane) = acc[i][j][q];
   __syncthreads();
-  if (group > 0) return;
-#pragma unroll
-  for (int g = 1; g < KS; ++g)
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          acc[i][j][q] += red[((((g - 1) * kGroupWaves + gwave) * 16 + (i * 2 + j) * 4 + q) * 64) + lane];
-
+  // This wave now owns the outputs of (wave gwave, i, q) = rows
+  // wm * 32 + 16 i + 4 kl + q of the tile handled by wave gwave of every
+  // group, for the q given by its group: q == group.
+  const int q = group;
   auto col_of = [&](int j) { return kTransB ? 16 * j + r : 2 * r + j; };
   float bias[2];
 #pragma unroll
@@ -932,20 +943,19 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8))) vo
     bias[j] = a.bias != nullptr && col < N ? a.bias[col] : 0.F;
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 2; ++i) {
+    const std::int64_t orow = m0 + wm * 32 + 16 * i + 4 * kl + q;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const std::int64_t orow = m0 + wm * 32 + 16 * i + 4 * kl + q;
-      if (orow >= M) continue;
+    for (int j = 0; j < 2; ++j) {
+      float x = *red_at(0, gwave, i, j, q, lane);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const std::int64_t col = n0 + wn * 32 + col_of(j);
-        if (col >= N) continue;
-        float x = acc[i][j][q];
-        if (a.bias != nullptr) x = x + bias[j];
-        C[orow * N + col] = activate(x, a.activation);
-      }
+      for (int g = 1; g < KS; ++g) x += *red_at(g, gwave, i, j, q, lane);
+      const std::int64_t col = n0 + wn * 32 + col_of(j);
+      if (orow >= M || col >= N) continue;
+      if (a.bias != nullptr) x = x + bias[j];
+      C[orow * N + col] = activate(x, a.activation);
     }
+  }
 }
 
 // True when gemm_f32_direct64_kernel can take the problem: 16-byte rows
@@ -967,9 +977,9 @@ inline int launch_direct64(GemmArgs& args, bool trans_b, hipStream_t stream) {
   if (args.total_tiles > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
   const dim3 grid(static_cast<unsigned>(args.total_tiles)), block(1024);
   if (trans_b)
-    hipLaunchKernelGGL(gemm_f32_direct64_kernel<true>, grid, block, 0, stream, args);
+    hipLaunchKernelGGL((gemm_f32_direct64_kernel<true>), grid, block, 0, stream, args);
   else
-    hipLaunchKernelGGL(gemm_f32_direct64_kernel<false>, grid, block, 0, stream, args);
+    hipLaunchKernelGGL((gemm_f32_direct64_kernel<false>), grid, block, 0, stream, args);
   return check(hipGetLastError(), "gemm_f32 direct 64x64 launch");
 }
 
