@@ -364,8 +364,11 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_kernel(GemmArgs
 //
 // LDS layout: A m-major ([m][k], the eight 16-byte chunks of a 32-wide row
 // XOR-swizzled by (m / 2) % 8, so both the DMA writes and the fragment reads
-// are conflict-free), a [k, n] B k-major with rows padded by 8 floats, a
-// transposed B like A. One wave instruction fills 8 rows of A (64 lanes x
+// are conflict-free), a [k, n] B k-major with unpadded rows, a transposed B
+// like A. A fragment read of a [k, n] B gives each 16-lane group 256
+// contiguous bytes of one k row: conflict-free with rows 4 * BN bytes apart,
+// two cycles per pass with rows padded by 8 floats (SQ_LDS_BANK_CONFLICT was
+// 40 % of SQ_LDS_IDX_ACTIVE at 4096^3 with the padding). One wave instruction fills 8 rows of A (64 lanes x
 // 16 B, contiguous) or one k row of a [k, n] B (64 lanes for 256 columns,
 // the first 32 for 128). A lane reads 4 consecutive k of one A row in one ds_read_b128, so inside
 // each 16-k group MFMA step s of lane group kl uses k = 4 * kl + s for A and B
@@ -379,7 +382,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64)
 __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(GemmArgs a) {
   constexpr int kWavesN = BN / WN, kWaves = (BM / WM) * kWavesN;
   constexpr int TM = WM / 16, TN = WN / 16;
-  constexpr int LDB = BN + 8;
+  constexpr int LDB = BN;
   constexpr int kChunks = BK / 4;
   // A [k, n] B takes one k row per wave instruction (all 64 lanes for 256
   // floats, the first 32 for 128) and 16-byte output stores; a transposed B
@@ -508,7 +511,7 @@ __attribute__((amdgpu_waves_per_eu(kMinWaves, 8))) void gemm_f32_direct_kernel(G
       for (int p = 0; p < kBInst; ++p) {
         const int soff = __builtin_amdgcn_readfirstlane((p * kWaves + k0) * static_cast<int>(N) * 4);
         // Lanes past the row stay off: the DMA writes LDS at M0 + 16 * lane,
-        // which for them would be the next (padded) row.
+        // which for them would be the next row.
         if (BN == 256 || lane < BN / 4) dma16(b_rsrc, b_lds + p * kWaves * LDB * 4, b_voff, soff);
       }
     }
