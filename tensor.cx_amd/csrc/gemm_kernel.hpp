@@ -867,13 +867,17 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8))) vo
         f.b[j] = *reinterpret_cast<const float4_t*>(&Bs[stage][bc][4 * (kc ^ (bc & 15))]);
       }
     } else {
+      // Indexing the stage as 8-byte pairs keeps every read a ds_read_b64
+      // (as float offsets the compiler split the q > 0 reads into
+      // ds_read2_b32, whose single-dword passes put the k rows of lane
+      // groups kl and kl + 2 on the same banks).
+      using float2v = float __attribute__((ext_vector_type(2)));
+      const auto* pairs = reinterpret_cast<const float2v*>(&Bs[stage][0][0]);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int kr = group * 16 + 4 * kl + q;
         const int c = wn * 8 + r / 2;  // chunk of columns 32 wn + 2r, + 1
-        using float2v = float __attribute__((ext_vector_type(2)));
-        const float2v bv =
-            *reinterpret_cast<const float2v*>(&Bs[stage][kr][4 * (c ^ (8 * ((kr >> 2) & 1))) + 2 * (r & 1)]);
+        const float2v bv = pairs[kr * 32 + 2 * (c ^ (8 * ((kr >> 2) & 1))) + (r & 1)];
         f.b[0][q] = bv.x;
         f.b[1][q] = bv.y;
       }
