@@ -6,6 +6,7 @@
 #include <cstdint>
 #include <string>
 
+#include "launch_grid.hpp"
 #include "tensorcx_hip.h"
 
 namespace tcx {
@@ -87,14 +88,6 @@ __device__ __forceinline__ bool better_i32(int v, std::int64_t i, int best, std:
   if (kLargest ? (v > best) : (v < best)) return true;
   if (kLargest ? (v < best) : (v > best)) return false;
   return i < bi;
-}
-
-// Grid helper: enough blocks to cover n items with `per_block` each, capped.
-inline unsigned grid_for(std::int64_t n, std::int64_t per_block, std::int64_t cap = 1 << 20) {
-  std::int64_t g = (n + per_block - 1) / per_block;
-  if (g < 1) g = 1;
-  if (g > cap) g = cap;
-  return static_cast<unsigned>(g);
 }
 
 }  // namespace tcx

@@ -291,18 +291,22 @@ __global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, 
                                                        std::int64_t reduce, std::int64_t segments,
                                                        std::int64_t seg_len) {
   const int lane = threadIdx.x & 63;
-  const std::int64_t gw = static_cast<std::int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (gw >= rows * segments) return;
-  const std::int64_t row = gw / segments, seg = gw % segments;
-  const std::int64_t begin = seg * seg_len;
-  const Partial r = wave_reduce<kOp, T, kVec>(x + row * reduce, begin, min(reduce, begin + seg_len), lane);
-  if (lane != 0) return;
-  if (segments == 1)
-    store_row<kOp, T>(out, row, r, reduce);
-  else if constexpr (kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN)
-    reinterpret_cast<std::uint32_t*>(partials)[gw] = r.bits;
-  else
-    partials[gw] = r;
+  // Grid-stride over the waves' items (the launcher caps the grid); the
+  // bound is wave-uniform, so every lane of a wave runs the same iterations.
+  const std::int64_t items = rows * segments;
+  const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * 4;
+  for (std::int64_t gw = static_cast<std::int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); gw < items; gw += step) {
+    const std::int64_t row = gw / segments, seg = gw % segments;
+    const std::int64_t begin = seg * seg_len;
+    const Partial r = wave_reduce<kOp, T, kVec>(x + row * reduce, begin, min(reduce, begin + seg_len), lane);
+    if (lane != 0) continue;
+    if (segments == 1)
+      store_row<kOp, T>(out, row, r, reduce);
+    else if constexpr (kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN)
+      reinterpret_cast<std::uint32_t*>(partials)[gw] = r.bits;
+    else
+      partials[gw] = r;
+  }
 }
 
 // One block of kThreads threads per row combines that row's segment
@@ -476,10 +480,12 @@ template <int kOp, typename T>
 __global__ __launch_bounds__(256) void lane_kernel(const T* __restrict__ x, void* __restrict__ out,
                                                    std::int64_t outer, std::int64_t reduce,
                                                    std::int64_t inner) {
-  const std::int64_t id = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (id >= outer * inner) return;
-  const T* base = x + (id / inner) * reduce * inner + id % inner;
-  sequential<kOp, T>(base, reduce, inner, out, id);
+  const std::int64_t items = outer * inner;
+  const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * blockDim.x;
+  for (std::int64_t id = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; id < items; id += step) {
+    const T* base = x + (id / inner) * reduce * inner + id % inner;
+    sequential<kOp, T>(base, reduce, inner, out, id);
+  }
 }
 
 struct AxesMeta {
@@ -498,12 +504,11 @@ __device__ __forceinline__ std::int64_t meta_offset(std::int64_t index, const Ax
   return value;
 }
 
+// Output g of an axis selection: the `count` selected elements of group g in
+// the reference's order.
 template <int kOp, typename T>
-__global__ __launch_bounds__(256) void axes_kernel(const T* __restrict__ x, void* __restrict__ out,
-                                                   AxesMeta meta, std::int64_t groups,
-                                                   std::int64_t count) {
-  const std::int64_t g = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (g >= groups) return;
+__device__ __forceinline__ void axes_item(const T* __restrict__ x, void* __restrict__ out, const AxesMeta& meta,
+                                          std::int64_t g, std::int64_t count) {
   const T* base = x + meta_offset(g, meta, 0, meta.outer_rank);
   constexpr bool kSum = kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN;
   auto item = [&](std::int64_t r) { return base[meta_offset(r, meta, meta.outer_rank, meta.rank)]; };
@@ -562,6 +567,15 @@ __global__ __launch_bounds__(256) void axes_kernel(const T* __restrict__ x, void
   }
 }
 
+template <int kOp, typename T>
+__global__ __launch_bounds__(256) void axes_kernel(const T* __restrict__ x, void* __restrict__ out,
+                                                   AxesMeta meta, std::int64_t groups,
+                                                   std::int64_t count) {
+  const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * blockDim.x;
+  for (std::int64_t g = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; g < groups; g += step)
+    axes_item<kOp, T>(x, out, meta, g, count);
+}
+
 // ------------------------------------------------------------ planning
 struct RowPlan {
   bool row_path;
@@ -601,7 +615,7 @@ int launch_reduce(const T* x, void* out, std::int64_t outer, std::int64_t reduce
                   void* workspace, std::size_t workspace_bytes, hipStream_t s) {
   const RowPlan plan = plan_rows(outer, reduce, inner);
   if (!plan.row_path) {
-    hipLaunchKernelGGL((lane_kernel<kOp, T>), dim3(grid_for(outer * inner, 256, 0x7fffffff)), dim3(256), 0,
+    hipLaunchKernelGGL((lane_kernel<kOp, T>), dim3(grid_for(outer * inner, 256, kStrideBlocks)), dim3(256), 0,
                        s, x, out, outer, reduce, inner);
     return check(hipGetLastError(), "reduce lane kernel launch");
   }
@@ -614,7 +628,7 @@ int launch_reduce(const T* x, void* out, std::int64_t outer, std::int64_t reduce
   }
   const bool vec = reduce % 4 == 0 && aligned16(x);
   const std::int64_t waves = outer * plan.segments;
-  const dim3 grid(grid_for(waves, 4, 0x7fffffff));
+  const dim3 grid(grid_for(waves, 4, kStrideBlocks));
   if (vec)
     hipLaunchKernelGGL((row_wave_kernel<kOp, T, true>), grid, dim3(256), 0, s, x, out, partials, outer,
                        reduce, plan.segments, plan.seg_len);
@@ -716,7 +730,7 @@ int dispatch_reduce(int op, const T* x, void* out, std::int64_t outer, std::int6
 template <typename T>
 int dispatch_axes(int op, const T* x, void* out, const AxesMeta& m, std::int64_t groups,
                   std::int64_t count, hipStream_t s) {
-  const dim3 grid(grid_for(groups, 256, 0x7fffffff));
+  const dim3 grid(grid_for(groups, 256, kStrideBlocks));
   switch (op) {
     case TCX_REDUCE_SUM: hipLaunchKernelGGL((axes_kernel<TCX_REDUCE_SUM, T>), grid, dim3(256), 0, s, x, out, m, groups, count); break;
     case TCX_REDUCE_MAX: hipLaunchKernelGGL((axes_kernel<TCX_REDUCE_MAX, T>), grid, dim3(256), 0, s, x, out, m, groups, count); break;

@@ -505,69 +505,71 @@ __global__ __launch_bounds__(256) void row_block_kernel(RowArgs a) {
 // Strided rows: one lane per (outer, inner) row in the reference's order.
 template <RowOp kOp>
 __global__ __launch_bounds__(256) void row_lane_kernel(RowArgs a, std::int64_t reduce, std::int64_t inner) {
-  const std::int64_t id = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (id >= a.rows) return;  // rows = outer * inner
-  const std::int64_t base = (id / inner) * reduce * inner + id % inner;
-  const float* __restrict__ x = a.x + base;
-  float* __restrict__ out = a.out + base;
-  if constexpr (kOp == RowOp::kSoftmax) {
-    float m = -__builtin_inff();
-    for (std::int64_t r = 0; r < reduce; ++r) {
-      const float e = x[r * inner];
-      if (is_nan(e)) {
-        m = e;
-        break;
-      }
-      m = (m < e) ? e : m;
-    }
-    float denom = 0.F;
-    for (std::int64_t r = 0; r < reduce; ++r) denom += expf(x[r * inner] - m);
-    for (std::int64_t r = 0; r < reduce; ++r) out[r * inner] = expf(x[r * inner] - m) / denom;
-  } else if constexpr (kOp == RowOp::kRms) {
-    float ss = 0.F;
-    for (std::int64_t r = 0; r < reduce; ++r) {
-      const float e = x[r * inner];
-      const float sq = e * e;
-      ss += sq;
-    }
-    const float scale = 1.0F / sqrtf(ss / static_cast<float>(reduce) + a.eps);
-    for (std::int64_t r = 0; r < reduce; ++r) {
-      float t = x[r * inner] * scale;
-      if (a.gamma) t = t * a.gamma[r];
-      out[r * inner] = t;
-    }
-  } else {
-    const float first = x[0];
-    float s = 0.F;
-    bool equal = true;
-    for (std::int64_t r = 0; r < reduce; ++r) {
-      const float e = x[r * inner];
-      s += e;
-      equal = equal && e == first;
-    }
-    if (equal && __builtin_isfinite(first)) {
-      const float fillv = a.eps == 0.F ? __builtin_nanf("") : 0.F;
+  // Grid-stride over rows = outer * inner (the launcher caps the grid).
+  const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * blockDim.x;
+  for (std::int64_t id = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; id < a.rows; id += step) {
+    const std::int64_t base = (id / inner) * reduce * inner + id % inner;
+    const float* __restrict__ x = a.x + base;
+    float* __restrict__ out = a.out + base;
+    if constexpr (kOp == RowOp::kSoftmax) {
+      float m = -__builtin_inff();
       for (std::int64_t r = 0; r < reduce; ++r) {
-        float t = fillv;
+        const float e = x[r * inner];
+        if (is_nan(e)) {
+          m = e;
+          break;
+        }
+        m = (m < e) ? e : m;
+      }
+      float denom = 0.F;
+      for (std::int64_t r = 0; r < reduce; ++r) denom += expf(x[r * inner] - m);
+      for (std::int64_t r = 0; r < reduce; ++r) out[r * inner] = expf(x[r * inner] - m) / denom;
+    } else if constexpr (kOp == RowOp::kRms) {
+      float ss = 0.F;
+      for (std::int64_t r = 0; r < reduce; ++r) {
+        const float e = x[r * inner];
+        const float sq = e * e;
+        ss += sq;
+      }
+      const float scale = 1.0F / sqrtf(ss / static_cast<float>(reduce) + a.eps);
+      for (std::int64_t r = 0; r < reduce; ++r) {
+        float t = x[r * inner] * scale;
+        if (a.gamma) t = t * a.gamma[r];
+        out[r * inner] = t;
+      }
+    } else {
+      const float first = x[0];
+      float s = 0.F;
+      bool equal = true;
+      for (std::int64_t r = 0; r < reduce; ++r) {
+        const float e = x[r * inner];
+        s += e;
+        equal = equal && e == first;
+      }
+      if (equal && __builtin_isfinite(first)) {
+        const float fillv = a.eps == 0.F ? __builtin_nanf("") : 0.F;
+        for (std::int64_t r = 0; r < reduce; ++r) {
+          float t = fillv;
+          if (a.gamma) t = t * a.gamma[r];
+          if (a.beta) t = t + a.beta[r];
+          out[r * inner] = t;
+        }
+        continue;
+      }
+      const float mean = s / static_cast<float>(reduce);
+      float d2 = 0.F;
+      for (std::int64_t r = 0; r < reduce; ++r) {
+        const float d = x[r * inner] - mean;
+        d2 += d * d;
+      }
+      bool nan_row = false;
+      const float scale = finish_scale_ln(d2, reduce, a.eps, nan_row);
+      for (std::int64_t r = 0; r < reduce; ++r) {
+        float t = nan_row ? __builtin_nanf("") : (x[r * inner] - mean) * scale;
         if (a.gamma) t = t * a.gamma[r];
         if (a.beta) t = t + a.beta[r];
         out[r * inner] = t;
       }
-      return;
-    }
-    const float mean = s / static_cast<float>(reduce);
-    float d2 = 0.F;
-    for (std::int64_t r = 0; r < reduce; ++r) {
-      const float d = x[r * inner] - mean;
-      d2 += d * d;
-    }
-    bool nan_row = false;
-    const float scale = finish_scale_ln(d2, reduce, a.eps, nan_row);
-    for (std::int64_t r = 0; r < reduce; ++r) {
-      float t = nan_row ? __builtin_nanf("") : (x[r * inner] - mean) * scale;
-      if (a.gamma) t = t * a.gamma[r];
-      if (a.beta) t = t + a.beta[r];
-      out[r * inner] = t;
     }
   }
 }
@@ -655,7 +657,7 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
   if (status != TCX_OK) return status;
   if (inner != 1) {
     a.rows = outer * inner;
-    hipLaunchKernelGGL((row_lane_kernel<kOp>), dim3(grid_for(a.rows, 256, 0x7fffffff)), dim3(256), 0, s,
+    hipLaunchKernelGGL((row_lane_kernel<kOp>), dim3(grid_for(a.rows, 256, kStrideBlocks)), dim3(256), 0, s,
                        a, reduce, inner);
     return check(hipGetLastError(), "row lane kernel launch");
   }

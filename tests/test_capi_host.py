@@ -328,3 +328,15 @@ def test_backend_library_has_no_cpu_compute_fallback():
                           env={**os.environ, "LD_LIBRARY_PATH": ""}).stdout
     assert "libtensorcx_hip.so" in deps
     assert "oracle" not in deps and "tcxref" not in deps
+
+
+def test_launch_grids_fit_hip_work_item_count(tmp_path):
+    """The grid-stride launchers' grid arithmetic (launch_grid.hpp), compiled
+    on the host: no launch exceeds HIP's 32-bit work-item count for item counts
+    up to 2^62, and shapes below the cap keep a single pass."""
+    src = ROOT / "tests" / "cpp" / "launch_grid_test.cpp"
+    exe = tmp_path / "launch_grid_test"
+    subprocess.run(["g++", "-std=c++20", "-O1", "-Wall", "-Werror", f"-I{ROOT / 'tensor.cx_amd' / 'csrc'}",
+                    "-o", str(exe), str(src)], check=True)
+    done = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert done.returncode == 0, done.stdout + done.stderr
