@@ -172,7 +172,10 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
   if (tiles_128 >= 256 && tiles_128 * 10 >= (tiles_128 + 255) / 256 * 256 * 9)
     return launch_config<128, 128, 16, 32, 64, 2, false, 2>(args, trans_b, vec, s);
   const std::int64_t tiles_64 = ((d->m + 63) / 64) * ((d->n + 63) / 64) * batches;
-  if (tiles_64 < 128) return launch_config<32, 32, 32, 32, 32, 2, false, 8>(args, trans_b, vec, s);
+  if (tiles_64 < 128) {
+    if (vec && gemm::small_fits(d->m, d->n, d->k)) return gemm::launch_small(args, trans_b, s);
+    return launch_config<32, 32, 32, 32, 32, 2, false, 8>(args, trans_b, vec, s);
+  }
   // Up to three rounds of 64x64 tiles: the direct-to-LDS 64x64 kernel, edge
   // tiles included (1000^3: 30.0 -> 28.5 us, transposed 31.2 -> 28.1 us,
   // 768^3 23.4 -> 22.6 us). With more rounds the register-staged kernel

@@ -990,6 +990,203 @@ inline int launch_direct64(GemmArgs& args, bool trans_b, hipStream_t stream) {
   return check(hipGetLastError(), "gemm_f32 direct 64x64 launch");
 }
 
+// Small GEMMs (fewer than 128 output tiles of 64x64): one 32x32 output tile
+// per block of KS waves, the waves splitting K into KS contiguous runs of
+// 16-k chunks. A wave loads its own operands straight into registers (A and
+// a transposed B: one 16-byte load per lane, 16-row block and chunk; a
+// [k, n] B: four 8-byte loads per chunk, a lane's two columns adjacent), kG
+// chunks per load group and two groups in flight, so a K of up to 64 KS
+// takes one memory round trip, with no LDS staging and no barrier before the
+// epilogue. MFMA step q of chunk c takes k = 16 c + 4 (lane / 16) + q, as in
+// the other kernels. The partial tiles meet in LDS and are added in wave
+// order (a fixed order for a given KS), with bias and activation, by all KS
+// waves.
+//   Edges as in gemm_f32_direct64_kernel: buffer resources end at the
+// operand panels, so rows past M or N read zero; lanes past K, [k, n] B
+// columns past N and chunks past the wave's run take an out-of-range offset
+// (zero, no memory access), so every group issues the same loads.
+template <bool kTransB, int KS, int kG>
+__global__ __launch_bounds__(64 * KS) void gemm_f32_small_kernel(GemmArgs a) {
+  const std::int64_t per_batch = a.tiles_m * a.tiles_n;
+  const std::int64_t grid = a.total_tiles;
+  const std::int64_t bid = blockIdx.x;
+  // Consecutive tiles per XCD (launch id L runs on XCD L % 8), grouped eight
+  // tile rows deep, so an XCD's blocks share A and B panels in its L2.
+  const std::int64_t tile = grid % 8 == 0 ? (bid % 8) * (grid / 8) + bid / 8 : bid;
+  const std::int64_t batch = tile / per_batch, t = tile % per_batch;
+  constexpr std::int64_t kGroupM = 8;
+  const std::int64_t group_tiles = kGroupM * a.tiles_n;
+  const std::int64_t first_m = (t / group_tiles) * kGroupM;
+  const std::int64_t gm = min(a.tiles_m - first_m, kGroupM);
+  const std::int64_t tm = first_m + (t % group_tiles) % gm;
+  const std::int64_t tn = (t % group_tiles) / gm;
+  std::int64_t lhs_off = 0, rhs_off = 0;
+  {
+    std::int64_t b = batch;
+    for (int ax = a.batch_rank - 1; ax >= 0; --ax) {
+      const std::int64_t e = a.batch_shape[ax];
+      const std::int64_t c = b % e;
+      b /= e;
+      lhs_off += c * a.lhs_bs[ax];
+      rhs_off += c * a.rhs_bs[ax];
+    }
+  }
+  const std::int64_t M = a.m, N = a.n, K = a.k;
+  const std::int64_t m0 = tm * 32, n0 = tn * 32;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, kl = lane >> 4;
+  auto rsrc_of = [](const float* base, std::int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
+  };
+  // The launcher checks that every panel spans less than 2^31 bytes.
+  const auto a_rsrc = rsrc_of(a.lhs + lhs_off + m0 * K, (M - m0) * K * 4);
+  const auto b_rsrc = kTransB ? rsrc_of(a.rhs + rhs_off + n0 * K, (N - n0) * K * 4)
+                              : rsrc_of(a.rhs + rhs_off + n0, (K * N - n0) * 4);
+  constexpr int kOut = 0x7fffffff;
+  const int Ki = static_cast<int>(K), Ni = static_cast<int>(N);
+  // This wave's chunks: [c_begin, c_end), at least one when KS <= chunks.
+  const int chunks = (Ki + 15) / 16;
+  const int c_begin = wave * chunks / KS, c_end = (wave + 1) * chunks / KS;
+  const bool b_col_in = n0 + 2 * r < N;
+
+  struct Frag {
+    float4_t a[2], b[2];
+  };
+  auto load = [&](int c, Frag& f) {
+    const int k = 16 * c + 4 * kl;
+    const bool k_in = c < c_end && k < Ki;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      f.a[i] = __builtin_bit_cast(
+          float4_t, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, k_in ? ((16 * i + r) * Ki + k) * 4 : kOut, 0, 0));
+    if constexpr (kTransB) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        f.b[j] = __builtin_bit_cast(
+            float4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, k_in ? ((16 * j + r) * Ki + k) * 4 : kOut, 0, 0));
+    } else {
+      using float2v = float __attribute__((ext_vector_type(2)));
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const bool in = c < c_end && k + q < Ki && b_col_in;
+        const float2v v = __builtin_bit_cast(
+            float2v, __builtin_amdgcn_raw_buffer_load_b64(b_rsrc, in ? ((k + q) * Ni + 2 * r) * 4 : kOut, 0, 0));
+        f.b[0][q] = v.x;
+        f.b[1][q] = v.y;
+      }
+    }
+  };
+  floatx4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.F, 0.F, 0.F, 0.F};
+  auto mma = [&](const Frag& f) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[i][q], f.b[j][q], acc[i][j], 0, 0, 0);
+  };
+  // Load groups of kG chunks, two in flight; a chunk's MFMAs run only when it
+  // is in this wave's run (zero-filled chunks past it are loaded, not used).
+  Frag f0[kG], f1[kG];
+  auto load_group = [&](int c0, Frag (&f)[kG]) {
+#pragma unroll
+    for (int u = 0; u < kG; ++u) load(c0 + u, f[u]);
+  };
+  auto mma_group = [&](int c0, const Frag (&f)[kG]) {
+#pragma unroll
+    for (int u = 0; u < kG; ++u)
+      if (c0 + u < c_end) mma(f[u]);
+  };
+  load_group(c_begin, f0);
+  for (int c0 = c_begin; c0 < c_end; c0 += 2 * kG) {
+    load_group(c0 + kG, f1);
+    mma_group(c0, f0);
+    load_group(c0 + 2 * kG, f0);
+    if (c0 + kG < c_end) mma_group(c0 + kG, f1);
+  }
+
+  // Output (i, j, q) of lane (r, kl): row 16 i + 4 kl + q, column 16 j + r
+  // (transposed B) or 2 r + j ([k, n] B) of the tile.
+  auto store = [&](int i, int j, int q, float x) {
+    const std::int64_t row = m0 + 16 * i + 4 * kl + q;
+    const std::int64_t col = n0 + (kTransB ? 16 * j + r : 2 * r + j);
+    if (row >= M || col >= N) return;
+    if (a.bias != nullptr) x = x + a.bias[col];
+    a.out[batch * M * N + row * N + col] = activate(x, a.activation);
+  };
+  if constexpr (KS == 1) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) store(i, j, q, acc[i][j][q]);
+  } else {
+    __shared__ float red[KS][16][64];  // partial (i, j, q) of each wave, per lane
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) red[wave][(i * 2 + j) * 4 + q][lane] = acc[i][j][q];
+    __syncthreads();
+    // Wave w adds and stores outputs e = w, w + KS, ... of the 16 per lane.
+    for (int e = wave; e < 16; e += KS) {
+      float x = red[0][e][lane];
+#pragma unroll
+      for (int w = 1; w < KS; ++w) x += red[w][e][lane];
+      store(e / 8, (e / 4) % 2, e % 4, x);
+    }
+  }
+}
+
+// True when gemm_f32_small_kernel can take the problem: 16-byte rows and
+// every byte offset into a panel below 2^31 (rows of a 32-row tile included).
+inline bool small_fits(std::int64_t m, std::int64_t n, std::int64_t k) {
+  constexpr double kLimit = 2147483647.0;
+  const double rows_m = static_cast<double>(m < 32 ? 32 : m), rows_n = static_cast<double>(n < 32 ? 32 : n);
+  return m > 0 && n > 0 && k > 0 && k % 4 == 0 && n % 4 == 0 && rows_m * k * 4 < kLimit &&
+         rows_n * k * 4 < kLimit && (static_cast<double>(k) + 16) * n * 4 < kLimit;
+}
+
+template <bool kTransB, int KS>
+void launch_small_as(GemmArgs& args, hipStream_t stream) {
+  // Two groups of four chunks in flight (160 VGPRs) up to two waves per SIMD
+  // (KS <= 8); two chunks per group at 16 waves per block.
+  constexpr int kG = KS <= 8 ? 4 : 2;
+  hipLaunchKernelGGL((gemm_f32_small_kernel<kTransB, KS, kG>), dim3(static_cast<unsigned>(args.total_tiles)),
+                     dim3(64 * KS), 0, stream, args);
+}
+
+// KS: enough waves for about sixteen per CU over the launch (512^3: 8.4
+// against 9.5 us with eight), at most one per 16-k chunk and at most 16.
+inline int launch_small(GemmArgs& args, bool trans_b, hipStream_t stream) {
+  if (!small_fits(args.m, args.n, args.k))
+    return fail(TCX_INTERNAL, "small gemm needs 16-byte rows and 31-bit panel offsets");
+  args.tiles_m = (args.m + 31) / 32;
+  args.tiles_n = (args.n + 31) / 32;
+  args.total_tiles = args.tiles_m * args.tiles_n * args.total_tiles;  // caller passes the batch count
+  if (args.total_tiles > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
+  const std::int64_t chunks = (args.k + 15) / 16;
+  int ks = 1;
+  while (ks < 16 && ks * 2 <= chunks && args.total_tiles * ks < 4096) ks *= 2;
+  switch (ks) {
+    case 1: trans_b ? launch_small_as<true, 1>(args, stream) : launch_small_as<false, 1>(args, stream); break;
+    case 2: trans_b ? launch_small_as<true, 2>(args, stream) : launch_small_as<false, 2>(args, stream); break;
+    case 4: trans_b ? launch_small_as<true, 4>(args, stream) : launch_small_as<false, 4>(args, stream); break;
+    case 8: trans_b ? launch_small_as<true, 8>(args, stream) : launch_small_as<false, 8>(args, stream); break;
+    default: trans_b ? launch_small_as<true, 16>(args, stream) : launch_small_as<false, 16>(args, stream); break;
+  }
+  return check(hipGetLastError(), "gemm_f32 small launch");
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int kMinWaves, bool kVecOnly = false, int KS = 1>
 int launch_config(GemmArgs& args, bool trans_b, bool vec, hipStream_t stream) {
   args.tiles_m = (args.m + BM - 1) / BM;

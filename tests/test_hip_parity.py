@@ -124,6 +124,84 @@ def test_matmul_direct64_batched(cx, sa, sb):
     assert_matmul(actual, a.astype(np.float64) @ b.astype(np.float64), a, b, f"direct64 {sa}x{sb}")
 
 
+# Shapes of fewer than 128 output tiles of 64x64 with 16-byte rows run the
+# register-direct small kernel: 32x32 tiles, the K split over 1 to 16 waves
+# (one 16-k chunk per wave at least), edges through buffer range checks.
+@pytest.mark.parametrize("sa,sb", [((1, 4), (4, 4)), ((31, 4), (4, 36)), ((33, 20), (20, 36)),
+                                   ((100, 300), (300, 200)), ((64, 4096), (4096, 64)), ((2, 3, 60), (60, 40)),
+                                   ((7, 33, 68), (68, 12)), ((500, 600), (600, 400)), ((512, 512), (512, 512)),
+                                   ((3, 1, 40, 36), (1, 5, 36, 44)), ((256, 2048), (2048, 512))])
+def test_matmul_small_kernel(cx, sa, sb):
+    rng = np.random.default_rng(21)
+    a = rng.standard_normal(sa).astype(np.float32)
+    b = rng.standard_normal(sb).astype(np.float32)
+    actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    assert_matmul(actual, np.matmul(a.astype(np.float64), b.astype(np.float64)), a, b, f"small {sa}x{sb}")
+
+
+def test_matmul_small_kernel_k_tail_isolation(cx):
+    # K = 60: each row's last 16-k chunk spans k 48..63, and k 60..63 of a
+    # [k, n] B are the next batch's rows 0..3, of an A row the next row's
+    # first four values. Infinities there must read as zero (not 0 * inf) and
+    # still reach their own outputs as the float64 sums give them.
+    rng = np.random.default_rng(22)
+    a = rng.standard_normal((2, 40, 60)).astype(np.float32)
+    b = rng.standard_normal((2, 60, 36)).astype(np.float32)
+    b[1, 0:4, :] = np.inf
+    b[1, 2, 5] = -np.inf
+    a[0, 7, 0:4] = np.inf  # row 6's tail would read these
+    actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    with np.errstate(invalid="ignore"):
+        truth = np.matmul(a.astype(np.float64), b.astype(np.float64))
+    assert np.all(np.isfinite(np.delete(actual[0], 7, axis=0)))
+    assert np.array_equal(np.isnan(actual), np.isnan(truth))
+    assert np.array_equal(np.isinf(actual), np.isinf(truth))
+    keep = np.setdiff1d(np.arange(40), [7])
+    assert_matmul(actual[0][keep], truth[0][keep], a[0][keep], b[0], "small batch 0")
+    # Transposed B (a linear's weight [n, k]): the next weight row's start.
+    w = rng.standard_normal((36, 60)).astype(np.float32)
+    w[5, 0:4] = np.inf
+    x = a[1]
+    lin = cx.linear(cx.tensor(x, device="hip"), cx.tensor(w, device="hip")).numpy()
+    with np.errstate(invalid="ignore"):
+        lt = x.astype(np.float64) @ w.astype(np.float64).T
+    assert np.all(np.isfinite(lin[:, 4])) and np.array_equal(np.isinf(lin[:, 5]), np.isinf(lt[:, 5]))
+    assert_matmul(lin[:, :5], lt[:, :5], x, w[:5].T, "small linear finite columns")
+
+
+@pytest.mark.parametrize("k", [4, 16, 28, 64, 132, 1024, 4100])
+def test_linear_small_kernel_bias_activation(cx, k):
+    # Every K split width (1 to 16 waves), a transposed B, and the fused bias
+    # and SiLU / GELU epilogue split over the block's waves.
+    rng = np.random.default_rng(23 + k)
+    x = rng.standard_normal((70, k)).astype(np.float32)
+    w = rng.standard_normal((52, k)).astype(np.float32)
+    bias = rng.standard_normal(52).astype(np.float32)
+    xh, wh, bh = (cx.tensor(v, device="hip") for v in (x, w, bias))
+    exact = x.astype(np.float64) @ w.astype(np.float64).T
+    assert_matmul(cx.linear(xh, wh, bh).numpy(), exact + bias, x, w.T, f"small linear k={k}")
+    z = exact + bias
+    bound = 1.1e-4 * np.sqrt(k) * np.sqrt(np.mean(x * x)) * np.sqrt(np.mean(w * w)) + 1e-6
+    silu = cx.hip.linear_act(xh, wh, bh, "silu").numpy()
+    assert np.max(np.abs(silu - z / (1.0 + np.exp(-z)))) <= bound
+    gelu = cx.hip.linear_act(xh, wh, bh, "gelu").numpy()
+    expected = 0.5 * z * (1.0 + np.tanh(0.7978845608028654 * (z + 0.044715 * z ** 3)))
+    assert np.max(np.abs(gelu - expected)) <= bound
+
+
+def test_matmul_small_kernel_dyadic_exact(cx):
+    # Exact in any summation order: pins the small kernel's k mapping, tile
+    # placement and the wave-ordered combine bit for bit.
+    i = np.arange(96 * 200)
+    a = ((i % 11 - 5) / 8).astype(np.float32).reshape(96, 200)
+    j = np.arange(200 * 68)
+    b = ((j % 7 - 3) / 16).astype(np.float32).reshape(200, 68)
+    actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    assert_bits(actual, (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32), "small dyadic")
+    lin = cx.linear(cx.tensor(a, device="hip"), cx.tensor(np.ascontiguousarray(b.T), device="hip")).numpy()
+    assert_bits(lin, (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32), "small dyadic linear")
+
+
 @pytest.mark.parametrize("sa,sb", [((1024, 8192), (8192, 1024)), ((2048, 4096), (4096, 2048)),
                                    ((4, 512, 8192), (4, 8192, 512))])
 def test_matmul_split_k(cx, sa, sb):
