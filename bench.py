@@ -457,7 +457,8 @@ def main() -> int:
                      "peak": 157.3, "unit": "TFLOP/s", "frac": round(headline["frac"], 4),
                      "traffic": traffic, "kernel_avg_ms": round(headline["kernel_avg_ms"], 4),
                      "kernel_median_ms": round(headline["kernel_median_ms"], 4),
-                     "flop_per_launch": headline["flop_per_launch"]},
+                     "flop_per_launch": headline["flop_per_launch"],
+                     "warmup_launches": headline["warmup_launches"]},
         "cpu_baseline": cpu,
         "secondary": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
                       for r in secondary],
