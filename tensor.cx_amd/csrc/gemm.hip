@@ -180,7 +180,14 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
   // tiles included (1000^3: 30.0 -> 28.5 us, transposed 31.2 -> 28.1 us,
   // 768^3 23.4 -> 22.6 us). With more rounds the register-staged kernel
   // measured as fast or faster (3000x3000x1000: 203 against 212 us).
-  if (vec && tiles_64 <= 768 && gemm::direct64_fits(d->m, d->n, d->k))
+  if (vec && tiles_64 <= 768 && gemm::direct64_fits(d->m, d->n, d->k)) {
+    // Skinny shapes whose 64x64 tiles are mostly padding run the small
+    // kernel's 32x32 tiles when those waste at most two thirds as much
+    // (8192x4x1000: 23.0 -> 13.1 us, 4x8192x1000: 22.5 -> 10.5 us; 1000^3
+    // stays on 64x64 tiles, 24.2 against 33.8 us).
+    const std::int64_t tiles_32 = ((d->m + 31) / 32) * ((d->n + 31) / 32) * batches;
+    if (8 * tiles_64 > 3 * tiles_32 && gemm::small_fits(d->m, d->n, d->k)) return gemm::launch_small(args, trans_b, s);
     return gemm::launch_direct64(args, trans_b, s);
+  }
   return launch_config<64, 64, 16, 32, 32, 4, false, 4>(args, trans_b, vec, s);
 }

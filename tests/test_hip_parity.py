@@ -114,9 +114,10 @@ def test_matmul_direct64_kn_b_k_tail_isolation(cx):
                                    ((8192, 1000), (1000, 4)), ((4, 1000), (1000, 8192)),
                                    ((999, 1001), (1001, 1003))])
 def test_matmul_direct64_batched(cx, sa, sb):
-    # Batched and skinny 64x64-tile shapes (a 4-wide n or m: all but 4 rows or
-    # columns of each tile past the edge), and an unaligned k (1001) that
-    # takes the register-staged 64x64 tile instead.
+    # Batched 64x64-tile shapes, skinny shapes (a 4-wide n or m, which run
+    # the small kernel's 32x32 tiles: all but 4 rows or columns of each tile
+    # past the edge), and an unaligned k (1001) that takes the
+    # register-staged 64x64 tile instead.
     rng = np.random.default_rng(15)
     a = rng.standard_normal(sa).astype(np.float32)
     b = rng.standard_normal(sb).astype(np.float32)
