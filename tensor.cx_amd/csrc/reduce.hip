@@ -186,16 +186,25 @@ __device__ __forceinline__ Partial wave_reduce(const T* __restrict__ p, std::int
         nan_seen |= v != v;
       };
       int r = 0;
-      // Every lane's four groups are in range while r + 1024 <= len.
-      for (; r + 1024 <= len; r += 1024) {
-        const vec4<float> a = stream_load(reinterpret_cast<const vec4<float>*>(q + lane4 + r));
-        const vec4<float> b = stream_load(reinterpret_cast<const vec4<float>*>(q + lane4 + r + 256));
-        const vec4<float> c = stream_load(reinterpret_cast<const vec4<float>*>(q + lane4 + r + 512));
-        const vec4<float> d = stream_load(reinterpret_cast<const vec4<float>*>(q + lane4 + r + 768));
-        step(0, a.x, r); step(1, a.y, r); step(2, a.z, r); step(3, a.w, r);
-        step(0, b.x, r + 256); step(1, b.y, r + 256); step(2, b.z, r + 256); step(3, b.w, r + 256);
-        step(0, c.x, r + 512); step(1, c.y, r + 512); step(2, c.z, r + 512); step(3, c.w, r + 512);
-        step(0, d.x, r + 768); step(1, d.y, r + 768); step(2, d.z, r + 768); step(3, d.w, r + 768);
+      // Every lane's four groups are in range while r + 1024 <= len. The
+      // next four loads are issued before the current four are scanned.
+      auto scan4 = [&](const vec4<float>& a, const vec4<float>& b, const vec4<float>& c, const vec4<float>& d,
+                       int at) {
+        step(0, a.x, at); step(1, a.y, at); step(2, a.z, at); step(3, a.w, at);
+        step(0, b.x, at + 256); step(1, b.y, at + 256); step(2, b.z, at + 256); step(3, b.w, at + 256);
+        step(0, c.x, at + 512); step(1, c.y, at + 512); step(2, c.z, at + 512); step(3, c.w, at + 512);
+        step(0, d.x, at + 768); step(1, d.y, at + 768); step(2, d.z, at + 768); step(3, d.w, at + 768);
+      };
+      auto ld = [&](int at) { return stream_load(reinterpret_cast<const vec4<float>*>(q + lane4 + at)); };
+      if (len >= 1024) {
+        vec4<float> a = ld(0), b = ld(256), c = ld(512), d = ld(768);
+        for (; r + 2048 <= len; r += 1024) {
+          const vec4<float> a2 = ld(r + 1024), b2 = ld(r + 1280), c2 = ld(r + 1536), d2 = ld(r + 1792);
+          scan4(a, b, c, d, r);
+          a = a2; b = b2; c = c2; d = d2;
+        }
+        scan4(a, b, c, d, r);
+        r += 1024;
       }
       for (; r < len; r += 256) {
         if (lane4 + r < len) {
