@@ -56,12 +56,15 @@ def log(msg: str) -> None:
 WARM_MS = 20.0
 # Operand copies rotate until they exceed the 256 MB Infinity Cache.
 ROTATE_BYTES = 320 * 1024 * 1024
+# The per-launch median is taken over at least this many launches.
+MEDIAN_REPS = 31
 
 
 def timed(launch, steps: int, warmup: int, warm_ms: float = WARM_MS):
     """Runs `launch` warmup times, then (untimed) until warm_ms of GPU time has
     passed; then K = steps launches between two HIP events on the launch
-    stream (total), then K more with an event pair around each (per launch).
+    stream (total), then max(K, MEDIAN_REPS) more with an event pair around
+    each (per launch).
     The stream is idle on both sides of each pass. Returns (total_ms,
     per_launch_ms list, warm-up launches)."""
     s = capi.stream()
@@ -88,14 +91,15 @@ def timed(launch, steps: int, warmup: int, warm_ms: float = WARM_MS):
     stop.record(s)
     stop.synchronize()
     total = start.elapsed_ms(stop)
-    marks = [capi.Event() for _ in range(steps + 1)]
+    reps = max(steps, MEDIAN_REPS)
+    marks = [capi.Event() for _ in range(reps + 1)]
     marks[0].record(s)
-    for i in range(steps):
+    for i in range(reps):
         launch(s)
         marks[i + 1].record(s)
     marks[-1].synchronize()
     capi.synchronize()
-    per = [marks[i].elapsed_ms(marks[i + 1]) for i in range(steps)]
+    per = [marks[i].elapsed_ms(marks[i + 1]) for i in range(reps)]
     return total, per, launches
 
 
@@ -143,6 +147,29 @@ def bench_gemm(name: str, steps: int, warmup: int):
             "achieved": flops / (avg * 1e-3) / 1e12, "peak": PEAK_FP32_MFMA / 1e12,
             "frac": flops / (avg * 1e-3) / PEAK_FP32_MFMA, "flop_per_launch": flops,
             "ms_per_step": avg, "operand_copies": len(sets), "warmup_launches": warm}
+
+
+def api_wall(steps: int, warmup: int) -> dict:
+    """Wall time of tensorcx.matmul at 4096^3 through the whole drop-in path
+    (Python binding, HipBackend::execute, an output allocation from a
+    memory_pool scope, the kernel, the stream synchronisation that makes the
+    call complete on return), per call, after warm-up calls."""
+    import tensorcx as cx
+    a, b = wl.gemm_inputs("c2_4096")
+    ta, tb = cx.tensor(a, device="hip"), cx.tensor(b, device="hip")
+    calls = max(steps, MEDIAN_REPS)
+    with cx.memory_pool("hip", max_cached_bytes=256 << 20):
+        for _ in range(max(warmup, 5)):
+            out = cx.matmul(ta, tb)
+        times = []
+        for _ in range(calls):
+            t = time.perf_counter()
+            out = cx.matmul(ta, tb)
+            times.append(time.perf_counter() - t)
+        del out
+    return {"path": "tensorcx.matmul -> HipBackend::execute (pooled output, synchronous)",
+            "calls": calls, "ms_per_call_median": statistics.median(times) * 1e3,
+            "ms_per_call_mean": statistics.mean(times) * 1e3}
 
 
 def bench_hbm(name: str, launch_for, nbytes: int, steps: int, warmup: int):
@@ -430,6 +457,8 @@ def main() -> int:
     headline = bench_gemm("c2_4096", args.steps, args.warmup)
     log(f"gemm 4096^3: {headline['achieved']:.1f} TFLOP/s ({headline['frac']:.1%} of fp32 MFMA peak), "
         f"median launch {headline['kernel_median_ms']:.4f} ms")
+    api = api_wall(args.steps, args.warmup)
+    log(f"gemm 4096^3 through tensorcx.matmul: {api['ms_per_call_median']:.4f} ms per call (median)")
     secondary = [] if args.headline_only else secondary_benches(args.steps, args.warmup, args.only,
                                                                   not args.no_cpu)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
@@ -459,6 +488,7 @@ def main() -> int:
                      "kernel_median_ms": round(headline["kernel_median_ms"], 4),
                      "flop_per_launch": headline["flop_per_launch"],
                      "warmup_launches": headline["warmup_launches"]},
+        "api_wall": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in api.items()},
         "cpu_baseline": cpu,
         "secondary": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
                       for r in secondary],
