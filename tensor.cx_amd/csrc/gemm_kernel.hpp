@@ -906,13 +906,29 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8))) vo
   // Each wave has two loads per tile in flight.
   const int k_tiles = static_cast<int>((K + BKT - 1) / BKT);
   for (int p = 0; p < kStages && p < k_tiles; ++p) issue(p, p * BKT);
-  // Tiles 0 and 1 have landed: vmcnt(4) with four tiles in flight, vmcnt(2)
-  // with three.
-  if (k_tiles > 3) __builtin_amdgcn_s_waitcnt(0x0F74);
-  else if (k_tiles == 3) __builtin_amdgcn_s_waitcnt(0x0F72);
-  else __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  for (int kt = 0; kt < k_tiles; kt += 2) {
+  int kt0 = 0;
+  if (k_tiles >= 4) {
+    // The first pair starts as soon as tile 0 has landed; tile 1 lands
+    // under tile 0's MFMAs, tiles 2 and 3 under tile 1's (one barrier more;
+    // 1000^3 24.2 -> 24.0 us, 1024^3 23.5 -> 23.1 us).
+    __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6): tile 0
+    __syncthreads();
+    compute(0);
+    __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4): tile 1
+    __syncthreads();
+    compute(1);
+    __builtin_amdgcn_s_waitcnt(0);  // tiles 2 and 3
+    __syncthreads();
+    kt0 = 2;
+  } else {
+    // Tiles 0 and 1 have landed: vmcnt(4) with four tiles in flight, vmcnt(2)
+    // with three.
+    if (k_tiles > 3) __builtin_amdgcn_s_waitcnt(0x0F74);
+    else if (k_tiles == 3) __builtin_amdgcn_s_waitcnt(0x0F72);
+    else __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  for (int kt = kt0; kt < k_tiles; kt += 2) {
     if (kt >= 2 && kt + 2 < k_tiles) issue((kt + 2) % kStages, (kt + 2) * BKT);
     if (kt >= 2 && kt + 3 < k_tiles) issue((kt + 3) % kStages, (kt + 3) * BKT);
     compute(kt % kStages);
