@@ -42,9 +42,10 @@ const char* tcx_hip_last_error(void);
 
 /* Initialises the HIP runtime once per process and checks for a device.
  * Replaces cuda::available() (reference backends/cuda/cuda_backend.h:37;
- * cuda_backend.cpp:166-169). Returns TCX_UNAVAILABLE without a device and in a
- * forked child of a process that initialised the runtime
- * (cf. cuda_context.cpp:16-20). */
+ * cuda_backend.cpp:166-169). Returns TCX_UNAVAILABLE without a device, and in
+ * any process forked from the one that loaded the library, before any HIP
+ * call there (cf. cuda_context.cpp:16-20). Every entry point that reaches the
+ * runtime checks this first. */
 int tcx_hip_init(void);
 int tcx_hip_device_count(int* count);
 

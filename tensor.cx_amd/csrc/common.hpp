@@ -18,6 +18,10 @@ int fail(int code, std::string message);
 int check(hipError_t error, const char* what);
 // Validates a launch on this thread (runtime ready, not in a forked child).
 int ready();
+// True in a process forked from the one that loaded the library; every entry
+// point that reaches the HIP runtime refuses to run there.
+bool forked();
+int refuse_forked();
 
 constexpr int kWave = 64;
 

@@ -19,7 +19,11 @@ thread_local std::string last_error;
 std::once_flag init_once;
 int init_status = TCX_UNAVAILABLE;
 std::string init_message;
-pid_t init_pid = 0;
+// The process that loaded the library. A forked child inherits the parent's
+// runtime state without its threads or device contexts, so every entry point
+// refuses to run there, before any HIP call (the reference's CUDA backend
+// refuses the same way, cuda_context.cpp:16-20).
+const pid_t load_pid = getpid();
 thread_local hipStream_t thread_stream = nullptr;
 }  // namespace
 
@@ -45,13 +49,11 @@ int check(hipError_t error, const char* what) {
   }
 }
 
-int ready() {
-  const int status = tcx_hip_init();
-  if (status != TCX_OK) return status;
-  if (getpid() != init_pid)
-    return fail(TCX_UNAVAILABLE, "HIP runtime is unavailable in a forked child process");
-  return TCX_OK;
-}
+bool forked() { return getpid() != load_pid; }
+
+int refuse_forked() { return fail(TCX_UNAVAILABLE, "HIP requires a fresh process after fork"); }
+
+int ready() { return tcx_hip_init(); }
 
 }  // namespace tcx
 
@@ -70,6 +72,7 @@ namespace {
 thread_local tcx_hip_pool* active_pool = nullptr;
 
 int hip_allocate(void** ptr, size_t bytes) {
+  if (tcx::forked()) return tcx::refuse_forked();
   const hipError_t error = hipMalloc(ptr, bytes);
   if (error == hipErrorOutOfMemory) {
     tcx::set_error("hipMalloc: out of memory");
@@ -77,8 +80,9 @@ int hip_allocate(void** ptr, size_t bytes) {
   }
   return tcx::check(error, "hipMalloc");
 }
-int hip_free(void* ptr) { return tcx::check(hipFree(ptr), "hipFree"); }
+int hip_free(void* ptr) { return tcx::forked() ? tcx::refuse_forked() : tcx::check(hipFree(ptr), "hipFree"); }
 int hip_clear_error() {
+  if (tcx::forked()) return tcx::refuse_forked();
   const hipError_t error = hipGetLastError();
   if (error == hipErrorOutOfMemory) return TCX_POOL_OOM;
   return tcx::check(error, "pending HIP error");
@@ -188,6 +192,7 @@ extern "C" {
 const char* tcx_hip_last_error(void) { return tcx::last_error.c_str(); }
 
 int tcx_hip_init(void) {
+  if (tcx::forked()) return tcx::refuse_forked();
   std::call_once(tcx::init_once, [] {
     hipError_t error = hipInit(0);
     int count = 0;
@@ -201,7 +206,6 @@ int tcx_hip_init(void) {
       tcx::init_message = "no HIP device is visible";
     } else {
       tcx::init_status = TCX_OK;
-      tcx::init_pid = getpid();
     }
   });
   if (tcx::init_status != TCX_OK) return tcx::fail(tcx::init_status, tcx::init_message);
@@ -255,6 +259,7 @@ int tcx_hip_stream(tcx_stream_t* stream) {
 }
 
 int tcx_hip_stream_synchronize(tcx_stream_t stream) {
+  if (tcx::forked()) return tcx::refuse_forked();
   return tcx::check(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "hipStreamSynchronize");
 }
 
@@ -273,7 +278,7 @@ int tcx_hip_allocate(size_t bytes, void** ptr, tcx_hip_pool_t** owner) {
 }
 
 void tcx_hip_release(void* ptr, size_t bytes, tcx_hip_pool_t* owner) {
-  if (ptr == nullptr) return;
+  if (ptr == nullptr || tcx::forked()) return;  // a child does not own the parent's memory
   if (owner != nullptr) {
     pool_release(owner, ptr, bytes, true);
     return;
@@ -282,7 +287,7 @@ void tcx_hip_release(void* ptr, size_t bytes, tcx_hip_pool_t* owner) {
 }
 
 void tcx_hip_release_uncached(void* ptr, size_t bytes, tcx_hip_pool_t* owner) {
-  if (ptr == nullptr) return;
+  if (ptr == nullptr || tcx::forked()) return;
   if (owner != nullptr) {
     pool_release(owner, ptr, bytes, false);
     return;
@@ -415,17 +420,21 @@ int tcx_hip_event_create(void** event) {
   return rc;
 }
 int tcx_hip_event_record(void* event, tcx_stream_t stream) {
+  if (tcx::forked()) return tcx::refuse_forked();
   return tcx::check(hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream)),
                     "hipEventRecord");
 }
 int tcx_hip_event_synchronize(void* event) {
+  if (tcx::forked()) return tcx::refuse_forked();
   return tcx::check(hipEventSynchronize(static_cast<hipEvent_t>(event)), "hipEventSynchronize");
 }
 int tcx_hip_event_elapsed_ms(void* start, void* stop, float* ms) {
+  if (tcx::forked()) return tcx::refuse_forked();
   return tcx::check(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)),
                     "hipEventElapsedTime");
 }
 int tcx_hip_event_destroy(void* event) {
+  if (tcx::forked()) return tcx::refuse_forked();
   return tcx::check(hipEventDestroy(static_cast<hipEvent_t>(event)), "hipEventDestroy");
 }
 

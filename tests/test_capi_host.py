@@ -340,3 +340,29 @@ def test_launch_grids_fit_hip_work_item_count(tmp_path):
                     "-o", str(exe), str(src)], check=True)
     done = subprocess.run([str(exe)], capture_output=True, text=True)
     assert done.returncode == 0, done.stdout + done.stderr
+
+
+def test_forked_child_is_refused_before_any_hip_call():
+    """A process forked from the one that loaded the library gets
+    TCX_UNAVAILABLE from every entry point that reaches the HIP runtime, with
+    the reference's message and before any HIP call (cf. the reference's
+    cuda_context.cpp:16-20): init, device queries, stream and event calls."""
+    lib = capi.lib()
+    read_end, write_end = os.pipe()
+    pid = os.fork()
+    if pid == 0:  # child: report the codes through the pipe, then leave at once
+        try:
+            os.close(read_end)
+            count = ctypes.c_int(-1)
+            codes = [lib.tcx_hip_init(), lib.tcx_hip_device_count(ctypes.byref(count)),
+                     lib.tcx_hip_stream_synchronize(None), lib.tcx_hip_event_destroy(None)]
+            os.write(write_end, (",".join(map(str, codes)) + "|" + capi.last_error()).encode())
+        finally:
+            os._exit(0)
+    os.close(write_end)
+    with os.fdopen(read_end) as pipe:
+        report = pipe.read()
+    os.waitpid(pid, 0)
+    codes, message = report.split("|", 1)
+    assert [int(c) for c in codes.split(",")] == [capi.TCX_UNAVAILABLE] * 4
+    assert message == "HIP requires a fresh process after fork"
