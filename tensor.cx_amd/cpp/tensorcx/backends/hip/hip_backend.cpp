@@ -3,6 +3,7 @@
 // slot it fills; semantics follow the CPU reference, cpu_backend.cpp).
 
 #include "tensorcx/backends/hip/hip_backend.h"
+#include "tensorcx/backends/hip/hip_device_interval.h"
 
 #include "tensorcx/core/predicate.h"
 #include "tensorcx/core/profiling.h"
@@ -1256,61 +1257,6 @@ Expected<void*> export_storage(const Tensor& tensor) {
   }
 }
 
-namespace {
-
-// One device interval per executed operation: HIP events recorded on the
-// execution stream before the first and after the last launch, read after the
-// synchronising wait that ends every execute (the reference's DeviceTimer
-// pattern, backends/cuda/cuda_profiling.h:22-77).
-class DeviceInterval {
- public:
-  DeviceInterval(const char* name, Stream& stream) noexcept : token_(reserve_device_profile(name, "hip")) {
-    if (!token_) return;
-    tcx_stream_t s = nullptr;
-    try {
-      s = stream;
-    } catch (const std::exception&) {
-      error_ = "event_failed";
-      return;
-    }
-    if (tcx_hip_event_create(&start_) != TCX_OK || tcx_hip_event_create(&stop_) != TCX_OK ||
-        tcx_hip_event_record(start_, s) != TCX_OK)
-      error_ = "event_failed";
-  }
-  void stop(Stream& stream) noexcept {
-    if (token_ && !error_) {
-      try {
-        if (tcx_hip_event_record(stop_, stream) != TCX_OK) error_ = "event_failed";
-      } catch (const std::exception&) {
-        error_ = "event_failed";
-      }
-    }
-    stopped_ = true;
-  }
-  ~DeviceInterval() {
-    if (token_) {
-      float ms = 0.F;
-      const char* error = error_ ? error_ : !stopped_ ? "launch_failed" : nullptr;
-      if (!error && (tcx_hip_event_synchronize(stop_) != TCX_OK || tcx_hip_event_elapsed_ms(start_, stop_, &ms) != TCX_OK))
-        error = "event_failed";
-      finish_device_profile(token_, error ? std::nullopt : std::optional<float>(ms), error);
-    }
-    if (start_) tcx_hip_event_destroy(start_);
-    if (stop_) tcx_hip_event_destroy(stop_);
-  }
-  DeviceInterval(const DeviceInterval&) = delete;
-  DeviceInterval& operator=(const DeviceInterval&) = delete;
-
- private:
-  DeviceProfileToken token_;
-  void* start_{};
-  void* stop_{};
-  const char* error_{};
-  bool stopped_{};
-};
-
-}  // namespace
-
 Status HipBackend::execute(const BackendExecution& e) {
   ProfileScope dispatch(ProfileCategory::kDispatch, "execute", "hip", std::nullopt,
                         e.op_class == BackendOpClass::kPrimitive ? std::optional<OpKind>(e.op.kind) : std::nullopt);
@@ -1323,7 +1269,16 @@ Status HipBackend::execute(const BackendExecution& e) {
     if (e.op.kind != OpKind::kFill)
       for (const Tensor& t : e.inputs) (void)device_ptr(t);
     Stream s;
-    DeviceInterval interval("hip_kernels", s);
+    DeviceInterval<> interval("hip_kernels");
+    auto interval_at = [&](auto mark) noexcept {
+      if (!interval.active()) return;
+      try {
+        mark(static_cast<tcx_stream_t>(s));
+      } catch (const std::exception&) {
+        interval.fail();
+      }
+    };
+    interval_at([&](tcx_stream_t stream) { interval.start(stream); });
     Tensor result;
     switch (e.op.kind) {
       case OpKind::kFill: result = fill(e.outputs[0], e.op.scalar_value, s); break;
@@ -1352,7 +1307,7 @@ Status HipBackend::execute(const BackendExecution& e) {
       case OpKind::kClip: result = clip(e.inputs, s); break;
       case OpKind::kTopK: {
         auto [values, indices] = topk(e.op, e.inputs[0], s);
-        interval.stop(s);
+        interval_at([&](tcx_stream_t stream) { interval.stop(stream); });
         if (s.used()) synchronize(s);
         e.outputs[0] = std::move(values);
         e.outputs[1] = std::move(indices);
@@ -1390,7 +1345,7 @@ Status HipBackend::execute(const BackendExecution& e) {
       default:
         return Status(StatusCode::kInvalidArgument, "unsupported HIP backend execution operation");
     }
-    interval.stop(s);
+    interval_at([&](tcx_stream_t stream) { interval.stop(stream); });
     if (s.used()) synchronize(s);  // nothing to wait for when nothing was launched
     e.outputs[0] = std::move(result);  // publish only after the work completed
     return Status::Ok();

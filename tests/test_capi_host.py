@@ -313,8 +313,8 @@ def test_hip_backend_compiles_against_reference_core_headers():
     src = ROOT / "tensor.cx_amd" / "cpp" / "tensorcx" / "backends" / "hip" / "hip_backend.cpp"
     shadow = ROOT / "tensor.cx_amd" / "_build" / "conformance"
     (shadow / "tensorcx" / "backends" / "hip").mkdir(parents=True, exist_ok=True)
-    header = shadow / "tensorcx" / "backends" / "hip" / "hip_backend.h"
-    header.write_text((src.parent / "hip_backend.h").read_text())
+    for name in ("hip_backend.h", "hip_device_interval.h"):
+        (shadow / "tensorcx" / "backends" / "hip" / name).write_text((src.parent / name).read_text())
     subprocess.run(["g++", "-std=c++20", "-fsyntax-only", "-Wall", f"-I{shadow}",
                     f"-I{REFERENCE_CPP}", f"-I{ROOT / 'include'}", str(src)], check=True)
 
@@ -366,3 +366,18 @@ def test_forked_child_is_refused_before_any_hip_call():
     codes, message = report.split("|", 1)
     assert [int(c) for c in codes.split(",")] == [capi.TCX_UNAVAILABLE] * 4
     assert message == "HIP requires a fresh process after fork"
+
+
+def test_device_interval_event_seam(tmp_path):
+    """HipBackend's device intervals through their event seam: a scripted
+    event API fails at every step in turn (the reference's fake-Events test of
+    DeviceTimer, test_cuda_profile.cpp:22-59), checked against the profile
+    session's device event and the event bookkeeping."""
+    obj = ROOT / "tensor.cx_amd" / "_build" / "cxx_cpp_tensorcx_core_profiling.o"
+    assert obj.exists(), "build() compiles the core objects first"
+    exe = tmp_path / "device_interval_test"
+    subprocess.run(["g++", "-std=c++20", "-O1", "-Wall", "-Werror", f"-I{ROOT / 'tensor.cx_amd' / 'cpp'}",
+                    f"-I{ROOT / 'include'}", "-o", str(exe), str(ROOT / "tests" / "cpp" / "device_interval_test.cpp"),
+                    str(obj), "-pthread"], check=True)
+    done = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert done.returncode == 0, done.stdout + done.stderr
