@@ -131,13 +131,23 @@ def test_matmul_direct64_batched(cx, sa, sb):
 @pytest.mark.parametrize("sa,sb", [((1, 4), (4, 4)), ((31, 4), (4, 36)), ((33, 20), (20, 36)),
                                    ((100, 300), (300, 200)), ((64, 4096), (4096, 64)), ((2, 3, 60), (60, 40)),
                                    ((7, 33, 68), (68, 12)), ((500, 600), (600, 400)), ((512, 512), (512, 512)),
-                                   ((3, 1, 40, 36), (1, 5, 36, 44)), ((256, 2048), (2048, 512))])
+                                   ((3, 1, 40, 36), (1, 5, 36, 44)), ((256, 2048), (2048, 512)),
+                                   ((16384, 512), (512, 4)), ((4, 1000), (1000, 16384))])
 def test_matmul_small_kernel(cx, sa, sb):
     rng = np.random.default_rng(21)
     a = rng.standard_normal(sa).astype(np.float32)
     b = rng.standard_normal(sb).astype(np.float32)
     actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
     assert_matmul(actual, np.matmul(a.astype(np.float64), b.astype(np.float64)), a, b, f"small {sa}x{sb}")
+
+
+def test_linear_small_kernel_skinny(cx):
+    # 512 output tiles of 32x32 (eight waves per tile) for a transposed B.
+    rng = np.random.default_rng(24)
+    x = rng.standard_normal((16384, 512)).astype(np.float32)
+    w = rng.standard_normal((4, 512)).astype(np.float32)
+    actual = cx.linear(cx.tensor(x, device="hip"), cx.tensor(w, device="hip")).numpy()
+    assert_matmul(actual, x.astype(np.float64) @ w.astype(np.float64).T, x, w.T, "small linear skinny")
 
 
 def test_matmul_small_kernel_k_tail_isolation(cx):
