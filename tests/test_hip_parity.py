@@ -150,6 +150,35 @@ def test_linear_small_kernel_skinny(cx):
     assert_matmul(actual, x.astype(np.float64) @ w.astype(np.float64).T, x, w.T, "small linear skinny")
 
 
+def test_matmul_random_shapes_every_route(cx):
+    # Seeded random shapes across every GEMM route (small 32x32 tiles, the
+    # skinny route, 64x64 direct and register-staged tiles, aligned and
+    # unaligned rows, transposed B, batches with broadcast), each against
+    # float64 truth at the matmul bar.
+    rng = np.random.default_rng(25)
+    failures = []
+    for case in range(96):
+        m, n, k = (int(v) for v in rng.integers(1, 700, 3))
+        if case % 3 == 0:  # 16-byte rows
+            n, k = 4 * ((n + 3) // 4), 4 * ((k + 3) // 4)
+        batch = int(rng.integers(1, 4)) if case % 4 == 1 else 0
+        linear = case % 5 == 2
+        a = rng.standard_normal(((batch,) if batch else ()) + (m, k)).astype(np.float32)
+        if linear:
+            w = rng.standard_normal((n, k)).astype(np.float32)
+            got = cx.linear(cx.tensor(a, device="hip"), cx.tensor(w, device="hip")).numpy()
+            b = w.T
+        else:
+            b = rng.standard_normal(((batch,) if batch and case % 8 == 1 else ()) + (k, n)).astype(np.float32)
+            got = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+        truth = np.matmul(a.astype(np.float64), b.astype(np.float64))
+        try:
+            assert_matmul(got, truth, a, b, f"case {case}: a {a.shape} b {b.shape} linear={linear}")
+        except AssertionError as error:
+            failures.append(str(error))
+    assert not failures, "\n".join(failures[:10])
+
+
 def test_matmul_small_kernel_k_tail_isolation(cx):
     # K = 60: each row's last 16-k chunk spans k 48..63, and k 60..63 of a
     # [k, n] B are the next batch's rows 0..3, of an A row the next row's
