@@ -19,12 +19,13 @@
 //                      taking items in turn; rows split into segments when
 //                      there are too few rows to fill the GPU (partials in
 //                      workspace)
-//   finish_kernel      combines per-row segment partials in segment order
+//   finish_kernel      combines per-row segment partials in a fixed order
 //   lane_kernel        one lane per output, reference element order
 //   axes_kernel        any axis selection through reduction-plan metadata
 
 #include <mutex>
 #include <string>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -32,7 +33,14 @@ namespace tcx {
 namespace {
 
 constexpr std::int64_t kSequentialMax = 64;   // rows up to this length keep exact order
-constexpr std::int64_t kTargetWaves = 8192;   // 32 waves per CU on 256 CUs
+// Segments a short-row reduction is split into (over all rows): one per wave
+// of the row path's persistent grid on 256 CUs (7 blocks of 4 waves per 4
+// CUs), so each wave streams one segment and the finish step folds few
+// partials. Measured against 8192 segments (4.6 per wave) on MI355X: the
+// 67 M-element full sum 75.6 -> 77.2 % of HBM peak, full max 66.1 -> 75.9 %,
+// int32 full max 72.1 -> 75.3 %, 2 x 33 M min 68.6 -> 76.2 %; 3584 segments
+// lost 7 points on 64 x 1 M max.
+constexpr std::int64_t kTargetSegments = 1792;
 constexpr std::int64_t kMinSegment = 4096;    // elements per segment when splitting rows
 
 // Partial result of one (row, segment) of an extremum search: (value bits,
@@ -71,6 +79,28 @@ __device__ __forceinline__ bool cand_better(T v, std::int64_t i, T best, std::in
     return better_f32<kLargest>(v, i, best, bi);
   else
     return better_i32<kLargest>(v, i, best, bi);
+}
+
+// Rank key of an extremum candidate's value bits: the larger key is the
+// better candidate, and equal keys go to the lower index, which is the order
+// cand_better defines. NaN ranks above every number (for min as for max), -0
+// and +0 share a key, other values map monotonically (the sign-flipped bit
+// pattern, inverted for min). An empty candidate is (key 0, kNoIndex): only
+// the int32 extreme (INT_MIN for max, INT_MAX for min) also has key 0, and it
+// wins on the index.
+constexpr std::int64_t kNoIndex = INT64_MAX;
+template <typename T, bool kLargest>
+__device__ __forceinline__ std::uint32_t rank_key(std::uint32_t bits) {
+  std::uint32_t o;
+  if constexpr (__is_same(T, float)) {
+    const std::uint32_t mag = bits & 0x7FFFFFFFU;
+    if (mag > 0x7F800000U) return 0xFFFFFFFFU;
+    if (mag == 0) bits = 0;
+    o = (bits & 0x80000000U) ? ~bits : bits | 0x80000000U;
+  } else {
+    o = bits ^ 0x80000000U;
+  }
+  return kLargest ? o : ~o;
 }
 
 template <typename T, bool kLargest>
@@ -320,111 +350,87 @@ __global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, 
   }
 }
 
-// One block of kThreads threads per row combines that row's segment
-// partials: thread t folds segments t, t + kThreads, ... in order (kUnroll
-// independent loads per step), then the waves and the block combine in a fixed
-// order, so the result is deterministic. Sum partials take 256 threads
-// (a full-tensor sum's 8192 in one round of 32 loads per thread); extremum
-// records take 1024 threads for rows of >= 2048 partials, 256 otherwise.
-// Every thread of the block calls it (it synchronises the block).
-template <int kOp, typename T, int kThreads>
-__device__ __forceinline__ void combine_row(const Partial* __restrict__ partials, void* __restrict__ out,
-                                            std::int64_t row, std::int64_t reduce, std::int64_t segments) {
-  constexpr int kWaves = kThreads / 64;
-  // Loads in flight per thread: all of a full-tensor sum's 8192 partials in
-  // one round (32 per thread at 256 threads, 8 at 1024).
-  constexpr int kUnroll = kThreads <= 256 ? 32 : 8192 / kThreads;
+// One block of kFinishThreads threads per row combines that row's segment
+// partials in a fixed order, so the result is deterministic: a sum's thread t
+// keeps kUnroll accumulators, accumulator u folding partials t + u * 256,
+// t + (u + kUnroll) * 256, ... (all kUnroll loads of a round in flight; one
+// round covers the 1792-segment full-tensor sum), then the accumulators, the
+// lanes and the waves combine pairwise. Extremum records fold on (rank key,
+// index) in a few selects per record, which keeps the kernel small: a
+// single-block kernel runs once per call, so its code is fetched cold, and
+// the former branchy fold (1210 instructions) took 9.2 us against 6.7 us for
+// this one (146).
+constexpr int kFinishThreads = 256;
+template <int kOp, typename T>
+__global__ __launch_bounds__(kFinishThreads) void finish_kernel(const Partial* __restrict__ partials,
+                                                                void* __restrict__ out, std::int64_t rows,
+                                                                std::int64_t reduce, std::int64_t segments) {
+  constexpr int kThreads = kFinishThreads, kWaves = kThreads / 64, kUnroll = 8;
+  if (static_cast<std::int64_t>(blockIdx.x) >= rows) return;
+  const std::int64_t row = blockIdx.x;
   __shared__ Partial waves[kWaves];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const Partial* p = partials + row * segments;
   constexpr bool kSum = kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN;
   constexpr bool kLargest = kOp != TCX_REDUCE_MIN;
   if constexpr (kSum) {
-    if constexpr (__is_same(T, float)) {
-      // Sum partials are dense 32-bit words.
-      const std::uint32_t* w = reinterpret_cast<const std::uint32_t*>(partials) + row * segments;
-      float acc[kUnroll] = {};
-      std::int64_t i = threadIdx.x;
-      for (; i + (kUnroll - 1) * kThreads < segments; i += kUnroll * kThreads) {
+    // Sum partials are dense 32-bit words (float bits or uint32).
+    const std::uint32_t* w = reinterpret_cast<const std::uint32_t*>(partials) + row * segments;
+    using Acc = std::conditional_t<__is_same(T, float), float, std::uint32_t>;
+    Acc acc[kUnroll] = {};
+    for (std::int64_t base = threadIdx.x; base < segments; base += kUnroll * kThreads) {
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) acc[u] += from_bits<float>(w[i + u * kThreads]);
-      }
-      for (; i < segments; i += kThreads) acc[0] += from_bits<float>(w[i]);
-#pragma unroll
-      for (int u = kUnroll / 2; u > 0; u >>= 1)
-#pragma unroll
-        for (int v = 0; v < u; ++v) acc[v] += acc[v + u];
-      float s = wave_sum(acc[0]);
-      if (lane == 0) waves[wave] = Partial{to_bits(s), 0U, 0};
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        // Pairwise over the waves: (w0 + w1) + (w2 + w3) for four, and so on.
-        float t[kWaves];
-#pragma unroll
-        for (int k = 0; k < kWaves; ++k) t[k] = from_bits<float>(waves[k].bits);
-#pragma unroll
-        for (int u = kWaves / 2; u > 0; u >>= 1)
-#pragma unroll
-          for (int v = 0; v < u; ++v) t[v] = t[2 * v] + t[2 * v + 1];
-        static_cast<float*>(out)[row] = kOp == TCX_REDUCE_MEAN ? t[0] / static_cast<float>(reduce) : t[0];
-      }
-    } else {
-      const std::uint32_t* w = reinterpret_cast<const std::uint32_t*>(partials) + row * segments;
-      std::uint32_t acc[kUnroll] = {};
-      std::int64_t i = threadIdx.x;
-      for (; i + (kUnroll - 1) * kThreads < segments; i += kUnroll * kThreads) {
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) acc[u] += w[i + u * kThreads];
-      }
-      for (; i < segments; i += kThreads) acc[0] += w[i];
-      std::uint32_t s = 0;
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) s += acc[u];
-      s = wave_sum_u32(s);
-      if (lane == 0) waves[wave] = Partial{s, 0U, 0};
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        std::uint32_t t = 0;
-#pragma unroll
-        for (int k = 0; k < kWaves; ++k) t += waves[k].bits;
-        static_cast<int*>(out)[row] = static_cast<int>(t);
+      for (int u = 0; u < kUnroll; ++u) {
+        const std::int64_t i = base + u * kThreads;
+        if (i < segments) acc[u] += __builtin_bit_cast(Acc, w[i]);
       }
     }
-  } else {
-    T best{};
-    std::int64_t bi = -1;
-    for (std::int64_t i = threadIdx.x; i < segments; i += kThreads) {
-      const T v = from_bits<T>(p[i].bits);
-      if (cand_better<T, kLargest>(v, p[i].index, best, bi)) {
-        best = v;
-        bi = p[i].index;
-      }
-    }
-    wave_extremum<T, kLargest>(best, bi);
-    if (lane == 0) waves[wave] = Partial{to_bits(best), 0U, bi};
+#pragma unroll
+    for (int u = kUnroll / 2; u > 0; u >>= 1)
+#pragma unroll
+      for (int v = 0; v < u; ++v) acc[v] += acc[v + u];
+    Acc t;
+    if constexpr (__is_same(T, float))
+      t = wave_sum(acc[0]);
+    else
+      t = wave_sum_u32(acc[0]);
+    if (lane == 0) waves[wave] = Partial{__builtin_bit_cast(std::uint32_t, t), 0U, 0};
     __syncthreads();
     if (threadIdx.x == 0) {
-      for (int w = 1; w < kWaves; ++w) {
-        const T v = from_bits<T>(waves[w].bits);
-        if (cand_better<T, kLargest>(v, waves[w].index, best, bi)) {
-          best = v;
-          bi = waves[w].index;
-        }
-      }
-      if constexpr (kOp == TCX_REDUCE_ARGMAX)
-        static_cast<int*>(out)[row] = static_cast<int>(bi);
-      else
-        static_cast<T*>(out)[row] = best;
+      // Pairwise over the waves: (w0 + w1) + (w2 + w3).
+      const Acc w01 = __builtin_bit_cast(Acc, waves[0].bits) + __builtin_bit_cast(Acc, waves[1].bits);
+      const Acc w23 = __builtin_bit_cast(Acc, waves[2].bits) + __builtin_bit_cast(Acc, waves[3].bits);
+      store_row<kOp, T>(out, row, Partial{__builtin_bit_cast(std::uint32_t, w01 + w23), 0U, 0}, reduce);
+    }
+  } else {
+    const Partial* p = partials + row * segments;
+    std::uint32_t bk = 0, bb = 0;
+    std::int64_t bi = kNoIndex;
+    auto take = [&](std::uint32_t k, std::uint32_t b, std::int64_t i) {
+      const bool win = k > bk || (k == bk && i < bi);
+      bk = win ? k : bk;
+      bb = win ? b : bb;
+      bi = win ? i : bi;
+    };
+#pragma unroll 1
+    for (std::int64_t i = threadIdx.x; i < segments; i += kThreads) {
+      const Partial r = p[i];
+      const bool empty = r.index < 0;
+      take(empty ? 0U : rank_key<T, kLargest>(r.bits), r.bits, empty ? kNoIndex : r.index);
+    }
+#pragma unroll 1
+    for (int offset = 32; offset > 0; offset >>= 1) {
+      const std::uint32_t k = static_cast<std::uint32_t>(__shfl_xor(static_cast<int>(bk), offset, kWave));
+      const std::uint32_t b = static_cast<std::uint32_t>(__shfl_xor(static_cast<int>(bb), offset, kWave));
+      take(k, b, __shfl_xor(bi, offset, kWave));
+    }
+    if (lane == 0) waves[wave] = Partial{bb, bk, bi};
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll 1
+      for (int v = 1; v < kWaves; ++v) take(waves[v].pad, waves[v].bits, waves[v].index);
+      store_row<kOp, T>(out, row, Partial{bb, 0U, bi == kNoIndex ? -1 : bi}, reduce);
     }
   }
-}
-
-template <int kOp, typename T, int kThreads>
-__global__ __launch_bounds__(kThreads) void finish_kernel(const Partial* __restrict__ partials,
-                                                          void* __restrict__ out, std::int64_t rows,
-                                                          std::int64_t reduce, std::int64_t segments) {
-  if (static_cast<std::int64_t>(blockIdx.x) >= rows) return;
-  combine_row<kOp, T, kThreads>(partials, out, blockIdx.x, reduce, segments);
 }
 
 // ------------------------------------------------------ exact-order paths
@@ -599,8 +605,8 @@ RowPlan plan_rows(std::int64_t outer, std::int64_t reduce, std::int64_t inner) {
   RowPlan p{false, 1, reduce};
   if (inner != 1 || reduce <= kSequentialMax) return p;
   p.row_path = true;
-  if (outer < kTargetWaves && reduce > 2 * kMinSegment) {
-    std::int64_t want = (kTargetWaves + outer - 1) / outer;
+  if (outer < kTargetSegments && reduce > 2 * kMinSegment) {
+    std::int64_t want = (kTargetSegments + outer - 1) / outer;
     const std::int64_t most = (reduce + kMinSegment - 1) / kMinSegment;
     if (want > most) want = most;
     if (want > 1) {
@@ -671,17 +677,8 @@ int launch_reduce(const T* x, void* out, std::int64_t outer, std::int64_t reduce
                        reduce, plan.segments, plan.seg_len);
   int rc = check(hipGetLastError(), "reduce row kernel launch");
   if (rc != TCX_OK || plan.segments == 1) return rc;
-  // Sums combine 32-bit words with 256 threads, all 8192 partials of a
-  // full-tensor sum in flight at once (78.2 -> 79.0 % of HBM peak for the
-  // 67 M-element sum against 1024 threads); extremum records, folded one at
-  // a time per thread, take 1024 threads when a row has >= 2048 of them.
-  constexpr bool kSumWords = kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN;
-  if (!kSumWords && plan.segments >= 2048)
-    hipLaunchKernelGGL((finish_kernel<kOp, T, 1024>), dim3(static_cast<unsigned>(outer)), dim3(1024), 0, s, partials,
-                       out, outer, reduce, plan.segments);
-  else
-    hipLaunchKernelGGL((finish_kernel<kOp, T, 256>), dim3(static_cast<unsigned>(outer)), dim3(256), 0, s, partials,
-                       out, outer, reduce, plan.segments);
+  hipLaunchKernelGGL((finish_kernel<kOp, T>), dim3(static_cast<unsigned>(outer)), dim3(kFinishThreads), 0, s,
+                     partials, out, outer, reduce, plan.segments);
   return check(hipGetLastError(), "reduce finish kernel launch");
 }
 

@@ -72,9 +72,9 @@ def test_reduce_workspace_fits_the_noalloc_scratch():
     # tcx_hip_reduce_noalloc accepts every plan whose workspace query is at
     # most TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE; the query stays under it for
     # every float32 tensor that fits in 288 GB of HBM (at most 2^36
-    # elements): segments are sized to about 8192 waves, so rows x segments
-    # stays below 16384 partials of 16 bytes, and rows longer than 2^30
-    # elements add at most 64 segments. A sweep of row counts and row lengths
+    # elements): rows are split into about 1792 segments in all, so rows x
+    # segments stays below 3584 partials of 16 bytes, and rows longer than
+    # 2^30 elements add at most 64 segments. A sweep of row counts and row lengths
     # around the segmenting thresholds shows it.
     if not capi.LIB_PATH.exists():
         pytest.fail("libtensorcx_hip.so is not built: run `python tensor.cx_amd/build.py`")
@@ -87,7 +87,8 @@ def test_reduce_workspace_fits_the_noalloc_scratch():
             for op in ("sum", "max", "argmax"):
                 largest = max(largest, query(capi.REDUCE[op], capi.TCX_FLOAT32, rows, cols, 1))
     assert 0 < largest <= capi.REDUCE_NOALLOC_MAX_WORKSPACE
-    assert query(0, capi.TCX_FLOAT32, 1, 8192 * 8192, 1) == 8192 * 16  # the full-tensor sum
+    # The full-tensor sum: 1772 segments of 37888 elements (37 x 1024).
+    assert query(0, capi.TCX_FLOAT32, 1, 8192 * 8192, 1) == 1772 * 16
 
 
 CONTRACT = ROOT / "tests" / "cpp" / "_bin" / "hip_backend_contract"

@@ -507,6 +507,40 @@ def test_extrema_special_values_vector_rows(cx, width):
         assert_bits(getattr(cx, op)(hy, None).numpy(), getattr(oracle, op)(y, None), f"{op} long row NaN")
 
 
+@pytest.mark.parametrize("width", [1 << 20, (1 << 20) + 3])
+def test_extrema_segment_combine_special_values(cx, width):
+    """Rows split into segments: the finish step's (rank key, index) fold must
+    keep the first of equal keys across segments (ties, -0 against +0, every
+    value -inf, two NaNs of different sign) and let a real int32 extreme,
+    whose key is 0, beat an empty candidate."""
+    x = np.zeros((6, width), np.float32)
+    x[0, :] = -0.0
+    x[0, 900000] = 0.0                            # +0 in a late segment: first -0 kept
+    x[1, :] = -np.inf
+    x[2, 700000] = x[2, 900000] = 5.0             # tie across segments
+    x[2, 300000] = x[2, 800000] = -7.0
+    x[3, 800000] = np.float32(np.nan) * -1
+    x[3, 300000] = np.nan                         # the first NaN is the positive one
+    x[4, :] = np.inf
+    x[4, 1000] = -0.0
+    x[5] = np.random.default_rng(15).integers(-2, 3, width)
+    h = cx.tensor(x, device="hip")
+    for op in ("max", "min", "argmax"):
+        assert_bits(getattr(cx, op)(h, 1).numpy(), getattr(oracle, op)(x, 1), f"{op} f32 width {width}")
+        assert_bits(getattr(cx, op)(h, None).numpy(), getattr(oracle, op)(x, None), f"{op} f32 all")
+    imin, imax = np.iinfo(np.int32).min, np.iinfo(np.int32).max
+    y = np.zeros((4, width), np.int32)
+    y[0, :] = imin                                # max: key 0 everywhere, index 0
+    y[1, :] = imax                                # min: key 0 everywhere, index 0
+    y[2, 600000] = y[2, 950000] = imax            # tie across segments
+    y[2, 100000] = y[2, 400000] = imin
+    y[3] = np.random.default_rng(16).integers(imin, imax, width, dtype=np.int64).astype(np.int32)
+    hy = cx.tensor(y, device="hip")
+    for op in ("max", "min", "argmax"):
+        assert_bits(getattr(cx, op)(hy, 1).numpy(), getattr(oracle, op)(y, 1), f"{op} i32 width {width}")
+        assert_bits(getattr(cx, op)(hy, None).numpy(), getattr(oracle, op)(y, None), f"{op} i32 all")
+
+
 def test_int32_reductions_wrap(cx):
     rng = np.random.default_rng(3)
     x = rng.integers(-2**31, 2**31 - 1, size=(300, 1031), dtype=np.int64).astype(np.int32)
