@@ -14,12 +14,13 @@
 // reference's exact left-to-right order, one lane per output.
 //
 // Paths:
-//   row_wave_kernel    inner == 1, long rows: each (row, segment) reduced by
-//                      one wave with 16-byte loads, waves of a persistent grid
-//                      taking items in turn; rows split into segments when
-//                      there are too few rows to fill the GPU (partials in
-//                      workspace)
-//   finish_kernel      combines per-row segment partials in a fixed order
+//   row_kernel         inner == 1, long rows: wave segments reduced by one
+//                      wave each with 16-byte loads; items of one segment per
+//                      wave (rows below kBlockRowMin) or four per 4-wave block
+//                      (longer rows) taken in turn by a persistent grid; rows
+//                      split into more items when there are too few rows to
+//                      fill the GPU (partials in workspace)
+//   finish_kernel      combines per-row item partials in a fixed order
 //   lane_kernel        one lane per output, reference element order
 //   axes_kernel        any axis selection through reduction-plan metadata
 
@@ -33,15 +34,21 @@ namespace tcx {
 namespace {
 
 constexpr std::int64_t kSequentialMax = 64;   // rows up to this length keep exact order
-// Segments a short-row reduction is split into (over all rows): one per wave
-// of the row path's persistent grid on 256 CUs (7 blocks of 4 waves per 4
-// CUs), so each wave streams one segment and the finish step folds few
+// Wave segments that too few long rows are split into (over all rows): one
+// per wave of the row path's persistent grid on 256 CUs (7 blocks of 4 waves
+// per 4 CUs), so each wave streams one segment and the finish step folds few
 // partials. Measured against 8192 segments (4.6 per wave) on MI355X: the
 // 67 M-element full sum 75.6 -> 77.2 % of HBM peak, full max 66.1 -> 75.9 %,
 // int32 full max 72.1 -> 75.3 %, 2 x 33 M min 68.6 -> 76.2 %; 3584 segments
 // lost 7 points on 64 x 1 M max.
 constexpr std::int64_t kTargetSegments = 1792;
-constexpr std::int64_t kMinSegment = 4096;    // elements per segment when splitting rows
+// Rows of at least this many elements are reduced a block at a time, four
+// wave segments of at least 8192 elements per block item. Shorter segments
+// cost extremum searches their per-segment tail (the wave's key reduction):
+// with block items from 8192 elements, [8192, 8192] max fell from 77.9 to
+// 57.0 % of HBM peak; from 32768, every shape measured kept or gained.
+constexpr std::int64_t kBlockRowMin = 32768;
+constexpr std::int64_t kMinSegment = 4096;    // fewest elements per wave segment of a split row
 
 // Partial result of one (row, segment) of an extremum search: (value bits,
 // index); index < 0 marks an empty candidate. Sum partials are stored instead
@@ -323,30 +330,81 @@ __device__ __forceinline__ void store_row(void* out, std::int64_t row, const Par
   }
 }
 
-// One wave per (row, segment). With one segment per row the wave writes the
-// row's result; otherwise it writes its partial to the workspace (sums as
-// dense 32-bit words, extrema as records) for finish_kernel.
-template <int kOp, typename T, bool kVec>
-__global__ __launch_bounds__(256) void row_wave_kernel(const T* __restrict__ x, void* __restrict__ out,
-                                                       Partial* __restrict__ partials, std::int64_t rows,
-                                                       std::int64_t reduce, std::int64_t segments,
-                                                       std::int64_t seg_len) {
-  const int lane = threadIdx.x & 63;
-  // Grid-stride over the waves' items (the launcher caps the grid); the
-  // bound is wave-uniform, so every lane of a wave runs the same iterations.
-  const std::int64_t items = rows * segments;
-  const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * 4;
-  for (std::int64_t gw = static_cast<std::int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); gw < items; gw += step) {
-    const std::int64_t row = gw / segments, seg = gw % segments;
-    const std::int64_t begin = seg * seg_len;
-    const Partial r = wave_reduce<kOp, T, kVec>(x + row * reduce, begin, min(reduce, begin + seg_len), lane);
-    if (lane != 0) continue;
-    if (segments == 1)
+// Combines the four wave partials of a block item in wave order: sums as
+// (w0 + w1) + (w2 + w3), extrema by cand_better (empty candidates lose).
+template <int kOp, typename T>
+__device__ __forceinline__ Partial combine_waves(const Partial (&w)[4]) {
+  if constexpr (kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN) {
+    if constexpr (__is_same(T, float)) {
+      const float s = (from_bits<float>(w[0].bits) + from_bits<float>(w[1].bits)) +
+                      (from_bits<float>(w[2].bits) + from_bits<float>(w[3].bits));
+      return Partial{to_bits(s), 0U, 0};
+    } else {
+      return Partial{(w[0].bits + w[1].bits) + (w[2].bits + w[3].bits), 0U, 0};
+    }
+  } else {
+    constexpr bool kLargest = kOp != TCX_REDUCE_MIN;
+    Partial best = w[0];
+#pragma unroll
+    for (int v = 1; v < 4; ++v)
+      if (cand_better<T, kLargest>(from_bits<T>(w[v].bits), w[v].index, from_bits<T>(best.bits), best.index))
+        best = w[v];
+    return best;
+  }
+}
+
+// The row path. Each row is cut into `segments` wave segments of seg_len
+// elements (the last ones may be short or empty), reduced by wave_reduce.
+//   kBlock false: one wave per (row, segment) item, the waves of a persistent
+//   grid taking items in turn.
+//   kBlock true: one 4-wave block per item of four consecutive segments, the
+//   blocks of a persistent grid taking items in turn; the block adds its four
+//   wave partials in wave order. A block finishes a long row four times
+//   sooner than a wave, so the last round of items leaves fewer waves idle.
+// With one item per row the row's result is stored; otherwise each item's
+// partial goes to the workspace (sums as dense 32-bit words, extrema as
+// records) for finish_kernel.
+template <int kOp, typename T, bool kVec, bool kBlock>
+__global__ __launch_bounds__(256) void row_kernel(const T* __restrict__ x, void* __restrict__ out,
+                                                  Partial* __restrict__ partials, std::int64_t rows,
+                                                  std::int64_t reduce, std::int64_t segments, std::int64_t seg_len) {
+  constexpr bool kSumWords = kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  auto publish = [&](std::int64_t row, std::int64_t item, std::int64_t per_row, const Partial& r) {
+    if (per_row == 1)
       store_row<kOp, T>(out, row, r, reduce);
-    else if constexpr (kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN)
-      reinterpret_cast<std::uint32_t*>(partials)[gw] = r.bits;
+    else if constexpr (kSumWords)
+      reinterpret_cast<std::uint32_t*>(partials)[item] = r.bits;
     else
-      partials[gw] = r;
+      partials[item] = r;
+  };
+  if constexpr (!kBlock) {
+    // Grid-stride over the waves' items (the launcher caps the grid); the
+    // bound is wave-uniform, so every lane of a wave runs the same iterations.
+    const std::int64_t items = rows * segments;
+    const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * 4;
+    for (std::int64_t gw = static_cast<std::int64_t>(blockIdx.x) * 4 + wave; gw < items; gw += step) {
+      const std::int64_t row = gw / segments, seg = gw % segments;
+      const std::int64_t begin = seg * seg_len;
+      const Partial r = wave_reduce<kOp, T, kVec>(x + row * reduce, begin, min(reduce, begin + seg_len), lane);
+      if (lane == 0) publish(row, gw, segments, r);
+    }
+  } else {
+    // Block-uniform bound: every thread reaches each barrier. The wave
+    // partials alternate between two slots, so thread 0 reads an item's
+    // slot while the waves fill the other one with the next item's.
+    __shared__ Partial slot[2][4];
+    const std::int64_t per_row = segments / 4;
+    const std::int64_t items = rows * per_row;
+    int parity = 0;
+    for (std::int64_t item = blockIdx.x; item < items; item += gridDim.x, parity ^= 1) {
+      const std::int64_t row = item / per_row;
+      const std::int64_t begin = min(reduce, ((item % per_row) * 4 + wave) * seg_len);
+      const Partial r = wave_reduce<kOp, T, kVec>(x + row * reduce, begin, min(reduce, begin + seg_len), lane);
+      if (lane == 0) slot[parity][wave] = r;
+      __syncthreads();
+      if (threadIdx.x == 0) publish(row, item, per_row, combine_waves<kOp, T>(slot[parity]));
+    }
   }
 }
 
@@ -598,39 +656,48 @@ __global__ __launch_bounds__(256) void axes_kernel(const T* __restrict__ x, void
 // ------------------------------------------------------------ planning
 struct RowPlan {
   bool row_path;
-  std::int64_t segments, seg_len;
+  bool block_items;        // row_kernel<..., kBlock = true>
+  std::int64_t segments;   // wave segments per row (4 per item with block_items)
+  std::int64_t seg_len;    // elements per wave segment, a multiple of 1024 when segments > 1
+  std::int64_t partials;   // items per row: 1 means row_kernel stores the row itself
 };
 
 RowPlan plan_rows(std::int64_t outer, std::int64_t reduce, std::int64_t inner) {
-  RowPlan p{false, 1, reduce};
+  RowPlan p{false, false, 1, reduce, 1};
   if (inner != 1 || reduce <= kSequentialMax) return p;
   p.row_path = true;
-  if (outer < kTargetSegments && reduce > 2 * kMinSegment) {
-    std::int64_t want = (kTargetSegments + outer - 1) / outer;
-    const std::int64_t most = (reduce + kMinSegment - 1) / kMinSegment;
-    if (want > most) want = most;
-    if (want > 1) {
-      // Segment length: a multiple of 1024 elements keeps 16-byte alignment
-      // and whole unrolled strides inside each segment.
-      std::int64_t len = (reduce + want - 1) / want;
-      len = (len + 1023) / 1024 * 1024;
-      p.segments = (reduce + len - 1) / len;
-      p.seg_len = len;
-    }
-  }
-  // 32-bit in-segment indices: split rows longer than 2^30 elements.
+  // 32-bit in-segment indices: segments stay at or below 2^30 elements.
   constexpr std::int64_t kMaxSegment = std::int64_t{1} << 30;
-  if (p.seg_len > kMaxSegment) {
-    p.segments = (reduce + kMaxSegment - 1) / kMaxSegment;
-    p.seg_len = kMaxSegment;
+  if (reduce >= kBlockRowMin || (reduce > 2 * kMinSegment && outer < kTargetSegments)) {
+    // Block items: four wave segments each, about kTargetSegments wave
+    // segments in all when the rows are too few to fill the grid (rows of
+    // 8193-32767 elements take block items only then).
+    p.block_items = true;
+    std::int64_t items = 1;
+    if (outer < kTargetSegments / 4) {
+      items = (kTargetSegments / 4 + outer - 1) / outer;
+      const std::int64_t most = (reduce + 4 * kMinSegment - 1) / (4 * kMinSegment);
+      if (items > most) items = most;
+    }
+    // A multiple of 1024 elements keeps 16-byte alignment and whole
+    // unrolled strides inside each wave segment.
+    std::int64_t len = (reduce + 4 * items - 1) / (4 * items);
+    len = (len + 1023) / 1024 * 1024;
+    if (len > kMaxSegment) len = kMaxSegment;
+    p.partials = (reduce + 4 * len - 1) / (4 * len);
+    p.segments = 4 * p.partials;
+    p.seg_len = len;
+    return p;
   }
+  // Rows of at most 8192 elements, or enough rows to fill the grid: one wave
+  // per row.
   return p;
 }
 
 bool aligned16(const void* q) { return (reinterpret_cast<std::uintptr_t>(q) & 15U) == 0; }
 
 // Blocks of the row path's persistent grid: 7 per 4 CUs (1792 waves on 256
-// CUs), each wave streaming its (row, segment) items in turn. Fewer streams
+// CUs), each wave (or block) streaming its items in turn. Fewer streams
 // open at once read HBM faster than one wave per item. Measured against one
 // wave per item on 8192 x 8192 f32: sum 81.1 -> 83.8 %, max 77.9 -> 80.0 %,
 // the 67 M-element full sum 75.6 -> 78.0 %, 65536 x 4096 84.7 -> 86.3 %,
@@ -660,30 +727,42 @@ int launch_reduce(const T* x, void* out, std::int64_t outer, std::int64_t reduce
     return check(hipGetLastError(), "reduce lane kernel launch");
   }
   Partial* partials = nullptr;
-  if (plan.segments > 1) {
-    const std::size_t need = static_cast<std::size_t>(outer * plan.segments) * sizeof(Partial);
+  if (plan.partials > 1) {
+    const std::size_t need = static_cast<std::size_t>(outer * plan.partials) * sizeof(Partial);
     if (workspace == nullptr || workspace_bytes < need)
       return fail(TCX_INVALID_ARGUMENT, "reduce workspace is smaller than tcx_hip_reduce_workspace_bytes");
     partials = static_cast<Partial*>(workspace);
   }
   const bool vec = reduce % 4 == 0 && aligned16(x);
-  const std::int64_t waves = outer * plan.segments;
-  const dim3 grid(grid_for(waves, 4, row_grid_blocks()));
-  if (vec)
-    hipLaunchKernelGGL((row_wave_kernel<kOp, T, true>), grid, dim3(256), 0, s, x, out, partials, outer,
-                       reduce, plan.segments, plan.seg_len);
+  // A grid of at most row_grid_blocks() blocks, sized so that every round of
+  // items keeps all of its waves (or blocks) busy: 4096 rows of 16384 floats
+  // take 3 rounds of 1366 waves, not 2 full rounds of 1792 and a third of
+  // 512. Against the full grid: [4096, 16384] sum 70.4 -> 78.7 % and max
+  // 69.2 -> 75.8 %, [16384, 8192] 83.0 -> 84.6 %, [1000, 32768] sum 71.2 ->
+  // 75.3 %, [3000, 20000] 76.7 -> 79.0 %.
+  auto balanced = [](std::int64_t work, std::int64_t per_block, std::int64_t cap_blocks) {
+    const std::int64_t slots = cap_blocks * per_block;
+    const std::int64_t rounds = (work + slots - 1) / slots;
+    return grid_for((work + rounds - 1) / rounds, per_block, cap_blocks);
+  };
+  const dim3 grid(plan.block_items ? balanced(outer * plan.partials, 1, row_grid_blocks())
+                                   : balanced(outer * plan.segments, 4, row_grid_blocks()));
+  auto launch_rows = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, x, out, partials, outer, reduce, plan.segments, plan.seg_len);
+  };
+  if (plan.block_items)
+    vec ? launch_rows(row_kernel<kOp, T, true, true>) : launch_rows(row_kernel<kOp, T, false, true>);
   else
-    hipLaunchKernelGGL((row_wave_kernel<kOp, T, false>), grid, dim3(256), 0, s, x, out, partials, outer,
-                       reduce, plan.segments, plan.seg_len);
+    vec ? launch_rows(row_kernel<kOp, T, true, false>) : launch_rows(row_kernel<kOp, T, false, false>);
   int rc = check(hipGetLastError(), "reduce row kernel launch");
-  if (rc != TCX_OK || plan.segments == 1) return rc;
+  if (rc != TCX_OK || plan.partials == 1) return rc;
   hipLaunchKernelGGL((finish_kernel<kOp, T>), dim3(static_cast<unsigned>(outer)), dim3(kFinishThreads), 0, s,
-                     partials, out, outer, reduce, plan.segments);
+                     partials, out, outer, reduce, plan.partials);
   return check(hipGetLastError(), "reduce finish kernel launch");
 }
 
 // The no-allocation scratch: the segment partials of the two-launch row path
-// (row_wave_kernel writes them, finish_kernel combines them), for every plan
+// (row_kernel writes them, finish_kernel combines them), for every plan
 // whose workspace query is at most TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE.
 constexpr std::size_t kScratchBytes = TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE;
 
@@ -726,8 +805,8 @@ template <int kOp, typename T>
 int launch_reduce_noalloc(const T* x, void* out, std::int64_t outer, std::int64_t reduce, std::int64_t inner,
                           hipStream_t s) {
   const RowPlan plan = plan_rows(outer, reduce, inner);
-  if (!plan.row_path || plan.segments == 1) return launch_reduce<kOp, T>(x, out, outer, reduce, inner, nullptr, 0, s);
-  const std::int64_t need = outer * plan.segments * static_cast<std::int64_t>(sizeof(Partial));
+  if (!plan.row_path || plan.partials == 1) return launch_reduce<kOp, T>(x, out, outer, reduce, inner, nullptr, 0, s);
+  const std::int64_t need = outer * plan.partials * static_cast<std::int64_t>(sizeof(Partial));
   if (need > TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE)
     return fail(TCX_INVALID_ARGUMENT, "reduction plan needs " + std::to_string(need) +
                                           " bytes of partials; the no-allocation scratch holds " +
@@ -805,8 +884,8 @@ size_t tcx_hip_reduce_workspace_bytes(int op, int dtype, int64_t outer, int64_t 
   (void)dtype;
   if (outer <= 0 || reduce <= 0 || inner <= 0) return 0;
   const tcx::RowPlan plan = tcx::plan_rows(outer, reduce, inner);
-  if (!plan.row_path || plan.segments == 1) return 0;
-  return static_cast<size_t>(outer * plan.segments) * sizeof(tcx::Partial);
+  if (!plan.row_path || plan.partials == 1) return 0;
+  return static_cast<size_t>(outer * plan.partials) * sizeof(tcx::Partial);
 }
 
 namespace {

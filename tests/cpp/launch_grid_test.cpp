@@ -25,9 +25,10 @@ void expect(bool ok, const char* what, std::int64_t n, std::int64_t per_block) {
 int main() {
   using tcx::grid_for;
   // (items per block, threads per block) of the grid-stride launchers:
-  // one item per thread (reduce lane/axes kernels, row_lane_kernel) and one
-  // per wave (row_wave_kernel, four waves per block).
-  const std::int64_t shapes[][2] = {{256, 256}, {4, 256}};
+  // one item per thread (reduce lane/axes kernels, row_lane_kernel), one per
+  // wave (row_kernel with wave items, four waves per block) and one per block
+  // (row_kernel with block items).
+  const std::int64_t shapes[][2] = {{256, 256}, {4, 256}, {1, 256}};
   std::int64_t sizes[64];
   int count = 0;
   for (std::int64_t v : {0LL, 1LL, 3LL, 4LL, 5LL, 255LL, 256LL, 257LL, 65535LL, 65536LL, 1LL << 20, (1LL << 24) - 1,

@@ -72,9 +72,9 @@ def test_reduce_workspace_fits_the_noalloc_scratch():
     # tcx_hip_reduce_noalloc accepts every plan whose workspace query is at
     # most TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE; the query stays under it for
     # every float32 tensor that fits in 288 GB of HBM (at most 2^36
-    # elements): rows are split into about 1792 segments in all, so rows x
-    # segments stays below 3584 partials of 16 bytes, and rows longer than
-    # 2^30 elements add at most 64 segments. A sweep of row counts and row lengths
+    # elements): fewer than 448 rows of 32768+ elements are split into about
+    # 448 items in all, so rows x items stays below 896 partials of 16 bytes,
+    # and rows longer than 2^32 elements add at most 16 items per row. A sweep of row counts and row lengths
     # around the segmenting thresholds shows it.
     if not capi.LIB_PATH.exists():
         pytest.fail("libtensorcx_hip.so is not built: run `python tensor.cx_amd/build.py`")
@@ -87,8 +87,12 @@ def test_reduce_workspace_fits_the_noalloc_scratch():
             for op in ("sum", "max", "argmax"):
                 largest = max(largest, query(capi.REDUCE[op], capi.TCX_FLOAT32, rows, cols, 1))
     assert 0 < largest <= capi.REDUCE_NOALLOC_MAX_WORKSPACE
-    # The full-tensor sum: 1772 segments of 37888 elements (37 x 1024).
-    assert query(0, capi.TCX_FLOAT32, 1, 8192 * 8192, 1) == 1772 * 16
+    # The full-tensor sum: 443 block items of four 37888-element (37 x 1024)
+    # wave segments.
+    assert query(0, capi.TCX_FLOAT32, 1, 8192 * 8192, 1) == 443 * 16
+    # Rows of 8192+ elements with enough rows to fill the grid: no partials.
+    assert query(0, capi.TCX_FLOAT32, 448, 1 << 20, 1) == 0
+    assert query(0, capi.TCX_FLOAT32, 447, 1 << 20, 1) == 447 * 2 * 16
 
 
 CONTRACT = ROOT / "tests" / "cpp" / "_bin" / "hip_backend_contract"

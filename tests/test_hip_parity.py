@@ -541,6 +541,39 @@ def test_extrema_segment_combine_special_values(cx, width):
         assert_bits(getattr(cx, op)(hy, None).numpy(), getattr(oracle, op)(y, None), f"{op} i32 all")
 
 
+@pytest.mark.parametrize("shape", [(5, 9000), (1, 8193), (700, 16384), (3, 40004), (2, 65548), (448, 32768),
+                                   (447, 32768), (2000, 4100)])
+def test_row_reduction_block_items(cx, shape):
+    """Rows cut into 4-wave block items: empty and short trailing wave
+    segments (9000 = 3 x 3072 - 216, 8193 unaligned), one item per row with
+    and without a full grid, items split into partials (fewer than 448 rows),
+    and extrema whose ties and NaNs straddle wave-segment boundaries."""
+    rows, cols = shape
+    rng = np.random.default_rng(cols)
+    x = rng.integers(-3, 4, shape).astype(np.float32)   # many ties
+    for r in range(min(rows, 4)):
+        for edge in (3072, 4096, 8192, cols - 1):
+            if edge < cols:
+                x[r, edge] = 9.0 if r % 2 == 0 else -9.0
+    if rows > 1:
+        x[1, cols // 2] = np.nan
+        x[1, cols - 1] = np.float32(np.nan) * -1
+    h = cx.tensor(x, device="hip")
+    for op in ("max", "min", "argmax"):
+        assert_bits(getattr(cx, op)(h, -1).numpy(), getattr(oracle, op)(x, -1), f"{op} {shape}")
+    y = rng.standard_normal(shape).astype(np.float32)
+    hy = cx.tensor(y, device="hip")
+    for op in ("sum", "mean"):
+        actual = getattr(cx, op)(hy, -1).numpy()
+        expected = getattr(oracle, op)(y, -1)
+        scale = cols if op == "mean" else 1
+        assert sum_error(actual * scale, expected * scale, y, rows, cols, 1) <= 1e-5, f"{op} {shape}"
+    yi = rng.integers(-2**31, 2**31 - 1, shape, dtype=np.int64).astype(np.int32)
+    hi = cx.tensor(yi, device="hip")
+    for op in ("sum", "max", "argmax"):
+        assert_bits(getattr(cx, op)(hi, -1).numpy(), getattr(oracle, op)(yi, -1), f"i32 {op} {shape}")
+
+
 def test_int32_reductions_wrap(cx):
     rng = np.random.default_rng(3)
     x = rng.integers(-2**31, 2**31 - 1, size=(300, 1031), dtype=np.int64).astype(np.int32)
