@@ -37,10 +37,9 @@ constexpr std::int64_t kSequentialMax = 64;   // rows up to this length keep exa
 // Wave segments that too few long rows are split into (over all rows): one
 // per wave of the row path's persistent grid on 256 CUs (7 blocks of 4 waves
 // per 4 CUs), so each wave streams one segment and the finish step folds few
-// partials. Measured against 8192 segments (4.6 per wave) on MI355X: the
-// 67 M-element full sum 75.6 -> 77.2 % of HBM peak, full max 66.1 -> 75.9 %,
-// int32 full max 72.1 -> 75.3 %, 2 x 33 M min 68.6 -> 76.2 %; 3584 segments
-// lost 7 points on 64 x 1 M max.
+// partials. Measured against 8192 segments (4.6 per wave) on MI355X: full
+// max 66.1 -> 75.9 % of HBM peak, int32 full max 72.1 -> 75.3 %, 2 x 33 M min
+// 68.6 -> 76.2 %; 3584 segments lost 7 points on 64 x 1 M max.
 constexpr std::int64_t kTargetSegments = 1792;
 // Rows of at least this many elements are reduced a block at a time, four
 // wave segments of at least 8192 elements per block item. Shorter segments
@@ -408,11 +407,11 @@ __global__ __launch_bounds__(256) void row_kernel(const T* __restrict__ x, void*
   }
 }
 
-// One block of kFinishThreads threads per row combines that row's segment
+// One block of kFinishThreads threads per row combines that row's item
 // partials in a fixed order, so the result is deterministic: a sum's thread t
 // keeps kUnroll accumulators, accumulator u folding partials t + u * 256,
 // t + (u + kUnroll) * 256, ... (all kUnroll loads of a round in flight; one
-// round covers the 1792-segment full-tensor sum), then the accumulators, the
+// round covers 2048 partials, the full-tensor sum has 443), then the accumulators, the
 // lanes and the waves combine pairwise. Extremum records fold on (rank key,
 // index) in a few selects per record: a lone block's time is its dependent
 // instruction path, and the former fold, exec-masked branches around every
