@@ -931,8 +931,15 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8))) vo
   for (int kt = kt0; kt < k_tiles; kt += 2) {
     if (kt >= 2 && kt + 2 < k_tiles) issue((kt + 2) % kStages, (kt + 2) * BKT);
     if (kt >= 2 && kt + 3 < k_tiles) issue((kt + 3) % kStages, (kt + 3) * BKT);
-    compute(kt % kStages);
-    if (kt + 1 < k_tiles) compute((kt + 1) % kStages);
+    // Both tiles' fragment reads go out before the first MFMA (the stage of
+    // a missing odd tile is read but not used): the second tile's reads land
+    // under the first tile's MFMAs (1000^3: 23.8 -> 23.55 us).
+    Frag f0, f1;
+    load(kt % kStages, f0);
+    load((kt + 1) % kStages, f1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(f0);
+    if (kt + 1 < k_tiles) mma(f1);
     __builtin_amdgcn_s_waitcnt(0);  // tiles kt + 2 and kt + 3 have landed
     __syncthreads();
   }
