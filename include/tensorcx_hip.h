@@ -216,8 +216,8 @@ int tcx_hip_reduce(int op, int dtype, const void* x, void* out, int64_t outer, i
 /* tcx_hip_reduce without a workspace, for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc); it has no counterpart in the reference. It runs the kernels of
- * tcx_hip_reduce with the segment partials of segmented plans (few long rows,
- * e.g. a full-tensor sum) in a static per-device scratch of 256 KiB, held
+ * tcx_hip_reduce with the partials of split-row plans (few long rows, e.g. a
+ * full-tensor sum) in a static per-device scratch of 256 KiB, held
  * until the process ends, so its results are bit-identical to
  * tcx_hip_reduce's. Plans are accepted when tcx_hip_reduce_workspace_bytes is
  * at most TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE (else TCX_INVALID_ARGUMENT),
