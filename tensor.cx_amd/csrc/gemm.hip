@@ -33,6 +33,10 @@ using gemm::launch_config;
 
 bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15U) == 0; }
 
+// Long-operand rows (16 per block) from which the streaming kernel takes a
+// skinny GEMM.
+constexpr std::int64_t kStreamMinRows = 256;
+
 // Shapes of >= 256 full 128x128 tiles: the direct kernel on 128x128 tiles of
 // eight waves (64x32 for a transposed B, 32x64 for a [k, n] B; 64-68 KB of
 // LDS and 79-84 registers, so two blocks share a CU), persistent past the
@@ -142,6 +146,22 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
   // (1000^3), else 32x32 blocks of eight one-wave groups with 32-wide k-tiles
   // (small shapes; 512^3: 17.9 -> 11.8 us). The in-block split gained 7 % on
   // 4096x1024x4096 and 21 % on 1000^3 over the same tiles without it.
+  // One skinny operand against a long one: at most 32 rows of A against a
+  // transposed B (the decode-time linear x W^T), or at most 32 columns of B.
+  // The streaming kernel reads the long operand's rows once, 16 per block.
+  // Against the tiled kernels: 1x4096x4096 transposed 25.0 -> 17.1 us,
+  // 16x4096x4096 31.8 -> 20.7, 1x11008x4096 49.8 -> 34.7, 4096x16x4096
+  // 31.8 -> 20.4, 2048x1x2048 28.3 -> 13.3, 64 batches of 8x1024x1024
+  // transposed 255.8 -> 57.6.
+  constexpr std::int64_t kSkinny = gemm::kStreamMaxSkinny;
+  if (strides_vec && gemm::stream_fits(d->k) && aligned16(lhs)) {
+    if (trans_b && d->m <= kSkinny && d->n >= kStreamMinRows && aligned16(rhs))
+      return gemm::launch_stream<false, true>(args, s);
+    if (d->n <= kSkinny && d->m >= kStreamMinRows) {
+      if (!trans_b) return gemm::launch_stream<true, false>(args, s);
+      if (aligned16(rhs)) return gemm::launch_stream<false, false>(args, s);
+    }
+  }
   const std::int64_t tiles_256 = ((d->m + 255) / 256) * ((d->n + 255) / 256) * batches;
   // (Unaligned shapes take the scalar-load variant, which does not fit the
   // 256x256 tile's registers; they use the 128x128 tile.)

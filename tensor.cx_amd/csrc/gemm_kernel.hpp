@@ -1210,6 +1210,191 @@ inline int launch_small(GemmArgs& args, bool trans_b, hipStream_t stream) {
   return check(hipGetLastError(), "gemm_f32 small launch");
 }
 
+// Streaming GEMM for one skinny operand: at most 32 rows of A against a
+// transposed B (the decode-time linear x W^T), or at most 32 columns of B.
+//   P[j][i] = sum_k X[j][k] W[i][k]: W [I, K] row-major (the long operand,
+//   each row read once from HBM), X the skinny one (J <= 16 kMB rows, read
+//   through the caches), row-major [J, K] or, with kXCols, held as [K, J] (a
+//   [k, n] B of few columns).
+//   kOutJI: W is the transposed B and X the lhs, out[j][i]; otherwise W is the
+//   lhs, out[i][j].
+// One block per 16 rows of W (and batch) of KS waves that split K into
+// contiguous runs of 16-k chunks, as in gemm_f32_small_kernel. Lane (r, kl)
+// holds W[i0 + r][16c + 4kl .. + 3] of chunk c as the MFMA's A operand (one
+// 16-byte load) and X[16g + r][16c + 4kl .. + 3] as its B operand for row
+// group g, so MFMA step q takes k = 16c + 4kl + q for both; output (g, v) of
+// lane (r, kl) is P[16g + r][i0 + 4kl + v]. kG chunks per load group, two
+// groups in flight. The KS partial tiles meet in LDS and are added in wave
+// order with the bias and activation. Rows of W past I, rows of X past J and
+// k past K read zero through the buffer range checks and an out-of-range
+// offset.
+template <bool kXCols, bool kOutJI, int kMB, int KS, int kG>
+__global__ __launch_bounds__(64 * KS) void gemm_f32_stream_kernel(GemmArgs a) {
+  const std::int64_t M = a.m, N = a.n, K = a.k;
+  const std::int64_t I = kOutJI ? N : M, J = kOutJI ? M : N;
+  const std::int64_t i_blocks = (I + 15) / 16;
+  const std::int64_t bid = blockIdx.x;
+  const std::int64_t batch = bid / i_blocks, i0 = (bid % i_blocks) * 16;
+  std::int64_t lhs_off = 0, rhs_off = 0;
+  {
+    std::int64_t b = batch;
+    for (int ax = a.batch_rank - 1; ax >= 0; --ax) {
+      const std::int64_t e = a.batch_shape[ax];
+      const std::int64_t c = b % e;
+      b /= e;
+      lhs_off += c * a.lhs_bs[ax];
+      rhs_off += c * a.rhs_bs[ax];
+    }
+  }
+  const float* const W = kOutJI ? a.rhs + rhs_off : a.lhs + lhs_off;
+  const float* const X = kOutJI ? a.lhs + lhs_off : a.rhs + rhs_off;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, kl = lane >> 4;
+  auto rsrc_of = [](const float* base, std::int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
+  };
+  // The launcher checks that 64 rows of K floats span less than 2^31 bytes.
+  const std::int64_t w_rows = I - i0 < 16 ? I - i0 : 16;
+  const auto w_rsrc = rsrc_of(W + i0 * K, w_rows * K * 4);
+  const auto x_rsrc = rsrc_of(X, J * K * 4);
+  constexpr int kOut = 0x7fffffff;
+  const int Ki = static_cast<int>(K), Ji = static_cast<int>(J);
+  const int chunks = (Ki + 15) / 16;
+  const int c_begin = wave * chunks / KS, c_end = (wave + 1) * chunks / KS;
+
+  struct Frag {
+    float4_t w, x[kMB];
+  };
+  auto load = [&](int c, Frag& f) {
+    const int k = 16 * c + 4 * kl;
+    const bool k_in = c < c_end && k < Ki;
+    f.w = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, k_in ? (r * Ki + k) * 4 : kOut,
+                                                                             0, 0));
+#pragma unroll
+    for (int g = 0; g < kMB; ++g) {
+      const int j = 16 * g + r;
+      if constexpr (kXCols) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          f.x[g][q] = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(x_rsrc, k_in && j < Ji ? ((k + q) * Ji + j) * 4 : kOut, 0, 0));
+      } else {
+        f.x[g] = __builtin_bit_cast(
+            float4_t, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, k_in && j < Ji ? (j * Ki + k) * 4 : kOut, 0, 0));
+      }
+    }
+  };
+  floatx4 acc[kMB];
+#pragma unroll
+  for (int g = 0; g < kMB; ++g) acc[g] = floatx4{0.F, 0.F, 0.F, 0.F};
+  auto mma = [&](const Frag& f) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int g = 0; g < kMB; ++g)
+        acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.w[q], f.x[g][q], acc[g], 0, 0, 0);
+  };
+  Frag f0[kG], f1[kG];
+  auto load_group = [&](int c0, Frag (&f)[kG]) {
+#pragma unroll
+    for (int u = 0; u < kG; ++u) load(c0 + u, f[u]);
+  };
+  auto mma_group = [&](int c0, const Frag (&f)[kG]) {
+#pragma unroll
+    for (int u = 0; u < kG; ++u)
+      if (c0 + u < c_end) mma(f[u]);
+  };
+  load_group(c_begin, f0);
+  for (int c0 = c_begin; c0 < c_end; c0 += 2 * kG) {
+    load_group(c0 + kG, f1);
+    mma_group(c0, f0);
+    load_group(c0 + 2 * kG, f0);
+    if (c0 + kG < c_end) mma_group(c0 + kG, f1);
+  }
+
+  auto store = [&](int g, int v, float x) {
+    const std::int64_t i = i0 + 4 * kl + v, j = 16 * g + r;
+    if (i >= I || j >= J) return;
+    const std::int64_t row = kOutJI ? j : i, col = kOutJI ? i : j;
+    if (a.bias != nullptr) x = x + a.bias[col];
+    a.out[batch * M * N + row * N + col] = activate(x, a.activation);
+  };
+  if constexpr (KS == 1) {
+#pragma unroll
+    for (int g = 0; g < kMB; ++g)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) store(g, v, acc[g][v]);
+  } else {
+    __shared__ float red[KS][kMB * 4][64];  // partial (g, v) of each wave, per lane
+#pragma unroll
+    for (int g = 0; g < kMB; ++g)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[wave][g * 4 + v][lane] = acc[g][v];
+    __syncthreads();
+    for (int e = wave; e < kMB * 4; e += KS) {
+      float x = red[0][e][lane];
+#pragma unroll
+      for (int w = 1; w < KS; ++w) x += red[w][e][lane];
+      store(e / 4, e % 4, x);
+    }
+  }
+}
+
+// Skinny rows or columns the streaming kernel takes: up to two row groups.
+// With four (33-64) its MFMAs outweigh the streamed bytes and the tiled
+// kernels were faster (48x4096x4096 transposed: 38.1 against 34.3 us).
+constexpr std::int64_t kStreamMaxSkinny = 32;
+
+// True when gemm_f32_stream_kernel can take a K: whole 16-byte groups of k
+// and kStreamMaxSkinny rows of K floats (the skinny operand's buffer range)
+// below 2^31 bytes.
+inline bool stream_fits(std::int64_t k) {
+  return k > 0 && k % 4 == 0 && static_cast<double>(kStreamMaxSkinny) * static_cast<double>(k) * 4 < 2147483647.0;
+}
+
+template <bool kXCols, bool kOutJI, int kMB, int KS>
+void launch_stream_as(const GemmArgs& args, std::int64_t blocks, hipStream_t stream) {
+  // Two groups of four chunks in flight for one row group of X, of two
+  // chunks for two (the registers of four waves per SIMD at KS = 16).
+  constexpr int kG = kMB == 1 ? 4 : 2;
+  hipLaunchKernelGGL((gemm_f32_stream_kernel<kXCols, kOutJI, kMB, KS, kG>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(64 * KS), 0, stream, args);
+}
+
+template <bool kXCols, bool kOutJI, int kMB>
+void launch_stream_ks(const GemmArgs& args, std::int64_t blocks, int ks, hipStream_t stream) {
+  switch (ks) {
+    case 1: launch_stream_as<kXCols, kOutJI, kMB, 1>(args, blocks, stream); break;
+    case 2: launch_stream_as<kXCols, kOutJI, kMB, 2>(args, blocks, stream); break;
+    case 4: launch_stream_as<kXCols, kOutJI, kMB, 4>(args, blocks, stream); break;
+    case 8: launch_stream_as<kXCols, kOutJI, kMB, 8>(args, blocks, stream); break;
+    default: launch_stream_as<kXCols, kOutJI, kMB, 16>(args, blocks, stream); break;
+  }
+}
+
+// kOutJI: W is the transposed B (at most 32 rows of A); otherwise W is A (at
+// most 32 columns of B, kXCols when B is [k, n]). args.total_tiles holds the
+// batch count. KS as for the small kernel: about sixteen waves per CU over
+// the launch, at most one per 16-k chunk and at most 16.
+template <bool kXCols, bool kOutJI>
+int launch_stream(GemmArgs& args, hipStream_t stream) {
+  const std::int64_t I = kOutJI ? args.n : args.m, J = kOutJI ? args.m : args.n;
+  if (J > kStreamMaxSkinny || !stream_fits(args.k))
+    return fail(TCX_INTERNAL, "streaming gemm needs at most 32 skinny rows");
+  const std::int64_t blocks = (I + 15) / 16 * args.total_tiles;
+  if (blocks > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
+  const std::int64_t chunks = (args.k + 15) / 16;
+  int ks = 1;
+  while (ks < 16 && ks * 2 <= chunks && blocks * ks < 4096) ks *= 2;
+  if (J <= 16)
+    launch_stream_ks<kXCols, kOutJI, 1>(args, blocks, ks, stream);
+  else
+    launch_stream_ks<kXCols, kOutJI, 2>(args, blocks, ks, stream);
+  return check(hipGetLastError(), "gemm_f32 streaming launch");
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int kMinWaves, bool kVecOnly = false, int KS = 1>
 int launch_config(GemmArgs& args, bool trans_b, bool vec, hipStream_t stream) {
   args.tiles_m = (args.m + BM - 1) / BM;

@@ -114,10 +114,10 @@ def test_matmul_direct64_kn_b_k_tail_isolation(cx):
                                    ((8192, 1000), (1000, 4)), ((4, 1000), (1000, 8192)),
                                    ((999, 1001), (1001, 1003))])
 def test_matmul_direct64_batched(cx, sa, sb):
-    # Batched 64x64-tile shapes, skinny shapes (a 4-wide n or m, which run
-    # the small kernel's 32x32 tiles: all but 4 rows or columns of each tile
-    # past the edge), and an unaligned k (1001) that takes the
-    # register-staged 64x64 tile instead.
+    # Batched 64x64-tile shapes, skinny shapes (a 4-wide n runs the
+    # streaming kernel, a 4-wide m with a [k, n] B the small kernel's 32x32
+    # tiles, all but 4 rows of each tile past the edge), and an unaligned k
+    # (1001) that takes the register-staged 64x64 tile instead.
     rng = np.random.default_rng(15)
     a = rng.standard_normal(sa).astype(np.float32)
     b = rng.standard_normal(sb).astype(np.float32)
@@ -127,7 +127,9 @@ def test_matmul_direct64_batched(cx, sa, sb):
 
 # Shapes of fewer than 128 output tiles of 64x64 with 16-byte rows run the
 # register-direct small kernel: 32x32 tiles, the K split over 1 to 16 waves
-# (one 16-k chunk per wave at least), edges through buffer range checks.
+# (one 16-k chunk per wave at least), edges through buffer range checks
+# ((16384, 512) x (512, 4), 4 columns against 16384 rows, runs the streaming
+# kernel).
 @pytest.mark.parametrize("sa,sb", [((1, 4), (4, 4)), ((31, 4), (4, 36)), ((33, 20), (20, 36)),
                                    ((100, 300), (300, 200)), ((64, 4096), (4096, 64)), ((2, 3, 60), (60, 40)),
                                    ((7, 33, 68), (68, 12)), ((500, 600), (600, 400)), ((512, 512), (512, 512)),
@@ -141,13 +143,15 @@ def test_matmul_small_kernel(cx, sa, sb):
     assert_matmul(actual, np.matmul(a.astype(np.float64), b.astype(np.float64)), a, b, f"small {sa}x{sb}")
 
 
-def test_linear_small_kernel_skinny(cx):
-    # 512 output tiles of 32x32 (eight waves per tile) for a transposed B.
+def test_matmul_small_kernel_skinny_batched(cx):
+    # 64 batches of 200 x 4 outputs: 256 tiles of 64x64, mostly padding, so
+    # the small kernel's 32x32 tiles (eight waves each) take them; 200 rows
+    # per batch are too few for the streaming kernel.
     rng = np.random.default_rng(24)
-    x = rng.standard_normal((16384, 512)).astype(np.float32)
-    w = rng.standard_normal((4, 512)).astype(np.float32)
-    actual = cx.linear(cx.tensor(x, device="hip"), cx.tensor(w, device="hip")).numpy()
-    assert_matmul(actual, x.astype(np.float64) @ w.astype(np.float64).T, x, w.T, "small linear skinny")
+    a = rng.standard_normal((64, 200, 512)).astype(np.float32)
+    b = rng.standard_normal((64, 512, 4)).astype(np.float32)
+    actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    assert_matmul(actual, np.matmul(a.astype(np.float64), b.astype(np.float64)), a, b, "small skinny batched")
 
 
 def test_matmul_random_shapes_every_route(cx):
@@ -227,6 +231,92 @@ def test_linear_small_kernel_bias_activation(cx, k):
     gelu = cx.hip.linear_act(xh, wh, bh, "gelu").numpy()
     expected = 0.5 * z * (1.0 + np.tanh(0.7978845608028654 * (z + 0.044715 * z ** 3)))
     assert np.max(np.abs(gelu - expected)) <= bound
+
+
+# One skinny operand against a long one (at least 256 rows) runs the
+# streaming kernel: at most 32 rows of A against a transposed B (a linear), or
+# at most 32 columns of B in either layout. The long operand's rows are read
+# once, 16 per block, K split over 1 to 16 waves; rows past the edge and k
+# past K read zero. 33 rows (and columns) are the first past it.
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (5, 1000, 300), (16, 256, 4), (17, 4100, 1028),
+                                   (32, 2048, 64), (32, 300, 8), (33, 3000, 516), (2, 11008, 512)])
+def test_linear_streaming_skinny_rows(cx, m, n, k):
+    rng = np.random.default_rng(40 + m)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    xh, wh, bh = (cx.tensor(v, device="hip") for v in (x, w, bias))
+    exact = x.astype(np.float64) @ w.astype(np.float64).T
+    assert_matmul(cx.linear(xh, wh).numpy(), exact, x, w.T, f"streaming linear {m}x{n}x{k}")
+    z = exact + bias
+    bound = 1.1e-4 * np.sqrt(k) * np.sqrt(np.mean(x * x)) * np.sqrt(np.mean(w * w)) + 1e-6
+    silu = cx.hip.linear_act(xh, wh, bh, "silu").numpy()
+    assert np.max(np.abs(silu - z / (1.0 + np.exp(-z)))) <= bound
+
+
+@pytest.mark.parametrize("sa,sb", [((4096, 4096), (4096, 1)), ((1000, 300), (300, 7)), ((300, 16), (16, 32)),
+                                   ((3, 500, 68), (3, 68, 20)), ((2, 1, 400, 132), (3, 132, 28)),
+                                   ((8192, 1000), (1000, 4)), ((257, 4100), (4100, 17)), ((600, 200), (200, 33))])
+def test_matmul_streaming_skinny_columns(cx, sa, sb):
+    # [k, n] B of at most 64 columns (its rows read as columns of the skinny
+    # operand), batches with broadcast, and the same shapes as a linear with
+    # the weight [n, k].
+    rng = np.random.default_rng(50 + sb[-1])
+    a = rng.standard_normal(sa).astype(np.float32)
+    b = rng.standard_normal(sb).astype(np.float32)
+    actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    assert_matmul(actual, np.matmul(a.astype(np.float64), b.astype(np.float64)), a, b, f"streaming {sa}x{sb}")
+    if b.ndim == 2:
+        w = np.ascontiguousarray(b.T)
+        lin = cx.linear(cx.tensor(a, device="hip"), cx.tensor(w, device="hip")).numpy()
+        assert_matmul(lin, np.matmul(a.astype(np.float64), b.astype(np.float64)), a, b, f"streaming linear {sa}")
+
+
+def test_streaming_k_tail_and_row_isolation(cx):
+    # K = 60: the last 16-k chunk spans k 48..63; k 60..63 of a row are the
+    # next row's first values (and past the last row, memory past the
+    # operand). Infinities there must read as zero, not 0 * inf, and still
+    # reach their own outputs as the float64 sums give them.
+    rng = np.random.default_rng(60)
+    x = rng.standard_normal((9, 60)).astype(np.float32)
+    w = rng.standard_normal((300, 60)).astype(np.float32)
+    w[5, 0:4] = np.inf       # row 4's tail would read these
+    x[3, 0:4] = -np.inf      # x row 2's tail would read these
+    with np.errstate(invalid="ignore"):
+        truth = x.astype(np.float64) @ w.astype(np.float64).T
+    lin = cx.linear(cx.tensor(x, device="hip"), cx.tensor(w, device="hip")).numpy()
+    assert np.array_equal(np.isnan(lin), np.isnan(truth))
+    assert np.array_equal(np.isinf(lin), np.isinf(truth))
+    assert np.all(np.isfinite(lin[2, :5])) and np.all(np.isfinite(lin[:3, 4]))
+    rows = [0, 1, 2, 4, 5, 6, 7, 8]
+    cols = np.setdiff1d(np.arange(300), [5])
+    assert_matmul(lin[np.ix_(rows, cols)], truth[np.ix_(rows, cols)], x[rows], w[cols].T, "streaming finite part")
+    # Skinny columns of a [k, n] B: A rows stream, B's columns are gathered.
+    a = rng.standard_normal((400, 60)).astype(np.float32)
+    a[11, 0:4] = np.inf      # row 10's tail would read these
+    b = rng.standard_normal((60, 12)).astype(np.float32)
+    with np.errstate(invalid="ignore"):
+        t2 = a.astype(np.float64) @ b.astype(np.float64)
+    got = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(t2)) and np.all(np.isfinite(got[10]))
+    keep = np.setdiff1d(np.arange(400), [11])
+    assert_matmul(got[keep], t2[keep], a[keep], b, "streaming columns finite part")
+
+
+def test_streaming_dyadic_exact(cx):
+    # Exact in any summation order: pins the streaming kernel's k mapping,
+    # row placement and wave-ordered combine bit for bit, in all three roles.
+    i = np.arange(40 * 1000)
+    x = ((i % 11 - 5) / 8).astype(np.float32).reshape(40, 1000)
+    j = np.arange(1000 * 600)
+    w = ((j % 7 - 3) / 16).astype(np.float32).reshape(600, 1000)
+    truth = (x.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32)
+    lin = cx.linear(cx.tensor(x, device="hip"), cx.tensor(w, device="hip")).numpy()
+    assert_bits(lin, truth, "streaming dyadic linear")
+    got = cx.matmul(cx.tensor(w, device="hip"), cx.tensor(np.ascontiguousarray(x.T), device="hip")).numpy()
+    assert_bits(got, np.ascontiguousarray(truth.T), "streaming dyadic columns")
+    lin2 = cx.linear(cx.tensor(w, device="hip"), cx.tensor(x, device="hip")).numpy()
+    assert_bits(lin2, np.ascontiguousarray(truth.T), "streaming dyadic linear columns")
 
 
 def test_matmul_small_kernel_dyadic_exact(cx):
