@@ -51,17 +51,25 @@ bool direct128_fits(const tcx_hip_gemm_desc_t* d, std::int64_t batches) {
 
 // K split of the direct 128x128 kernel for shapes with fewer than 256 full
 // 128x128 tiles and a long K: the smallest power of two that gives >= 512
-// items (two blocks per CU; at most 16 splits), when every split keeps >= 512
-// of K in whole k-tiles. 1 = none. (First built on 256x256 tiles with a
-// 256-block target: 1024x1024x8192 546 -> 261 us at 8 splits.)
+// items (two blocks per CU; at most 16 splits) when every split keeps >= 384
+// of K in whole k-tiles, else the smallest split count that gives >= 384
+// items under the same rule. 1 = none. (First built on 256x256 tiles with a
+// 256-block target: 1024x1024x8192 546 -> 261 us at 8 splits.) Swept over
+// split counts 1-8 on MI355X: the 384 floor (512 before) and the fallback
+// took 1536^3 88.7 -> 81.5 us (4 splits), 2048x1536x1536 90.2 -> 84.3 (4),
+// 1792^3 148.8 -> 121.5 (4), and left 1024^3 (no split), 1024x1024x2048
+// (no split) and the other measured shapes as they were.
 std::int64_t gemm_splits(const tcx_hip_gemm_desc_t* d, std::int64_t batches) {
   if (!gemm::direct_fits<128, 128, 32>(d->m, d->n, d->k) || d->n % 4 != 0) return 1;
   if (direct128_fits(d, batches)) return 1;
   const std::int64_t tiles = (d->m / 128) * (d->n / 128) * batches;
+  auto whole = [&](std::int64_t splits) { return d->k % (32 * splits) == 0 && d->k / splits >= 384; };
   std::int64_t splits = 1;
   while (tiles * splits < 512 && splits < 16) splits *= 2;
-  if (splits == 1 || d->k % (32 * splits) != 0 || d->k / splits < 512) return 1;
-  return splits;
+  if (splits > 1 && whole(splits)) return splits;
+  for (splits = 2; splits <= 16; ++splits)
+    if (tiles * splits >= 384 && whole(splits)) return splits;
+  return 1;
 }
 
 std::int64_t batch_product(const tcx_hip_gemm_desc_t* d) {
