@@ -24,6 +24,8 @@
 // which the parity bound max|dC| <= 1e-4 * sqrt(K) * rms(A) * rms(B) covers.
 
 
+#include <cmath>
+
 #include "gemm_kernel.hpp"
 
 namespace tcx {
@@ -59,11 +61,29 @@ bool direct128_fits(const tcx_hip_gemm_desc_t* d, std::int64_t batches) {
 // took 1536^3 88.7 -> 81.5 us (4 splits), 2048x1536x1536 90.2 -> 84.3 (4),
 // 1792^3 148.8 -> 121.5 (4), and left 1024^3 (no split), 1024x1024x2048
 // (no split) and the other measured shapes as they were.
+//   With >= 256 full tiles the unsplit direct kernel runs them in rounds of
+// 256 CUs, and a last round that leaves most CUs idle is worth splitting
+// K: the split count s in {1, 2, 3, 4, 8} (>= 384 of K in whole k-tiles per
+// split) minimising idle(T s / 256) + 0.02 s, where idle(x) = (ceil(x) - x)
+// / ceil(x) is the share of the last round left idle and 0.02 s charges the
+// partial tiles' traffic. The constants fit a sweep of s = 1-8 on MI355X:
+// 3072^3 522 -> 438 us (s = 4), 2304x2304x4096 468 -> 362 (2),
+// 3072x2048x2048 238 -> 194 (2), 2560^3 295 -> 288 (4); 4096x3072x1024
+// (three full rounds) stays unsplit, 183 against 213 us with s = 2.
 std::int64_t gemm_splits(const tcx_hip_gemm_desc_t* d, std::int64_t batches) {
   if (!gemm::direct_fits<128, 128, 32>(d->m, d->n, d->k) || d->n % 4 != 0) return 1;
-  if (direct128_fits(d, batches)) return 1;
   const std::int64_t tiles = (d->m / 128) * (d->n / 128) * batches;
   auto whole = [&](std::int64_t splits) { return d->k % (32 * splits) == 0 && d->k / splits >= 384; };
+  if (direct128_fits(d, batches)) {
+    auto cost = [&](std::int64_t splits) {
+      const double x = static_cast<double>(tiles * splits) / 256.0, rounds = std::ceil(x);
+      return (rounds - x) / rounds + 0.02 * static_cast<double>(splits);
+    };
+    std::int64_t best = 1;
+    for (const std::int64_t splits : {2, 3, 4, 8})
+      if (whole(splits) && cost(splits) < cost(best) - 1e-9) best = splits;
+    return best;
+  }
   std::int64_t splits = 1;
   while (tiles * splits < 512 && splits < 16) splits *= 2;
   if (splits > 1 && whole(splits)) return splits;
@@ -173,15 +193,8 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
   const std::int64_t tiles_256 = ((d->m + 255) / 256) * ((d->n + 255) / 256) * batches;
   // (Unaligned shapes take the scalar-load variant, which does not fit the
   // 256x256 tile's registers; they use the 128x128 tile.)
-  // Full 128x128 tiles, >= 256 of them: the direct-to-LDS kernel (see
-  // direct128_fits).
-  if (vec && direct128_fits(d, batches)) {
-    if (trans_b) return gemm::launch_direct<128, 128, 32, 64, 32, 2>(args, true, s);
-    return gemm::launch_direct<128, 128, 32, 32, 64, 2>(args, false, s);
-  }
-  // Fewer full tiles and a long K: split K over several blocks of the direct
-  // 128x128 kernel when the caller brought the workspace
-  // (tcx_hip_gemm_workspace_bytes).
+  // K split over several blocks of the direct 128x128 kernel (gemm_splits)
+  // when the caller brought the workspace (tcx_hip_gemm_workspace_bytes).
   if (vec && workspace != nullptr && aligned16(workspace)) {
     const std::int64_t splits = gemm_splits(d, batches);
     const size_t need = static_cast<size_t>(splits * batches * d->m * d->n) * sizeof(float);
@@ -191,6 +204,12 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
       if (trans_b) return gemm::launch_direct<128, 128, 32, 64, 32, 2>(args, true, s);
       return gemm::launch_direct<128, 128, 32, 32, 64, 2>(args, false, s);
     }
+  }
+  // Full 128x128 tiles, >= 256 of them: the direct-to-LDS kernel (see
+  // direct128_fits).
+  if (vec && direct128_fits(d, batches)) {
+    if (trans_b) return gemm::launch_direct<128, 128, 32, 64, 32, 2>(args, true, s);
+    return gemm::launch_direct<128, 128, 32, 32, 64, 2>(args, false, s);
   }
   if (vec && tiles_256 >= 256) return launch_config<256, 256, 32, 64, 128, 2, true>(args, trans_b, true, s);
   // 128x128 tiles when there are >= 256 of them and the last round of 256

@@ -53,7 +53,9 @@ def test_library_exports_every_declared_symbol():
     (2048, 1024, 4096, (), True, 4 * 2048 * 1024 * 4),   # 128 tiles of 128x128: 4 splits
     (1024, 1024, 8192, (), False, 8 * 1024 * 1024 * 4),   # 64 tiles: 8 splits of 1024
     (512, 512, 8192, (4,), False, 8 * 4 * 512 * 512 * 4),  # batched: 64 tiles
-    (4096, 4096, 4096, (), False, 0),                     # 256 tiles already
+    (4096, 4096, 4096, (), False, 0),                     # four full rounds of 256 tiles
+    (3072, 3072, 3072, (), False, 4 * 3072 * 3072 * 4),   # 576 tiles: the third round 1/4 full
+    (4096, 3072, 1024, (), True, 0),                      # 768 tiles: three full rounds
     (1000, 1000, 1000, (), False, 0),                     # partial tiles
     (1024, 1024, 1024, (), False, 0),                     # splits would keep < 512 of K
     (512, 512, 16384, (), False, 16 * 512 * 512 * 4),     # 16 tiles: the 16-split cap

@@ -333,10 +333,13 @@ def test_matmul_small_kernel_dyadic_exact(cx):
 
 
 @pytest.mark.parametrize("sa,sb", [((1024, 8192), (8192, 1024)), ((2048, 4096), (4096, 2048)),
-                                   ((4, 512, 8192), (4, 8192, 512))])
+                                   ((4, 512, 8192), (4, 8192, 512)), ((3072, 2048), (2048, 2048)),
+                                   ((1536, 1536), (1536, 1536))])
 def test_matmul_split_k(cx, sa, sb):
-    # Few output tiles and a long K: K split over blocks through the pool
-    # workspace, checked against float64 truth at the matmul bar.
+    # Few output tiles and a long K, or a last round of tiles that would leave
+    # most CUs idle (3072 x 2048: 384 tiles, two splits; 1536^3: 144 tiles,
+    # four splits): K split over blocks through the pool workspace, checked
+    # against float64 truth at the matmul bar.
     rng = np.random.default_rng(11)
     a = rng.standard_normal(sa).astype(np.float32)
     b = rng.standard_normal(sb).astype(np.float32)
