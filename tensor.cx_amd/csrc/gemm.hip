@@ -55,8 +55,9 @@ bool direct128_fits(const tcx_hip_gemm_desc_t* d, std::int64_t batches) {
 // 128x128 tiles and a long K: the smallest power of two that gives >= 512
 // items (two blocks per CU; at most 16 splits) when every split keeps >= 384
 // of K in whole k-tiles, else the smallest split count that gives >= 384
-// items under the same rule. 1 = none. (First built on 256x256 tiles with a
-// 256-block target: 1024x1024x8192 546 -> 261 us at 8 splits.) Swept over
+// items under the same rule (else see below). 1 = none. (First built on
+// 256x256 tiles with a 256-block target: 1024x1024x8192 546 -> 261 us at 8
+// splits.) Swept over
 // split counts 1-8 on MI355X: the 384 floor (512 before) and the fallback
 // took 1536^3 88.7 -> 81.5 us (4 splits), 2048x1536x1536 90.2 -> 84.3 (4),
 // 1792^3 148.8 -> 121.5 (4), and left 1024^3 (no split), 1024x1024x2048
@@ -89,6 +90,13 @@ std::int64_t gemm_splits(const tcx_hip_gemm_desc_t* d, std::int64_t batches) {
   if (splits > 1 && whole(splits)) return splits;
   for (splits = 2; splits <= 16; ++splits)
     if (tiles * splits >= 384 && whole(splits)) return splits;
+  // Failing both, with fewer 64x64 tiles than CUs for the unsplit kernels,
+  // the most splits that still give >= 256 items (128 x 4096 x 4096: 32
+  // tiles, 8 splits, 72.2 -> 43.4 us transposed; 1024 x 1024 x 2048, whose
+  // 256 64x64 tiles fill the CUs, stays unsplit: 40.3 against 42.7 us).
+  if (tiles * 4 < 256)
+    for (splits = 16; splits >= 2; --splits)
+      if (tiles * splits >= 256 && whole(splits)) return splits;
   return 1;
 }
 
