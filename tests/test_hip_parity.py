@@ -183,6 +183,42 @@ def test_matmul_random_shapes_every_route(cx):
     assert not failures, "\n".join(failures[:10])
 
 
+def test_matmul_random_streaming_and_split_routes(cx):
+    # Seeded random shapes aimed at the streaming kernel (one side of at most
+    # 32 against 256+ rows, both B layouts, batches) and at the K splits
+    # (multiples of 128 with few tiles or a badly filled last round), each
+    # against float64 truth at the matmul bar.
+    rng = np.random.default_rng(26)
+    failures = []
+    for case in range(40):
+        kind = case % 4
+        k = 4 * int(rng.integers(1, 600))
+        if kind == 0:    # linear with at most 32 rows of x
+            m, n = int(rng.integers(1, 33)), int(rng.integers(256, 3000))
+        elif kind == 1:  # at most 32 columns of B
+            m, n = int(rng.integers(256, 3000)), int(rng.integers(1, 33))
+        elif kind == 2:  # few 128x128 tiles, long K: split K
+            m, n, k = 128 * int(rng.integers(1, 9)), 128 * int(rng.integers(1, 9)), 128 * int(rng.integers(8, 33))
+        else:            # 256+ tiles with a partial last round
+            m, n, k = 128 * int(rng.integers(16, 24)), 128 * int(rng.integers(16, 24)), 128 * int(rng.integers(3, 7))
+        batch = int(rng.integers(2, 4)) if case % 5 == 3 and kind != 3 else 0
+        lead = (batch,) if batch else ()
+        a = rng.standard_normal(lead + (m, k)).astype(np.float32)
+        if kind == 0:
+            w = rng.standard_normal((n, k)).astype(np.float32)
+            got = cx.linear(cx.tensor(a, device="hip"), cx.tensor(w, device="hip")).numpy()
+            b = w.T
+        else:
+            b = rng.standard_normal(lead + (k, n)).astype(np.float32)
+            got = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+        truth = np.matmul(a.astype(np.float64), b.astype(np.float64))
+        try:
+            assert_matmul(got, truth, a, b, f"case {case}: a {a.shape} b {b.shape} kind {kind}")
+        except AssertionError as error:
+            failures.append(str(error))
+    assert not failures, "\n".join(failures[:10])
+
+
 def test_matmul_small_kernel_k_tail_isolation(cx):
     # K = 60: each row's last 16-k chunk spans k 48..63, and k 60..63 of a
     # [k, n] B are the next batch's rows 0..3, of an A row the next row's
