@@ -182,6 +182,19 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
   // (1000^3), else 32x32 blocks of eight one-wave groups with 32-wide k-tiles
   // (small shapes; 512^3: 17.9 -> 11.8 us). The in-block split gained 7 % on
   // 4096x1024x4096 and 21 % on 1000^3 over the same tiles without it.
+  // One row of A against a transposed B, or one column of B: a
+  // matrix-vector product, the long operand's rows streamed in whole cache
+  // lines (one or no batch axis).
+  if (d->batch_rank <= 1 && strides_vec && d->k % 4 == 0 && aligned16(lhs) && aligned16(rhs)) {
+    const std::int64_t lbs = d->batch_rank == 1 ? d->lhs_batch_strides[0] : 0;
+    const std::int64_t rbs = d->batch_rank == 1 ? d->rhs_batch_strides[0] : 0;
+    if (trans_b && d->m == 1)
+      return gemm::launch_gemv(rhs, lhs, out, d->bias, d->n, d->k, batches, rbs, lbs, d->n, 1, true,
+                               d->activation, s);
+    if (d->n == 1)
+      return gemm::launch_gemv(lhs, rhs, out, d->bias, d->m, d->k, batches, lbs, rbs, d->m, 1, false,
+                               d->activation, s);
+  }
   // One skinny operand against a long one: at most 32 rows of A against a
   // transposed B (the decode-time linear x W^T), or at most 32 columns of B.
   // The streaming kernel reads the long operand's rows once, 16 per block.

@@ -1342,6 +1342,95 @@ __global__ __launch_bounds__(64 * KS) void gemm_f32_stream_kernel(GemmArgs a) {
   }
 }
 
+// Matrix-vector products: y[i] = act(dot(R[i], v) + bias) for every row i of
+// a row-major R [I, K], batched. The decode-time linear x W^T with one row of
+// x (R = W, v = x, y = that row of the output), and A b with one column of b
+// (R = A, v = b, y = that column). Lanes stream K in 16-byte loads, so one
+// wave instruction reads 1 KB of one row (eight whole 128-byte lines; the
+// MFMA operand layout of gemm_f32_stream_kernel reads 16 rows x 64 B per
+// instruction). KW waves of a 4-wave block split a row's K into contiguous
+// runs (KW = 1, 2 or 4, more when rows are few); lane sums add in a fixed
+// tree, the waves' in wave order. Eight loads per lane in flight. v is
+// contiguous (a row of x, or the column of a [k, 1] b); y_stride is the
+// element stride of y in the output; bias is per row (bias_per_row) or one
+// value.
+template <int KW>
+__global__ __launch_bounds__(256) void gemv_f32_kernel(const float* __restrict__ R, const float* __restrict__ v,
+                                                       float* __restrict__ y, const float* __restrict__ bias,
+                                                       std::int64_t rows, std::int64_t K, std::int64_t batches,
+                                                       std::int64_t r_batch, std::int64_t v_batch,
+                                                       std::int64_t y_batch, std::int64_t y_stride, int bias_per_row,
+                                                       int act) {
+  constexpr int kRowsPerBlock = 4 / KW;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int part = wave % KW;
+  const std::int64_t row_in_grid = static_cast<std::int64_t>(blockIdx.x) * kRowsPerBlock + wave / KW;
+  const std::int64_t batch = row_in_grid / rows, i = row_in_grid % rows;
+  __shared__ float partial[4];
+  float sum = 0.F;
+  if (batch < batches) {
+    const float* __restrict__ rp = R + batch * r_batch + i * K;
+    const float* __restrict__ vp = v + batch * v_batch;
+    // This wave's run of K: whole 1024-element strides first, 4-element
+    // groups after (K % 4 == 0).
+    const std::int64_t run = (K / 4 + KW - 1) / KW * 4;
+    const std::int64_t k_begin = part * run, k_end = min(K, k_begin + run);
+    float s[8] = {};
+    std::int64_t k = k_begin + 4 * lane;
+    for (; k + 7 * 256 < k_end; k += 8 * 256) {
+      float4_t w[8], x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) w[u] = stream_load(reinterpret_cast<const float4_t*>(rp + k + 256 * u));
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = *reinterpret_cast<const float4_t*>(vp + k + 256 * u);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s[u] += (w[u].x * x[u].x + w[u].y * x[u].y) + (w[u].z * x[u].z + w[u].w * x[u].w);
+    }
+    for (; k < k_end; k += 256) {
+      const float4_t w = stream_load(reinterpret_cast<const float4_t*>(rp + k));
+      const float4_t x = *reinterpret_cast<const float4_t*>(vp + k);
+      s[0] += (w.x * x.x + w.y * x.y) + (w.z * x.z + w.w * x.w);
+    }
+    sum = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+  }
+  sum = wave_sum(sum);
+  if constexpr (KW > 1) {
+    if (lane == 0) partial[wave] = sum;
+    __syncthreads();
+    if (part != 0 || lane != 0 || batch >= batches) return;
+    sum = partial[wave];
+#pragma unroll
+    for (int w = 1; w < KW; ++w) sum += partial[wave + w];
+  } else {
+    if (lane != 0 || batch >= batches) return;
+  }
+  if (bias != nullptr) sum = sum + bias[bias_per_row ? i : 0];
+  y[batch * y_batch + i * y_stride] = activate(sum, act);
+}
+
+// rows x batches dot products of K (K % 4 == 0, R, v and every batch offset
+// 16-byte aligned): KW waves per row, more when rows are few.
+inline int launch_gemv(const float* R, const float* v, float* y, const float* bias, std::int64_t rows,
+                       std::int64_t K, std::int64_t batches, std::int64_t r_batch, std::int64_t v_batch,
+                       std::int64_t y_batch, std::int64_t y_stride, bool bias_per_row, int act, hipStream_t stream) {
+  const std::int64_t total = rows * batches;
+  const int kw = total >= 4096 ? 1 : total >= 2048 ? 2 : 4;
+  const std::int64_t blocks = (total * kw + 3) / 4;
+  if (blocks > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
+  const dim3 grid(static_cast<unsigned>(blocks));
+  const int bpr = bias_per_row ? 1 : 0;
+  if (kw == 1)
+    hipLaunchKernelGGL(gemv_f32_kernel<1>, grid, dim3(256), 0, stream, R, v, y, bias, rows, K, batches, r_batch,
+                       v_batch, y_batch, y_stride, bpr, act);
+  else if (kw == 2)
+    hipLaunchKernelGGL(gemv_f32_kernel<2>, grid, dim3(256), 0, stream, R, v, y, bias, rows, K, batches, r_batch,
+                       v_batch, y_batch, y_stride, bpr, act);
+  else
+    hipLaunchKernelGGL(gemv_f32_kernel<4>, grid, dim3(256), 0, stream, R, v, y, bias, rows, K, batches, r_batch,
+                       v_batch, y_batch, y_stride, bpr, act);
+  return check(hipGetLastError(), "gemv launch");
+}
+
 // Skinny rows or columns the streaming kernel takes: up to two row groups.
 // With four (33-64) its MFMAs outweigh the streamed bytes and the tiled
 // kernels were faster (48x4096x4096 transposed: 38.1 against 34.3 us).

@@ -308,6 +308,55 @@ def test_matmul_streaming_skinny_columns(cx, sa, sb):
         assert_matmul(lin, np.matmul(a.astype(np.float64), b.astype(np.float64)), a, b, f"streaming linear {sa}")
 
 
+@pytest.mark.parametrize("n,k", [(4096, 4096), (1, 4), (7, 4100), (300, 8), (2000, 1028), (11008, 512),
+                                 (5000, 64)])
+def test_gemv_one_row_and_one_column(cx, n, k):
+    # One row of x against a weight [n, k] (the decode-time linear), and one
+    # column of B in both layouts: rows streamed in whole cache lines, K
+    # split over 1, 2 or 4 waves by the row count.
+    rng = np.random.default_rng(70 + n)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    xh, wh, bh = (cx.tensor(v, device="hip") for v in (x, w, bias))
+    exact = x.astype(np.float64) @ w.astype(np.float64).T
+    assert_matmul(cx.linear(xh, wh).numpy(), exact, x, w.T, f"gemv linear {n}x{k}")
+    z = exact + bias
+    bound = 1.1e-4 * np.sqrt(k) * np.sqrt(np.mean(x * x)) * np.sqrt(np.mean(w * w)) + 1e-6
+    gelu = cx.hip.linear_act(xh, wh, bh, "gelu").numpy()
+    expected = 0.5 * z * (1.0 + np.tanh(0.7978845608028654 * (z + 0.044715 * z ** 3)))
+    assert np.max(np.abs(gelu - expected)) <= bound
+    col = np.ascontiguousarray(x.T)
+    got = cx.matmul(wh, cx.tensor(col, device="hip")).numpy()
+    assert_matmul(got, w.astype(np.float64) @ col.astype(np.float64), w, col, f"gemv column {n}x{k}")
+    got_t = cx.linear(wh, xh).numpy()
+    assert_matmul(got_t, w.astype(np.float64) @ col.astype(np.float64), w, col, f"gemv column linear {n}x{k}")
+
+
+def test_gemv_batched_and_special_values(cx):
+    # A batch axis on both operands and broadcast on one; a NaN and an inf in
+    # one row each, and a dyadic case that must be exact in any order.
+    rng = np.random.default_rng(77)
+    a = rng.standard_normal((3, 500, 260)).astype(np.float32)
+    b = rng.standard_normal((3, 260, 1)).astype(np.float32)
+    a[1, 7, 100] = np.nan
+    a[2, 9, 3] = np.inf
+    got = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    with np.errstate(invalid="ignore"):
+        truth = np.matmul(a.astype(np.float64), b.astype(np.float64))
+    assert np.array_equal(np.isnan(got), np.isnan(truth)) and np.array_equal(np.isinf(got), np.isinf(truth))
+    finite = np.isfinite(truth)
+    assert np.max(np.abs(got[finite] - truth[finite])) <= 1e-4 * np.sqrt(260) * 1.1
+    shared = rng.standard_normal((260, 1)).astype(np.float32)
+    got2 = cx.matmul(cx.tensor(a[0:1], device="hip"), cx.tensor(shared, device="hip")).numpy()
+    assert_matmul(got2[0], a[0].astype(np.float64) @ shared.astype(np.float64), a[0], shared, "gemv broadcast")
+    i = np.arange(3000 * 1000)
+    w = ((i % 11 - 5) / 8).astype(np.float32).reshape(3000, 1000)
+    x = ((np.arange(1000) % 7 - 3) / 16).astype(np.float32).reshape(1, 1000)
+    lin = cx.linear(cx.tensor(x, device="hip"), cx.tensor(w, device="hip")).numpy()
+    assert_bits(lin, (x.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32), "gemv dyadic")
+
+
 def test_streaming_k_tail_and_row_isolation(cx):
     # K = 60: the last 16-k chunk spans k 48..63; k 60..63 of a row are the
     # next row's first values (and past the last row, memory past the
