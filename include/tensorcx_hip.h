@@ -216,16 +216,17 @@ int tcx_hip_reduce(int op, int dtype, const void* x, void* out, int64_t outer, i
 /* tcx_hip_reduce without a workspace, for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc); it has no counterpart in the reference. It runs the kernels of
- * tcx_hip_reduce with the partials of split-row plans (few long rows, e.g. a
- * full-tensor sum) in a static per-device scratch of 256 KiB, held
- * until the process ends, so its results are bit-identical to
+ * tcx_hip_reduce with the partials of split plans (few long rows, e.g. a
+ * full-tensor sum; few columns over many rows) in a static per-device
+ * scratch of 4 MiB, held until the process ends, so its results are
+ * bit-identical to
  * tcx_hip_reduce's. Plans are accepted when tcx_hip_reduce_workspace_bytes is
  * at most TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE (else TCX_INVALID_ARGUMENT),
  * which holds for every float32 or int32 input that fits in 288 GB. All calls
  * on one GPU share the scratch: calls that overlap in time on one GPU (other
  * streams, other threads) race and must be serialised by the caller. It
  * never allocates. */
-#define TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE 262144
+#define TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE 4194304
 int tcx_hip_reduce_noalloc(int op, int dtype, const void* x, void* out, int64_t outer, int64_t reduce,
                            int64_t inner, tcx_stream_t stream);
 

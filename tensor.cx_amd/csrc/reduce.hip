@@ -10,8 +10,10 @@
 // max/min/argmax and int32 sums are order-free under these rules, so the
 // parallel paths are bit-exact. A float32 sum depends on order: rows longer
 // than kSequentialMax use a fixed tree order (per-lane strided partials, then a
-// butterfly), shorter rows and strided (inner > 1) reductions keep the
-// reference's exact left-to-right order, one lane per output.
+// butterfly), strided (inner > 1) reductions of more than kSequentialMax rows
+// a fixed blocked order (sequential runs of rows, folded in row order), and
+// shorter reductions keep the reference's exact left-to-right order, one lane
+// per output.
 //
 // Paths:
 //   row_kernel         inner == 1, long rows: wave segments reduced by one
@@ -21,6 +23,10 @@
 //                      split into more items when there are too few rows to
 //                      fill the GPU (partials in workspace)
 //   finish_kernel      combines per-row item partials in a fixed order
+//   col_kernel         inner > 1, more than kSequentialMax rows: a block per
+//                      tile of 64 or 256 columns, its waves folding runs of
+//                      rows (rows split over blocks when tiles are few)
+//   col_finish_kernel  combines the column splits' partials in split order
 //   lane_kernel        one lane per output, reference element order
 //   axes_kernel        any axis selection through reduction-plan metadata
 
@@ -490,6 +496,191 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(const Partial* _
   }
 }
 
+// ------------------------------------------------------- strided path
+// Reductions over a middle axis (inner > 1) of more than kSequentialMax rows,
+// x as [outer, R, inner]: the R elements of one output lie inner elements
+// apart. One block of kColWaves waves per column tile (64 x kVec consecutive
+// columns of one outer index; a lane holds kVec columns, so a wave reads 256
+// or 1024 contiguous bytes of each row). When column tiles are too few to
+// fill the GPU, `splits` blocks share a tile's rows, in contiguous runs of
+// split_rows; inside a block each wave takes a contiguous run of the block's
+// rows. A lane folds its run in row order with kColDepth loads in flight; the
+// waves' results are folded in wave order through LDS and the splits' in
+// split order by col_finish_kernel. Extrema and int32 sums are exact in any
+// order; a float32 sum takes this blocked order (each run sequential, then
+// runs in row order).
+constexpr int kColWaves = 8;
+constexpr int kColDepth = 16;
+constexpr std::int64_t kColMaxGrid = std::int64_t{1} << 22;
+
+template <int kOp, typename T>
+__device__ __forceinline__ void fold_into(Partial& into, const Partial& c) {
+  constexpr bool kLargest = kOp != TCX_REDUCE_MIN;
+  if constexpr (kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN) {
+    if constexpr (__is_same(T, float))
+      into.bits = to_bits(from_bits<float>(into.bits) + from_bits<float>(c.bits));
+    else
+      into.bits += c.bits;
+  } else if (cand_better<T, kLargest>(from_bits<T>(c.bits), c.index, from_bits<T>(into.bits), into.index)) {
+    into = c;
+  }
+}
+
+// Output `id` from its fold over all R rows.
+template <int kOp, typename T>
+__device__ __forceinline__ void store_output(void* out, std::int64_t id, const Partial& r, std::int64_t R) {
+  if constexpr (kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN) {
+    if constexpr (__is_same(T, float)) {
+      const float v = from_bits<float>(r.bits);
+      static_cast<float*>(out)[id] = kOp == TCX_REDUCE_MEAN ? v / static_cast<float>(R) : v;
+    } else {
+      static_cast<int*>(out)[id] = static_cast<int>(r.bits);
+    }
+  } else if constexpr (kOp == TCX_REDUCE_ARGMAX) {
+    static_cast<int*>(out)[id] = static_cast<int>(r.index);
+  } else {
+    static_cast<T*>(out)[id] = from_bits<T>(r.bits);
+  }
+}
+
+template <typename T, int kVec>
+__device__ __forceinline__ void load_cols(const T* __restrict__ p, T (&v)[kVec]) {
+  if constexpr (kVec == 4) {
+    const vec4<T> q = stream_load(reinterpret_cast<const vec4<T>*>(p));
+    v[0] = q.x;
+    v[1] = q.y;
+    v[2] = q.z;
+    v[3] = q.w;
+  } else {
+    v[0] = stream_load(p);
+  }
+}
+
+template <int kOp, typename T, int kVec>
+__device__ __forceinline__ void col_block(const T* __restrict__ x, void* __restrict__ out,
+                                          Partial* __restrict__ partials, std::int64_t outer, std::int64_t R,
+                                          std::int64_t inner, std::int64_t split_rows, std::int64_t b,
+                                          Partial (&lds)[kColWaves][64 * kVec]) {
+  constexpr bool kSum = kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN;
+  constexpr bool kLargest = kOp != TCX_REDUCE_MIN;
+  constexpr int kTile = 64 * kVec;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const std::int64_t tiles_per_outer = (inner + kTile - 1) / kTile;
+  const std::int64_t col_tiles = outer * tiles_per_outer;
+  const std::int64_t split = b / col_tiles, tile = b % col_tiles;
+  const std::int64_t o = tile / tiles_per_outer, tile_col = (tile % tiles_per_outer) * kTile;
+  const std::int64_t j = tile_col + lane * kVec;
+  const std::int64_t rb = split * split_rows, re = min(R, rb + split_rows);
+  const std::int64_t per_wave = (re - rb + kColWaves - 1) / kColWaves;
+  const std::int64_t r0 = min(re, rb + wave * per_wave), r1 = min(re, r0 + per_wave);
+  // Lanes past the last column read the last kVec columns (in bounds: inner
+  // is a multiple of kVec) and their results are not stored.
+  const T* __restrict__ p = x + o * R * inner + (j < inner ? j : inner - kVec);
+  Partial acc[kVec];
+  if constexpr (kSum) {
+    using Acc = std::conditional_t<__is_same(T, float), float, std::uint32_t>;
+    Acc sum[kVec];
+#pragma unroll
+    for (int c = 0; c < kVec; ++c) sum[c] = 0;
+    std::int64_t r = r0;
+    for (; r + kColDepth <= r1; r += kColDepth) {
+      T v[kColDepth][kVec];
+#pragma unroll
+      for (int u = 0; u < kColDepth; ++u) load_cols<T, kVec>(p + (r + u) * inner, v[u]);
+#pragma unroll
+      for (int u = 0; u < kColDepth; ++u)
+#pragma unroll
+        for (int c = 0; c < kVec; ++c) sum[c] += static_cast<Acc>(v[u][c]);
+    }
+    for (; r < r1; ++r) {
+      T v[kVec];
+      load_cols<T, kVec>(p + r * inner, v);
+#pragma unroll
+      for (int c = 0; c < kVec; ++c) sum[c] += static_cast<Acc>(v[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < kVec; ++c) acc[c] = Partial{__builtin_bit_cast(std::uint32_t, sum[c]), 0U, 0};
+  } else {
+    // An empty run (more waves or splits than rows) gives empty candidates.
+#pragma unroll
+    for (int c = 0; c < kVec; ++c) acc[c] = Partial{0U, 0U, -1};
+    if (r0 < r1) {
+      T best[kVec];
+      std::int64_t bi[kVec];
+      load_cols<T, kVec>(p + r0 * inner, best);
+#pragma unroll
+      for (int c = 0; c < kVec; ++c) bi[c] = r0;
+      std::int64_t r = r0 + 1;
+      for (; r + kColDepth <= r1; r += kColDepth) {
+        T v[kColDepth][kVec];
+#pragma unroll
+        for (int u = 0; u < kColDepth; ++u) load_cols<T, kVec>(p + (r + u) * inner, v[u]);
+#pragma unroll
+        for (int u = 0; u < kColDepth; ++u)
+#pragma unroll
+          for (int c = 0; c < kVec; ++c)
+            if (lane_takes<T, kLargest>(v[u][c], best[c])) {
+              best[c] = v[u][c];
+              bi[c] = r + u;
+            }
+      }
+      for (; r < r1; ++r) {
+        T v[kVec];
+        load_cols<T, kVec>(p + r * inner, v);
+#pragma unroll
+        for (int c = 0; c < kVec; ++c)
+          if (lane_takes<T, kLargest>(v[c], best[c])) {
+            best[c] = v[c];
+            bi[c] = r;
+          }
+      }
+#pragma unroll
+      for (int c = 0; c < kVec; ++c) acc[c] = Partial{to_bits(best[c]), 0U, bi[c]};
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < kVec; ++c) lds[wave][lane * kVec + c] = acc[c];
+  __syncthreads();
+  // Threads 0 .. kTile-1 fold one column each over the waves, in wave order.
+  const int t = threadIdx.x;
+  if (t >= kTile || tile_col + t >= inner) return;
+  Partial total = lds[0][t];
+#pragma unroll
+  for (int w = 1; w < kColWaves; ++w) fold_into<kOp, T>(total, lds[w][t]);
+  const std::int64_t id = o * inner + tile_col + t;
+  if (split_rows >= R)
+    store_output<kOp, T>(out, id, total, R);
+  else
+    partials[split * outer * inner + id] = total;
+}
+
+template <int kOp, typename T, int kVec>
+__global__ __launch_bounds__(64 * kColWaves) void col_kernel(const T* __restrict__ x, void* __restrict__ out,
+                                                             Partial* __restrict__ partials, std::int64_t outer,
+                                                             std::int64_t R, std::int64_t inner,
+                                                             std::int64_t split_rows, std::int64_t blocks) {
+  constexpr int kTile = 64 * kVec;
+  __shared__ Partial lds[kColWaves][kTile];
+  // Block-stride over (split, tile) pairs: a grid of at most kColMaxGrid
+  // blocks keeps gridDim.x x blockDim.x inside 32 bits.
+  for (std::int64_t b = blockIdx.x; b < blocks; b += gridDim.x) {
+    col_block<kOp, T, kVec>(x, out, partials, outer, R, inner, split_rows, b, lds);
+    __syncthreads();  // lds is rewritten by the next pair
+  }
+}
+
+// Folds each output's split partials in split order.
+template <int kOp, typename T>
+__global__ __launch_bounds__(256) void col_finish_kernel(const Partial* __restrict__ partials, void* __restrict__ out,
+                                                         std::int64_t outputs, std::int64_t splits, std::int64_t R) {
+  const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * blockDim.x;
+  for (std::int64_t id = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; id < outputs; id += step) {
+    Partial total = partials[id];
+    for (std::int64_t sp = 1; sp < splits; ++sp) fold_into<kOp, T>(total, partials[sp * outputs + id]);
+    store_output<kOp, T>(out, id, total, R);
+  }
+}
+
 // ------------------------------------------------------ exact-order paths
 // Sequential per-output loop in the reference's element order.
 template <int kOp, typename T>
@@ -695,6 +886,38 @@ RowPlan plan_rows(std::int64_t outer, std::int64_t reduce, std::int64_t inner) {
 
 bool aligned16(const void* q) { return (reinterpret_cast<std::uintptr_t>(q) & 15U) == 0; }
 
+// Strided (inner > 1) reductions of more than kSequentialMax rows: column
+// tiles of 256 columns (inner a multiple of 4) or 64, and the rows of each
+// tile split `splits` ways when tiles are too few for kColTargetBlocks
+// blocks (two 8-wave blocks per CU on 256 CUs), keeping at least
+// kColMinRows rows per split and the split partials within the
+// no-allocation scratch.
+constexpr std::int64_t kColTargetBlocks = 512;
+constexpr std::int64_t kColMinRows = 128;
+
+struct ColPlan {
+  bool col_path;
+  std::int64_t splits;      // > 1: partials in workspace, folded by col_finish_kernel
+  std::int64_t split_rows;  // rows per split (the last may be shorter)
+};
+
+ColPlan plan_cols(std::int64_t outer, std::int64_t reduce, std::int64_t inner) {
+  ColPlan p{false, 1, reduce};
+  if (inner <= 1 || reduce <= kSequentialMax) return p;
+  p.col_path = true;
+  const std::int64_t tile = inner % 4 == 0 ? 256 : 64;
+  const std::int64_t col_tiles = outer * ((inner + tile - 1) / tile);
+  const std::int64_t partial_cap =
+      static_cast<std::int64_t>(TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE / sizeof(Partial));
+  std::int64_t splits = 1;
+  while (col_tiles * splits < kColTargetBlocks && reduce / (2 * splits) >= kColMinRows &&
+         2 * splits * outer * inner <= partial_cap)
+    splits *= 2;
+  p.split_rows = (reduce + splits - 1) / splits;
+  p.splits = (reduce + p.split_rows - 1) / p.split_rows;
+  return p;
+}
+
 // Blocks of the row path's persistent grid: 7 per 4 CUs (1792 waves on 256
 // CUs), each wave (or block) streaming its items in turn. Fewer streams
 // open at once read HBM faster than one wave per item. Measured against one
@@ -716,9 +939,47 @@ unsigned row_grid_blocks() {
   return static_cast<unsigned>(blocks);
 }
 
+// Bytes of partials a plan keeps in workspace (0 for single-launch plans).
+std::int64_t workspace_need(std::int64_t outer, std::int64_t reduce, std::int64_t inner) {
+  const std::int64_t entry = static_cast<std::int64_t>(sizeof(Partial));
+  const ColPlan cols = plan_cols(outer, reduce, inner);
+  if (cols.col_path) return cols.splits > 1 ? cols.splits * outer * inner * entry : 0;
+  const RowPlan rows = plan_rows(outer, reduce, inner);
+  return rows.row_path && rows.partials > 1 ? outer * rows.partials * entry : 0;
+}
+
+template <int kOp, typename T>
+int launch_cols(const T* x, void* out, std::int64_t outer, std::int64_t reduce, std::int64_t inner,
+                const ColPlan& plan, void* workspace, std::size_t workspace_bytes, hipStream_t s) {
+  Partial* partials = nullptr;
+  if (plan.splits > 1) {
+    const std::size_t need = static_cast<std::size_t>(plan.splits * outer * inner) * sizeof(Partial);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(TCX_INVALID_ARGUMENT, "reduce workspace is smaller than tcx_hip_reduce_workspace_bytes");
+    partials = static_cast<Partial*>(workspace);
+  }
+  const bool vec = inner % 4 == 0 && aligned16(x);
+  const std::int64_t tile = vec ? 256 : 64;
+  const std::int64_t blocks = outer * ((inner + tile - 1) / tile) * plan.splits;
+  const dim3 grid(static_cast<unsigned>(blocks < kColMaxGrid ? blocks : kColMaxGrid));
+  if (vec)
+    hipLaunchKernelGGL((col_kernel<kOp, T, 4>), grid, dim3(64 * kColWaves), 0, s, x, out, partials, outer, reduce,
+                       inner, plan.split_rows, blocks);
+  else
+    hipLaunchKernelGGL((col_kernel<kOp, T, 1>), grid, dim3(64 * kColWaves), 0, s, x, out, partials, outer, reduce,
+                       inner, plan.split_rows, blocks);
+  int rc = check(hipGetLastError(), "reduce column kernel launch");
+  if (rc != TCX_OK || plan.splits == 1) return rc;
+  hipLaunchKernelGGL((col_finish_kernel<kOp, T>), dim3(grid_for(outer * inner, 256, kStrideBlocks)), dim3(256), 0, s,
+                     partials, out, outer * inner, plan.splits, reduce);
+  return check(hipGetLastError(), "reduce column finish kernel launch");
+}
+
 template <int kOp, typename T>
 int launch_reduce(const T* x, void* out, std::int64_t outer, std::int64_t reduce, std::int64_t inner,
                   void* workspace, std::size_t workspace_bytes, hipStream_t s) {
+  const ColPlan cols = plan_cols(outer, reduce, inner);
+  if (cols.col_path) return launch_cols<kOp, T>(x, out, outer, reduce, inner, cols, workspace, workspace_bytes, s);
   const RowPlan plan = plan_rows(outer, reduce, inner);
   if (!plan.row_path) {
     hipLaunchKernelGGL((lane_kernel<kOp, T>), dim3(grid_for(outer * inner, 256, kStrideBlocks)), dim3(256), 0,
@@ -803,9 +1064,8 @@ int scratch_address(void** address) {
 template <int kOp, typename T>
 int launch_reduce_noalloc(const T* x, void* out, std::int64_t outer, std::int64_t reduce, std::int64_t inner,
                           hipStream_t s) {
-  const RowPlan plan = plan_rows(outer, reduce, inner);
-  if (!plan.row_path || plan.partials == 1) return launch_reduce<kOp, T>(x, out, outer, reduce, inner, nullptr, 0, s);
-  const std::int64_t need = outer * plan.partials * static_cast<std::int64_t>(sizeof(Partial));
+  const std::int64_t need = workspace_need(outer, reduce, inner);
+  if (need == 0) return launch_reduce<kOp, T>(x, out, outer, reduce, inner, nullptr, 0, s);
   if (need > TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE)
     return fail(TCX_INVALID_ARGUMENT, "reduction plan needs " + std::to_string(need) +
                                           " bytes of partials; the no-allocation scratch holds " +
@@ -882,9 +1142,7 @@ size_t tcx_hip_reduce_workspace_bytes(int op, int dtype, int64_t outer, int64_t 
   (void)op;
   (void)dtype;
   if (outer <= 0 || reduce <= 0 || inner <= 0) return 0;
-  const tcx::RowPlan plan = tcx::plan_rows(outer, reduce, inner);
-  if (!plan.row_path || plan.partials == 1) return 0;
-  return static_cast<size_t>(outer * plan.partials) * sizeof(tcx::Partial);
+  return static_cast<size_t>(tcx::workspace_need(outer, reduce, inner));
 }
 
 namespace {

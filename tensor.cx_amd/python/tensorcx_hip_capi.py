@@ -20,7 +20,7 @@ LIB_PATH = PKG / "lib" / "libtensorcx_hip.so"
 TCX_OK, TCX_INVALID_ARGUMENT, TCX_UNAVAILABLE, TCX_INTERNAL = 0, 1, 2, 3
 TCX_FLOAT32, TCX_INT32 = 0, 1
 TCX_POOL_OOM = 102
-REDUCE_NOALLOC_MAX_WORKSPACE = 262144
+REDUCE_NOALLOC_MAX_WORKSPACE = 4194304
 ACT = {"none": 0, "silu": 1, "gelu": 2}
 REDUCE = {"sum": 0, "max": 1, "mean": 2, "min": 3, "argmax": 4}
 UNARY = {"exp": 0, "gelu": 1, "silu": 2}

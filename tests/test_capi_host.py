@@ -97,6 +97,30 @@ def test_reduce_workspace_fits_the_noalloc_scratch():
     assert query(0, capi.TCX_FLOAT32, 447, 1 << 20, 1) == 447 * 2 * 16
 
 
+def test_column_reduce_workspace_query():
+    # Strided reductions (inner > 1) of more than 64 rows split the rows of
+    # too few column tiles (256 columns when inner is a multiple of 4, else
+    # 64) by doubling, while tiles x splits < 512, each split keeps at least
+    # 128 rows and the 16-byte partials fit the no-allocation scratch.
+    if not capi.LIB_PATH.exists():
+        pytest.fail("libtensorcx_hip.so is not built: run `python tensor.cx_amd/build.py`")
+    query = capi.lib().tcx_hip_reduce_workspace_bytes
+    assert query(0, capi.TCX_FLOAT32, 1, 8192, 64) == 64 * 64 * 16          # 64 splits of 128 rows
+    assert query(1, capi.TCX_FLOAT32, 1, 4096, 4096) == 32 * 4096 * 16      # 16 tiles x 32 splits
+    assert query(4, capi.TCX_FLOAT32, 1, 100_000, 3) == 511 * 3 * 16        # 512 -> 511 splits of 196 rows
+    assert query(0, capi.TCX_FLOAT32, 2, 1000, 1030) == 4 * 2 * 1030 * 16   # 34 tiles of 64, 4 splits
+    assert query(0, capi.TCX_FLOAT32, 16, 512, 8192) == 0                   # 512 tiles: no split
+    assert query(0, capi.TCX_FLOAT32, 1, 65, 600) == 0                      # 65 rows: too few to split
+    assert query(0, capi.TCX_FLOAT32, 1, 64, 600) == 0                      # exact-order lanes
+    largest = 0
+    for outer in (1, 2, 7, 64, 1000):
+        for rows in (65, 300, 4096, 65536, 2**24):
+            for inner in (2, 3, 64, 65, 256, 4100, 2**20):
+                if outer * rows * inner <= 2**36:
+                    largest = max(largest, query(0, capi.TCX_FLOAT32, outer, rows, inner))
+    assert 0 < largest <= capi.REDUCE_NOALLOC_MAX_WORKSPACE
+
+
 CONTRACT = ROOT / "tests" / "cpp" / "_bin" / "hip_backend_contract"
 
 

@@ -82,6 +82,28 @@ def test_noalloc_special_values_and_ties(capi):
     assert actual[0] == 10.0 and np.isnan(actual[1]) and np.isnan(reference[1])
 
 
+def test_noalloc_column_plans_match(capi):
+    # Strided reductions whose rows are split over blocks keep their split
+    # partials in the scratch; consecutive calls shrink.
+    rng = np.random.default_rng(34)
+    for outer, rows, inner in [(1, 4096, 4096), (1, 100_000, 3), (2, 1000, 1030), (1, 8192, 64)]:
+        x = rng.standard_normal(outer * rows * inner).astype(np.float32)
+        x[::977] = 2.0
+        dx = capi.DeviceArray.from_numpy(x)
+        for op in ("sum", "mean", "max", "argmax"):
+            ws = capi.reduce_workspace(op, capi.TCX_FLOAT32, outer, rows, inner)
+            assert ws is not None and ws.nbytes <= capi.REDUCE_NOALLOC_MAX_WORKSPACE
+            out_dtype = np.int32 if op == "argmax" else np.float32
+            a = capi.DeviceArray((outer * inner,), out_dtype)
+            b = capi.DeviceArray((outer * inner,), out_dtype)
+            capi.reduce(op, capi.TCX_FLOAT32, dx.ptr, a.ptr, outer, rows, inner, workspace=ws)
+            capi.reduce_noalloc(op, capi.TCX_FLOAT32, dx.ptr, b.ptr, outer, rows, inner)
+            capi.synchronize()
+            assert_bits(b.numpy(), a.numpy(), f"column {op} {(outer, rows, inner)}")
+            if op == "max":
+                assert_bits(b.numpy(), oracle.max(x.reshape(outer, rows, inner), 1).reshape(-1), "column max")
+
+
 def test_noalloc_unsegmented_plans_match(capi):
     # Plans without segments need no scratch and run the same kernels.
     rng = np.random.default_rng(33)
