@@ -509,8 +509,15 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(const Partial* _
 // split order by col_finish_kernel. Extrema and int32 sums are exact in any
 // order; a float32 sum takes this blocked order (each run sequential, then
 // runs in row order).
+// Eight waves per block and eight 16-byte loads in flight per lane: against
+// sixteen loads, large strided reductions on MI355X took 0.93x the time
+// (geometric mean of 18 cases of 16-268 MB; 8192 x 8200 columns sum 67.3
+// -> 52.7 us, [32768, 2052] max 82.0 -> 72.2 us, the worst 8192 x 8192
+// columns sum 52.0 -> 62.4 us); two or four vectors per row per lane (2-4
+// KB contiguous per wave row), 16-wave blocks and 256 or 1024 target blocks
+// measured no better.
 constexpr int kColWaves = 8;
-constexpr int kColDepth = 16;
+constexpr int kColDepth = 8;
 constexpr std::int64_t kColMaxGrid = std::int64_t{1} << 22;
 
 template <int kOp, typename T>
@@ -556,94 +563,133 @@ __device__ __forceinline__ void load_cols(const T* __restrict__ p, T (&v)[kVec])
   }
 }
 
+// One (split, column tile) pair. A wave steps through its run G rows at a
+// time, W columns of each (W * G = 64 * kVec; W = 64 * kVec when inner is at
+// least that, else the power of two at or above inner, so narrow tensors
+// still give every lane a column): lane (g, c) folds rows r0 + g, r0 + g + G,
+// ... of column c, kColDepth of its rows loaded at once. For a float32 sum
+// the order is fixed: each lane's rows in order, the wave's row groups by a
+// butterfly, the waves in row order, then the splits.
 template <int kOp, typename T, int kVec>
 __device__ __forceinline__ void col_block(const T* __restrict__ x, void* __restrict__ out,
                                           Partial* __restrict__ partials, std::int64_t outer, std::int64_t R,
-                                          std::int64_t inner, std::int64_t split_rows, std::int64_t b,
+                                          std::int64_t inner, std::int64_t split_rows, int W, std::int64_t b,
                                           Partial (&lds)[kColWaves][64 * kVec]) {
   constexpr bool kSum = kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN;
   constexpr bool kLargest = kOp != TCX_REDUCE_MIN;
-  constexpr int kTile = 64 * kVec;
+  constexpr int kRows = kColDepth;
+  const int G = 64 * kVec / W;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const std::int64_t tiles_per_outer = (inner + kTile - 1) / kTile;
+  const int lanes_per_row = W / kVec;
+  const int g = lane / lanes_per_row, cl = (lane % lanes_per_row) * kVec;
+  const std::int64_t tiles_per_outer = (inner + W - 1) / W;
   const std::int64_t col_tiles = outer * tiles_per_outer;
   const std::int64_t split = b / col_tiles, tile = b % col_tiles;
-  const std::int64_t o = tile / tiles_per_outer, tile_col = (tile % tiles_per_outer) * kTile;
-  const std::int64_t j = tile_col + lane * kVec;
+  const std::int64_t o = tile / tiles_per_outer, tile_col = (tile % tiles_per_outer) * W;
   const std::int64_t rb = split * split_rows, re = min(R, rb + split_rows);
   const std::int64_t per_wave = (re - rb + kColWaves - 1) / kColWaves;
   const std::int64_t r0 = min(re, rb + wave * per_wave), r1 = min(re, r0 + per_wave);
+  // This lane's rows: a, a + G, ... below r1 (n of them).
+  const std::int64_t a = r0 + g;
+  const std::int64_t n = a < r1 ? (r1 - a + G - 1) / G : 0;
   // Lanes past the last column read the last kVec columns (in bounds: inner
   // is a multiple of kVec) and their results are not stored.
-  const T* __restrict__ p = x + o * R * inner + (j < inner ? j : inner - kVec);
+  const std::int64_t j = tile_col + cl;
+  const T* __restrict__ base = x + o * R * inner + a * inner + (j < inner ? j : inner - kVec);
+  const std::int64_t step = static_cast<std::int64_t>(G) * inner;
+  auto load_row = [&](std::int64_t i, T (&v)[kVec]) { load_cols<T, kVec>(base + i * step, v); };
   Partial acc[kVec];
   if constexpr (kSum) {
     using Acc = std::conditional_t<__is_same(T, float), float, std::uint32_t>;
     Acc sum[kVec];
 #pragma unroll
     for (int c = 0; c < kVec; ++c) sum[c] = 0;
-    std::int64_t r = r0;
-    for (; r + kColDepth <= r1; r += kColDepth) {
-      T v[kColDepth][kVec];
+    std::int64_t i = 0;
+    for (; i + kRows <= n; i += kRows) {
+      T v[kRows][kVec];
 #pragma unroll
-      for (int u = 0; u < kColDepth; ++u) load_cols<T, kVec>(p + (r + u) * inner, v[u]);
+      for (int u = 0; u < kRows; ++u) load_row(i + u, v[u]);
 #pragma unroll
-      for (int u = 0; u < kColDepth; ++u)
+      for (int u = 0; u < kRows; ++u)
 #pragma unroll
         for (int c = 0; c < kVec; ++c) sum[c] += static_cast<Acc>(v[u][c]);
     }
-    for (; r < r1; ++r) {
-      T v[kVec];
-      load_cols<T, kVec>(p + r * inner, v);
+    if (i < n) {  // the last partial batch: loads clamped to row n - 1
+      T v[kRows][kVec];
 #pragma unroll
-      for (int c = 0; c < kVec; ++c) sum[c] += static_cast<Acc>(v[c]);
+      for (int u = 0; u < kRows; ++u) load_row(min(i + u, n - 1), v[u]);
+#pragma unroll
+      for (int u = 0; u < kRows; ++u)
+        if (i + u < n)
+#pragma unroll
+          for (int c = 0; c < kVec; ++c) sum[c] += static_cast<Acc>(v[u][c]);
     }
 #pragma unroll
     for (int c = 0; c < kVec; ++c) acc[c] = Partial{__builtin_bit_cast(std::uint32_t, sum[c]), 0U, 0};
   } else {
-    // An empty run (more waves or splits than rows) gives empty candidates.
+    // A lane without rows (more waves or splits than rows) gives empty
+    // candidates.
 #pragma unroll
     for (int c = 0; c < kVec; ++c) acc[c] = Partial{0U, 0U, -1};
-    if (r0 < r1) {
+    if (n > 0) {
+      // Candidates hold the lane's row count (below 2^31: a lane takes at
+      // most split_rows / kColWaves rows, checked at launch); the row index
+      // is a + count x G.
       T best[kVec];
-      std::int64_t bi[kVec];
-      load_cols<T, kVec>(p + r0 * inner, best);
+      int bi[kVec];
+      load_row(0, best);
 #pragma unroll
-      for (int c = 0; c < kVec; ++c) bi[c] = r0;
-      std::int64_t r = r0 + 1;
-      for (; r + kColDepth <= r1; r += kColDepth) {
-        T v[kColDepth][kVec];
-#pragma unroll
-        for (int u = 0; u < kColDepth; ++u) load_cols<T, kVec>(p + (r + u) * inner, v[u]);
-#pragma unroll
-        for (int u = 0; u < kColDepth; ++u)
-#pragma unroll
-          for (int c = 0; c < kVec; ++c)
-            if (lane_takes<T, kLargest>(v[u][c], best[c])) {
-              best[c] = v[u][c];
-              bi[c] = r + u;
-            }
-      }
-      for (; r < r1; ++r) {
-        T v[kVec];
-        load_cols<T, kVec>(p + r * inner, v);
+      for (int c = 0; c < kVec; ++c) bi[c] = 0;
+      auto visit = [&](const T (&v)[kVec], int i) {
 #pragma unroll
         for (int c = 0; c < kVec; ++c)
           if (lane_takes<T, kLargest>(v[c], best[c])) {
             best[c] = v[c];
-            bi[c] = r;
+            bi[c] = i;
           }
+      };
+      int i = 1;
+      for (; i + kRows <= n; i += kRows) {
+        T v[kRows][kVec];
+#pragma unroll
+        for (int u = 0; u < kRows; ++u) load_row(i + u, v[u]);
+#pragma unroll
+        for (int u = 0; u < kRows; ++u) visit(v[u], i + u);
+      }
+      if (i < n) {
+        T v[kRows][kVec];
+#pragma unroll
+        for (int u = 0; u < kRows; ++u) load_row(min<std::int64_t>(i + u, n - 1), v[u]);
+#pragma unroll
+        for (int u = 0; u < kRows; ++u)
+          if (i + u < n) visit(v[u], i + u);
       }
 #pragma unroll
-      for (int c = 0; c < kVec; ++c) acc[c] = Partial{to_bits(best[c]), 0U, bi[c]};
+      for (int c = 0; c < kVec; ++c)
+        acc[c] = Partial{to_bits(best[c]), 0U, a + static_cast<std::int64_t>(bi[c]) * G};
     }
   }
+  // The G row groups of a wave fold by a butterfly over the lane bits that
+  // select the group (a fixed order); group 0's lanes then hold the wave's
+  // result for their columns.
+  for (int sh = lanes_per_row; sh < 64; sh <<= 1) {
 #pragma unroll
-  for (int c = 0; c < kVec; ++c) lds[wave][lane * kVec + c] = acc[c];
+    for (int c = 0; c < kVec; ++c) {
+      Partial other;
+      other.bits = static_cast<std::uint32_t>(__shfl_xor(static_cast<int>(acc[c].bits), sh, kWave));
+      other.pad = 0U;
+      other.index = kSum ? 0 : __shfl_xor(acc[c].index, sh, kWave);
+      fold_into<kOp, T>(acc[c], other);
+    }
+  }
+  if (g == 0) {
+#pragma unroll
+    for (int c = 0; c < kVec; ++c) lds[wave][cl + c] = acc[c];
+  }
   __syncthreads();
-  // Threads 0 .. kTile-1 fold one column each over the waves, in wave order.
+  // Thread t < W folds column tile_col + t over the waves, in wave order.
   const int t = threadIdx.x;
-  if (t >= kTile || tile_col + t >= inner) return;
+  if (t >= W || tile_col + t >= inner) return;
   Partial total = lds[0][t];
 #pragma unroll
   for (int w = 1; w < kColWaves; ++w) fold_into<kOp, T>(total, lds[w][t]);
@@ -658,26 +704,53 @@ template <int kOp, typename T, int kVec>
 __global__ __launch_bounds__(64 * kColWaves) void col_kernel(const T* __restrict__ x, void* __restrict__ out,
                                                              Partial* __restrict__ partials, std::int64_t outer,
                                                              std::int64_t R, std::int64_t inner,
-                                                             std::int64_t split_rows, std::int64_t blocks) {
-  constexpr int kTile = 64 * kVec;
-  __shared__ Partial lds[kColWaves][kTile];
+                                                             std::int64_t split_rows, int W, std::int64_t blocks) {
+  __shared__ Partial lds[kColWaves][64 * kVec];
   // Block-stride over (split, tile) pairs: a grid of at most kColMaxGrid
   // blocks keeps gridDim.x x blockDim.x inside 32 bits.
   for (std::int64_t b = blockIdx.x; b < blocks; b += gridDim.x) {
-    col_block<kOp, T, kVec>(x, out, partials, outer, R, inner, split_rows, b, lds);
+    col_block<kOp, T, kVec>(x, out, partials, outer, R, inner, split_rows, W, b, lds);
     __syncthreads();  // lds is rewritten by the next pair
   }
 }
 
-// Folds each output's split partials in split order.
+// Folds each output's split partials: L lanes per output (a power of two up
+// to 64, so that many splits are read in one pass), lane k folding splits k,
+// k + L, ... in order, then the L lanes by a butterfly (a fixed order).
 template <int kOp, typename T>
 __global__ __launch_bounds__(256) void col_finish_kernel(const Partial* __restrict__ partials, void* __restrict__ out,
-                                                         std::int64_t outputs, std::int64_t splits, std::int64_t R) {
-  const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * blockDim.x;
-  for (std::int64_t id = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; id < outputs; id += step) {
-    Partial total = partials[id];
-    for (std::int64_t sp = 1; sp < splits; ++sp) fold_into<kOp, T>(total, partials[sp * outputs + id]);
-    store_output<kOp, T>(out, id, total, R);
+                                                         std::int64_t outputs, std::int64_t splits, std::int64_t R,
+                                                         int L) {
+  constexpr bool kSum = kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN;
+  const int k = threadIdx.x & (L - 1);
+  const std::int64_t per_pass = static_cast<std::int64_t>(gridDim.x) * (blockDim.x / L);
+  // Every lane runs the same number of passes (the butterfly needs the whole
+  // wave): lanes past the last output fold a clamped one and store nothing.
+  const std::int64_t passes = (outputs + per_pass - 1) / per_pass;
+  for (std::int64_t pass = 0; pass < passes; ++pass) {
+    const std::int64_t id0 = pass * per_pass + static_cast<std::int64_t>(blockIdx.x) * (blockDim.x / L) + threadIdx.x / L;
+    const std::int64_t id = id0 < outputs ? id0 : outputs - 1;
+    Partial total{0U, 0U, kSum ? 0 : -1};
+    if (k < splits) {
+      total = partials[k * outputs + id];
+      std::int64_t sp = k + L;
+      for (; sp + 7 * L < splits; sp += 8 * L) {  // eight loads in flight, folded in order
+        Partial q[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) q[u] = partials[(sp + u * L) * outputs + id];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) fold_into<kOp, T>(total, q[u]);
+      }
+      for (; sp < splits; sp += L) fold_into<kOp, T>(total, partials[sp * outputs + id]);
+    }
+    for (int off = 1; off < L; off <<= 1) {
+      Partial other;
+      other.bits = static_cast<std::uint32_t>(__shfl_xor(static_cast<int>(total.bits), off, kWave));
+      other.pad = 0U;
+      other.index = kSum ? 0 : __shfl_xor(total.index, off, kWave);
+      fold_into<kOp, T>(total, other);
+    }
+    if (k == 0 && id0 < outputs) store_output<kOp, T>(out, id, total, R);
   }
 }
 
@@ -886,14 +959,27 @@ RowPlan plan_rows(std::int64_t outer, std::int64_t reduce, std::int64_t inner) {
 
 bool aligned16(const void* q) { return (reinterpret_cast<std::uintptr_t>(q) & 15U) == 0; }
 
-// Strided (inner > 1) reductions of more than kSequentialMax rows: column
-// tiles of 256 columns (inner a multiple of 4) or 64, and the rows of each
-// tile split `splits` ways when tiles are too few for kColTargetBlocks
-// blocks (two 8-wave blocks per CU on 256 CUs), keeping at least
-// kColMinRows rows per split and the split partials within the
-// no-allocation scratch.
+// Strided (inner > 1) reductions of more than kSequentialMax rows. A column
+// tile is W columns: 64 x kVec (256 when inner is a multiple of 4, so lanes
+// load 16 bytes, else 64), or the power of two at or above a narrower inner,
+// the wave then stepping G = 64 x kVec / W rows at a time. The rows of each
+// tile are split `splits` ways (by doubling) while tiles x splits is below
+// kColTargetBlocks (two 8-wave blocks per CU on 256 CUs), each split keeps
+// at least kColMinRows x G rows (a batch of kColDepth loads per lane) and
+// the split partials fit the no-allocation scratch.
 constexpr std::int64_t kColTargetBlocks = 512;
-constexpr std::int64_t kColMinRows = 128;
+constexpr std::int64_t kColMinRows = 64;
+
+// Columns of a full tile: 64 lanes x 4 (inner a multiple of 4, 16-byte
+// loads) or x 1.
+std::int64_t col_full(bool vec) { return vec ? 256 : 64; }
+
+std::int64_t col_width(std::int64_t inner, std::int64_t full) {
+  if (inner >= full) return full;
+  std::int64_t w = 1;
+  while (w < inner) w *= 2;
+  return w;
+}
 
 struct ColPlan {
   bool col_path;
@@ -905,12 +991,14 @@ ColPlan plan_cols(std::int64_t outer, std::int64_t reduce, std::int64_t inner) {
   ColPlan p{false, 1, reduce};
   if (inner <= 1 || reduce <= kSequentialMax) return p;
   p.col_path = true;
-  const std::int64_t tile = inner % 4 == 0 ? 256 : 64;
-  const std::int64_t col_tiles = outer * ((inner + tile - 1) / tile);
+  const std::int64_t full = col_full(inner % 4 == 0);
+  const std::int64_t width = col_width(inner, full);
+  const std::int64_t col_tiles = outer * ((inner + width - 1) / width);
+  const std::int64_t min_rows = kColMinRows * (full / width);
   const std::int64_t partial_cap =
       static_cast<std::int64_t>(TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE / sizeof(Partial));
   std::int64_t splits = 1;
-  while (col_tiles * splits < kColTargetBlocks && reduce / (2 * splits) >= kColMinRows &&
+  while (col_tiles * splits < kColTargetBlocks && reduce / (2 * splits) >= min_rows &&
          2 * splits * outer * inner <= partial_cap)
     splits *= 2;
   p.split_rows = (reduce + splits - 1) / splits;
@@ -951,6 +1039,8 @@ std::int64_t workspace_need(std::int64_t outer, std::int64_t reduce, std::int64_
 template <int kOp, typename T>
 int launch_cols(const T* x, void* out, std::int64_t outer, std::int64_t reduce, std::int64_t inner,
                 const ColPlan& plan, void* workspace, std::size_t workspace_bytes, hipStream_t s) {
+  if (plan.split_rows / kColWaves >= INT32_MAX)
+    return fail(TCX_INVALID_ARGUMENT, "strided reduction has too many rows per split for 32-bit row counts");
   Partial* partials = nullptr;
   if (plan.splits > 1) {
     const std::size_t need = static_cast<std::size_t>(plan.splits * outer * inner) * sizeof(Partial);
@@ -958,20 +1048,30 @@ int launch_cols(const T* x, void* out, std::int64_t outer, std::int64_t reduce, 
       return fail(TCX_INVALID_ARGUMENT, "reduce workspace is smaller than tcx_hip_reduce_workspace_bytes");
     partials = static_cast<Partial*>(workspace);
   }
+  // An unaligned base with inner a multiple of 4 runs the 4-byte kernel with
+  // the splits planned for 16-byte loads.
   const bool vec = inner % 4 == 0 && aligned16(x);
-  const std::int64_t tile = vec ? 256 : 64;
-  const std::int64_t blocks = outer * ((inner + tile - 1) / tile) * plan.splits;
+  const std::int64_t full = col_full(vec);
+  const std::int64_t width = col_width(inner, full);
+  const std::int64_t blocks = outer * ((inner + width - 1) / width) * plan.splits;
   const dim3 grid(static_cast<unsigned>(blocks < kColMaxGrid ? blocks : kColMaxGrid));
+  const int w = static_cast<int>(width);
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(64 * kColWaves), 0, s, x, out, partials, outer, reduce, inner,
+                       plan.split_rows, w, blocks);
+  };
   if (vec)
-    hipLaunchKernelGGL((col_kernel<kOp, T, 4>), grid, dim3(64 * kColWaves), 0, s, x, out, partials, outer, reduce,
-                       inner, plan.split_rows, blocks);
+    launch(col_kernel<kOp, T, 4>);
   else
-    hipLaunchKernelGGL((col_kernel<kOp, T, 1>), grid, dim3(64 * kColWaves), 0, s, x, out, partials, outer, reduce,
-                       inner, plan.split_rows, blocks);
+    launch(col_kernel<kOp, T, 1>);
   int rc = check(hipGetLastError(), "reduce column kernel launch");
   if (rc != TCX_OK || plan.splits == 1) return rc;
-  hipLaunchKernelGGL((col_finish_kernel<kOp, T>), dim3(grid_for(outer * inner, 256, kStrideBlocks)), dim3(256), 0, s,
-                     partials, out, outer * inner, plan.splits, reduce);
+  // Lanes per output: about eight splits per lane, at most a wave.
+  int lanes = 1;
+  while (lanes < 64 && 16 * lanes <= plan.splits) lanes *= 2;
+  const std::int64_t outputs = outer * inner;
+  hipLaunchKernelGGL((col_finish_kernel<kOp, T>), dim3(grid_for(outputs * lanes, 256, kStrideBlocks)), dim3(256), 0,
+                     s, partials, out, outputs, plan.splits, reduce, lanes);
   return check(hipGetLastError(), "reduce column finish kernel launch");
 }
 

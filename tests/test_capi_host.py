@@ -98,17 +98,20 @@ def test_reduce_workspace_fits_the_noalloc_scratch():
 
 
 def test_column_reduce_workspace_query():
-    # Strided reductions (inner > 1) of more than 64 rows split the rows of
-    # too few column tiles (256 columns when inner is a multiple of 4, else
-    # 64) by doubling, while tiles x splits < 512, each split keeps at least
-    # 128 rows and the 16-byte partials fit the no-allocation scratch.
+    # Strided reductions (inner > 1) of more than 64 rows: column tiles of
+    # 256 columns (inner a multiple of 4) or 64, or the power of two at or
+    # above a narrower inner, whose waves then step G = 256 / W (or 64 / W)
+    # rows at a time. Rows split by doubling while tiles x splits < 512,
+    # each split keeps at least 64 x G rows and the 16-byte partials fit the
+    # no-allocation scratch.
     if not capi.LIB_PATH.exists():
         pytest.fail("libtensorcx_hip.so is not built: run `python tensor.cx_amd/build.py`")
     query = capi.lib().tcx_hip_reduce_workspace_bytes
-    assert query(0, capi.TCX_FLOAT32, 1, 8192, 64) == 64 * 64 * 16          # 64 splits of 128 rows
+    assert query(0, capi.TCX_FLOAT32, 1, 8192, 64) == 32 * 64 * 16          # G 4: 32 splits of 256 rows
     assert query(1, capi.TCX_FLOAT32, 1, 4096, 4096) == 32 * 4096 * 16      # 16 tiles x 32 splits
-    assert query(4, capi.TCX_FLOAT32, 1, 100_000, 3) == 511 * 3 * 16        # 512 -> 511 splits of 196 rows
-    assert query(0, capi.TCX_FLOAT32, 2, 1000, 1030) == 4 * 2 * 1030 * 16   # 34 tiles of 64, 4 splits
+    assert query(4, capi.TCX_FLOAT32, 1, 100_000, 3) == 64 * 3 * 16         # G 16: 64 splits of 1563 rows
+    assert query(0, capi.TCX_FLOAT32, 2, 1000, 1030) == 8 * 2 * 1030 * 16   # 34 tiles of 64, 8 splits
+    assert query(0, capi.TCX_FLOAT32, 5, 3001, 7) == 4 * 5 * 7 * 16         # G 8: 4 splits
     assert query(0, capi.TCX_FLOAT32, 16, 512, 8192) == 0                   # 512 tiles: no split
     assert query(0, capi.TCX_FLOAT32, 1, 65, 600) == 0                      # 65 rows: too few to split
     assert query(0, capi.TCX_FLOAT32, 1, 64, 600) == 0                      # exact-order lanes

@@ -83,15 +83,17 @@ def plant_specials(x, rng):
 # last tile partly past the end, one tile split many ways, many tiles with no
 # split, outer > 1, 65 rows (the smallest strided plan) and 64 (exact order).
 SHAPES = [
-    ((8192, 64), 0),          # one tile, 64 splits of 128 rows
+    ((8192, 64), 0),          # 64 columns, waves stepping 4 rows: 32 splits
     ((300, 2052), 0),         # 9 tiles of 256, 4 columns in the last
     ((2, 1000, 1030), 1),     # tiles of 64 (1030 is not a multiple of 4)
-    ((5, 3001, 7), 1),        # 7 columns: most lanes past the end
+    ((5, 3001, 7), 1),        # 7 columns of an 8-wide tile, stepping 8 rows
     ((4096, 4096), 0),        # 16 tiles x 32 splits
     ((65, 600), 0),           # 65 rows
     ((64, 600), 0),           # exact order
     ((3, 777, 2, 2), 1),      # inner 4 from two axes
-    ((100_000, 3), 0),        # 3 columns: 511 splits of 196 rows
+    ((100_000, 3), 0),        # 3 columns of a 4-wide tile, stepping 16 rows
+    ((70, 2, 2), 0),          # inner 4 stepping 64 rows, 70 rows: one split
+    ((1000, 12), 0),          # 12 columns of a 16-wide tile (16-byte loads)
 ]
 
 
