@@ -252,6 +252,24 @@ int tcx_hip_layernorm_f32(const float* x, const float* gamma, const float* beta,
                           int64_t outer, int64_t reduce, int64_t inner, float eps,
                           tcx_stream_t stream);
 
+/* The same row ops with a workspace (the reference has one entry per op,
+ * cpu_backend.cpp:125-240; these add the workspace argument). Over a middle
+ * axis (inner > 1) whose column tiles are too few to fill the GPU, the rows
+ * of each column are split over blocks: per-split statistics go to the
+ * workspace, then a fold and a write pass (three launches). Without a
+ * workspace (the entry points above) a strided op runs unsplit in one launch.
+ * tcx_hip_rownorm_workspace_bytes gives the size (0: none needed; at most
+ * 16 MiB); a smaller workspace is TCX_INVALID_ARGUMENT. */
+size_t tcx_hip_rownorm_workspace_bytes(int64_t outer, int64_t reduce, int64_t inner);
+int tcx_hip_softmax_f32_ws(const float* x, float* out, int64_t outer, int64_t reduce, int64_t inner,
+                           void* workspace, size_t workspace_bytes, tcx_stream_t stream);
+int tcx_hip_rmsnorm_f32_ws(const float* x, const float* gamma, float* out, int64_t outer,
+                           int64_t reduce, int64_t inner, float eps, void* workspace,
+                           size_t workspace_bytes, tcx_stream_t stream);
+int tcx_hip_layernorm_f32_ws(const float* x, const float* gamma, const float* beta, float* out,
+                             int64_t outer, int64_t reduce, int64_t inner, float eps,
+                             void* workspace, size_t workspace_bytes, tcx_stream_t stream);
+
 /* out[r, c] = act(x[r, c] + bias[c]) (bias optional): fused bias+activation,
  * the kAdd-broadcast of kLinear followed by kSilu/kGelu (cpu_backend.cpp:
  * 1004-1006, 1014-1097) in one pass. */

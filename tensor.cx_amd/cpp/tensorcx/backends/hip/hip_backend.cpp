@@ -406,14 +406,25 @@ Tensor row_op(const OpDesc& op, const Tensor& x, const Tensor* gamma, const Tens
   Tensor out = make_tensor(DType::kFloat32, x.shape);
   if (numel(x.shape) == 0) return out;
   auto* o = static_cast<float*>(out_ptr(out));
+  // Strided rows with few columns split their rows over blocks, with the
+  // split statistics in a workspace held until the stream has finished.
+  const std::size_t ws = tcx_hip_rownorm_workspace_bytes(d.outer, d.reduce, d.inner);
+  std::shared_ptr<HipBuffer> workspace;
+  if (ws) {
+    auto created = HipBuffer::create(ws);
+    if (!created) throw std::runtime_error(created.status().message());
+    workspace = created.move_value();
+  }
+  void* wp = workspace ? workspace->data() : nullptr;
   int rc = TCX_OK;
   if (op.kind == OpKind::kSoftmax)
-    rc = tcx_hip_softmax_f32(xp, o, d.outer, d.reduce, d.inner, s);
+    rc = tcx_hip_softmax_f32_ws(xp, o, d.outer, d.reduce, d.inner, wp, ws, s);
   else if (op.kind == OpKind::kRmsNorm)
-    rc = tcx_hip_rmsnorm_f32(xp, g, o, d.outer, d.reduce, d.inner, eps, s);
+    rc = tcx_hip_rmsnorm_f32_ws(xp, g, o, d.outer, d.reduce, d.inner, eps, wp, ws, s);
   else
-    rc = tcx_hip_layernorm_f32(xp, g, b, o, d.outer, d.reduce, d.inner, eps, s);
+    rc = tcx_hip_layernorm_f32_ws(xp, g, b, o, d.outer, d.reduce, d.inner, eps, wp, ws, s);
   ok_or_throw(rc, name);
+  if (workspace) ok_or_throw(tcx_hip_stream_synchronize(s), name);
   return out;
 }
 

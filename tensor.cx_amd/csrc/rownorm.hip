@@ -7,8 +7,10 @@
 // (kChunks 16-byte loads per lane, wave-wide butterfly statistics); rows of up
 // to kMaxSplit elements take one 256-thread block per row (four waves, whose
 // partial statistics meet in LDS). Longer rows use one block per row that
-// re-reads the row (mostly from L2). Strided rows (inner > 1) use one lane per
-// row in the reference's exact element order.
+// re-reads the row (mostly from L2). Strided rows (inner > 1) run
+// col_norm_kernel: column tiles whose waves fold per-column statistics over
+// runs of rows, then write the row from them in a second walk (rows split
+// over blocks, with a workspace, when tiles are few).
 //
 // Per-element arithmetic follows the reference step by step (exp(x - max),
 // sum, division; (x - mean) * scale; x * scale), each step rounded separately
@@ -502,75 +504,382 @@ __global__ __launch_bounds__(256) void row_block_kernel(RowArgs a) {
   }
 }
 
-// Strided rows: one lane per (outer, inner) row in the reference's order.
+// ------------------------------------------------------------ strided rows
+// Row ops over a middle axis (inner > 1), x as [outer, R, inner]: the row of
+// (outer o, column j) is R elements, inner apart. A column tile is W columns
+// (64 lanes x 4 with 16-byte loads when inner is a multiple of 4 and x and
+// out are 16-byte aligned, else x 1; or the power of two at or above a
+// narrower inner, the wave then stepping G = 64 x kVec / W rows at a time).
+// A block of kNormWaves waves takes one (split, tile) pair; its waves take
+// contiguous runs of the split's rows and lane (g, c) walks rows r0 + g,
+// r0 + g + G, ... of column c with kNormDepth rows loaded at once.
+//
+// Column statistics fold lane -> row groups (butterfly) -> waves (LDS, in
+// order) -> splits (in order); then each element is written from them in a
+// last walk over the rows. Softmax takes one statistics walk (a running
+// maximum with its rescaled sum of exponentials), RMSNorm one (sum of
+// squares), LayerNorm two as the reference: the sum, then the squared
+// deviations from the rounded mean, which a near-constant row's output
+// depends on. With one split (col_norm_kernel kMode 0) one block does every
+// walk; with several, statistics launches (kMode 1) write per-split
+// statistics to the workspace, col_norm_finalize_kernel folds them into
+// per-column parameters, and a write launch (kMode 2) reads those.
+constexpr int kNormWaves = 8;
+constexpr int kNormDepth = 8;
+constexpr std::int64_t kNormTargetBlocks = 512;  // two 8-wave blocks per CU on 256 CUs
+constexpr std::int64_t kNormMinRows = 64;        // rows per split, times G
+constexpr std::int64_t kNormMaxWorkspace = std::int64_t{16} << 20;
+
+// Statistics of one column over some of its rows:
+//   softmax  a = running maximum m (NaN once a NaN is seen), b = sum of
+//            e^(x - m) over the elements other than -inf (rescaled when m
+//            grows), so the row's denominator is sum_p b_p e^(m_p - M)
+//   rms      a = sum of x^2
+//   layer    walk 0: a = sum of x, c = a value of the rows, n bit 31 set
+//            while every element equals c (n counts rows); walk 1: a = sum of
+//            (x - mean)^2
+struct NormStat {
+  float a, b, c;
+  std::uint32_t n;
+};
+constexpr std::uint32_t kAllEqual = 0x80000000U;
+
+// Per-column parameters of the write walk: softmax (m, 1 / denominator);
+// rms (scale); layer (mean, scale), or a fill value for a row of equal
+// finite elements (0; NaN when eps is 0) or a zero variance + eps (NaN).
+struct NormParams {
+  float p0, p1, fill;
+  int special;
+};
+
+struct ColNormArgs {
+  const float* x;
+  const float* gamma;
+  const float* beta;
+  float* out;
+  NormStat* stats;     // [splits][outer * inner] (kMode 1)
+  NormParams* params;  // [outer * inner] (kMode 1 walk 1, kMode 2)
+  std::int64_t outer, R, inner, split_rows, splits, blocks;
+  float eps;
+  int W;
+  int walk;            // kMode 1: LayerNorm's statistics walk (0 or 1)
+};
+
 template <RowOp kOp>
-__global__ __launch_bounds__(256) void row_lane_kernel(RowArgs a, std::int64_t reduce, std::int64_t inner) {
-  // Grid-stride over rows = outer * inner (the launcher caps the grid).
-  const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * blockDim.x;
-  for (std::int64_t id = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; id < a.rows; id += step) {
-    const std::int64_t base = (id / inner) * reduce * inner + id % inner;
-    const float* __restrict__ x = a.x + base;
-    float* __restrict__ out = a.out + base;
-    if constexpr (kOp == RowOp::kSoftmax) {
-      float m = -__builtin_inff();
-      for (std::int64_t r = 0; r < reduce; ++r) {
-        const float e = x[r * inner];
-        if (is_nan(e)) {
-          m = e;
-          break;
-        }
-        m = (m < e) ? e : m;
-      }
-      float denom = 0.F;
-      for (std::int64_t r = 0; r < reduce; ++r) denom += expf(x[r * inner] - m);
-      for (std::int64_t r = 0; r < reduce; ++r) out[r * inner] = expf(x[r * inner] - m) / denom;
-    } else if constexpr (kOp == RowOp::kRms) {
-      float ss = 0.F;
-      for (std::int64_t r = 0; r < reduce; ++r) {
-        const float e = x[r * inner];
-        const float sq = e * e;
-        ss += sq;
-      }
-      const float scale = 1.0F / sqrtf(ss / static_cast<float>(reduce) + a.eps);
-      for (std::int64_t r = 0; r < reduce; ++r) {
-        float t = x[r * inner] * scale;
-        if (a.gamma) t = t * a.gamma[r];
-        out[r * inner] = t;
-      }
+__device__ __forceinline__ NormStat empty_stat() {
+  if constexpr (kOp == RowOp::kSoftmax) return NormStat{-__builtin_inff(), 0.F, 0.F, 0U};
+  else return NormStat{0.F, 0.F, 0.F, kAllEqual};
+}
+
+// Folds statistics b (of later rows) into a.
+template <RowOp kOp>
+__device__ __forceinline__ void fold_stat(NormStat& a, const NormStat& b) {
+  if constexpr (kOp == RowOp::kSoftmax) {
+    if (is_nan(a.a)) return;
+    if (is_nan(b.a)) {
+      a = b;
+      return;
+    }
+    const float m = a.a < b.a ? b.a : a.a;
+    // A side with no element other than -inf adds nothing (its b is 0, and
+    // e^(-inf - m) would be NaN when m is -inf too).
+    const float ta = a.a == -__builtin_inff() ? 0.F : a.b * exp_softmax(a.a - m);
+    const float tb = b.a == -__builtin_inff() ? 0.F : b.b * exp_softmax(b.a - m);
+    a.a = m;
+    a.b = ta + tb;
+  } else if constexpr (kOp == RowOp::kRms) {
+    a.a = a.a + b.a;
+  } else {
+    const std::uint32_t na = a.n & ~kAllEqual, nb = b.n & ~kAllEqual;
+    if (nb == 0) return;
+    if (na == 0) {
+      a = b;
+      return;
+    }
+    const bool equal = (a.n & kAllEqual) && (b.n & kAllEqual) && a.c == b.c;
+    a.a = a.a + b.a;
+    a.n = (na + nb) | (equal ? kAllEqual : 0U);
+  }
+}
+
+template <RowOp kOp>
+__device__ __forceinline__ NormStat shfl_stat(const NormStat& v, int off) {
+  NormStat r;
+  r.a = __shfl_xor(v.a, off, kWave);
+  r.b = kOp == RowOp::kSoftmax ? __shfl_xor(v.b, off, kWave) : 0.F;
+  r.c = kOp == RowOp::kLayer ? __shfl_xor(v.c, off, kWave) : 0.F;
+  r.n = kOp == RowOp::kLayer ? static_cast<std::uint32_t>(__shfl_xor(static_cast<int>(v.n), off, kWave)) : 0U;
+  return r;
+}
+
+// Parameters from a column's folded statistics: for LayerNorm, walk 0 sets
+// the mean and the equal-row fill, walk 1 the scale (into p, which holds
+// walk 0's parameters).
+template <RowOp kOp>
+__device__ __forceinline__ void norm_params(NormParams& p, const NormStat& st, int walk, std::int64_t R, float eps) {
+  if constexpr (kOp == RowOp::kSoftmax) {
+    p = NormParams{st.a, 1.0F / st.b, 0.F, 0};  // one correctly rounded reciprocal, as the row kernels
+  } else if constexpr (kOp == RowOp::kRms) {
+    p = NormParams{1.0F / sqrtf(st.a / static_cast<float>(R) + eps), 0.F, 0.F, 0};
+  } else if (walk == 0) {
+    const bool const_row = (st.n & kAllEqual) && __builtin_isfinite(st.c);
+    p = NormParams{st.a / static_cast<float>(R), 0.F, const_row && eps != 0.F ? 0.F : __builtin_nanf(""),
+                   const_row ? 1 : 0};
+  } else {
+    bool nan_row = false;
+    p.p1 = finish_scale_ln(st.a, R, eps, nan_row);
+    if (nan_row && !p.special) {
+      p.special = 1;
+      p.fill = __builtin_nanf("");
+    }
+  }
+}
+
+template <RowOp kOp, int kVec, int kMode>
+__device__ __forceinline__ void col_norm_block(const ColNormArgs& a, std::int64_t b,
+                                               NormStat (&lds)[kNormWaves][64 * kVec],
+                                               NormParams (&params)[64 * kVec]) {
+  const int W = a.W;
+  const int G = 64 * kVec / W;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lanes_per_row = W / kVec;
+  const int g = lane / lanes_per_row, cl = (lane % lanes_per_row) * kVec;
+  const int t = threadIdx.x;
+  const std::int64_t inner = a.inner, R = a.R;
+  const std::int64_t tiles_per_outer = (inner + W - 1) / W;
+  const std::int64_t col_tiles = a.outer * tiles_per_outer;
+  const std::int64_t split = b / col_tiles, tile = b % col_tiles;
+  const std::int64_t o = tile / tiles_per_outer, tile_col = (tile % tiles_per_outer) * W;
+  const std::int64_t rb = split * a.split_rows, re = min(R, rb + a.split_rows);
+  const std::int64_t per_wave = (re - rb + kNormWaves - 1) / kNormWaves;
+  const std::int64_t r0 = min(re, rb + wave * per_wave), r1 = min(re, r0 + per_wave);
+  const std::int64_t row0 = r0 + g;  // this lane's rows: row0, row0 + G, ... below r1
+  const std::int64_t n = row0 < r1 ? (r1 - row0 + G - 1) / G : 0;
+  // Lanes past the last column read the last kVec columns (in bounds: inner
+  // is a multiple of kVec) and store nothing.
+  const std::int64_t j = tile_col + cl;
+  const bool col_in = j < inner;
+  const bool t_in = t < W && tile_col + t < inner;  // thread t folds column tile_col + t
+  const std::int64_t offset = o * R * inner + row0 * inner + (col_in ? j : inner - kVec);
+  const float* __restrict__ xb = a.x + offset;
+  const std::int64_t step = static_cast<std::int64_t>(G) * inner;
+  auto load_row = [&](std::int64_t i, float (&v)[kVec]) {
+    if constexpr (kVec == 4) {
+      const float4_t q = stream_load(reinterpret_cast<const float4_t*>(xb + i * step));
+      v[0] = q.x;
+      v[1] = q.y;
+      v[2] = q.z;
+      v[3] = q.w;
     } else {
-      const float first = x[0];
-      float s = 0.F;
-      bool equal = true;
-      for (std::int64_t r = 0; r < reduce; ++r) {
-        const float e = x[r * inner];
-        s += e;
-        equal = equal && e == first;
-      }
-      if (equal && __builtin_isfinite(first)) {
-        const float fillv = a.eps == 0.F ? __builtin_nanf("") : 0.F;
-        for (std::int64_t r = 0; r < reduce; ++r) {
-          float t = fillv;
-          if (a.gamma) t = t * a.gamma[r];
-          if (a.beta) t = t + a.beta[r];
-          out[r * inner] = t;
+      v[0] = stream_load(xb + i * step);
+    }
+  };
+
+  // One statistics walk over this lane's rows, folded to column t's block
+  // statistics (valid for t_in threads; the call is block-wide).
+  auto stats_walk = [&](int walk, const float (&mean)[kVec]) -> NormStat {
+    NormStat st[kVec];
+#pragma unroll
+    for (int c = 0; c < kVec; ++c) st[c] = empty_stat<kOp>();
+    float first[kVec];
+    if (kOp == RowOp::kLayer && walk == 0 && n > 0) {
+      load_row(0, first);
+#pragma unroll
+      for (int c = 0; c < kVec; ++c) st[c].c = first[c];
+    }
+    for (std::int64_t i = 0; i < n; i += kNormDepth) {
+      float v[kNormDepth][kVec];
+#pragma unroll
+      for (int u = 0; u < kNormDepth; ++u) load_row(min(i + u, n - 1), v[u]);  // clamped past the run
+#pragma unroll
+      for (int c = 0; c < kVec; ++c) {
+        if constexpr (kOp == RowOp::kSoftmax) {
+          float bm = st[c].a;
+#pragma unroll
+          for (int u = 0; u < kNormDepth; ++u)
+            if (i + u < n && (is_nan(v[u][c]) || v[u][c] > bm)) bm = v[u][c];
+          if (is_nan(bm)) {
+            st[c].a = st[c].b = bm;
+          } else {
+            if (bm > st[c].a) {
+              st[c].b = st[c].b * exp_softmax(st[c].a - bm);
+              st[c].a = bm;
+            }
+#pragma unroll
+            for (int u = 0; u < kNormDepth; ++u)
+              if (i + u < n && v[u][c] != -__builtin_inff()) st[c].b += exp_softmax(v[u][c] - st[c].a);
+          }
+        } else if constexpr (kOp == RowOp::kRms) {
+#pragma unroll
+          for (int u = 0; u < kNormDepth; ++u)
+            if (i + u < n) {
+              const float sq = v[u][c] * v[u][c];
+              st[c].a += sq;
+            }
+        } else if (walk == 0) {
+#pragma unroll
+          for (int u = 0; u < kNormDepth; ++u)
+            if (i + u < n) {
+              st[c].a += v[u][c];
+              if (v[u][c] != first[c]) st[c].n &= ~kAllEqual;
+            }
+        } else {
+#pragma unroll
+          for (int u = 0; u < kNormDepth; ++u)
+            if (i + u < n) {
+              const float d = v[u][c] - mean[c];
+              const float dd = d * d;
+              st[c].a += dd;
+            }
         }
-        continue;
-      }
-      const float mean = s / static_cast<float>(reduce);
-      float d2 = 0.F;
-      for (std::int64_t r = 0; r < reduce; ++r) {
-        const float d = x[r * inner] - mean;
-        d2 += d * d;
-      }
-      bool nan_row = false;
-      const float scale = finish_scale_ln(d2, reduce, a.eps, nan_row);
-      for (std::int64_t r = 0; r < reduce; ++r) {
-        float t = nan_row ? __builtin_nanf("") : (x[r * inner] - mean) * scale;
-        if (a.gamma) t = t * a.gamma[r];
-        if (a.beta) t = t + a.beta[r];
-        out[r * inner] = t;
       }
     }
+    if constexpr (kOp == RowOp::kLayer) {
+#pragma unroll
+      for (int c = 0; c < kVec; ++c) st[c].n = (st[c].n & kAllEqual) | static_cast<std::uint32_t>(n);
+    }
+    // Row groups of the wave: a butterfly over the lane bits above the
+    // column, each pair folded in row order (group 0 ends with the wave's).
+    for (int off = lanes_per_row; off < 64; off <<= 1) {
+#pragma unroll
+      for (int c = 0; c < kVec; ++c) {
+        const NormStat other = shfl_stat<kOp>(st[c], off);
+        if (g & (off / lanes_per_row)) {
+          NormStat mine = other;
+          fold_stat<kOp>(mine, st[c]);
+          st[c] = mine;
+        } else {
+          fold_stat<kOp>(st[c], other);
+        }
+      }
+    }
+    if (g == 0) {
+#pragma unroll
+      for (int c = 0; c < kVec; ++c) lds[wave][cl + c] = st[c];
+    }
+    __syncthreads();
+    NormStat total = empty_stat<kOp>();
+    if (t_in) {
+      total = lds[0][t];
+#pragma unroll
+      for (int w = 1; w < kNormWaves; ++w) fold_stat<kOp>(total, lds[w][t]);
+    }
+    __syncthreads();  // lds is free again
+    return total;
+  };
+
+  const float no_mean[kVec] = {};
+  if constexpr (kMode == 1) {
+    float mean[kVec] = {};
+    if (kOp == RowOp::kLayer && a.walk == 1) {
+#pragma unroll
+      for (int c = 0; c < kVec; ++c) mean[c] = a.params[o * inner + (col_in ? j : inner - kVec) + c].p0;
+    }
+    const NormStat total = stats_walk(a.walk, mean);
+    if (t_in) a.stats[split * a.outer * inner + o * inner + tile_col + t] = total;
+    return;
+  } else if constexpr (kMode == 0) {
+    const NormStat total = stats_walk(0, no_mean);
+    if (t_in) norm_params<kOp>(params[t], total, 0, R, a.eps);
+    if constexpr (kOp == RowOp::kLayer) {
+      __syncthreads();
+      float mean[kVec];
+#pragma unroll
+      for (int c = 0; c < kVec; ++c) mean[c] = params[cl + c].p0;
+      const NormStat dev = stats_walk(1, mean);
+      if (t_in) norm_params<kOp>(params[t], dev, 1, R, a.eps);
+    }
+  } else {
+    if (t_in) params[t] = a.params[o * inner + tile_col + t];
+  }
+  __syncthreads();
+
+  // The write walk over this lane's rows.
+  NormParams pc[kVec];
+#pragma unroll
+  for (int c = 0; c < kVec; ++c) pc[c] = params[cl + c];
+  float* __restrict__ ob = a.out + offset;
+  for (std::int64_t i = 0; i < n; i += kNormDepth) {
+    float v[kNormDepth][kVec];
+#pragma unroll
+    for (int u = 0; u < kNormDepth; ++u) load_row(min(i + u, n - 1), v[u]);
+#pragma unroll
+    for (int u = 0; u < kNormDepth; ++u) {
+      if (i + u >= n) continue;
+      const std::int64_t r = row0 + (i + u) * G;
+      const float gr = a.gamma ? a.gamma[r] : 1.F;
+      const float br = a.beta ? a.beta[r] : 0.F;
+      float y[kVec];
+#pragma unroll
+      for (int c = 0; c < kVec; ++c) {
+        float e;
+        if constexpr (kOp == RowOp::kSoftmax) {
+          e = exp_softmax(v[u][c] - pc[c].p0) * pc[c].p1;
+        } else if constexpr (kOp == RowOp::kRms) {
+          e = v[u][c] * pc[c].p0;
+        } else {
+          e = pc[c].special ? pc[c].fill : (v[u][c] - pc[c].p0) * pc[c].p1;
+        }
+        // Affine steps (multiply then add, each rounded).
+        if (a.gamma) e = e * gr;
+        if (a.beta) e = e + br;
+        y[c] = e;
+      }
+      if (!col_in) continue;
+      float* __restrict__ q = ob + (i + u) * step;
+      if constexpr (kVec == 4) {
+        const float4_t o4 = {y[0], y[1], y[2], y[3]};
+        __builtin_nontemporal_store(o4, reinterpret_cast<float4_t*>(q));
+      } else {
+        __builtin_nontemporal_store(y[0], q);
+      }
+    }
+  }
+}
+
+// Folds each column's split statistics into its parameters: L lanes per
+// column (a power of two up to 64, about eight splits each), lane k folding
+// splits k, k + L, ... in order, then the L lanes by a butterfly.
+template <RowOp kOp>
+__global__ __launch_bounds__(256) void col_norm_finalize_kernel(const NormStat* __restrict__ stats,
+                                                                NormParams* __restrict__ params,
+                                                                std::int64_t outputs, std::int64_t splits,
+                                                                std::int64_t R, float eps, int L, int walk) {
+  const int k = threadIdx.x & (L - 1);
+  const std::int64_t per_pass = static_cast<std::int64_t>(gridDim.x) * (blockDim.x / L);
+  // Every lane runs the same passes (the butterfly needs the whole wave):
+  // lanes past the last column fold a clamped one and store nothing.
+  const std::int64_t passes = (outputs + per_pass - 1) / per_pass;
+  for (std::int64_t pass = 0; pass < passes; ++pass) {
+    const std::int64_t id0 = pass * per_pass + static_cast<std::int64_t>(blockIdx.x) * (blockDim.x / L) + threadIdx.x / L;
+    const std::int64_t id = id0 < outputs ? id0 : outputs - 1;
+    NormStat total = empty_stat<kOp>();
+    std::int64_t sp = k;
+    for (; sp + 7 * L < splits; sp += 8 * L) {
+      NormStat q[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) q[u] = stats[(sp + u * L) * outputs + id];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) fold_stat<kOp>(total, q[u]);
+    }
+    for (; sp < splits; sp += L) fold_stat<kOp>(total, stats[sp * outputs + id]);
+    for (int off = 1; off < L; off <<= 1) fold_stat<kOp>(total, shfl_stat<kOp>(total, off));
+    if (k == 0 && id0 < outputs) {
+      NormParams p = walk == 1 ? params[id] : NormParams{};
+      norm_params<kOp>(p, total, walk, R, eps);
+      params[id] = p;
+    }
+  }
+}
+
+template <RowOp kOp, int kVec, int kMode>
+__global__ __launch_bounds__(64 * kNormWaves) void col_norm_kernel(ColNormArgs a) {
+  __shared__ NormStat lds[kNormWaves][64 * kVec];
+  __shared__ NormParams params[64 * kVec];
+  // Block-stride over (split, tile) pairs; the launcher caps the grid.
+  for (std::int64_t b = blockIdx.x; b < a.blocks; b += gridDim.x) {
+    col_norm_block<kOp, kVec, kMode>(a, b, lds, params);
+    __syncthreads();  // lds and params are rewritten by the next pair
   }
 }
 
@@ -650,17 +959,103 @@ void launch_cached(const RowArgs& a, bool vec, hipStream_t s) {
     launch_cached_as<kOp, kChunks, false, false>(a, s);
 }
 
+// Columns of a strided tile: 64 x 4 with 16-byte loads, else 64; a
+// narrower inner takes the power of two at or above it.
+std::int64_t norm_width(std::int64_t inner, bool vec) {
+  const std::int64_t full = vec ? 256 : 64;
+  if (inner >= full) return full;
+  std::int64_t w = 1;
+  while (w < inner) w *= 2;
+  return w;
+}
+
+struct NormPlan {
+  std::int64_t splits, split_rows;
+};
+
+// Rows of a strided tile are split by doubling while tiles x splits is
+// below kNormTargetBlocks, each split keeps at least kNormMinRows x G rows
+// and the workspace (split statistics plus one parameter record per column)
+// stays within kNormMaxWorkspace. Planned for 16-byte loads whenever inner
+// is a multiple of 4, so the workspace query needs no pointers.
+NormPlan plan_norm(std::int64_t outer, std::int64_t reduce, std::int64_t inner) {
+  const bool vec = inner % 4 == 0;
+  const std::int64_t width = norm_width(inner, vec);
+  const std::int64_t g = (vec ? 256 : 64) / width;
+  const std::int64_t tiles = outer * ((inner + width - 1) / width);
+  const std::int64_t entry = static_cast<std::int64_t>(sizeof(NormStat));
+  std::int64_t splits = 1;
+  while (tiles * splits < kNormTargetBlocks && reduce / (2 * splits) >= kNormMinRows * g &&
+         (2 * splits + 1) * outer * inner * entry <= kNormMaxWorkspace)
+    splits *= 2;
+  const std::int64_t rows = (reduce + splits - 1) / splits;
+  return NormPlan{(reduce + rows - 1) / rows, rows};
+}
+
+std::int64_t norm_workspace(std::int64_t outer, std::int64_t reduce, std::int64_t inner) {
+  if (outer <= 0 || reduce <= 0 || inner <= 1) return 0;
+  const NormPlan plan = plan_norm(outer, reduce, inner);
+  if (plan.splits == 1) return 0;
+  return (plan.splits + 1) * outer * inner * static_cast<std::int64_t>(sizeof(NormStat));
+}
+
 template <RowOp kOp>
-int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t inner, hipStream_t s) {
+int run_cols(const RowArgs& r, std::int64_t outer, std::int64_t reduce, std::int64_t inner, void* workspace,
+             std::size_t workspace_bytes, bool split, hipStream_t s) {
+  NormPlan plan{1, reduce};
+  if (split) plan = plan_norm(outer, reduce, inner);
+  if (plan.split_rows / kNormWaves >= INT32_MAX)
+    return fail(TCX_INVALID_ARGUMENT, "strided row op has too many rows per split");
+  const std::int64_t outputs = outer * inner;
+  NormStat* stats = nullptr;
+  NormParams* params = nullptr;
+  if (plan.splits > 1) {
+    const std::int64_t need = norm_workspace(outer, reduce, inner);
+    if (workspace == nullptr || workspace_bytes < static_cast<std::size_t>(need))
+      return fail(TCX_INVALID_ARGUMENT, "row op workspace is smaller than tcx_hip_rownorm_workspace_bytes");
+    stats = static_cast<NormStat*>(workspace);
+    params = reinterpret_cast<NormParams*>(stats + plan.splits * outputs);
+  }
+  // 16-byte loads and stores need inner a multiple of 4 and aligned x and
+  // out; gamma and beta are read one element per row. Otherwise the 4-byte
+  // kernel runs with the same splits.
+  const bool vec = inner % 4 == 0 && aligned16(r.x) && aligned16(r.out);
+  const std::int64_t width = norm_width(inner, vec);
+  const std::int64_t blocks = outer * ((inner + width - 1) / width) * plan.splits;
+  ColNormArgs a{r.x, r.gamma, r.beta, r.out, stats, params, outer, reduce, inner, plan.split_rows, plan.splits,
+                blocks, r.eps, static_cast<int>(width), 0};
+  const dim3 grid(static_cast<unsigned>(blocks < kStrideBlocks ? blocks : kStrideBlocks));
+  const dim3 block(64 * kNormWaves);
+  auto launch = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, s, a); };
+  if (plan.splits == 1) {
+    vec ? launch(col_norm_kernel<kOp, 4, 0>) : launch(col_norm_kernel<kOp, 1, 0>);
+    return check(hipGetLastError(), "strided row kernel launch");
+  }
+  int lanes = 1;  // about eight splits per lane, at most a wave per column
+  while (lanes < 64 && 16 * lanes <= plan.splits) lanes *= 2;
+  // Statistics walks, each folded into the parameters (LayerNorm: the sum,
+  // then the squared deviations from the mean).
+  for (int walk = 0; walk < (kOp == RowOp::kLayer ? 2 : 1); ++walk) {
+    a.walk = walk;
+    vec ? launch(col_norm_kernel<kOp, 4, 1>) : launch(col_norm_kernel<kOp, 1, 1>);
+    int rc = check(hipGetLastError(), "strided row statistics launch");
+    if (rc != TCX_OK) return rc;
+    hipLaunchKernelGGL((col_norm_finalize_kernel<kOp>), dim3(grid_for(outputs * lanes, 256, kStrideBlocks)),
+                       dim3(256), 0, s, stats, params, outputs, plan.splits, reduce, r.eps, lanes, walk);
+    rc = check(hipGetLastError(), "strided row finalize launch");
+    if (rc != TCX_OK) return rc;
+  }
+  vec ? launch(col_norm_kernel<kOp, 4, 2>) : launch(col_norm_kernel<kOp, 1, 2>);
+  return check(hipGetLastError(), "strided row write launch");
+}
+
+template <RowOp kOp>
+int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t inner, void* workspace,
+             std::size_t workspace_bytes, bool split, hipStream_t s) {
   if (outer == 0 || reduce == 0 || inner == 0) return TCX_OK;
   const int status = ready();
   if (status != TCX_OK) return status;
-  if (inner != 1) {
-    a.rows = outer * inner;
-    hipLaunchKernelGGL((row_lane_kernel<kOp>), dim3(grid_for(a.rows, 256, kStrideBlocks)), dim3(256), 0, s,
-                       a, reduce, inner);
-    return check(hipGetLastError(), "row lane kernel launch");
-  }
+  if (inner != 1) return run_cols<kOp>(a, outer, reduce, inner, workspace, workspace_bytes, split, s);
   a.rows = outer;
   a.n = reduce;
   const bool vec = reduce % 4 == 0 && aligned16(a.x) && aligned16(a.out) &&
@@ -696,33 +1091,74 @@ int check_extents(std::int64_t outer, std::int64_t reduce, std::int64_t inner, c
 
 extern "C" {
 
-int tcx_hip_softmax_f32(const float* x, float* out, int64_t outer, int64_t reduce, int64_t inner,
-                        tcx_stream_t stream) {
+size_t tcx_hip_rownorm_workspace_bytes(int64_t outer, int64_t reduce, int64_t inner) {
+  return static_cast<size_t>(tcx::norm_workspace(outer, reduce, inner));
+}
+
+namespace {
+
+int softmax_entry(const float* x, float* out, int64_t outer, int64_t reduce, int64_t inner, void* ws,
+                  size_t wsb, bool split, tcx_stream_t stream) {
   using namespace tcx;
   const int rc = check_extents(outer, reduce, inner, x, out);
   if (rc != TCX_OK) return rc;
   RowArgs a{x, nullptr, nullptr, out, 0, 0, 0.F};
-  return run_rows<RowOp::kSoftmax>(a, outer, reduce, inner, static_cast<hipStream_t>(stream));
+  return run_rows<RowOp::kSoftmax>(a, outer, reduce, inner, ws, wsb, split, static_cast<hipStream_t>(stream));
 }
 
-int tcx_hip_rmsnorm_f32(const float* x, const float* gamma, float* out, int64_t outer, int64_t reduce,
-                        int64_t inner, float eps, tcx_stream_t stream) {
+int rmsnorm_entry(const float* x, const float* gamma, float* out, int64_t outer, int64_t reduce, int64_t inner,
+                  float eps, void* ws, size_t wsb, bool split, tcx_stream_t stream) {
   using namespace tcx;
   const int rc = check_extents(outer, reduce, inner, x, out);
   if (rc != TCX_OK) return rc;
   if (!(eps >= 0.F) || __builtin_isinf(eps)) return fail(TCX_INVALID_ARGUMENT, "epsilon must be finite and non-negative");
   RowArgs a{x, gamma, nullptr, out, 0, 0, eps};
-  return run_rows<RowOp::kRms>(a, outer, reduce, inner, static_cast<hipStream_t>(stream));
+  return run_rows<RowOp::kRms>(a, outer, reduce, inner, ws, wsb, split, static_cast<hipStream_t>(stream));
 }
 
-int tcx_hip_layernorm_f32(const float* x, const float* gamma, const float* beta, float* out, int64_t outer,
-                          int64_t reduce, int64_t inner, float eps, tcx_stream_t stream) {
+int layernorm_entry(const float* x, const float* gamma, const float* beta, float* out, int64_t outer,
+                    int64_t reduce, int64_t inner, float eps, void* ws, size_t wsb, bool split,
+                    tcx_stream_t stream) {
   using namespace tcx;
   const int rc = check_extents(outer, reduce, inner, x, out);
   if (rc != TCX_OK) return rc;
   if (!(eps >= 0.F) || __builtin_isinf(eps)) return fail(TCX_INVALID_ARGUMENT, "epsilon must be finite and non-negative");
   RowArgs a{x, gamma, beta, out, 0, 0, eps};
-  return run_rows<RowOp::kLayer>(a, outer, reduce, inner, static_cast<hipStream_t>(stream));
+  return run_rows<RowOp::kLayer>(a, outer, reduce, inner, ws, wsb, split, static_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+
+int tcx_hip_softmax_f32(const float* x, float* out, int64_t outer, int64_t reduce, int64_t inner,
+                        tcx_stream_t stream) {
+  return softmax_entry(x, out, outer, reduce, inner, nullptr, 0, false, stream);
+}
+
+int tcx_hip_rmsnorm_f32(const float* x, const float* gamma, float* out, int64_t outer, int64_t reduce,
+                        int64_t inner, float eps, tcx_stream_t stream) {
+  return rmsnorm_entry(x, gamma, out, outer, reduce, inner, eps, nullptr, 0, false, stream);
+}
+
+int tcx_hip_layernorm_f32(const float* x, const float* gamma, const float* beta, float* out, int64_t outer,
+                          int64_t reduce, int64_t inner, float eps, tcx_stream_t stream) {
+  return layernorm_entry(x, gamma, beta, out, outer, reduce, inner, eps, nullptr, 0, false, stream);
+}
+
+int tcx_hip_softmax_f32_ws(const float* x, float* out, int64_t outer, int64_t reduce, int64_t inner,
+                           void* workspace, size_t workspace_bytes, tcx_stream_t stream) {
+  return softmax_entry(x, out, outer, reduce, inner, workspace, workspace_bytes, true, stream);
+}
+
+int tcx_hip_rmsnorm_f32_ws(const float* x, const float* gamma, float* out, int64_t outer, int64_t reduce,
+                           int64_t inner, float eps, void* workspace, size_t workspace_bytes,
+                           tcx_stream_t stream) {
+  return rmsnorm_entry(x, gamma, out, outer, reduce, inner, eps, workspace, workspace_bytes, true, stream);
+}
+
+int tcx_hip_layernorm_f32_ws(const float* x, const float* gamma, const float* beta, float* out, int64_t outer,
+                             int64_t reduce, int64_t inner, float eps, void* workspace, size_t workspace_bytes,
+                             tcx_stream_t stream) {
+  return layernorm_entry(x, gamma, beta, out, outer, reduce, inner, eps, workspace, workspace_bytes, true, stream);
 }
 
 }  // extern "C"

@@ -38,6 +38,8 @@ EXPORTS = [
     "tcx_hip_gemm_f32", "tcx_hip_gemm_workspace_bytes", "tcx_hip_gemm_f32_ws",
     "tcx_hip_reduce_workspace_bytes", "tcx_hip_reduce", "tcx_hip_reduce_noalloc",
     "tcx_hip_reduce_axes", "tcx_hip_softmax_f32", "tcx_hip_rmsnorm_f32", "tcx_hip_layernorm_f32",
+    "tcx_hip_rownorm_workspace_bytes", "tcx_hip_softmax_f32_ws", "tcx_hip_rmsnorm_f32_ws",
+    "tcx_hip_layernorm_f32_ws",
     "tcx_hip_bias_act_f32", "tcx_hip_unary_f32", "tcx_hip_binary", "tcx_hip_fill",
     "tcx_hip_math_unary", "tcx_hip_clip", "tcx_hip_topk", "tcx_hip_embedding_f32",
     "tcx_hip_attention_softmax_f32", "tcx_hip_flash_attention_supported", "tcx_hip_flash_attention_f32",
@@ -132,6 +134,11 @@ def lib() -> ctypes.CDLL:
         L.tcx_hip_softmax_f32.argtypes = [vp, vp, i64, i64, i64, vp]
         L.tcx_hip_rmsnorm_f32.argtypes = [vp, vp, vp, i64, i64, i64, ctypes.c_float, vp]
         L.tcx_hip_layernorm_f32.argtypes = [vp, vp, vp, vp, i64, i64, i64, ctypes.c_float, vp]
+        L.tcx_hip_rownorm_workspace_bytes.argtypes = [i64, i64, i64]
+        L.tcx_hip_rownorm_workspace_bytes.restype = sz
+        L.tcx_hip_softmax_f32_ws.argtypes = [vp, vp, i64, i64, i64, vp, sz, vp]
+        L.tcx_hip_rmsnorm_f32_ws.argtypes = [vp, vp, vp, i64, i64, i64, ctypes.c_float, vp, sz, vp]
+        L.tcx_hip_layernorm_f32_ws.argtypes = [vp, vp, vp, vp, i64, i64, i64, ctypes.c_float, vp, sz, vp]
         L.tcx_hip_bias_act_f32.argtypes = [vp, vp, vp, i64, i64, ctypes.c_int, vp]
         L.tcx_hip_unary_f32.argtypes = [ctypes.c_int, vp, vp, i64, vp]
         L.tcx_hip_binary.argtypes = [ctypes.c_int, ctypes.c_int, vp, vp, vp, ctypes.c_int32, vp, vp,
@@ -317,6 +324,33 @@ def layernorm(x: int, gamma: int | None, beta: int | None, out: int, outer, redu
               s=None) -> None:
     check(lib().tcx_hip_layernorm_f32(x, gamma, beta, out, outer, reduce_, inner, eps, s or stream()),
           "layernorm")
+
+
+def rownorm_workspace(outer: int, reduce_: int, inner: int) -> DeviceBuffer | None:
+    """A workspace for the *_ws row ops of this shape, or None when none is needed."""
+    nbytes = lib().tcx_hip_rownorm_workspace_bytes(outer, reduce_, inner)
+    return DeviceBuffer(nbytes) if nbytes else None
+
+
+def _ws_args(workspace):
+    return (workspace.address, workspace.nbytes) if workspace is not None else (None, 0)
+
+
+def softmax_ws(x: int, out: int, outer: int, reduce_: int, inner: int, workspace=None, s=None) -> None:
+    check(lib().tcx_hip_softmax_f32_ws(x, out, outer, reduce_, inner, *_ws_args(workspace), s or stream()),
+          "softmax_ws")
+
+
+def rmsnorm_ws(x: int, gamma: int | None, out: int, outer, reduce_, inner, eps=1e-5, workspace=None,
+               s=None) -> None:
+    check(lib().tcx_hip_rmsnorm_f32_ws(x, gamma, out, outer, reduce_, inner, eps, *_ws_args(workspace),
+                                       s or stream()), "rmsnorm_ws")
+
+
+def layernorm_ws(x: int, gamma: int | None, beta: int | None, out: int, outer, reduce_, inner, eps=1e-5,
+                 workspace=None, s=None) -> None:
+    check(lib().tcx_hip_layernorm_f32_ws(x, gamma, beta, out, outer, reduce_, inner, eps,
+                                         *_ws_args(workspace), s or stream()), "layernorm_ws")
 
 
 def bias_act(x: int, bias: int | None, out: int, rows: int, cols: int, activation="none", s=None) -> None:
