@@ -299,6 +299,15 @@ def secondary_benches(steps: int, warmup: int, only: str | None, cpu: bool):
         add(bench_hbm("reduce_full_sum_f32_8192x8192", lambda s: capi.reduce_noalloc(
             "sum", capi.TCX_FLOAT32, nxt().ptr, full.ptr, 1, rows * cols, 1, s), rows * cols * 4 + 4, steps, warmup),
             full_cpu)
+        # Over the first axis (a strided reduction: 32 column tiles x 16 row
+        # splits, the split partials in the static scratch).
+        for op in ("sum", "max"):
+            nxt = rotate(copies)
+            fn = getattr(oracle, op)
+            add(bench_hbm(f"reduce_col{op}_f32_8192x8192", lambda s, op=op: capi.reduce_noalloc(
+                op, capi.TCX_FLOAT32, nxt().ptr, res.ptr, 1, rows, cols, s), nbytes, steps, warmup),
+                lambda fn=fn, op=op: cpu_line(lambda r: fn(x[:r], 0, threads=1), rows, nbytes, "GB/s", 1e9,
+                                              f"{op} over the first axis of [8192, 8192] (a sample of its rows)"))
         del copies, x, flat
 
     if want("i32"):
