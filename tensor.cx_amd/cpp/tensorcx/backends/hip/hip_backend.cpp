@@ -274,6 +274,81 @@ FoldedAxes fold_axes(const Shape& shape, const std::vector<bool>& selected) {
 // selection that is one run of axes is an (outer, reduce, inner) reduction
 // with the same element order; any other runs the general metadata kernel
 // over the folded axes, kept first.
+// Selections of several reduced runs with at most this many elements per
+// output run the metadata kernel: one lane per output, the reference's
+// element order (bit-exact sums), the same bound as a single run's exact
+// order in the reduction kernels.
+constexpr Dim kExactSelectionMax = 64;
+
+// Selections of several reduced runs (after folding) with more elements per
+// output. sum / mean / max / min fold one reduced run at a time, innermost
+// first, through the (outer, reduce, inner) kernels, so every pass streams
+// its input with the row or column kernels and the first pass, over the whole
+// tensor, leaves a tensor R times smaller; max / min and int32 sums are exact
+// in any order, float32 sums take this fixed order (the reductions' sum bar),
+// and mean divides the sum once by float(count), as the reference
+// (cpu_backend.cpp:1102-1153). argmax, whose index runs over the selected
+// axes in row-major order, gathers them innermost ([kept..., reduced...],
+// one strided copy of at most TCX_HIP_MAX_RANK folded axes) and takes one row
+// argmax per output. Returns false, having launched nothing, for an argmax
+// over more folded axes than the gather takes.
+bool reduce_runs(int code, const Tensor& x, const Tensor& out, const FoldedAxes& f, Dim count, Stream& s) {
+  std::vector<Tensor> held;  // intermediates, alive until the stream has run
+  if (code == TCX_REDUCE_ARGMAX) {
+    if (f.extent.size() > TCX_HIP_MAX_RANK) return false;
+    const Shape strides = contiguous_strides(f.extent);
+    Shape shape, in_strides;
+    for (int pass = 0; pass < 2; ++pass)
+      for (std::size_t i = 0; i < f.extent.size(); ++i)
+        if (f.reduced[i] == (pass == 1)) {
+          shape.push_back(f.extent[i]);
+          in_strides.push_back(strides[i]);
+        }
+    Tensor gathered = make_tensor(x.dtype, Shape{numel(f.extent)});
+    ok_or_throw(tcx_hip_gather_strided(static_cast<int>(dtype_size(x.dtype)), device_ptr(x), out_ptr(gathered),
+                                       static_cast<int32_t>(shape.size()), shape.data(), in_strides.data(), 0, s),
+                "HIP reduction gather");
+    run_rows(code, gathered, out, numel(f.extent) / count, count, 1, s);
+    ok_or_throw(tcx_hip_stream_synchronize(s), "HIP reduction");
+    return true;
+  }
+  const int pass_code = code == TCX_REDUCE_MEAN ? TCX_REDUCE_SUM : code;
+  Shape extent = f.extent;
+  std::vector<bool> reduced = f.reduced;
+  Tensor cur = x;
+  for (;;) {
+    std::size_t k = extent.size();
+    while (!reduced[k - 1]) --k;
+    --k;  // the innermost reduced run
+    Dim outer = 1, inner = 1;
+    for (std::size_t i = 0; i < k; ++i) outer *= extent[i];
+    for (std::size_t i = k + 1; i < extent.size(); ++i) inner *= extent[i];
+    const bool last = std::count(reduced.begin(), reduced.end(), true) == 1;
+    if (last) {
+      run_rows(pass_code, cur, out, outer, extent[k], inner, s);
+      break;
+    }
+    Tensor next = make_tensor(x.dtype, Shape{outer * inner});
+    run_rows(pass_code, cur, next, outer, extent[k], inner, s);
+    held.push_back(next);
+    cur = next;
+    // Drop the run; its kept neighbours merge.
+    extent.erase(extent.begin() + static_cast<std::ptrdiff_t>(k));
+    reduced.erase(reduced.begin() + static_cast<std::ptrdiff_t>(k));
+    if (k > 0 && k < extent.size() && !reduced[k - 1] && !reduced[k]) {
+      extent[k - 1] *= extent[k];
+      extent.erase(extent.begin() + static_cast<std::ptrdiff_t>(k));
+      reduced.erase(reduced.begin() + static_cast<std::ptrdiff_t>(k));
+    }
+  }
+  if (code == TCX_REDUCE_MEAN)
+    ok_or_throw(tcx_hip_scalar_op(TCX_SCALAR_DIVIDE, TCX_FLOAT32, out_ptr(out), out_ptr(out), numel(out.shape),
+                                  static_cast<double>(count), 0, s),
+                "HIP reduction mean");
+  if (!held.empty()) ok_or_throw(tcx_hip_stream_synchronize(s), "HIP reduction");
+  return true;
+}
+
 void run_selection(int code, const Tensor& x, const Tensor& out, const Shape& axes, const ReductionPlan& plan,
                    Stream& s) {
   const Dim groups = numel(plan.output_shape);
@@ -302,6 +377,7 @@ void run_selection(int code, const Tensor& x, const Tensor& out, const Shape& ax
     run_rows(code, x, out, outer, reduce, inner, s);
     return;
   }
+  if (plan.reduction_size > kExactSelectionMax && reduce_runs(code, x, out, f, plan.reduction_size, s)) return;
   // Every folded axis has extent >= 2, so a folded rank above the kernel's
   // metadata capacity would need more than 2^40 elements.
   if (f.extent.size() > TCX_HIP_MAX_FOLDED_RANK)

@@ -159,3 +159,45 @@ def test_column_unaligned_base_takes_the_scalar_tiles(capi):
             assert sum_error(actual, expected, view, 1, R, C) <= SUM_BAR
         else:
             assert_bits(actual, expected, f"unaligned {op}")
+
+
+# Selections of several reduced runs (after folding): more than 64 elements
+# per output fold one run at a time, innermost first, through the row and
+# column kernels (argmax gathers the selected axes innermost and takes a row
+# argmax); at most 64 run the exact-order metadata kernel.
+SELECTIONS = [
+    ((16, 64, 300), (0, 2)),           # R K R: 4800 per output
+    ((32, 8, 16, 16), (0, 2, 3)),      # the per-channel statistics shape
+    ((4, 100, 3, 50), (1, 3)),         # K R K R
+    ((3, 40, 5, 70, 2), (0, 2, 4)),    # R K R K R
+    ((6, 5, 7, 9), (0, 2)),            # 42 per output: metadata kernel
+    ((2, 1, 500, 1, 3, 130), (0, 2, 5)),
+]
+
+
+@pytest.mark.parametrize("shape,axes", SELECTIONS)
+def test_multi_run_selections(cx, shape, axes):
+    from hip_cases import check_case
+    rng = np.random.default_rng(sum(shape))
+    x = rng.integers(-3, 4, shape).astype(np.float32)   # ties across runs
+    flat = x.reshape(-1)
+    flat[rng.integers(0, flat.size, 3)] = 9.0
+    flat[rng.integers(0, flat.size, 2)] = np.nan
+    h = cx.tensor(x, device="hip")
+    for op in ("max", "min"):
+        assert_bits(getattr(cx, op)(h, axes).numpy(), getattr(oracle, op)(x, axes), f"{op} {shape} {axes}")
+    assert_bits(cx.Tensor(cx._core._argmax_axes(h._impl, list(axes))).numpy(), oracle.argmax(x, axes),
+                f"argmax {shape} {axes}")
+    y = rng.standard_normal(shape).astype(np.float32)
+    hy = cx.tensor(y, device="hip")
+    for op in ("sum", "mean", "max", "min"):
+        check_case(f"{op} {shape} {axes}", op, [y], {"axes": list(axes)}, getattr(cx, op)(hy, axes).numpy(),
+                   getattr(oracle, op)(y, axes))
+    assert_bits(cx.Tensor(cx._core._argmax_axes(hy._impl, list(axes))).numpy(), oracle.argmax(y, axes),
+                f"argmax random {shape} {axes}")
+    yi = rng.integers(-2**31, 2**31 - 1, shape, dtype=np.int64).astype(np.int32)
+    hi = cx.tensor(yi, device="hip")
+    for op in ("sum", "max", "min"):
+        assert_bits(getattr(cx, op)(hi, axes).numpy(), getattr(oracle, op)(yi, axes), f"i32 {op} {shape} {axes}")
+    assert_bits(cx.Tensor(cx._core._argmax_axes(hi._impl, list(axes))).numpy(), oracle.argmax(yi, axes),
+                f"i32 argmax {shape} {axes}")

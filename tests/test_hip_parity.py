@@ -812,7 +812,8 @@ def test_high_rank_and_empty_metadata(cx, name):
 def test_folded_selections_at_scale(cx):
     # Selections that fold into one long row (size-1 axes between the reduced
     # ones) take the tree path; alternating selections over more than eight
-    # folded axes take the metadata kernel at its 40-axis capacity.
+    # folded axes take the metadata kernel at its 40-axis capacity (at most
+    # 64 elements per output: (0, 5, 8, 10)) or fold one run at a time.
     rng = np.random.default_rng(17)
     x = rng.standard_normal((300, 1, 1, 700)).astype(np.float32)
     h = cx.tensor(x, device="hip")
@@ -822,9 +823,12 @@ def test_folded_selections_at_scale(cx):
     shape = (3, 2, 4, 1, 3, 2, 5, 1, 2, 3, 2, 2)
     y = rng.standard_normal(shape).astype(np.float32)
     hy = cx.tensor(y, device="hip")
-    for axes in ((0, 2, 5, 8, 10), (1, 4, 6, 9, 11)):
+    for axes in ((0, 2, 5, 8, 10), (1, 4, 6, 9, 11), (0, 5, 8, 10)):
         for op in ("sum", "mean", "max", "min"):
-            assert_bits(getattr(cx, op)(hy, axes).numpy(), getattr(oracle, op)(y, axes), f"{op} {axes}")
+            check_case(f"{op} {axes}", op, [y], {"axes": list(axes)}, getattr(cx, op)(hy, axes).numpy(),
+                       getattr(oracle, op)(y, axes))
+        assert_bits(cx.Tensor(cx._core._argmax_axes(hy._impl, list(axes))).numpy(),
+                    oracle.argmax(y, axes), f"argmax {axes}")
     yi = rng.integers(-2**31, 2**31 - 1, shape, dtype=np.int64).astype(np.int32)
     hi = cx.tensor(yi, device="hip")
     assert_bits(cx.sum(hi, (0, 2, 5, 8, 10)).numpy(), oracle.sum(yi, (0, 2, 5, 8, 10)), "i32 sum")
