@@ -27,7 +27,11 @@
 //                      tile of 64 or 256 columns, its waves folding runs of
 //                      rows (rows split over blocks when tiles are few)
 //   col_finish_kernel  combines the column splits' partials in split order
-//   lane_kernel        one lane per output, reference element order
+//   short_row_kernel   inner == 1, rows of at most kSequentialMax: 64 rows per
+//                      wave staged in LDS, each lane folding one row in the
+//                      reference's element order
+//   lane_kernel        inner > 1, at most kSequentialMax rows: one lane per
+//                      output, reference element order
 //   axes_kernel        any axis selection through reduction-plan metadata
 
 #include <mutex>
@@ -828,6 +832,63 @@ __global__ __launch_bounds__(256) void lane_kernel(const T* __restrict__ x, void
   }
 }
 
+// Contiguous rows (inner == 1) of 2 .. kSequentialMax elements: each wave
+// stages 64 whole rows (one tile of 64 x R contiguous elements) in LDS with
+// coalesced loads, 64 / R rows per load instruction, then each lane folds
+// its own row from LDS in the reference's order (sequential). Rows sit at an
+// odd LDS stride (R or R + 1), so the lanes' reads of one column fall in
+// distinct banks. The waves of a block take tiles independently; a block of
+// kShortWaves waves takes at most 2 x 64 x 65 x 4 bytes (33 KB) of LDS.
+constexpr int kShortWaves = 2;
+// Below this row length one lane per row reads its row's few contiguous
+// words well enough. Sum, lanes against staged tiles on MI355X: [4194304, 4]
+// 23.7 / 32.3 us, [2097152, 6] 17.1 / 18.3 us, [2097152, 8] 36.0 / 17.7 us,
+// [2097152, 12] 46.0 / 19.7 us, [262144, 64] 70.6 / 19.2 us.
+constexpr std::int64_t kShortRowMin = 8;
+
+template <int kOp, typename T>
+__global__ __launch_bounds__(64 * kShortWaves) void short_row_kernel(const T* __restrict__ x, void* __restrict__ out,
+                                                                     std::int64_t rows, int R) {
+  // Dynamic LDS, 64 x stride elements per wave: short rows take little, so
+  // more waves fit on a CU.
+  extern __shared__ unsigned char short_lds[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int stride = R | 1;
+  const int per_step = 64 / R;             // rows per load instruction
+  const int q = lane / R, m = lane % R;    // this lane's row within a step, and its column
+  const bool loads = q < per_step;
+  T* tile = reinterpret_cast<T*>(short_lds) + wave * 64 * stride;
+  const std::int64_t tiles = (rows + 63) / 64;
+  const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * kShortWaves;
+  for (std::int64_t tl = static_cast<std::int64_t>(blockIdx.x) * kShortWaves + wave; tl < tiles; tl += step) {
+    const std::int64_t row0 = tl * 64;
+    const int nrows = static_cast<int>(rows - row0 < 64 ? rows - row0 : 64);
+    const T* __restrict__ src = x + row0 * R;
+    for (int r = 0; r < nrows; r += 16 * per_step) {  // sixteen loads in flight per lane
+      T v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int rr = r + u * per_step + q;
+        if (loads && rr < nrows) v[u] = src[rr * R + m];
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int rr = r + u * per_step + q;
+        if (loads && rr < nrows) tile[rr * stride + m] = v[u];
+      }
+    }
+    // The wave's LDS writes are visible to all its lanes before they read.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < nrows) sequential<kOp, T>(tile + lane * stride, R, 1, out, row0 + lane);
+    // Every lane has read its row before the next tile is staged.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
 struct AxesMeta {
   std::int64_t extent[TCX_HIP_MAX_FOLDED_RANK];
   std::int64_t stride[TCX_HIP_MAX_FOLDED_RANK];
@@ -1082,6 +1143,13 @@ int launch_reduce(const T* x, void* out, std::int64_t outer, std::int64_t reduce
   if (cols.col_path) return launch_cols<kOp, T>(x, out, outer, reduce, inner, cols, workspace, workspace_bytes, s);
   const RowPlan plan = plan_rows(outer, reduce, inner);
   if (!plan.row_path) {
+    if (inner == 1 && reduce >= kShortRowMin) {
+      const std::int64_t tiles = (outer + 63) / 64;
+      const std::size_t lds = static_cast<std::size_t>(kShortWaves) * 64 * (reduce | 1) * sizeof(T);
+      hipLaunchKernelGGL((short_row_kernel<kOp, T>), dim3(grid_for(tiles, kShortWaves, kStrideBlocks)),
+                         dim3(64 * kShortWaves), lds, s, x, out, outer, static_cast<int>(reduce));
+      return check(hipGetLastError(), "reduce short row kernel launch");
+    }
     hipLaunchKernelGGL((lane_kernel<kOp, T>), dim3(grid_for(outer * inner, 256, kStrideBlocks)), dim3(256), 0,
                        s, x, out, outer, reduce, inner);
     return check(hipGetLastError(), "reduce lane kernel launch");

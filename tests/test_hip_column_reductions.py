@@ -201,3 +201,27 @@ def test_multi_run_selections(cx, shape, axes):
         assert_bits(getattr(cx, op)(hi, axes).numpy(), getattr(oracle, op)(yi, axes), f"i32 {op} {shape} {axes}")
     assert_bits(cx.Tensor(cx._core._argmax_axes(hi._impl, list(axes))).numpy(), oracle.argmax(yi, axes),
                 f"i32 argmax {shape} {axes}")
+
+
+@pytest.mark.parametrize("width", [2, 3, 4, 7, 8, 16, 31, 32, 33, 48, 63, 64])
+def test_short_rows_exact_order(cx, width):
+    # Contiguous rows of at most 64 elements: 64 rows per wave staged in LDS,
+    # each folded in the reference's order, so float32 sums are bit-exact
+    # too. 1000 rows leave a partial last tile; ties, NaNs and signed zeros
+    # sit in the rows.
+    rng = np.random.default_rng(width)
+    rows = 1000
+    x = rng.standard_normal((rows, width)).astype(np.float32) * np.float32(1e3)
+    x[1, :] = 0.0
+    x[1, width - 1] = -0.0
+    x[2, width // 2] = np.nan
+    x[3, :] = 7.0
+    x[4, :] = -np.inf
+    x[rows - 1, 0] = np.inf
+    h = cx.tensor(x, device="hip")
+    for op in ("sum", "mean", "max", "min", "argmax"):
+        assert_bits(getattr(cx, op)(h, 1).numpy(), getattr(oracle, op)(x, 1), f"{op} width {width}")
+    xi = rng.integers(-2**31, 2**31 - 1, (rows, width), dtype=np.int64).astype(np.int32)
+    hi = cx.tensor(xi, device="hip")
+    for op in ("sum", "max", "min", "argmax"):
+        assert_bits(getattr(cx, op)(hi, 1).numpy(), getattr(oracle, op)(xi, 1), f"i32 {op} width {width}")
