@@ -3,7 +3,8 @@
 // (core/inference.cpp:103-122) fused into the same pass.
 //
 // Contiguous rows (inner == 1) stay in registers, so each element is read from
-// HBM once and written once: rows of up to 1024 elements take one wave per row
+// HBM once and written once: rows of up to 128 elements pack several per wave
+// (row_packed_kernel), rows of up to 1024 elements take one wave per row
 // (kChunks 16-byte loads per lane, wave-wide butterfly statistics); rows of up
 // to kMaxSplit elements take one 256-thread block per row (four waves, whose
 // partial statistics meet in LDS). Longer rows use one block per row that
@@ -23,6 +24,8 @@ namespace tcx {
 namespace {
 
 constexpr int kMaxWaveChunks = 4;  // one wave per row up to 1024 floats
+constexpr std::int64_t kPackedMax = 128;      // rows up to this length pack several per wave
+constexpr std::int64_t kPackedBlocks = 4096;  // grid cap of the packed kernel (it strides over rows)
 constexpr int kMaxSplit = 16;      // one block per row up to 256*4*16 floats
 
 enum class RowOp { kSoftmax, kRms, kLayer };
@@ -208,6 +211,138 @@ row_cached_kernel(RowArgs a) {
     }
     // Keep the next row's loads from being hoisted into this row's live range.
     asm volatile("" ::: "memory");
+  }
+}
+
+// Rows of at most 128 elements, several per wave: a row takes L lanes (the
+// power of two at or above n / 4), each holding one float4 at column 4k
+// (vector rows) or four floats at k, k + L, k + 2L, k + 3L (scalar rows),
+// and a wave holds 64 / L rows. Row statistics are butterflies over the L
+// lanes of the row (both partners add the same operands, so the row's lanes
+// agree bit for bit); the per-element steps are row_cached_kernel's.
+__device__ __forceinline__ float group_sum(float v, int L) {
+  for (int offset = L >> 1; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
+  return v;
+}
+__device__ __forceinline__ float group_max_nan(float v, int L) {
+  for (int offset = L >> 1; offset > 0; offset >>= 1) {
+    const float o = __shfl_xor(v, offset, kWave);
+    v = (is_nan(o) || o > v) ? o : v;
+  }
+  return v;
+}
+__device__ __forceinline__ bool group_all(bool v, int L) {
+  int f = v ? 1 : 0;
+  for (int offset = L >> 1; offset > 0; offset >>= 1) f &= __shfl_xor(f, offset, kWave);
+  return f != 0;
+}
+
+template <RowOp kOp, bool kVec>
+__global__ __launch_bounds__(256) void row_packed_kernel(RowArgs a, int L) {
+  const int lane = threadIdx.x & 63;
+  const int k = lane & (L - 1);
+  const int rows_per_wave = 64 / L;
+  const int ni = static_cast<int>(a.n);
+  auto column = [&](int q) -> int { return kVec ? 4 * k + q : k + L * q; };
+  auto valid = [&](int q) -> bool { return column(q) < ni; };
+  const bool has_g = a.gamma != nullptr, has_b = a.beta != nullptr;
+  float g[4], b[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    g[q] = has_g && valid(q) ? a.gamma[column(q)] : 1.F;
+    b[q] = has_b && valid(q) ? a.beta[column(q)] : 0.F;
+  }
+  const std::int64_t per_pass = static_cast<std::int64_t>(gridDim.x) * 4 * rows_per_wave;
+  const std::int64_t passes = (a.rows + per_pass - 1) / per_pass;
+  // Every lane runs every pass (the butterflies need the whole group);
+  // rows past the end are masked.
+  for (std::int64_t pass = 0; pass < passes; ++pass) {
+    const std::int64_t row = pass * per_pass + (static_cast<std::int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) *
+                                                   rows_per_wave + lane / L;
+    const bool live = row < a.rows;
+    const float* __restrict__ x = a.x + (live ? row : 0) * a.n;
+    float* __restrict__ out = a.out + row * a.n;
+    float v[4] = {0.F, 0.F, 0.F, 0.F};
+    if (live) {
+      if constexpr (kVec) {
+        if (valid(0)) {
+          const float4_t t = stream_load(reinterpret_cast<const float4_t*>(x + column(0)));
+          v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (valid(q)) v[q] = x[column(q)];
+      }
+    }
+    if constexpr (kOp == RowOp::kSoftmax) {
+      float m = -__builtin_inff();
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (valid(q) && (is_nan(v[q]) || v[q] > m)) m = v[q];
+      m = group_max_nan(m, L);
+      float sum = 0.F;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (valid(q)) {
+          v[q] = exp_softmax(v[q] - m);
+          sum += v[q];
+        }
+      const float inv = 1.0F / group_sum(sum, L);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = v[q] * inv;
+    } else if constexpr (kOp == RowOp::kRms) {
+      float sum = 0.F;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float t = v[q] * v[q];
+        sum += t;  // masked elements are zero
+      }
+      const float scale = 1.0F / sqrtf(group_sum(sum, L) / static_cast<float>(ni) + a.eps);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = v[q] * scale;
+    } else {
+      const float first = live ? x[0] : 0.F;
+      float sum = 0.F;
+      bool equal = true;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        sum += v[q];
+        if (valid(q)) equal = equal && v[q] == first;
+      }
+      const float mean = group_sum(sum, L) / static_cast<float>(ni);
+      float d2 = 0.F;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (valid(q)) {
+          const float d = v[q] - mean;
+          d2 += d * d;
+        }
+      bool nan_row = false;
+      const float scale = finish_scale_ln(group_sum(d2, L), ni, a.eps, nan_row);
+      const bool const_row = group_all(equal, L) && __builtin_isfinite(first);
+      const bool special = const_row || nan_row;
+      const float special_value = const_row && a.eps != 0.F ? 0.F : __builtin_nanf("");
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = special ? special_value : (v[q] - mean) * scale;
+    }
+    if (!live) continue;
+    // Affine steps (multiply then add, each rounded) and the store.
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (has_g) v[q] = v[q] * g[q];
+      if (has_b) v[q] = v[q] + b[q];
+    }
+    if constexpr (kVec) {
+      if (valid(0)) {
+        const float4_t t = {v[0], v[1], v[2], v[3]};
+        __builtin_nontemporal_store(t, reinterpret_cast<float4_t*>(out + column(0)));
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (valid(q)) out[column(q)] = v[q];
+    }
   }
 }
 
@@ -1062,7 +1197,17 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
                    (a.gamma == nullptr || aligned16(a.gamma)) && (a.beta == nullptr || aligned16(a.beta));
   const std::int64_t chunks = (reduce + 255) / 256;  // per lane, one wave per row
   const std::int64_t per = (reduce + 1023) / 1024;    // per thread, one block per row
-  if (chunks <= 1) launch_cached<kOp, 1>(a, vec, s);
+  if (reduce <= kPackedMax) {
+    // Several rows per wave, L lanes per row.
+    int L = 1;
+    while (4 * L < reduce) L *= 2;
+    const std::int64_t waves = (outer + 64 / L - 1) / (64 / L);
+    const unsigned grid = grid_for(waves, 4, kPackedBlocks);
+    if (vec)
+      hipLaunchKernelGGL((row_packed_kernel<kOp, true>), dim3(grid), dim3(256), 0, s, a, L);
+    else
+      hipLaunchKernelGGL((row_packed_kernel<kOp, false>), dim3(grid), dim3(256), 0, s, a, L);
+  } else if (chunks <= 1) launch_cached<kOp, 1>(a, vec, s);
   else if (chunks <= 2) launch_cached<kOp, 2>(a, vec, s);
   else if (chunks <= kMaxWaveChunks) launch_cached<kOp, 4>(a, vec, s);
   else if (per <= 2) return launch_split<kOp, 2>(a, vec, s);

@@ -208,3 +208,22 @@ def test_column_row_ops_workspace_query():
     assert query(1, 8192, 64) == (32 + 1) * 64 * 16
     assert query(1, 100_000, 3) == (64 + 1) * 3 * 16
     assert query(1, 8192, 8192) == (16 + 1) * 8192 * 16
+
+
+@pytest.mark.parametrize("width", [1, 2, 3, 4, 5, 7, 8, 16, 31, 32, 33, 64, 100, 127, 128])
+def test_packed_short_rows(cx, width):
+    # Contiguous rows of at most 128 elements pack 64 / L rows per wave (L
+    # lanes per row); 1001 rows leave a partly filled last wave. Special
+    # rows: a NaN, infinities, a constant row (LayerNorm's fill), overflowing
+    # squares.
+    rng = np.random.default_rng(width)
+    x = (rng.standard_normal((1001, width)) * 3).astype(np.float32)
+    x[0, width // 2] = np.nan
+    x[1, width - 1] = np.inf
+    x[2, 0] = -np.inf
+    x[3] = -np.inf
+    x[4] = 2.5
+    x[5] *= np.float32(1e20)
+    check_all(cx, x, 1, f"packed width {width}", rng)
+    for eps in (0.0, 1e-5):
+        check_all(cx, np.full((70, width), 2.5, np.float32), 1, f"constant width {width} eps {eps}", rng, eps)
