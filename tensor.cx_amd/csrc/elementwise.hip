@@ -19,34 +19,89 @@ __device__ __forceinline__ float act_apply(float v, int act) {
   return v;
 }
 
+// 16-byte rows: a block takes 256 consecutive float4 columns of a row and
+// strides over rows (blockIdx.y), so a thread's bias float4 is loaded once and
+// no column index is divided out; loads and stores are non-temporal (each
+// element is touched once).
 __global__ __launch_bounds__(256) void bias_act_vec_kernel(const float* __restrict__ x,
                                                            const float* __restrict__ bias,
                                                            float* __restrict__ out, std::int64_t rows,
                                                            std::int64_t cols, int act) {
-  const std::int64_t quads = rows * cols / 4;
   const std::int64_t cq = cols / 4;
-  for (std::int64_t i = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < quads;
-       i += static_cast<std::int64_t>(gridDim.x) * blockDim.x) {
-    float4_t v = reinterpret_cast<const float4_t*>(x)[i];
+  const std::int64_t c = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (c >= cq) return;
+  float4_t b = {0.F, 0.F, 0.F, 0.F};
+  if (bias) b = reinterpret_cast<const float4_t*>(bias)[c];
+  for (std::int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    const std::int64_t i = r * cq + c;
+    float4_t v = stream_load(reinterpret_cast<const float4_t*>(x) + i);
     if (bias) {
-      const float4_t b = reinterpret_cast<const float4_t*>(bias)[i % cq];
       v.x = v.x + b.x; v.y = v.y + b.y; v.z = v.z + b.z; v.w = v.w + b.w;
     }
     v.x = act_apply(v.x, act); v.y = act_apply(v.y, act);
     v.z = act_apply(v.z, act); v.w = act_apply(v.w, act);
-    reinterpret_cast<float4_t*>(out)[i] = v;
+    __builtin_nontemporal_store(v, reinterpret_cast<float4_t*>(out) + i);
   }
 }
 
+// Narrower 16-byte rows: one float4 per thread per step over the flat
+// stream; the bias column advances by the grid stride modulo cols / 4, one
+// compare per step instead of a 64-bit division.
+__global__ __launch_bounds__(256) void bias_act_quad_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ bias,
+                                                            float* __restrict__ out, std::int64_t rows,
+                                                            std::int64_t cols, int act) {
+  const std::int64_t quads = rows * cols / 4, cq = cols / 4;
+  const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * blockDim.x;
+  const std::int64_t start = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const std::int64_t col_step = step % cq;
+  std::int64_t c = start % cq;
+  for (std::int64_t i = start; i < quads; i += step) {
+    float4_t v = stream_load(reinterpret_cast<const float4_t*>(x) + i);
+    if (bias) {
+      const float4_t b = reinterpret_cast<const float4_t*>(bias)[c];
+      v.x = v.x + b.x; v.y = v.y + b.y; v.z = v.z + b.z; v.w = v.w + b.w;
+    }
+    v.x = act_apply(v.x, act); v.y = act_apply(v.y, act);
+    v.z = act_apply(v.z, act); v.w = act_apply(v.w, act);
+    __builtin_nontemporal_store(v, reinterpret_cast<float4_t*>(out) + i);
+    c += col_step;
+    if (c >= cq) c -= cq;
+  }
+}
+
+// Any layout: one element per thread per step, the column stepped as above.
 __global__ __launch_bounds__(256) void bias_act_kernel(const float* __restrict__ x, const float* __restrict__ bias,
                                                        float* __restrict__ out, std::int64_t rows,
                                                        std::int64_t cols, int act) {
   const std::int64_t n = rows * cols;
-  for (std::int64_t i = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-       i += static_cast<std::int64_t>(gridDim.x) * blockDim.x) {
+  const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * blockDim.x;
+  const std::int64_t start = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const std::int64_t col_step = step % cols;
+  std::int64_t c = start % cols;
+  for (std::int64_t i = start; i < n; i += step) {
     float v = x[i];
-    if (bias) v = v + bias[i % cols];
+    if (bias) v = v + bias[c];
     out[i] = act_apply(v, act);
+    c += col_step;
+    if (c >= cols) c -= cols;
+  }
+}
+
+__device__ __forceinline__ float unary_apply(float v, int op) {
+  return op == TCX_UNARY_EXP ? expf(v) : act_apply(v, op == TCX_UNARY_GELU ? TCX_ACT_GELU : TCX_ACT_SILU);
+}
+
+// n a multiple of 4 on 16-byte aligned buffers: one float4 per thread per
+// step, non-temporal.
+__global__ __launch_bounds__(256) void unary_vec_kernel(const float* __restrict__ x, float* __restrict__ out,
+                                                        std::int64_t quads, int op) {
+  for (std::int64_t i = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < quads;
+       i += static_cast<std::int64_t>(gridDim.x) * blockDim.x) {
+    float4_t v = stream_load(reinterpret_cast<const float4_t*>(x) + i);
+    v.x = unary_apply(v.x, op); v.y = unary_apply(v.y, op);
+    v.z = unary_apply(v.z, op); v.w = unary_apply(v.w, op);
+    __builtin_nontemporal_store(v, reinterpret_cast<float4_t*>(out) + i);
   }
 }
 
@@ -55,7 +110,7 @@ __global__ __launch_bounds__(256) void unary_kernel(const float* __restrict__ x,
   for (std::int64_t i = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
        i += static_cast<std::int64_t>(gridDim.x) * blockDim.x) {
     const float v = x[i];
-    out[i] = op == TCX_UNARY_EXP ? expf(v) : act_apply(v, op == TCX_UNARY_GELU ? TCX_ACT_GELU : TCX_ACT_SILU);
+    out[i] = unary_apply(v, op);
   }
 }
 
@@ -111,6 +166,9 @@ __global__ __launch_bounds__(256) void fill_kernel(T* __restrict__ out, std::int
 
 bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15U) == 0; }
 constexpr std::int64_t kMaxBlocks = 256 * 32;  // 32 blocks per CU for grid-stride loops
+// The 16-byte streams: up to one float4 per thread (a 1 GiB copy probe ran
+// best so, at 81 % of HBM peak), grid-stride beyond.
+constexpr std::int64_t kVecBlocks = std::int64_t{1} << 18;
 
 }  // namespace
 }  // namespace tcx
@@ -127,8 +185,15 @@ int tcx_hip_bias_act_f32(const float* x, const float* bias, float* out, int64_t 
   const int rc = ready();
   if (rc != TCX_OK) return rc;
   const auto s = static_cast<hipStream_t>(stream);
-  if (cols % 4 == 0 && aligned16(x) && aligned16(out) && (bias == nullptr || aligned16(bias))) {
-    hipLaunchKernelGGL(bias_act_vec_kernel, dim3(grid_for(rows * cols / 4, 256, kMaxBlocks)), dim3(256), 0, s,
+  if (cols % 4 == 0 && cols >= 1024 && aligned16(x) && aligned16(out) && (bias == nullptr || aligned16(bias))) {
+    // Rows of at least 256 float4 (narrower rows would leave most of a
+    // block's lanes idle and take the scalar kernel).
+    const unsigned gx = grid_for(cols / 4, 256, kVecBlocks);
+    const std::int64_t gy_max = kVecBlocks / gx < 65535 ? kVecBlocks / gx : 65535;
+    const unsigned gy = static_cast<unsigned>(rows < gy_max ? rows : (gy_max > 0 ? gy_max : 1));
+    hipLaunchKernelGGL(bias_act_vec_kernel, dim3(gx, gy), dim3(256), 0, s, x, bias, out, rows, cols, act);
+  } else if (cols % 4 == 0 && aligned16(x) && aligned16(out) && (bias == nullptr || aligned16(bias))) {
+    hipLaunchKernelGGL(bias_act_quad_kernel, dim3(grid_for(rows * cols / 4, 256, kVecBlocks)), dim3(256), 0, s,
                        x, bias, out, rows, cols, act);
   } else {
     hipLaunchKernelGGL(bias_act_kernel, dim3(grid_for(rows * cols, 256, kMaxBlocks)), dim3(256), 0, s, x, bias,
@@ -145,8 +210,12 @@ int tcx_hip_unary_f32(int op, const float* x, float* out, int64_t n, tcx_stream_
   if (x == nullptr || out == nullptr) return fail(TCX_INVALID_ARGUMENT, "unary buffers are null");
   const int rc = ready();
   if (rc != TCX_OK) return rc;
-  hipLaunchKernelGGL(unary_kernel, dim3(grid_for(n, 256, kMaxBlocks)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), x, out, n, op);
+  if (n % 4 == 0 && aligned16(x) && aligned16(out))
+    hipLaunchKernelGGL(unary_vec_kernel, dim3(grid_for(n / 4, 256, kVecBlocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), x, out, n / 4, op);
+  else
+    hipLaunchKernelGGL(unary_kernel, dim3(grid_for(n, 256, kMaxBlocks)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), x, out, n, op);
   return check(hipGetLastError(), "unary launch");
 }
 

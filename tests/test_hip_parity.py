@@ -973,10 +973,13 @@ def test_unary_and_bias_act(cx):
         assert_close(fused, getattr(oracle, act)(oracle.binary("add", y, b)), 1e-6, 1e-6, act)
 
 
-@pytest.mark.parametrize("rows,cols", [(3, 5), (7, 1001), (2048, 2052), (4096, 4096)])
+@pytest.mark.parametrize("rows,cols", [(3, 5), (7, 1001), (2048, 2052), (4096, 4096), (999, 512), (300, 8),
+                                       (70000, 1024)])
 def test_bias_act_special_values(cx, rows, cols):
-    # The fused bias + activation kernel (float4 path for 4-aligned rows,
-    # scalar path otherwise, grid-stride loops at the largest size) with
+    # The fused bias + activation kernel (rows of 1024+ 4-aligned floats: a
+    # column tile per block striding over rows, 70000 rows past the grid's
+    # row extent; narrower 4-aligned rows: a flat float4 stream whose bias
+    # column steps with the grid stride; scalar path otherwise) with
     # non-finite and overflowing inputs in both operands, against the
     # reference's add-then-activation.
     rng = np.random.default_rng(29)
