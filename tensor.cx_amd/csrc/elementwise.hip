@@ -157,6 +157,43 @@ __global__ __launch_bounds__(256) void binary_kernel(const U* __restrict__ lhs, 
   }
 }
 
+// Broadcasts of at most two folded axes, out [R, C] (a same-shape stream is
+// [1, n]): a block strides over rows (blockIdx.y) and columns, so each
+// element's operand offsets are a multiply-add, not a chain of 64-bit
+// divisions. kVec: C a multiple of 4, inner strides 0 or 1, 16-byte aligned
+// rows; a stride-0 operand is one word per row, splatted.
+template <typename T, typename U, bool kVec>
+__global__ __launch_bounds__(256) void binary_2d_kernel(const U* __restrict__ lhs, const U* __restrict__ rhs,
+                                                        U* __restrict__ out, std::int64_t R, std::int64_t C,
+                                                        std::int64_t l0, std::int64_t l1, std::int64_t r0,
+                                                        std::int64_t r1, int op) {
+  using V = U __attribute__((ext_vector_type(4)));
+  const std::int64_t units = kVec ? C / 4 : C;
+  const std::int64_t cstep = static_cast<std::int64_t>(gridDim.x) * blockDim.x;
+  for (std::int64_t r = blockIdx.y; r < R; r += gridDim.y) {
+    const U* __restrict__ lrow = lhs + r * l0;
+    const U* __restrict__ rrow = rhs + r * r0;
+    U* __restrict__ orow = out + r * C;
+    for (std::int64_t c = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; c < units; c += cstep) {
+      if constexpr (kVec) {
+        V a, b;
+        if (l1) a = stream_load(reinterpret_cast<const V*>(lrow) + c);
+        else a = V{lrow[0], lrow[0], lrow[0], lrow[0]};
+        if (r1) b = stream_load(reinterpret_cast<const V*>(rrow) + c);
+        else b = V{rrow[0], rrow[0], rrow[0], rrow[0]};
+        V o;
+        o.x = static_cast<U>(binary_op<T>(static_cast<T>(a.x), static_cast<T>(b.x), op));
+        o.y = static_cast<U>(binary_op<T>(static_cast<T>(a.y), static_cast<T>(b.y), op));
+        o.z = static_cast<U>(binary_op<T>(static_cast<T>(a.z), static_cast<T>(b.z), op));
+        o.w = static_cast<U>(binary_op<T>(static_cast<T>(a.w), static_cast<T>(b.w), op));
+        __builtin_nontemporal_store(o, reinterpret_cast<V*>(orow) + c);
+      } else {
+        orow[c] = static_cast<U>(binary_op<T>(static_cast<T>(lrow[c * l1]), static_cast<T>(rrow[c * r1]), op));
+      }
+    }
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void fill_kernel(T* __restrict__ out, std::int64_t n, T value) {
   for (std::int64_t i = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
@@ -245,6 +282,29 @@ int tcx_hip_binary(int op, int dtype, const void* lhs, const void* rhs, void* ou
   const int rc = ready();
   if (rc != TCX_OK) return rc;
   const auto s = static_cast<hipStream_t>(stream);
+  if (rank <= 2) {
+    const std::int64_t R = rank == 2 ? m.shape[0] : 1, C = rank == 0 ? 1 : m.shape[rank - 1];
+    const std::int64_t l0 = rank == 2 ? m.lhs[0] : 0, r0 = rank == 2 ? m.rhs[0] : 0;
+    const std::int64_t l1 = rank == 0 ? 0 : m.lhs[rank - 1], r1 = rank == 0 ? 0 : m.rhs[rank - 1];
+    const bool unit = (l1 == 0 || l1 == 1) && (r1 == 0 || r1 == 1);
+    const bool vec = unit && C % 4 == 0 && aligned16(out) && (l1 == 0 || (aligned16(lhs) && l0 % 4 == 0)) &&
+                     (r1 == 0 || (aligned16(rhs) && r0 % 4 == 0));
+    const std::int64_t units = vec ? C / 4 : C;
+    const unsigned gx = grid_for(units, 256, kVecBlocks);
+    const std::int64_t gy_max = kVecBlocks / gx < 65535 ? kVecBlocks / gx : 65535;
+    const dim3 grid2(gx, static_cast<unsigned>(R < gy_max ? R : (gy_max > 0 ? gy_max : 1)));
+    auto launch2 = [&](auto kernel, auto p) {
+      using P = decltype(p);
+      hipLaunchKernelGGL(kernel, grid2, dim3(256), 0, s, static_cast<const P*>(lhs), static_cast<const P*>(rhs),
+                         static_cast<P*>(out), R, C, l0, l1, r0, r1, op);
+    };
+    if (dtype == TCX_FLOAT32)
+      vec ? launch2(binary_2d_kernel<float, float, true>, 0.F) : launch2(binary_2d_kernel<float, float, false>, 0.F);
+    else
+      vec ? launch2(binary_2d_kernel<std::uint32_t, std::uint32_t, true>, 0U)
+          : launch2(binary_2d_kernel<std::uint32_t, std::uint32_t, false>, 0U);
+    return check(hipGetLastError(), "binary launch");
+  }
   const dim3 grid(grid_for(n, 256, kMaxBlocks));
   if (dtype == TCX_FLOAT32)
     hipLaunchKernelGGL((binary_kernel<float, float>), grid, dim3(256), 0, s, static_cast<const float*>(lhs),

@@ -1098,3 +1098,27 @@ def test_memory_pool_reuse(cx):
             del y
         stats = pool.stats()
     assert stats["hits"] >= 1 and stats["active"]
+
+
+@pytest.mark.parametrize("ls,rs", [((300, 1028), (1028,)), ((300, 1028), (300, 1)), ((1, 1030), (257, 1)),
+                                   ((4097,), (4097,)), ((), (5000,)), ((64, 8), (64, 8)), ((3, 7, 5), (7, 1))])
+def test_binary_two_axis_streams(cx, ls, rs):
+    # Broadcasts that fold to at most two axes (a same-shape stream, a row or
+    # column operand, a scalar) take the row/column-strided kernel, 16-byte
+    # where the inner strides are 0 or 1 on aligned rows; bit-exact against
+    # the reference's one IEEE operation per element, int32 wrapping.
+    rng = np.random.default_rng(len(ls) * 7 + len(rs))
+    a = rng.standard_normal(ls).astype(np.float32)
+    b = rng.standard_normal(rs).astype(np.float32)
+    b.reshape(-1)[:1] = 0.0
+    ha, hb = cx.tensor(a, device="hip"), cx.tensor(b, device="hip")
+    for op, fn in (("add", lambda p, q: p + q), ("subtract", lambda p, q: p - q),
+                   ("multiply", lambda p, q: p * q), ("divide", lambda p, q: p / q)):
+        with np.errstate(all="ignore"):
+            assert_bits(fn(ha, hb).numpy(), oracle.binary(op, a, b), f"{op} {ls} {rs}")
+            assert_bits(fn(hb, ha).numpy(), oracle.binary(op, b, a), f"{op} {rs} {ls}")
+    ai = rng.integers(-2**31, 2**31 - 1, ls, dtype=np.int64).astype(np.int32)
+    bi = rng.integers(-2**31, 2**31 - 1, rs, dtype=np.int64).astype(np.int32)
+    hai, hbi = cx.tensor(ai, device="hip"), cx.tensor(bi, device="hip")
+    for op, fn in (("add", lambda p, q: p + q), ("multiply", lambda p, q: p * q)):
+        assert_bits(fn(hai, hbi).numpy(), oracle.binary(op, ai, bi), f"i32 {op} {ls} {rs}")
