@@ -124,6 +124,26 @@ def test_column_reduce_workspace_query():
     assert 0 < largest <= capi.REDUCE_NOALLOC_MAX_WORKSPACE
 
 
+def test_rownorm_workspace_query():
+    # Strided row ops split the rows of few column tiles (256 columns when
+    # inner is a multiple of 4, else 64, or the power of two at or above a
+    # narrower inner, whose waves step 256 / W or 64 / W rows): doubling
+    # while tiles x splits < 512 and each split keeps 64 x G rows; the
+    # workspace holds the split statistics and one parameter record per
+    # column, 16 bytes each. Contiguous rows and unsplit plans need none.
+    if not capi.LIB_PATH.exists():
+        pytest.fail("libtensorcx_hip.so is not built: run `python tensor.cx_amd/build.py`")
+    query = capi.lib().tcx_hip_rownorm_workspace_bytes
+    assert query(8192, 8192, 1) == 0
+    assert query(64, 64, 4096) == 0
+    assert query(1, 8192, 64) == (32 + 1) * 64 * 16
+    assert query(1, 100_000, 3) == (64 + 1) * 3 * 16
+    assert query(1, 8192, 8192) == (16 + 1) * 8192 * 16
+    assert query(0, 8192, 64) == 0 and query(1, 0, 64) == 0
+    largest = max(query(o, r, i) for o in (1, 3, 64) for r in (65, 1000, 2**20) for i in (2, 7, 64, 4096, 2**16))
+    assert 0 < largest <= 16 << 20
+
+
 CONTRACT = ROOT / "tests" / "cpp" / "_bin" / "hip_backend_contract"
 
 

@@ -197,18 +197,6 @@ def test_column_row_ops_unaligned_and_unsplit(capi):
         capi.softmax_ws(dx.ptr, out.ptr, outer, rows, inner, small)
 
 
-def test_column_row_ops_workspace_query():
-    # Host-side plan: contiguous rows and unsplit strided plans need none.
-    import tensorcx_hip_capi as capi
-    if not capi.LIB_PATH.exists():
-        pytest.fail("libtensorcx_hip.so is not built")
-    query = capi.lib().tcx_hip_rownorm_workspace_bytes
-    assert query(8192, 8192, 1) == 0
-    assert query(64, 64, 4096) == 0
-    assert query(1, 8192, 64) == (32 + 1) * 64 * 16
-    assert query(1, 100_000, 3) == (64 + 1) * 3 * 16
-    assert query(1, 8192, 8192) == (16 + 1) * 8192 * 16
-
 
 @pytest.mark.parametrize("width", [1, 2, 3, 4, 5, 7, 8, 16, 31, 32, 33, 64, 100, 127, 128])
 def test_packed_short_rows(cx, width):
