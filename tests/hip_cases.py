@@ -6,7 +6,7 @@ Bars (stated once, used everywhere):
     SEQUENTIAL_MAX elements, and selections of several reduced runs);
   * matmul / linear: max|dC| / (sqrt(K) * rms(A) * rms(B)) <= 1e-4;
   * float32 sum/mean over more than SEQUENTIAL_MAX elements of one reduced
-    run (tree order along rows, blocked order down columns):
+    run (tree order along rows, a fixed interleaved order down columns):
     max|d| / sum|x| <= 1e-5 per output, a mean's error taken times its count;
   * softmax, LayerNorm, RMSNorm, affine norms, MLP output:
     allclose(rtol=1e-5, atol=1e-5), the reference's reduction class;
