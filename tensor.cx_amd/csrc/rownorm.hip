@@ -646,8 +646,9 @@ __global__ __launch_bounds__(256) void row_block_kernel(RowArgs a) {
 // out are 16-byte aligned, else x 1; or the power of two at or above a
 // narrower inner, the wave then stepping G = 64 x kVec / W rows at a time).
 // A block of kNormWaves waves takes one (split, tile) pair; its waves take
-// contiguous runs of the split's rows and lane (g, c) walks rows r0 + g,
-// r0 + g + G, ... of column c with kNormDepth rows loaded at once.
+// the split's row groups in turn (as the column reductions) and lane (g, c)
+// of wave w walks rows rb + w G + g + i G kNormWaves of column c with
+// kNormDepth rows loaded at once.
 //
 // Column statistics fold lane -> row groups (butterfly) -> waves (LDS, in
 // order) -> splits (in order); then each element is written from them in a
@@ -786,10 +787,12 @@ __device__ __forceinline__ void col_norm_block(const ColNormArgs& a, std::int64_
   const std::int64_t split = b / col_tiles, tile = b % col_tiles;
   const std::int64_t o = tile / tiles_per_outer, tile_col = (tile % tiles_per_outer) * W;
   const std::int64_t rb = split * a.split_rows, re = min(R, rb + a.split_rows);
-  const std::int64_t per_wave = (re - rb + kNormWaves - 1) / kNormWaves;
-  const std::int64_t r0 = min(re, rb + wave * per_wave), r1 = min(re, r0 + per_wave);
-  const std::int64_t row0 = r0 + g;  // this lane's rows: row0, row0 + G, ... below r1
-  const std::int64_t n = row0 < r1 ? (r1 - row0 + G - 1) / G : 0;
+  // This lane's rows: row0, row0 + GS, ... below re, GS = G x kNormWaves
+  // (the block's waves take row groups in turn, streaming neighbouring rows
+  // together).
+  const std::int64_t GS = static_cast<std::int64_t>(G) * kNormWaves;
+  const std::int64_t row0 = rb + wave * G + g;
+  const std::int64_t n = row0 < re ? (re - row0 + GS - 1) / GS : 0;
   // Lanes past the last column read the last kVec columns (in bounds: inner
   // is a multiple of kVec) and store nothing.
   const std::int64_t j = tile_col + cl;
@@ -797,7 +800,7 @@ __device__ __forceinline__ void col_norm_block(const ColNormArgs& a, std::int64_
   const bool t_in = t < W && tile_col + t < inner;  // thread t folds column tile_col + t
   const std::int64_t offset = o * R * inner + row0 * inner + (col_in ? j : inner - kVec);
   const float* __restrict__ xb = a.x + offset;
-  const std::int64_t step = static_cast<std::int64_t>(G) * inner;
+  const std::int64_t step = GS * inner;
   auto load_row = [&](std::int64_t i, float (&v)[kVec]) {
     if constexpr (kVec == 4) {
       const float4_t q = stream_load(reinterpret_cast<const float4_t*>(xb + i * step));
@@ -941,7 +944,7 @@ __device__ __forceinline__ void col_norm_block(const ColNormArgs& a, std::int64_
 #pragma unroll
     for (int u = 0; u < kNormDepth; ++u) {
       if (i + u >= n) continue;
-      const std::int64_t r = row0 + (i + u) * G;
+      const std::int64_t r = row0 + (i + u) * GS;
       const float gr = a.gamma ? a.gamma[r] : 1.F;
       const float br = a.beta ? a.beta[r] : 0.F;
       float y[kVec];
