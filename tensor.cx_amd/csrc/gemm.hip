@@ -38,6 +38,9 @@ bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15
 // Long-operand rows (16 per block) from which the streaming kernel takes a
 // skinny GEMM.
 constexpr std::int64_t kStreamMinRows = 256;
+// Batched products of items up to 64 x 64 x 64 run the tiny kernel from this
+// many items on (fewer items leave the tiled kernels enough tiles).
+constexpr std::int64_t kTinyMinBatches = 64;
 
 // Shapes of >= 256 full 128x128 tiles: the direct kernel on 128x128 tiles of
 // eight waves (64x32 for a transposed B, 32x64 for a [k, n] B; 64-68 KB of
@@ -195,6 +198,8 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
       return gemm::launch_gemv(lhs, rhs, out, d->bias, d->m, d->k, batches, lbs, rbs, d->m, 1, false,
                                d->activation, s);
   }
+  // Many small products: whole items staged in LDS, several per block.
+  if (batches >= kTinyMinBatches && gemm::tiny_fits(d->m, d->n, d->k)) return gemm::launch_tiny(args, trans_b, s);
   // One skinny operand against a long one: at most 32 rows of A against a
   // transposed B (the decode-time linear x W^T), or at most 32 columns of B.
   // The streaming kernel reads the long operand's rows once, 16 per block.

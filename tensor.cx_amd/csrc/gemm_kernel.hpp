@@ -1408,6 +1408,135 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(const float* __restrict__
   y[batch * y_batch + i * y_stride] = activate(sum, act);
 }
 
+// Many small products (M, N, K <= kTinyMax): P whole items per block are
+// staged in LDS (A [P][M][K], B [P][K][N], a transposed B transposed on the
+// way in), then each thread computes outputs of the block's items in output
+// order, summing its k in order as separately rounded products and sums
+// (the reference's loop order, -ffp-contract=off). One 64x64 tile per item
+// wastes most of an MFMA tile on 8x8 items and pays a block's latency per
+// item: 65536 batches of 8x8x8 took 3.6 ms on the tiled kernel.
+constexpr std::int64_t kTinyMax = 64;
+constexpr int kTinyFloats = 8192;  // 32 KB of LDS per block
+
+constexpr int kTinyItems = 256;    // most items per block
+
+template <bool kTransB>
+__global__ __launch_bounds__(256) void gemm_f32_tiny_kernel(GemmArgs a, int P) {
+  __shared__ float lds[kTinyFloats];
+  __shared__ std::int64_t item_off[2][kTinyItems];  // each item's A and B offsets
+  const int M = static_cast<int>(a.m), N = static_cast<int>(a.n), K = static_cast<int>(a.k);
+  const int a_size = M * K, b_size = K * N, item_size = a_size + b_size;
+  const std::int64_t items = a.total_tiles;
+  const std::int64_t first = static_cast<std::int64_t>(blockIdx.x) * P;
+  const int count = static_cast<int>(items - first < P ? items - first : P);
+  for (int p = threadIdx.x; p < count; p += blockDim.x) {
+    std::int64_t b = first + p, lo = 0, ro = 0;
+    for (int ax = a.batch_rank - 1; ax >= 0; --ax) {
+      const std::int64_t e = a.batch_shape[ax];
+      const std::int64_t c = b % e;
+      b /= e;
+      lo += c * a.lhs_bs[ax];
+      ro += c * a.rhs_bs[ax];
+    }
+    item_off[0][p] = lo;
+    item_off[1][p] = ro;
+  }
+  __syncthreads();
+  // Stage item p's A at lds[p * item_size] and its B (as [K][N]) after it:
+  // one flat walk over the block's elements, eight loads in flight; each
+  // thread's (item, offset) advances by the block size without a division.
+  const int total = count * item_size;
+  const int T = static_cast<int>(blockDim.x);
+  const int dp = T / item_size, dr = T % item_size;
+  int sp = static_cast<int>(threadIdx.x) / item_size, sr = static_cast<int>(threadIdx.x) % item_size;
+  for (int e0 = threadIdx.x; e0 < total; e0 += 8 * T) {
+    float v[8];
+    int dst[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (e0 + u * T < total) {
+        if (sr < a_size) {
+          v[u] = a.lhs[item_off[0][sp] + sr];
+          dst[u] = sp * item_size + sr;
+        } else {
+          const int rb = sr - a_size;
+          v[u] = a.rhs[item_off[1][sp] + rb];
+          if constexpr (kTransB) {
+            const int nn = rb / K, kk = rb - nn * K;  // B is [N][K]
+            dst[u] = sp * item_size + a_size + kk * N + nn;
+          } else {
+            dst[u] = sp * item_size + sr;
+          }
+        }
+      }
+      sp += dp;
+      sr += dr;
+      if (sr >= item_size) {
+        sr -= item_size;
+        ++sp;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (e0 + u * T < total) lds[dst[u]] = v[u];
+  }
+  __syncthreads();
+  // Outputs in output order: this thread's (item, row, column) advances by
+  // the block size the same way.
+  const int outs = M * N;
+  const int op = T / outs, orem = T % outs, oi = orem / N, oj = orem % N;
+  int p = static_cast<int>(threadIdx.x) / outs;
+  int i = (static_cast<int>(threadIdx.x) % outs) / N, j = static_cast<int>(threadIdx.x) % N;
+  for (int e = threadIdx.x; e < count * outs; e += T) {
+    const float* A = lds + p * item_size + i * K;
+    const float* B = lds + p * item_size + a_size + j;
+    float acc = 0.F;
+    for (int k = 0; k < K; ++k) acc += A[k] * B[k * N];
+    if (a.bias != nullptr) acc = acc + a.bias[j];
+    a.out[(first + p) * outs + i * N + j] = activate(acc, a.activation);
+    p += op;
+    i += oi;
+    j += oj;
+    if (j >= N) {
+      j -= N;
+      ++i;
+    }
+    if (i >= M) {
+      i -= M;
+      ++p;
+    }
+  }
+}
+
+inline bool tiny_fits(std::int64_t m, std::int64_t n, std::int64_t k) {
+  return m >= 1 && n >= 1 && k >= 1 && m <= kTinyMax && n <= kTinyMax && k <= kTinyMax &&
+         m * k + k * n <= kTinyFloats;
+}
+
+inline int launch_tiny(GemmArgs& args, bool trans_b, hipStream_t stream) {
+  const std::int64_t item = args.m * args.k + args.k * args.n;
+  if (!tiny_fits(args.m, args.n, args.k) || item <= 0)
+    return fail(TCX_INTERNAL, "tiny gemm needs M, N, K <= 64");
+  const std::int64_t items = args.total_tiles;  // the caller passes the batch count
+  // Items per block: as many as the LDS holds, at most enough for about 16
+  // outputs per thread and at most kTinyItems, and at least one.
+  std::int64_t P = kTinyFloats / item;
+  const std::int64_t by_outputs = (16 * 256 + args.m * args.n - 1) / (args.m * args.n);
+  if (P > by_outputs) P = by_outputs;
+  if (P > kTinyItems) P = kTinyItems;
+  if (P < 1) P = 1;
+  const std::int64_t blocks = (items + P - 1) / P;
+  if (blocks > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
+  if (trans_b)
+    hipLaunchKernelGGL((gemm_f32_tiny_kernel<true>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                       args, static_cast<int>(P));
+  else
+    hipLaunchKernelGGL((gemm_f32_tiny_kernel<false>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                       args, static_cast<int>(P));
+  return check(hipGetLastError(), "gemm_f32 tiny launch");
+}
+
+
 // rows x batches dot products of K (K % 4 == 0, R, v and every batch offset
 // 16-byte aligned): KW waves per row, more when rows are few.
 inline int launch_gemv(const float* R, const float* v, float* y, const float* bias, std::int64_t rows,

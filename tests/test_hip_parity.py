@@ -1122,3 +1122,30 @@ def test_binary_two_axis_streams(cx, ls, rs):
     hai, hbi = cx.tensor(ai, device="hip"), cx.tensor(bi, device="hip")
     for op, fn in (("add", lambda p, q: p + q), ("multiply", lambda p, q: p * q)):
         assert_bits(fn(hai, hbi).numpy(), oracle.binary(op, ai, bi), f"i32 {op} {ls} {rs}")
+
+
+@pytest.mark.parametrize("batch,m,n,k,trans", [(65536, 8, 8, 8, False), (300, 16, 16, 16, True), (64, 64, 64, 64, False),
+                                               (100, 3, 5, 7, False), (77, 1, 64, 33, True), (129, 64, 1, 2, False),
+                                               (64, 17, 29, 64, True)])
+def test_matmul_tiny_batched(cx, batch, m, n, k, trans):
+    # Many small products (items up to 64 x 64 x 64, at least 64 of them)
+    # stage whole items in LDS, several per block, and sum each output's k in
+    # order: bit-exact against the reference's sequential float32 loop.
+    rng = np.random.default_rng(batch + m + n + k)
+    clean = rng.standard_normal((batch, m, k)).astype(np.float32)
+    b = rng.standard_normal((batch, n, k) if trans else (batch, k, n)).astype(np.float32)
+    a = clean.copy()
+    a.reshape(-1)[5] = np.inf
+    bt = np.ascontiguousarray(np.swapaxes(b, 1, 2)) if trans else b
+    expected = oracle.matmul(a, bt)
+    ha, hb = cx.tensor(a, device="hip"), cx.tensor(bt, device="hip")
+    with np.errstate(all="ignore"):
+        assert_bits(cx.matmul(ha, hb).numpy(), expected, f"tiny {batch}x{m}x{n}x{k}")
+    if trans:
+        # The transposed-B route: linear over batched rows (x @ W^T, W shared).
+        w = rng.standard_normal((n, k)).astype(np.float32)
+        bias = rng.standard_normal(n).astype(np.float32)
+        hc = cx.tensor(clean, device="hip")
+        got = cx.linear(hc, cx.tensor(w, device="hip"), cx.tensor(bias, device="hip")).numpy()
+        assert_matmul(got, (clean.astype(np.float64) @ w.T.astype(np.float64)) + bias, clean.reshape(-1, k), w.T,
+                      f"tiny linear {batch}x{m}x{n}x{k}")
