@@ -41,6 +41,8 @@ constexpr std::int64_t kStreamMinRows = 256;
 // Batched products of items up to 64 x 64 x 64 run the tiny kernel from this
 // many items on (fewer items leave the tiled kernels enough tiles).
 constexpr std::int64_t kTinyMinBatches = 64;
+// Products with K <= 16 stream their output from this many outputs on.
+constexpr std::int64_t kSmallKMinOutputs = 65536;
 
 // Shapes of >= 256 full 128x128 tiles: the direct kernel on 128x128 tiles of
 // eight waves (64x32 for a transposed B, 32x64 for a [k, n] B; 64-68 KB of
@@ -198,6 +200,14 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
       return gemm::launch_gemv(lhs, rhs, out, d->bias, d->m, d->k, batches, lbs, rbs, d->m, 1, false,
                                d->activation, s);
   }
+  // A short K (unbatched, row-major B): the output streamed as float4 from B
+  // columns held in registers. Against the tiled kernels: 4096 x 4096 x 4
+  // 26.5 -> 15.2 us, x 8 26.5 -> 17.0, x 16 26.6 -> 23.8, 1000000 x 16 x 16
+  // 114 -> 36. A transposed B's strided column loads made 3000 x 1028 x 16
+  // take 67 us, so it keeps the tiled route.
+  if (d->batch_rank == 0 && !trans_b && d->k >= 1 && d->k <= gemm::kSmallK && d->n % 4 == 0 && aligned16(out) &&
+      aligned16(rhs) && d->m * d->n >= kSmallKMinOutputs)
+    return gemm::launch_smallk(args, false, s);
   // Many small products: whole items staged in LDS, several per block.
   if (batches >= kTinyMinBatches && gemm::tiny_fits(d->m, d->n, d->k)) return gemm::launch_tiny(args, trans_b, s);
   // One skinny operand against a long one: at most 32 rows of A against a

@@ -1508,6 +1508,113 @@ __global__ __launch_bounds__(256) void gemm_f32_tiny_kernel(GemmArgs a, int P) {
   }
 }
 
+// Products with K <= kSmallK (unbatched, N a multiple of 4, 16-byte aligned
+// B rows and output): each thread owns four output columns, holds their K x 4
+// B values in registers and walks rows, so the output is written once as a
+// float4 stream and A rows come from cache. Rows of at least 256 float4 take
+// a column tile of 256 per block and stride over rows (blockIdx.y);
+// narrower rows put 256 / (N / 4) rows in a block. Each output sums its k in
+// order as separately rounded products and sums, the reference's loop. A
+// grid of about 2048 blocks makes each block load its B columns once for
+// many rows (one row per block took 26.8 us at 4096 x 4096 x 4, 15.2 us so).
+constexpr std::int64_t kSmallK = 16;
+
+template <bool kTransB>
+__global__ __launch_bounds__(256) void gemm_f32_smallk_kernel(GemmArgs a, int rows_per_block) {
+  const std::int64_t M = a.m, N = a.n;
+  const int K = static_cast<int>(a.k);
+  const std::int64_t CQ = N / 4;
+  std::int64_t cq, row0, row_step;
+  if (rows_per_block == 0) {
+    cq = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    row0 = blockIdx.y;
+    row_step = gridDim.y;
+  } else {
+    cq = threadIdx.x % CQ;
+    const int rb = static_cast<int>(threadIdx.x / CQ);
+    if (rb >= rows_per_block) return;
+    row0 = static_cast<std::int64_t>(blockIdx.y) * rows_per_block + rb;
+    row_step = static_cast<std::int64_t>(gridDim.y) * rows_per_block;
+  }
+  if (cq >= CQ) return;
+  float4_t b[kSmallK];
+#pragma unroll
+  for (int k = 0; k < kSmallK; ++k) {
+    b[k] = float4_t{0.F, 0.F, 0.F, 0.F};
+    if (k < K) {
+      if constexpr (kTransB) {  // B is [N][K]
+        const float* col = a.rhs + 4 * cq * K + k;
+        b[k] = float4_t{col[0], col[K], col[2 * K], col[3 * K]};
+      } else {
+        b[k] = reinterpret_cast<const float4_t*>(a.rhs + k * N)[cq];
+      }
+    }
+  }
+  float4_t bias = {0.F, 0.F, 0.F, 0.F};
+  if (a.bias != nullptr) bias = float4_t{a.bias[4 * cq], a.bias[4 * cq + 1], a.bias[4 * cq + 2], a.bias[4 * cq + 3]};
+  // Two rows per step: both rows' A values are loaded before either is used.
+  for (std::int64_t m = row0; m < M; m += 2 * row_step) {
+    const std::int64_t m2 = m + row_step < M ? m + row_step : m;  // a lone last row repeats itself
+    float x0[kSmallK], x1[kSmallK];
+#pragma unroll
+    for (int k = 0; k < kSmallK; ++k) {
+      x0[k] = k < K ? a.lhs[m * K + k] : 0.F;
+      x1[k] = k < K ? a.lhs[m2 * K + k] : 0.F;
+    }
+    float4_t acc[2] = {{0.F, 0.F, 0.F, 0.F}, {0.F, 0.F, 0.F, 0.F}};
+#pragma unroll
+    for (int k = 0; k < kSmallK; ++k) {
+      if (k < K) {
+        acc[0].x += x0[k] * b[k].x;
+        acc[0].y += x0[k] * b[k].y;
+        acc[0].z += x0[k] * b[k].z;
+        acc[0].w += x0[k] * b[k].w;
+        acc[1].x += x1[k] * b[k].x;
+        acc[1].y += x1[k] * b[k].y;
+        acc[1].z += x1[k] * b[k].z;
+        acc[1].w += x1[k] * b[k].w;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      float4_t v = acc[r];
+      if (a.bias != nullptr) {
+        v.x = v.x + bias.x; v.y = v.y + bias.y; v.z = v.z + bias.z; v.w = v.w + bias.w;
+      }
+      v.x = activate(v.x, a.activation);
+      v.y = activate(v.y, a.activation);
+      v.z = activate(v.z, a.activation);
+      v.w = activate(v.w, a.activation);
+      if (r == 0 || m2 != m) __builtin_nontemporal_store(v, reinterpret_cast<float4_t*>(a.out + (r ? m2 : m) * N) + cq);
+    }
+  }
+}
+
+inline int launch_smallk(GemmArgs& args, bool trans_b, hipStream_t stream) {
+  if (args.k < 1 || args.k > kSmallK || args.n % 4 != 0)
+    return fail(TCX_INTERNAL, "small-K gemm needs 1 <= K <= 16 and N a multiple of 4");
+  const std::int64_t CQ = args.n / 4;
+  int rows_per_block = 0;
+  unsigned gx = 1;
+  std::int64_t rows_in_y = args.m;
+  if (CQ >= 256) {
+    gx = static_cast<unsigned>((CQ + 255) / 256);
+  } else {
+    rows_per_block = static_cast<int>(256 / CQ);
+    rows_in_y = (args.m + rows_per_block - 1) / rows_per_block;
+  }
+  // About 2048 blocks (eight per CU): each loads its B columns once and
+  // strides over many rows.
+  const std::int64_t gy_cap = 2048 / gx > 0 ? 2048 / gx : 1;
+  const std::int64_t gy = rows_in_y < gy_cap ? rows_in_y : (gy_cap < 65535 ? gy_cap : 65535);
+  const dim3 grid(gx, static_cast<unsigned>(gy < 65535 ? gy : 65535));
+  if (trans_b)
+    hipLaunchKernelGGL((gemm_f32_smallk_kernel<true>), grid, dim3(256), 0, stream, args, rows_per_block);
+  else
+    hipLaunchKernelGGL((gemm_f32_smallk_kernel<false>), grid, dim3(256), 0, stream, args, rows_per_block);
+  return check(hipGetLastError(), "gemm_f32 small-K launch");
+}
+
 inline bool tiny_fits(std::int64_t m, std::int64_t n, std::int64_t k) {
   return m >= 1 && n >= 1 && k >= 1 && m <= kTinyMax && n <= kTinyMax && k <= kTinyMax &&
          m * k + k * n <= kTinyFloats;

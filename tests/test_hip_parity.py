@@ -1149,3 +1149,27 @@ def test_matmul_tiny_batched(cx, batch, m, n, k, trans):
         got = cx.linear(hc, cx.tensor(w, device="hip"), cx.tensor(bias, device="hip")).numpy()
         assert_matmul(got, (clean.astype(np.float64) @ w.T.astype(np.float64)) + bias, clean.reshape(-1, k), w.T,
                       f"tiny linear {batch}x{m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k,trans", [(4096, 4096, 4, False), (3000, 1028, 16, True), (20000, 16, 16, False),
+                                         (70000, 4, 1, False), (999, 2052, 7, False), (513, 260, 13, True)])
+def test_matmul_small_k(cx, m, n, k, trans):
+    # K <= 16 (unbatched, at least 65536 outputs): B columns in registers and
+    # the output streamed as float4 rows, each output's k summed in order:
+    # bit-exact against the reference's sequential float32 loop, and fused
+    # bias + activation through linear.
+    rng = np.random.default_rng(m + n + k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((n, k) if trans else (k, n)).astype(np.float32)
+    a[3, 0] = np.inf
+    bt = np.ascontiguousarray(b.T) if trans else b
+    with np.errstate(all="ignore"):
+        expected = oracle.matmul(a, bt)
+        assert_bits(cx.matmul(cx.tensor(a, device="hip"), cx.tensor(bt, device="hip")).numpy(), expected,
+                    f"small-k {m}x{n}x{k}")
+    if trans:
+        clean = rng.standard_normal((m, k)).astype(np.float32)
+        bias = rng.standard_normal(n).astype(np.float32)
+        got = cx.linear(cx.tensor(clean, device="hip"), cx.tensor(b, device="hip"), cx.tensor(bias, device="hip"))
+        assert_matmul(got.numpy(), clean.astype(np.float64) @ b.T.astype(np.float64) + bias, clean, b.T,
+                      f"small-k linear {m}x{n}x{k}")
