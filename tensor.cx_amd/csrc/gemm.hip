@@ -43,6 +43,9 @@ constexpr std::int64_t kStreamMinRows = 256;
 constexpr std::int64_t kTinyMinBatches = 64;
 // Products with K <= 16 stream their output from this many outputs on.
 constexpr std::int64_t kSmallKMinOutputs = 65536;
+// One-row products against a row-major B take the vector-matrix kernel from
+// this many 1024-column blocks on.
+constexpr std::int64_t kVecMatMinBlocks = 128;
 
 // Shapes of >= 256 full 128x128 tiles: the direct kernel on 128x128 tiles of
 // eight waves (64x32 for a transposed B, 32x64 for a [k, n] B; 64-68 KB of
@@ -200,6 +203,14 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
       return gemm::launch_gemv(lhs, rhs, out, d->bias, d->m, d->k, batches, lbs, rbs, d->m, 1, false,
                                d->activation, s);
   }
+  // One row of A against a row-major B per batch item (rows of 512+
+  // columns), with enough items x 1024-column chunks to give every CU a
+  // block.
+  bool rhs_strides_vec = true;  // A's row is read a word at a time: only B's rows need 16 bytes
+  for (int i = 0; i < d->batch_rank; ++i) rhs_strides_vec = rhs_strides_vec && d->rhs_batch_strides[i] % 4 == 0;
+  if (d->m == 1 && !trans_b && d->n >= 512 && d->n % 4 == 0 && aligned16(rhs) && aligned16(out) &&
+      rhs_strides_vec && batches * ((d->n / 4 + 255) / 256) >= kVecMatMinBlocks)
+    return gemm::launch_vecmat(args, s);
   // A short K (unbatched, row-major B): the output streamed as float4 from B
   // columns held in registers. Against the tiled kernels: 4096 x 4096 x 4
   // 26.5 -> 15.2 us, x 8 26.5 -> 17.0, x 16 26.6 -> 23.8, 1000000 x 16 x 16

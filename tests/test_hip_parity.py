@@ -1173,3 +1173,19 @@ def test_matmul_small_k(cx, m, n, k, trans):
         got = cx.linear(cx.tensor(clean, device="hip"), cx.tensor(b, device="hip"), cx.tensor(bias, device="hip"))
         assert_matmul(got.numpy(), clean.astype(np.float64) @ b.T.astype(np.float64) + bias, clean, b.T,
                       f"small-k linear {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("batch,n,k", [(200, 2048, 1024), (128, 1028, 333), (300, 516, 7)])
+def test_matmul_batched_vector_matrix(cx, batch, n, k):
+    # One row of A against a row-major B per batch item: 1024-column blocks,
+    # K in four in-block groups added in order; at the matmul bar.
+    rng = np.random.default_rng(batch + n + k)
+    a = rng.standard_normal((batch, 1, k)).astype(np.float32)
+    b = rng.standard_normal((batch, k, n)).astype(np.float32)
+    got = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
+    assert_matmul(got, np.matmul(a.astype(np.float64), b.astype(np.float64)), a, b, f"vecmat {batch}x{n}x{k}")
+    # Dyadic operands make every partial sum exact: any order matches bitwise.
+    ad = rng.integers(-8, 9, (batch, 1, k)).astype(np.float32)
+    bd = rng.integers(-8, 9, (batch, k, n)).astype(np.float32)
+    got = cx.matmul(cx.tensor(ad, device="hip"), cx.tensor(bd, device="hip")).numpy()
+    assert_bits(got, np.matmul(ad.astype(np.float64), bd.astype(np.float64)).astype(np.float32), "vecmat dyadic")
