@@ -237,6 +237,14 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
       if (aligned16(rhs)) return gemm::launch_stream<false, false>(args, s);
     }
   }
+  // Many tiles of a short K (<= 64) and a narrow N (<= 64): the 64x64 tiles
+  // spend a block's life on one k-tile's latency; the small kernel's 32x32
+  // tiles (register-direct, little LDS, several blocks per CU) halve it:
+  // 1000000 x 64 x 64 468 -> 251 us. With wide rows it lost (4096 x 4096 x 64:
+  // 30 -> 61 us), so it stays narrow.
+  if (vec && d->k <= 64 && d->n <= 64 && gemm::small_fits(d->m, d->n, d->k) &&
+      ((d->m + 63) / 64) * ((d->n + 63) / 64) * batches > 768)
+    return gemm::launch_small(args, trans_b, s);
   const std::int64_t tiles_256 = ((d->m + 255) / 256) * ((d->n + 255) / 256) * batches;
   // (Unaligned shapes take the scalar-load variant, which does not fit the
   // 256x256 tile's registers; they use the 128x128 tile.)

@@ -1189,3 +1189,19 @@ def test_matmul_batched_vector_matrix(cx, batch, n, k):
     bd = rng.integers(-8, 9, (batch, k, n)).astype(np.float32)
     got = cx.matmul(cx.tensor(ad, device="hip"), cx.tensor(bd, device="hip")).numpy()
     assert_bits(got, np.matmul(ad.astype(np.float64), bd.astype(np.float64)).astype(np.float32), "vecmat dyadic")
+
+
+@pytest.mark.parametrize("m,n,k,trans", [(70000, 64, 64, False), (50000, 48, 32, True), (40000, 20, 60, False)])
+def test_matmul_tall_short_k_narrow_n(cx, m, n, k, trans):
+    # Many 64x64 tiles of a short K and a narrow N run the small kernel's
+    # 32x32 tiles; at the matmul bar, fused bias + activation included.
+    rng = np.random.default_rng(m + n + k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((n, k) if trans else (k, n)).astype(np.float32)
+    bt = b.T if trans else b
+    got = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(np.ascontiguousarray(bt), device="hip")).numpy()
+    assert_matmul(got, a.astype(np.float64) @ bt.astype(np.float64), a, bt, f"tall {m}x{n}x{k}")
+    if trans:
+        bias = rng.standard_normal(n).astype(np.float32)
+        got = cx.linear(cx.tensor(a, device="hip"), cx.tensor(b, device="hip"), cx.tensor(bias, device="hip")).numpy()
+        assert_matmul(got, a.astype(np.float64) @ b.T.astype(np.float64) + bias, a, b.T, f"tall linear {m}x{n}x{k}")
