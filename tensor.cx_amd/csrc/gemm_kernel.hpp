@@ -1414,15 +1414,16 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(const float* __restrict__
 // order, summing its k in order as separately rounded products and sums
 // (the reference's loop order, -ffp-contract=off). One 64x64 tile per item
 // wastes most of an MFMA tile on 8x8 items and pays a block's latency per
-// item: 65536 batches of 8x8x8 took 3.6 ms on the tiled kernel.
+// item: 65536 batches of 8x8x8 took 3.6 ms on the tiled kernel, 16 us here;
+// four columns per thread (kQuad) took 64^3 x 4096 from 145 to 88 us.
 constexpr std::int64_t kTinyMax = 64;
 constexpr int kTinyFloats = 8192;  // 32 KB of LDS per block
 
 constexpr int kTinyItems = 256;    // most items per block
 
-template <bool kTransB>
+template <bool kTransB, bool kQuad>
 __global__ __launch_bounds__(256) void gemm_f32_tiny_kernel(GemmArgs a, int P) {
-  __shared__ float lds[kTinyFloats];
+  __shared__ __attribute__((aligned(16))) float lds[kTinyFloats];
   __shared__ std::int64_t item_off[2][kTinyItems];  // each item's A and B offsets
   const int M = static_cast<int>(a.m), N = static_cast<int>(a.n), K = static_cast<int>(a.k);
   const int a_size = M * K, b_size = K * N, item_size = a_size + b_size;
@@ -1482,23 +1483,53 @@ __global__ __launch_bounds__(256) void gemm_f32_tiny_kernel(GemmArgs a, int P) {
   }
   __syncthreads();
   // Outputs in output order: this thread's (item, row, column) advances by
-  // the block size the same way.
-  const int outs = M * N;
-  const int op = T / outs, orem = T % outs, oi = orem / N, oj = orem % N;
+  // the block size the same way. kQuad: a thread computes four adjacent
+  // columns (N, M K and K N multiples of 4, so every staged row and output
+  // row is 16-byte aligned), one broadcast A read and one float4 B read per
+  // four multiply-adds, each output's k still in order.
+  constexpr int Q = kQuad ? 4 : 1;
+  const int NQ = N / Q;
+  const int outs = M * NQ;
+  const int op = T / outs, orem = T % outs, oi = orem / NQ, oj = orem % NQ;
   int p = static_cast<int>(threadIdx.x) / outs;
-  int i = (static_cast<int>(threadIdx.x) % outs) / N, j = static_cast<int>(threadIdx.x) % N;
+  int i = (static_cast<int>(threadIdx.x) % outs) / NQ, j = static_cast<int>(threadIdx.x) % NQ;
   for (int e = threadIdx.x; e < count * outs; e += T) {
     const float* A = lds + p * item_size + i * K;
-    const float* B = lds + p * item_size + a_size + j;
-    float acc = 0.F;
-    for (int k = 0; k < K; ++k) acc += A[k] * B[k * N];
-    if (a.bias != nullptr) acc = acc + a.bias[j];
-    a.out[(first + p) * outs + i * N + j] = activate(acc, a.activation);
+    float* o = a.out + (first + p) * static_cast<std::int64_t>(M) * N + i * N + j * Q;
+    if constexpr (kQuad) {
+      const float4_t* B = reinterpret_cast<const float4_t*>(lds + p * item_size + a_size) + j;
+      float4_t acc = {0.F, 0.F, 0.F, 0.F};
+      for (int k = 0; k < K; ++k) {
+        const float x = A[k];
+        const float4_t bv = B[k * NQ];
+        acc.x += x * bv.x;
+        acc.y += x * bv.y;
+        acc.z += x * bv.z;
+        acc.w += x * bv.w;
+      }
+      if (a.bias != nullptr) {
+        acc.x = acc.x + a.bias[4 * j];
+        acc.y = acc.y + a.bias[4 * j + 1];
+        acc.z = acc.z + a.bias[4 * j + 2];
+        acc.w = acc.w + a.bias[4 * j + 3];
+      }
+      acc.x = activate(acc.x, a.activation);
+      acc.y = activate(acc.y, a.activation);
+      acc.z = activate(acc.z, a.activation);
+      acc.w = activate(acc.w, a.activation);
+      *reinterpret_cast<float4_t*>(o) = acc;
+    } else {
+      const float* B = lds + p * item_size + a_size + j;
+      float acc = 0.F;
+      for (int k = 0; k < K; ++k) acc += A[k] * B[k * N];
+      if (a.bias != nullptr) acc = acc + a.bias[j];
+      *o = activate(acc, a.activation);
+    }
     p += op;
     i += oi;
     j += oj;
-    if (j >= N) {
-      j -= N;
+    if (j >= NQ) {
+      j -= NQ;
       ++i;
     }
     if (i >= M) {
@@ -1713,19 +1744,26 @@ inline int launch_tiny(GemmArgs& args, bool trans_b, hipStream_t stream) {
   const std::int64_t items = args.total_tiles;  // the caller passes the batch count
   // Items per block: as many as the LDS holds, at most enough for about 16
   // outputs per thread and at most kTinyItems, and at least one.
+  // Four columns per thread where rows stay 16-byte aligned and an item
+  // still has at least 64 such outputs (fewer left most threads idle: 10000
+  // items of 1 x 64 x 64 60 -> 69 us).
+  const bool quad = args.n % 4 == 0 && (args.m * args.k) % 4 == 0 && (args.k * args.n) % 4 == 0 &&
+                    (reinterpret_cast<std::uintptr_t>(args.out) & 15U) == 0 && args.m * args.n >= 256;
+  const std::int64_t per_item = quad ? args.m * args.n / 4 : args.m * args.n;  // thread outputs per item
   std::int64_t P = kTinyFloats / item;
-  const std::int64_t by_outputs = (16 * 256 + args.m * args.n - 1) / (args.m * args.n);
+  const std::int64_t by_outputs = (16 * 256 + per_item - 1) / per_item;
   if (P > by_outputs) P = by_outputs;
   if (P > kTinyItems) P = kTinyItems;
   if (P < 1) P = 1;
   const std::int64_t blocks = (items + P - 1) / P;
   if (blocks > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, args, static_cast<int>(P));
+  };
   if (trans_b)
-    hipLaunchKernelGGL((gemm_f32_tiny_kernel<true>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
-                       args, static_cast<int>(P));
+    quad ? launch(gemm_f32_tiny_kernel<true, true>) : launch(gemm_f32_tiny_kernel<true, false>);
   else
-    hipLaunchKernelGGL((gemm_f32_tiny_kernel<false>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
-                       args, static_cast<int>(P));
+    quad ? launch(gemm_f32_tiny_kernel<false, true>) : launch(gemm_f32_tiny_kernel<false, false>);
   return check(hipGetLastError(), "gemm_f32 tiny launch");
 }
 
