@@ -1744,17 +1744,24 @@ inline int launch_tiny(GemmArgs& args, bool trans_b, hipStream_t stream) {
   const std::int64_t items = args.total_tiles;  // the caller passes the batch count
   // Items per block: as many as the LDS holds, at most enough for about 16
   // outputs per thread and at most kTinyItems, and at least one.
-  // Four columns per thread where rows stay 16-byte aligned and an item
-  // still has at least 64 such outputs (fewer left most threads idle: 10000
-  // items of 1 x 64 x 64 60 -> 69 us).
-  const bool quad = args.n % 4 == 0 && (args.m * args.k) % 4 == 0 && (args.k * args.n) % 4 == 0 &&
-                    (reinterpret_cast<std::uintptr_t>(args.out) & 15U) == 0 && args.m * args.n >= 256;
-  const std::int64_t per_item = quad ? args.m * args.n / 4 : args.m * args.n;  // thread outputs per item
-  std::int64_t P = kTinyFloats / item;
-  const std::int64_t by_outputs = (16 * 256 + per_item - 1) / per_item;
-  if (P > by_outputs) P = by_outputs;
-  if (P > kTinyItems) P = kTinyItems;
-  if (P < 1) P = 1;
+  // Four columns per thread where rows stay 16-byte aligned and a block's
+  // items still give its 256 threads a four-column output each (fewer left
+  // most threads idle: 10000 items of 1 x 64 x 64, one item per block,
+  // 60 -> 69 us).
+  bool quad = args.n % 4 == 0 && (args.m * args.k) % 4 == 0 && (args.k * args.n) % 4 == 0 &&
+              (reinterpret_cast<std::uintptr_t>(args.out) & 15U) == 0;
+  auto items_per_block = [&](std::int64_t per_item) {  // thread outputs per item
+    std::int64_t P = kTinyFloats / item;
+    const std::int64_t by_outputs = (16 * 256 + per_item - 1) / per_item;
+    if (P > by_outputs) P = by_outputs;
+    if (P > kTinyItems) P = kTinyItems;
+    return P < 1 ? std::int64_t{1} : P;
+  };
+  std::int64_t P = items_per_block(args.m * args.n / 4);
+  if (!quad || P * (args.m * args.n / 4) < 256) {
+    quad = false;
+    P = items_per_block(args.m * args.n);
+  }
   const std::int64_t blocks = (items + P - 1) / P;
   if (blocks > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
   auto launch = [&](auto kernel) {
