@@ -178,7 +178,9 @@ int tcx_hip_gemm_f32(const float* lhs, const float* rhs, float* out,
 
 /* Workspace bytes that tcx_hip_gemm_f32_ws can use for desc: > 0 when the
  * shape has few output tiles and a long K, which then runs with K split over
- * several blocks whose partial sums land in the workspace; 0 otherwise. */
+ * several blocks whose partial sums land in the workspace, or when an
+ * unbatched product's K or N is not a multiple of 4 (zero-padded copies of
+ * A, B and the output, so that the 16-byte kernels run); 0 otherwise. */
 size_t tcx_hip_gemm_workspace_bytes(const tcx_hip_gemm_desc_t* desc);
 /* tcx_hip_gemm_f32 with that workspace (16-byte aligned). With NULL or fewer
  * bytes than the query it runs unsplit. Same results to the matmul bar (the

@@ -108,6 +108,68 @@ std::int64_t gemm_splits(const tcx_hip_gemm_desc_t* d, std::int64_t batches) {
   return 1;
 }
 
+// Unbatched products whose K or N is not a multiple of 4 cannot use 16-byte
+// rows and run the scalar-load kernels (1025^3: 62 us against 23 us for
+// 1024^3). With a workspace, large ones run zero-padded copies instead: A [M][K4],
+// B [K4][N4] (or [N4][K4]) and the output [M][N4] in the workspace, the
+// aligned routes on those, then the output stripped back to [M][N] with the
+// bias and activation applied as the kernels' epilogue applies them. The
+// padded k terms are 0 x 0. Only products of at least kPadMinWork
+// multiply-adds pay for the copies and three extra launches: measured on
+// MI355X, padded against scalar loads, 4096 x 4095 x 4096 1058 against 1276
+// us, 2048 x 2049 x 2048 249 / 267, 3000 x 3001 x 1000 241 / 253; around
+// 10^9 multiply-adds it lost (1000 x 1001 x 999 transposed 40 / 32 us).
+constexpr std::int64_t kPadMinWork = std::int64_t{1} << 32;
+constexpr std::int64_t kPadAlign = 64;  // floats: 256-byte aligned regions
+
+struct PadPlan {
+  bool pad;
+  std::int64_t k4, n4, a_floats, b_floats, c_floats;
+};
+
+PadPlan pad_plan(const tcx_hip_gemm_desc_t* d) {
+  PadPlan p{false, 0, 0, 0, 0, 0};
+  if (d->batch_rank != 0 || (d->k % 4 == 0 && d->n % 4 == 0) || d->m * d->n * d->k < kPadMinWork) return p;
+  auto up = [](std::int64_t v, std::int64_t q) { return (v + q - 1) / q * q; };
+  p.pad = true;
+  p.k4 = up(d->k, 4);
+  p.n4 = up(d->n, 4);
+  p.a_floats = up(d->m * p.k4, kPadAlign);
+  p.b_floats = up(p.k4 * p.n4, kPadAlign);
+  p.c_floats = up(d->m * p.n4, kPadAlign);
+  return p;
+}
+
+// out [rows_out][cols_out] = in [rows][cols] (row stride ld), zero past it.
+__global__ __launch_bounds__(256) void pad_copy_kernel(const float* __restrict__ in, float* __restrict__ out,
+                                                       std::int64_t rows, std::int64_t cols, std::int64_t ld,
+                                                       std::int64_t rows_out, std::int64_t cols_out) {
+  for (std::int64_t r = blockIdx.y; r < rows_out; r += gridDim.y)
+    for (std::int64_t c = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; c < cols_out;
+         c += static_cast<std::int64_t>(gridDim.x) * blockDim.x)
+      out[r * cols_out + c] = r < rows && c < cols ? in[r * ld + c] : 0.F;
+}
+
+// out [rows][cols] = act(in [rows][ld] + bias[col]): the kernels' epilogue
+// (bias added, then the activation) on the padded output.
+__global__ __launch_bounds__(256) void strip_kernel(const float* __restrict__ in, float* __restrict__ out,
+                                                    const float* __restrict__ bias, std::int64_t rows,
+                                                    std::int64_t cols, std::int64_t ld, int act) {
+  for (std::int64_t r = blockIdx.y; r < rows; r += gridDim.y)
+    for (std::int64_t c = static_cast<std::int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; c < cols;
+         c += static_cast<std::int64_t>(gridDim.x) * blockDim.x) {
+      float x = in[r * ld + c];
+      if (bias != nullptr) x = x + bias[c];
+      out[r * cols + c] = gemm::activate(x, act);
+    }
+}
+
+dim3 grid2d(std::int64_t rows, std::int64_t cols) {
+  const std::int64_t gx = (cols + 255) / 256 < 64 ? (cols + 255) / 256 : 64;
+  const std::int64_t gy = rows < 4096 ? rows : 4096;
+  return dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+}
+
 std::int64_t batch_product(const tcx_hip_gemm_desc_t* d) {
   std::int64_t batches = 1;
   for (int i = 0; i < d->batch_rank; ++i) batches *= d->batch_shape[i];
@@ -124,6 +186,8 @@ extern "C" size_t tcx_hip_gemm_workspace_bytes(const tcx_hip_gemm_desc_t* d) {
     return 0;
   const std::int64_t batches = batch_product(d);
   if (batches <= 0) return 0;
+  const PadPlan pad = pad_plan(d);
+  if (pad.pad) return static_cast<size_t>(pad.a_floats + pad.b_floats + pad.c_floats) * sizeof(float);
   const std::int64_t splits = gemm_splits(d, batches);
   if (splits == 1) return 0;
   return static_cast<size_t>(splits * batches * d->m * d->n) * sizeof(float);
@@ -148,6 +212,37 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
   for (int i = 0; i < d->batch_rank; ++i) batches *= d->batch_shape[i];
   if (batches != d->batch_count) return fail(TCX_INVALID_ARGUMENT, "gemm batch_count mismatch");
   if (d->m == 0 || d->n == 0 || batches == 0) return TCX_OK;
+  if (const PadPlan pad = pad_plan(d); pad.pad && d->k > 0 && lhs != nullptr && rhs != nullptr && out != nullptr &&
+      workspace != nullptr && aligned16(workspace) &&
+      workspace_bytes >= static_cast<size_t>(pad.a_floats + pad.b_floats + pad.c_floats) * sizeof(float)) {
+    const int status = ready();
+    if (status != TCX_OK) return status;
+    const auto s = static_cast<hipStream_t>(stream);
+    float* a4 = static_cast<float*>(workspace);
+    float* b4 = a4 + pad.a_floats;
+    float* c4 = b4 + pad.b_floats;
+    const bool trans = d->rhs_transposed != 0;
+    hipLaunchKernelGGL(pad_copy_kernel, grid2d(d->m, pad.k4), dim3(256), 0, s, lhs, a4, d->m, d->k, d->k, d->m,
+                       pad.k4);
+    if (trans)
+      hipLaunchKernelGGL(pad_copy_kernel, grid2d(pad.n4, pad.k4), dim3(256), 0, s, rhs, b4, d->n, d->k, d->k,
+                         pad.n4, pad.k4);
+    else
+      hipLaunchKernelGGL(pad_copy_kernel, grid2d(pad.k4, pad.n4), dim3(256), 0, s, rhs, b4, d->k, d->n, d->n,
+                         pad.k4, pad.n4);
+    int rc = check(hipGetLastError(), "gemm pad launch");
+    if (rc != TCX_OK) return rc;
+    tcx_hip_gemm_desc_t padded = *d;
+    padded.k = pad.k4;
+    padded.n = pad.n4;
+    padded.bias = nullptr;
+    padded.activation = TCX_ACT_NONE;
+    rc = tcx_hip_gemm_f32_ws(a4, b4, c4, &padded, nullptr, 0, stream);
+    if (rc != TCX_OK) return rc;
+    hipLaunchKernelGGL(strip_kernel, grid2d(d->m, d->n), dim3(256), 0, s, c4, out, d->bias, d->m, d->n, pad.n4,
+                       d->activation);
+    return check(hipGetLastError(), "gemm strip launch");
+  }
   if (lhs == nullptr && d->k != 0) return fail(TCX_INVALID_ARGUMENT, "gemm lhs is null");
   if (rhs == nullptr && d->k != 0) return fail(TCX_INVALID_ARGUMENT, "gemm rhs is null");
   if (out == nullptr) return fail(TCX_INVALID_ARGUMENT, "gemm output is null");

@@ -60,6 +60,13 @@ def test_library_exports_every_declared_symbol():
     (1024, 1024, 1024, (), False, 0),                     # splits would keep < 512 of K
     (512, 512, 16384, (), False, 16 * 512 * 512 * 4),     # 16 tiles: the 16-split cap
     (512, 512, 512, (), False, 0),
+    # K or N not a multiple of 4, at least 2^32 multiply-adds, unbatched:
+    # zero-padded copies of A [M][K4], B [K4][N4] and the output [M][N4],
+    # each rounded up to 64 floats.
+    (2048, 2049, 2048, (), False, (4194304 + 4202496 + 4202496) * 4),
+    (2048, 2049, 2048, (), True, (4194304 + 4202496 + 4202496) * 4),
+    (2048, 2049, 2048, (2,), False, 0),                   # batched: not padded
+    (1025, 1025, 1025, (), False, 0),                     # too small to pay
 ])
 def test_gemm_workspace_query(m, n, k, batch, trans, expect):
     if not capi.LIB_PATH.exists():

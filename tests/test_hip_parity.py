@@ -1205,3 +1205,29 @@ def test_matmul_tall_short_k_narrow_n(cx, m, n, k, trans):
         bias = rng.standard_normal(n).astype(np.float32)
         got = cx.linear(cx.tensor(a, device="hip"), cx.tensor(b, device="hip"), cx.tensor(bias, device="hip")).numpy()
         assert_matmul(got, a.astype(np.float64) @ b.T.astype(np.float64) + bias, a, b.T, f"tall linear {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k,trans", [(2048, 2049, 2048, False), (2049, 2051, 1027, True), (1025, 1025, 1025, False),
+                                         (1000, 1001, 999, True)])
+def test_matmul_padded_odd_shapes(cx, m, n, k, trans):
+    # Unbatched products whose K or N is not a multiple of 4 and of at least
+    # 2^32 multiply-adds run zero-padded copies through the 16-byte kernels
+    # when a workspace is brought (the backend brings it); the output is
+    # stripped with the bias and activation applied as the kernels' epilogue
+    # applies them. Smaller odd shapes keep the scalar-load kernels.
+    rng = np.random.default_rng(m + n + k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((n, k) if trans else (k, n)).astype(np.float32)
+    bt = b.T if trans else b
+    truth = a.astype(np.float64) @ bt.astype(np.float64)
+    got = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(np.ascontiguousarray(bt), device="hip")).numpy()
+    assert_matmul(got, truth, a, bt, f"padded {m}x{n}x{k}")
+    if trans:
+        bias = rng.standard_normal(n).astype(np.float32)
+        xa, wb, bb = cx.tensor(a, device="hip"), cx.tensor(b, device="hip"), cx.tensor(bias, device="hip")
+        pre = cx.linear(xa, wb, bb).numpy()
+        assert_matmul(pre, truth + bias, a, bt, f"padded linear {m}x{n}x{k}")
+        for act in ("silu", "gelu"):
+            # The same padded product, so the activation meets the same bits.
+            fused = cx.hip.linear_act(xa, wb, bb, act).numpy()
+            assert_close(fused, getattr(oracle, act)(pre), 1e-6, 1e-6, f"padded {act} {m}x{n}x{k}")
