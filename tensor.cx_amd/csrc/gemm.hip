@@ -188,6 +188,13 @@ extern "C" size_t tcx_hip_gemm_workspace_bytes(const tcx_hip_gemm_desc_t* d) {
   if (batches <= 0) return 0;
   const PadPlan pad = pad_plan(d);
   if (pad.pad) return static_cast<size_t>(pad.a_floats + pad.b_floats + pad.c_floats) * sizeof(float);
+  bool rhs_strides_vec = true;
+  for (int i = 0; i < d->batch_rank; ++i) rhs_strides_vec = rhs_strides_vec && d->rhs_batch_strides[i] % 4 == 0;
+  if (d->m == 1 && d->rhs_transposed == 0 && d->n >= 512 && d->n % 4 == 0 && rhs_strides_vec &&
+      batches * ((d->n / 4 + 255) / 256) < kVecMatMinBlocks) {
+    const std::int64_t splits = gemm::vecmat_splits(batches, d->n, d->k);
+    return splits > 1 ? static_cast<size_t>(splits * batches * d->n) * sizeof(float) : 0;
+  }
   const std::int64_t splits = gemm_splits(d, batches);
   if (splits == 1) return 0;
   return static_cast<size_t>(splits * batches * d->m * d->n) * sizeof(float);
@@ -304,8 +311,17 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
   bool rhs_strides_vec = true;  // A's row is read a word at a time: only B's rows need 16 bytes
   for (int i = 0; i < d->batch_rank; ++i) rhs_strides_vec = rhs_strides_vec && d->rhs_batch_strides[i] % 4 == 0;
   if (d->m == 1 && !trans_b && d->n >= 512 && d->n % 4 == 0 && aligned16(rhs) && aligned16(out) &&
-      rhs_strides_vec && batches * ((d->n / 4 + 255) / 256) >= kVecMatMinBlocks)
-    return gemm::launch_vecmat(args, s);
+      rhs_strides_vec) {
+    if (batches * ((d->n / 4 + 255) / 256) >= kVecMatMinBlocks) return gemm::launch_vecmat(args, s);
+    // Fewer blocks: K split over blocks, partials in the caller's workspace.
+    const std::int64_t splits = gemm::vecmat_splits(batches, d->n, d->k);
+    const size_t need = static_cast<size_t>(splits * batches * d->n) * sizeof(float);
+    if (splits > 1 && workspace != nullptr && aligned16(workspace) && workspace_bytes >= need) {
+      args.splits = static_cast<std::int32_t>(splits);
+      args.partial = static_cast<float*>(workspace);
+      return gemm::launch_vecmat(args, s);
+    }
+  }
   // A short K (unbatched, row-major B): the output streamed as float4 from B
   // columns held in registers. Against the tiled kernels: 4096 x 4096 x 4
   // 26.5 -> 15.2 us, x 8 26.5 -> 17.0, x 16 26.6 -> 23.8, 1000000 x 16 x 16

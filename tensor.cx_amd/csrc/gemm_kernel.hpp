@@ -1670,8 +1670,16 @@ __global__ __launch_bounds__(1024) void gemm_f32_vecmat_kernel(GemmArgs a) {
     }
     const float* x = a.lhs + lo;
     const float4_t* B = reinterpret_cast<const float4_t*>(a.rhs + ro);
-    const std::int64_t kq = (K + kVecMatGroups - 1) / kVecMatGroups;
-    const std::int64_t k0 = group * kq, k1 = k0 + kq < K ? k0 + kq : K;
+    // This block's k range: all of K, or split blockIdx.z of a.splits.
+    std::int64_t ks0 = 0, ks1 = K;
+    if (a.splits > 1) {
+      const std::int64_t per = (K + a.splits - 1) / a.splits;
+      ks0 = blockIdx.z * per < K ? blockIdx.z * per : K;
+      ks1 = ks0 + per < K ? ks0 + per : K;
+    }
+    const std::int64_t kq = (ks1 - ks0 + kVecMatGroups - 1) / kVecMatGroups;
+    const std::int64_t k0 = ks0 + group * kq < ks1 ? ks0 + group * kq : ks1;
+    const std::int64_t k1 = k0 + kq < ks1 ? k0 + kq : ks1;
     const std::int64_t cl = c < CQ ? c : CQ - 1;  // lanes past the last column read a valid one
     float4_t acc = {0.F, 0.F, 0.F, 0.F};
     std::int64_t k = k0;
@@ -1707,29 +1715,52 @@ __global__ __launch_bounds__(1024) void gemm_f32_vecmat_kernel(GemmArgs a) {
         acc.z += p.z;
         acc.w += p.w;
       }
-      if (a.bias != nullptr) {
-        acc.x = acc.x + a.bias[4 * c];
-        acc.y = acc.y + a.bias[4 * c + 1];
-        acc.z = acc.z + a.bias[4 * c + 2];
-        acc.w = acc.w + a.bias[4 * c + 3];
+      if (a.splits > 1) {  // a partial sum: split_reduce_kernel adds the splits in order
+        reinterpret_cast<float4_t*>(a.partial + (blockIdx.z * a.total_tiles + item) * N)[c] = acc;
+      } else {
+        if (a.bias != nullptr) {
+          acc.x = acc.x + a.bias[4 * c];
+          acc.y = acc.y + a.bias[4 * c + 1];
+          acc.z = acc.z + a.bias[4 * c + 2];
+          acc.w = acc.w + a.bias[4 * c + 3];
+        }
+        acc.x = activate(acc.x, a.activation);
+        acc.y = activate(acc.y, a.activation);
+        acc.z = activate(acc.z, a.activation);
+        acc.w = activate(acc.w, a.activation);
+        reinterpret_cast<float4_t*>(a.out + item * N)[c] = acc;
       }
-      acc.x = activate(acc.x, a.activation);
-      acc.y = activate(acc.y, a.activation);
-      acc.z = activate(acc.z, a.activation);
-      acc.w = activate(acc.w, a.activation);
-      reinterpret_cast<float4_t*>(a.out + item * N)[c] = acc;
     }
     __syncthreads();  // part is rewritten by the next item
   }
+}
+
+// K splits of the vector-matrix kernel for items x 1024-column chunks too
+// few to fill the GPU: the smallest power of two giving >= 256 blocks, each
+// split keeping >= 128 rows of B, at most 128. Measured against 512 blocks
+// of >= 64 rows and 1024 of >= 32: 1 x 4096 x 4096 22.5 / 27.4 / 42.3 us,
+// 1 x 8192 x 8192 48.6 / 70.2 / 68.3 us (more splits only add partials).
+inline std::int64_t vecmat_splits(std::int64_t items, std::int64_t n, std::int64_t k) {
+  const std::int64_t blocks = items * ((n / 4 + 255) / 256);
+  std::int64_t splits = 1;
+  while (blocks * splits < 256 && splits < 128 && k / (2 * splits) >= 128) splits *= 2;
+  return splits;
 }
 
 inline int launch_vecmat(GemmArgs& args, hipStream_t stream) {
   if (args.m != 1 || args.n % 4 != 0 || args.k < 1) return fail(TCX_INTERNAL, "vector-matrix gemm needs M == 1");
   const std::int64_t chunks = (args.n / 4 + 255) / 256;
   const std::int64_t items = args.total_tiles;  // the caller passes the batch count
-  const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(items < 65535 ? items : 65535));
+  const int splits = args.splits > 1 ? args.splits : 1;
+  const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(items < 65535 ? items : 65535),
+                  static_cast<unsigned>(splits));
   hipLaunchKernelGGL(gemm_f32_vecmat_kernel, grid, dim3(256 * kVecMatGroups), 0, stream, args);
-  return check(hipGetLastError(), "gemm_f32 vector-matrix launch");
+  int rc = check(hipGetLastError(), "gemm_f32 vector-matrix launch");
+  if (rc != TCX_OK || splits == 1) return rc;
+  const std::int64_t count4 = items * args.n / 4;
+  hipLaunchKernelGGL(split_reduce_kernel, dim3(grid_for(count4, 256, 256 * 16)), dim3(256), 0, stream, args.partial,
+                     args.out, args.bias, count4, args.n, splits, args.activation);
+  return check(hipGetLastError(), "gemm_f32 vector-matrix split reduce launch");
 }
 
 inline bool tiny_fits(std::int64_t m, std::int64_t n, std::int64_t k) {

@@ -67,6 +67,10 @@ def test_library_exports_every_declared_symbol():
     (2048, 2049, 2048, (), True, (4194304 + 4202496 + 4202496) * 4),
     (2048, 2049, 2048, (2,), False, 0),                   # batched: not padded
     (1025, 1025, 1025, (), False, 0),                     # too small to pay
+    # One row against a row-major B with too few 1024-column blocks: K split
+    # (4 blocks x 32 splits of 128 rows), partials [splits][N].
+    (1, 4096, 4096, (), False, 32 * 4096 * 4),
+    (1, 4096, 4096, (), True, 0),                         # the GEMV route
 ])
 def test_gemm_workspace_query(m, n, k, batch, trans, expect):
     if not capi.LIB_PATH.exists():

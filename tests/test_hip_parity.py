@@ -1175,10 +1175,13 @@ def test_matmul_small_k(cx, m, n, k, trans):
                       f"small-k linear {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("batch,n,k", [(200, 2048, 1024), (128, 1028, 333), (300, 516, 7)])
+@pytest.mark.parametrize("batch,n,k", [(200, 2048, 1024), (128, 1028, 333), (300, 516, 7), (1, 4096, 4096),
+                                       (4, 2052, 3001)])
 def test_matmul_batched_vector_matrix(cx, batch, n, k):
     # One row of A against a row-major B per batch item: 1024-column blocks,
-    # K in four in-block groups added in order; at the matmul bar.
+    # K in four in-block groups added in order, and with too few blocks K
+    # split over blocks (partials in the workspace the backend brings, added
+    # in split order); at the matmul bar.
     rng = np.random.default_rng(batch + n + k)
     a = rng.standard_normal((batch, 1, k)).astype(np.float32)
     b = rng.standard_normal((batch, k, n)).astype(np.float32)
