@@ -225,3 +225,39 @@ def test_short_rows_exact_order(cx, width):
     hi = cx.tensor(xi, device="hip")
     for op in ("sum", "max", "min", "argmax"):
         assert_bits(getattr(cx, op)(hi, 1).numpy(), getattr(oracle, op)(xi, 1), f"i32 {op} width {width}")
+
+
+@pytest.mark.parametrize("width", [65, 66, 67, 1021, 4099, 8191, 40001])
+def test_unaligned_rows_head_body_tail(cx, width):
+    # Rows whose length is not a multiple of 4 start at every 4-byte offset:
+    # each wave segment splits into a head (to the next 16-byte boundary), a
+    # float4 body and a tail. Ties, NaNs and signed zeros sit in the heads
+    # and tails, where the fold must keep the lowest index.
+    rows = 9
+    rng = np.random.default_rng(width)
+    x = rng.integers(-3, 4, (rows, width)).astype(np.float32)
+    flat = x.reshape(-1)
+    for r in range(rows):
+        x[r, 0] = 9.0                        # head ties the body's later 9
+        x[r, width // 2] = 9.0
+        x[r, width - 1] = -9.0               # tail ties an earlier -9
+        x[r, 1] = -9.0
+    x[3, width - 2] = np.nan                 # NaN in a tail
+    x[4, 0] = np.nan                         # NaN in a head
+    x[4, width - 1] = np.nan
+    x[5, :] = -0.0
+    x[5, width - 1] = 0.0
+    h = cx.tensor(x, device="hip")
+    for op in ("max", "min", "argmax"):
+        assert_bits(getattr(cx, op)(h, 1).numpy(), getattr(oracle, op)(x, 1), f"{op} width {width}")
+    y = rng.standard_normal((rows, width)).astype(np.float32)
+    hy = cx.tensor(y, device="hip")
+    for op in ("sum", "mean"):
+        actual, expected = getattr(cx, op)(hy, 1).numpy(), getattr(oracle, op)(y, 1)
+        scale = np.float64(width if op == "mean" else 1)
+        assert sum_error(actual * scale, expected * scale, y, rows, width, 1) <= SUM_BAR, f"{op} {width}"
+    yi = rng.integers(-2**31, 2**31 - 1, (rows, width), dtype=np.int64).astype(np.int32)
+    hi = cx.tensor(yi, device="hip")
+    for op in ("sum", "max", "min", "argmax"):
+        assert_bits(getattr(cx, op)(hi, 1).numpy(), getattr(oracle, op)(yi, 1), f"i32 {op} width {width}")
+    assert_bits(cx.sum(hi).numpy(), oracle.sum(yi, None), f"i32 full sum {width}")
