@@ -227,12 +227,14 @@ def test_short_rows_exact_order(cx, width):
         assert_bits(getattr(cx, op)(hi, 1).numpy(), getattr(oracle, op)(xi, 1), f"i32 {op} width {width}")
 
 
-@pytest.mark.parametrize("width", [65, 66, 67, 1021, 4099, 8191, 40001])
+@pytest.mark.parametrize("width", [65, 66, 67, 128, 130, 255, 257, 511, 512, 513, 1021, 1027, 4099, 8191, 40001])
 def test_unaligned_rows_head_body_tail(cx, width):
     # Rows whose length is not a multiple of 4 start at every 4-byte offset:
     # each wave segment splits into a head (to the next 16-byte boundary), a
     # float4 body and a tail. Ties, NaNs and signed zeros sit in the heads
-    # and tails, where the fold must keep the lowest index.
+    # and tails, where the fold must keep the lowest index. Rows of up to 512
+    # elements are packed 16, 32 or 64 lanes per row, 9 rows leaving a wave
+    # partly filled.
     rows = 9
     rng = np.random.default_rng(width)
     x = rng.integers(-3, 4, (rows, width)).astype(np.float32)
