@@ -871,13 +871,14 @@ def test_empty_and_scalar(cx):
 
 # ------------------------------------------------------------- row ops
 # Widths cover each row kernel: one wave per row (<= 1024), one block per row
-# with the row in registers (aligned up to 16384 floats, full and masked;
-# unaligned up to 4096), the re-reading block kernel, and strided rows.
+# with the row in registers (up to 16384 floats: aligned full and masked, and
+# unaligned at 2, 4, 8 and 16 elements per thread per 1024), the re-reading
+# block kernel, and strided rows.
 @pytest.mark.parametrize("shape,axis", [((16, 4096), 1), ((5, 300), 1), ((7, 8192), 1), ((3, 20000), -1),
                                         ((3, 7), 0), ((2, 3, 70), 1), ((9, 1), 1), ((4, 1022), 1),
                                         ((4, 1024), 1), ((6, 1501), 1), ((4, 2048), 1), ((3, 3001), 1),
                                         ((5, 4100), 1), ((2, 12288), 1), ((3, 16384), 1), ((2, 16383), 1),
-                                        ((1000, 1028), 1)])
+                                        ((1000, 1028), 1), ((3, 5001), 1), ((2, 9999), 1)])
 def test_row_ops_random(cx, shape, axis):
     rng = np.random.default_rng(13)
     x = (rng.standard_normal(shape) * 3).astype(np.float32)
@@ -895,7 +896,7 @@ def test_row_ops_random(cx, shape, axis):
                  oracle.affine_norm(x, axis, 1e-5, g, None, rms=True), 1e-5, 1e-5, "affine rmsnorm")
 
 
-@pytest.mark.parametrize("width", [200, 500, 1024, 2048, 3001, 4096, 8192, 16384, 20003, 70000])
+@pytest.mark.parametrize("width", [200, 500, 1024, 2048, 3001, 4096, 8191, 8192, 16383, 16384, 20003, 70000])
 def test_row_ops_special_values_wide_rows(cx, width):
     # Non-finite values in rows of every width class (one-wave cached rows,
     # split rows at 2, 4, 8 and 16 float4 per thread, unaligned scalar rows,
