@@ -550,7 +550,7 @@ __global__ __launch_bounds__(256) void row_split_kernel(RowArgs a) {
   }
 }
 
-// Rows too long for registers: one block per row, three passes over the row.
+// Block-wide maximum (NaN first) or sum of one value per thread.
 __device__ float block_reduce(float v, bool is_max, float* scratch) {
   v = is_max ? wave_max_nan(v) : wave_sum(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -565,6 +565,44 @@ __device__ float block_reduce(float v, bool is_max, float* scratch) {
   return r;
 }
 
+// Walks row x[0, n) with the 256 threads of a block: the elements before
+// x's first 16-byte boundary (threads 0-2, f1(value, i)), whole float4s four
+// deep per thread (f4(vector, i) for elements i .. i + 3, all four loads of
+// a round issued before any is used), then the last elements (threads 0-2).
+// Scalar loads one per iteration ran [1000, 100003] softmax at 14 % of HBM.
+template <typename F4, typename F1>
+__device__ __forceinline__ void block_row_walk(const float* __restrict__ x, std::int64_t n, F4&& f4, F1&& f1) {
+  const int t = threadIdx.x;
+  std::int64_t head = static_cast<std::int64_t>(((16U - (reinterpret_cast<std::uintptr_t>(x) & 15U)) & 15U) / 4);
+  if (head > n) head = n;
+  const std::int64_t vectors = (n - head) / 4;
+  const float4_t* __restrict__ body = reinterpret_cast<const float4_t*>(x + head);
+  std::int64_t k = t;
+  for (; k + 768 < vectors; k += 1024) {
+    const float4_t a = stream_load(body + k), b = stream_load(body + k + 256), c = stream_load(body + k + 512),
+                   d = stream_load(body + k + 768);
+    f4(a, head + 4 * k);
+    f4(b, head + 4 * (k + 256));
+    f4(c, head + 4 * (k + 512));
+    f4(d, head + 4 * (k + 768));
+  }
+  float4_t last[3];
+#pragma unroll
+  for (int u = 0; u < 3; ++u)
+    if (k + 256 * u < vectors) last[u] = stream_load(body + k + 256 * u);
+#pragma unroll
+  for (int u = 0; u < 3; ++u)
+    if (k + 256 * u < vectors) f4(last[u], head + 4 * (k + 256 * u));
+  if (t < head) f1(x[t], static_cast<std::int64_t>(t));
+  const std::int64_t tail = head + 4 * vectors;
+  if (t < n - tail) f1(x[tail + t], tail + t);
+}
+
+// Rows too long for registers: one block per row, passes over the row
+// through block_row_walk (softmax: running maximum and sum, write;
+// RMSNorm: sum of squares, write; LayerNorm: sum, squared deviations,
+// write). Outputs go out as float4 when out and x share their offset within
+// 16 bytes, else element by element.
 template <RowOp kOp>
 __global__ __launch_bounds__(256) void row_block_kernel(RowArgs a) {
   __shared__ float scratch[4];
@@ -573,69 +611,129 @@ __global__ __launch_bounds__(256) void row_block_kernel(RowArgs a) {
   const std::int64_t n = a.n;
   const float* __restrict__ x = a.x + row * n;
   float* __restrict__ out = a.out + row * n;
-  const int t = threadIdx.x;
+  const bool vec_out = ((reinterpret_cast<std::uintptr_t>(out) - reinterpret_cast<std::uintptr_t>(x)) & 15U) == 0;
+  // Writes f(value, i) for every element of the row.
+  auto write_row = [&](auto&& f) {
+    block_row_walk(
+        x, n,
+        [&](const float4_t& v, std::int64_t i) {
+          const float4_t r = {f(v.x, i), f(v.y, i + 1), f(v.z, i + 2), f(v.w, i + 3)};
+          if (vec_out) {
+            *reinterpret_cast<float4_t*>(out + i) = r;
+          } else {
+            out[i] = r.x; out[i + 1] = r.y; out[i + 2] = r.z; out[i + 3] = r.w;
+          }
+        },
+        [&](float v, std::int64_t i) { out[i] = f(v, i); });
+  };
   if constexpr (kOp == RowOp::kSoftmax) {
-    float m = -__builtin_inff();
-    for (std::int64_t i = t; i < n; i += 256) {
-      const float e = x[i];
-      if (is_nan(e) || e > m) m = e;
+    // One read pass for the maximum and the sum: each thread keeps (m, s),
+    // s relative to its running maximum m and rescaled when m grows (a sum
+    // begun under m = -inf starts over). A separate maximum pass read every
+    // row three times: [1000, 100000] 284 us at 35 % of HBM.
+    float m = -__builtin_inff(), s = 0.F;
+    auto grow = [&](float top) {
+      if ((is_nan(top) && !is_nan(m)) || top > m) {
+        s = m == -__builtin_inff() ? 0.F : s * exp_softmax(m - top);
+        m = top;
+      }
+    };
+    auto nan_max = [](float p, float q) { return (is_nan(q) || q > p) ? q : p; };
+    block_row_walk(
+        x, n,
+        [&](const float4_t& v, std::int64_t) {
+          grow(nan_max(nan_max(v.x, v.y), nan_max(v.z, v.w)));
+          s += (exp_softmax(v.x - m) + exp_softmax(v.y - m)) + (exp_softmax(v.z - m) + exp_softmax(v.w - m));
+        },
+        [&](float v, std::int64_t) {
+          grow(v);
+          s += exp_softmax(v - m);
+        });
+    // Merge (m, s) over the wave, then the block's four waves in order.
+    auto merge = [&](float om, float os) {
+      const float top = nan_max(m, om);
+      if (top == -__builtin_inff()) {
+        s = s + os;
+      } else {
+        const float mine = m == -__builtin_inff() ? 0.F : s * exp_softmax(m - top);
+        const float other = om == -__builtin_inff() ? 0.F : os * exp_softmax(om - top);
+        s = mine + other;
+      }
+      m = top;
+    };
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) merge(__shfl_xor(m, offset, kWave), __shfl_xor(s, offset, kWave));
+    __shared__ float wave_ms[2][4];
+    if ((threadIdx.x & 63) == 0) {
+      wave_ms[0][threadIdx.x >> 6] = m;
+      wave_ms[1][threadIdx.x >> 6] = s;
     }
-    m = block_reduce(m, true, scratch);
-    float s = 0.F;
-    for (std::int64_t i = t; i < n; i += 256) s += expf(x[i] - m);
-    const float denom = block_reduce(s, false, scratch);
-    for (std::int64_t i = t; i < n; i += 256) out[i] = expf(x[i] - m) / denom;
+    __syncthreads();
+    m = wave_ms[0][0];
+    s = wave_ms[1][0];
+    for (int w = 1; w < 4; ++w) merge(wave_ms[0][w], wave_ms[1][w]);
+    // One correctly rounded reciprocal per row; each output is e * (1/denom),
+    // within 1.5 ulp of the reference's e / denom.
+    const float inv = 1.0F / s;
+    write_row([&](float v, std::int64_t) { return exp_softmax(v - m) * inv; });
   } else if constexpr (kOp == RowOp::kRms) {
-    float s = 0.F;
-    for (std::int64_t i = t; i < n; i += 256) {
-      const float e = x[i];
-      const float sq = e * e;
-      s += sq;
-    }
-    const float ss = block_reduce(s, false, scratch);
+    float s0 = 0.F, s1 = 0.F;
+    block_row_walk(
+        x, n, [&](const float4_t& v, std::int64_t) { s0 += v.x * v.x + v.y * v.y; s1 += v.z * v.z + v.w * v.w; },
+        [&](float v, std::int64_t) { s0 += v * v; });
+    const float ss = block_reduce(s0 + s1, false, scratch);
     const float scale = 1.0F / sqrtf(ss / static_cast<float>(n) + a.eps);
-    for (std::int64_t i = t; i < n; i += 256) {
-      float r = x[i] * scale;
-      if (a.gamma) r = r * a.gamma[i];
-      out[i] = r;
-    }
-    return;
+    const float* __restrict__ g = a.gamma;
+    write_row([&](float v, std::int64_t i) {
+      const float r = v * scale;
+      return g ? r * g[i] : r;
+    });
   } else {
-    if (t == 0) eq_flag = 1;
+    if (threadIdx.x == 0) eq_flag = 1;
     const float first = x[0];
-    float s = 0.F;
+    float s0 = 0.F, s1 = 0.F;
     bool equal = true;
-    for (std::int64_t i = t; i < n; i += 256) {
-      s += x[i];
-      equal = equal && x[i] == first;
-    }
-    const float mean = block_reduce(s, false, scratch) / static_cast<float>(n);
+    block_row_walk(
+        x, n,
+        [&](const float4_t& v, std::int64_t) {
+          s0 += v.x + v.y;
+          s1 += v.z + v.w;
+          equal = equal && v.x == first && v.y == first && v.z == first && v.w == first;
+        },
+        [&](float v, std::int64_t) {
+          s0 += v;
+          equal = equal && v == first;
+        });
+    const float mean = block_reduce(s0 + s1, false, scratch) / static_cast<float>(n);
     if (!equal) eq_flag = 0;
     __syncthreads();
+    const float* __restrict__ g = a.gamma;
+    const float* __restrict__ b = a.beta;
+    auto affine = [&](float r, std::int64_t i) {
+      if (g) r = r * g[i];
+      if (b) r = r + b[i];
+      return r;
+    };
     if (eq_flag && __builtin_isfinite(first)) {
       const float fillv = a.eps == 0.F ? __builtin_nanf("") : 0.F;
-      for (std::int64_t i = t; i < n; i += 256) {
-        float r = fillv;
-        if (a.gamma) r = r * a.gamma[i];
-        if (a.beta) r = r + a.beta[i];
-        out[i] = r;
-      }
+      write_row([&](float, std::int64_t i) { return affine(fillv, i); });
       return;
     }
-    float d2 = 0.F;
-    for (std::int64_t i = t; i < n; i += 256) {
-      const float d = x[i] - mean;
-      d2 += d * d;
-    }
+    float d0 = 0.F, d1 = 0.F;
+    block_row_walk(
+        x, n,
+        [&](const float4_t& v, std::int64_t) {
+          const float dx = v.x - mean, dy = v.y - mean, dz = v.z - mean, dw = v.w - mean;
+          d0 += dx * dx + dy * dy;
+          d1 += dz * dz + dw * dw;
+        },
+        [&](float v, std::int64_t) {
+          const float d = v - mean;
+          d0 += d * d;
+        });
     bool nan_row = false;
-    const float scale = finish_scale_ln(block_reduce(d2, false, scratch), n, a.eps, nan_row);
-    for (std::int64_t i = t; i < n; i += 256) {
-      float r = nan_row ? __builtin_nanf("") : (x[i] - mean) * scale;
-      if (a.gamma) r = r * a.gamma[i];
-      if (a.beta) r = r + a.beta[i];
-      out[i] = r;
-    }
-    return;
+    const float scale = finish_scale_ln(block_reduce(d0 + d1, false, scratch), n, a.eps, nan_row);
+    write_row([&](float v, std::int64_t i) { return affine(nan_row ? __builtin_nanf("") : (v - mean) * scale, i); });
   }
 }
 
