@@ -565,7 +565,11 @@ __device__ float block_reduce(float v, bool is_max, float* scratch) {
   return r;
 }
 
-// Walks row x[0, n) with the 256 threads of a block: the elements before
+// Threads of the long-row block: 1024 keep four times the loads of 256 in
+// flight per row, which matters when a few hundred rows fill the GPU.
+constexpr int kRowBlockThreads = 1024;
+
+// Walks row x[0, n) with the kRowBlockThreads threads of a block: the elements before
 // x's first 16-byte boundary (threads 0-2, f1(value, i)), whole float4s four
 // deep per thread (f4(vector, i) for elements i .. i + 3, all four loads of
 // a round issued before any is used), then the last elements (threads 0-2).
@@ -578,21 +582,22 @@ __device__ __forceinline__ void block_row_walk(const float* __restrict__ x, std:
   const std::int64_t vectors = (n - head) / 4;
   const float4_t* __restrict__ body = reinterpret_cast<const float4_t*>(x + head);
   std::int64_t k = t;
-  for (; k + 768 < vectors; k += 1024) {
-    const float4_t a = stream_load(body + k), b = stream_load(body + k + 256), c = stream_load(body + k + 512),
-                   d = stream_load(body + k + 768);
+  constexpr int T = kRowBlockThreads;
+  for (; k + 3 * T < vectors; k += 4 * T) {
+    const float4_t a = stream_load(body + k), b = stream_load(body + k + T), c = stream_load(body + k + 2 * T),
+                   d = stream_load(body + k + 3 * T);
     f4(a, head + 4 * k);
-    f4(b, head + 4 * (k + 256));
-    f4(c, head + 4 * (k + 512));
-    f4(d, head + 4 * (k + 768));
+    f4(b, head + 4 * (k + T));
+    f4(c, head + 4 * (k + 2 * T));
+    f4(d, head + 4 * (k + 3 * T));
   }
   float4_t last[3];
 #pragma unroll
   for (int u = 0; u < 3; ++u)
-    if (k + 256 * u < vectors) last[u] = stream_load(body + k + 256 * u);
+    if (k + T * u < vectors) last[u] = stream_load(body + k + T * u);
 #pragma unroll
   for (int u = 0; u < 3; ++u)
-    if (k + 256 * u < vectors) f4(last[u], head + 4 * (k + 256 * u));
+    if (k + T * u < vectors) f4(last[u], head + 4 * (k + T * u));
   if (t < head) f1(x[t], static_cast<std::int64_t>(t));
   const std::int64_t tail = head + 4 * vectors;
   if (t < n - tail) f1(x[tail + t], tail + t);
@@ -604,8 +609,9 @@ __device__ __forceinline__ void block_row_walk(const float* __restrict__ x, std:
 // write). Outputs go out as float4 when out and x share their offset within
 // 16 bytes, else element by element.
 template <RowOp kOp>
-__global__ __launch_bounds__(256) void row_block_kernel(RowArgs a) {
-  __shared__ float scratch[4];
+__global__ __launch_bounds__(kRowBlockThreads) void row_block_kernel(RowArgs a) {
+  constexpr int kWaves = kRowBlockThreads / 64;
+  __shared__ float scratch[kWaves];
   __shared__ int eq_flag;
   const std::int64_t row = blockIdx.x;
   const std::int64_t n = a.n;
@@ -649,7 +655,7 @@ __global__ __launch_bounds__(256) void row_block_kernel(RowArgs a) {
           grow(v);
           s += exp_softmax(v - m);
         });
-    // Merge (m, s) over the wave, then the block's four waves in order.
+    // Merge (m, s) over the wave, then the block's waves in order.
     auto merge = [&](float om, float os) {
       const float top = nan_max(m, om);
       if (top == -__builtin_inff()) {
@@ -663,7 +669,7 @@ __global__ __launch_bounds__(256) void row_block_kernel(RowArgs a) {
     };
 #pragma unroll
     for (int offset = 32; offset > 0; offset >>= 1) merge(__shfl_xor(m, offset, kWave), __shfl_xor(s, offset, kWave));
-    __shared__ float wave_ms[2][4];
+    __shared__ float wave_ms[2][kWaves];
     if ((threadIdx.x & 63) == 0) {
       wave_ms[0][threadIdx.x >> 6] = m;
       wave_ms[1][threadIdx.x >> 6] = s;
@@ -671,7 +677,7 @@ __global__ __launch_bounds__(256) void row_block_kernel(RowArgs a) {
     __syncthreads();
     m = wave_ms[0][0];
     s = wave_ms[1][0];
-    for (int w = 1; w < 4; ++w) merge(wave_ms[0][w], wave_ms[1][w]);
+    for (int w = 1; w < kWaves; ++w) merge(wave_ms[0][w], wave_ms[1][w]);
     // One correctly rounded reciprocal per row; each output is e * (1/denom),
     // within 1.5 ulp of the reference's e / denom.
     const float inv = 1.0F / s;
@@ -1321,7 +1327,8 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
     // Rows wider than the register budget (1024 x kMaxSplit floats): one
     // block per row, re-read passes.
     if (outer > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "too many rows");
-    hipLaunchKernelGGL((row_block_kernel<kOp>), dim3(static_cast<unsigned>(outer)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((row_block_kernel<kOp>), dim3(static_cast<unsigned>(outer)), dim3(kRowBlockThreads), 0, s,
+                       a);
     return check(hipGetLastError(), "row block kernel launch");
   }
   return check(hipGetLastError(), "row kernel launch");
