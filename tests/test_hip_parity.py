@@ -896,11 +896,13 @@ def test_row_ops_random(cx, shape, axis):
                  oracle.affine_norm(x, axis, 1e-5, g, None, rms=True), 1e-5, 1e-5, "affine rmsnorm")
 
 
-@pytest.mark.parametrize("width", [200, 500, 1024, 2048, 3001, 4096, 8191, 8192, 16383, 16384, 20003, 70000])
+@pytest.mark.parametrize("width", [200, 500, 1024, 2048, 3001, 4096, 8191, 8192, 16383, 16384, 20003, 40001,
+                                   40961, 70000])
 def test_row_ops_special_values_wide_rows(cx, width):
     # Non-finite values in rows of every width class (one-wave cached rows,
     # split rows at 2, 4, 8 and 16 float4 per thread, unaligned scalar rows,
-    # block-per-row re-read rows): a NaN, +inf last, -inf first, a row of
+    # block-per-row rows staged in LDS (up to about 40700 floats on a 160 KB
+    # LDS) and re-read beyond): a NaN, +inf last, -inf first, a row of
     # -inf, +inf with -inf, and a row whose squares overflow to inf.
     rng = np.random.default_rng(23)
     x = rng.standard_normal((7, width)).astype(np.float32)
