@@ -1013,26 +1013,35 @@ __global__ __launch_bounds__(256) void packed_row_kernel(const T* __restrict__ x
         r.bits = s;
       }
     } else {
+      // One 64-bit key per element: its rank key above the complemented row
+      // index, so the largest key is the extreme value and, among equal
+      // ranks (ties, +0 and -0, every NaN), the lowest index. Real keys are
+      // nonzero (the low word alone is), 0 marks no element. The winner's
+      // own bits (a NaN's payload, a zero's sign) come from the lane that
+      // holds it. Against (value, index) butterflies under cand_better:
+      // [100000, 130] max 26.5 -> 16.7 us on MI355X.
+      std::uint64_t key = 0;
       T best{};
-      int bi = -1;
 #pragma unroll
       for (int u = 0; u < kPackedLoads; ++u) {
         const int j = l + u * kL;
-        if (live && j < R && (bi < 0 || lane_takes<T, kLargest>(v[u], best))) {
-          best = v[u];
-          bi = j;
+        if (live && j < R) {
+          const std::uint64_t k = (static_cast<std::uint64_t>(rank_key<T, kLargest>(to_bits(v[u]))) << 32) |
+                                  (0xFFFFFFFFU - static_cast<std::uint32_t>(j));
+          if (k > key) {
+            key = k;
+            best = v[u];
+          }
         }
       }
 #pragma unroll
       for (int offset = kL / 2; offset > 0; offset >>= 1) {
-        const T ov = from_bits<T>(static_cast<std::uint32_t>(__shfl_xor(static_cast<int>(to_bits(best)), offset, kWave)));
-        const int oi = __shfl_xor(bi, offset, kWave);
-        if (cand_better<T, kLargest>(ov, oi, best, bi)) {
-          best = ov;
-          bi = oi;
-        }
+        const std::uint64_t o = __shfl_xor(key, offset, kWave);
+        key = o > key ? o : key;
       }
-      r.bits = to_bits(best);
+      const int bi = key ? static_cast<int>(0xFFFFFFFFU - static_cast<std::uint32_t>(key)) : -1;
+      const int owner = (lane & ~(kL - 1)) + (bi < 0 ? 0 : bi % kL);
+      r.bits = static_cast<std::uint32_t>(__shfl(static_cast<int>(to_bits(best)), owner, kWave));
       r.index = bi;
     }
     if (live && l == 0) store_row<kOp, T>(out, row, r, R);
