@@ -375,9 +375,23 @@ __device__ __forceinline__ Partial wave_reduce(const T* __restrict__ p, std::int
         return Partial{body.bits + extra, 0U, 0};
       }
     } else {
-      T best = edge;
-      std::int64_t bi = idx;
-      wave_extremum<T, kLargest>(best, bi);
+      // The head and tail candidates sit in lanes 0-5: a 64-bit key maximum
+      // (rank key above the complemented segment-relative index, as in
+      // packed_row_kernel) over lanes 0-7 in three steps, the winner's bits
+      // from its lane; lane 0, which publishes the result, then holds it.
+      const std::int64_t rel = idx - begin;
+      std::uint64_t key = idx >= 0 ? (static_cast<std::uint64_t>(rank_key<T, kLargest>(to_bits(edge))) << 32) |
+                                         (0xFFFFFFFFU - static_cast<std::uint32_t>(rel))
+                                   : 0;
+#pragma unroll
+      for (int offset = 4; offset > 0; offset >>= 1) {
+        const std::uint64_t o = __shfl_xor(key, offset, kWave);
+        key = o > key ? o : key;
+      }
+      const std::int64_t won = key ? static_cast<std::int64_t>(0xFFFFFFFFU - static_cast<std::uint32_t>(key)) : -1;
+      const int owner = won < 0 ? 0 : won < head ? static_cast<int>(won) : static_cast<int>(3 + won - (body_end - begin));
+      const T best = from_bits<T>(static_cast<std::uint32_t>(__shfl(static_cast<int>(to_bits(edge)), owner, kWave)));
+      const std::int64_t bi = won < 0 ? -1 : begin + won;
       T v = from_bits<T>(body.bits);
       std::int64_t vi = body.index;
       if (cand_better<T, kLargest>(best, bi, v, vi)) {
