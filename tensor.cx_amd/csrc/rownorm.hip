@@ -6,9 +6,10 @@
 // HBM once and written once: rows of up to 128 elements pack several per wave
 // (row_packed_kernel), rows of up to 1024 elements take one wave per row
 // (kChunks 16-byte loads per lane, wave-wide butterfly statistics); rows of up
-// to kMaxSplit elements take one 256-thread block per row (four waves, whose
-// partial statistics meet in LDS). Longer rows use one block per row that
-// re-reads the row (mostly from L2). Strided rows (inner > 1) run
+// to 1024 x kMaxSplit elements take one 256-thread block per row (four waves,
+// whose partial statistics meet in LDS). Longer rows use one 1024-thread block
+// per row (row_block_kernel) that stages the row in LDS when it fits there and
+// otherwise reads it once per pass. Strided rows (inner > 1) run
 // col_norm_kernel: column tiles whose waves fold per-column statistics over
 // runs of rows, then write the row from them in a second walk (rows split
 // over blocks, with a workspace, when tiles are few).
