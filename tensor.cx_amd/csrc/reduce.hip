@@ -976,18 +976,20 @@ __global__ __launch_bounds__(64 * kShortWaves) void short_row_kernel(const T* __
 }
 
 // Contiguous rows (inner == 1) of kSequentialMax + 1 .. kPackedRowMax
-// elements: L lanes per row (the power of two at or above R / 8, at least
-// 16), 64 / L rows per wave. Lane l of a row's group takes elements l,
-// l + L, ... (at most kPackedLoads, all loaded before any is used), then the
+// elements: L lanes per row (the power of two at or above R / 8, at most
+// 64, at least 16), 64 / L rows per wave. Lane l of a row's group takes
+// elements l, l + L, ... (kLoads of them at most: kPackedLoads, or two or
+// four times that for rows of 513-2048, all loaded before any is used), then the
 // group folds its lanes by butterfly: sums in a fixed tree (every lane ends
 // with the same bits), extrema as (value, row index) candidates under
 // cand_better, so ties and NaNs keep the reference's lowest-index rule. One
 // wave per row spent each row's load latency and two wave-wide folds on
-// 130 elements: [100000, 130] sum ran at 8.6 % and max at 4.8 % of HBM.
-constexpr std::int64_t kPackedRowMax = 512;
+// 130 elements: [100000, 130] sum ran at 8.6 % and max at 4.8 % of HBM,
+// and [16384, 1023] sum 20.5 us against 11.0 us here.
+constexpr std::int64_t kPackedRowMax = 2048;
 constexpr int kPackedLoads = 8;
 
-template <int kOp, typename T, int kL>
+template <int kOp, typename T, int kL, int kLoads>
 __global__ __launch_bounds__(256) void packed_row_kernel(const T* __restrict__ x, void* __restrict__ out,
                                                          std::int64_t rows, int R) {
   constexpr bool kSum = kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN;
@@ -1003,15 +1005,15 @@ __global__ __launch_bounds__(256) void packed_row_kernel(const T* __restrict__ x
     const std::int64_t row = t * kRows + lane / kL;
     const bool live = row < rows;
     const T* __restrict__ p = x + (live ? row : 0) * R;
-    T v[kPackedLoads];
+    T v[kLoads];
 #pragma unroll
-    for (int u = 0; u < kPackedLoads; ++u) v[u] = (live && l + u * kL < R) ? p[l + u * kL] : T{};
+    for (int u = 0; u < kLoads; ++u) v[u] = (live && l + u * kL < R) ? p[l + u * kL] : T{};
     Partial r{0U, 0U, 0};
     if constexpr (kSum) {
       if constexpr (__is_same(T, float)) {
         float s = 0.F;
 #pragma unroll
-        for (int u = 0; u < kPackedLoads; ++u)
+        for (int u = 0; u < kLoads; ++u)
           if (l + u * kL < R) s += v[u];
 #pragma unroll
         for (int offset = kL / 2; offset > 0; offset >>= 1) s += __shfl_xor(s, offset, kWave);
@@ -1019,7 +1021,7 @@ __global__ __launch_bounds__(256) void packed_row_kernel(const T* __restrict__ x
       } else {
         std::uint32_t s = 0;
 #pragma unroll
-        for (int u = 0; u < kPackedLoads; ++u)
+        for (int u = 0; u < kLoads; ++u)
           if (l + u * kL < R) s += static_cast<std::uint32_t>(v[u]);
 #pragma unroll
         for (int offset = kL / 2; offset > 0; offset >>= 1)
@@ -1037,7 +1039,7 @@ __global__ __launch_bounds__(256) void packed_row_kernel(const T* __restrict__ x
       std::uint64_t key = 0;
       T best{};
 #pragma unroll
-      for (int u = 0; u < kPackedLoads; ++u) {
+      for (int u = 0; u < kLoads; ++u) {
         const int j = l + u * kL;
         if (live && j < R) {
           const std::uint64_t k = (static_cast<std::uint64_t>(rank_key<T, kLargest>(to_bits(v[u]))) << 32) |
@@ -1322,9 +1324,11 @@ int launch_reduce(const T* x, void* out, std::int64_t outer, std::int64_t reduce
                            dim3(256), 0, s, x, out, outer, static_cast<int>(reduce));
         return check(hipGetLastError(), "reduce packed row kernel launch");
       };
-      if (reduce <= 16 * kPackedLoads) return packed(packed_row_kernel<kOp, T, 16>, 4);
-      if (reduce <= 32 * kPackedLoads) return packed(packed_row_kernel<kOp, T, 32>, 2);
-      return packed(packed_row_kernel<kOp, T, 64>, 1);
+      if (reduce <= 16 * kPackedLoads) return packed(packed_row_kernel<kOp, T, 16, kPackedLoads>, 4);
+      if (reduce <= 32 * kPackedLoads) return packed(packed_row_kernel<kOp, T, 32, kPackedLoads>, 2);
+      if (reduce <= 64 * kPackedLoads) return packed(packed_row_kernel<kOp, T, 64, kPackedLoads>, 1);
+      if (reduce <= 128 * kPackedLoads) return packed(packed_row_kernel<kOp, T, 64, 2 * kPackedLoads>, 1);
+      return packed(packed_row_kernel<kOp, T, 64, 4 * kPackedLoads>, 1);
     }
     if (inner == 1 && reduce >= kShortRowMin) {
       const std::int64_t tiles = (outer + 63) / 64;

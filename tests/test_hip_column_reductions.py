@@ -227,7 +227,7 @@ def test_short_rows_exact_order(cx, width):
         assert_bits(getattr(cx, op)(hi, 1).numpy(), getattr(oracle, op)(xi, 1), f"i32 {op} width {width}")
 
 
-@pytest.mark.parametrize("width", [65, 66, 67, 128, 130, 255, 257, 511, 512, 513, 1021, 1027, 4099, 8191, 40001])
+@pytest.mark.parametrize("width", [65, 66, 67, 128, 130, 255, 257, 511, 512, 513, 700, 1021, 1024, 1027, 1500, 2047, 2048, 2049, 4099, 8191, 40001])
 def test_unaligned_rows_head_body_tail(cx, width):
     # Rows whose length is not a multiple of 4 start at every 4-byte offset:
     # each wave segment splits into a head (to the next 16-byte boundary), a
