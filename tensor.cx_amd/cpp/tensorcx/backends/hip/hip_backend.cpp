@@ -216,8 +216,10 @@ void run_gemm(const float* lhs, const float* rhs, float* out, const tcx_hip_gemm
   if (workspace) ok_or_throw(tcx_hip_stream_synchronize(s), what);
 }
 
-// Serialises this process's calls of tcx_hip_reduce_noalloc, whose scratch is
-// one per device: each holds it from launch until its stream has finished.
+// Guards tcx_hip_reduce_noalloc's scratch, one per device: a call holds it
+// from launch until its stream has finished. Only one call at a time uses it;
+// a call that finds it taken runs on a workspace of its own instead of
+// waiting, so concurrent segmented reductions never queue behind each other.
 std::mutex reduce_scratch_mutex;
 
 void run_rows(int code, const Tensor& x, const Tensor& out, Dim outer, Dim reduce, Dim inner, Stream& s) {
@@ -225,12 +227,15 @@ void run_rows(int code, const Tensor& x, const Tensor& out, Dim outer, Dim reduc
   const std::size_t ws = tcx_hip_reduce_workspace_bytes(code, dtype, outer, reduce, inner);
   if (ws != 0 && ws <= TCX_HIP_REDUCE_NOALLOC_MAX_WORKSPACE) {
     // Segmented rows (a full-tensor sum, few long rows): the partials go to
-    // the library's static scratch, so no workspace is allocated per call.
-    std::lock_guard lock(reduce_scratch_mutex);
-    ok_or_throw(tcx_hip_reduce_noalloc(code, dtype, device_ptr(x), out_ptr(out), outer, reduce, inner, s),
-                "HIP reduction");
-    ok_or_throw(tcx_hip_stream_synchronize(s), "HIP reduction");
-    return;
+    // the library's static scratch when it is free, so no workspace is
+    // allocated per call.
+    std::unique_lock lock(reduce_scratch_mutex, std::try_to_lock);
+    if (lock.owns_lock()) {
+      ok_or_throw(tcx_hip_reduce_noalloc(code, dtype, device_ptr(x), out_ptr(out), outer, reduce, inner, s),
+                  "HIP reduction");
+      ok_or_throw(tcx_hip_stream_synchronize(s), "HIP reduction");
+      return;
+    }
   }
   std::shared_ptr<HipBuffer> workspace;
   if (ws) {
