@@ -164,6 +164,7 @@ def _work(cx, t):
     }
 
 
+@pytest.mark.gpu
 def test_barrier_aligned_shared_state(cx):
     inputs = [_inputs(i) for i in range(THREADS)]
     device = [{k: cx.tensor(v, device="hip") for k, v in inp.items()} for inp in inputs]
@@ -185,6 +186,7 @@ def test_barrier_aligned_shared_state(cx):
     _run_in_threads(worker)
 
 
+@pytest.mark.gpu
 def test_barrier_aligned_pool_scopes(cx):
     """Pools entered on every thread at once, each serving its own thread's
     output and workspace allocations, then trimmed and closed."""
@@ -210,6 +212,7 @@ def test_barrier_aligned_pool_scopes(cx):
     _run_in_threads(worker)
 
 
+@pytest.mark.gpu
 def test_concurrent_inference_chain(cx):
     """Reference tests/python/test_cuda_primitives.py:90-101 with the same
     chain of primitives, four workers, twelve calls."""
