@@ -92,11 +92,37 @@ __device__ __forceinline__ int output_feature(int r, int t) {
   else return kT * r + t;
 }
 
-// kKeys keys per tile (64, or 32 to fit two blocks per CU), kB = kKeys / 16
-// MFMA blocks of keys.
+// Online-softmax state of a wave's 16 queries: the output accumulators in
+// MFMA layout and the running maximum and sum (the lanes of query j hold its
+// m and l).
+template <int kT>
+struct FlashState {
+  mfma_acc o[kT];
+  float m, l;
+};
+
+template <int kT>
+__device__ __forceinline__ void flash_init(FlashState<kT>& st) {
+#pragma unroll
+  for (int t = 0; t < kT; ++t) st.o[t] = mfma_acc{0.F, 0.F, 0.F, 0.F};
+  st.m = -__builtin_inff();
+  st.l = 0.F;
+}
+
+// Key tiles [t_begin, t_end) of query tile `qtile` of batch matrix `batch`,
+// folded into the state of the calling wave's 16 queries by the block's
+// kWaves waves (thread tid) on two K and two V stages. kKeys keys per tile
+// (64, or 32 to fit two blocks per CU), kB = kKeys / 16 MFMA blocks of keys.
+// With scan_tail, the V rows after the range (keys the causal mask hides from
+// every query of the tile) mark the feature columns holding an inf or NaN in
+// bad_column, cleared by the caller. The segment opens with a barrier, so a
+// segment may follow another on the same stages.
+
 template <int D, int kWaves, int kKeys, bool kCausal>
-__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 8))) void flash_attention_kernel(
-    FlashArgs a) {
+__device__ __forceinline__ void flash_segment(const FlashArgs& a, float (&ks)[2][kKeys * D],
+                                              float (&vs)[2][kKeys * D], int* bad_column, int tid,
+                                              std::int64_t batch, std::int64_t qtile, std::int64_t t_begin,
+                                              std::int64_t t_end, bool scan_tail, FlashState<D / 16>& st) {
   constexpr int kQTile = 16 * kWaves;
   constexpr int kT = D / 16;
   constexpr int kB = kKeys / 16;
@@ -105,40 +131,11 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
   constexpr int kRowsPerInst = 64 / kChunks;             // rows one wave instruction fills
   constexpr int kInst = kKeys / kRowsPerInst / kWaves;   // instructions per wave per K (or V) tile
   static_assert(D % 16 == 0 && kInst >= 1 && kInst * kRowsPerInst * kWaves == kKeys);
-  __shared__ float ks[2][kKeys * D];
-  __shared__ float vs[2][kKeys * D];
-  __shared__ int bad_column[D];
-
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
-  // One block per work item on a 1-D grid of n = qtiles x batch blocks; the
-  // launch id maps to an item (batch-major by default).
-  const std::int64_t n = a.qtiles * a.batch;
-  const std::int64_t id = blockIdx.x;
-  std::int64_t batch = id / a.qtiles, qtile = id % a.qtiles;
-  if (a.xcd_blocks) {
-    // Launch id L runs on XCD L % 8: give XCD x the consecutive (batch-major)
-    // work items x * n/8 .. (x + 1) * n/8 - 1, so that the query tiles of one
-    // batch matrix share its K and V in that XCD's L2 (n % 8 == 0).
-    const std::int64_t item = (id % 8) * (n / 8) + id / 8;
-    batch = item / a.qtiles;
-    qtile = item % a.qtiles;
-  }
-  if constexpr (kCausal) {
-    // Under causal masking the last query tiles see the most keys. Work items
-    // are ranked by their key-tile count; the first half of the grid takes
-    // them heaviest first and the second half lightest first, so the two
-    // blocks that share a CU (launch ids L and L + n/2) carry about the same
-    // total work.
-    const std::int64_t half = (n + 1) / 2;
-    const std::int64_t rank = id < half ? id : n - 1 - (id - half);
-    qtile = a.qtiles - 1 - rank / a.batch;
-    batch = rank % a.batch;
-  }
   const std::int64_t q0 = qtile * kQTile + wave * 16;
-  const std::int64_t q_last = min(qtile * kQTile + kQTile, a.rows) - 1;
-  for (int d = tid; d < D; d += 64 * kWaves) bad_column[d] = 0;
+  const std::int64_t tiles = (a.cols + kKeys - 1) / kKeys;
   const float* __restrict__ qb = a.q + batch * a.rows * D;
   const float* __restrict__ kb = a.k + batch * a.cols * D;
   const float* __restrict__ vb = a.v + batch * a.cols * D;
@@ -156,11 +153,10 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
       if (qrow >= a.rows) qf[t] = float4_t{0.F, 0.F, 0.F, 0.F};
     }
   }
-  mfma_acc o[kT];
-#pragma unroll
-  for (int t = 0; t < kT; ++t) o[t] = mfma_acc{0.F, 0.F, 0.F, 0.F};
+  mfma_acc (&o)[kT] = st.o;
+  float& m = st.m;
+  float& l = st.l;
   const float neg_inf = -__builtin_inff();
-  float m = neg_inf, l = 0.F;
   const std::int64_t query = q0 + r;
 
   // DMA. Each tile is read through a buffer resource based at the tile's
@@ -365,33 +361,32 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
     }
   };
 
-  const std::int64_t tiles = (a.cols + kKeys - 1) / kKeys;
-  // Under causal masking tiles past the block's last query are not run. The
-  // loop below takes every tile but the last, which are full unless masked
-  // causally.
-  const std::int64_t run = kCausal ? min(tiles, q_last / kKeys + 1) : tiles;
+  // Every tile but the last of the segment is full unless masked causally.
   mfma_acc s_cur[kB], s_next[kB];
   float4_t kf[2][kB];
   float vv[2][kT];
-  if (run > 0) {
-    issue(kb, ks[0], 0);
-    issue(vb, vs[0], 0);
-    if (run > 1) issue(kb, ks[1], 1);
+  // The stages may still be read by this team's previous segment.
+  __syncthreads();
+  if (t_begin < t_end) {
+    issue(kb, ks[0], t_begin);
+    issue(vb, vs[0], t_begin);
+    if (t_begin + 1 < t_end) issue(kb, ks[1], t_begin + 1);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();  // K 0, V 0 and K 1 have landed
     scores(ks[0], s_cur);
     __syncthreads();  // every wave is done with K stage 0
   } else {
-    __syncthreads();  // bad_column is cleared
+    __syncthreads();
   }
-  // Iteration `tile`: K tile + 1 sits in stage (tile + 1) & 1, V tile in
-  // stage tile & 1; K tile + 2 and V tile + 1 load into the other stages,
-  // whose last readers finished before the previous barrier.
-  std::int64_t tile = 0;
-  for (; tile + 1 < run; ++tile) {
-    const int st = static_cast<int>(tile & 1);
+  // Iteration `tile` (stage parity counted from t_begin): K tile + 1 sits in
+  // stage (tile + 1) & 1, V tile in stage tile & 1; K tile + 2 and V tile + 1
+  // load into the other stages, whose last readers finished before the
+  // previous barrier.
+  std::int64_t tile = t_begin;
+  for (; tile + 1 < t_end; ++tile) {
+    const int st = static_cast<int>((tile - t_begin) & 1);
     issue(vb, vs[st ^ 1], tile + 1);
-    if (tile + 2 < run) issue(kb, ks[st], tile + 2);
+    if (tile + 2 < t_end) issue(kb, ks[st], tile + 2);
     begin_tile(tile);
 #pragma unroll
     for (int b = 0; b < kB; ++b) s_next[b] = mfma_acc{0.F, 0.F, 0.F, 0.F};
@@ -412,14 +407,15 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads have landed
     __syncthreads();                // and every wave is done with this iteration's stages
   }
-  if (tile < run) {
+  if (tile < t_end) {
+    const int st = static_cast<int>((tile - t_begin) & 1);
     begin_tile(tile);
     all_steps(s_cur, std::make_integer_sequence<int, kSteps>{});
-    read_v(vs[tile & 1], 0, vv[0]);
-    accumulate(vs[tile & 1], s_cur, vv, std::make_integer_sequence<int, 4 * kB>{});
+    read_v(vs[st], 0, vv[0]);
+    accumulate(vs[st], s_cur, vv, std::make_integer_sequence<int, 4 * kB>{});
   }
 
-  if (run < tiles) {
+  if (scan_tail && t_end < tiles) {
     // Columns of the V rows past the last run tile that hold an inf or NaN
     // (exponent all ones), eight independent loads in flight per thread and
     // no branch in the loop (a branch on each load's value serialised the
@@ -432,7 +428,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
 #pragma unroll
       for (int e = 0; e < 4; ++e) flag[e] |= (__float_as_uint(w[e]) & kExp) == kExp ? 1U : 0U;
     };
-    std::int64_t row = run * kKeys + tid / (D / 4);
+    std::int64_t row = t_end * kKeys + tid / (D / 4);
     for (; row + 7 * kPass < a.cols; row += 8 * kPass) {
       float4_t w[8];
 #pragma unroll
@@ -445,21 +441,33 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
     for (int e = 0; e < 4; ++e)
       if (flag[e]) bad_column[c + e] = 1;
   }
-  __syncthreads();
+}
+
+// Stores the calling wave's 16 output rows of query tile `qtile` from its
+// state (NaN in the columns bad_column marks, 0 * V for an all-masked row).
+template <int D, int kWaves>
+__device__ __forceinline__ void flash_store(const FlashArgs& a, const int* bad_column, int tid, std::int64_t batch,
+                                            std::int64_t qtile, const FlashState<D / 16>& st) {
+  constexpr int kT = D / 16;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const std::int64_t q0 = qtile * (16 * kWaves) + wave * 16;
+  const float neg_inf = -__builtin_inff();
   float* __restrict__ ob = a.out + batch * a.rows * D;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int src = 4 * g + v;
-    const float lv = __shfl(l, src, kWave);
-    const float mv = __shfl(m, src, kWave);
+    const float lv = __shfl(st.l, src, kWave);
+    const float mv = __shfl(st.m, src, kWave);
     const std::int64_t qrow = q0 + 4 * g + v;
     if (qrow >= a.rows) continue;
     float y[kT];
 #pragma unroll
     for (int t = 0; t < kT; ++t) {
       if (bad_column[output_feature<kT>(r, t)]) y[t] = __builtin_nanf("");
-      else if (mv == neg_inf) y[t] = o[t][v] * 0.F;
-      else y[t] = o[t][v] / lv;
+      else if (mv == neg_inf) y[t] = st.o[t][v] * 0.F;
+      else y[t] = st.o[t][v] / lv;
     }
     float* const orow = ob + qrow * D;
     if constexpr (kT >= 4) {
@@ -471,6 +479,51 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
       store_row<kT>(orow + kT * r, y);
     }
   }
+}
+
+// One block per query tile.
+template <int D, int kWaves, int kKeys, bool kCausal>
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 8))) void flash_attention_kernel(
+    FlashArgs a) {
+  constexpr int kQTile = 16 * kWaves;
+  __shared__ float ks[2][kKeys * D];
+  __shared__ float vs[2][kKeys * D];
+  __shared__ int bad_column[D];
+  const int tid = threadIdx.x;
+  // One block per work item on a 1-D grid of n = qtiles x batch blocks; the
+  // launch id maps to an item (batch-major by default).
+  const std::int64_t n = a.qtiles * a.batch;
+  const std::int64_t id = blockIdx.x;
+  std::int64_t batch = id / a.qtiles, qtile = id % a.qtiles;
+  if (a.xcd_blocks) {
+    // Launch id L runs on XCD L % 8: give XCD x the consecutive (batch-major)
+    // work items x * n/8 .. (x + 1) * n/8 - 1, so that the query tiles of one
+    // batch matrix share its K and V in that XCD's L2 (n % 8 == 0).
+    const std::int64_t item = (id % 8) * (n / 8) + id / 8;
+    batch = item / a.qtiles;
+    qtile = item % a.qtiles;
+  }
+  if constexpr (kCausal) {
+    // Under causal masking the last query tiles see the most keys. Work items
+    // are ranked by their key-tile count; the first half of the grid takes
+    // them heaviest first and the second half lightest first, so the two
+    // blocks that share a CU (launch ids L and L + n/2) carry about the same
+    // total work.
+    const std::int64_t half = (n + 1) / 2;
+    const std::int64_t rank = id < half ? id : n - 1 - (id - half);
+    qtile = a.qtiles - 1 - rank / a.batch;
+    batch = rank % a.batch;
+  }
+  const std::int64_t q_last = min(qtile * kQTile + kQTile, a.rows) - 1;
+  const std::int64_t tiles = (a.cols + kKeys - 1) / kKeys;
+  // Under causal masking tiles past the block's last query are not run.
+  const std::int64_t run = kCausal ? min(tiles, q_last / kKeys + 1) : tiles;
+  for (int d = tid; d < D; d += 64 * kWaves) bad_column[d] = 0;
+  FlashState<D / 16> st;
+  flash_init(st);
+  flash_segment<D, kWaves, kKeys, kCausal>(a, ks, vs, bad_column, tid, batch, qtile, 0, run, true, st);
+  __syncthreads();
+  flash_store<D, kWaves>(a, bad_column, tid, batch, qtile, st);
 }
 
 template <int D, int kWaves, int kKeys, bool kCausal>

@@ -430,3 +430,48 @@ def test_fused_attention_special_values(cx, d):
     k2[0, :, :] = 1.0
     with np.errstate(all="ignore"):
         attention_check(cx, q2, k2, v2)
+
+
+# Causal shapes with 256 or more batch matrices: at least two query tiles per
+# CU, in the heavy/light block order, with partial last tiles, key lengths
+# other than the query length and empty keys.
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("rows,cols", [(64, 64), (130, 130), (257, 200), (200, 257), (300, 37), (65, 0)])
+def test_fused_attention_causal_many_tiles(cx, d, rows, cols):
+    q, k, v = f32((256, rows, d), 41), f32((256, cols, d), 42), f32((256, cols, d), 43)
+    attention_check(cx, q, k, v, None, True)
+    attention_check(cx, q, k, v, None, True, scale=0.05)
+
+
+@pytest.mark.parametrize("d", [32, 128])
+def test_fused_attention_causal_odd_tile_count(cx, d):
+    # 3 query tiles per matrix: the heavy/light order pairs tiles of
+    # different matrices on one CU.
+    q, k, v = f32((512, 150, d), 44), f32((512, 150, d), 45), f32((512, 150, d), 46)
+    attention_check(cx, q, k, v, None, True)
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+def test_fused_attention_causal_many_value_scan(cx, d):
+    # Non-finite V rows behind the causal masks of early query tiles (the
+    # tail scan) and inside the key ranges the tiles run.
+    q, k, v = f32((256, 300, d), 47), f32((256, 300, d), 48), f32((256, 300, d), 49)
+    v[0, 290, 3] = np.nan      # inside the key range of the last query tile
+    v[3, 70, d - 1] = np.inf   # behind the first query tile (queries 0..63)
+    v[5, 20, 0] = -np.inf      # an early key, seen by every query tile
+    v[7, 200, 1] = np.nan      # behind the first three query tiles
+    v[9, 299, 2] = np.inf      # the last key
+    with np.errstate(all="ignore"):
+        attention_check(cx, q, k, v, None, True)
+
+
+@pytest.mark.parametrize("d", [32, 128])
+def test_fused_attention_causal_many_special_values(cx, d):
+    q, k, v = f32((256, 200, d), 50), f32((256, 200, d), 51), f32((256, 200, d), 52)
+    q[0, 3, 7] = np.nan          # a NaN query: its row is NaN
+    q[1, 190, 0] = np.nan        # in the last query tile
+    k[2, 11] = np.inf            # +inf / NaN scores for every query after key 11
+    k[3, 150] = -np.inf
+    q[4, 199] = -np.inf          # scores of -inf and +inf / NaN
+    with np.errstate(all="ignore"):
+        attention_check(cx, q, k, v, None, True)
