@@ -569,6 +569,7 @@ __device__ float block_reduce(float v, bool is_max, float* scratch) {
 // Threads of the long-row block: 1024 keep four times the loads of 256 in
 // flight per row, which matters when a few hundred rows fill the GPU.
 constexpr int kRowBlockThreads = 1024;
+constexpr int kNonTemporal = 2;  // buffer instruction cache policy: nt
 
 // Walks row x[0, n) with the kRowBlockThreads threads of a block: the elements before
 // x's first 16-byte boundary (threads 0-2, f1(value, i)), whole float4s four
@@ -604,12 +605,25 @@ __device__ __forceinline__ void block_row_walk(const float* __restrict__ x, std:
   if (t < n - tail) f1(x[tail + t], tail + t);
 }
 
+// exp(d) for -150 <= d <= 88 (the caller clamps): 2^t exp(r) with
+// t = d log2(e) and r = d - t ln(2) taken in two parts (Cody and Waite), so
+// that exp(r) = 1 + r to within 2^-35 (|r| < 2^-16). Within 1.5 ulp of exp(d)
+// where the result is normal; 0 below 2^-126 (and at d = -150).
+__device__ __forceinline__ float exp_reduced(float d) {
+  constexpr float kLog2e = 1.44269502F;
+  constexpr float kLn2Hi = 0.693145752F;    // 0x3f317200: ln 2 to 16 bits
+  constexpr float kLn2Lo = 1.42860677e-6F;  // ln 2 - kLn2Hi
+  const float t = d * kLog2e;
+  const float e = __builtin_amdgcn_exp2f(t);
+  const float r = fmaf(-t, kLn2Lo, fmaf(-t, kLn2Hi, d));
+  return fmaf(e, r, e);
+}
+
 // Rows too long for registers: one block per row, passes over the row
-// (softmax: running maximum and sum, write;
-// RMSNorm: sum of squares, write; LayerNorm: sum, squared deviations,
-// write). Outputs go out as float4 when out and x share their offset within
-// 16 bytes, else element by element. Rows that fit in the block's LDS are
-// read from HBM once (kStaged), longer ones once per pass.
+// (softmax: maximum, exponentials and their sum, write; RMSNorm: sum of
+// squares, write; LayerNorm: sum, squared deviations, write). Rows that fit
+// in the block's LDS are read from HBM once (kStaged), longer ones once per
+// pass.
 template <RowOp kOp, bool kStaged>
 __global__ __launch_bounds__(kRowBlockThreads) void row_block_kernel(RowArgs a) {
   constexpr int kWaves = kRowBlockThreads / 64;
@@ -619,7 +633,6 @@ __global__ __launch_bounds__(kRowBlockThreads) void row_block_kernel(RowArgs a) 
   const std::int64_t n = a.n;
   const float* __restrict__ x = a.x + row * n;
   float* __restrict__ out = a.out + row * n;
-  const bool vec_out = ((reinterpret_cast<std::uintptr_t>(out) - reinterpret_cast<std::uintptr_t>(x)) & 15U) == 0;
   // kStaged: the first walk copies the row into LDS (dynamic, n + 3 floats),
   // pad floats in, so that the float4 body block_row_walk reads from x sits
   // 16-byte aligned in LDS too; later walks read LDS instead of HBM.
@@ -654,39 +667,121 @@ __global__ __launch_bounds__(kRowBlockThreads) void row_block_kernel(RowArgs a) 
       block_row_walk(x, n, f4, f1);
     }
   };
-  // Writes f(value, i) for every element of the row.
+  // Writes f(value) for every element of the row, times the weight and plus
+  // the bias when present, as float4 at x's float4 offsets (16-byte buffer
+  // accesses need only 4-byte alignment in out, gamma and beta).
+  const float* __restrict__ g = a.gamma;
+  const float* __restrict__ b = a.beta;
+  auto rsrc_of = [&](const float* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), static_cast<short>(0),
+                                             static_cast<int>(4 * n), 0x00020000);
+  };
   auto write_row = [&](auto&& f) {
+    if (n >= (std::int64_t{1} << 29)) {  // past 32-bit buffer offsets: element by element
+      walk(
+          [&](const float4_t& v, std::int64_t i) {
+            const float q[4] = {v.x, v.y, v.z, v.w};
+            for (int e = 0; e < 4; ++e) {
+              float r = f(q[e]);
+              if (g) r = r * g[i + e];
+              if (b) r = r + b[i + e];
+              out[i + e] = r;
+            }
+          },
+          [&](float v, std::int64_t i) {
+            float r = f(v);
+            if (g) r = r * g[i];
+            if (b) r = r + b[i];
+            out[i] = r;
+          });
+      return;
+    }
+    const auto o_rsrc = rsrc_of(out);
+    const auto g_rsrc = rsrc_of(g ? g : out);
+    const auto b_rsrc = rsrc_of(b ? b : out);
+    using b128_t = decltype(__builtin_amdgcn_raw_buffer_load_b128(o_rsrc, 0, 0, 0));
     walk(
         [&](const float4_t& v, std::int64_t i) {
-          const float4_t r = {f(v.x, i), f(v.y, i + 1), f(v.z, i + 2), f(v.w, i + 3)};
-          if (vec_out) {
-            *reinterpret_cast<float4_t*>(out + i) = r;
-          } else {
-            out[i] = r.x; out[i + 1] = r.y; out[i + 2] = r.z; out[i + 3] = r.w;
+          float4_t r = {f(v.x), f(v.y), f(v.z), f(v.w)};
+          const int off = static_cast<int>(4 * i);
+          if (g) {
+            const auto gv = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(g_rsrc, off, 0, 0));
+            r = float4_t{r.x * gv.x, r.y * gv.y, r.z * gv.z, r.w * gv.w};
           }
+          if (b) {
+            const auto bv = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, off, 0, 0));
+            r = float4_t{r.x + bv.x, r.y + bv.y, r.z + bv.z, r.w + bv.w};
+          }
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(b128_t, r), o_rsrc, off, 0, kNonTemporal);
         },
-        [&](float v, std::int64_t i) { out[i] = f(v, i); });
+        [&](float v, std::int64_t i) {
+          float r = f(v);
+          if (g) r = r * g[i];
+          if (b) r = r + b[i];
+          out[i] = r;
+        });
   };
   if constexpr (kOp == RowOp::kSoftmax) {
-    // One read pass for the maximum and the sum: each thread keeps (m, s),
-    // s relative to its running maximum m and rescaled when m grows (a sum
-    // begun under m = -inf starts over). A separate maximum pass read every
-    // row three times: [1000, 100000] 284 us at 35 % of HBM.
-    float m = -__builtin_inff(), s = 0.F;
-    auto grow = [&](float top) {
-      if ((is_nan(top) && !is_nan(m)) || top > m) {
-        s = m == -__builtin_inff() ? 0.F : s * exp_softmax(m - top);
-        m = top;
-      }
-    };
-    auto nan_max = [](float p, float q) { return (is_nan(q) || q > p) ? q : p; };
     if constexpr (kStaged) {
-      // A staged row is summed from LDS after the merge: the walk over HBM
-      // only takes the maximum, so its loads are not held up behind the
-      // exponentials (fused here, [4096, 20001] took 180 us against 159).
-      first_walk([&](const float4_t& v, std::int64_t) { m = nan_max(m, nan_max(nan_max(v.x, v.y), nan_max(v.z, v.w))); },
-                 [&](float v, std::int64_t) { m = nan_max(m, v); });
+      // The walk over HBM takes only the maximum (NaN-propagating, so a NaN
+      // anywhere makes it NaN), so its loads are not held up behind the
+      // exponentials; the exponentials then go back into LDS in place,
+      // e = exp(x - M), and the write multiplies them by 1 / denom. A row
+      // whose maximum is not finite (a NaN, +inf, or -inf throughout) is NaN
+      // throughout, as in the reference.
+      auto vmax = [](float p, float q) { return __builtin_elementwise_maximum(p, q); };
+      float m = -__builtin_inff();
+      first_walk([&](const float4_t& v, std::int64_t) { m = vmax(vmax(vmax(vmax(m, v.x), v.y), v.z), v.w); },
+                 [&](float v, std::int64_t) { m = vmax(m, v); });
+      m = wave_max_nan(m);
+      __shared__ float wave_m[kWaves];
+      if ((threadIdx.x & 63) == 0) wave_m[threadIdx.x >> 6] = m;
+      __syncthreads();
+      m = wave_m[0];
+      for (int w = 1; w < kWaves; ++w) m = vmax(m, wave_m[w]);
+      if (!__builtin_isfinite(m)) {
+        write_row([](float) { return __builtin_nanf(""); });
+        return;
+      }
+      // Clamped at -150 (exp 0): -inf elements give exactly 0.
+      auto ex = [&](float v) { return exp_reduced(fmaxf(v - m, -150.F)); };
+      float s0 = 0.F, s1 = 0.F;
+      {
+        const int t = threadIdx.x;
+        const std::int64_t vectors = (n - head) / 4;
+        float4_t* body = reinterpret_cast<float4_t*>(staged + pad + head);
+        for (std::int64_t k = t; k < vectors; k += kRowBlockThreads) {
+          const float4_t v = body[k];
+          const float4_t e = {ex(v.x), ex(v.y), ex(v.z), ex(v.w)};
+          body[k] = e;
+          s0 += e.x + e.y;
+          s1 += e.z + e.w;
+        }
+        const std::int64_t tail = head + 4 * vectors;
+        float* ends[2] = {t < head ? staged + pad + t : nullptr, t < n - tail ? staged + pad + tail + t : nullptr};
+        for (float* e : ends)
+          if (e != nullptr) {
+            *e = ex(*e);
+            s0 += *e;
+          }
+      }
+      // One correctly rounded reciprocal per row (each thread reads back
+      // only the LDS slots it wrote).
+      const float inv = 1.0F / block_reduce(s0 + s1, false, scratch);
+      write_row([&](float e) { return e * inv; });
     } else {
+      // One read pass for the maximum and the sum: each thread keeps (m, s),
+      // s relative to its running maximum m and rescaled when m grows (a sum
+      // begun under m = -inf starts over). A separate maximum pass read every
+      // row three times: [1000, 100000] 284 us at 35 % of HBM.
+      float m = -__builtin_inff(), s = 0.F;
+      auto grow = [&](float top) {
+        if ((is_nan(top) && !is_nan(m)) || top > m) {
+          s = m == -__builtin_inff() ? 0.F : s * exp_softmax(m - top);
+          m = top;
+        }
+      };
+      auto nan_max = [](float p, float q) { return (is_nan(q) || q > p) ? q : p; };
       first_walk(
           [&](const float4_t& v, std::int64_t) {
             grow(nan_max(nan_max(v.x, v.y), nan_max(v.z, v.w)));
@@ -696,44 +791,34 @@ __global__ __launch_bounds__(kRowBlockThreads) void row_block_kernel(RowArgs a) 
             grow(v);
             s += exp_softmax(v - m);
           });
-    }
-    // Merge (m, s) over the wave, then the block's waves in order.
-    auto merge = [&](float om, float os) {
-      const float top = nan_max(m, om);
-      if (top == -__builtin_inff()) {
-        s = s + os;
-      } else {
-        const float mine = m == -__builtin_inff() ? 0.F : s * exp_softmax(m - top);
-        const float other = om == -__builtin_inff() ? 0.F : os * exp_softmax(om - top);
-        s = mine + other;
-      }
-      m = top;
-    };
+      // Merge (m, s) over the wave, then the block's waves in order.
+      auto merge = [&](float om, float os) {
+        const float top = nan_max(m, om);
+        if (top == -__builtin_inff()) {
+          s = s + os;
+        } else {
+          const float mine = m == -__builtin_inff() ? 0.F : s * exp_softmax(m - top);
+          const float other = om == -__builtin_inff() ? 0.F : os * exp_softmax(om - top);
+          s = mine + other;
+        }
+        m = top;
+      };
 #pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) merge(__shfl_xor(m, offset, kWave), __shfl_xor(s, offset, kWave));
-    __shared__ float wave_ms[2][kWaves];
-    if ((threadIdx.x & 63) == 0) {
-      wave_ms[0][threadIdx.x >> 6] = m;
-      wave_ms[1][threadIdx.x >> 6] = s;
+      for (int offset = 32; offset > 0; offset >>= 1) merge(__shfl_xor(m, offset, kWave), __shfl_xor(s, offset, kWave));
+      __shared__ float wave_ms[2][kWaves];
+      if ((threadIdx.x & 63) == 0) {
+        wave_ms[0][threadIdx.x >> 6] = m;
+        wave_ms[1][threadIdx.x >> 6] = s;
+      }
+      __syncthreads();
+      m = wave_ms[0][0];
+      s = wave_ms[1][0];
+      for (int w = 1; w < kWaves; ++w) merge(wave_ms[0][w], wave_ms[1][w]);
+      // One correctly rounded reciprocal per row; each output is e * (1/denom),
+      // within 1.5 ulp of the reference's e / denom.
+      const float inv = 1.0F / s;
+      write_row([&](float v) { return exp_softmax(v - m) * inv; });
     }
-    __syncthreads();
-    m = wave_ms[0][0];
-    s = wave_ms[1][0];
-    for (int w = 1; w < kWaves; ++w) merge(wave_ms[0][w], wave_ms[1][w]);
-    if constexpr (kStaged) {
-      float s0 = 0.F, s1 = 0.F;
-      walk(
-          [&](const float4_t& v, std::int64_t) {
-            s0 += exp_softmax(v.x - m) + exp_softmax(v.y - m);
-            s1 += exp_softmax(v.z - m) + exp_softmax(v.w - m);
-          },
-          [&](float v, std::int64_t) { s0 += exp_softmax(v - m); });
-      s = block_reduce(s0 + s1, false, scratch);
-    }
-    // One correctly rounded reciprocal per row; each output is e * (1/denom),
-    // within 1.5 ulp of the reference's e / denom.
-    const float inv = 1.0F / s;
-    write_row([&](float v, std::int64_t) { return exp_softmax(v - m) * inv; });
   } else if constexpr (kOp == RowOp::kRms) {
     float s0 = 0.F, s1 = 0.F;
     first_walk(
@@ -741,11 +826,7 @@ __global__ __launch_bounds__(kRowBlockThreads) void row_block_kernel(RowArgs a) 
         [&](float v, std::int64_t) { s0 += v * v; });
     const float ss = block_reduce(s0 + s1, false, scratch);
     const float scale = 1.0F / sqrtf(ss / static_cast<float>(n) + a.eps);
-    const float* __restrict__ g = a.gamma;
-    write_row([&](float v, std::int64_t i) {
-      const float r = v * scale;
-      return g ? r * g[i] : r;
-    });
+    write_row([&](float v) { return v * scale; });
   } else {
     if (threadIdx.x == 0) eq_flag = 1;
     const float first = x[0];
@@ -764,16 +845,9 @@ __global__ __launch_bounds__(kRowBlockThreads) void row_block_kernel(RowArgs a) 
     const float mean = block_reduce(s0 + s1, false, scratch) / static_cast<float>(n);
     if (!equal) eq_flag = 0;
     __syncthreads();
-    const float* __restrict__ g = a.gamma;
-    const float* __restrict__ b = a.beta;
-    auto affine = [&](float r, std::int64_t i) {
-      if (g) r = r * g[i];
-      if (b) r = r + b[i];
-      return r;
-    };
     if (eq_flag && __builtin_isfinite(first)) {
       const float fillv = a.eps == 0.F ? __builtin_nanf("") : 0.F;
-      write_row([&](float, std::int64_t i) { return affine(fillv, i); });
+      write_row([&](float) { return fillv; });
       return;
     }
     float d0 = 0.F, d1 = 0.F;
@@ -789,7 +863,278 @@ __global__ __launch_bounds__(kRowBlockThreads) void row_block_kernel(RowArgs a) 
         });
     bool nan_row = false;
     const float scale = finish_scale_ln(block_reduce(d0 + d1, false, scratch), n, a.eps, nan_row);
-    write_row([&](float v, std::int64_t i) { return affine(nan_row ? __builtin_nanf("") : (v - mean) * scale, i); });
+    write_row([&](float v) { return nan_row ? __builtin_nanf("") : (v - mean) * scale; });
+  }
+}
+
+// Rows too long for one block's LDS and up to about 139 K floats: one
+// 512-thread block per row holds the whole row, its first 4 x 512 x
+// kResidentVec floats (after the elements before its first 16-byte boundary)
+// in registers, float4 k = t + 512 c in thread t's v[c], and the rest in LDS,
+// loaded straight from HBM (buffer_load ... lds) in 1 KB wave chunks, chunk j
+// by wave j mod 8, so that each lane reads back only what its own loads
+// wrote and no barrier is needed. A CU's registers (512 KB) and LDS (160 KB)
+// together hold such a row, so it is read from HBM once and written once.
+//
+// One row per CU at a time leaves no other block to overlap the row's
+// arithmetic with its loads, so the first statistics pass takes each float4
+// as it arrives: the LDS chunks (issued first, so landing first), then the
+// register chunks in order. For softmax that pass already takes the
+// exponentials, against the maximum m0 of the thread's first register
+// float4: e = exp(x - m0) in place, and the thread's sum of them. The block
+// maximum M then rescales: denom = sum over threads of sum_t * exp(m0_t - M)
+// in a fixed order, out = e * (exp(m0_t - M) / denom). A thread whose own
+// maximum lies more than kResidentShift above m0 reloads its elements from
+// HBM before any output is written and takes them against its own maximum,
+// so e stays below exp(16) and exp(m0_t - M) keeps the precision of the
+// outputs that matter. A row whose maximum is not finite (a NaN, +inf, or
+// -inf throughout) is NaN throughout, as in the reference.
+//
+// Loads and stores go through buffer resources (one address register for the
+// row, range-checked: float4s past the row read as zero and are not stored).
+// The affine weight and bias (which of them is present is a template
+// argument) are read as float4 beside each output float4.
+constexpr int kResidentThreads = 512;
+constexpr int kResidentVec = 44;
+constexpr float kResidentShift = 16.0F;
+constexpr int kAffGamma = 1, kAffBeta = 2;
+
+
+// One wave's 1 KB load from HBM straight into LDS at lds (a wave-uniform
+// address): lane l's 16 bytes at byte voffset of r land at lds + 16 l.
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, void* lds, int voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0,
+                                           kNonTemporal);
+}
+
+template <RowOp kOp, int kAff>
+__global__ __launch_bounds__(kResidentThreads) void row_resident_kernel(RowArgs a) {
+  constexpr int T = kResidentThreads, P = kResidentVec, kWaves = T / 64;
+  constexpr bool kG = (kAff & kAffGamma) != 0, kB = (kAff & kAffBeta) != 0;
+  extern __shared__ float4_t rest4[];
+  __shared__ float scratch[kWaves];
+  __shared__ int equal_waves[kWaves];
+  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const std::int64_t row = blockIdx.x;
+  const int n = static_cast<int>(a.n);  // below 2^29 (the launcher checks)
+  const float* __restrict__ x = a.x + row * a.n;
+  float* __restrict__ out = a.out + row * a.n;
+  int head = static_cast<int>(((16U - (reinterpret_cast<std::uintptr_t>(x) & 15U)) & 15U) / 4);
+  if (head > n) head = n;
+  const int vectors = (n - head) / 4, tail = head + 4 * vectors;
+  const int first = T * P;  // float4s from here on are in LDS
+  const int lds_chunks = vectors > first ? (vectors - first + 63) / 64 : 0;
+  auto rsrc_of = [](const float* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), static_cast<short>(0), bytes, 0x00020000);
+  };
+  const auto x_rsrc = rsrc_of(x + head, vectors * 16);
+  using b128_t = decltype(__builtin_amdgcn_raw_buffer_load_b128(x_rsrc, 0, 0, 0));
+  auto load4 = [&](int k) {
+    return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, k * 16, 0, kNonTemporal));
+  };
+  // Thread t's index, copied opaquely for each pass over the register
+  // chunks: the compiler would otherwise keep all 44 chunk offsets live from
+  // the loads to the stores.
+  auto opaque_t = [&] {
+    int u = t;
+    asm volatile("" : "+v"(u));
+    return u;
+  };
+
+  // LDS chunks first (they land first), then the register part, then the
+  // elements before the first 16-byte boundary and after the last whole
+  // float4 (threads 0-2, clamped loads used only where in range). A partial
+  // last LDS chunk reads zero past the row, into LDS the launch reserves.
+  for (int j = wave; j < lds_chunks; j += kWaves)
+    load_lds16(x_rsrc, rest4 + 64 * j, (first + 64 * j + lane) * 16);
+  float4_t v[P];
+#pragma unroll
+  for (int c = 0; c < P; ++c) v[c] = load4(t + T * c);
+  const bool has_h = t < head, has_t = t < n - tail;
+  float hv = x[has_h ? t : 0], tv = x[has_t ? tail + t : 0];
+  // Register chunks below full are in range for every thread (a uniform
+  // test), chunk full only for some.
+  const int full = vectors / T < P ? vectors / T : P;
+  auto in_regs = [&](int c) { return c < full || (c == full && t + T * c < vectors); };
+
+  // Applies f(float4&, float4 index) to this thread's float4s (its LDS slots,
+  // then its registers in arrival order) and g(float&) to its head and tail
+  // elements.
+  auto for_each = [&](auto&& f, auto&& g) {
+    for (int j = wave; j < lds_chunks; j += kWaves)
+      if (first + 64 * j + lane < vectors) f(rest4[64 * j + lane]);
+    // An opaque copy of full per pass: the per-chunk tests are then scalar
+    // compares used once, not 44 lane masks the compiler keeps across passes.
+    int f_full = full;
+    asm volatile("" : "+s"(f_full));
+#pragma unroll
+    for (int c = 0; c < P; ++c) {
+      if (c < f_full) {
+        f(v[c]);
+      } else if (c == f_full && t + T * c < vectors) {
+        f(v[c]);
+      }
+    }
+    if (has_h) g(hv);
+    if (has_t) g(tv);
+  };
+  auto block_sum = [&](float s) {
+    s = wave_sum(s);
+    if (lane == 0) scratch[wave] = s;
+    __syncthreads();
+    float r = scratch[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) r += scratch[w];
+    __syncthreads();  // scratch is reused
+    return r;
+  };
+
+  // Writes r(value) for every element, times the weight and plus the bias.
+  // The output, weight and bias float4s sit at x's float4 offsets, which are
+  // 16-byte aligned in x but only 4-byte aligned in the others when they
+  // start at another offset within 16 bytes: a 16-byte buffer access needs
+  // only 4-byte alignment.
+  const float* __restrict__ gamma = a.gamma;
+  const float* __restrict__ beta = a.beta;
+  auto write = [&](auto&& r) {
+    auto aff1 = [&](float q, int i) {
+      if constexpr (kG) q = q * gamma[i];
+      if constexpr (kB) q = q + beta[i];
+      return q;
+    };
+    const auto o_rsrc = rsrc_of(out + head, vectors * 16);
+    const auto g_rsrc = rsrc_of(kG ? gamma + head : out + head, vectors * 16);
+    const auto b_rsrc = rsrc_of(kB ? beta + head : out + head, vectors * 16);
+    auto put = [&](const float4_t& q, int k) {
+      float4_t o = {r(q.x), r(q.y), r(q.z), r(q.w)};
+      if constexpr (kG) {
+        const auto g = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(g_rsrc, k * 16, 0, 0));
+        o = float4_t{o.x * g.x, o.y * g.y, o.z * g.z, o.w * g.w};
+      }
+      if constexpr (kB) {
+        const auto b = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, k * 16, 0, 0));
+        o = float4_t{o.x + b.x, o.y + b.y, o.z + b.z, o.w + b.w};
+      }
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(b128_t, o), o_rsrc, k * 16, 0, kNonTemporal);
+    };
+    for (int j = wave; j < lds_chunks; j += kWaves) put(rest4[64 * j + lane], first + 64 * j + lane);
+#pragma unroll
+    for (int c = 0, u = opaque_t(); c < P; ++c) put(v[c], u + T * c);  // past the row: not stored
+    if (has_h) out[t] = aff1(r(hv), t);
+    if (has_t) out[tail + t] = aff1(r(tv), tail + t);
+  };
+
+  if constexpr (kOp == RowOp::kSoftmax) {
+    // NaN-propagating maxima (v_maximum3_f32): a NaN anywhere makes M NaN.
+    auto vmax = [](float p, float q) { return __builtin_elementwise_maximum(p, q); };
+    auto max4 = [&](float m, const float4_t& q) { return vmax(vmax(vmax(vmax(m, q.x), q.y), q.z), q.w); };
+    float m0 = max4(v[0].x, v[0]);  // v[0] is in range: the row has more than 512 float4s
+    float mt = m0, s0 = 0.F, s1 = 0.F;
+    // Clamped at -150 (exp 0): -inf elements give exactly 0; a NaN is caught
+    // by the maximum instead.
+    auto ex = [](float d) { return exp_reduced(fmaxf(d, -150.F)); };
+    auto exps = [&](float4_t& q, float m) {
+      q = float4_t{ex(q.x - m), ex(q.y - m), ex(q.z - m), ex(q.w - m)};
+      s0 += q.x + q.y;
+      s1 += q.z + q.w;
+    };
+    for_each(
+        [&](float4_t& q) {
+          mt = max4(mt, q);
+          exps(q, m0);
+        },
+        [&](float& q) {
+          mt = vmax(mt, q);
+          q = ex(q - m0);
+          s0 += q;
+        });
+    if (mt - m0 > kResidentShift && __builtin_isfinite(mt)) {
+      // Reload and take the exponentials against the thread's own maximum.
+      m0 = mt;
+      s0 = 0.F;
+      s1 = 0.F;
+      for (int j = wave; j < lds_chunks; j += kWaves)
+        if (first + 64 * j + lane < vectors) {
+          float4_t q = load4(first + 64 * j + lane);
+          exps(q, m0);
+          rest4[64 * j + lane] = q;
+        }
+#pragma unroll
+      for (int c = 0, u = opaque_t(); c < P; ++c)
+        if (in_regs(c)) {
+          v[c] = load4(u + T * c);
+          exps(v[c], m0);
+        }
+      if (has_h) {
+        hv = ex(x[t] - m0);
+        s0 += hv;
+      }
+      if (has_t) {
+        tv = ex(x[tail + t] - m0);
+        s0 += tv;
+      }
+    }
+    float m = wave_max_nan(mt);
+    if (lane == 0) scratch[wave] = m;
+    __syncthreads();
+    m = scratch[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) m = vmax(m, scratch[w]);
+    __syncthreads();
+    if (!__builtin_isfinite(m)) {
+      write([](float) { return __builtin_nanf(""); });
+      return;
+    }
+    const float w = ex(m0 - m);  // 0 for a thread of -inf only (m0 = -inf)
+    // One correctly rounded reciprocal per row.
+    const float f = w * (1.0F / block_sum((s0 + s1) * w));
+    write([&](float e) { return e * f; });
+  } else if constexpr (kOp == RowOp::kRms) {
+    float s0 = 0.F, s1 = 0.F;
+    for_each([&](const float4_t& q) { s0 += q.x * q.x + q.y * q.y; s1 += q.z * q.z + q.w * q.w; },
+             [&](float q) { s0 += q * q; });
+    const float scale = 1.0F / sqrtf(block_sum(s0 + s1) / static_cast<float>(n) + a.eps);
+    write([&](float q) { return q * scale; });
+  } else {
+    const float x0 = x[0];
+    float s0 = 0.F, s1 = 0.F;
+    bool equal = true;
+    for_each(
+        [&](const float4_t& q) {
+          s0 += q.x + q.y;
+          s1 += q.z + q.w;
+          equal = equal && q.x == x0 && q.y == x0 && q.z == x0 && q.w == x0;
+        },
+        [&](float q) {
+          s0 += q;
+          equal = equal && q == x0;
+        });
+    const bool wave_equal = __all(equal);  // all 64 lanes vote: outside the lane-0 branch
+    if (lane == 0) equal_waves[wave] = wave_equal ? 1 : 0;
+    const float mean = block_sum(s0 + s1) / static_cast<float>(n);
+    bool all_equal = true;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) all_equal = all_equal && equal_waves[w] != 0;
+    if (all_equal && __builtin_isfinite(x0)) {
+      // An all-equal finite row: 0, or NaN when eps is 0 (cpu_backend.cpp:205-213).
+      const float fill = a.eps == 0.F ? __builtin_nanf("") : 0.F;
+      write([&](float) { return fill; });
+      return;
+    }
+    float d0 = 0.F, d1 = 0.F;
+    for_each(
+        [&](const float4_t& q) {
+          const float dx = q.x - mean, dy = q.y - mean, dz = q.z - mean, dw = q.w - mean;
+          d0 += dx * dx + dy * dy;
+          d1 += dz * dz + dw * dw;
+        },
+        [&](float q) {
+          const float d = q - mean;
+          d0 += d * d;
+        });
+    bool nan_row = false;
+    const float scale = finish_scale_ln(block_sum(d0 + d1), n, a.eps, nan_row);
+    write([&](float q) { return nan_row ? __builtin_nanf("") : (q - mean) * scale; });
   }
 }
 
@@ -1343,6 +1688,18 @@ int run_cols(const RowArgs& r, std::int64_t outer, std::int64_t reduce, std::int
   return check(hipGetLastError(), "strided row write launch");
 }
 
+// Calls f(kernel, affine bits) for each resident-row kernel the op launches.
+using RowKernel = void (*)(RowArgs);
+template <RowOp kOp, typename F>
+void resident_variants(F&& f) {
+  f(static_cast<RowKernel>(&row_resident_kernel<kOp, 0>), 0);
+  if constexpr (kOp != RowOp::kSoftmax) f(static_cast<RowKernel>(&row_resident_kernel<kOp, kAffGamma>), kAffGamma);
+  if constexpr (kOp == RowOp::kLayer) {
+    f(static_cast<RowKernel>(&row_resident_kernel<kOp, kAffBeta>), kAffBeta);
+    f(static_cast<RowKernel>(&row_resident_kernel<kOp, kAffGamma | kAffBeta>), kAffGamma | kAffBeta);
+  }
+}
+
 template <RowOp kOp>
 int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t inner, void* workspace,
              std::size_t workspace_bytes, bool split, hipStream_t s) {
@@ -1386,14 +1743,29 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
       int bytes = 0;
       if (hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, device) != hipSuccess) bytes = 0;
       limit = bytes > 0 ? bytes : -1;
-      if (limit > 0)
+      if (limit > 0) {
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&row_block_kernel<kOp, true>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, limit - 1024);
+        resident_variants<kOp>([&](RowKernel kernel, int) {
+          (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    limit - 1024);
+        });
+      }
     }
     const std::int64_t staged_bytes = (reduce + 4) * static_cast<std::int64_t>(sizeof(float));
+    // Resident rows: LDS for the float4s past the registers' share, in whole
+    // 1 KB DMA instructions (a row has at most reduce / 4 float4s).
+    const std::int64_t past_regs = reduce / 4 - static_cast<std::int64_t>(kResidentThreads) * kResidentVec;
+    const std::int64_t resident_bytes = past_regs > 0 ? (past_regs + 63) / 64 * 1024 : 0;
     if (limit > 0 && staged_bytes <= limit - 1024)
       hipLaunchKernelGGL((row_block_kernel<kOp, true>), dim3(static_cast<unsigned>(outer)), dim3(kRowBlockThreads),
                          static_cast<unsigned>(staged_bytes), s, a);
+    else if (limit > 0 && resident_bytes <= limit - 1024)
+      resident_variants<kOp>([&](RowKernel kernel, int aff) {
+        if (aff == (a.gamma ? kAffGamma : 0) + (a.beta ? kAffBeta : 0))
+          hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(outer)), dim3(kResidentThreads),
+                             static_cast<unsigned>(resident_bytes), s, a);
+      });
     else
       hipLaunchKernelGGL((row_block_kernel<kOp, false>), dim3(static_cast<unsigned>(outer)), dim3(kRowBlockThreads),
                          0, s, a);
