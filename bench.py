@@ -24,6 +24,7 @@ Peaks: fp32 MFMA 157.3 TFLOP/s, HBM 8.0 TB/s (MI355X published figures).
 from __future__ import annotations
 
 import argparse
+import contextlib
 import json
 import os
 import pathlib
@@ -60,13 +61,48 @@ ROTATE_BYTES = 320 * 1024 * 1024
 MEDIAN_REPS = 31
 
 
-def timed(launch, steps: int, warmup: int, warm_ms: float = WARM_MS):
+def _roctx():
+    """The ROCTx library of rocprofiler-sdk, if present: every bench line runs
+    inside a range named for it, so that a `rocprofv3 --kernel-trace
+    --marker-trace` run attributes each dispatch to its line. Outside a
+    profiler the ranges cost a call each and record nothing."""
+    import ctypes
+    for name in ("librocprofiler-sdk-roctx.so.1", "/opt/rocm/lib/librocprofiler-sdk-roctx.so.1"):
+        try:
+            lib = ctypes.CDLL(name)
+        except OSError:
+            continue
+        lib.roctxRangePushA.argtypes = [ctypes.c_char_p]
+        return lib
+    return None
+
+
+ROCTX = _roctx()
+
+
+@contextlib.contextmanager
+def marked(name: str):
+    if ROCTX is not None:
+        ROCTX.roctxRangePushA(name.encode())
+    try:
+        yield
+    finally:
+        if ROCTX is not None:
+            ROCTX.roctxRangePop()
+
+
+def timed(launch, steps: int, warmup: int, warm_ms: float = WARM_MS, name: str = "launches"):
     """Runs `launch` warmup times, then (untimed) until warm_ms of GPU time has
     passed; then K = steps launches between two HIP events on the launch
     stream (total), then max(K, MEDIAN_REPS) more with an event pair around
-    each (per launch).
+    each (per launch), all inside a ROCTx range called name.
     The stream is idle on both sides of each pass. Returns (total_ms,
     per_launch_ms list, warm-up launches)."""
+    with marked(name):
+        return _timed(launch, steps, warmup, warm_ms)
+
+
+def _timed(launch, steps: int, warmup: int, warm_ms: float):
     s = capi.stream()
     launches = 0
     for _ in range(warmup):
@@ -139,7 +175,7 @@ def bench_gemm(name: str, steps: int, warmup: int):
         da, db = nxt()
         capi.gemm(da.ptr, db.ptr, out.ptr, desc, s, ws)
 
-    total, per, warm = timed(launch, steps, warmup)
+    total, per, warm = timed(launch, steps, warmup, name=f"gemm_{name}")
     flops = wl.gemm_flops(name)
     avg = total / steps
     return {"name": f"gemm_{name}", "unit": "TFLOP/s", "value": flops / (avg * 1e-3) / 1e12,
@@ -173,7 +209,7 @@ def api_wall(steps: int, warmup: int) -> dict:
 
 
 def bench_hbm(name: str, launch_for, nbytes: int, steps: int, warmup: int):
-    total, per, warm = timed(launch_for, steps, warmup)
+    total, per, warm = timed(launch_for, steps, warmup, name=name)
     avg = total / steps
     return {"name": name, "unit": "GB/s", "value": nbytes / (avg * 1e-3) / 1e9,
             "kernel_avg_ms": avg, "kernel_median_ms": statistics.median(per),
@@ -347,6 +383,36 @@ def secondary_benches(steps: int, warmup: int, only: str | None, cpu: bool):
                              "layernorm then weight then bias (the affine composite) over [16384, 4096]"))
         del copies, x
 
+    # Rows as wide as a vocabulary: one block per row holds the whole row in
+    # registers and LDS ([512, 128256]), or stages it in LDS ([4096, 32000]).
+    for rows, cols, ops in ((512, 128256, ("softmax", "rmsnorm", "layernorm_affine")), (4096, 32000, ("softmax",))):
+        if not any(want(f"{op}_{rows}x{cols}") for op in ops):
+            continue
+        x, g, b = wl.long_row_inputs(rows, cols)
+        copies = [capi.DeviceArray.from_numpy(x) for _ in range(2)]
+        gd, bd = capi.DeviceArray.from_numpy(g), capi.DeviceArray.from_numpy(b)
+        y = capi.DeviceArray((rows, cols))
+        nbytes = 2 * rows * cols * 4
+        nxt = rotate(copies)
+        shape = f"[{rows}, {cols}]"
+        launches = {
+            "softmax": (lambda s: capi.softmax(nxt().ptr, y.ptr, rows, cols, 1, s), nbytes,
+                        lambda r: oracle.softmax(x[:r], -1, threads=1), f"softmax over the last axis of {shape}"),
+            "rmsnorm": (lambda s: capi.rmsnorm(nxt().ptr, None, y.ptr, rows, cols, 1, 1e-5, s), nbytes,
+                        lambda r: oracle.rmsnorm(x[:r], -1, 1e-5, threads=1), f"rmsnorm over the last axis of {shape}"),
+            "layernorm_affine": (
+                lambda s: capi.layernorm(nxt().ptr, gd.ptr, bd.ptr, y.ptr, rows, cols, 1, 1e-5, s), nbytes + 2 * cols * 4,
+                lambda r: oracle.affine_norm(x[:r], -1, 1e-5, g, b, rms=False, threads=1),
+                f"layernorm then weight then bias (the affine composite) over {shape}"),
+        }
+        for op in ops:
+            if not want(f"{op}_{rows}x{cols}"):
+                continue
+            launch, nb, cpu_rows, what = launches[op]
+            add(bench_hbm(f"{op}_{rows}x{cols}", launch, nb, steps, warmup),
+                lambda cpu_rows=cpu_rows, nb=nb, what=what: cpu_line(cpu_rows, rows, nb, "GB/s", 1e9, what))
+        del copies, x
+
     if want("mlp"):
         x, w1, b1, w2, b2 = wl.mlp_inputs()
         dx, dw1, db1, dw2, db2 = (capi.DeviceArray.from_numpy(v) for v in (x, w1, b1, w2, b2))
@@ -362,7 +428,7 @@ def secondary_benches(steps: int, warmup: int, only: str | None, cpu: bool):
             capi.gemm(h.ptr, dw2.ptr, logits.ptr, d2, s, ws2)
             capi.softmax(logits.ptr, prob.ptr, 4096, 1024, 1, s)
 
-        total, per, warm = timed(mlp, steps, warmup)
+        total, per, warm = timed(mlp, steps, warmup, name="mlp_forward_4096x1024x4096")
         flops = 2 * 2 * 4096 * 4096 * 1024
         avg = total / steps
         add({"name": "mlp_forward_4096x1024x4096", "unit": "TFLOP/s", "value": flops / (avg * 1e-3) / 1e12,
@@ -382,7 +448,8 @@ def secondary_benches(steps: int, warmup: int, only: str | None, cpu: bool):
         for causal in (False, True):
             flops = wl.attention_flops(causal)
             total, per, warm = timed(lambda s, c=causal: capi.flash_attention(
-                dq.ptr, dk.ptr, dv.ptr, o.ptr, bh, seq, seq, d, 1.0 / np.sqrt(d), c, s), steps, warmup)
+                dq.ptr, dk.ptr, dv.ptr, o.ptr, bh, seq, seq, d, 1.0 / np.sqrt(d), c, s), steps, warmup,
+                name=f"attention_fused_{bh}x{seq}x{d}" + ("_causal" if causal else ""))
             avg = total / steps
             # The reference composite computes every score and masks it, so
             # its time does not shrink with the causal mask; the rate counts
@@ -395,6 +462,63 @@ def secondary_benches(steps: int, warmup: int, only: str | None, cpu: bool):
                 lambda c=causal, flops=flops: cpu_line(
                     lambda r: oracle.attention(q[:1, :r], k[:1], v[:1], None, c, None, threads=1), bh * seq, flops,
                     "TFLOP/s", 1e12, "attention composite (transpose, matmul, softmax, matmul) of one head's queries"))
+    return out
+
+
+def extra_benches(steps: int, warmup: int):
+    """Shapes off the bench lines that route to other kernels (rows that are
+    short, unaligned, staged in LDS or resident in registers; the matrix-vector,
+    streaming, vector-matrix, short-K and tiny-item GEMM routes), timed like
+    the secondary lines against HBM (algorithmic bytes: each input read once
+    plus the output), for the kernel traces of the profiles. No CPU legs."""
+    out = []
+    rng = np.random.default_rng(13)
+
+    def operands(*shapes):
+        arrays = [rng.standard_normal(sh, dtype=np.float32) for sh in shapes]
+        nbytes = sum(a.nbytes for a in arrays)
+        sets = [[capi.DeviceArray.from_numpy(a) for a in arrays] for _ in range(copies_for(nbytes))]
+        return rotate(sets), nbytes
+
+    def add(name, launch, nbytes):
+        line = bench_hbm(name, launch, nbytes, steps, warmup)
+        out.append(line)
+        log(f"{name}: {line['achieved']:.0f} GB/s ({line['frac']:.1%})")
+
+    for rows, cols in ((100000, 130), (16384, 1023), (8192, 8191)):
+        nxt, nbytes = operands((rows, cols))
+        res = capi.DeviceArray((rows,), np.float32)
+        for op in ("sum", "max"):
+            add(f"reduce_{op}_f32_{rows}x{cols}", lambda s, op=op, rows=rows, cols=cols, nxt=nxt, res=res: capi.reduce(
+                op, capi.TCX_FLOAT32, nxt()[0].ptr, res.ptr, rows, cols, 1, None, s), nbytes + rows * 4)
+    for rows, cols in ((8192, 8191), (4096, 20001), (1000, 100003)):
+        nxt, nbytes = operands((rows, cols))
+        g = capi.DeviceArray.from_numpy(rng.uniform(0.5, 1.5, cols).astype(np.float32))
+        b = capi.DeviceArray.from_numpy(rng.uniform(-0.1, 0.1, cols).astype(np.float32))
+        y = capi.DeviceArray((rows, cols))
+        add(f"softmax_{rows}x{cols}", lambda s, rows=rows, cols=cols, nxt=nxt, y=y: capi.softmax(
+            nxt()[0].ptr, y.ptr, rows, cols, 1, s), 2 * nbytes)
+        add(f"layernorm_affine_{rows}x{cols}", lambda s, rows=rows, cols=cols, nxt=nxt, y=y, g=g, b=b: capi.layernorm(
+            nxt()[0].ptr, g.ptr, b.ptr, y.ptr, rows, cols, 1, 1e-5, s), 2 * nbytes + 2 * cols * 4)
+    # GEMM routes: (name, m, n, k, batch, B transposed)
+    for name, m, n, k, batch, trans in (("gemv_1x4096x4096_linear", 1, 4096, 4096, 1, True),
+                                        ("stream_16x4096x4096_linear", 16, 4096, 4096, 1, True),
+                                        ("vecmat_16x1x4096x4096", 1, 4096, 4096, 16, False),
+                                        ("smallk_4096x4096x4", 4096, 4096, 4, 1, False),
+                                        ("tiny_65536x8x8x8", 8, 8, 8, 65536, False)):
+        a_shape = (batch, m, k) if batch > 1 else (m, k)
+        b_shape = ((batch,) if batch > 1 else ()) + ((n, k) if trans else (k, n))
+        nxt, nbytes = operands(a_shape, b_shape)
+        desc = capi.gemm_desc(m, n, k, batch_shape=(batch,) if batch > 1 else (),
+                              lhs_batch_strides=(m * k,) if batch > 1 else (),
+                              rhs_batch_strides=(k * n,) if batch > 1 else (), rhs_transposed=trans)
+        c = capi.DeviceArray((batch * m, n))
+        ws = capi.gemm_workspace(desc)
+
+        def launch(s, nxt=nxt, c=c, desc=desc, ws=ws):
+            da, db = nxt()
+            capi.gemm(da.ptr, db.ptr, c.ptr, desc, s, ws)
+        add(f"gemm_{name}", launch, nbytes + batch * m * n * 4)
     return out
 
 
@@ -432,6 +556,8 @@ def main() -> int:
     parser.add_argument("--headline-only", action="store_true")
     parser.add_argument("--no-headline", action="store_true",
                         help="skip the 4096^3 GEMM (profiling runs of the secondary kernels)")
+    parser.add_argument("--extra-shapes", action="store_true",
+                        help="only time the shapes off the bench lines that route to other kernels (profiling)")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run 1 GiB device-to-device copies (PMC byte-counter calibration)")
     args = parser.parse_args()
@@ -459,6 +585,10 @@ def main() -> int:
         log("copy calibration: 3 x 1 GiB device-to-device copies, "
             + ", ".join(f"{2 * (1 << 30) / m / 1e6:.0f} GB/s" for m in ms) + " (read + write)")
         return 0
+    if args.extra_shapes:
+        for r in extra_benches(args.steps, args.warmup):
+            print(json.dumps(r), flush=True)
+        return 0
     if args.no_headline:
         for r in secondary_benches(args.steps, args.warmup, args.only, not args.no_cpu):
             print(json.dumps(r), flush=True)
@@ -466,7 +596,8 @@ def main() -> int:
     headline = bench_gemm("c2_4096", args.steps, args.warmup)
     log(f"gemm 4096^3: {headline['achieved']:.1f} TFLOP/s ({headline['frac']:.1%} of fp32 MFMA peak), "
         f"median launch {headline['kernel_median_ms']:.4f} ms")
-    api = api_wall(args.steps, args.warmup)
+    with marked("api_wall_gemm_c2_4096"):
+        api = api_wall(args.steps, args.warmup)
     log(f"gemm 4096^3 through tensorcx.matmul: {api['ms_per_call_median']:.4f} ms per call (median)")
     secondary = [] if args.headline_only else secondary_benches(args.steps, args.warmup, args.only,
                                                                   not args.no_cpu)

@@ -880,15 +880,17 @@ __global__ __launch_bounds__(kRowBlockThreads) void row_block_kernel(RowArgs a) 
 // arithmetic with its loads, so the first statistics pass takes each float4
 // as it arrives: the LDS chunks (issued first, so landing first), then the
 // register chunks in order. For softmax that pass already takes the
-// exponentials, against the maximum m0 of the thread's first register
-// float4: e = exp(x - m0) in place, and the thread's sum of them. The block
-// maximum M then rescales: denom = sum over threads of sum_t * exp(m0_t - M)
-// in a fixed order, out = e * (exp(m0_t - M) / denom). A thread whose own
-// maximum lies more than kResidentShift above m0 reloads its elements from
-// HBM before any output is written and takes them against its own maximum,
-// so e stays below exp(16) and exp(m0_t - M) keeps the precision of the
-// outputs that matter. A row whose maximum is not finite (a NaN, +inf, or
-// -inf throughout) is NaN throughout, as in the reference.
+// exponentials, against the maximum m0 of the wave's first register float4s
+// (256 elements): e = exp(x - m0) in place, and the thread's sum of them. The
+// block maximum M then rescales: denom = sum over threads of
+// sum_t * exp(m0_t - M) in a fixed order, out = e * (exp(m0_t - M) / denom).
+// A thread whose own maximum lies more than kResidentShift above m0 reloads
+// its elements from HBM before any output is written and takes them against
+// its own maximum, so e stays below exp(32) and exp(m0_t - M) keeps the
+// precision of the outputs that matter; on ordinary data no thread does (one
+// that did stalled its row for several microseconds). A row whose maximum is
+// not finite (a NaN, +inf, or -inf throughout) is NaN throughout, as in the
+// reference.
 //
 // Loads and stores go through buffer resources (one address register for the
 // row, range-checked: float4s past the row read as zero and are not stored).
@@ -896,7 +898,7 @@ __global__ __launch_bounds__(kRowBlockThreads) void row_block_kernel(RowArgs a) 
 // argument) are read as float4 beside each output float4.
 constexpr int kResidentThreads = 512;
 constexpr int kResidentVec = 44;
-constexpr float kResidentShift = 16.0F;
+constexpr float kResidentShift = 32.0F;
 constexpr int kAffGamma = 1, kAffBeta = 2;
 
 
@@ -1028,7 +1030,9 @@ __global__ __launch_bounds__(kResidentThreads) void row_resident_kernel(RowArgs 
     // NaN-propagating maxima (v_maximum3_f32): a NaN anywhere makes M NaN.
     auto vmax = [](float p, float q) { return __builtin_elementwise_maximum(p, q); };
     auto max4 = [&](float m, const float4_t& q) { return vmax(vmax(vmax(vmax(m, q.x), q.y), q.z), q.w); };
-    float m0 = max4(v[0].x, v[0]);  // v[0] is in range: the row has more than 512 float4s
+    // The reference maximum m0 is the wave's over its first float4s (v[0] is
+    // in range: the row has more than 512 float4s).
+    float m0 = wave_max_nan(max4(v[0].x, v[0]));
     float mt = m0, s0 = 0.F, s1 = 0.F;
     // Clamped at -150 (exp 0): -inf elements give exactly 0; a NaN is caught
     // by the maximum instead.

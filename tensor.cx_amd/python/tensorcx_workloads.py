@@ -54,6 +54,16 @@ def rownorm_inputs():
     return x, gamma, beta
 
 
+def long_row_inputs(rows: int = 512, cols: int = 128256):
+    """Rows of a vocabulary-wide axis (128256, the Llama 3 vocabulary): x [512, 128256] ~ N(0,1)*3 seed 10;
+    gamma ~ U(0.5,1.5) seed 11; beta ~ U(-0.1,0.1) seed 12. rows and cols pick another shape of the
+    same draws."""
+    x = (np.random.default_rng(10).standard_normal((rows, cols), dtype=np.float32) * np.float32(3))
+    gamma = np.random.default_rng(11).uniform(0.5, 1.5, cols).astype(np.float32)
+    beta = np.random.default_rng(12).uniform(-0.1, 0.1, cols).astype(np.float32)
+    return x, gamma, beta
+
+
 def mlp_inputs():
     """C5: x [4096,1024] seed 7; W1 [4096,1024], W2 [1024,4096] Kaiming-uniform (gain sqrt 2,
     bound sqrt(6/fan_in)) seeds 8/9; zero biases."""
