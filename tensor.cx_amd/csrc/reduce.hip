@@ -84,7 +84,13 @@ template <typename T, bool kLargest>
 __device__ __forceinline__ bool lane_takes(T v, T best) {
   // Within one lane indices only grow, so ties keep the earlier element.
   if constexpr (sizeof(T) == 4 && __is_same(T, float)) {
-    return is_nan(v) ? !is_nan(best) : (kLargest ? v > best : v < best);
+    // As lane masks, two compares: !(v <= best) holds for v > best and for a
+    // NaN on either side, so it takes a larger or NaN v unless best is
+    // already NaN. (The select form, is_nan(v) ? !is_nan(best) : v > best,
+    // compiled to booleans kept as 0/1 integers: six selects per element;
+    // [8192, 8192] over axis 0 max 53.0 -> 49.7 us.)
+    const bool beats = kLargest ? !(v <= best) : !(v >= best);
+    return beats & !is_nan(best);
   } else {
     return kLargest ? v > best : v < best;
   }
