@@ -7,9 +7,11 @@
 // (row_packed_kernel), rows of up to 1024 elements take one wave per row
 // (kChunks 16-byte loads per lane, wave-wide butterfly statistics); rows of up
 // to 1024 x kMaxSplit elements take one 256-thread block per row (four waves,
-// whose partial statistics meet in LDS). Longer rows use one 1024-thread block
-// per row (row_block_kernel) that stages the row in LDS when it fits there and
-// otherwise reads it once per pass. Strided rows (inner > 1) run
+// whose partial statistics meet in LDS). Longer rows take one 512-thread block
+// per row that holds the whole row in registers, and past about 90 K floats
+// in LDS too (row_resident_kernel, to about 139 K floats); longer ones one
+// 1024-thread block per row that reads it once per pass (row_block_kernel).
+// Strided rows (inner > 1) run
 // col_norm_kernel: column tiles whose waves fold per-column statistics over
 // runs of rows, then write the row from them in a second walk (rows split
 // over blocks, with a workspace, when tiles are few).
@@ -619,12 +621,11 @@ __device__ __forceinline__ float exp_reduced(float d) {
   return fmaf(e, r, e);
 }
 
-// Rows too long for registers: one block per row, passes over the row
-// (softmax: maximum, exponentials and their sum, write; RMSNorm: sum of
-// squares, write; LayerNorm: sum, squared deviations, write). Rows that fit
-// in the block's LDS are read from HBM once (kStaged), longer ones once per
-// pass.
-template <RowOp kOp, bool kStaged>
+// Rows longer than a CU's registers and LDS hold (past about 139 K floats):
+// one block per row, passes over the row read from HBM each time (softmax: a
+// running maximum and rescaled sum, write; RMSNorm: sum of squares, write;
+// LayerNorm: sum, squared deviations, write).
+template <RowOp kOp>
 __global__ __launch_bounds__(kRowBlockThreads) void row_block_kernel(RowArgs a) {
   constexpr int kWaves = kRowBlockThreads / 64;
   __shared__ float scratch[kWaves];
@@ -633,40 +634,7 @@ __global__ __launch_bounds__(kRowBlockThreads) void row_block_kernel(RowArgs a) 
   const std::int64_t n = a.n;
   const float* __restrict__ x = a.x + row * n;
   float* __restrict__ out = a.out + row * n;
-  // kStaged: the first walk copies the row into LDS (dynamic, n + 3 floats),
-  // pad floats in, so that the float4 body block_row_walk reads from x sits
-  // 16-byte aligned in LDS too; later walks read LDS instead of HBM.
-  extern __shared__ float4_t staged4[];
-  float* staged = reinterpret_cast<float*>(staged4);
-  std::int64_t head = static_cast<std::int64_t>(((16U - (reinterpret_cast<std::uintptr_t>(x) & 15U)) & 15U) / 4);
-  if (head > n) head = n;
-  const std::int64_t pad = (4 - head) & 3;
-  auto first_walk = [&](auto&& f4, auto&& f1) {
-    block_row_walk(
-        x, n,
-        [&](const float4_t& v, std::int64_t i) {
-          if constexpr (kStaged) *reinterpret_cast<float4_t*>(staged + pad + i) = v;
-          f4(v, i);
-        },
-        [&](float v, std::int64_t i) {
-          if constexpr (kStaged) staged[pad + i] = v;
-          f1(v, i);
-        });
-    if constexpr (kStaged) __syncthreads();
-  };
-  auto walk = [&](auto&& f4, auto&& f1) {
-    if constexpr (kStaged) {
-      const int t = threadIdx.x;
-      const std::int64_t vectors = (n - head) / 4;
-      const float4_t* body = reinterpret_cast<const float4_t*>(staged + pad + head);
-      for (std::int64_t k = t; k < vectors; k += kRowBlockThreads) f4(body[k], head + 4 * k);
-      if (t < head) f1(staged[pad + t], static_cast<std::int64_t>(t));
-      const std::int64_t tail = head + 4 * vectors;
-      if (t < n - tail) f1(staged[pad + tail + t], tail + t);
-    } else {
-      block_row_walk(x, n, f4, f1);
-    }
-  };
+  auto walk = [&](auto&& f4, auto&& f1) { block_row_walk(x, n, f4, f1); };
   // Writes f(value) for every element of the row, times the weight and plus
   // the bias when present, as float4 at x's float4 offsets (16-byte buffer
   // accesses need only 4-byte alignment in out, gamma and beta).
@@ -722,106 +690,57 @@ __global__ __launch_bounds__(kRowBlockThreads) void row_block_kernel(RowArgs a) 
         });
   };
   if constexpr (kOp == RowOp::kSoftmax) {
-    if constexpr (kStaged) {
-      // The walk over HBM takes only the maximum (NaN-propagating, so a NaN
-      // anywhere makes it NaN), so its loads are not held up behind the
-      // exponentials; the exponentials then go back into LDS in place,
-      // e = exp(x - M), and the write multiplies them by 1 / denom. A row
-      // whose maximum is not finite (a NaN, +inf, or -inf throughout) is NaN
-      // throughout, as in the reference.
-      auto vmax = [](float p, float q) { return __builtin_elementwise_maximum(p, q); };
-      float m = -__builtin_inff();
-      first_walk([&](const float4_t& v, std::int64_t) { m = vmax(vmax(vmax(vmax(m, v.x), v.y), v.z), v.w); },
-                 [&](float v, std::int64_t) { m = vmax(m, v); });
-      m = wave_max_nan(m);
-      __shared__ float wave_m[kWaves];
-      if ((threadIdx.x & 63) == 0) wave_m[threadIdx.x >> 6] = m;
-      __syncthreads();
-      m = wave_m[0];
-      for (int w = 1; w < kWaves; ++w) m = vmax(m, wave_m[w]);
-      if (!__builtin_isfinite(m)) {
-        write_row([](float) { return __builtin_nanf(""); });
-        return;
-      }
-      // Clamped at -150 (exp 0): -inf elements give exactly 0.
-      auto ex = [&](float v) { return exp_reduced(fmaxf(v - m, -150.F)); };
-      float s0 = 0.F, s1 = 0.F;
-      {
-        const int t = threadIdx.x;
-        const std::int64_t vectors = (n - head) / 4;
-        float4_t* body = reinterpret_cast<float4_t*>(staged + pad + head);
-        for (std::int64_t k = t; k < vectors; k += kRowBlockThreads) {
-          const float4_t v = body[k];
-          const float4_t e = {ex(v.x), ex(v.y), ex(v.z), ex(v.w)};
-          body[k] = e;
-          s0 += e.x + e.y;
-          s1 += e.z + e.w;
-        }
-        const std::int64_t tail = head + 4 * vectors;
-        float* ends[2] = {t < head ? staged + pad + t : nullptr, t < n - tail ? staged + pad + tail + t : nullptr};
-        for (float* e : ends)
-          if (e != nullptr) {
-            *e = ex(*e);
-            s0 += *e;
-          }
-      }
-      // One correctly rounded reciprocal per row (each thread reads back
-      // only the LDS slots it wrote).
-      const float inv = 1.0F / block_reduce(s0 + s1, false, scratch);
-      write_row([&](float e) { return e * inv; });
-    } else {
-      // One read pass for the maximum and the sum: each thread keeps (m, s),
-      // s relative to its running maximum m and rescaled when m grows (a sum
-      // begun under m = -inf starts over). A separate maximum pass read every
-      // row three times: [1000, 100000] 284 us at 35 % of HBM.
-      float m = -__builtin_inff(), s = 0.F;
-      auto grow = [&](float top) {
-        if ((is_nan(top) && !is_nan(m)) || top > m) {
-          s = m == -__builtin_inff() ? 0.F : s * exp_softmax(m - top);
-          m = top;
-        }
-      };
-      auto nan_max = [](float p, float q) { return (is_nan(q) || q > p) ? q : p; };
-      first_walk(
-          [&](const float4_t& v, std::int64_t) {
-            grow(nan_max(nan_max(v.x, v.y), nan_max(v.z, v.w)));
-            s += (exp_softmax(v.x - m) + exp_softmax(v.y - m)) + (exp_softmax(v.z - m) + exp_softmax(v.w - m));
-          },
-          [&](float v, std::int64_t) {
-            grow(v);
-            s += exp_softmax(v - m);
-          });
-      // Merge (m, s) over the wave, then the block's waves in order.
-      auto merge = [&](float om, float os) {
-        const float top = nan_max(m, om);
-        if (top == -__builtin_inff()) {
-          s = s + os;
-        } else {
-          const float mine = m == -__builtin_inff() ? 0.F : s * exp_softmax(m - top);
-          const float other = om == -__builtin_inff() ? 0.F : os * exp_softmax(om - top);
-          s = mine + other;
-        }
+    // One read pass for the maximum and the sum: each thread keeps (m, s),
+    // s relative to its running maximum m and rescaled when m grows (a sum
+    // begun under m = -inf starts over). A separate maximum pass read every
+    // row three times: [1000, 100000] 284 us at 35 % of HBM.
+    float m = -__builtin_inff(), s = 0.F;
+    auto grow = [&](float top) {
+      if ((is_nan(top) && !is_nan(m)) || top > m) {
+        s = m == -__builtin_inff() ? 0.F : s * exp_softmax(m - top);
         m = top;
-      };
-#pragma unroll
-      for (int offset = 32; offset > 0; offset >>= 1) merge(__shfl_xor(m, offset, kWave), __shfl_xor(s, offset, kWave));
-      __shared__ float wave_ms[2][kWaves];
-      if ((threadIdx.x & 63) == 0) {
-        wave_ms[0][threadIdx.x >> 6] = m;
-        wave_ms[1][threadIdx.x >> 6] = s;
       }
-      __syncthreads();
-      m = wave_ms[0][0];
-      s = wave_ms[1][0];
-      for (int w = 1; w < kWaves; ++w) merge(wave_ms[0][w], wave_ms[1][w]);
-      // One correctly rounded reciprocal per row; each output is e * (1/denom),
-      // within 1.5 ulp of the reference's e / denom.
-      const float inv = 1.0F / s;
-      write_row([&](float v) { return exp_softmax(v - m) * inv; });
+    };
+    auto nan_max = [](float p, float q) { return (is_nan(q) || q > p) ? q : p; };
+    walk(
+        [&](const float4_t& v, std::int64_t) {
+          grow(nan_max(nan_max(v.x, v.y), nan_max(v.z, v.w)));
+          s += (exp_softmax(v.x - m) + exp_softmax(v.y - m)) + (exp_softmax(v.z - m) + exp_softmax(v.w - m));
+        },
+        [&](float v, std::int64_t) {
+          grow(v);
+          s += exp_softmax(v - m);
+        });
+    // Merge (m, s) over the wave, then the block's waves in order.
+    auto merge = [&](float om, float os) {
+      const float top = nan_max(m, om);
+      if (top == -__builtin_inff()) {
+        s = s + os;
+      } else {
+        const float mine = m == -__builtin_inff() ? 0.F : s * exp_softmax(m - top);
+        const float other = om == -__builtin_inff() ? 0.F : os * exp_softmax(om - top);
+        s = mine + other;
+      }
+      m = top;
+    };
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) merge(__shfl_xor(m, offset, kWave), __shfl_xor(s, offset, kWave));
+    __shared__ float wave_ms[2][kWaves];
+    if ((threadIdx.x & 63) == 0) {
+      wave_ms[0][threadIdx.x >> 6] = m;
+      wave_ms[1][threadIdx.x >> 6] = s;
     }
+    __syncthreads();
+    m = wave_ms[0][0];
+    s = wave_ms[1][0];
+    for (int w = 1; w < kWaves; ++w) merge(wave_ms[0][w], wave_ms[1][w]);
+    // One correctly rounded reciprocal per row; each output is e * (1/denom),
+    // within 1.5 ulp of the reference's e / denom.
+    const float inv = 1.0F / s;
+    write_row([&](float v) { return exp_softmax(v - m) * inv; });
   } else if constexpr (kOp == RowOp::kRms) {
     float s0 = 0.F, s1 = 0.F;
-    first_walk(
+    walk(
         [&](const float4_t& v, std::int64_t) { s0 += v.x * v.x + v.y * v.y; s1 += v.z * v.z + v.w * v.w; },
         [&](float v, std::int64_t) { s0 += v * v; });
     const float ss = block_reduce(s0 + s1, false, scratch);
@@ -832,7 +751,7 @@ __global__ __launch_bounds__(kRowBlockThreads) void row_block_kernel(RowArgs a) 
     const float first = x[0];
     float s0 = 0.F, s1 = 0.F;
     bool equal = true;
-    first_walk(
+    walk(
         [&](const float4_t& v, std::int64_t) {
           s0 += v.x + v.y;
           s1 += v.z + v.w;
@@ -909,9 +828,16 @@ __device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, void* lds, 
                                            kNonTemporal);
 }
 
-template <RowOp kOp, int kAff>
-__global__ __launch_bounds__(kResidentThreads) void row_resident_kernel(RowArgs a) {
-  constexpr int T = kResidentThreads, P = kResidentVec, kWaves = T / 64;
+// Waves per SIMD a block of P float4 per thread leaves room for: rows held in
+// 12 or 20 float4 per thread (at most 24576 or 40960 floats, no LDS) run
+// three or two blocks per CU, so one row's arithmetic overlaps another's
+// loads.
+constexpr int resident_waves_per_eu(int P) { return P <= 12 ? 6 : P <= 20 ? 4 : 2; }
+
+template <RowOp kOp, int kAff, int P>
+__global__ __launch_bounds__(kResidentThreads) __attribute__((amdgpu_waves_per_eu(resident_waves_per_eu(P))))
+void row_resident_kernel(RowArgs a) {
+  constexpr int T = kResidentThreads, kWaves = T / 64;
   constexpr bool kG = (kAff & kAffGamma) != 0, kB = (kAff & kAffBeta) != 0;
   extern __shared__ float4_t rest4[];
   __shared__ float scratch[kWaves];
@@ -1692,15 +1618,17 @@ int run_cols(const RowArgs& r, std::int64_t outer, std::int64_t reduce, std::int
   return check(hipGetLastError(), "strided row write launch");
 }
 
-// Calls f(kernel, affine bits) for each resident-row kernel the op launches.
+// Calls f(kernel, affine bits) for each resident-row kernel of P float4 per
+// thread that the op launches.
 using RowKernel = void (*)(RowArgs);
-template <RowOp kOp, typename F>
+template <RowOp kOp, int P, typename F>
 void resident_variants(F&& f) {
-  f(static_cast<RowKernel>(&row_resident_kernel<kOp, 0>), 0);
-  if constexpr (kOp != RowOp::kSoftmax) f(static_cast<RowKernel>(&row_resident_kernel<kOp, kAffGamma>), kAffGamma);
+  f(static_cast<RowKernel>(&row_resident_kernel<kOp, 0, P>), 0);
+  if constexpr (kOp != RowOp::kSoftmax)
+    f(static_cast<RowKernel>(&row_resident_kernel<kOp, kAffGamma, P>), kAffGamma);
   if constexpr (kOp == RowOp::kLayer) {
-    f(static_cast<RowKernel>(&row_resident_kernel<kOp, kAffBeta>), kAffBeta);
-    f(static_cast<RowKernel>(&row_resident_kernel<kOp, kAffGamma | kAffBeta>), kAffGamma | kAffBeta);
+    f(static_cast<RowKernel>(&row_resident_kernel<kOp, kAffBeta, P>), kAffBeta);
+    f(static_cast<RowKernel>(&row_resident_kernel<kOp, kAffGamma | kAffBeta, P>), kAffGamma | kAffBeta);
   }
 }
 
@@ -1736,8 +1664,10 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
   else if (per <= kMaxSplit) return launch_split<kOp, 16>(a, vec, s);
   else {
     // Rows wider than the register budget (1024 x kMaxSplit floats): one
-    // block per row, the row staged in LDS when it fits the device's
-    // per-block LDS (its static arrays and a margin aside), else re-read.
+    // 512-thread block per row holding the row, in 12 or 20 float4 per thread
+    // of registers (up to 24576 and 40960 floats; three and two blocks per
+    // CU), or 44 plus the rest in LDS within the device's per-block LDS (its
+    // static arrays and a margin aside); longer rows are re-read.
     if (outer > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "too many rows");
     thread_local int lds_limit[64] = {};
     int device = 0;
@@ -1748,31 +1678,32 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
       if (hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, device) != hipSuccess) bytes = 0;
       limit = bytes > 0 ? bytes : -1;
       if (limit > 0) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&row_block_kernel<kOp, true>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, limit - 1024);
-        resident_variants<kOp>([&](RowKernel kernel, int) {
+        resident_variants<kOp, kResidentVec>([&](RowKernel kernel, int) {
           (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                     limit - 1024);
         });
       }
     }
-    const std::int64_t staged_bytes = (reduce + 4) * static_cast<std::int64_t>(sizeof(float));
     // Resident rows: LDS for the float4s past the registers' share, in whole
     // 1 KB DMA instructions (a row has at most reduce / 4 float4s).
     const std::int64_t past_regs = reduce / 4 - static_cast<std::int64_t>(kResidentThreads) * kResidentVec;
     const std::int64_t resident_bytes = past_regs > 0 ? (past_regs + 63) / 64 * 1024 : 0;
-    if (limit > 0 && staged_bytes <= limit - 1024)
-      hipLaunchKernelGGL((row_block_kernel<kOp, true>), dim3(static_cast<unsigned>(outer)), dim3(kRowBlockThreads),
-                         static_cast<unsigned>(staged_bytes), s, a);
-    else if (limit > 0 && resident_bytes <= limit - 1024)
-      resident_variants<kOp>([&](RowKernel kernel, int aff) {
-        if (aff == (a.gamma ? kAffGamma : 0) + (a.beta ? kAffBeta : 0))
-          hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(outer)), dim3(kResidentThreads),
-                             static_cast<unsigned>(resident_bytes), s, a);
+    const int aff = (a.gamma ? kAffGamma : 0) + (a.beta ? kAffBeta : 0);
+    auto launch_resident = [&](auto p, unsigned lds_bytes) {
+      resident_variants<kOp, decltype(p)::value>([&](RowKernel kernel, int k) {
+        if (k == aff)
+          hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(outer)), dim3(kResidentThreads), lds_bytes, s, a);
       });
+    };
+    if (reduce / 4 <= static_cast<std::int64_t>(kResidentThreads) * 12)
+      launch_resident(std::integral_constant<int, 12>{}, 0U);
+    else if (reduce / 4 <= static_cast<std::int64_t>(kResidentThreads) * 20)
+      launch_resident(std::integral_constant<int, 20>{}, 0U);
+    else if (limit > 0 && resident_bytes <= limit - 1024)
+      launch_resident(std::integral_constant<int, kResidentVec>{}, static_cast<unsigned>(resident_bytes));
     else
-      hipLaunchKernelGGL((row_block_kernel<kOp, false>), dim3(static_cast<unsigned>(outer)), dim3(kRowBlockThreads),
-                         0, s, a);
+      hipLaunchKernelGGL((row_block_kernel<kOp>), dim3(static_cast<unsigned>(outer)), dim3(kRowBlockThreads), 0, s,
+                         a);
     return check(hipGetLastError(), "row block kernel launch");
   }
   return check(hipGetLastError(), "row kernel launch");
