@@ -831,8 +831,8 @@ __device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, void* lds, 
 // Waves per SIMD a block of P float4 per thread leaves room for: rows held in
 // 12 or 20 float4 per thread (at most 24576 or 40960 floats, no LDS) run
 // three or two blocks per CU, so one row's arithmetic overlaps another's
-// loads.
-constexpr int resident_waves_per_eu(int P) { return P <= 12 ? 6 : P <= 20 ? 4 : 2; }
+// loads; 4 or 8 (unaligned rows of up to 8192 or 16384 floats) four.
+constexpr int resident_waves_per_eu(int P) { return P <= 8 ? 8 : P <= 12 ? 6 : P <= 20 ? 4 : 2; }
 
 template <RowOp kOp, int kAff, int P>
 __global__ __launch_bounds__(kResidentThreads) __attribute__((amdgpu_waves_per_eu(resident_waves_per_eu(P))))
@@ -1658,7 +1658,29 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
   } else if (chunks <= 1) launch_cached<kOp, 1>(a, vec, s);
   else if (chunks <= 2) launch_cached<kOp, 2>(a, vec, s);
   else if (chunks <= kMaxWaveChunks) launch_cached<kOp, 4>(a, vec, s);
-  else if (per <= 2) return launch_split<kOp, 2>(a, vec, s);
+  else if (!vec && reduce > 3072 && reduce <= 4 * kResidentThreads * 8 &&
+           (reduce > 4096 || (a.gamma == nullptr && a.beta == nullptr))) {
+    // Rows of 3073-16384 floats off 16-byte alignment (an odd length, or a
+    // buffer off 16 bytes): held in registers by row_resident_kernel, whose
+    // float4 body starts at the row's first 16-byte boundary (the split
+    // kernel takes such rows one float per load: [16384, 4097] softmax 176 ->
+    // 91 us). Up to 4096 floats with a weight or bias the split kernel stays:
+    // it keeps them in registers across rows, where this kernel reads them
+    // from L2 for each row ([8192, 3001] LayerNorm 40 against 54 us); so do
+    // rows of up to 3072 (one float4 per thread here: [4096, 2049] RMSNorm
+    // 13.4 against 15.4 us).
+    if (outer > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "too many rows");
+    const int aff = (a.gamma ? kAffGamma : 0) + (a.beta ? kAffBeta : 0);
+    auto launch_resident = [&](auto p) {
+      resident_variants<kOp, decltype(p)::value>([&](RowKernel kernel, int k) {
+        if (k == aff) hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(outer)), dim3(kResidentThreads), 0, s, a);
+      });
+    };
+    if (reduce <= 4 * kResidentThreads * 4)
+      launch_resident(std::integral_constant<int, 4>{});
+    else
+      launch_resident(std::integral_constant<int, 8>{});
+  } else if (per <= 2) return launch_split<kOp, 2>(a, vec, s);
   else if (per <= 4) return launch_split<kOp, 4>(a, vec, s);
   else if (per <= 8) return launch_split<kOp, 8>(a, vec, s);
   else if (per <= kMaxSplit) return launch_split<kOp, 16>(a, vec, s);

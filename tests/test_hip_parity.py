@@ -896,15 +896,17 @@ def test_row_ops_random(cx, shape, axis):
                  oracle.affine_norm(x, axis, 1e-5, g, None, rms=True), 1e-5, 1e-5, "affine rmsnorm")
 
 
-@pytest.mark.parametrize("width", [200, 500, 1024, 2048, 3001, 4096, 8191, 8192, 16383, 16384, 16385, 20003, 24577,
-                                   32000, 40001, 40961, 70000, 90113, 100003, 128256, 130816, 131000])
+@pytest.mark.parametrize("width", [200, 500, 1024, 2048, 3001, 3073, 4095, 4096, 8191, 8192, 16383, 16384, 16385, 20003,
+                                   24577, 32000, 40001, 40961, 70000, 90113, 100003, 128256, 130816, 131000])
 def test_row_ops_special_values_wide_rows(cx, width):
     # Non-finite values in rows of every width class (one-wave cached rows,
-    # split rows at 2, 4, 8 and 16 float4 per thread, unaligned scalar rows,
-    # block-per-row rows held in registers at 12 or 20 float4 per thread (up
-    # to 24576 and 40960 floats), at 44 (up to 90112) and then LDS (up to
-    # 130816), and re-read beyond): a NaN, +inf last, -inf first, a row of
-    # -inf, +inf with -inf, and a row whose squares overflow to inf.
+    # split rows at 2, 4, 8 and 16 float4 per thread, unaligned scalar rows
+    # and unaligned rows of 3073-16384 held at 4 or 8 float4 per thread (the
+    # latter without a weight or bias up to 4096), block-per-row rows held in
+    # registers at 12 or 20 float4 per thread (up to 24576 and 40960 floats),
+    # at 44 (up to 90112) and then LDS (up to 130816), and re-read beyond): a
+    # NaN, +inf last, -inf first, a row of -inf, +inf with -inf, and a row
+    # whose squares overflow to inf.
     rng = np.random.default_rng(23)
     x = rng.standard_normal((7, width)).astype(np.float32)
     x[0, width // 2] = np.nan
