@@ -6,11 +6,12 @@
 // HBM once and written once: rows of up to 128 elements pack several per wave
 // (row_packed_kernel), rows of up to 1024 elements take one wave per row
 // (kChunks 16-byte loads per lane, wave-wide butterfly statistics); rows of up
-// to 1024 x kMaxSplit elements take one 256-thread block per row (four waves,
-// whose partial statistics meet in LDS). Longer rows take one 512-thread block
-// per row that holds the whole row in registers, and past about 90 K floats
-// in LDS too (row_resident_kernel, to about 139 K floats); longer ones one
-// 1024-thread block per row that reads it once per pass (row_block_kernel).
+// to 3072 elements (4096 with an affine weight or bias) take one 256-thread
+// block per row (four waves, whose partial statistics meet in LDS). Longer
+// rows take one 512-thread block per row that holds the whole row in
+// registers, and past about 90 K floats in LDS too (row_resident_kernel, to
+// about 139 K floats); longer ones one 1024-thread block per row that reads it
+// once per pass (row_block_kernel).
 // Strided rows (inner > 1) run
 // col_norm_kernel: column tiles whose waves fold per-column statistics over
 // runs of rows, then write the row from them in a second walk (rows split
@@ -29,7 +30,7 @@ namespace {
 constexpr int kMaxWaveChunks = 4;  // one wave per row up to 1024 floats
 constexpr std::int64_t kPackedMax = 128;      // rows up to this length pack several per wave
 constexpr std::int64_t kPackedBlocks = 4096;  // grid cap of the packed kernel (it strides over rows)
-constexpr int kMaxSplit = 16;      // one block per row up to 256*4*16 floats
+constexpr int kMaxSplit = 4;       // one block per row up to 256*4*4 floats
 
 enum class RowOp { kSoftmax, kRms, kLayer };
 
@@ -354,12 +355,13 @@ __global__ __launch_bounds__(256) void row_packed_kernel(RowArgs a, int L) {
 // t + 256*(4c + q) (scalar rows). Each wave reduces its part with butterflies
 // and the four wave partials meet in LDS, combined in wave order. Blocks are
 // persistent (a few per CU walk the rows, stepping by the grid), which keeps
-// the set of rows in flight, and the HBM pages they touch, small. For kPer <= 4
-// the affine weight and bias of a thread's columns stay in registers across
-// rows; wider rows re-read them (L2-resident) for every row.
+// the set of rows in flight, and the HBM pages they touch, small. The affine
+// weight and bias of a thread's columns stay in registers across rows, and the
+// block's next row loads into a second register set while the current one
+// reduces and stores (global loads stay in flight across the barriers).
 template <RowOp kOp, int kPer, bool kVec, bool kFull>
 __global__ __launch_bounds__(256) void row_split_kernel(RowArgs a) {
-  constexpr bool kAffRegs = kPer <= 4;
+  static_assert(kPer <= kMaxSplit, "two register copies of the row and the affine terms per thread");
   // Statistics exchange, double-buffered by row parity so a wave that runs
   // ahead never overwrites a slot another wave has yet to read.
   __shared__ float red[2][2][4];  // [row parity][statistic][wave]
@@ -383,13 +385,11 @@ __global__ __launch_bounds__(256) void row_split_kernel(RowArgs a) {
       for (int q = 0; q < 4; ++q) dst[q] = (p != nullptr && valid(c, q)) ? p[column(c, q)] : fallback;
     }
   };
-  float g[kAffRegs ? kPer : 1][4], b[kAffRegs ? kPer : 1][4];
-  if constexpr (kAffRegs) {
+  float g[kPer][4], b[kPer][4];
 #pragma unroll
-    for (int c = 0; c < kPer; ++c) {
-      load_affine(a.gamma, c, 1.F, g[c]);
-      load_affine(a.beta, c, 0.F, b[c]);
-    }
+  for (int c = 0; c < kPer; ++c) {
+    load_affine(a.gamma, c, 1.F, g[c]);
+    load_affine(a.beta, c, 0.F, b[c]);
   }
   auto combine = [&](float v, int par, int stat, bool is_max) -> float {
     if (lane == 0) red[par][stat][wave] = v;
@@ -403,10 +403,6 @@ __global__ __launch_bounds__(256) void row_split_kernel(RowArgs a) {
     return r;
   };
 
-  // Rows of up to 4 float4 per thread prefetch the block's next row into a
-  // second register set while the current row reduces and stores (global
-  // loads stay in flight across the barriers). Wider rows load in place.
-  constexpr bool kPrefetch = kPer <= 4;
   auto load_row = [&](std::int64_t row, float (&dst)[kPer][4], float& first) {
     const float* __restrict__ x = a.x + row * n;
 #pragma unroll
@@ -422,19 +418,15 @@ __global__ __launch_bounds__(256) void row_split_kernel(RowArgs a) {
     }
     if constexpr (kOp == RowOp::kLayer) first = x[0];
   };
-  float v[kPer][4], nv[kPrefetch ? kPer : 1][4];
+  float v[kPer][4], nv[kPer][4];
   float first = 0.F, next_first = 0.F;
-  if (kPrefetch && blockIdx.x < a.rows) load_row(blockIdx.x, v, first);
+  if (blockIdx.x < a.rows) load_row(blockIdx.x, v, first);
 
   int par = 0;
   for (std::int64_t row = blockIdx.x; row < a.rows; row += gridDim.x, par ^= 1) {
     float* __restrict__ out = a.out + row * n;
-    if constexpr (kPrefetch) {
-      const std::int64_t next = row + gridDim.x;
-      if (next < a.rows) load_row(next, nv, next_first);
-    } else {
-      load_row(row, v, first);
-    }
+    const std::int64_t next = row + gridDim.x;
+    if (next < a.rows) load_row(next, nv, next_first);
 
     if constexpr (kOp == RowOp::kSoftmax) {
       float m = -__builtin_inff();
@@ -516,20 +508,12 @@ __global__ __launch_bounds__(256) void row_split_kernel(RowArgs a) {
     // Affine steps (multiply then add, each rounded) and the store.
 #pragma unroll
     for (int c = 0; c < kPer; ++c) {
-      float gc[4], bc[4];
-      if constexpr (kAffRegs) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) { gc[q] = g[c][q]; bc[q] = b[c][q]; }
-      } else {
-        if (has_g) load_affine(a.gamma, c, 1.F, gc);
-        if (has_b) load_affine(a.beta, c, 0.F, bc);
-      }
       float r[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         r[q] = v[c][q];
-        if (has_g) r[q] = r[q] * gc[q];
-        if (has_b) r[q] = r[q] + bc[q];
+        if (has_g) r[q] = r[q] * g[c][q];
+        if (has_b) r[q] = r[q] + b[c][q];
       }
       if constexpr (kVec) {
         if (!valid(c, 0)) continue;
@@ -541,13 +525,11 @@ __global__ __launch_bounds__(256) void row_split_kernel(RowArgs a) {
           if (valid(c, q)) out[column(c, q)] = r[q];
       }
     }
-    if constexpr (kPrefetch) {
 #pragma unroll
-      for (int c = 0; c < kPer; ++c)
+    for (int c = 0; c < kPer; ++c)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[c][q] = nv[c][q];
-      first = next_first;
-    }
+      for (int q = 0; q < 4; ++q) v[c][q] = nv[c][q];
+    first = next_first;
     // Keep later rows' loads from being hoisted into this row's live range.
     asm volatile("" ::: "memory");
   }
@@ -831,7 +813,7 @@ __device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, void* lds, 
 // Waves per SIMD a block of P float4 per thread leaves room for: rows held in
 // 12 or 20 float4 per thread (at most 24576 or 40960 floats, no LDS) run
 // three or two blocks per CU, so one row's arithmetic overlaps another's
-// loads; 4 or 8 (unaligned rows of up to 8192 or 16384 floats) four.
+// loads; 4 or 8 (rows of 3073 to 8192 or 16384 floats) four.
 constexpr int resident_waves_per_eu(int P) { return P <= 8 ? 8 : P <= 12 ? 6 : P <= 20 ? 4 : 2; }
 
 template <RowOp kOp, int kAff, int P>
@@ -1499,22 +1481,16 @@ void launch_split_as(const RowArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((row_split_kernel<kOp, kPer, kVec, kFull>), dim3(grid), dim3(256), 0, s, a);
 }
 
-// Scalar (unaligned) rows take the split kernel too, up to kMaxScalarSplit
-// groups of four per thread. At 8 and 16 they keep fewer blocks per CU than
-// aligned rows, yet beat re-reading the row: softmax [16384, 4097] 258 ->
-// 184 us and [8192, 8191] 239 -> 135 us on MI355X.
-constexpr int kMaxScalarSplit = 16;
-
+// Scalar (unaligned) rows take the split kernel too, four floats per group
+// (one float per load).
 template <RowOp kOp, int kPer>
 int launch_split(const RowArgs& a, bool vec, hipStream_t s) {
-  if (vec && a.n == 1024 * kPer) {
+  if (vec && a.n == 1024 * kPer)
     launch_split_as<kOp, kPer, true, true>(a, s);
-  } else if (vec) {
+  else if (vec)
     launch_split_as<kOp, kPer, true, false>(a, s);
-  } else {
-    if constexpr (kPer > kMaxScalarSplit) return fail(TCX_INTERNAL, "unaligned row too wide for the split kernel");
-    else launch_split_as<kOp, kPer, false, false>(a, s);
-  }
+  else
+    launch_split_as<kOp, kPer, false, false>(a, s);
   return check(hipGetLastError(), "row kernel launch");
 }
 
@@ -1658,17 +1634,20 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
   } else if (chunks <= 1) launch_cached<kOp, 1>(a, vec, s);
   else if (chunks <= 2) launch_cached<kOp, 2>(a, vec, s);
   else if (chunks <= kMaxWaveChunks) launch_cached<kOp, 4>(a, vec, s);
-  else if (!vec && reduce > 3072 && reduce <= 4 * kResidentThreads * 8 &&
+  else if (reduce > 3072 && reduce <= 4 * kResidentThreads * 8 &&
            (reduce > 4096 || (a.gamma == nullptr && a.beta == nullptr))) {
-    // Rows of 3073-16384 floats off 16-byte alignment (an odd length, or a
-    // buffer off 16 bytes): held in registers by row_resident_kernel, whose
-    // float4 body starts at the row's first 16-byte boundary (the split
-    // kernel takes such rows one float per load: [16384, 4097] softmax 176 ->
-    // 91 us). Up to 4096 floats with a weight or bias the split kernel stays:
-    // it keeps them in registers across rows, where this kernel reads them
-    // from L2 for each row ([8192, 3001] LayerNorm 40 against 54 us); so do
-    // rows of up to 3072 (one float4 per thread here: [4096, 2049] RMSNorm
-    // 13.4 against 15.4 us).
+    // Rows of 3073-16384 floats: held in registers by row_resident_kernel,
+    // one 512-thread block per row, whose float4 body starts at the row's
+    // first 16-byte boundary. Off 16-byte alignment (an odd length, or a
+    // buffer off 16 bytes) the split kernel takes a row one float per load
+    // ([16384, 4097] softmax 176 -> 91 us); aligned, the single read of the
+    // row still beats the split kernel's per-row phases ([2048, 12288]
+    // softmax 44.4 -> 34.1 us, LayerNorm 49.9 -> 39.0 us; [8192, 8192]
+    // softmax 95.9 -> 90.8 us). Up to 4096 floats with a weight or bias the
+    // split kernel stays: it keeps them in registers across rows, where this
+    // kernel reads them from L2 for each row ([8192, 3001] LayerNorm 40
+    // against 54 us); so do rows of up to 3072 (one float4 per thread here:
+    // [4096, 2049] RMSNorm 13.4 against 15.4 us).
     if (outer > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "too many rows");
     const int aff = (a.gamma ? kAffGamma : 0) + (a.beta ? kAffBeta : 0);
     auto launch_resident = [&](auto p) {
@@ -1681,12 +1660,10 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
     else
       launch_resident(std::integral_constant<int, 8>{});
   } else if (per <= 2) return launch_split<kOp, 2>(a, vec, s);
-  else if (per <= 4) return launch_split<kOp, 4>(a, vec, s);
-  else if (per <= 8) return launch_split<kOp, 8>(a, vec, s);
-  else if (per <= kMaxSplit) return launch_split<kOp, 16>(a, vec, s);
+  else if (per <= kMaxSplit) return launch_split<kOp, kMaxSplit>(a, vec, s);
   else {
-    // Rows wider than the register budget (1024 x kMaxSplit floats): one
-    // 512-thread block per row holding the row, in 12 or 20 float4 per thread
+    // Rows of more than 16384 floats: one 512-thread block per row holding
+    // the row, in 12 or 20 float4 per thread
     // of registers (up to 24576 and 40960 floats; three and two blocks per
     // CU), or 44 plus the rest in LDS within the device's per-block LDS (its
     // static arrays and a margin aside); longer rows are re-read.

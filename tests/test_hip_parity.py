@@ -870,10 +870,11 @@ def test_empty_and_scalar(cx):
 
 
 # ------------------------------------------------------------- row ops
-# Widths cover each row kernel: one wave per row (<= 1024), one block per row
-# with the row in registers (up to 16384 floats: aligned full and masked, and
-# unaligned at 2, 4, 8 and 16 elements per thread per 1024), the re-reading
-# block kernel, and strided rows.
+# Widths cover each row kernel: one wave per row (<= 1024), one 256-thread
+# block per row (up to 3072 floats, 4096 with a weight or bias: aligned full
+# and masked, and unaligned), one 512-thread block per row holding 3073-16384
+# floats in 4 or 8 float4 per thread (aligned and unaligned) and wider rows in
+# 12 or 20, the re-reading block kernel, and strided rows.
 @pytest.mark.parametrize("shape,axis", [((16, 4096), 1), ((5, 300), 1), ((7, 8192), 1), ((3, 20000), -1),
                                         ((3, 7), 0), ((2, 3, 70), 1), ((9, 1), 1), ((4, 1022), 1),
                                         ((4, 1024), 1), ((6, 1501), 1), ((4, 2048), 1), ((3, 3001), 1),
@@ -900,10 +901,10 @@ def test_row_ops_random(cx, shape, axis):
                                    24577, 32000, 40001, 40961, 70000, 90113, 100003, 128256, 130816, 131000])
 def test_row_ops_special_values_wide_rows(cx, width):
     # Non-finite values in rows of every width class (one-wave cached rows,
-    # split rows at 2, 4, 8 and 16 float4 per thread, unaligned scalar rows
-    # and unaligned rows of 3073-16384 held at 4 or 8 float4 per thread (the
-    # latter without a weight or bias up to 4096), block-per-row rows held in
-    # registers at 12 or 20 float4 per thread (up to 24576 and 40960 floats),
+    # split rows at 2 and 4 float4 per thread, aligned and unaligned, rows of
+    # 3073-16384 held at 4 or 8 float4 per thread by a 512-thread block
+    # (without a weight or bias up to 4096), rows held in registers at 12 or
+    # 20 float4 per thread (up to 24576 and 40960 floats),
     # at 44 (up to 90112) and then LDS (up to 130816), and re-read beyond): a
     # NaN, +inf last, -inf first, a row of -inf, +inf with -inf, and a row
     # whose squares overflow to inf.
@@ -963,7 +964,7 @@ def test_row_ops_special_values_wide_rows(cx, width):
 
 
 @pytest.mark.parametrize("eps", [0.0, 1e-45, 1e-5, 1e30])
-@pytest.mark.parametrize("width", [512, 4096, 3001, 20003, 32000, 100003])
+@pytest.mark.parametrize("width", [512, 4096, 3001, 8192, 16384, 20003, 32000, 100003])
 def test_constant_rows(cx, eps, width):
     x = np.full((5, width), 2.5, np.float32)
     x[3] = -7.0
