@@ -42,7 +42,8 @@ struct FlashArgs {
   std::int64_t qtiles, batch;  // work items: qtiles query tiles of each batch matrix
   float scale;
   int causal;
-  int xcd_blocks;  // group the blocks of one batch matrix on one XCD
+  int xcd_blocks;   // group the blocks of one batch matrix on one XCD
+  int heavy_first;  // causal: more blocks than fit at once, heaviest first
 };
 
 using float2_t = float __attribute__((ext_vector_type(2)));
@@ -505,12 +506,15 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 
   }
   if constexpr (kCausal) {
     // Under causal masking the last query tiles see the most keys. Work items
-    // are ranked by their key-tile count; the first half of the grid takes
-    // them heaviest first and the second half lightest first, so the two
-    // blocks that share a CU (launch ids L and L + n/2) carry about the same
-    // total work.
+    // are ranked by their key-tile count. When every block fits on the device
+    // at once, the first half of the grid takes them heaviest first and the
+    // second half lightest first, so the two blocks that share a CU (launch
+    // ids L and L + n/2) carry about the same total work. With more blocks
+    // than fit, the grid runs heaviest first throughout, so that the light
+    // items fill the CUs the heavy ones leave (longest job first: 16 x 4096 x
+    // 128 720 -> 658 us, 48 x 2048 x 128 536 -> 482 us on MI355X).
     const std::int64_t half = (n + 1) / 2;
-    const std::int64_t rank = id < half ? id : n - 1 - (id - half);
+    const std::int64_t rank = a.heavy_first || id < half ? id : n - 1 - (id - half);
     qtile = a.qtiles - 1 - rank / a.batch;
     batch = rank % a.batch;
   }
@@ -535,6 +539,21 @@ int launch_flash(FlashArgs a, std::int64_t batch, hipStream_t s) {
   const std::int64_t blocks = a.qtiles * batch;
   // Causal blocks keep their heavy/light order instead.
   a.xcd_blocks = !kCausal && blocks % 8 == 0 ? 1 : 0;
+  if constexpr (kCausal) {
+    thread_local int slots = 0;
+    if (slots == 0) {
+      int per_cu = 0, cus = 0, device = 0;
+      (void)hipGetDevice(&device);
+      if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus < 1)
+        cus = 256;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, flash_attention_kernel<D, kWaves, kKeys, kCausal>,
+                                                        64 * kWaves, 0) != hipSuccess ||
+          per_cu < 1)
+        per_cu = 2;
+      slots = per_cu * cus;
+    }
+    a.heavy_first = blocks > slots ? 1 : 0;
+  }
   hipLaunchKernelGGL((flash_attention_kernel<D, kWaves, kKeys, kCausal>), dim3(static_cast<unsigned>(blocks)),
                      dim3(64 * kWaves), 0, s, a);
   return check(hipGetLastError(), "flash attention launch");
@@ -564,7 +583,7 @@ int tcx_hip_flash_attention_f32(const float* q, const float* k, const float* v, 
     if (p != nullptr && (reinterpret_cast<std::uintptr_t>(p) & 15U) != 0)
       return fail(TCX_INVALID_ARGUMENT, "fused attention buffers must be 16-byte aligned");
   if (int rc = ready(); rc != TCX_OK) return rc;
-  const FlashArgs a{q, k, v, out, rows, cols, 0, 0, scale, causal != 0, 0};
+  const FlashArgs a{q, k, v, out, rows, cols, 0, 0, scale, causal != 0, 0, 0};
   const auto s = static_cast<hipStream_t>(stream);
   // Tile shapes measured on MI355X at 2048 x 2048. Unmasked: 8 waves and
   // 64-key tiles for D = 128 and 64 (one block per CU at D = 128: 110 against

@@ -433,8 +433,10 @@ def test_fused_attention_special_values(cx, d):
 
 
 # Causal shapes with 256 or more batch matrices: at least two query tiles per
-# CU, in the heavy/light block order, with partial last tiles, key lengths
-# other than the query length and empty keys.
+# CU, more blocks than fit on the device at once (heaviest first: 130 rows
+# and more at D = 128, two blocks per CU) or all resident (the heavy/light
+# block order: 64 rows, one query tile per matrix), with
+# partial last tiles, key lengths other than the query length and empty keys.
 @pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("rows,cols", [(64, 64), (130, 130), (257, 200), (200, 257), (300, 37), (65, 0)])
 def test_fused_attention_causal_many_tiles(cx, d, rows, cols):
