@@ -392,7 +392,12 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
   // Up to three rounds of 64x64 tiles: the direct-to-LDS 64x64 kernel, edge
   // tiles included (1000^3: 30.0 -> 28.5 us, transposed 31.2 -> 28.1 us,
   // 768^3 23.4 -> 22.6 us). With more rounds the register-staged kernel
-  // measured as fast or faster (3000x3000x1000: 203 against 212 us).
+  // measured as fast or faster (3000x3000x1000: 203 against 212 us). When a
+  // last round of at most 128 tiles follows full ones, 32x64 tiles (two
+  // blocks per CU) run that round as lone half tiles: 1100^3 48.0 -> 39.1 us,
+  // 1200^3 50.2 -> 40.8, 1600^3 92.4 -> 82.0, 4 x 500x600x700 34.2 -> 27.6 us;
+  // with a fuller last round, or one round, 64x64 tiles stay ahead by 2-6 %
+  // (1280^3, 1400^3, 1700^3; 1000^3 23.5 against 24.6 us).
   if (vec && tiles_64 <= 768 && gemm::direct64_fits(d->m, d->n, d->k)) {
     // Skinny shapes whose 64x64 tiles are mostly padding run the small
     // kernel's 32x32 tiles when those waste at most two thirds as much
@@ -400,7 +405,8 @@ extern "C" int tcx_hip_gemm_f32_ws(const float* lhs, const float* rhs, float* ou
     // stays on 64x64 tiles, 24.2 against 33.8 us).
     const std::int64_t tiles_32 = ((d->m + 31) / 32) * ((d->n + 31) / 32) * batches;
     if (8 * tiles_64 > 3 * tiles_32 && gemm::small_fits(d->m, d->n, d->k)) return gemm::launch_small(args, trans_b, s);
-    return gemm::launch_direct64(args, trans_b, s);
+    const std::int64_t last = tiles_64 % 256;
+    return gemm::launch_direct64(args, trans_b, tiles_64 > 256 && last > 0 && last <= 128, s);
   }
   return launch_config<64, 64, 16, 32, 32, 4, false, 4>(args, trans_b, vec, s);
 }

@@ -732,12 +732,17 @@ int launch_direct(GemmArgs& args, bool trans_b, hipStream_t stream) {
   return check(hipGetLastError(), "gemm_f32 split reduce launch");
 }
 
-// Direct-to-LDS GEMM for 64x64 output tiles of any shape (edge tiles
-// included): 16 waves in four K groups of four 32x32 waves, each group taking
-// 16 of every 64 staged k (its partial tile is added in group order at the
-// end, as in gemm_f32_kernel with KS = 4). Tiles go from HBM to LDS with
-// buffer_load ... lds through four stages, two k-tiles between barriers,
-// two 16-byte instructions per wave and stage.
+// Direct-to-LDS GEMM for BM x 64 output tiles of any shape (edge tiles
+// included), BM = 64 or 32: BM / 4 waves in four K groups of BM / 16 32x32
+// waves, each group taking 16 of every 64 staged k (its partial tile is added
+// in group order at the end, as in gemm_f32_kernel with KS = 4). Tiles go from
+// HBM to LDS with buffer_load ... lds. 64x64 tiles: 16 waves, four stages
+// (128 KB, one block per CU), two k-tiles between barriers, two 16-byte
+// instructions per wave and stage. 32x64 tiles: 8 waves, three stages (72 KB,
+// two blocks per CU), one k-tile per barrier with two in flight, three
+// instructions per wave and stage. The half-height tiles serve launches whose
+// last round of 64x64 tiles would be mostly empty: the blocks of that round
+// then run half the work each, alone on their CUs.
 //   Edges: each operand panel is read through a buffer resource whose
 //   num_records ends at the matrix, so rows past M (and past N for a
 //   transposed B) read as zero through the VGPR offset alone. Lanes whose k
@@ -746,7 +751,8 @@ int launch_direct(GemmArgs& args, bool trans_b, hipStream_t stream) {
 //   out-of-range VGPR offset and read zero too: a value past K, which may be
 //   infinite (the next batch's B rows, say), never meets the zero of the
 //   other operand, and no load leaves the operand's own rows.
-//   LDS layouts (conflict-free reads): A (and a transposed B) [64 rows][64 k]
+//   LDS layouts (conflict-free reads): A [BM rows][64 k] (a transposed B
+//   [64 rows][64 k])
 //   with the 16-byte chunk c of row r at c ^ (r & 15); a [k, n] B
 //   [64 k][64 n] with chunk c of k row kr at c ^ (8 ((kr >> 2) & 1)), which
 //   puts the two k rows one 32-lane read pass takes in opposite halves of
@@ -754,14 +760,18 @@ int launch_direct(GemmArgs& args, bool trans_b, hipStream_t stream) {
 //   Output column of MFMA column r in block j: 32 wn + 2r + j for a [k, n] B
 //   (a lane's two columns are adjacent, one 8-byte read per k), 32 wn + 16j +
 //   r for a transposed B.
-template <bool kTransB>
-__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8))) void gemm_f32_direct64_kernel(
+template <bool kTransB, int BM>
+__global__ __launch_bounds__(16 * BM) __attribute__((amdgpu_waves_per_eu(4, 8))) void gemm_f32_direct64_kernel(
     GemmArgs a) {
-  constexpr int BM = 64, BN = 64, KS = 4, BKT = 64, kStages = 4;
-  constexpr int kGroupWaves = 4;
-  constexpr std::int64_t kGroupM = 8;
-  __shared__ float As[kStages][BM][BKT];
-  __shared__ float Bs[kStages][64][64];  // [n][k] transposed, [k][n] otherwise
+  static_assert(BM == 64 || BM == 32);
+  constexpr int BN = 64, KS = 4, BKT = 64, kStages = BM == 64 ? 4 : 3;
+  constexpr int kWaves = BM / 4, kGroupWaves = kWaves / KS;
+  constexpr int kBInst = 64 / (4 * kWaves);  // B instructions per wave and stage
+  constexpr std::int64_t kGroupM = 512 / BM;  // tile rows per group: 512 rows of A
+  // One array, so that the group reduction can span both operands' stages.
+  __shared__ float smem[kStages * (BM + 64) * BKT];
+  auto As = reinterpret_cast<float (*)[BM][BKT]>(smem);
+  auto Bs = reinterpret_cast<float (*)[64][64]>(smem + kStages * BM * BKT);  // [n][k] transposed, [k][n] otherwise
 
   const std::int64_t grid = a.total_tiles;
   const std::int64_t bid = blockIdx.x;
@@ -807,13 +817,21 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8))) vo
   // checks that every panel spans less than 2^31 bytes.
   const int4v a_rsrc = rsrc_of(A + m0 * K, (M - m0) * K * 4);
   const int4v b_rsrc = kTransB ? rsrc_of(B + n0 * K, (N - n0) * K * 4) : rsrc_of(B + n0, (K * N - n0) * 4);
-  // Instruction of wave w: rows 4w .. 4w + 3 of the stage's A tile and of its
-  // B tile; lane i fills chunk slot i % 16 of row 4w + i / 16.
+  // Instruction of wave w: rows 4w .. 4w + 3 of the stage's A tile and rows
+  // 4 kWaves h + 4w .. + 3 of its B tile (h < kBInst); lane i fills chunk slot
+  // i % 16 of row 4w + i / 16 (+ 4 kWaves h). The chunk swizzles read the
+  // row's low five bits, which 4 kWaves h (0 or 32) leaves alone, so a lane's
+  // B rows share one chunk.
   const int row = 4 * wave + lane / 16, slot = lane % 16;
   const int a_chunk = slot ^ (row & 15);
   const int a_voff = (row * static_cast<int>(K) + 4 * a_chunk) * 4;
   const int b_chunk = kTransB ? a_chunk : slot ^ (8 * ((row >> 2) & 1));
-  const int b_voff = kTransB ? a_voff : (row * static_cast<int>(N) + 4 * b_chunk) * 4;
+  int b_voff[kBInst];
+#pragma unroll
+  for (int h = 0; h < kBInst; ++h) {
+    const int b_row = 4 * kWaves * h + row;
+    b_voff[h] = (b_row * static_cast<int>(kTransB ? K : N) + 4 * b_chunk) * 4;
+  }
   auto lds_of = [](const void* p) {
     return static_cast<unsigned>(reinterpret_cast<std::uintptr_t>((__attribute__((address_space(3))) const void*)p));
   };
@@ -830,16 +848,20 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8))) vo
     const unsigned row_byte = static_cast<unsigned>(4 * wave * 64 * 4);
     const bool a_in = k0 + 4 * a_chunk < K;
     dma16(a_rsrc, lds_of(&As[stage][0][0]) + row_byte, a_in ? a_voff : kOut, __builtin_amdgcn_readfirstlane(k0 * 4));
-    if constexpr (kTransB) {
-      dma16(b_rsrc, lds_of(&Bs[stage][0][0]) + row_byte, a_in ? b_voff : kOut,
-            __builtin_amdgcn_readfirstlane(k0 * 4));
-    } else {
-      // k rows past K and column chunks past N take the out-of-range offset
-      // on the VGPR side alone, so the zero fill does not depend on whether
-      // the range check counts the SGPR offset.
-      const bool b_in = k0 + row < K && n0 + 4 * b_chunk < N;
-      dma16(b_rsrc, lds_of(&Bs[stage][0][0]) + row_byte, b_in ? b_voff : kOut,
-            __builtin_amdgcn_readfirstlane(k0 * static_cast<int>(N) * 4));
+#pragma unroll
+    for (int h = 0; h < kBInst; ++h) {
+      const unsigned b_byte = row_byte + static_cast<unsigned>(4 * kWaves * h * 64 * 4);
+      if constexpr (kTransB) {
+        dma16(b_rsrc, lds_of(&Bs[stage][0][0]) + b_byte, a_in ? b_voff[h] : kOut,
+              __builtin_amdgcn_readfirstlane(k0 * 4));
+      } else {
+        // k rows past K and column chunks past N take the out-of-range
+        // offset on the VGPR side alone, so the zero fill does not depend on
+        // whether the range check counts the SGPR offset.
+        const bool b_in = k0 + 4 * kWaves * h + row < K && n0 + 4 * b_chunk < N;
+        dma16(b_rsrc, lds_of(&Bs[stage][0][0]) + b_byte, b_in ? b_voff[h] : kOut,
+              __builtin_amdgcn_readfirstlane(k0 * static_cast<int>(N) * 4));
+      }
     }
   };
 
@@ -898,13 +920,27 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8))) vo
     mma(f);
   };
 
+  const int k_tiles = static_cast<int>((K + BKT - 1) / BKT);
+  if constexpr (BM == 32) {
+    // One k-tile per barrier over three stages, two tiles in flight: the
+    // barrier of tile kt frees the stage of tile kt - 1 for tile kt + 2. The
+    // other block on the CU covers this block's barrier waits.
+    issue(0, 0);
+    if (k_tiles > 1) issue(1, BKT);
+    for (int kt = 0; kt < k_tiles; ++kt) {
+      if (kt + 1 < k_tiles) __builtin_amdgcn_s_waitcnt(0x0F70 | (kBInst + 1));  // tile kt + 1 may still be out
+      else __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (kt + 2 < k_tiles) issue((kt + 2) % kStages, (kt + 2) * BKT);
+      compute(kt % kStages);
+    }
+  } else {
   // Two k-tiles per barrier over four stages: tiles kt and kt + 1 are read
   // between two barriers while tiles kt + 2 and kt + 3 land in the stages of
   // kt - 2 and kt - 1, free since the last barrier. Each wave runs 32 MFMAs
   // between barriers and a load has two tiles' MFMAs to land (one tile per
   // barrier, three tiles ahead, measured 26.0 against 24.0 us at 1000^3).
   // Each wave has two loads per tile in flight.
-  const int k_tiles = static_cast<int>((K + BKT - 1) / BKT);
   for (int p = 0; p < kStages && p < k_tiles; ++p) issue(p, p * BKT);
   int kt0 = 0;
   if (k_tiles >= 4) {
@@ -943,14 +979,16 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 8))) vo
     __builtin_amdgcn_s_waitcnt(0);  // tiles kt + 2 and kt + 3 have landed
     __syncthreads();
   }
+  }
+  if constexpr (BM == 32) __syncthreads();  // every wave is done with the stages
 
   // Every group passes its partial tile through LDS (the stages are free
   // after the last barrier); group g then adds the four partials of rows
   // 16 g .. 16 g + 15 of its tile in group order (the sum order of an
   // unsplit k loop over the groups' ranges, the same bits whichever group
   // adds) and stores them, so the adds and stores are spread over all
-  // sixteen waves.
-  float* red = &As[0][0][0];  // KS x 4 waves x 64 lanes x 16 floats = 64 KB
+  // waves.
+  float* red = smem;  // KS x kGroupWaves waves x 64 lanes x 16 floats: 64 or 32 KB
   auto red_at = [&](int g, int w, int i, int j, int q, int ln) {
     return red + ((((g * kGroupWaves + w) * 16 + (i * 2 + j) * 4 + q) * 64) + ln);
   };
@@ -998,19 +1036,25 @@ inline bool direct64_fits(std::int64_t m, std::int64_t n, std::int64_t k) {
          rows_n * k * 4 < kLimit && (static_cast<double>(k) + 64) * n * 4 < kLimit;
 }
 
-inline int launch_direct64(GemmArgs& args, bool trans_b, hipStream_t stream) {
+// half: 32x64 tiles instead of 64x64.
+inline int launch_direct64(GemmArgs& args, bool trans_b, bool half, hipStream_t stream) {
   if (!direct64_fits(args.m, args.n, args.k))
     return fail(TCX_INTERNAL, "direct 64x64 gemm needs 16-byte rows and 31-bit panel offsets");
-  args.tiles_m = (args.m + 63) / 64;
+  const int bm = half ? 32 : 64;
+  args.tiles_m = (args.m + bm - 1) / bm;
   args.tiles_n = (args.n + 63) / 64;
   args.total_tiles = args.tiles_m * args.tiles_n * args.total_tiles;  // caller passes the batch count
   if (args.total_tiles > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
-  const dim3 grid(static_cast<unsigned>(args.total_tiles)), block(1024);
-  if (trans_b)
-    hipLaunchKernelGGL((gemm_f32_direct64_kernel<true>), grid, block, 0, stream, args);
+  const dim3 grid(static_cast<unsigned>(args.total_tiles)), block(16 * bm);
+  if (half && trans_b)
+    hipLaunchKernelGGL((gemm_f32_direct64_kernel<true, 32>), grid, block, 0, stream, args);
+  else if (half)
+    hipLaunchKernelGGL((gemm_f32_direct64_kernel<false, 32>), grid, block, 0, stream, args);
+  else if (trans_b)
+    hipLaunchKernelGGL((gemm_f32_direct64_kernel<true, 64>), grid, block, 0, stream, args);
   else
-    hipLaunchKernelGGL((gemm_f32_direct64_kernel<false>), grid, block, 0, stream, args);
-  return check(hipGetLastError(), "gemm_f32 direct 64x64 launch");
+    hipLaunchKernelGGL((gemm_f32_direct64_kernel<false, 64>), grid, block, 0, stream, args);
+  return check(hipGetLastError(), "gemm_f32 direct 64-column tile launch");
 }
 
 // Small GEMMs (fewer than 128 output tiles of 64x64): one 32x32 output tile

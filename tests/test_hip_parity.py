@@ -64,15 +64,18 @@ def test_matmul_shapes(cx, m, k, n):
         assert_matmul(actual, expected, a, b, f"{m}x{k}x{n}")
 
 
-def test_matmul_direct64_k_tail_isolation(cx):
-    # 64x64 direct-to-LDS tiles with a K tail (1000 = 15 x 64 + 40): an
-    # infinity at the start of the next row, which the tail of a row's last
-    # k-tile would read, must not reach that row (it is zeroed, not 0 * inf).
+@pytest.mark.parametrize("size", [1000, 1100])
+def test_matmul_direct64_k_tail_isolation(cx, size):
+    # Direct-to-LDS tiles with a K tail: 1000 = 15 x 64 + 40 (256 tiles of
+    # 64x64) and 1100 = 17 x 64 + 12 (324 tiles of 64x64, whose last round of
+    # 68 runs the 32x64 tiles). An infinity at the start of the next row,
+    # which the tail of a row's last k-tile would read, must not reach that
+    # row (it is zeroed, not 0 * inf).
     rng = np.random.default_rng(14)
-    a = rng.standard_normal((1000, 1000)).astype(np.float32)
-    b = rng.standard_normal((1000, 1000)).astype(np.float32)
-    a[5, 0] = np.inf        # row 4's tail reads a[5, 0..23] past its K
-    a[9, 999] = -np.inf     # row 9 itself: -inf times its B row
+    a = rng.standard_normal((size, size)).astype(np.float32)
+    b = rng.standard_normal((size, size)).astype(np.float32)
+    a[5, 0] = np.inf           # row 4's tail reads a[5, 0..] past its K
+    a[9, size - 1] = -np.inf   # row 9 itself: -inf times its B row
     actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
     with np.errstate(invalid="ignore"):
         truth = a.astype(np.float64) @ b.astype(np.float64)
@@ -80,30 +83,36 @@ def test_matmul_direct64_k_tail_isolation(cx):
     bad = [5, 9]
     assert np.array_equal(np.isinf(actual[bad]), np.isinf(truth[bad]))
     assert np.array_equal(np.isnan(actual[bad]), np.isnan(truth[bad]))
-    keep = np.setdiff1d(np.arange(1000), bad)
+    keep = np.setdiff1d(np.arange(size), bad)
     assert_matmul(actual[keep], truth[keep], a[keep], b, "direct64 finite rows")
     # Transposed B (a linear's weight): the weight row after a column's row.
-    w = rng.standard_normal((1000, 1000)).astype(np.float32)
+    w = rng.standard_normal((size, size)).astype(np.float32)
     w[7, 0] = np.inf
-    lin = cx.linear(cx.tensor(a[keep[:512]], device="hip"), cx.tensor(w, device="hip")).numpy()
+    lin = cx.linear(cx.tensor(a[keep], device="hip"), cx.tensor(w, device="hip")).numpy()
     with np.errstate(invalid="ignore"):
-        lt = a[keep[:512]].astype(np.float64) @ w.astype(np.float64).T
+        lt = a[keep].astype(np.float64) @ w.astype(np.float64).T
     assert np.all(np.isfinite(lin[:, 6])) and np.array_equal(np.isinf(lin[:, 7]), np.isinf(lt[:, 7]))
+    others = np.setdiff1d(np.arange(size), [7])
+    assert_matmul(lin[:, others], lt[:, others], a[keep], w[others].T, "direct64 linear finite columns")
 
 
-def test_matmul_direct64_kn_b_k_tail_isolation(cx):
+@pytest.mark.parametrize("batches", [2, 4])
+def test_matmul_direct64_kn_b_k_tail_isolation(cx, batches):
     # A [k, n] B with K = 700 = 10 x 64 + 60: batch 0's last k-tile spans
     # k rows 640..703, and rows 700..703 of that span are batch 1's B rows
     # 0..3. Infinities there must read as zero for batch 0 (not 0 * inf), and
-    # still reach batch 1's outputs as the reference's sums give them.
+    # still reach batch 1's outputs as the reference's sums give them. Two
+    # batches make 160 tiles of 64x64; four make 320, whose last round of 64
+    # runs the 32x64 tiles.
     rng = np.random.default_rng(16)
-    a = rng.standard_normal((2, 500, 700)).astype(np.float32)
-    b = rng.standard_normal((2, 700, 600)).astype(np.float32)
+    a = rng.standard_normal((batches, 500, 700)).astype(np.float32)
+    b = rng.standard_normal((batches, 700, 600)).astype(np.float32)
     b[1, 0:4, :] = np.inf
     b[1, 2, 5] = -np.inf
     actual = cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy()
-    assert np.all(np.isfinite(actual[0]))
-    assert_matmul(actual[0], a[0].astype(np.float64) @ b[0].astype(np.float64), a[0], b[0], "batch 0")
+    for i in [0] + list(range(2, batches)):
+        assert np.all(np.isfinite(actual[i]))
+        assert_matmul(actual[i], a[i].astype(np.float64) @ b[i].astype(np.float64), a[i], b[i], f"batch {i}")
     with np.errstate(invalid="ignore"):
         truth = a[1].astype(np.float64) @ b[1].astype(np.float64)
     assert np.array_equal(np.isnan(actual[1]), np.isnan(truth))
@@ -112,12 +121,16 @@ def test_matmul_direct64_kn_b_k_tail_isolation(cx):
 
 @pytest.mark.parametrize("sa,sb", [((4, 500, 700), (4, 700, 600)), ((3, 1000, 1000), (1000, 1000)),
                                    ((8192, 1000), (1000, 4)), ((4, 1000), (1000, 8192)),
-                                   ((999, 1001), (1001, 1003))])
+                                   ((999, 1001), (1001, 1003)), ((1200, 1204), (1204, 1196)),
+                                   ((1599, 1600), (1600, 1596)), ((2, 700, 1100), (2, 1100, 1012))])
 def test_matmul_direct64_batched(cx, sa, sb):
     # Batched 64x64-tile shapes, skinny shapes (a 4-wide n runs the
     # streaming kernel, a 4-wide m with a [k, n] B the small kernel's 32x32
-    # tiles, all but 4 rows of each tile past the edge), and an unaligned k
-    # (1001) that takes the register-staged 64x64 tile instead.
+    # tiles, all but 4 rows of each tile past the edge), an unaligned k
+    # (1001) that takes the register-staged 64x64 tile instead, and shapes
+    # whose last round of 64x64 tiles holds at most 128 (4 x 500x600: 320
+    # tiles; 1200 x 1196: 361; 1599 x 1596: 625, three rounds; 2 x 700 x
+    # 1012: 352), which run 32x64 tiles with edges in m, n and k.
     rng = np.random.default_rng(15)
     a = rng.standard_normal(sa).astype(np.float32)
     b = rng.standard_normal(sb).astype(np.float32)
