@@ -1386,6 +1386,155 @@ __global__ __launch_bounds__(64 * KS) void gemm_f32_stream_kernel(GemmArgs a) {
   }
 }
 
+// Streaming GEMM for the decode-time linear out = X W^T (X: J <= 16 kMB rows
+// of A, W: the transposed B, I rows), with both operands staged in LDS. The
+// operand layout of gemm_f32_stream_kernel makes every load instruction
+// touch 16 rows of 64 B; here each wave moves 64-k spans of its 16 W rows and
+// of X into its own LDS stage by DMA (buffer_load ... lds), four rows x 256 B
+// per instruction, and reads the MFMA operands back with ds_read_b128. Lane
+// i of instruction u fills slot i % 16 of row 4u + i / 16, which holds the
+// row's 16-byte chunk slot ^ row, so the operand reads (chunk 4c + kl of row
+// r, at slot (4c + kl) ^ r) are conflict-free. Three stages per wave, two
+// spans in flight, no barrier in the loop: a wave reads only what its own
+// loads wrote, after its own vmcnt wait. Lane (r, kl) takes k = 64s + 16c +
+// 4kl + q at MFMA step (c, q), as gemm_f32_stream_kernel does; chunks of even
+// and odd c accumulate separately (two dependence chains) and are added at
+// the end. KS waves split the spans into contiguous runs and meet in LDS, in
+// wave order. Rows of W past I, rows of X past J and k past K read zero.
+// Against gemm_f32_stream_kernel on MI355X: 16x4096x4096 20.8 -> 16.2 us,
+// 32x4096x4096 28.5 -> 19.3, 16x14336x4096 66.2 -> 54.4, 32x11008x4096
+// 76.1 -> 54.0, 24x2048x2048 13.7 -> 10.7.
+template <int kMB, int KS>
+__global__ __launch_bounds__(64 * KS) void gemm_f32_stream_lds_kernel(GemmArgs a) {
+  constexpr int kStages = 3, kSpan = 64, kTile = 16 * kSpan;
+  constexpr int kPer = (1 + kMB) * kTile;  // floats of one stage: W, then kMB row groups of X
+  __shared__ float lds[KS * kStages * kPer];
+  const std::int64_t M = a.m, N = a.n, K = a.k;
+  const std::int64_t I = N, J = M;
+  const std::int64_t i_blocks = (I + 15) / 16;
+  const std::int64_t bid = blockIdx.x;
+  const std::int64_t batch = bid / i_blocks, i0 = (bid % i_blocks) * 16;
+  std::int64_t lhs_off = 0, rhs_off = 0;
+  {
+    std::int64_t b = batch;
+    for (int ax = a.batch_rank - 1; ax >= 0; --ax) {
+      const std::int64_t e = a.batch_shape[ax];
+      const std::int64_t c = b % e;
+      b /= e;
+      lhs_off += c * a.lhs_bs[ax];
+      rhs_off += c * a.rhs_bs[ax];
+    }
+  }
+  const float* const W = a.rhs + rhs_off;
+  const float* const X = a.lhs + lhs_off;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, kl = lane >> 4;
+  using int4v = int __attribute__((ext_vector_type(4)));
+  auto rsrc_of = [](const float* base, std::int64_t bytes) {
+    const auto addr = reinterpret_cast<std::uint64_t>(base);
+    return int4v{static_cast<int>(addr), static_cast<int>(addr >> 32), static_cast<int>(bytes), 0x00020000};
+  };
+  // The launcher checks that 32 rows of K floats span less than 2^31 bytes.
+  const std::int64_t w_rows = I - i0 < 16 ? I - i0 : 16;
+  const int4v w_rsrc = rsrc_of(W + i0 * K, w_rows * K * 4);
+  const int4v x_rsrc = rsrc_of(X, J * K * 4);
+  constexpr int kOut = 0x7fffffff;
+  const int Ki = static_cast<int>(K), Ji = static_cast<int>(J);
+  const int spans = (Ki + kSpan - 1) / kSpan;
+  const int s_begin = wave * spans / KS, s_end = (wave + 1) * spans / KS;
+  float* const mine = lds + wave * kStages * kPer;
+  auto lds_of = [](const void* ptr) {
+    return static_cast<unsigned>(reinterpret_cast<std::uintptr_t>((__attribute__((address_space(3))) const void*)ptr));
+  };
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  auto dma16 = [](const int4v& rsrc, unsigned lds_byte, int voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :: "s"(lds_byte), "v"(voff), "s"(rsrc), "s"(0) : "memory", "m0");
+  };
+#pragma clang diagnostic pop
+  const int slot = lane % 16;
+  auto issue = [&](int s, int stage) {
+    const int k0 = s * kSpan;
+    float* const base = mine + stage * kPer;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int row = 4 * u + lane / 16;
+      const int k = k0 + 4 * (slot ^ row);
+      const bool k_in = k < Ki;  // K % 4 == 0: a chunk is whole or past K
+      dma16(w_rsrc, lds_of(base) + u * 1024, k_in ? (row * Ki + k) * 4 : kOut);
+#pragma unroll
+      for (int g = 0; g < kMB; ++g) {
+        const int j = 16 * g + row;
+        dma16(x_rsrc, lds_of(base + (1 + g) * kTile) + u * 1024, k_in && j < Ji ? (j * Ki + k) * 4 : kOut);
+      }
+    }
+  };
+  floatx4 acc[2][kMB];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int g = 0; g < kMB; ++g) acc[h][g] = floatx4{0.F, 0.F, 0.F, 0.F};
+  auto compute = [&](int stage) {
+    const float* const base = mine + stage * kPer;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int off = r * kSpan + 4 * ((4 * c + kl) ^ r);
+      const float4_t w = *reinterpret_cast<const float4_t*>(base + off);
+      float4_t x[kMB];
+#pragma unroll
+      for (int g = 0; g < kMB; ++g) x[g] = *reinterpret_cast<const float4_t*>(base + (1 + g) * kTile + off);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int g = 0; g < kMB; ++g)
+          acc[c & 1][g] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[q], x[g][q], acc[c & 1][g], 0, 0, 0);
+    }
+  };
+  constexpr int kInst = 4 * (1 + kMB);  // DMA instructions per span
+  if (s_begin < s_end) issue(s_begin, 0);
+  if (s_begin + 1 < s_end) issue(s_begin + 1, 1);
+  for (int s = s_begin; s < s_end; ++s) {
+    // Span s has landed (span s + 1's loads may still be out).
+    if (s + 1 < s_end) __builtin_amdgcn_s_waitcnt(0x0F70 | kInst);
+    else __builtin_amdgcn_s_waitcnt(0x0F70);
+    asm volatile("" ::: "memory");  // the stage's LDS reads stay after the wait
+    compute((s - s_begin) % kStages);
+    // The stage of span s - 1, whose reads this wave has consumed.
+    if (s + 2 < s_end) issue(s + 2, (s + 2 - s_begin) % kStages);
+  }
+#pragma unroll
+  for (int g = 0; g < kMB; ++g) acc[0][g] = acc[0][g] + acc[1][g];
+
+  auto store = [&](int g, int v, float x) {
+    const std::int64_t i = i0 + 4 * kl + v, j = 16 * g + r;
+    if (i >= I || j >= J) return;
+    if (a.bias != nullptr) x = x + a.bias[i];
+    a.out[batch * M * N + j * N + i] = activate(x, a.activation);
+  };
+  if constexpr (KS == 1) {
+#pragma unroll
+    for (int g = 0; g < kMB; ++g)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) store(g, v, acc[0][g][v]);
+  } else {
+    __syncthreads();  // every wave is done with its stages
+    float* const red = lds;  // KS x kMB * 4 x 64 floats
+#pragma unroll
+    for (int g = 0; g < kMB; ++g)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[(wave * kMB * 4 + g * 4 + v) * 64 + lane] = acc[0][g][v];
+    __syncthreads();
+    for (int e = wave; e < kMB * 4; e += KS) {
+      float x = red[e * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < KS; ++w) x += red[(w * kMB * 4 + e) * 64 + lane];
+      store(e / 4, e % 4, x);
+    }
+  }
+}
+
 // Matrix-vector products: y[i] = act(dot(R[i], v) + bias) for every row i of
 // a row-major R [I, K], batched. The decode-time linear x W^T with one row of
 // x (R = W, v = x, y = that row of the output), and A b with one column of b
@@ -1916,6 +2065,28 @@ int launch_stream(GemmArgs& args, hipStream_t stream) {
     return fail(TCX_INTERNAL, "streaming gemm needs at most 32 skinny rows");
   const std::int64_t blocks = (I + 15) / 16 * args.total_tiles;
   if (blocks > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "gemm grid is too large");
+  if constexpr (kOutJI && !kXCols) {
+    // The LDS-staged kernel while every block stays resident (24 KB of LDS
+    // per wave for one row group of X, 36 KB for two; 160 KB per CU), with up
+    // to four waves per block. One wave per block with at most four rows of
+    // X left the register kernel ahead (4x14336x4096: 56.6 against 48.1 us).
+    const std::int64_t capacity = 256 * (J <= 16 ? 6 : 4);
+    const std::int64_t spans = (args.k + 63) / 64;
+    int waves = 1;
+    while (waves < 4 && waves * 2 <= spans && blocks * waves * 2 <= capacity) waves *= 2;
+    if (blocks <= capacity && (waves > 1 || J > 4)) {
+      auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(64 * waves), 0, stream, args);
+      };
+      if (J <= 16)
+        go(waves == 1 ? gemm_f32_stream_lds_kernel<1, 1>
+                      : waves == 2 ? gemm_f32_stream_lds_kernel<1, 2> : gemm_f32_stream_lds_kernel<1, 4>);
+      else
+        go(waves == 1 ? gemm_f32_stream_lds_kernel<2, 1>
+                      : waves == 2 ? gemm_f32_stream_lds_kernel<2, 2> : gemm_f32_stream_lds_kernel<2, 4>);
+      return check(hipGetLastError(), "gemm_f32 streaming launch");
+    }
+  }
   const std::int64_t chunks = (args.k + 15) / 16;
   int ks = 1;
   while (ks < 16 && ks * 2 <= chunks && blocks * ks < 4096) ks *= 2;

@@ -286,9 +286,14 @@ def test_linear_small_kernel_bias_activation(cx, k):
 # streaming kernel: at most 32 rows of A against a transposed B (a linear), or
 # at most 32 columns of B in either layout. The long operand's rows are read
 # once, 16 per block, K split over 1 to 16 waves; rows past the edge and k
-# past K read zero. 33 rows (and columns) are the first past it.
+# past K read zero. A linear whose blocks all stay resident stages both
+# operands in LDS (5, 16, 17, 32 and 2 rows here, the last over 11008 W rows
+# at two waves per block); 4 rows over 14336 (one wave per block) and 20 over
+# 20000 (too many blocks to stay resident) keep the register kernel. 33 rows
+# (and columns) are the first past it.
 @pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (5, 1000, 300), (16, 256, 4), (17, 4100, 1028),
-                                   (32, 2048, 64), (32, 300, 8), (33, 3000, 516), (2, 11008, 512)])
+                                   (32, 2048, 64), (32, 300, 8), (33, 3000, 516), (2, 11008, 512),
+                                   (4, 14336, 64), (20, 20000, 68)])
 def test_linear_streaming_skinny_rows(cx, m, n, k):
     rng = np.random.default_rng(40 + m)
     x = rng.standard_normal((m, k)).astype(np.float32)
@@ -301,6 +306,43 @@ def test_linear_streaming_skinny_rows(cx, m, n, k):
     bound = 1.1e-4 * np.sqrt(k) * np.sqrt(np.mean(x * x)) * np.sqrt(np.mean(w * w)) + 1e-6
     silu = cx.hip.linear_act(xh, wh, bh, "silu").numpy()
     assert np.max(np.abs(silu - z / (1.0 + np.exp(-z)))) <= bound
+
+
+@pytest.mark.parametrize("batch,m,n,k", [(3, 12, 700, 520), (2, 24, 300, 1000), (1, 20, 300, 1000),
+                                         (4, 3, 1000, 256), (1, 16, 4096, 4096), (1, 32, 2048, 2048)])
+def test_linear_streaming_batched_transposed(cx, batch, m, n, k):
+    # x W^T through the C ABI with a batch axis on both operands, and again
+    # with the weight broadcast (batch stride 0): the LDS-staged streaming
+    # kernel at one and two row groups of x, one to four waves per block, a
+    # K tail (520, 1000) and rows of W past the last 16-row block (700, 300),
+    # with a bias and SiLU in the second pass; 3 rows of x over 1000 W rows
+    # keep two waves per block.
+    import tensorcx_hip_capi as capi
+    rng = np.random.default_rng(90 + m)
+    x = rng.standard_normal((batch, m, k)).astype(np.float32)
+    w = rng.standard_normal((batch, n, k)).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    dx, db = capi.DeviceArray.from_numpy(x), capi.DeviceArray.from_numpy(bias)
+    for shared in (False, True):
+        wb = w[:1] if shared else w
+        dw = capi.DeviceArray.from_numpy(wb)
+        out = capi.DeviceArray((batch, m, n))
+        act = "silu" if shared else "none"
+        d = capi.gemm_desc(m, n, k, batch_shape=(batch,), lhs_batch_strides=(m * k,),
+                           rhs_batch_strides=(0 if shared else n * k,), rhs_transposed=True,
+                           bias=db.ptr if shared else None, activation=act)
+        capi.gemm(dx.ptr, dw.ptr, out.ptr, d)
+        capi.synchronize()
+        got = out.numpy()
+        wf = np.broadcast_to(wb, w.shape).astype(np.float64)
+        exact = np.matmul(x.astype(np.float64), np.swapaxes(wf, 1, 2))
+        if not shared:
+            for i in range(batch):
+                assert_matmul(got[i], exact[i], x[i], wf[i].T, f"streaming batch {i} {m}x{n}x{k}")
+        else:
+            z = exact + bias
+            bound = 1.1e-4 * np.sqrt(k) * np.sqrt(np.mean(x * x)) * np.sqrt(np.mean(w[0] * w[0])) + 1e-6
+            assert np.max(np.abs(got - z / (1.0 + np.exp(-z)))) <= bound
 
 
 @pytest.mark.parametrize("sa,sb", [((4096, 4096), (4096, 1)), ((1000, 300), (300, 7)), ((300, 16), (16, 32)),
