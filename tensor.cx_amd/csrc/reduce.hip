@@ -18,7 +18,7 @@
 //
 // Paths:
 //   packed_row_kernel  inner == 1, rows of kSequentialMax + 1 .. kPackedRowMax:
-//                      16, 32 or 64 lanes per row, butterfly folds
+//                      8 to 64 lanes per row, 16-byte loads, butterfly folds
 //   row_kernel         inner == 1, longer rows: wave segments reduced by one
 //                      wave each with 16-byte loads; items of one segment per
 //                      wave (rows below kBlockRowMin) or four per 4-wave block
@@ -982,53 +982,79 @@ __global__ __launch_bounds__(64 * kShortWaves) void short_row_kernel(const T* __
 }
 
 // Contiguous rows (inner == 1) of kSequentialMax + 1 .. kPackedRowMax
-// elements: L lanes per row (the power of two at or above R / 8, at most
-// 64, at least 16), 64 / L rows per wave. Lane l of a row's group takes
-// elements l, l + L, ... (kLoads of them at most: kPackedLoads, or two or
-// four times that for rows of 513-2048, all loaded before any is used), then the
-// group folds its lanes by butterfly: sums in a fixed tree (every lane ends
-// with the same bits), extrema as (value, row index) candidates under
-// cand_better, so ties and NaNs keep the reference's lowest-index rule. One
-// wave per row spent each row's load latency and two wave-wide folds on
-// 130 elements: [100000, 130] sum ran at 8.6 % and max at 4.8 % of HBM,
-// and [16384, 1023] sum 20.5 us against 11.0 us here.
+// elements: L lanes per row, 64 / L rows per wave. Lane l of a row's group
+// takes elements 4l + 4Lu .. + 3 (u < kV, all loaded before any is used)
+// with 16-byte loads through a buffer resource based at the wave's first
+// row, whatever the rows' alignment (a 16-byte buffer load needs 4-byte
+// alignment), so a row group reads 16 L contiguous bytes per instruction.
+// Elements past the row (the next row's, or past the range, which read zero)
+// are masked; a float4 wholly past the row is not loaded. L and kV are the
+// smallest that cover the row ((8, 4) up to 128 elements, then (16, 3),
+// (16, 4), (32, 3), (32, 4), (64, 3), (64, 4), (64, 6), (64, 8)), which
+// keeps the per-element work of masked elements low. The group then folds
+// its lanes by butterfly: sums in a fixed tree (every lane ends with the same
+// bits: each lane adds its elements in order first), extrema by 64-bit keys
+// (below), so ties and NaNs keep the reference's lowest-index rule. Against
+// 4-byte loads at stride L (16-64 lanes, up to 8-32 loads), in one process
+// on MI355X: [100000, 130] sum 11.5 -> 9.0 us, max 13.5 -> 11.3; [200000,
+// 100] int32 argmax 22.8 -> 12.7; [50000, 257] max 14.2 -> 11.3; [10000,
+// 1500] max 13.1 -> 11.1 us. One wave per row had spent each row's load
+// latency and two wave-wide folds on 130 elements: [100000, 130] sum ran at
+// 8.6 % and max at 4.8 % of HBM.
 constexpr std::int64_t kPackedRowMax = 2048;
-constexpr int kPackedLoads = 8;
 
-template <int kOp, typename T, int kL, int kLoads>
+template <int kOp, typename T, int kL, int kV>
 __global__ __launch_bounds__(256) void packed_row_kernel(const T* __restrict__ x, void* __restrict__ out,
                                                          std::int64_t rows, int R) {
   constexpr bool kSum = kOp == TCX_REDUCE_SUM || kOp == TCX_REDUCE_MEAN;
   constexpr bool kLargest = kOp != TCX_REDUCE_MIN;
   constexpr int kRows = 64 / kL;
+  constexpr int kOut = 0x7fffffff;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int l = lane % kL;
+  const int l = lane % kL, g = lane / kL;
   const std::int64_t tiles = (rows + kRows - 1) / kRows;
   const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * 4;
   // The bound is wave-uniform: every lane of a wave takes part in each
   // butterfly, lanes past the last row with empty values.
   for (std::int64_t t = static_cast<std::int64_t>(blockIdx.x) * 4 + wave; t < tiles; t += step) {
-    const std::int64_t row = t * kRows + lane / kL;
+    const std::int64_t row0 = t * kRows;
+    const std::int64_t row = row0 + g;
     const bool live = row < rows;
-    const T* __restrict__ p = x + (live ? row : 0) * R;
-    T v[kLoads];
+    const int nrows = rows - row0 < kRows ? static_cast<int>(rows - row0) : kRows;
+    const auto rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(x + row0 * R), static_cast<short>(0),
+                                                        nrows * R * static_cast<int>(sizeof(T)), 0x00020000);
+    T v[kV][4];
 #pragma unroll
-    for (int u = 0; u < kLoads; ++u) v[u] = (live && l + u * kL < R) ? p[l + u * kL] : T{};
+    for (int u = 0; u < kV; ++u) {
+      const int j0 = 4 * l + 4 * kL * u;
+      const int off = live && j0 < R ? (g * R + j0) * static_cast<int>(sizeof(T)) : kOut;
+      // The whole vector is cast before its elements are taken: element
+      // reads of the builtin's result itself compiled to one 4-byte load
+      // whose value stood in for all four elements.
+      using vec4 = T __attribute__((ext_vector_type(4)));
+      const vec4 q = __builtin_bit_cast(vec4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[u][e] = q[e];
+    }
     Partial r{0U, 0U, 0};
     if constexpr (kSum) {
       if constexpr (__is_same(T, float)) {
         float s = 0.F;
 #pragma unroll
-        for (int u = 0; u < kLoads; ++u)
-          if (l + u * kL < R) s += v[u];
+        for (int u = 0; u < kV; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (4 * l + 4 * kL * u + e < R) s += v[u][e];
 #pragma unroll
         for (int offset = kL / 2; offset > 0; offset >>= 1) s += __shfl_xor(s, offset, kWave);
         r.bits = to_bits(s);
       } else {
         std::uint32_t s = 0;
 #pragma unroll
-        for (int u = 0; u < kLoads; ++u)
-          if (l + u * kL < R) s += static_cast<std::uint32_t>(v[u]);
+        for (int u = 0; u < kV; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (4 * l + 4 * kL * u + e < R) s += static_cast<std::uint32_t>(v[u][e]);
 #pragma unroll
         for (int offset = kL / 2; offset > 0; offset >>= 1)
           s += static_cast<std::uint32_t>(__shfl_xor(static_cast<int>(s), offset, kWave));
@@ -1045,24 +1071,27 @@ __global__ __launch_bounds__(256) void packed_row_kernel(const T* __restrict__ x
       std::uint64_t key = 0;
       T best{};
 #pragma unroll
-      for (int u = 0; u < kLoads; ++u) {
-        const int j = l + u * kL;
-        if (live && j < R) {
-          const std::uint64_t k = (static_cast<std::uint64_t>(rank_key<T, kLargest>(to_bits(v[u]))) << 32) |
-                                  (0xFFFFFFFFU - static_cast<std::uint32_t>(j));
-          if (k > key) {
-            key = k;
-            best = v[u];
+      for (int u = 0; u < kV; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = 4 * l + 4 * kL * u + e;
+          if (live && j < R) {
+            const std::uint64_t k = (static_cast<std::uint64_t>(rank_key<T, kLargest>(to_bits(v[u][e]))) << 32) |
+                                    (0xFFFFFFFFU - static_cast<std::uint32_t>(j));
+            if (k > key) {
+              key = k;
+              best = v[u][e];
+            }
           }
         }
-      }
 #pragma unroll
       for (int offset = kL / 2; offset > 0; offset >>= 1) {
         const std::uint64_t o = __shfl_xor(key, offset, kWave);
         key = o > key ? o : key;
       }
       const int bi = key ? static_cast<int>(0xFFFFFFFFU - static_cast<std::uint32_t>(key)) : -1;
-      const int owner = (lane & ~(kL - 1)) + (bi < 0 ? 0 : bi % kL);
+      // Element j sits in lane (j / 4) % L of the group.
+      const int owner = (lane & ~(kL - 1)) + (bi < 0 ? 0 : (bi / 4) % kL);
       r.bits = static_cast<std::uint32_t>(__shfl(static_cast<int>(to_bits(best)), owner, kWave));
       r.index = bi;
     }
@@ -1333,11 +1362,15 @@ int launch_reduce(const T* x, void* out, std::int64_t outer, std::int64_t reduce
                            dim3(256), 0, s, x, out, outer, static_cast<int>(reduce));
         return check(hipGetLastError(), "reduce packed row kernel launch");
       };
-      if (reduce <= 16 * kPackedLoads) return packed(packed_row_kernel<kOp, T, 16, kPackedLoads>, 4);
-      if (reduce <= 32 * kPackedLoads) return packed(packed_row_kernel<kOp, T, 32, kPackedLoads>, 2);
-      if (reduce <= 64 * kPackedLoads) return packed(packed_row_kernel<kOp, T, 64, kPackedLoads>, 1);
-      if (reduce <= 128 * kPackedLoads) return packed(packed_row_kernel<kOp, T, 64, 2 * kPackedLoads>, 1);
-      return packed(packed_row_kernel<kOp, T, 64, 4 * kPackedLoads>, 1);
+      if (reduce <= 128) return packed(packed_row_kernel<kOp, T, 8, 4>, 8);
+      if (reduce <= 192) return packed(packed_row_kernel<kOp, T, 16, 3>, 4);
+      if (reduce <= 256) return packed(packed_row_kernel<kOp, T, 16, 4>, 4);
+      if (reduce <= 384) return packed(packed_row_kernel<kOp, T, 32, 3>, 2);
+      if (reduce <= 512) return packed(packed_row_kernel<kOp, T, 32, 4>, 2);
+      if (reduce <= 768) return packed(packed_row_kernel<kOp, T, 64, 3>, 1);
+      if (reduce <= 1024) return packed(packed_row_kernel<kOp, T, 64, 4>, 1);
+      if (reduce <= 1536) return packed(packed_row_kernel<kOp, T, 64, 6>, 1);
+      return packed(packed_row_kernel<kOp, T, 64, 8>, 1);
     }
     if (inner == 1 && reduce >= kShortRowMin) {
       const std::int64_t tiles = (outer + 63) / 64;

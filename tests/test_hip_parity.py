@@ -807,6 +807,50 @@ def test_row_reduction_block_items(cx, shape):
         assert_bits(getattr(cx, op)(hi, -1).numpy(), getattr(oracle, op)(yi, -1), f"i32 {op} {shape}")
 
 
+@pytest.mark.parametrize("width", [65, 100, 128, 129, 193, 256, 257, 385, 512, 513, 769, 1023, 1025, 1537,
+                                   2047, 2048])
+def test_packed_row_reductions_special_values(cx, width):
+    """Rows of 65-2048 elements: 8 to 64 lanes per row with 16-byte loads at
+    any alignment, 1 to 8 loads per lane (each width is the first or last of
+    one shape). A float4 that runs past a row reads the next row's first
+    elements and must mask them: those are NaN, +inf or -inf here. Ties inside
+    a float4, across lanes and across loop steps, signed zeros, the extreme at
+    the last element, a partial last wave (11 rows), and int32 rows whose sums
+    wrap."""
+    rows = 11
+    rng = np.random.default_rng(width)
+    x = rng.integers(-3, 4, (rows, width)).astype(np.float32)   # many ties
+    x[1, 0] = np.nan                       # row 0's last float4 may read it
+    x[2, 0:3] = np.inf                     # row 1's
+    x[3, 0] = -np.inf                      # row 2's
+    x[4, 1] = x[4, 2] = 9.0                # tie inside a float4
+    x[5, 4] = x[5, 0] = 9.0                # tie across lanes
+    x[6, width - 1] = 9.0                  # extreme at the last element
+    x[7, :] = -0.0
+    x[7, width // 2] = 0.0                 # +0/-0 equal: first (-0) kept
+    x[8, width - 2] = np.nan               # NaN late in the row
+    x[9, 4 * 8 * (width // 64)] = 9.0      # a later loop step
+    x[9, 0] = 9.0
+    h = cx.tensor(x, device="hip")
+    for op in ("max", "min", "argmax"):
+        assert_bits(getattr(cx, op)(h, 1).numpy(), getattr(oracle, op)(x, 1), f"{op} width {width}")
+    with np.errstate(invalid="ignore"):
+        for op in ("sum", "mean"):
+            actual, expected = getattr(cx, op)(h, 1).numpy(), getattr(oracle, op)(x, 1)
+            assert np.array_equal(np.isnan(actual), np.isnan(expected)), op
+            assert np.array_equal(np.isinf(actual), np.isinf(expected)), op
+            fin = np.isfinite(expected)
+            scale = width if op == "mean" else 1
+            assert sum_error(actual[fin] * scale, expected[fin] * scale, x[fin], int(fin.sum()), width, 1) <= 1e-5
+    y = rng.standard_normal((rows, width)).astype(np.float32)
+    hy = cx.tensor(y, device="hip")
+    assert sum_error(cx.sum(hy, 1).numpy(), oracle.sum(y, 1), y, rows, width, 1) <= 1e-5
+    yi = rng.integers(-2**31, 2**31 - 1, (rows, width), dtype=np.int64).astype(np.int32)
+    hi = cx.tensor(yi, device="hip")
+    for op in ("sum", "max", "min", "argmax"):
+        assert_bits(getattr(cx, op)(hi, 1).numpy(), getattr(oracle, op)(yi, 1), f"i32 {op} width {width}")
+
+
 def test_int32_reductions_wrap(cx):
     rng = np.random.default_rng(3)
     x = rng.integers(-2**31, 2**31 - 1, size=(300, 1031), dtype=np.int64).astype(np.int32)
