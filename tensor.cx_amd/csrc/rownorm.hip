@@ -3,10 +3,11 @@
 // (core/inference.cpp:103-122) fused into the same pass.
 //
 // Contiguous rows (inner == 1) stay in registers, so each element is read from
-// HBM once and written once: rows of up to 128 elements pack several per wave
-// (row_packed_kernel), rows of up to 1024 elements take one wave per row
-// (kChunks 16-byte loads per lane, wave-wide butterfly statistics); rows of up
-// to 3072 elements (4096 with an affine weight or bias) take one 256-thread
+// HBM once and written once: rows of up to 64 elements pack several per wave
+// (row_packed_kernel, one float4 or four floats per lane), rows of up to 1536
+// elements take L lanes each, 64 / L rows per wave (row_group_kernel, 16-byte
+// loads at any alignment, butterfly statistics over the row's lanes); rows of
+// up to 3072 elements (4096 with an affine weight or bias) take one 256-thread
 // block per row (four waves, whose partial statistics meet in LDS). Longer
 // rows take one 512-thread block per row that holds the whole row in
 // registers, and past about 90 K floats in LDS too (row_resident_kernel, to
@@ -27,8 +28,8 @@
 namespace tcx {
 namespace {
 
-constexpr int kMaxWaveChunks = 4;  // one wave per row up to 1024 floats
-constexpr std::int64_t kPackedMax = 128;      // rows up to this length pack several per wave
+constexpr std::int64_t kPackedMax = 64;       // rows up to this length pack several per wave
+constexpr std::int64_t kGroupMax = 1536;      // row_group_kernel up to this length
 constexpr std::int64_t kPackedBlocks = 4096;  // grid cap of the packed kernel (it strides over rows)
 constexpr int kMaxSplit = 4;       // one block per row up to 256*4*4 floats
 
@@ -59,171 +60,13 @@ __device__ __forceinline__ float finish_scale_ln(float ssd, std::int64_t n, floa
   return 1.0F / sqrtf(denom);
 }
 
-// One wave per row, row cached in registers (kChunks float4 per lane).
-// Blocks are persistent: each of the grid's blocks walks rows
-// blockIdx*4 + wave, stepping by the grid, so the affine weight and bias are
-// staged into LDS once per block instead of being re-read for every row.
-template <RowOp kOp, int kChunks, bool kVec, bool kFull>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void
-row_cached_kernel(RowArgs a) {
-  extern __shared__ float4_t affine4[];  // gamma [n] then beta [n], when present
-  float* affine = reinterpret_cast<float*>(affine4);
-  const int lane = threadIdx.x & 63;
-  const std::int64_t n = a.n;
-  const bool has_g = a.gamma != nullptr, has_b = a.beta != nullptr;
-  if (has_g || has_b) {
-    for (std::int64_t i = threadIdx.x; i < n; i += 256) {
-      if (has_g) affine[i] = a.gamma[i];
-      if (has_b) affine[n + i] = a.beta[i];
-    }
-    __syncthreads();
-  }
-  // Element (c, q) sits at column 4*(lane + 64c) + q (vector rows) or at
-  // lane + 64*(4c + q) (scalar rows); columns >= n are masked. kFull rows
-  // (n == 256 * kChunks, 16-byte aligned) have no masked elements.
-  auto column = [&](int c, int q) -> int {
-    return kVec ? 4 * (lane + 64 * c) + q : lane + 64 * (4 * c + q);
-  };
-  const int ni = static_cast<int>(n);
-  auto valid = [&](int c, int q) -> bool {
-    if constexpr (kFull) return true;
-    return kVec ? column(c, 0) < ni : column(c, q) < ni;
-  };
-  const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * 4;
-  for (std::int64_t row = static_cast<std::int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); row < a.rows;
-       row += step) {
-    const float* __restrict__ x = a.x + row * n;
-    float* __restrict__ out = a.out + row * n;
-    float v[kChunks][4];
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c) {
-      if constexpr (kVec) {
-        const int i = column(c, 0);
-        float4_t t = {0.F, 0.F, 0.F, 0.F};
-        if (valid(c, 0)) t = stream_load(reinterpret_cast<const float4_t*>(x + i));
-        v[c][0] = t.x; v[c][1] = t.y; v[c][2] = t.z; v[c][3] = t.w;
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          v[c][q] = valid(c, q) ? x[column(c, q)] : 0.F;
-        }
-      }
-    }
-
-    if constexpr (kOp == RowOp::kSoftmax) {
-      float m = -__builtin_inff();
-#pragma unroll
-      for (int c = 0; c < kChunks; ++c)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (valid(c, q) && (is_nan(v[c][q]) || v[c][q] > m)) m = v[c][q];
-      m = wave_max_nan(m);
-      float sum = 0.F;
-#pragma unroll
-      for (int c = 0; c < kChunks; ++c)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (valid(c, q)) {
-            v[c][q] = exp_softmax(v[c][q] - m);
-            sum += v[c][q];
-          }
-        }
-      // One correctly rounded reciprocal per row; each output is e * (1/denom),
-      // within 1.5 ulp of the reference's e / denom.
-      const float inv = 1.0F / wave_sum(sum);
-#pragma unroll
-      for (int c = 0; c < kChunks; ++c)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v[c][q] = v[c][q] * inv;
-    } else if constexpr (kOp == RowOp::kRms) {
-      float sum = 0.F;
-#pragma unroll
-      for (int c = 0; c < kChunks; ++c)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float t = v[c][q] * v[c][q];
-          sum += t;  // masked elements are zero
-        }
-      const float ss = wave_sum(sum);
-      const float scale = 1.0F / sqrtf(ss / static_cast<float>(n) + a.eps);
-#pragma unroll
-      for (int c = 0; c < kChunks; ++c)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v[c][q] = v[c][q] * scale;
-    } else {
-      const float first = x[0];
-      float sum = 0.F;
-      bool equal = true;
-#pragma unroll
-      for (int c = 0; c < kChunks; ++c)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          sum += v[c][q];
-          if (valid(c, q)) equal = equal && v[c][q] == first;
-        }
-      const float mean = wave_sum(sum) / static_cast<float>(n);
-      float d2 = 0.F;
-#pragma unroll
-      for (int c = 0; c < kChunks; ++c)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (valid(c, q)) {
-            const float d = v[c][q] - mean;
-            d2 += d * d;
-          }
-        }
-      bool nan_row = false;
-      const float scale = finish_scale_ln(wave_sum(d2), n, a.eps, nan_row);
-      // Row-uniform special cases as selects: an all-equal finite row gives 0
-      // (NaN when eps is 0); a zero variance + eps gives NaN.
-      const bool const_row = __all(equal) && __builtin_isfinite(first);
-      const bool special = const_row || nan_row;
-      const float special_value = const_row && a.eps != 0.F ? 0.F : __builtin_nanf("");
-#pragma unroll
-      for (int c = 0; c < kChunks; ++c)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v[c][q] = special ? special_value : (v[c][q] - mean) * scale;
-    }
-
-    // Affine steps (multiply then add, each rounded) and the store.
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c) {
-      if constexpr (kVec) {
-        const int i = column(c, 0);
-        if (!valid(c, 0)) continue;
-        float4_t t = {v[c][0], v[c][1], v[c][2], v[c][3]};
-        if (has_g) {
-          const float4_t g = affine4[i / 4];
-          t.x = t.x * g.x; t.y = t.y * g.y; t.z = t.z * g.z; t.w = t.w * g.w;
-        }
-        if (has_b) {
-          const float4_t b = affine4[(ni + i) / 4];
-          t.x = t.x + b.x; t.y = t.y + b.y; t.z = t.z + b.z; t.w = t.w + b.w;
-        }
-        __builtin_nontemporal_store(t, reinterpret_cast<float4_t*>(out + i));
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (!valid(c, q)) continue;
-          const int i = column(c, q);
-          float t = v[c][q];
-          if (has_g) t = t * affine[i];
-          if (has_b) t = t + affine[ni + i];
-          out[i] = t;
-        }
-      }
-    }
-    // Keep the next row's loads from being hoisted into this row's live range.
-    asm volatile("" ::: "memory");
-  }
-}
-
-// Rows of at most 128 elements, several per wave: a row takes L lanes (the
+// Rows of at most 64 elements, several per wave: a row takes L lanes (the
 // power of two at or above n / 4), each holding one float4 at column 4k
 // (vector rows) or four floats at k, k + L, k + 2L, k + 3L (scalar rows),
 // and a wave holds 64 / L rows. Row statistics are butterflies over the L
 // lanes of the row (both partners add the same operands, so the row's lanes
-// agree bit for bit); the per-element steps are row_cached_kernel's.
+// agree bit for bit); the per-element steps are those of the other row
+// kernels.
 __device__ __forceinline__ float group_sum(float v, int L) {
   for (int offset = L >> 1; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
   return v;
@@ -359,9 +202,15 @@ __global__ __launch_bounds__(256) void row_packed_kernel(RowArgs a, int L) {
 // weight and bias of a thread's columns stay in registers across rows, and the
 // block's next row loads into a second register set while the current one
 // reduces and stores (global loads stay in flight across the barriers).
+// Rows of 4 float4 per thread load and store non-temporally; rows of 2 (the
+// 1537-2048 floats this kernel takes there) with the default policy:
+// [8192, 2048] LayerNorm + weight/bias 25.5 -> 22.4 us, softmax 25.9 ->
+// 23.0, where [16384, 4096] LayerNorm + weight/bias lost 87.1 -> 92.6 us
+// without the non-temporal hint.
 template <RowOp kOp, int kPer, bool kVec, bool kFull>
 __global__ __launch_bounds__(256) void row_split_kernel(RowArgs a) {
   static_assert(kPer <= kMaxSplit, "two register copies of the row and the affine terms per thread");
+  constexpr bool kNT = kPer > 2;
   // Statistics exchange, double-buffered by row parity so a wave that runs
   // ahead never overwrites a slot another wave has yet to read.
   __shared__ float red[2][2][4];  // [row parity][statistic][wave]
@@ -409,7 +258,10 @@ __global__ __launch_bounds__(256) void row_split_kernel(RowArgs a) {
     for (int c = 0; c < kPer; ++c) {
       if constexpr (kVec) {
         float4_t q = {0.F, 0.F, 0.F, 0.F};
-        if (valid(c, 0)) q = stream_load(reinterpret_cast<const float4_t*>(x + column(c, 0)));
+        if (valid(c, 0)) {
+          const auto* src = reinterpret_cast<const float4_t*>(x + column(c, 0));
+          q = kNT ? stream_load(src) : *src;
+        }
         dst[c][0] = q.x; dst[c][1] = q.y; dst[c][2] = q.z; dst[c][3] = q.w;
       } else {
 #pragma unroll
@@ -518,7 +370,9 @@ __global__ __launch_bounds__(256) void row_split_kernel(RowArgs a) {
       if constexpr (kVec) {
         if (!valid(c, 0)) continue;
         const float4_t o = {r[0], r[1], r[2], r[3]};
-        __builtin_nontemporal_store(o, reinterpret_cast<float4_t*>(out + column(c, 0)));
+        auto* dst = reinterpret_cast<float4_t*>(out + column(c, 0));
+        if constexpr (kNT) __builtin_nontemporal_store(o, dst);
+        else *dst = o;
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -1434,29 +1288,6 @@ __global__ __launch_bounds__(64 * kNormWaves) void col_norm_kernel(ColNormArgs a
 
 bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15U) == 0; }
 
-// Persistent grid: as many blocks as fit on the device at once (cached per
-// kernel instance and LDS size), never more than there are 4-row groups.
-template <RowOp kOp, int kChunks, bool kVec, bool kFull>
-void launch_cached_as(const RowArgs& a, hipStream_t s) {
-  const std::size_t lds = (a.gamma || a.beta) ? static_cast<std::size_t>(2 * a.n) * sizeof(float) : 0;
-  thread_local int cached_blocks = 0;
-  thread_local std::size_t cached_lds = ~std::size_t{0};
-  if (cached_lds != lds) {
-    int per_cu = 0, cus = 0, device = 0;
-    (void)hipGetDevice(&device);
-    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, row_cached_kernel<kOp, kChunks, kVec, kFull>, 256, lds) !=
-            hipSuccess ||
-        per_cu < 1)
-      per_cu = 1;
-    cached_blocks = per_cu * (cus > 0 ? cus : 256);
-    cached_lds = lds;
-  }
-  const std::int64_t groups = (a.rows + 3) / 4;
-  const unsigned grid = static_cast<unsigned>(groups < cached_blocks ? groups : cached_blocks);
-  hipLaunchKernelGGL((row_cached_kernel<kOp, kChunks, kVec, kFull>), dim3(grid), dim3(256), lds, s, a);
-}
-
 // Persistent split grid: kSplitBlocksPerCu blocks per CU (fewer if the
 // occupancy calculator allows fewer), never more than there are rows. A few
 // blocks per CU keep enough loads in flight while the rows being streamed at
@@ -1492,16 +1323,6 @@ int launch_split(const RowArgs& a, bool vec, hipStream_t s) {
   else
     launch_split_as<kOp, kPer, false, false>(a, s);
   return check(hipGetLastError(), "row kernel launch");
-}
-
-template <RowOp kOp, int kChunks>
-void launch_cached(const RowArgs& a, bool vec, hipStream_t s) {
-  if (vec && a.n == 256 * kChunks)
-    launch_cached_as<kOp, kChunks, true, true>(a, s);
-  else if (vec)
-    launch_cached_as<kOp, kChunks, true, false>(a, s);
-  else
-    launch_cached_as<kOp, kChunks, false, false>(a, s);
 }
 
 // Columns of a strided tile: 64 x 4 with 16-byte loads, else 64; a
@@ -1608,6 +1429,228 @@ void resident_variants(F&& f) {
   }
 }
 
+// Rows of 65-1536 elements at any alignment: L lanes per row, 64 / L rows
+// per wave; lane l of a row's group holds elements 4l + 4Lu .. + 3 (u < kV),
+// read with 16-byte buffer loads (4-byte alignment suffices) through a
+// resource based at the group's first row. Elements past the row are
+// masked to zero; a float4 wholly past it is not loaded, and the one that
+// crosses the row's end is stored element by element (whole float4s take
+// 16-byte buffer stores), so no other row's elements are written. The
+// waves are persistent (as many blocks as stay resident) and load their
+// next row group into a second register set before the current group's
+// reductions. Row statistics are butterflies over the group's L lanes, in
+// the per-element steps of the other row kernels. Loads and stores take the
+// default cache policy: with the non-temporal one, whose partial-line writes
+// these rows make at every row boundary, [100000, 100] softmax ran 28.1
+// against 15.9 us and [100000, 130] 30.1 against 20.1 us on MI355X.
+template <RowOp kOp, int kL, int kV, int kAff>
+__global__ __launch_bounds__(256) void row_group_kernel(RowArgs a) {
+  constexpr int kRows = 64 / kL;
+  constexpr int kOut = 0x7fffffff;
+  constexpr bool kG = (kAff & kAffGamma) != 0, kB = (kAff & kAffBeta) != 0;
+  using b128_t = unsigned int __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l = lane % kL, gr = lane / kL;
+  const int n = static_cast<int>(a.n);  // at most 1536
+  auto col = [&](int u) { return 4 * l + 4 * kL * u; };
+  // The weight and bias go to LDS once per (persistent) block: gamma at 0,
+  // beta at nq (n rounded up to 4), so both read as aligned float4s.
+  extern __shared__ float4_t affine4[];
+  float* const affine = reinterpret_cast<float*>(affine4);
+  const int nq = (n + 3) / 4 * 4;
+  if constexpr (kG || kB) {
+    for (int i = threadIdx.x; i < n; i += 256) {
+      if constexpr (kG) affine[i] = a.gamma[i];
+      if constexpr (kB) affine[nq + i] = a.beta[i];
+    }
+    __syncthreads();
+  }
+  auto rsrc_at = [&](const float* base, std::int64_t row0, int nrows) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base + row0 * a.n), static_cast<short>(0),
+                                             nrows * n * 4, 0x00020000);
+  };
+  const std::int64_t groups = (a.rows + kRows - 1) / kRows;
+  auto rows_in = [&](std::int64_t t) {
+    const std::int64_t left = a.rows - t * kRows;
+    return left < kRows ? static_cast<int>(left) : kRows;
+  };
+  auto load = [&](std::int64_t t, float (&v)[kV][4]) {
+    const int nrows = rows_in(t);
+    const auto r = rsrc_at(a.x, t * kRows, nrows);
+    const bool live = gr < nrows;
+#pragma unroll
+    for (int u = 0; u < kV; ++u) {
+      const int j0 = col(u);
+      const int off = live && j0 < n ? (gr * n + j0) * 4 : kOut;
+      const float4_t q = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[u][e] = j0 + e < n ? q[e] : 0.F;
+    }
+  };
+  const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * 4;
+  std::int64_t t = static_cast<std::int64_t>(blockIdx.x) * 4 + wave;
+  float v[kV][4], nv[kV][4];
+  if (t < groups) load(t, v);
+  for (; t < groups; t += step) {
+    if (t + step < groups) load(t + step, nv);
+    const int nrows = rows_in(t);
+    const bool live = gr < nrows;
+    auto valid = [&](int u, int e) { return col(u) + e < n; };
+    if constexpr (kOp == RowOp::kSoftmax) {
+      float m = -__builtin_inff();
+#pragma unroll
+      for (int u = 0; u < kV; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (valid(u, e) && (is_nan(v[u][e]) || v[u][e] > m)) m = v[u][e];
+      m = group_max_nan(m, kL);
+      float sum = 0.F;
+#pragma unroll
+      for (int u = 0; u < kV; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (valid(u, e)) {
+            v[u][e] = exp_softmax(v[u][e] - m);
+            sum += v[u][e];
+          }
+      const float inv = 1.0F / group_sum(sum, kL);
+#pragma unroll
+      for (int u = 0; u < kV; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[u][e] = v[u][e] * inv;
+    } else if constexpr (kOp == RowOp::kRms) {
+      float sum = 0.F;
+#pragma unroll
+      for (int u = 0; u < kV; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float sq = v[u][e] * v[u][e];
+          sum += sq;  // masked elements are zero
+        }
+      const float scale = 1.0F / sqrtf(group_sum(sum, kL) / static_cast<float>(n) + a.eps);
+#pragma unroll
+      for (int u = 0; u < kV; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[u][e] = v[u][e] * scale;
+    } else {
+      // Element 0 of the row sits in the group's first lane.
+      const float first = __shfl(v[0][0], lane & ~(kL - 1), kWave);
+      float sum = 0.F;
+      bool equal = true;
+#pragma unroll
+      for (int u = 0; u < kV; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sum += v[u][e];  // masked elements are zero
+          if (valid(u, e)) equal = equal && v[u][e] == first;
+        }
+      const float mean = group_sum(sum, kL) / static_cast<float>(n);
+      float d2 = 0.F;
+#pragma unroll
+      for (int u = 0; u < kV; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (valid(u, e)) {
+            const float d = v[u][e] - mean;
+            d2 += d * d;
+          }
+      bool nan_row = false;
+      const float scale = finish_scale_ln(group_sum(d2, kL), n, a.eps, nan_row);
+      const bool const_row = group_all(equal, kL) && __builtin_isfinite(first);
+      const bool special = const_row || nan_row;
+      const float special_value = const_row && a.eps != 0.F ? 0.F : __builtin_nanf("");
+#pragma unroll
+      for (int u = 0; u < kV; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[u][e] = special ? special_value : (v[u][e] - mean) * scale;
+    }
+    // Affine steps (multiply then add, each rounded) and the store.
+    const auto o = rsrc_at(a.out, t * kRows, nrows);
+#pragma unroll
+    for (int u = 0; u < kV; ++u) {
+      float r[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        r[e] = v[u][e];
+      }
+      const int j0 = col(u);
+      if constexpr (kG) {
+        const float4_t w = affine4[j0 / 4];  // past n: unset lanes of LDS, not stored
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = r[e] * w[e];
+      }
+      if constexpr (kB) {
+        const float4_t w = affine4[nq / 4 + j0 / 4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = r[e] + w[e];
+      }
+      if (!live || j0 >= n) continue;
+      const int off = (gr * n + j0) * 4;
+      if (j0 + 4 <= n) {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(b128_t, float4_t{r[0], r[1], r[2], r[3]}), o, off,
+                                               0, 0);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 3; ++e)
+          if (j0 + e < n) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, r[e]), o, off + 4 * e, 0,
+                                                                0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kV; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[u][e] = nv[u][e];
+    // Keep later groups' loads from being hoisted into this group's live range.
+    asm volatile("" ::: "memory");
+  }
+}
+
+template <RowOp kOp, int kL, int kV, int kAff>
+void launch_group_as(const RowArgs& a, hipStream_t s) {
+  const std::size_t lds = (kAff != 0 ? 2 : 0) * static_cast<std::size_t>((a.n + 3) / 4 * 4) * sizeof(float);
+  thread_local int cached_blocks = 0;
+  if (cached_blocks == 0) {
+    int per_cu = 0, cus = 0, device = 0;
+    (void)hipGetDevice(&device);
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, row_group_kernel<kOp, kL, kV, kAff>, 256,
+                                                     kAff != 0 ? 2 * kGroupMax * 4 : 0) !=
+            hipSuccess ||
+        per_cu < 1)
+      per_cu = 1;
+    cached_blocks = per_cu * (cus > 0 ? cus : 256);
+  }
+  const std::int64_t groups = (a.rows + 64 / kL - 1) / (64 / kL);
+  const std::int64_t need = (groups + 3) / 4;
+  const unsigned grid = static_cast<unsigned>(need < cached_blocks ? need : cached_blocks);
+  hipLaunchKernelGGL((row_group_kernel<kOp, kL, kV, kAff>), dim3(grid), dim3(256), lds, s, a);
+}
+
+template <RowOp kOp, int kL, int kV>
+void launch_group(const RowArgs& a, hipStream_t s) {
+  const int aff = (a.gamma ? kAffGamma : 0) + (a.beta ? kAffBeta : 0);
+  if (aff == 0) launch_group_as<kOp, kL, kV, 0>(a, s);
+  if constexpr (kOp != RowOp::kSoftmax)
+    if (aff == kAffGamma) launch_group_as<kOp, kL, kV, kAffGamma>(a, s);
+  if constexpr (kOp == RowOp::kLayer) {
+    if (aff == kAffBeta) launch_group_as<kOp, kL, kV, kAffBeta>(a, s);
+    if (aff == (kAffGamma | kAffBeta)) launch_group_as<kOp, kL, kV, kAffGamma | kAffBeta>(a, s);
+  }
+}
+
+// (L, kV): the smallest that covers the row, as for the packed reductions.
+template <RowOp kOp>
+void launch_group_for(const RowArgs& a, std::int64_t n, hipStream_t s) {
+  if (n <= 128) launch_group<kOp, 8, 4>(a, s);
+  else if (n <= 192) launch_group<kOp, 16, 3>(a, s);
+  else if (n <= 256) launch_group<kOp, 16, 4>(a, s);
+  else if (n <= 384) launch_group<kOp, 32, 3>(a, s);
+  else if (n <= 512) launch_group<kOp, 32, 4>(a, s);
+  else if (n <= 768) launch_group<kOp, 64, 3>(a, s);
+  else if (n <= 1024) launch_group<kOp, 64, 4>(a, s);
+  else launch_group<kOp, 64, 6>(a, s);
+}
+
 template <RowOp kOp>
 int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t inner, void* workspace,
              std::size_t workspace_bytes, bool split, hipStream_t s) {
@@ -1619,9 +1662,10 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
   a.n = reduce;
   const bool vec = reduce % 4 == 0 && aligned16(a.x) && aligned16(a.out) &&
                    (a.gamma == nullptr || aligned16(a.gamma)) && (a.beta == nullptr || aligned16(a.beta));
-  const std::int64_t chunks = (reduce + 255) / 256;  // per lane, one wave per row
   const std::int64_t per = (reduce + 1023) / 1024;    // per thread, one block per row
-  if (reduce <= kPackedMax) {
+  if (reduce > kPackedMax && reduce <= kGroupMax) {
+    launch_group_for<kOp>(a, reduce, s);
+  } else if (reduce <= kPackedMax) {
     // Several rows per wave, L lanes per row.
     int L = 1;
     while (4 * L < reduce) L *= 2;
@@ -1631,10 +1675,7 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
       hipLaunchKernelGGL((row_packed_kernel<kOp, true>), dim3(grid), dim3(256), 0, s, a, L);
     else
       hipLaunchKernelGGL((row_packed_kernel<kOp, false>), dim3(grid), dim3(256), 0, s, a, L);
-  } else if (chunks <= 1) launch_cached<kOp, 1>(a, vec, s);
-  else if (chunks <= 2) launch_cached<kOp, 2>(a, vec, s);
-  else if (chunks <= kMaxWaveChunks) launch_cached<kOp, 4>(a, vec, s);
-  else if (reduce > 3072 && reduce <= 4 * kResidentThreads * 8 &&
+  } else if (reduce > 3072 && reduce <= 4 * kResidentThreads * 8 &&
            (reduce > 4096 || (a.gamma == nullptr && a.beta == nullptr))) {
     // Rows of 3073-16384 floats: held in registers by row_resident_kernel,
     // one 512-thread block per row, whose float4 body starts at the row's

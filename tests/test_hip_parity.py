@@ -969,16 +969,20 @@ def test_empty_and_scalar(cx):
 
 
 # ------------------------------------------------------------- row ops
-# Widths cover each row kernel: one wave per row (<= 1024), one 256-thread
-# block per row (up to 3072 floats, 4096 with a weight or bias: aligned full
-# and masked, and unaligned), one 512-thread block per row holding 3073-16384
+# Widths cover each row kernel: rows of at most 64 packed several per wave,
+# rows of 65-1536 in lane groups (8 to 64 lanes, 1 to 6 float4 per lane, any
+# alignment, partial last groups), one 256-thread block per row (1537-3072
+# floats, 4096 with a weight or bias: aligned full and masked, and
+# unaligned), one 512-thread block per row holding 3073-16384
 # floats in 4 or 8 float4 per thread (aligned and unaligned) and wider rows in
 # 12 or 20, the re-reading block kernel, and strided rows.
 @pytest.mark.parametrize("shape,axis", [((16, 4096), 1), ((5, 300), 1), ((7, 8192), 1), ((3, 20000), -1),
                                         ((3, 7), 0), ((2, 3, 70), 1), ((9, 1), 1), ((4, 1022), 1),
                                         ((4, 1024), 1), ((6, 1501), 1), ((4, 2048), 1), ((3, 3001), 1),
                                         ((5, 4100), 1), ((2, 12288), 1), ((3, 16384), 1), ((2, 16383), 1),
-                                        ((1000, 1028), 1), ((3, 5001), 1), ((2, 9999), 1)])
+                                        ((1000, 1028), 1), ((3, 5001), 1), ((2, 9999), 1), ((9, 130), 1),
+                                        ((17, 100), 1), ((33, 257), 1), ((5, 1536), 1), ((3, 1537), 1),
+                                        ((1001, 65), 1)])
 def test_row_ops_random(cx, shape, axis):
     rng = np.random.default_rng(13)
     x = (rng.standard_normal(shape) * 3).astype(np.float32)
@@ -996,11 +1000,14 @@ def test_row_ops_random(cx, shape, axis):
                  oracle.affine_norm(x, axis, 1e-5, g, None, rms=True), 1e-5, 1e-5, "affine rmsnorm")
 
 
-@pytest.mark.parametrize("width", [200, 500, 1024, 2048, 3001, 3073, 4095, 4096, 8191, 8192, 16383, 16384, 16385, 20003,
+@pytest.mark.parametrize("width", [65, 100, 127, 129, 130, 193, 200, 257, 385, 500, 513, 769, 1024, 1025, 1536, 1537,
+                                   2048, 3001, 3073, 4095, 4096, 8191, 8192, 16383, 16384, 16385, 20003,
                                    24577, 32000, 40001, 40961, 70000, 90113, 100003, 128256, 130816, 131000])
 def test_row_ops_special_values_wide_rows(cx, width):
-    # Non-finite values in rows of every width class (one-wave cached rows,
-    # split rows at 2 and 4 float4 per thread, aligned and unaligned, rows of
+    # Non-finite values in rows of every width class (rows of 65-1536 in
+    # groups of 8 to 64 lanes at 1 to 6 float4 per lane, any alignment, with
+    # row 1's last float4 reading row 2's leading -inf; split rows at 2 and 4
+    # float4 per thread, aligned and unaligned, rows of
     # 3073-16384 held at 4 or 8 float4 per thread by a 512-thread block
     # (without a weight or bias up to 4096), rows held in registers at 12 or
     # 20 float4 per thread (up to 24576 and 40960 floats),
@@ -1063,7 +1070,7 @@ def test_row_ops_special_values_wide_rows(cx, width):
 
 
 @pytest.mark.parametrize("eps", [0.0, 1e-45, 1e-5, 1e30])
-@pytest.mark.parametrize("width", [512, 4096, 3001, 8192, 16384, 20003, 32000, 100003])
+@pytest.mark.parametrize("width", [100, 130, 512, 1025, 1537, 4096, 3001, 8192, 16384, 20003, 32000, 100003])
 def test_constant_rows(cx, eps, width):
     x = np.full((5, width), 2.5, np.float32)
     x[3] = -7.0
