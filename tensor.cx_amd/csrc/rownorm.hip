@@ -3,10 +3,9 @@
 // (core/inference.cpp:103-122) fused into the same pass.
 //
 // Contiguous rows (inner == 1) stay in registers, so each element is read from
-// HBM once and written once: rows of up to 64 elements pack several per wave
-// (row_packed_kernel, one float4 or four floats per lane), rows of up to 1536
-// elements take L lanes each, 64 / L rows per wave (row_group_kernel, 16-byte
-// loads at any alignment, butterfly statistics over the row's lanes); rows of
+// HBM once and written once: rows of up to 1536 elements take L lanes each,
+// 64 / L rows per wave (row_group_kernel, 16-byte loads at any alignment,
+// butterfly statistics over the row's lanes); rows of
 // up to 3072 elements (4096 with an affine weight or bias) take one 256-thread
 // block per row (four waves, whose partial statistics meet in LDS). Longer
 // rows take one 512-thread block per row that holds the whole row in
@@ -28,9 +27,7 @@
 namespace tcx {
 namespace {
 
-constexpr std::int64_t kPackedMax = 64;       // rows up to this length pack several per wave
-constexpr std::int64_t kGroupMax = 1536;      // row_group_kernel up to this length
-constexpr std::int64_t kPackedBlocks = 4096;  // grid cap of the packed kernel (it strides over rows)
+constexpr std::int64_t kGroupMax = 1536;  // row_group_kernel up to this length
 constexpr int kMaxSplit = 4;       // one block per row up to 256*4*4 floats
 
 enum class RowOp { kSoftmax, kRms, kLayer };
@@ -60,13 +57,9 @@ __device__ __forceinline__ float finish_scale_ln(float ssd, std::int64_t n, floa
   return 1.0F / sqrtf(denom);
 }
 
-// Rows of at most 64 elements, several per wave: a row takes L lanes (the
-// power of two at or above n / 4), each holding one float4 at column 4k
-// (vector rows) or four floats at k, k + L, k + 2L, k + 3L (scalar rows),
-// and a wave holds 64 / L rows. Row statistics are butterflies over the L
-// lanes of the row (both partners add the same operands, so the row's lanes
-// agree bit for bit); the per-element steps are those of the other row
-// kernels.
+// Statistics of a row held by a group of L lanes (L a power of two, aligned
+// groups): butterflies in which both partners add the same operands, so the
+// row's lanes agree bit for bit.
 __device__ __forceinline__ float group_sum(float v, int L) {
   for (int offset = L >> 1; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
   return v;
@@ -82,115 +75,6 @@ __device__ __forceinline__ bool group_all(bool v, int L) {
   int f = v ? 1 : 0;
   for (int offset = L >> 1; offset > 0; offset >>= 1) f &= __shfl_xor(f, offset, kWave);
   return f != 0;
-}
-
-template <RowOp kOp, bool kVec>
-__global__ __launch_bounds__(256) void row_packed_kernel(RowArgs a, int L) {
-  const int lane = threadIdx.x & 63;
-  const int k = lane & (L - 1);
-  const int rows_per_wave = 64 / L;
-  const int ni = static_cast<int>(a.n);
-  auto column = [&](int q) -> int { return kVec ? 4 * k + q : k + L * q; };
-  auto valid = [&](int q) -> bool { return column(q) < ni; };
-  const bool has_g = a.gamma != nullptr, has_b = a.beta != nullptr;
-  float g[4], b[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    g[q] = has_g && valid(q) ? a.gamma[column(q)] : 1.F;
-    b[q] = has_b && valid(q) ? a.beta[column(q)] : 0.F;
-  }
-  const std::int64_t per_pass = static_cast<std::int64_t>(gridDim.x) * 4 * rows_per_wave;
-  const std::int64_t passes = (a.rows + per_pass - 1) / per_pass;
-  // Every lane runs every pass (the butterflies need the whole group);
-  // rows past the end are masked.
-  for (std::int64_t pass = 0; pass < passes; ++pass) {
-    const std::int64_t row = pass * per_pass + (static_cast<std::int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) *
-                                                   rows_per_wave + lane / L;
-    const bool live = row < a.rows;
-    const float* __restrict__ x = a.x + (live ? row : 0) * a.n;
-    float* __restrict__ out = a.out + row * a.n;
-    float v[4] = {0.F, 0.F, 0.F, 0.F};
-    if (live) {
-      if constexpr (kVec) {
-        if (valid(0)) {
-          const float4_t t = stream_load(reinterpret_cast<const float4_t*>(x + column(0)));
-          v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
-        }
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (valid(q)) v[q] = x[column(q)];
-      }
-    }
-    if constexpr (kOp == RowOp::kSoftmax) {
-      float m = -__builtin_inff();
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (valid(q) && (is_nan(v[q]) || v[q] > m)) m = v[q];
-      m = group_max_nan(m, L);
-      float sum = 0.F;
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (valid(q)) {
-          v[q] = exp_softmax(v[q] - m);
-          sum += v[q];
-        }
-      const float inv = 1.0F / group_sum(sum, L);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) v[q] = v[q] * inv;
-    } else if constexpr (kOp == RowOp::kRms) {
-      float sum = 0.F;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float t = v[q] * v[q];
-        sum += t;  // masked elements are zero
-      }
-      const float scale = 1.0F / sqrtf(group_sum(sum, L) / static_cast<float>(ni) + a.eps);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) v[q] = v[q] * scale;
-    } else {
-      const float first = live ? x[0] : 0.F;
-      float sum = 0.F;
-      bool equal = true;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        sum += v[q];
-        if (valid(q)) equal = equal && v[q] == first;
-      }
-      const float mean = group_sum(sum, L) / static_cast<float>(ni);
-      float d2 = 0.F;
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (valid(q)) {
-          const float d = v[q] - mean;
-          d2 += d * d;
-        }
-      bool nan_row = false;
-      const float scale = finish_scale_ln(group_sum(d2, L), ni, a.eps, nan_row);
-      const bool const_row = group_all(equal, L) && __builtin_isfinite(first);
-      const bool special = const_row || nan_row;
-      const float special_value = const_row && a.eps != 0.F ? 0.F : __builtin_nanf("");
-#pragma unroll
-      for (int q = 0; q < 4; ++q) v[q] = special ? special_value : (v[q] - mean) * scale;
-    }
-    if (!live) continue;
-    // Affine steps (multiply then add, each rounded) and the store.
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (has_g) v[q] = v[q] * g[q];
-      if (has_b) v[q] = v[q] + b[q];
-    }
-    if constexpr (kVec) {
-      if (valid(0)) {
-        const float4_t t = {v[0], v[1], v[2], v[3]};
-        __builtin_nontemporal_store(t, reinterpret_cast<float4_t*>(out + column(0)));
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (valid(q)) out[column(q)] = v[q];
-    }
-  }
 }
 
 // One 256-thread block per row, the row cached in registers: thread t holds
@@ -1429,7 +1313,7 @@ void resident_variants(F&& f) {
   }
 }
 
-// Rows of 65-1536 elements at any alignment: L lanes per row, 64 / L rows
+// Rows of 1-1536 elements at any alignment: L lanes per row, 64 / L rows
 // per wave; lane l of a row's group holds elements 4l + 4Lu .. + 3 (u < kV),
 // read with 16-byte buffer loads (4-byte alignment suffices) through a
 // resource based at the group's first row. Elements past the row are
@@ -1638,10 +1522,22 @@ void launch_group(const RowArgs& a, hipStream_t s) {
   }
 }
 
-// (L, kV): the smallest that covers the row, as for the packed reductions.
+// (L, kV): up to 64 elements one float4 per lane (L = n / 4 rounded up to a
+// power of two, 64 / L rows per wave), then the smallest that covers the row,
+// as for the packed reductions. Against lanes of one float4 at k, k + L, ...
+// for unaligned rows: [1000000, 50] softmax 105.0 -> 93.5 us, [1000000, 33]
+// 75.7 -> 63.9; aligned, with the default cache policy against the
+// non-temporal one: [4194304, 8] LayerNorm 53.1 -> 44.8 us, softmax 45.3 ->
+// 43.4. Two float4 per lane from 33 elements lost at 50 and 63 (105 -> 112
+// and 121 -> 138 us).
 template <RowOp kOp>
 void launch_group_for(const RowArgs& a, std::int64_t n, hipStream_t s) {
-  if (n <= 128) launch_group<kOp, 8, 4>(a, s);
+  if (n <= 4) launch_group<kOp, 1, 1>(a, s);
+  else if (n <= 8) launch_group<kOp, 2, 1>(a, s);
+  else if (n <= 16) launch_group<kOp, 4, 1>(a, s);
+  else if (n <= 32) launch_group<kOp, 8, 1>(a, s);
+  else if (n <= 64) launch_group<kOp, 16, 1>(a, s);
+  else if (n <= 128) launch_group<kOp, 8, 4>(a, s);
   else if (n <= 192) launch_group<kOp, 16, 3>(a, s);
   else if (n <= 256) launch_group<kOp, 16, 4>(a, s);
   else if (n <= 384) launch_group<kOp, 32, 3>(a, s);
@@ -1663,18 +1559,8 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
   const bool vec = reduce % 4 == 0 && aligned16(a.x) && aligned16(a.out) &&
                    (a.gamma == nullptr || aligned16(a.gamma)) && (a.beta == nullptr || aligned16(a.beta));
   const std::int64_t per = (reduce + 1023) / 1024;    // per thread, one block per row
-  if (reduce > kPackedMax && reduce <= kGroupMax) {
+  if (reduce <= kGroupMax) {
     launch_group_for<kOp>(a, reduce, s);
-  } else if (reduce <= kPackedMax) {
-    // Several rows per wave, L lanes per row.
-    int L = 1;
-    while (4 * L < reduce) L *= 2;
-    const std::int64_t waves = (outer + 64 / L - 1) / (64 / L);
-    const unsigned grid = grid_for(waves, 4, kPackedBlocks);
-    if (vec)
-      hipLaunchKernelGGL((row_packed_kernel<kOp, true>), dim3(grid), dim3(256), 0, s, a, L);
-    else
-      hipLaunchKernelGGL((row_packed_kernel<kOp, false>), dim3(grid), dim3(256), 0, s, a, L);
   } else if (reduce > 3072 && reduce <= 4 * kResidentThreads * 8 &&
            (reduce > 4096 || (a.gamma == nullptr && a.beta == nullptr))) {
     // Rows of 3073-16384 floats: held in registers by row_resident_kernel,

@@ -969,9 +969,9 @@ def test_empty_and_scalar(cx):
 
 
 # ------------------------------------------------------------- row ops
-# Widths cover each row kernel: rows of at most 64 packed several per wave,
-# rows of 65-1536 in lane groups (8 to 64 lanes, 1 to 6 float4 per lane, any
-# alignment, partial last groups), one 256-thread block per row (1537-3072
+# Widths cover each row kernel: rows of 1-1536 in lane groups (1 to 64
+# lanes, 1 to 6 float4 per lane, any alignment, partial last groups), one
+# 256-thread block per row (1537-3072
 # floats, 4096 with a weight or bias: aligned full and masked, and
 # unaligned), one 512-thread block per row holding 3073-16384
 # floats in 4 or 8 float4 per thread (aligned and unaligned) and wider rows in
@@ -1000,12 +1000,13 @@ def test_row_ops_random(cx, shape, axis):
                  oracle.affine_norm(x, axis, 1e-5, g, None, rms=True), 1e-5, 1e-5, "affine rmsnorm")
 
 
-@pytest.mark.parametrize("width", [65, 100, 127, 129, 130, 193, 200, 257, 385, 500, 513, 769, 1024, 1025, 1536, 1537,
+@pytest.mark.parametrize("width", [2, 3, 5, 8, 13, 16, 17, 31, 33, 50, 63, 64,
+                                   65, 100, 127, 129, 130, 193, 200, 257, 385, 500, 513, 769, 1024, 1025, 1536, 1537,
                                    2048, 3001, 3073, 4095, 4096, 8191, 8192, 16383, 16384, 16385, 20003,
                                    24577, 32000, 40001, 40961, 70000, 90113, 100003, 128256, 130816, 131000])
 def test_row_ops_special_values_wide_rows(cx, width):
-    # Non-finite values in rows of every width class (rows of 65-1536 in
-    # groups of 8 to 64 lanes at 1 to 6 float4 per lane, any alignment, with
+    # Non-finite values in rows of every width class (rows of 2-1536 in
+    # groups of 1 to 64 lanes at 1 to 6 float4 per lane, any alignment, with
     # row 1's last float4 reading row 2's leading -inf; split rows at 2 and 4
     # float4 per thread, aligned and unaligned, rows of
     # 3073-16384 held at 4 or 8 float4 per thread by a 512-thread block
@@ -1070,7 +1071,7 @@ def test_row_ops_special_values_wide_rows(cx, width):
 
 
 @pytest.mark.parametrize("eps", [0.0, 1e-45, 1e-5, 1e30])
-@pytest.mark.parametrize("width", [100, 130, 512, 1025, 1537, 4096, 3001, 8192, 16384, 20003, 32000, 100003])
+@pytest.mark.parametrize("width", [5, 33, 100, 130, 512, 1025, 1537, 4096, 3001, 8192, 16384, 20003, 32000, 100003])
 def test_constant_rows(cx, eps, width):
     x = np.full((5, width), 2.5, np.float32)
     x[3] = -7.0
