@@ -1262,7 +1262,7 @@ def test_binary_two_axis_streams(cx, ls, rs):
 
 @pytest.mark.parametrize("batch,m,n,k,trans", [(65536, 8, 8, 8, False), (300, 16, 16, 16, True), (64, 64, 64, 64, False),
                                                (100, 3, 5, 7, False), (77, 1, 64, 33, True), (129, 64, 1, 2, False),
-                                               (64, 17, 29, 64, True)])
+                                               (64, 17, 29, 64, True), (1000, 5, 7, 3, False)])
 def test_matmul_tiny_batched(cx, batch, m, n, k, trans):
     # Many small products (items up to 64 x 64 x 64, at least 64 of them)
     # stage whole items in LDS, several per block, and sum each output's k in
@@ -1285,6 +1285,19 @@ def test_matmul_tiny_batched(cx, batch, m, n, k, trans):
         got = cx.linear(hc, cx.tensor(w, device="hip"), cx.tensor(bias, device="hip")).numpy()
         assert_matmul(got, (clean.astype(np.float64) @ w.T.astype(np.float64)) + bias, clean.reshape(-1, k), w.T,
                       f"tiny linear {batch}x{m}x{n}x{k}")
+
+
+def test_matmul_tiny_shared_a(cx):
+    # One A shared by 300 items of a [k, n] B (A's batch stride 0; a shared
+    # B would fold into one 2-D product instead): not a dense batch, so items
+    # are staged one element at a time through their offsets, where dense
+    # batches (the cases above without a transposed B) stage two contiguous
+    # runs with 16-byte loads. Bit-exact against the sequential loop.
+    rng = np.random.default_rng(91)
+    a = rng.standard_normal((1, 5, 7)).astype(np.float32)
+    b = rng.standard_normal((300, 7, 6)).astype(np.float32)
+    assert_bits(cx.matmul(cx.tensor(a, device="hip"), cx.tensor(b, device="hip")).numpy(), oracle.matmul(a, b),
+                "tiny shared a")
 
 
 @pytest.mark.parametrize("m,n,k,trans", [(4096, 4096, 4, False), (3000, 1028, 16, True), (20000, 16, 16, False),
