@@ -470,7 +470,8 @@ def extra_benches(steps: int, warmup: int):
     short, unaligned, staged in LDS or resident in registers; the matrix-vector,
     streaming, vector-matrix, short-K and tiny-item GEMM routes), timed like
     the secondary lines against HBM (algorithmic bytes: each input read once
-    plus the output), for the kernel traces of the profiles. No CPU legs."""
+    plus the output), and the 32x64-tile GEMM against the fp32 MFMA peak, for
+    the kernel traces of the profiles. No CPU legs."""
     out = []
     rng = np.random.default_rng(13)
 
@@ -491,7 +492,7 @@ def extra_benches(steps: int, warmup: int):
         for op in ("sum", "max"):
             add(f"reduce_{op}_f32_{rows}x{cols}", lambda s, op=op, rows=rows, cols=cols, nxt=nxt, res=res: capi.reduce(
                 op, capi.TCX_FLOAT32, nxt()[0].ptr, res.ptr, rows, cols, 1, None, s), nbytes + rows * 4)
-    for rows, cols in ((8192, 8191), (4096, 20001), (1000, 100003)):
+    for rows, cols in ((8192, 8191), (4096, 20001), (1000, 100003), (100000, 130), (8192, 1500)):
         nxt, nbytes = operands((rows, cols))
         g = capi.DeviceArray.from_numpy(rng.uniform(0.5, 1.5, cols).astype(np.float32))
         b = capi.DeviceArray.from_numpy(rng.uniform(-0.1, 0.1, cols).astype(np.float32))
@@ -519,6 +520,24 @@ def extra_benches(steps: int, warmup: int):
             da, db = nxt()
             capi.gemm(da.ptr, db.ptr, c.ptr, desc, s, ws)
         add(f"gemm_{name}", launch, nbytes + batch * m * n * 4)
+    # The 32x64-tile route (more than 256 tiles of 64x64 whose last round
+    # holds at most 128): 1100^3, 324 such tiles, rated in TFLOP/s.
+    m = n = k = 1100
+    nxt, _ = operands((m, k), (k, n))
+    desc = capi.gemm_desc(m, n, k)
+    c = capi.DeviceArray((m, n))
+
+    def launch_half(s, nxt=nxt, c=c, desc=desc):
+        da, db = nxt()
+        capi.gemm(da.ptr, db.ptr, c.ptr, desc, s)
+    name = "gemm_half_1100x1100x1100"
+    total, per, warm = timed(launch_half, steps, warmup, name=name)
+    avg, flops = total / steps, 2 * m * n * k
+    out.append({"name": name, "unit": "TFLOP/s", "value": flops / (avg * 1e-3) / 1e12, "kernel_avg_ms": avg,
+                "kernel_median_ms": statistics.median(per), "achieved": flops / (avg * 1e-3) / 1e12,
+                "peak": PEAK_FP32_MFMA / 1e12, "frac": flops / (avg * 1e-3) / PEAK_FP32_MFMA,
+                "flop_per_launch": flops, "warmup_launches": warm})
+    log(f"{name}: {out[-1]['achieved']:.1f} TFLOP/s ({out[-1]['frac']:.1%})")
     return out
 
 
