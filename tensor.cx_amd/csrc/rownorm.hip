@@ -1320,13 +1320,14 @@ void resident_variants(F&& f) {
 // masked to zero; a float4 wholly past it is not loaded, and the one that
 // crosses the row's end is stored element by element (whole float4s take
 // 16-byte buffer stores), so no other row's elements are written. The
-// waves are persistent (as many blocks as stay resident) and load their
-// next row group into a second register set before the current group's
-// reductions. Row statistics are butterflies over the group's L lanes, in
-// the per-element steps of the other row kernels. Loads and stores take the
-// default cache policy: with the non-temporal one, whose partial-line writes
-// these rows make at every row boundary, [100000, 100] softmax ran 28.1
-// against 15.9 us and [100000, 130] 30.1 against 20.1 us on MI355X.
+// waves are persistent (as many blocks as stay resident); at two shapes
+// (below) they load their next row group into a second register set before
+// the current group's reductions. Row statistics are butterflies over the
+// group's L lanes, in the per-element steps of the other row kernels. Loads
+// and stores take the default cache policy: with the non-temporal one, whose
+// partial-line writes these rows make at every row boundary, [100000, 100]
+// softmax ran 26.7 against 17.0 us and [1000000, 50] 108.1 against 89.4 us
+// on MI355X (inputs rotated past the Infinity Cache).
 template <RowOp kOp, int kL, int kV, int kAff>
 __global__ __launch_bounds__(256) void row_group_kernel(RowArgs a) {
   constexpr int kRows = 64 / kL;
@@ -1373,10 +1374,20 @@ __global__ __launch_bounds__(256) void row_group_kernel(RowArgs a) {
   };
   const std::int64_t step = static_cast<std::int64_t>(gridDim.x) * 4;
   std::int64_t t = static_cast<std::int64_t>(blockIdx.x) * 4 + wave;
-  float v[kV][4], nv[kV][4];
-  if (t < groups) load(t, v);
+  // The next group's loads go out before this group's reductions at 8 lanes
+  // x 4 float4 and 64 x 6; other shapes measured as fast or faster loading in
+  // place (with inputs rotated past the Infinity Cache: [100000, 100] softmax
+  // 16.9 against 20.6 us with and without, [8192, 1500] 19.1 against 20.8;
+  // [16384, 1023] 27.0 against 25.0, [25000, 700] 26.9 against 25.4).
+  constexpr bool kPrefetch = (kL == 8 && kV == 4) || kV == 6;
+  float v[kV][4], nv[kPrefetch ? kV : 1][4];
+  if (kPrefetch && t < groups) load(t, v);
   for (; t < groups; t += step) {
-    if (t + step < groups) load(t + step, nv);
+    if constexpr (kPrefetch) {
+      if (t + step < groups) load(t + step, nv);
+    } else {
+      load(t, v);
+    }
     const int nrows = rows_in(t);
     const bool live = gr < nrows;
     auto valid = [&](int u, int e) { return col(u) + e < n; };
@@ -1480,10 +1491,12 @@ __global__ __launch_bounds__(256) void row_group_kernel(RowArgs a) {
                                                                 0);
       }
     }
+    if constexpr (kPrefetch) {
 #pragma unroll
-    for (int u = 0; u < kV; ++u)
+      for (int u = 0; u < kV; ++u)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[u][e] = nv[u][e];
+        for (int e = 0; e < 4; ++e) v[u][e] = nv[u][e];
+    }
     // Keep later groups' loads from being hoisted into this group's live range.
     asm volatile("" ::: "memory");
   }
@@ -1524,11 +1537,12 @@ void launch_group(const RowArgs& a, hipStream_t s) {
 
 // (L, kV): up to 64 elements one float4 per lane (L = n / 4 rounded up to a
 // power of two, 64 / L rows per wave), then the smallest that covers the row,
-// as for the packed reductions. Against lanes of one float4 at k, k + L, ...
-// for unaligned rows: [1000000, 50] softmax 105.0 -> 93.5 us, [1000000, 33]
-// 75.7 -> 63.9; aligned, with the default cache policy against the
-// non-temporal one: [4194304, 8] LayerNorm 53.1 -> 44.8 us, softmax 45.3 ->
-// 43.4. Two float4 per lane from 33 elements lost at 50 and 63 (105 -> 112
+// as for the packed reductions, except 193-256 at 32 x 2 ([65536, 200]
+// softmax 24.0 -> 20.0 us against 16 x 4). Against lanes of one float4 (or
+// four floats at k, k + L, ... for unaligned rows) with non-temporal loads
+// and stores, inputs rotated past the Infinity Cache: [1000000, 50] softmax
+// 105.7 -> 93.9 us, [4194304, 8] LayerNorm 53.0 -> 44.9, softmax 45.6 ->
+// 42.8. Two float4 per lane from 33 elements lost at 50 and 63 (105 -> 112
 // and 121 -> 138 us).
 template <RowOp kOp>
 void launch_group_for(const RowArgs& a, std::int64_t n, hipStream_t s) {
@@ -1539,7 +1553,7 @@ void launch_group_for(const RowArgs& a, std::int64_t n, hipStream_t s) {
   else if (n <= 64) launch_group<kOp, 16, 1>(a, s);
   else if (n <= 128) launch_group<kOp, 8, 4>(a, s);
   else if (n <= 192) launch_group<kOp, 16, 3>(a, s);
-  else if (n <= 256) launch_group<kOp, 16, 4>(a, s);
+  else if (n <= 256) launch_group<kOp, 32, 2>(a, s);
   else if (n <= 384) launch_group<kOp, 32, 3>(a, s);
   else if (n <= 512) launch_group<kOp, 32, 4>(a, s);
   else if (n <= 768) launch_group<kOp, 64, 3>(a, s);
