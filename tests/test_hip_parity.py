@@ -982,7 +982,7 @@ def test_empty_and_scalar(cx):
                                         ((5, 4100), 1), ((2, 12288), 1), ((3, 16384), 1), ((2, 16383), 1),
                                         ((1000, 1028), 1), ((3, 5001), 1), ((2, 9999), 1), ((9, 130), 1),
                                         ((17, 100), 1), ((33, 257), 1), ((5, 1536), 1), ((3, 1537), 1),
-                                        ((1001, 65), 1)])
+                                        ((1001, 65), 1), ((3, 30001), 1)])
 def test_row_ops_random(cx, shape, axis):
     rng = np.random.default_rng(13)
     x = (rng.standard_normal(shape) * 3).astype(np.float32)
