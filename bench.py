@@ -501,6 +501,14 @@ def extra_benches(steps: int, warmup: int):
             nxt()[0].ptr, y.ptr, rows, cols, 1, s), 2 * nbytes)
         add(f"layernorm_affine_{rows}x{cols}", lambda s, rows=rows, cols=cols, nxt=nxt, y=y, g=g, b=b: capi.layernorm(
             nxt()[0].ptr, g.ptr, b.ptr, y.ptr, rows, cols, 1, 1e-5, s), 2 * nbytes + 2 * cols * 4)
+    # RMSNorm with a weight on rows held at 20 float4 per thread (the
+    # two-phase weighted write).
+    rows, cols = 4096, 32000
+    nxt, nbytes = operands((rows, cols))
+    g = capi.DeviceArray.from_numpy(rng.uniform(0.5, 1.5, cols).astype(np.float32))
+    y = capi.DeviceArray((rows, cols))
+    add(f"rmsnorm_weight_{rows}x{cols}", lambda s, rows=rows, cols=cols, nxt=nxt, y=y, g=g: capi.rmsnorm(
+        nxt()[0].ptr, g.ptr, y.ptr, rows, cols, 1, 1e-5, s), 2 * nbytes + cols * 4)
     # GEMM routes: (name, m, n, k, batch, B transposed)
     for name, m, n, k, batch, trans in (("gemv_1x4096x4096_linear", 1, 4096, 4096, 1, True),
                                         ("stream_16x4096x4096_linear", 16, 4096, 4096, 1, True),
