@@ -20,7 +20,7 @@ import pytest
 
 import oracle
 from conftest import require_gpu
-from hip_cases import assert_close
+from hip_cases import SUM_BAR, assert_bits, assert_close, sum_error
 
 pytestmark = pytest.mark.gpu
 
@@ -196,6 +196,70 @@ def test_column_row_ops_unaligned_and_unsplit(capi):
     with pytest.raises(capi.HipError):
         capi.softmax_ws(dx.ptr, out.ptr, outer, rows, inner, small)
 
+
+
+def test_strided_random_shapes_and_bases(capi):
+    # Seeded random [outer, R, inner] inputs reduced and normalised over the
+    # middle axis through the C ABI: R and inner log-uniform (1-20000 rows,
+    # 2-9000 columns, so column tiles narrower than a wave, partial tiles,
+    # unsplit and split rows all occur), bases 0-3 floats past a 16-byte
+    # boundary, the row ops with and without a workspace. Softmax, RMSNorm +
+    # weight and LayerNorm + weight/bias meet the row-op bar, widened by the
+    # oracle's own distance from float64 truth, against both truth and the
+    # oracle: the reference's float32 steps drift from float64 where a few
+    # terms dominate a sum or where x - mean cancels (two nearly equal
+    # elements), and the kernel may drift as far. Max and argmax are
+    # bit-exact, sums within the sum bar.
+    rng = np.random.default_rng(37)
+    failures = []
+    for case in range(40):
+        R = int(np.exp(rng.uniform(0.0, np.log(20000.0))))
+        inner = int(np.exp(rng.uniform(np.log(2.0), np.log(9000.0))))
+        outer = int(max(1, min(int(rng.integers(1, 9)), 2_000_000 // (R * inner))))
+        if R * inner > 2_000_000:
+            R = max(1, 2_000_000 // inner)
+        off, ws = int(rng.integers(0, 4)), case % 2 == 1
+        n = outer * R * inner
+        flat = (rng.standard_normal(n + off) * 3).astype(np.float32)
+        x = flat[off:].reshape(outer, R, inner)
+        g = rng.uniform(0.5, 1.5, R).astype(np.float32)
+        b = rng.uniform(-0.1, 0.1, R).astype(np.float32)
+        dx, dg, db = (capi.DeviceArray.from_numpy(t) for t in (flat, g, b))
+        out = capi.DeviceArray((n + off,))
+        xp, op_ = dx.ptr + 4 * off, out.ptr + 4 * off
+        context = f"case {case}: [{outer}, {R}, {inner}] base +{off} floats workspace={ws}"
+        x64 = x.astype(np.float64)
+        g64, b64 = g.astype(np.float64)[None, :, None], b.astype(np.float64)[None, :, None]
+        e = np.exp(x64 - x64.max(axis=1, keepdims=True))
+        mean = x64.mean(axis=1, keepdims=True)
+        ln = (x64 - mean) / np.sqrt(((x64 - mean) ** 2).mean(axis=1, keepdims=True) + 1e-5)
+        rms = x64 / np.sqrt((x64 * x64).mean(axis=1, keepdims=True) + 1e-5)
+        cases = {"softmax": (None, None, oracle.softmax(x, 1), e / e.sum(axis=1, keepdims=True)),
+                 "rmsnorm": (dg.ptr, None, oracle.affine_norm(x, 1, 1e-5, g, None, rms=True), rms * g64),
+                 "layernorm": (dg.ptr, db.ptr, oracle.affine_norm(x, 1, 1e-5, g, b), ln * g64 + b64)}
+        try:
+            for op, (gp, bp, expected, truth) in cases.items():
+                run_capi(capi, op, xp, op_, outer, R, inner, gp, bp, ws)
+                got = out.numpy()[off:].reshape(outer, R, inner)
+                drift = float(np.max(np.abs(expected - truth) / np.maximum(np.abs(truth), 1e-30)))
+                assert_close(got, truth, 1e-5 + drift, 1e-5, f"{op} vs float64 {context} (oracle drift {drift:.1e})")
+                assert_close(got, expected, 1e-5 + drift, 1e-5, f"{op} {context} (oracle drift {drift:.1e})")
+            res = capi.DeviceArray((outer * inner,))
+            for op in ("max", "argmax", "sum"):
+                workspace = capi.reduce_workspace(op, capi.TCX_FLOAT32, outer, R, inner)
+                capi.reduce(op, capi.TCX_FLOAT32, xp, res.ptr, outer, R, inner, workspace)
+                capi.synchronize()
+                got = res.numpy().reshape(outer, inner)
+                if op == "max":
+                    assert_bits(got, oracle.max(x, 1), f"max {context}")
+                elif op == "argmax":
+                    assert_bits(got.view(np.int32), oracle.argmax(x, 1), f"argmax {context}")
+                else:
+                    err = sum_error(got, oracle.sum(x, 1), x, outer, R, inner)
+                    assert err <= SUM_BAR, f"sum {context}: {err:.3e}"
+        except AssertionError as error:
+            failures.append(str(error))
+    assert not failures, "\n".join(failures[:10])
 
 
 @pytest.mark.parametrize("width", [1, 2, 3, 4, 5, 7, 8, 16, 31, 32, 33, 64, 100, 127, 128])

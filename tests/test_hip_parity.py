@@ -1000,6 +1000,78 @@ def test_row_ops_random(cx, shape, axis):
                  oracle.affine_norm(x, axis, 1e-5, g, None, rms=True), 1e-5, 1e-5, "affine rmsnorm")
 
 
+@pytest.fixture(scope="module")
+def capi():
+    require_gpu()
+    import tensorcx_hip_capi
+    return tensorcx_hip_capi
+
+
+def test_row_ops_and_reductions_random_widths_and_bases(capi):
+    # Seeded random contiguous rows through the C ABI: widths log-uniform
+    # over 1-140000 (every width class of the row kernels, from lane groups
+    # to rows held in registers and LDS), row counts, and bases 0-3 floats
+    # past a 16-byte boundary (input and output alike, so rows start at every
+    # alignment). Softmax, RMSNorm + weight and LayerNorm + weight/bias meet
+    # the row-op bar, widened by the oracle's own distance from float64
+    # truth, against both truth and the oracle: on N(0, 9) rows a few large
+    # terms dominate the softmax denominator and the reference's sequential
+    # float32 sum drifts from float64 by up to 1e-4 relative (the kernel's
+    # tree sums measured within 1e-5 of truth here), as past 65536 elements
+    # for the wide rows above; two nearly equal elements make x - mean
+    # cancel in any float32 LayerNorm. Max and argmax are bit-exact, sums
+    # within the sum bar.
+    rng = np.random.default_rng(31)
+    failures = []
+    for case in range(48):
+        width = int(np.exp(rng.uniform(0.0, np.log(140000.0))))
+        rows = int(max(1, min(int(rng.integers(1, 400)), 2_000_000 // width)))
+        off = int(rng.integers(0, 4))
+        flat = (rng.standard_normal(rows * width + off) * 3).astype(np.float32)
+        x = flat[off:].reshape(rows, width)
+        g = rng.uniform(0.5, 1.5, width).astype(np.float32)
+        b = rng.uniform(-0.1, 0.1, width).astype(np.float32)
+        dx, dg, db = (capi.DeviceArray.from_numpy(t) for t in (flat, g, b))
+        out = capi.DeviceArray((rows * width + off,))
+        xp, op_ = dx.ptr + 4 * off, out.ptr + 4 * off
+        context = f"case {case}: [{rows}, {width}] base +{off} floats"
+        x64 = x.astype(np.float64)
+        e = np.exp(x64 - x64.max(axis=1, keepdims=True))
+        mean = x64.mean(axis=1, keepdims=True)
+        ln = (x64 - mean) / np.sqrt(((x64 - mean) ** 2).mean(axis=1, keepdims=True) + 1e-5)
+        rms = x64 / np.sqrt((x64 * x64).mean(axis=1, keepdims=True) + 1e-5)
+        runs = {"softmax": (lambda: capi.softmax(xp, op_, rows, width, 1), oracle.softmax(x, 1),
+                            e / e.sum(axis=1, keepdims=True)),
+                "rmsnorm + weight": (lambda: capi.rmsnorm(xp, dg.ptr, op_, rows, width, 1, 1e-5),
+                                     oracle.affine_norm(x, 1, 1e-5, g, None, rms=True), rms * g),
+                "layernorm + weight/bias": (lambda: capi.layernorm(xp, dg.ptr, db.ptr, op_, rows, width, 1, 1e-5),
+                                            oracle.affine_norm(x, 1, 1e-5, g, b), ln * g + b)}
+        try:
+            for name, (run, expected, truth) in runs.items():
+                run()
+                capi.synchronize()
+                got = out.numpy()[off:].reshape(rows, width)
+                drift = float(np.max(np.abs(expected - truth) / np.maximum(np.abs(truth), 1e-30)))
+                assert_close(got, truth, 1e-5 + drift, 1e-5, f"{name} vs float64 {context} (oracle drift {drift:.1e})")
+                assert_close(got, expected, 1e-5 + drift, 1e-5, f"{name} {context} (oracle drift {drift:.1e})")
+            res = capi.DeviceArray((rows,))
+            for op in ("max", "argmax", "sum"):
+                ws = capi.reduce_workspace(op, capi.TCX_FLOAT32, rows, width, 1)
+                capi.reduce(op, capi.TCX_FLOAT32, xp, res.ptr, rows, width, 1, ws)
+                capi.synchronize()
+                got = res.numpy()
+                if op == "max":
+                    assert_bits(got, oracle.max(x, 1), f"max {context}")
+                elif op == "argmax":
+                    assert_bits(got.view(np.int32), oracle.argmax(x, 1), f"argmax {context}")
+                else:
+                    err = sum_error(got, oracle.sum(x, 1), x, rows, width, 1)
+                    assert err <= 1e-5, f"sum {context}: {err:.3e}"
+        except AssertionError as error:
+            failures.append(str(error))
+    assert not failures, "\n".join(failures[:10])
+
+
 @pytest.mark.parametrize("width", [2, 3, 5, 8, 13, 16, 17, 31, 33, 50, 63, 64,
                                    65, 100, 127, 129, 130, 193, 200, 257, 385, 500, 513, 769, 1024, 1025, 1536, 1537,
                                    2048, 3001, 3073, 4095, 4096, 8191, 8192, 16383, 16384, 16385, 20003,
