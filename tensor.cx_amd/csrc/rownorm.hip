@@ -1611,7 +1611,9 @@ void launch_group(const RowArgs& a, hipStream_t s) {
 // and stores, inputs rotated past the Infinity Cache: [1000000, 50] softmax
 // 105.7 -> 93.9 us, [4194304, 8] LayerNorm 53.0 -> 44.9, softmax 45.6 ->
 // 42.8. Two float4 per lane from 33 elements lost at 50 and 63 (105 -> 112
-// and 121 -> 138 us).
+// and 121 -> 138 us); 8 x 5-6 for 129-192 and 16 x 5-6 for 257-384 lost
+// ([100000, 130] softmax 24.2 -> 26.6 us, [50000, 300] 22.9 -> 25.5,
+// [40000, 350] LayerNorm 21.9 -> 27.2) but at [65536, 180] softmax.
 template <RowOp kOp>
 void launch_group_for(const RowArgs& a, std::int64_t n, hipStream_t s) {
   if (n <= 4) launch_group<kOp, 1, 1>(a, s);
