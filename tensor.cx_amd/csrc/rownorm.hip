@@ -9,9 +9,10 @@
 // up to 3072 elements (4096 with an affine weight or bias) take one 256-thread
 // block per row (four waves, whose partial statistics meet in LDS). Longer
 // rows take one 512-thread block per row that holds the whole row in
-// registers, and past about 90 K floats in LDS too (row_resident_kernel, to
-// about 139 K floats); longer ones one 1024-thread block per row that reads it
-// once per pass (row_block_kernel).
+// registers, from about 41 K floats with the rest in LDS (two blocks per CU
+// to about 61 K, 69 K for LayerNorm; one, with more registers, past 90 K)
+// (row_resident_kernel, to about 139 K floats); longer ones one 1024-thread
+// block per row that reads it once per pass (row_block_kernel).
 // Strided rows (inner > 1) run
 // col_norm_kernel: column tiles whose waves fold per-column statistics over
 // runs of rows, then write the row from them in a second walk (rows split
@@ -21,6 +22,8 @@
 // sum, division; (x - mean) * scale; x * scale), each step rounded separately
 // (built with -ffp-contract=off). Statistics are summed in a fixed tree order,
 // which stays within allclose(rtol=1e-5, atol=1e-5) of the sequential sums.
+
+#include <algorithm>
 
 #include "common.hpp"
 
@@ -549,10 +552,16 @@ __device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, void* lds, 
 }
 
 // Waves per SIMD a block of P float4 per thread leaves room for: rows held in
-// 12 or 20 float4 per thread (at most 24576 or 40960 floats, no LDS) run
-// three or two blocks per CU, so one row's arithmetic overlaps another's
-// loads; 4 or 8 (rows of 3073 to 8192 or 16384 floats) four.
-constexpr int resident_waves_per_eu(int P) { return P <= 8 ? 8 : P <= 12 ? 6 : P <= 20 ? 4 : 2; }
+// 12 or 20 float4 per thread (at most 24576 or 40960 floats in registers,
+// up to kPairLdsChunks KB more in LDS) run three or two blocks per CU, so one
+// row's arithmetic overlaps another's loads, and so does 24 (LayerNorm rows
+// held partly in LDS); 4 or 8 (rows of 3073 to 8192 or 16384 floats) four.
+constexpr int resident_waves_per_eu(int P) { return P <= 8 ? 8 : P <= 12 ? 6 : P <= 24 ? 4 : 2; }
+
+// LDS per block (1 KB chunks of 64 float4) for rows held at 20 or 24 float4
+// per thread plus LDS: two blocks, with their static arrays, fit in the
+// 160 KB of a CU.
+constexpr int kPairLdsChunks = 79;
 
 template <RowOp kOp, int kAff, int P>
 __global__ __launch_bounds__(kResidentThreads) __attribute__((amdgpu_waves_per_eu(resident_waves_per_eu(P))))
@@ -1692,6 +1701,16 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
           (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                     limit - 1024);
         });
+        const int pair_bytes = std::min(kPairLdsChunks * 1024, limit - 1024);
+        resident_variants<kOp, 20>([&](RowKernel kernel, int) {
+          (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    pair_bytes);
+        });
+        if constexpr (kOp == RowOp::kLayer)
+          resident_variants<kOp, 24>([&](RowKernel kernel, int) {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, pair_bytes);
+          });
       }
     }
     // Resident rows: LDS for the float4s past the registers' share, in whole
@@ -1705,11 +1724,32 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
           hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(outer)), dim3(kResidentThreads), lds_bytes, s, a);
       });
     };
+    // Rows past the registers of 20 (LayerNorm also 24) float4 per thread
+    // keep two blocks per CU with the rest in LDS, so one row's writes
+    // overlap another's reads, where that measured faster than one block of
+    // 44 float4 per CU (inputs rotated): softmax [2048, 50257] 170.1 -> 159.6
+    // us, [4096, 41000] 280.7 -> 250.0; LayerNorm + weight/bias [2048, 50257]
+    // 198.4 -> 169.2, [4096, 45000] 358.2 -> 291.5, at 24 [2048, 65536]
+    // 235.7 -> 210.5, [1024, 69000] 125.4 -> 116.2; RMSNorm + weight [2048,
+    // 50257] 166.3 -> 161.7. Plain RMSNorm lost 0.5-3 % ([4096, 45000] 274.9
+    // -> 282.3), softmax at 24 float4 lost at [2048, 65536] (205.1 -> 218.0)
+    // and RMSNorm + weight at 24 at [2048, 50257], so those keep 44.
+    const std::int64_t regs20 = static_cast<std::int64_t>(kResidentThreads) * 20;
+    const std::int64_t regs24 = static_cast<std::int64_t>(kResidentThreads) * 24;
+    const bool pair20 = kOp != RowOp::kRms || a.gamma != nullptr;
+    const std::int64_t pair_chunks = limit > 0 ? std::min<std::int64_t>(kPairLdsChunks, (limit - 1024) / 1024) : 0;
+    auto pair_bytes = [&](std::int64_t regs) {
+      return static_cast<unsigned>((reduce / 4 - regs + 63) / 64 * 1024);  // reduce / 4 > regs here
+    };
     if (reduce / 4 <= static_cast<std::int64_t>(kResidentThreads) * 12)
       launch_resident(std::integral_constant<int, 12>{}, 0U);
-    else if (reduce / 4 <= static_cast<std::int64_t>(kResidentThreads) * 20)
+    else if (reduce / 4 <= regs20)
       launch_resident(std::integral_constant<int, 20>{}, 0U);
-    else if (limit > 0 && resident_bytes <= limit - 1024)
+    else if (pair20 && reduce / 4 <= regs20 + 64 * pair_chunks)
+      launch_resident(std::integral_constant<int, 20>{}, pair_bytes(regs20));
+    else if (kOp == RowOp::kLayer && reduce / 4 > regs24 && reduce / 4 <= regs24 + 64 * pair_chunks) {
+      if constexpr (kOp == RowOp::kLayer) launch_resident(std::integral_constant<int, 24>{}, pair_bytes(regs24));
+    } else if (limit > 0 && resident_bytes <= limit - 1024)
       launch_resident(std::integral_constant<int, kResidentVec>{}, static_cast<unsigned>(resident_bytes));
     else
       hipLaunchKernelGGL((row_block_kernel<kOp>), dim3(static_cast<unsigned>(outer)), dim3(kRowBlockThreads), 0, s,
