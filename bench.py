@@ -492,7 +492,7 @@ def extra_benches(steps: int, warmup: int):
         for op in ("sum", "max"):
             add(f"reduce_{op}_f32_{rows}x{cols}", lambda s, op=op, rows=rows, cols=cols, nxt=nxt, res=res: capi.reduce(
                 op, capi.TCX_FLOAT32, nxt()[0].ptr, res.ptr, rows, cols, 1, None, s), nbytes + rows * 4)
-    for rows, cols in ((8192, 8191), (4096, 20001), (1000, 100003), (100000, 130), (8192, 1500)):
+    for rows, cols in ((8192, 8191), (4096, 20001), (1000, 100003), (100000, 130), (8192, 1500), (2048, 50257)):
         nxt, nbytes = operands((rows, cols))
         g = capi.DeviceArray.from_numpy(rng.uniform(0.5, 1.5, cols).astype(np.float32))
         b = capi.DeviceArray.from_numpy(rng.uniform(-0.1, 0.1, cols).astype(np.float32))
