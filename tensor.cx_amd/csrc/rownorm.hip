@@ -509,14 +509,15 @@ __global__ __launch_bounds__(kRowBlockThreads) void row_block_kernel(RowArgs a) 
   }
 }
 
-// Rows too long for one block's LDS and up to about 139 K floats: one
-// 512-thread block per row holds the whole row, its first 4 x 512 x
-// kResidentVec floats (after the elements before its first 16-byte boundary)
-// in registers, float4 k = t + 512 c in thread t's v[c], and the rest in LDS,
-// loaded straight from HBM (buffer_load ... lds) in 1 KB wave chunks, chunk j
-// by wave j mod 8, so that each lane reads back only what its own loads
-// wrote and no barrier is needed. A CU's registers (512 KB) and LDS (160 KB)
-// together hold such a row, so it is read from HBM once and written once.
+// Rows too long for one block's LDS and up to about 139 K floats: one block
+// of T threads per row (512, or 1024 for the widest softmax and RMSNorm
+// rows) holds the whole row, its first 4 T P floats (after the elements
+// before its first 16-byte boundary) in registers, float4 k = t + T c in
+// thread t's v[c], and the rest in LDS, loaded straight from HBM
+// (buffer_load ... lds) in 1 KB wave chunks, chunk j by wave j mod (T / 64),
+// so that each lane reads back only what its own loads wrote and no barrier
+// is needed. A CU's registers (512 KB) and LDS (160 KB) together hold such a
+// row, so it is read from HBM once and written once.
 //
 // One row per CU at a time leaves no other block to overlap the row's
 // arithmetic with its loads, so the first statistics pass takes each float4
@@ -563,10 +564,21 @@ constexpr int resident_waves_per_eu(int P) { return P <= 8 ? 8 : P <= 12 ? 6 : P
 // 160 KB of a CU.
 constexpr int kPairLdsChunks = 79;
 
-template <RowOp kOp, int kAff, int P>
-__global__ __launch_bounds__(kResidentThreads) __attribute__((amdgpu_waves_per_eu(resident_waves_per_eu(P))))
+// Softmax and RMSNorm rows past the two-block routes: 1024 threads of 24
+// float4 (16 waves per CU, 128 VGPRs) plus LDS, to 139008 floats. With
+// inputs rotated, against 512 threads of 44 float4: softmax [512, 128256]
+// 98.1 -> 91.9 us, [1000, 100003] 164.7 -> 157.5, [300, 130000] 77.0 ->
+// 66.3; RMSNorm [512, 128256] 94.8 -> 92.7, [2048, 70000] 210.7 -> 203.3;
+// RMSNorm + weight [512, 128256] 98.3 -> 97.3. LayerNorm spilled at 24
+// (12 dwords; [512, 128256] 104.3 -> 110.4 us) and at 22 float4 (4;
+// 102.2 -> 104.9) and keeps 512 threads of 44.
+constexpr int kWideThreads = 1024;
+constexpr int kWideVec = 24;
+
+template <RowOp kOp, int kAff, int P, int kT = kResidentThreads>
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(resident_waves_per_eu(P))))
 void row_resident_kernel(RowArgs a) {
-  constexpr int T = kResidentThreads, kWaves = T / 64;
+  constexpr int T = kT, kWaves = T / 64;
   constexpr bool kG = (kAff & kAffGamma) != 0, kB = (kAff & kAffBeta) != 0;
   extern __shared__ float4_t rest4[];
   __shared__ float scratch[kWaves];
@@ -754,7 +766,7 @@ void row_resident_kernel(RowArgs a) {
     auto vmax = [](float p, float q) { return __builtin_elementwise_maximum(p, q); };
     auto max4 = [&](float m, const float4_t& q) { return vmax(vmax(vmax(vmax(m, q.x), q.y), q.z), q.w); };
     // The reference maximum m0 is the wave's over its first float4s (v[0] is
-    // in range: the row has more than 512 float4s).
+    // in range: the row has more than T float4s).
     float m0 = wave_max_nan(max4(v[0].x, v[0]));
     float mt = m0, s0 = 0.F, s1 = 0.F;
     // Clamped at -150 (exp 0): -inf elements give exactly 0; a NaN is caught
@@ -1377,16 +1389,16 @@ int run_cols(const RowArgs& r, std::int64_t outer, std::int64_t reduce, std::int
 }
 
 // Calls f(kernel, affine bits) for each resident-row kernel of P float4 per
-// thread that the op launches.
+// thread (kT threads) that the op launches.
 using RowKernel = void (*)(RowArgs);
-template <RowOp kOp, int P, typename F>
+template <RowOp kOp, int P, int kT = kResidentThreads, typename F>
 void resident_variants(F&& f) {
-  f(static_cast<RowKernel>(&row_resident_kernel<kOp, 0, P>), 0);
+  f(static_cast<RowKernel>(&row_resident_kernel<kOp, 0, P, kT>), 0);
   if constexpr (kOp != RowOp::kSoftmax)
-    f(static_cast<RowKernel>(&row_resident_kernel<kOp, kAffGamma, P>), kAffGamma);
+    f(static_cast<RowKernel>(&row_resident_kernel<kOp, kAffGamma, P, kT>), kAffGamma);
   if constexpr (kOp == RowOp::kLayer) {
-    f(static_cast<RowKernel>(&row_resident_kernel<kOp, kAffBeta, P>), kAffBeta);
-    f(static_cast<RowKernel>(&row_resident_kernel<kOp, kAffGamma | kAffBeta, P>), kAffGamma | kAffBeta);
+    f(static_cast<RowKernel>(&row_resident_kernel<kOp, kAffBeta, P, kT>), kAffBeta);
+    f(static_cast<RowKernel>(&row_resident_kernel<kOp, kAffGamma | kAffBeta, P, kT>), kAffGamma | kAffBeta);
   }
 }
 
@@ -1697,10 +1709,16 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
       if (hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, device) != hipSuccess) bytes = 0;
       limit = bytes > 0 ? bytes : -1;
       if (limit > 0) {
-        resident_variants<kOp, kResidentVec>([&](RowKernel kernel, int) {
-          (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    limit - 1024);
-        });
+        if constexpr (kOp == RowOp::kLayer)
+          resident_variants<kOp, kResidentVec>([&](RowKernel kernel, int) {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, limit - 1024);
+          });
+        if constexpr (kOp != RowOp::kLayer)
+          resident_variants<kOp, kWideVec, kWideThreads>([&](RowKernel kernel, int) {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, limit - 1024);
+          });
         const int pair_bytes = std::min(kPairLdsChunks * 1024, limit - 1024);
         resident_variants<kOp, 20>([&](RowKernel kernel, int) {
           (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1749,11 +1767,27 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
       launch_resident(std::integral_constant<int, 20>{}, pair_bytes(regs20));
     else if (kOp == RowOp::kLayer && reduce / 4 > regs24 && reduce / 4 <= regs24 + 64 * pair_chunks) {
       if constexpr (kOp == RowOp::kLayer) launch_resident(std::integral_constant<int, 24>{}, pair_bytes(regs24));
-    } else if (limit > 0 && resident_bytes <= limit - 1024)
-      launch_resident(std::integral_constant<int, kResidentVec>{}, static_cast<unsigned>(resident_bytes));
-    else
+    } else if (kOp != RowOp::kLayer && limit > 0 &&
+               reduce / 4 <= static_cast<std::int64_t>(kWideThreads) * kWideVec + 64 * ((limit - 1024) / 1024)) {
+      // Softmax and RMSNorm rows past those: 1024 threads of 24 float4, the
+      // rest in LDS, 16 waves per CU where 512 threads of 44 float4 ran 8.
+      if constexpr (kOp != RowOp::kLayer) {
+        const std::int64_t past = reduce / 4 - static_cast<std::int64_t>(kWideThreads) * kWideVec;
+        const unsigned wide_bytes = static_cast<unsigned>(past > 0 ? (past + 63) / 64 * 1024 : 0);
+        resident_variants<kOp, kWideVec, kWideThreads>([&](RowKernel kernel, int k) {
+          if (k == aff)
+            hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(outer)), dim3(kWideThreads), wide_bytes, s, a);
+        });
+      }
+    } else if (kOp == RowOp::kLayer && limit > 0 && resident_bytes <= limit - 1024) {
+      // LayerNorm: 512 threads of 44 float4 (the wide route above covers
+      // longer softmax and RMSNorm rows than this would).
+      if constexpr (kOp == RowOp::kLayer)
+        launch_resident(std::integral_constant<int, kResidentVec>{}, static_cast<unsigned>(resident_bytes));
+    } else {
       hipLaunchKernelGGL((row_block_kernel<kOp>), dim3(static_cast<unsigned>(outer)), dim3(kRowBlockThreads), 0, s,
                          a);
+    }
     return check(hipGetLastError(), "row block kernel launch");
   }
   return check(hipGetLastError(), "row kernel launch");

@@ -1076,7 +1076,7 @@ def test_row_ops_and_reductions_random_widths_and_bases(capi):
                                    65, 100, 127, 129, 130, 193, 200, 257, 385, 500, 513, 769, 1024, 1025, 1536, 1537,
                                    2048, 3001, 3073, 4095, 4096, 8191, 8192, 16383, 16384, 16385, 20003,
                                    24577, 32000, 40001, 40961, 50257, 61184, 61185, 65536, 69376, 69377, 70000,
-                                   90113, 100003, 128256, 130816, 131000])
+                                   90113, 100003, 128256, 130816, 130817, 131000, 139008, 139009])
 def test_row_ops_special_values_wide_rows(cx, width):
     # Non-finite values in rows of every width class (rows of 2-1536 in
     # groups of 1 to 64 lanes at 1 to 6 float4 per lane, any alignment, with
@@ -1085,8 +1085,10 @@ def test_row_ops_special_values_wide_rows(cx, width):
     # 3073-16384 held at 4 or 8 float4 per thread by a 512-thread block
     # (without a weight or bias up to 4096), rows held in registers at 12 or
     # 20 float4 per thread (up to 24576 and 40960 floats), at 20 or (for
-    # LayerNorm) 24 with up to 79 KB of LDS (to 61184 and 69376 floats), at
-    # 44 (up to 90112) and then LDS (up to 130816), and re-read beyond): a
+    # LayerNorm) 24 with up to 79 KB of LDS (to 61184 and 69376 floats),
+    # softmax and RMSNorm at 24 float4 for 1024 threads plus LDS (to 139008),
+    # LayerNorm at 44 (up to 90112) and then LDS (up to 130816), and re-read
+    # beyond): a
     # NaN, +inf last, -inf first, a row of -inf, +inf with -inf, and a row
     # whose squares overflow to inf.
     rng = np.random.default_rng(23)
