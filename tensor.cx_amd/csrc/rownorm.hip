@@ -540,7 +540,6 @@ __global__ __launch_bounds__(kRowBlockThreads) void row_block_kernel(RowArgs a) 
 // The affine weight and bias (which of them is present is a template
 // argument) are read as float4 beside each output float4.
 constexpr int kResidentThreads = 512;
-constexpr int kResidentVec = 44;
 constexpr float kResidentShift = 32.0F;
 constexpr int kAffGamma = 1, kAffBeta = 2;
 
@@ -564,14 +563,16 @@ constexpr int resident_waves_per_eu(int P) { return P <= 8 ? 8 : P <= 12 ? 6 : P
 // 160 KB of a CU.
 constexpr int kPairLdsChunks = 79;
 
-// Softmax and RMSNorm rows past the two-block routes: 1024 threads of 24
-// float4 (16 waves per CU, 128 VGPRs) plus LDS, to 139008 floats. With
-// inputs rotated, against 512 threads of 44 float4: softmax [512, 128256]
-// 98.1 -> 91.9 us, [1000, 100003] 164.7 -> 157.5, [300, 130000] 77.0 ->
-// 66.3; RMSNorm [512, 128256] 94.8 -> 92.7, [2048, 70000] 210.7 -> 203.3;
-// RMSNorm + weight [512, 128256] 98.3 -> 97.3. LayerNorm spilled at 24
-// (12 dwords; [512, 128256] 104.3 -> 110.4 us) and at 22 float4 (4;
-// 102.2 -> 104.9) and keeps 512 threads of 44.
+// Rows past the two-block routes: 1024 threads of 24 float4 (16 waves per
+// CU, at most 128 VGPRs) plus LDS, to 139008 floats. With inputs rotated,
+// against the 512 threads of 44 float4 that held these rows before (the same
+// register share, 8 waves): softmax [512, 128256] 98.1 -> 91.9 us, [1000,
+// 100003] 164.7 -> 157.5, [300, 130000] 77.0 -> 66.3; RMSNorm [512, 128256]
+// 94.8 -> 92.7, [2048, 70000] 210.7 -> 203.3; RMSNorm + weight [512,
+// 128256] 98.3 -> 97.3; LayerNorm + weight/bias [512, 128256] 104.5 ->
+// 101.5, [2048, 70000] 234.7 -> 224.8, [256, 139000] (re-read before) 100.7
+// -> 59.2. LayerNorm fits only with the block folds' LDS reads fenced four
+// at a time (12 dwords spilled before: [512, 128256] 110.4 us).
 constexpr int kWideThreads = 1024;
 constexpr int kWideVec = 24;
 
@@ -602,7 +603,7 @@ void row_resident_kernel(RowArgs a) {
     return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, k * 16, 0, kNonTemporal));
   };
   // Thread t's index, copied opaquely for each pass over the register
-  // chunks: the compiler would otherwise keep all 44 chunk offsets live from
+  // chunks: the compiler would otherwise keep all P chunk offsets live from
   // the loads to the stores.
   auto opaque_t = [&] {
     int u = t;
@@ -633,7 +634,7 @@ void row_resident_kernel(RowArgs a) {
     for (int j = wave; j < lds_chunks; j += kWaves)
       if (first + 64 * j + lane < vectors) f(rest4[64 * j + lane]);
     // An opaque copy of full per pass: the per-chunk tests are then scalar
-    // compares used once, not 44 lane masks the compiler keeps across passes.
+    // compares used once, not P lane masks the compiler keeps across passes.
     int f_full = full;
     asm volatile("" : "+s"(f_full));
 #pragma unroll
@@ -651,9 +652,15 @@ void row_resident_kernel(RowArgs a) {
     s = wave_sum(s);
     if (lane == 0) scratch[wave] = s;
     __syncthreads();
+    // The waves' sums in wave order, at most four LDS reads in flight: all
+    // sixteen at once (1024 threads) kept 16 VGPRs live beside the row and
+    // made LayerNorm spill.
     float r = scratch[0];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) r += scratch[w];
+    for (int w = 1; w < kWaves; ++w) {
+      r += scratch[w];
+      if (w % 4 == 3) asm volatile("" ::: "memory");
+    }
     __syncthreads();  // scratch is reused
     return r;
   };
@@ -818,7 +825,10 @@ void row_resident_kernel(RowArgs a) {
     __syncthreads();
     m = scratch[0];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) m = vmax(m, scratch[w]);
+    for (int w = 1; w < kWaves; ++w) {
+      m = vmax(m, scratch[w]);
+      if (w % 4 == 3) asm volatile("" ::: "memory");
+    }
     __syncthreads();
     if (!__builtin_isfinite(m)) {
       write([](float) { return __builtin_nanf(""); });
@@ -853,7 +863,10 @@ void row_resident_kernel(RowArgs a) {
     const float mean = block_sum(s0 + s1) / static_cast<float>(n);
     bool all_equal = true;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) all_equal = all_equal && equal_waves[w] != 0;
+    for (int w = 0; w < kWaves; ++w) {
+      all_equal = all_equal && equal_waves[w] != 0;
+      if (w % 4 == 3) asm volatile("" ::: "memory");
+    }
     if (all_equal && __builtin_isfinite(x0)) {
       // An all-equal finite row: 0, or NaN when eps is 0 (cpu_backend.cpp:205-213).
       const float fill = a.eps == 0.F ? __builtin_nanf("") : 0.F;
@@ -1694,11 +1707,12 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
   } else if (per <= 2) return launch_split<kOp, 2>(a, vec, s);
   else if (per <= kMaxSplit) return launch_split<kOp, kMaxSplit>(a, vec, s);
   else {
-    // Rows of more than 16384 floats: one 512-thread block per row holding
-    // the row, in 12 or 20 float4 per thread
-    // of registers (up to 24576 and 40960 floats; three and two blocks per
-    // CU), or 44 plus the rest in LDS within the device's per-block LDS (its
-    // static arrays and a margin aside); longer rows are re-read.
+    // Rows of more than 16384 floats: one block per row holding the row, 512
+    // threads of 12 or 20 float4 of registers (up to 24576 and 40960 floats;
+    // three and two blocks per CU), then of 20 or 24 with the rest in LDS
+    // (two blocks per CU), then 1024 threads of 24 with the rest in LDS
+    // within the device's per-block LDS (its static arrays and a margin
+    // aside); longer rows are re-read.
     if (outer > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "too many rows");
     thread_local int lds_limit[64] = {};
     int device = 0;
@@ -1709,16 +1723,10 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
       if (hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, device) != hipSuccess) bytes = 0;
       limit = bytes > 0 ? bytes : -1;
       if (limit > 0) {
-        if constexpr (kOp == RowOp::kLayer)
-          resident_variants<kOp, kResidentVec>([&](RowKernel kernel, int) {
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, limit - 1024);
-          });
-        if constexpr (kOp != RowOp::kLayer)
-          resident_variants<kOp, kWideVec, kWideThreads>([&](RowKernel kernel, int) {
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, limit - 1024);
-          });
+        resident_variants<kOp, kWideVec, kWideThreads>([&](RowKernel kernel, int) {
+          (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    limit - 1024);
+        });
         const int pair_bytes = std::min(kPairLdsChunks * 1024, limit - 1024);
         resident_variants<kOp, 20>([&](RowKernel kernel, int) {
           (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1731,10 +1739,8 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
           });
       }
     }
-    // Resident rows: LDS for the float4s past the registers' share, in whole
-    // 1 KB DMA instructions (a row has at most reduce / 4 float4s).
-    const std::int64_t past_regs = reduce / 4 - static_cast<std::int64_t>(kResidentThreads) * kResidentVec;
-    const std::int64_t resident_bytes = past_regs > 0 ? (past_regs + 63) / 64 * 1024 : 0;
+    // LDS holds the float4s past the registers' share, in whole 1 KB DMA
+    // instructions (a row has at most reduce / 4 float4s).
     const int aff = (a.gamma ? kAffGamma : 0) + (a.beta ? kAffBeta : 0);
     auto launch_resident = [&](auto p, unsigned lds_bytes) {
       resident_variants<kOp, decltype(p)::value>([&](RowKernel kernel, int k) {
@@ -1744,14 +1750,17 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
     };
     // Rows past the registers of 20 (LayerNorm also 24) float4 per thread
     // keep two blocks per CU with the rest in LDS, so one row's writes
-    // overlap another's reads, where that measured faster than one block of
-    // 44 float4 per CU (inputs rotated): softmax [2048, 50257] 170.1 -> 159.6
-    // us, [4096, 41000] 280.7 -> 250.0; LayerNorm + weight/bias [2048, 50257]
-    // 198.4 -> 169.2, [4096, 45000] 358.2 -> 291.5, at 24 [2048, 65536]
-    // 235.7 -> 210.5, [1024, 69000] 125.4 -> 116.2; RMSNorm + weight [2048,
-    // 50257] 166.3 -> 161.7. Plain RMSNorm lost 0.5-3 % ([4096, 45000] 274.9
-    // -> 282.3), softmax at 24 float4 lost at [2048, 65536] (205.1 -> 218.0)
-    // and RMSNorm + weight at 24 at [2048, 50257], so those keep 44.
+    // overlap another's reads, where that measured faster (inputs rotated)
+    // than one block per CU: against 512 threads of 44 float4, softmax
+    // [2048, 50257] 170.1 -> 159.6 us, [4096, 41000] 280.7 -> 250.0;
+    // LayerNorm + weight/bias [2048, 50257] 198.4 -> 169.2, at 24 [2048,
+    // 65536] 235.7 -> 210.5, [1024, 69000] 125.4 -> 116.2; RMSNorm + weight
+    // [2048, 50257] 166.3 -> 161.7; against the 1024-thread route below,
+    // softmax [4096, 45000] 288.4 -> 276.8, LayerNorm + weight/bias 350.4 ->
+    // 291.9, [2048, 50257] 191.5 -> 169.3, [1024, 69000] 124.3 -> 114.9.
+    // Plain RMSNorm (0.5-3 % behind 44 float4), softmax at 24 ([2048,
+    // 65536] 205.1 -> 218.0 against 44 float4) and RMSNorm + weight at 24
+    // take the 1024-thread route instead.
     const std::int64_t regs20 = static_cast<std::int64_t>(kResidentThreads) * 20;
     const std::int64_t regs24 = static_cast<std::int64_t>(kResidentThreads) * 24;
     const bool pair20 = kOp != RowOp::kRms || a.gamma != nullptr;
@@ -1767,23 +1776,15 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
       launch_resident(std::integral_constant<int, 20>{}, pair_bytes(regs20));
     else if (kOp == RowOp::kLayer && reduce / 4 > regs24 && reduce / 4 <= regs24 + 64 * pair_chunks) {
       if constexpr (kOp == RowOp::kLayer) launch_resident(std::integral_constant<int, 24>{}, pair_bytes(regs24));
-    } else if (kOp != RowOp::kLayer && limit > 0 &&
+    } else if (limit > 0 &&
                reduce / 4 <= static_cast<std::int64_t>(kWideThreads) * kWideVec + 64 * ((limit - 1024) / 1024)) {
-      // Softmax and RMSNorm rows past those: 1024 threads of 24 float4, the
-      // rest in LDS, 16 waves per CU where 512 threads of 44 float4 ran 8.
-      if constexpr (kOp != RowOp::kLayer) {
-        const std::int64_t past = reduce / 4 - static_cast<std::int64_t>(kWideThreads) * kWideVec;
-        const unsigned wide_bytes = static_cast<unsigned>(past > 0 ? (past + 63) / 64 * 1024 : 0);
-        resident_variants<kOp, kWideVec, kWideThreads>([&](RowKernel kernel, int k) {
-          if (k == aff)
-            hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(outer)), dim3(kWideThreads), wide_bytes, s, a);
-        });
-      }
-    } else if (kOp == RowOp::kLayer && limit > 0 && resident_bytes <= limit - 1024) {
-      // LayerNorm: 512 threads of 44 float4 (the wide route above covers
-      // longer softmax and RMSNorm rows than this would).
-      if constexpr (kOp == RowOp::kLayer)
-        launch_resident(std::integral_constant<int, kResidentVec>{}, static_cast<unsigned>(resident_bytes));
+      // Rows past those: 1024 threads of 24 float4, the rest in LDS.
+      const std::int64_t past = reduce / 4 - static_cast<std::int64_t>(kWideThreads) * kWideVec;
+      const unsigned wide_bytes = static_cast<unsigned>(past > 0 ? (past + 63) / 64 * 1024 : 0);
+      resident_variants<kOp, kWideVec, kWideThreads>([&](RowKernel kernel, int k) {
+        if (k == aff)
+          hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(outer)), dim3(kWideThreads), wide_bytes, s, a);
+      });
     } else {
       hipLaunchKernelGGL((row_block_kernel<kOp>), dim3(static_cast<unsigned>(outer)), dim3(kRowBlockThreads), 0, s,
                          a);
