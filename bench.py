@@ -95,14 +95,16 @@ def timed(launch, steps: int, warmup: int, warm_ms: float = WARM_MS, name: str =
     """Runs `launch` warmup times, then (untimed) until warm_ms of GPU time has
     passed; then K = steps launches between two HIP events on the launch
     stream (total), then max(K, MEDIAN_REPS) more with an event pair around
-    each (per launch), all inside a ROCTx range called name.
+    each (per launch). The timed launches, not the warm-up, run inside a
+    ROCTx range called name, so a kernel trace's per-line average covers the
+    launches the HIP events time (warm-up launches at a rising clock had
+    lifted it 3 % above them at 4096^3).
     The stream is idle on both sides of each pass. Returns (total_ms,
     per_launch_ms list, warm-up launches)."""
-    with marked(name):
-        return _timed(launch, steps, warmup, warm_ms)
+    return _timed(launch, steps, warmup, warm_ms, name)
 
 
-def _timed(launch, steps: int, warmup: int, warm_ms: float):
+def _timed(launch, steps: int, warmup: int, warm_ms: float, name: str):
     s = capi.stream()
     launches = 0
     for _ in range(warmup):
@@ -120,21 +122,22 @@ def _timed(launch, steps: int, warmup: int, warm_ms: float):
             if begin.elapsed_ms(now) >= warm_ms:
                 break
     capi.synchronize()
-    start, stop = capi.Event(), capi.Event()
-    start.record(s)
-    for _ in range(steps):
-        launch(s)
-    stop.record(s)
-    stop.synchronize()
-    total = start.elapsed_ms(stop)
-    reps = max(steps, MEDIAN_REPS)
-    marks = [capi.Event() for _ in range(reps + 1)]
-    marks[0].record(s)
-    for i in range(reps):
-        launch(s)
-        marks[i + 1].record(s)
-    marks[-1].synchronize()
-    capi.synchronize()
+    with marked(name):
+        start, stop = capi.Event(), capi.Event()
+        start.record(s)
+        for _ in range(steps):
+            launch(s)
+        stop.record(s)
+        stop.synchronize()
+        total = start.elapsed_ms(stop)
+        reps = max(steps, MEDIAN_REPS)
+        marks = [capi.Event() for _ in range(reps + 1)]
+        marks[0].record(s)
+        for i in range(reps):
+            launch(s)
+            marks[i + 1].record(s)
+        marks[-1].synchronize()
+        capi.synchronize()
     per = [marks[i].elapsed_ms(marks[i + 1]) for i in range(reps)]
     return total, per, launches
 
