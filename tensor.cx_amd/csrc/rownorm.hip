@@ -1739,8 +1739,6 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
           });
       }
     }
-    // LDS holds the float4s past the registers' share, in whole 1 KB DMA
-    // instructions (a row has at most reduce / 4 float4s).
     const int aff = (a.gamma ? kAffGamma : 0) + (a.beta ? kAffBeta : 0);
     auto launch_resident = [&](auto p, unsigned lds_bytes) {
       resident_variants<kOp, decltype(p)::value>([&](RowKernel kernel, int k) {
@@ -1765,6 +1763,8 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
     const std::int64_t regs24 = static_cast<std::int64_t>(kResidentThreads) * 24;
     const bool pair20 = kOp != RowOp::kRms || a.gamma != nullptr;
     const std::int64_t pair_chunks = limit > 0 ? std::min<std::int64_t>(kPairLdsChunks, (limit - 1024) / 1024) : 0;
+    // LDS holds the float4s past the registers' share, in whole 1 KB DMA
+    // instructions (a row has at most reduce / 4 float4s).
     auto pair_bytes = [&](std::int64_t regs) {
       return static_cast<unsigned>((reduce / 4 - regs + 63) / 64 * 1024);  // reduce / 4 > regs here
     };
