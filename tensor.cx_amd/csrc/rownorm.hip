@@ -1691,7 +1691,9 @@ int run_rows(RowArgs a, std::int64_t outer, std::int64_t reduce, std::int64_t in
     // softmax 95.9 -> 90.8 us). Up to 4096 floats with a weight or bias the
     // split kernel stays: it keeps them in registers across rows, where this
     // kernel reads them from L2 for each row ([8192, 3001] LayerNorm 40
-    // against 54 us); so do rows of up to 3072 (one float4 per thread here:
+    // against 54 us; with this kernel's weight/bias loads grouped, inputs
+    // rotated, [16384, 4096] LayerNorm + weight/bias 92.8 against 100.9 us,
+    // [32768, 3500] 161.4 against 195.0); so do rows of up to 3072 (one float4 per thread here:
     // [4096, 2049] RMSNorm 13.4 against 15.4 us).
     if (outer > 0x7fffffff) return fail(TCX_INVALID_ARGUMENT, "too many rows");
     const int aff = (a.gamma ? kAffGamma : 0) + (a.beta ? kAffBeta : 0);
