@@ -1007,6 +1007,54 @@ def capi():
     return tensorcx_hip_capi
 
 
+@pytest.mark.parametrize("width", [45000, 50257, 65536, 100003, 128256, 139008])
+@pytest.mark.parametrize("off", [1, 2, 3])
+def test_resident_lds_rows_at_every_base(capi, width, off):
+    # Rows held in registers plus LDS (two 512-thread blocks per CU at 20 or,
+    # for LayerNorm, 24 float4 per thread; 1024 threads of 24 float4 past
+    # them), with input and output bases 1-3 floats past a 16-byte boundary:
+    # the float4 body, its head and tail and the LDS chunks all shift. Held
+    # to the row-op bar against float64 truth widened by the oracle's own
+    # drift, and against the oracle within the same bar.
+    rows = 5
+    rng = np.random.default_rng(width + off)
+    flat = rng.standard_normal(rows * width + off).astype(np.float32)
+    x = flat[off:].reshape(rows, width)
+    x[1, width // 3] = np.nan
+    g = rng.uniform(0.5, 1.5, width).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, width).astype(np.float32)
+    dx, dg, db = (capi.DeviceArray.from_numpy(t) for t in (flat, g, b))
+    # Output with a sentinel before the base and 4 floats past the last row.
+    out = capi.DeviceArray.from_numpy(np.full(rows * width + off + 4, 7.0, np.float32))
+    xp, op_ = dx.ptr + 4 * off, out.ptr + 4 * off
+    x64 = x.astype(np.float64)
+    e = np.exp(x64 - x64.max(axis=1, keepdims=True))
+    mean = x64.mean(axis=1, keepdims=True)
+    ln = (x64 - mean) / np.sqrt(((x64 - mean) ** 2).mean(axis=1, keepdims=True) + 1e-5)
+    rms = x64 / np.sqrt((x64 * x64).mean(axis=1, keepdims=True) + 1e-5)
+    runs = {"softmax": (lambda: capi.softmax(xp, op_, rows, width, 1), oracle.softmax(x, 1),
+                        e / e.sum(axis=1, keepdims=True)),
+            "rmsnorm": (lambda: capi.rmsnorm(xp, None, op_, rows, width, 1, 1e-5), oracle.rmsnorm(x, 1), rms),
+            "rmsnorm + weight": (lambda: capi.rmsnorm(xp, dg.ptr, op_, rows, width, 1, 1e-5),
+                                 oracle.affine_norm(x, 1, 1e-5, g, None, rms=True), rms * g),
+            "layernorm + weight/bias": (lambda: capi.layernorm(xp, dg.ptr, db.ptr, op_, rows, width, 1, 1e-5),
+                                        oracle.affine_norm(x, 1, 1e-5, g, b), ln * g + b)}
+    with np.errstate(all="ignore"):
+        for name, (run, expected, truth) in runs.items():
+            run()
+            capi.synchronize()
+            whole = out.numpy()
+            assert np.all(whole[:off] == 7.0) and np.all(whole[off + rows * width:] == 7.0), \
+                f"{name} wrote outside the rows, width {width} +{off}"
+            got = whole[off:off + rows * width].reshape(rows, width)
+            fin = np.isfinite(truth)
+            assert np.array_equal(np.isnan(got), np.isnan(expected)), f"{name} NaN rows, width {width} +{off}"
+            drift = float(np.max(np.abs(expected[fin] - truth[fin]) / np.maximum(np.abs(truth[fin]), 1e-30)))
+            assert_close(got[fin].reshape(-1), truth[fin].reshape(-1), 1e-5 + drift, 1e-5,
+                         f"{name} vs float64, width {width} +{off}")
+            assert_close(got, expected, 1e-5 + drift, 1e-5, f"{name}, width {width} +{off}")
+
+
 def test_row_ops_and_reductions_random_widths_and_bases(capi):
     # Seeded random contiguous rows through the C ABI: widths log-uniform
     # over 1-140000 (every width class of the row kernels, from lane groups
