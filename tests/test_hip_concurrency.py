@@ -187,6 +187,40 @@ def test_barrier_aligned_shared_state(cx):
 
 
 @pytest.mark.gpu
+def test_barrier_aligned_first_wide_rows(cx):
+    """Each worker's first device calls are rows held in registers plus LDS,
+    on both wide routes (two 512-thread blocks per CU at 50257 floats, 1024
+    threads at 100003): every thread sets those kernels' LDS limit on its
+    first call and launches them at once. Results equal the single-thread
+    bits."""
+    rng = np.random.default_rng(23)
+    shapes = ((16, 50257), (16, 100003))
+    xs = [(2.0 * rng.standard_normal(sh)).astype(np.float32) for sh in shapes]
+    gs = [rng.uniform(0.5, 1.5, sh[1]).astype(np.float32) for sh in shapes]
+    bs = [rng.uniform(-0.1, 0.1, sh[1]).astype(np.float32) for sh in shapes]
+    device = [(cx.tensor(x, device="hip"), cx.tensor(g, device="hip"), cx.tensor(b, device="hip"))
+              for x, g, b in zip(xs, gs, bs)]
+
+    def work():
+        out = {}
+        for i, (x, g, b) in enumerate(device):
+            out[f"softmax {i}"] = cx.softmax(x, 1).numpy()
+            out[f"rmsnorm {i}"] = cx.rmsnorm(x, 1, weight=g).numpy()
+            out[f"layernorm {i}"] = cx.layernorm(x, 1, weight=g, bias=b).numpy()
+        return out
+
+    expected = work()
+
+    def worker(index, barrier):
+        barrier.wait()
+        for it in range(ITERATIONS):
+            for name, value in work().items():
+                assert_bits(value, expected[name], f"thread {index} iteration {it} {name}")
+
+    _run_in_threads(worker)
+
+
+@pytest.mark.gpu
 def test_barrier_aligned_pool_scopes(cx):
     """Pools entered on every thread at once, each serving its own thread's
     output and workspace allocations, then trimmed and closed."""
